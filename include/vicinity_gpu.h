@@ -1,0 +1,182 @@
+/*
+ * vicinity_gpu.h -- C ABI of the MI355X (gfx950) IVF-PQ search engine.
+ *
+ * This is the drop-in boundary for vicinity's IVF-PQ index
+ * (src/ivf_pq/search.rs).  Every entry point names the reference interface it
+ * replaces.  All arguments are plain pointers and sizes; host buffers are
+ * owned by the caller and copied (inputs) or filled (outputs) before the call
+ * returns.  No C++ exception crosses this boundary.
+ *
+ * Status codes map onto vicinity's RetrieveError (src/error.rs:17-80).  The
+ * message of the last failure on the calling thread is vgpu_last_error().
+ *
+ * Threading: one handle may be searched from several threads (calls on one
+ * handle are serialised internally, like the Python binding's search_lock,
+ * src/python.rs:155); add/build/load/free need exclusive access, as the
+ * reference's &mut self methods do.
+ */
+#ifndef VICINITY_GPU_H
+#define VICINITY_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes (src/error.rs:17-80) ----------------------------------- */
+#define VGPU_OK 0
+#define VGPU_ERR_EMPTY_INDEX 1        /* RetrieveError::EmptyIndex */
+#define VGPU_ERR_INVALID_PARAMETER 2  /* RetrieveError::InvalidParameter */
+#define VGPU_ERR_INVALID_CONFIG 3     /* RetrieveError::InvalidConfig */
+#define VGPU_ERR_NOT_BUILT 4          /* RetrieveError::NotBuilt */
+#define VGPU_ERR_ALREADY_BUILT 5      /* RetrieveError::AlreadyBuilt */
+#define VGPU_ERR_UNSUPPORTED 6        /* RetrieveError::Unsupported */
+#define VGPU_ERR_DIMENSION_MISMATCH 7 /* RetrieveError::DimensionMismatch */
+#define VGPU_ERR_DEVICE 8             /* HIP runtime failure (RetrieveError::Other) */
+#define VGPU_ERR_OUT_OF_MEMORY 9      /* device allocation failed (RetrieveError::Other) */
+
+/* Scan arithmetic.  Both modes return the oracle's bit-exact distances:
+ *   FAST  ranks candidates with a per-query decomposed table
+ *         (||q-c||^2 + b(x) - 2 q.cw), then rescores the survivors with the
+ *         reference's residual-table arithmetic (pq.rs:232-251) and falls
+ *         back to EXACT for a query whose margin check fails;
+ *   EXACT builds the reference's per-(query, list) residual table. */
+#define VGPU_MODE_FAST 0
+#define VGPU_MODE_EXACT 1
+
+/* IVFPQParams (src/ivf_pq/search.rs:284-312).  OPQ is not supported
+ * (use_opq != 0 -> VGPU_ERR_UNSUPPORTED). */
+typedef struct vgpu_ivfpq_params {
+    size_t num_clusters;  /* nlist */
+    size_t nprobe;        /* default probes per query */
+    size_t num_codebooks; /* M, must divide the dimension */
+    size_t codebook_size; /* ksub, 1..=256; 16 selects 4-bit FastScan */
+    uint64_t seed;        /* k-means seed */
+    int use_opq;
+} vgpu_ivfpq_params;
+
+typedef struct vgpu_ivfpq_info {
+    size_t dimension, num_vectors, num_clusters, nprobe, num_codebooks, codebook_size;
+    size_t subvector_dim;
+    int built, has_vectors, mode;
+} vgpu_ivfpq_info;
+
+/* Per-call device timings (ms, hipEvents on the handle's stream) and
+ * counters of the last search_batch on a handle. */
+typedef struct vgpu_search_stats {
+    float ms_normalize, ms_coarse, ms_select, ms_scan, ms_fallback, ms_rerank, ms_total;
+    uint64_t candidates;     /* sum over queries of scanned list entries */
+    uint64_t scan_bytes;     /* algorithmic bytes of the scan: candidates * (code bytes + 4) */
+    uint32_t fallback_queries; /* FAST queries recomputed in EXACT mode */
+    uint32_t coarse_overflow;  /* queries whose coarse margin set exceeded LDS */
+    uint32_t nq;
+} vgpu_search_stats;
+
+typedef struct vgpu_ivfpq vgpu_ivfpq;
+
+const char *vgpu_last_error(void);
+/* 1 when a gfx950 device is visible, 0 otherwise (never initialises work). */
+int vgpu_device_available(void);
+
+/* IVFPQIndex::new (search.rs:382-405).  Uses the current HIP device. */
+int vgpu_ivfpq_new(size_t dimension, const vgpu_ivfpq_params *params, vgpu_ivfpq **out);
+void vgpu_ivfpq_free(vgpu_ivfpq *h);
+
+/* IVFPQIndex::add_slice (search.rs:488-512) for n rows: each row is
+ * L2-normalised on insert; doc_ids[i] is returned by search. */
+int vgpu_ivfpq_add(vgpu_ivfpq *h, const uint32_t *doc_ids, const float *vectors, size_t n);
+
+/* IVFPQIndex::build_with_training_options (search.rs:534-544):
+ * training_sample_size 0 = train on every vector.  k-means runs its
+ * assignment steps on the GPU. */
+int vgpu_ivfpq_build(vgpu_ivfpq *h, size_t training_sample_size, size_t kmeans_max_iter);
+
+/* Upload an index built elsewhere (the reference's build() or
+ * load_from_dir(), search.rs:1034-1084): centroids f32[L*d], codebooks
+ * f32[M*K*ds], list_offsets u64[L+1], list_ids u32[n] (insertion indices,
+ * ascending inside a list), codes u8[n*M] in insertion order
+ * (quantized_codes), doc_ids u32[n] or NULL (identity), vectors f32[n*d]
+ * normalised or NULL (no rerank).  Marks the index built. */
+int vgpu_ivfpq_load(vgpu_ivfpq *h, const float *centroids, size_t num_centroids,
+                    const float *codebooks, size_t codebook_size,
+                    const uint64_t *list_offsets, const uint32_t *list_ids,
+                    const uint8_t *codes, const uint32_t *doc_ids, const float *vectors,
+                    size_t num_vectors);
+
+int vgpu_ivfpq_set_nprobe(vgpu_ivfpq *h, size_t nprobe); /* search.rs:342-348 */
+int vgpu_ivfpq_set_mode(vgpu_ivfpq *h, int mode);
+int vgpu_ivfpq_compact(vgpu_ivfpq *h);                  /* search.rs compact() */
+int vgpu_ivfpq_get_info(const vgpu_ivfpq *h, vgpu_ivfpq_info *out);
+
+/* IVFPQIndex::search (search.rs:1087-1093): up to k (doc_id, distance)
+ * pairs, ascending; *out_len receives the count. */
+int vgpu_ivfpq_search(vgpu_ivfpq *h, const float *query, size_t dim, size_t k,
+                      uint32_t *out_ids, float *out_dists, size_t *out_len);
+/* IVFPQIndex::search_reranked (search.rs:1117-1158): distances are exact
+ * cosine distances 1 - q.v. */
+int vgpu_ivfpq_search_reranked(vgpu_ivfpq *h, const float *query, size_t dim, size_t k,
+                               size_t pool, uint32_t *out_ids, float *out_dists, size_t *out_len);
+
+/* Batch search, the shape of PyIVFPQIndex.batch_search (python.rs:744-793)
+ * and HNSW's search_batch (src/hnsw/graph.rs:2716-2768): queries f32[nq*dim]
+ * row-major (dim != the index dimension -> DimensionMismatch, search.rs:1188-1193);
+ * nprobe 0 = the index default; rerank_pool 0 = no rerank.
+ * Output rows (nq, k), padded with (-1, +inf) (python.rs:778-785). */
+int vgpu_ivfpq_search_batch(vgpu_ivfpq *h, const float *queries, size_t nq, size_t dim, size_t k,
+                            size_t nprobe, size_t rerank_pool, int64_t *out_ids,
+                            float *out_dists);
+/* Same with device pointers on `stream` (a hipStream_t, NULL = the handle's
+ * stream); returns after enqueueing and waiting for completion. */
+int vgpu_ivfpq_search_batch_device(vgpu_ivfpq *h, const float *d_queries, size_t nq,
+                                   size_t dim, size_t k, size_t nprobe, size_t rerank_pool,
+                                   int64_t *d_out_ids, float *d_out_dists, void *stream);
+int vgpu_ivfpq_last_stats(const vgpu_ivfpq *h, vgpu_search_stats *out);
+/* Enable per-phase hipEvent timing for later search calls (off by default). */
+int vgpu_ivfpq_set_profiling(vgpu_ivfpq *h, int enabled);
+
+/* The probed lists of each query in probe order (search.rs:1602-1617),
+ * lists u32[nq*nprobe]; returns the probe count per query in *out_p. */
+int vgpu_ivfpq_probe_batch(vgpu_ivfpq *h, const float *queries, size_t nq, size_t dim,
+                           size_t nprobe, uint32_t *lists, size_t *out_p);
+
+/* Copy the built artifacts back (any pointer may be NULL): same layouts as
+ * vgpu_ivfpq_load; codes in insertion order. */
+int vgpu_ivfpq_export(const vgpu_ivfpq *h, float *centroids, float *codebooks,
+                      uint64_t *list_offsets, uint32_t *list_ids, uint8_t *codes,
+                      uint32_t *doc_ids, float *vectors);
+
+/* ---- flat exact search (src/distance.rs:78-109) ---------------------------
+ * metric 0: squared L2 ||q||^2 - 2 q.x + ||x||^2 ranking, distances rescored
+ * with l2_distance_squared; metric 1: 1 - q.x (cosine_distance_normalized). */
+typedef struct vgpu_flat vgpu_flat;
+int vgpu_flat_new(size_t dimension, int metric, vgpu_flat **out);
+void vgpu_flat_free(vgpu_flat *h);
+int vgpu_flat_add(vgpu_flat *h, const float *vectors, size_t n);
+int vgpu_flat_search_batch(vgpu_flat *h, const float *queries, size_t nq, size_t dim, size_t k,
+                           int64_t *out_ids, float *out_dists);
+int vgpu_flat_search_batch_device(vgpu_flat *h, const float *d_queries, size_t nq, size_t dim,
+                                  size_t k, int64_t *d_out_ids, float *d_out_dists, void *stream);
+int vgpu_flat_last_ms(const vgpu_flat *h, float *ms_gemm, float *ms_total);
+
+/* ---- per-kernel test entry points (host buffers) -------------------------- */
+/* compute_adc_table_into (pq.rs:196-266) for nr residuals: tables f32[nr*M*K]. */
+int vgpu_test_adc_tables(const float *codebooks, size_t M, size_t K, size_t ds,
+                         const float *residuals, size_t nr, float *tables);
+/* quantize (pq.rs:136-161) of n vectors: codes u8[n*M]. */
+int vgpu_test_pq_encode(const float *codebooks, size_t M, size_t K, size_t ds,
+                        const float *x, size_t n, uint8_t *codes);
+/* normalize (search.rs:55-62) of n rows. */
+int vgpu_test_normalize(const float *x, size_t n, size_t d, float *out);
+/* quantize_lut_flat + fastscan_batch_flat (pq_simd.rs:576-769) of one
+ * packed list (pq_simd.rs:426-486 layout): out f32[n]. */
+int vgpu_test_fastscan(const uint8_t *packed, size_t n, size_t M, const float *lut, float *out);
+/* Coarse dot products Q.C^T with the MFMA kernel: out f32[nq*L]. */
+int vgpu_test_coarse_dots(const float *q, size_t nq, const float *c, size_t L, size_t d,
+                          float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

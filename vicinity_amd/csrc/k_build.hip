@@ -1,0 +1,162 @@
+// Build-side kernels: residual PQ encode, the per-entry FAST term b(x), the
+// FastScan nibble packing, and the per-kernel LUT test entry.
+//
+// Reference: quantize src/ivf_pq/pq.rs:136-161 (argmin over codewords of the
+// squared L2 distance, strict `<`, lowest code wins); residuals v - c
+// src/ivf_pq/search.rs:722-729; PackedCodes4bit::pack src/pq_simd.rs:426-486;
+// compute_adc_table_into pq.rs:196-266.
+#include "vgpu_device.h"
+#include "vgpu_launch.h"
+
+namespace vgpu {
+
+// codes[i*M + m] for one subspace per grid row.  r_j = x_j - c_j (or x_j when
+// there is no centroid), dist = sum_j (r_j - cw_j)^2 in order.
+template <int DS>
+__global__ __launch_bounds__(256) void encode_kernel(const float* __restrict__ x, int n, int d,
+                                                     const float* __restrict__ centroids,
+                                                     const uint32_t* __restrict__ assign,
+                                                     const float* __restrict__ cb, int M, int K,
+                                                     int ds, uint8_t* __restrict__ codes) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int m = blockIdx.y;
+    if (i >= n) return;
+    const float* xs = x + (size_t)i * d + m * ds;
+    const float* cs = centroids ? centroids + (size_t)assign[i] * d + m * ds : nullptr;
+    const float* cbm = cb + (size_t)m * K * ds;
+    int best = 0;
+    float best_d = __int_as_float(0x7f800000);
+    if constexpr (DS > 0) {
+        float r[DS];
+#pragma unroll
+        for (int j = 0; j < DS; j++) r[j] = cs ? xs[j] - cs[j] : xs[j];
+        for (int k = 0; k < K; k++) {
+            const float* cw = cbm + (size_t)k * DS;
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < DS; j++) {
+                float t = r[j] - cw[j];
+                s += t * t;
+            }
+            if (s < best_d) {
+                best_d = s;
+                best = k;
+            }
+        }
+    } else {
+        for (int k = 0; k < K; k++) {
+            const float* cw = cbm + (size_t)k * ds;
+            float s = 0.0f;
+            for (int j = 0; j < ds; j++) {
+                float rj = cs ? xs[j] - cs[j] : xs[j];
+                float t = rj - cw[j];
+                s += t * t;
+            }
+            if (s < best_d) {
+                best_d = s;
+                best = k;
+            }
+        }
+    }
+    codes[(size_t)i * M + m] = (uint8_t)(best < 255 ? best : 255);
+}
+
+void launch_encode(const float* x, int n, int d, const float* centroids, const uint32_t* assign,
+                   const float* codebooks, int M, int K, int ds, uint8_t* codes, hipStream_t s) {
+    if (n <= 0) return;
+    dim3 grid((n + 255) / 256, M);
+#define ENC(DSV) hipLaunchKernelGGL(encode_kernel<DSV>, grid, dim3(256), 0, s, x, n, d, centroids, \
+                                    assign, codebooks, M, K, ds, codes)
+    switch (ds) {
+        case 1: ENC(1); break;
+        case 2: ENC(2); break;
+        case 4: ENC(4); break;
+        case 8: ENC(8); break;
+        case 16: ENC(16); break;
+        default: ENC(0); break;
+    }
+#undef ENC
+}
+
+// b(x) = sum_m (||cw||^2 + 2 c_m . cw) for the entry at each list position.
+__global__ void bias_kernel(DevIndex ix, float* __restrict__ bias) {
+    const uint32_t pos = blockIdx.x * blockDim.x + threadIdx.x;
+    if (pos >= ix.n) return;
+    int lo = 0, hi = ix.L;  // find l with off[l] <= pos < off[l+1]
+    while (hi - lo > 1) {
+        int mid = (lo + hi) >> 1;
+        if (ix.offsets[mid] <= pos) lo = mid;
+        else hi = mid;
+    }
+    const float* c = ix.centroids + (size_t)lo * ix.d;
+    const uint8_t* row = ix.codes + (size_t)pos * ix.M;
+    float b = 0.0f;
+    for (int m = 0; m < ix.M; m++) {
+        const float* cw = ix.codebooks + ((size_t)m * ix.K + row[m]) * ix.ds;
+        float e1 = 0.0f, e2 = 0.0f;
+        for (int j = 0; j < ix.ds; j++) {
+            e1 += cw[j] * cw[j];
+            e2 += c[m * ix.ds + j] * cw[j];
+        }
+        b += e1 + 2.0f * e2;
+    }
+    bias[pos] = b;
+}
+
+void launch_bias(const DevIndex& ix, float* bias, hipStream_t s) {
+    if (ix.n == 0) return;
+    hipLaunchKernelGGL(bias_kernel, dim3((ix.n + 255) / 256), dim3(256), 0, s, ix, bias);
+}
+
+// One workgroup per list; lists shorter than 16 entries have no blocks
+// (they take the exact float path, search.rs:1355-1375).
+__global__ void pack4_kernel(DevIndex ix, uint8_t* __restrict__ packed) {
+    const int l = blockIdx.x;
+    const uint32_t beg = ix.offsets[l], len = ix.offsets[l + 1] - beg;
+    const uint32_t nb = ix.pack_off[l + 1] - ix.pack_off[l];
+    if (nb == 0) return;
+    const int M = ix.M;
+    uint8_t* out = packed + (size_t)ix.pack_off[l] * 16 * M;
+    const uint32_t total = nb * 16u * M;
+    for (uint32_t e = threadIdx.x; e < total; e += blockDim.x) {
+        uint32_t b = e / (16u * M), rem = e % (16u * M);
+        uint32_t m = rem / 16u, lane = rem % 16u;
+        uint32_t lo = b * 32u + lane, hi = lo + 16u;
+        uint8_t clo = lo < len ? (ix.codes[(size_t)(beg + lo) * M + m] & 0x0F) : 0;
+        uint8_t chi = hi < len ? (ix.codes[(size_t)(beg + hi) * M + m] & 0x0F) : 0;
+        out[e] = (uint8_t)(clo | (chi << 4));
+    }
+}
+
+void launch_pack4(const DevIndex& ix, uint8_t* packed, hipStream_t s) {
+    if (ix.L <= 0) return;
+    hipLaunchKernelGGL(pack4_kernel, dim3(ix.L), dim3(256), 0, s, ix, packed);
+}
+
+// tables[t*M*K + m*K + k] = sum_j (r_tj - cw_j)^2 (pq.rs:232-251 order).
+__global__ void adc_tables_kernel(const float* __restrict__ cb, int M, int K, int ds,
+                                  const float* __restrict__ r, int nr, float* __restrict__ tables) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t per = (size_t)M * K;
+    if (e >= per * nr) return;
+    const size_t t = e / per, mk = e % per;
+    const int m = (int)(mk / K);
+    const float* rr = r + t * (size_t)M * ds + (size_t)m * ds;
+    const float* cw = cb + mk * ds;
+    float acc = 0.0f;
+    for (int j = 0; j < ds; j++) {
+        float diff = rr[j] - cw[j];
+        acc += diff * diff;
+    }
+    tables[e] = acc;
+}
+
+void launch_adc_tables(const float* codebooks, int M, int K, int ds, const float* r, int nr,
+                       float* tables, hipStream_t s) {
+    size_t total = (size_t)M * K * nr;
+    if (total == 0) return;
+    hipLaunchKernelGGL(adc_tables_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       codebooks, M, K, ds, r, nr, tables);
+}
+
+}  // namespace vgpu

@@ -1,0 +1,372 @@
+// 4-bit FastScan scan (codebook_size == 16), one workgroup per query, one
+// wave per probed list.
+//
+// Reference: search.rs:1261-1287 (lists of >= 16 entries take FastScan, the
+// rest the exact float path :1355-1375); quantize_lut_flat
+// src/pq_simd.rs:576-611 (global min/max, scale = range/255, inv = 255/range,
+// round half away from zero, clamp); fastscan_block_portable :629-654 (u16
+// accumulation); fastscan_batch_quantized :721-769 (acc * scale + offset * M);
+// PackedCodes4bit layout :426-486 (32-entry blocks, per codebook 16 bytes,
+// byte[lane] = code[lane] | code[lane + 16] << 4).
+//
+// The quantised table of one codebook is 16 bytes = 4 dwords; a packed dword
+// holds the nibbles of 8 entries, looked up 4 at a time with v_perm_b32
+// (byte select from a 64-bit pair) and accumulated as packed u16 pairs, which
+// cannot carry across halves because M <= 257 keeps every sum <= 65535.
+#include "vgpu_device.h"
+#include "vgpu_launch.h"
+
+namespace vgpu {
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Round half away from zero, then Rust's saturating f32 -> u8 cast.
+__device__ __forceinline__ uint32_t round_to_u8(float v) {
+    float r = roundf(v);
+    if (!(r >= 0.0f)) return 0u;
+    if (r > 255.0f) return 255u;
+    return (uint32_t)r;
+}
+
+// Four byte lookups: sel holds four indices 0..15 (one per byte) into the
+// 16-byte table t0..t3.
+__device__ __forceinline__ uint32_t lookup16(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3,
+                                             uint32_t sel) {
+    uint32_t i7 = sel & 0x07070707u;
+    uint32_t lo = __builtin_amdgcn_perm(t1, t0, i7);  // entries 0..7
+    uint32_t hi = __builtin_amdgcn_perm(t3, t2, i7);  // entries 8..15
+    uint32_t m = ((sel >> 3) & 0x01010101u) * 0xffu;
+    return (hi & m) | (lo & ~m);
+}
+
+// Accumulate one codebook of one packed dword (8 entries) into four packed
+// u16 pairs: a0 = entries (4w, 4w+2), a1 = (4w+1, 4w+3), a2/a3 the same + 16.
+__device__ __forceinline__ void fs_accumulate(uint32_t x, uint32_t t0, uint32_t t1, uint32_t t2,
+                                              uint32_t t3, uint32_t& a0, uint32_t& a1,
+                                              uint32_t& a2, uint32_t& a3) {
+    uint32_t rl = lookup16(t0, t1, t2, t3, x & 0x0f0f0f0fu);
+    uint32_t rh = lookup16(t0, t1, t2, t3, (x >> 4) & 0x0f0f0f0fu);
+    a0 += rl & 0x00ff00ffu;
+    a1 += (rl >> 8) & 0x00ff00ffu;
+    a2 += rh & 0x00ff00ffu;
+    a3 += (rh >> 8) & 0x00ff00ffu;
+}
+
+// u16 accumulator of entry c (0..7) of a lane: c -> vector 4w + c (c < 4) or
+// 16 + 4w + (c - 4).
+__device__ __forceinline__ uint32_t fs_acc(int c, uint32_t a0, uint32_t a1, uint32_t a2,
+                                           uint32_t a3) {
+    switch (c) {
+        case 0: return a0 & 0xffffu;
+        case 1: return a1 & 0xffffu;
+        case 2: return a0 >> 16;
+        case 3: return a1 >> 16;
+        case 4: return a2 & 0xffffu;
+        case 5: return a3 & 0xffffu;
+        case 6: return a2 >> 16;
+        default: return a3 >> 16;
+    }
+}
+
+// Wave-level quantisation of a float table lutf[M*16] into qlut (bytes).
+__device__ inline void fs_quantize(const float* lutf, uint8_t* qlut, int M, float& scale,
+                                   float& base_offset) {
+    const int lane = threadIdx.x & 63;
+    float mn = __int_as_float(0x7f800000), mx = __int_as_float(0xff800000);
+    for (int e = lane; e < M * 16; e += 64) {
+        float v = lutf[e];
+        if (v < mn) mn = v;
+        if (v > mx) mx = v;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        float omn = __shfl_xor(mn, off, 64), omx = __shfl_xor(mx, off, 64);
+        if (omn < mn) mn = omn;
+        if (omx > mx) mx = omx;
+    }
+    float range = mx - mn;
+    float sc, inv;
+    if (range < 1.1920929e-07f) {
+        sc = 1.0f;
+        inv = 0.0f;
+    } else {
+        sc = range / 255.0f;
+        inv = 255.0f / range;
+    }
+    for (int e = lane; e < M * 16; e += 64) qlut[e] = (uint8_t)round_to_u8((lutf[e] - mn) * inv);
+    scale = sc;
+    base_offset = mn * (float)M;
+}
+
+// Ascending bitonic sort of keys[0..n) by one wave (n a power of two).
+__device__ inline void wave_bitonic_sort_keys(uint64_t* keys, int n) {
+    const int lane = threadIdx.x & 63;
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            wave_sync();
+            for (int t = lane; t < (n >> 1); t += 64) {
+                int i = 2 * t - (t & (stride - 1));
+                int j = i + stride;
+                bool asc = (i & size) == 0;
+                uint64_t a = keys[i], b = keys[j];
+                if ((a > b) == asc) {
+                    keys[i] = b;
+                    keys[j] = a;
+                }
+            }
+        }
+    }
+    wave_sync();
+}
+
+__device__ inline void block_bitonic_sort_keys(uint64_t* keys, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (int t = threadIdx.x; t < (n >> 1); t += blockDim.x) {
+                int i = 2 * t - (t & (stride - 1));
+                int j = i + stride;
+                bool asc = (i & size) == 0;
+                uint64_t a = keys[i], b = keys[j];
+                if ((a > b) == asc) {
+                    keys[i] = b;
+                    keys[j] = a;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Per-wave top-k buffer in LDS.
+struct WaveTopk {
+    uint64_t* keys;  // [buf]
+    uint32_t* count; // wave counter
+    uint32_t thr;    // accept fkey(dist) <= thr
+    int buf, keep;
+
+    __device__ void flush() {
+        wave_sync();
+        const int lane = threadIdx.x & 63;
+        int n = (int)*count;
+        int n2 = next_pow2(n > 0 ? n : 1);
+        for (int i = n + lane; i < n2; i += 64) keys[i] = ~0ull;
+        wave_bitonic_sort_keys(keys, n2);
+        if (n >= keep) {
+            thr = (uint32_t)(keys[keep - 1] >> 32);
+            n = keep;
+        }
+        wave_sync();
+        if (lane == 0) *count = (uint32_t)n;
+        wave_sync();
+    }
+
+    // Push one candidate per lane (take may differ by lane).
+    __device__ void push(bool take, float dist, uint32_t vidx) {
+        uint32_t fk = fkey(dist);
+        take = take && fk <= thr;
+        uint64_t m = __ballot(take);
+        if (m == 0) return;
+        if ((int)*count > buf - 64) flush();
+        take = take && fk <= thr;
+        int slot = wave_append_slot(take, count);
+        if (take) keys[slot] = ((uint64_t)fk << 32) | vidx;
+        wave_sync();
+    }
+};
+
+__host__ __device__ inline int fs_wave_buf(int keep) {
+    int need = keep + 64;
+    int b = 1;
+    while (b < need) b <<= 1;
+    return b;
+}
+
+__host__ __device__ inline size_t fs_align16(size_t x) { return (x + 15) & ~(size_t)15; }
+
+__host__ __device__ inline size_t fs_lds_layout(int d, int M, int P, int wbuf, size_t* off) {
+    size_t o = 0;
+    off[0] = o; o = fs_align16(o + (size_t)d * 4);            // qs
+    off[1] = o; o = fs_align16(o + (size_t)4 * d * 4);        // residual per wave
+    off[2] = o; o = fs_align16(o + (size_t)4 * M * 16 * 4);   // float LUT per wave
+    off[3] = o; o = fs_align16(o + (size_t)4 * M * 16);       // byte LUT per wave
+    off[4] = o; o = fs_align16(o + (size_t)P * 4 * 2);        // lid, llen
+    off[5] = o; o = fs_align16(o + (size_t)4 * wbuf * 8);     // wave buffers (contiguous)
+    off[6] = o; o = fs_align16(o + 16 * 4);                   // counters
+    return o;
+}
+
+__global__ __launch_bounds__(256) void fastscan_kernel(DevIndex ix, ScanArgs a, int wbuf) {
+    extern __shared__ __align__(16) char smem[];
+    const int q = blockIdx.x;
+    if (q >= a.nq) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int d = ix.d, M = ix.M, ds = ix.ds, P = a.P;
+    size_t off[7];
+    fs_lds_layout(d, M, P, wbuf, off);
+    float* qs = (float*)(smem + off[0]);
+    float* rw = (float*)(smem + off[1]) + wave * d;
+    float* lutf = (float*)(smem + off[2]) + wave * M * 16;
+    uint8_t* qlut = (uint8_t*)(smem + off[3]) + wave * M * 16;
+    uint32_t* lid = (uint32_t*)(smem + off[4]);
+    uint32_t* llen = lid + P;
+    uint64_t* allkeys = (uint64_t*)(smem + off[5]);
+    uint32_t* cnt = (uint32_t*)(smem + off[6]);
+
+    for (int j = tid; j < d; j += blockDim.x) qs[j] = a.qn[(size_t)q * d + j];
+    for (int p = tid; p < P; p += blockDim.x) {
+        uint32_t l = a.probe[(size_t)q * P + p];
+        bool ok = l < (uint32_t)ix.L;  // no such list: scanned as empty
+        lid[p] = ok ? l : 0u;
+        llen[p] = ok ? ix.offsets[l + 1] - ix.offsets[l] : 0u;
+    }
+    if (tid < 4) cnt[tid] = 0;
+    __syncthreads();
+
+    WaveTopk tk;
+    tk.keys = allkeys + (size_t)wave * wbuf;
+    tk.count = cnt + wave;
+    tk.thr = 0xffffffffu;
+    tk.buf = wbuf;
+    tk.keep = a.kout;
+    uint32_t scanned = 0;
+
+    for (int p = wave; p < P; p += 4) {
+        const uint32_t l = lid[p], len = llen[p];
+        if (len == 0) continue;
+        const uint32_t beg = ix.offsets[l];
+        scanned += len;
+        const float* c = ix.centroids + (size_t)l * d;
+        for (int j = lane; j < d; j += 64) rw[j] = qs[j] - c[j];  // search.rs:1242-1245
+        wave_sync();
+        for (int e = lane; e < M * 16; e += 64) {  // pq.rs:232-251
+            const int m = e >> 4;
+            const float* cw = ix.codebooks + (size_t)e * ds;
+            float acc = 0.0f;
+            for (int j = 0; j < ds; j++) {
+                float diff = rw[m * ds + j] - cw[j];
+                acc += diff * diff;
+            }
+            lutf[e] = acc;
+        }
+        wave_sync();
+        if (len < 16) {
+            // Exact float path: m-ordered sum (pq.rs:272-279).
+            bool take = (uint32_t)lane < len;
+            float dist = 0.0f;
+            uint32_t vidx = 0;
+            if (take) {
+                const uint32_t pos = beg + lane;
+                const uint8_t* row = ix.codes + (size_t)pos * M;
+                for (int m = 0; m < M; m++) dist += lutf[m * 16 + row[m]];
+                vidx = ix.list_ids[pos];
+            }
+            tk.push(take, dist, vidx);
+            continue;
+        }
+        float scale, base_offset;
+        fs_quantize(lutf, qlut, M, scale, base_offset);
+        wave_sync();
+        const uint32_t* qw = (const uint32_t*)qlut;
+        const uint32_t nb = ix.pack_off[l + 1] - ix.pack_off[l];
+        const uint8_t* blocks = ix.packed + (size_t)ix.pack_off[l] * 16 * M;
+        for (uint32_t b0 = 0; b0 < nb; b0 += 16) {
+            const uint32_t b = b0 + (lane >> 2), w = lane & 3;
+            uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+            if (b < nb) {
+                const uint32_t* src = (const uint32_t*)(blocks + (size_t)b * 16 * M) + w;
+                for (int m = 0; m < M; m++) {
+                    uint32_t x = src[m * 4];
+                    fs_accumulate(x, qw[m * 4], qw[m * 4 + 1], qw[m * 4 + 2], qw[m * 4 + 3], a0, a1,
+                                  a2, a3);
+                }
+            }
+#pragma unroll
+            for (int cc = 0; cc < 8; cc++) {
+                const uint32_t vi = b * 32 + (cc < 4 ? 4 * w + cc : 16 + 4 * w + (cc - 4));
+                bool take = b < nb && vi < len;
+                float dist = 0.0f;
+                uint32_t vidx = 0;
+                if (take) {
+                    dist = (float)fs_acc(cc, a0, a1, a2, a3) * scale + base_offset;
+                    vidx = ix.list_ids[beg + vi];
+                }
+                tk.push(take, dist, vidx);
+            }
+        }
+        wave_sync();
+    }
+    tk.flush();
+    // Pad each wave buffer past its kept prefix, then one block sort merges all.
+    for (int i = (int)*tk.count + lane; i < wbuf; i += 64) tk.keys[i] = ~0ull;
+    if (lane == 0 && a.counters) atomicAdd(&a.counters[0], (unsigned long long)scanned);
+    __syncthreads();
+    block_bitonic_sort_keys(allkeys, 4 * wbuf);
+    for (int j = tid; j < a.kout; j += blockDim.x) {
+        size_t o = (size_t)q * a.kout + j;
+        uint64_t key = allkeys[j];
+        if (key != ~0ull) {
+            a.out_vidx[o] = (uint32_t)key;
+            a.out_dist[o] = key_dist(key);
+        } else {
+            a.out_vidx[o] = 0xffffffffu;
+            a.out_dist[o] = __int_as_float(0x7f800000);
+        }
+    }
+}
+
+size_t fastscan_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
+    size_t off[7];
+    return fs_lds_layout(ix.d, ix.M, a.P, fs_wave_buf(a.kout), off);
+}
+
+void launch_fastscan(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
+    if (a.nq <= 0) return;
+    size_t lds = fastscan_lds_bytes(ix, a);
+    (void)hipFuncSetAttribute((const void*)fastscan_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)lds);
+    hipLaunchKernelGGL(fastscan_kernel, dim3(a.nq), dim3(VGPU_BLOCK), lds, s, ix, a,
+                       fs_wave_buf(a.kout));
+}
+
+// Test entry: one packed list, one wave quantises `lut` and scans every block.
+__global__ void fastscan_test_kernel(const uint8_t* __restrict__ packed, int n, int M,
+                                     const float* __restrict__ lut, float* __restrict__ out) {
+    extern __shared__ __align__(16) char smem[];
+    float* lutf = (float*)smem;
+    uint8_t* qlut = (uint8_t*)(smem + fs_align16((size_t)M * 16 * 4));
+    const int lane = threadIdx.x & 63;
+    for (int e = lane; e < M * 16; e += 64) lutf[e] = lut[e];
+    wave_sync();
+    float scale, base_offset;
+    fs_quantize(lutf, qlut, M, scale, base_offset);
+    wave_sync();
+    const uint32_t* qw = (const uint32_t*)qlut;
+    const int nb = (n + 31) / 32;
+    for (int b0 = 0; b0 < nb; b0 += 16) {
+        const int b = b0 + (lane >> 2), w = lane & 3;
+        uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+        if (b < nb) {
+            const uint32_t* src = (const uint32_t*)(packed + (size_t)b * 16 * M) + w;
+            for (int m = 0; m < M; m++)
+                fs_accumulate(src[m * 4], qw[m * 4], qw[m * 4 + 1], qw[m * 4 + 2], qw[m * 4 + 3], a0,
+                              a1, a2, a3);
+            for (int cc = 0; cc < 8; cc++) {
+                const int vi = b * 32 + (cc < 4 ? 4 * w + cc : 16 + 4 * w + (cc - 4));
+                if (vi < n) out[vi] = (float)fs_acc(cc, a0, a1, a2, a3) * scale + base_offset;
+            }
+        }
+    }
+}
+
+void launch_fastscan_test(const uint8_t* packed, int n, int M, const float* lut, float* out,
+                          hipStream_t s) {
+    size_t lds = fs_align16((size_t)M * 16 * 4) + fs_align16((size_t)M * 16);
+    (void)hipFuncSetAttribute((const void*)fastscan_test_kernel,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL(fastscan_test_kernel, dim3(1), dim3(64), lds, s, packed, n, M, lut, out);
+}
+
+}  // namespace vgpu

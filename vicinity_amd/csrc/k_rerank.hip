@@ -1,0 +1,80 @@
+// Exact rerank of the approximate pool and the final id mapping / padding.
+//
+// Reference: search_reranked src/ivf_pq/search.rs:1117-1158 (exact
+// cosine_distance_normalized 1 - dot(q, v) over the stored normalised vector,
+// src/distance.rs:104-109, then finish_top_k_by_distance :64-75);
+// search :1087-1093 (insertion index -> doc id); batch padding
+// src/python.rs:778-785 (MISSING_LABEL -1, MISSING_DISTANCE +inf).
+#include "vgpu_device.h"
+#include "vgpu_launch.h"
+
+namespace vgpu {
+
+#define RERANK_CAP 2048
+
+__global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ vectors, int d,
+                                                     const float* __restrict__ qn, int nq,
+                                                     const uint32_t* __restrict__ pool_vidx,
+                                                     int pool, int k, uint32_t* __restrict__ out_vidx,
+                                                     float* __restrict__ out_dist) {
+    __shared__ uint64_t keys[RERANK_CAP];
+    __shared__ uint32_t pay[RERANK_CAP];
+    const int q = blockIdx.x;
+    if (q >= nq) return;
+    const float* qv = qn + (size_t)q * d;
+    const int n2 = next_pow2(pool);
+    for (int t = threadIdx.x; t < n2; t += blockDim.x) {
+        uint64_t key = ~0ull;
+        if (t < pool) {
+            uint32_t v = pool_vidx[(size_t)q * pool + t];
+            if (v != 0xffffffffu) key = cand_key(1.0f - seq_dot(qv, vectors + (size_t)v * d, d), v);
+        }
+        keys[t] = key;
+        pay[t] = 0;
+    }
+    block_bitonic_sort(keys, pay, n2);
+    for (int j = threadIdx.x; j < k; j += blockDim.x) {
+        uint64_t key = j < pool ? keys[j] : ~0ull;
+        size_t o = (size_t)q * k + j;
+        if (key != ~0ull) {
+            out_vidx[o] = (uint32_t)key;
+            out_dist[o] = key_dist(key);
+        } else {
+            out_vidx[o] = 0xffffffffu;
+            out_dist[o] = __int_as_float(0x7f800000);
+        }
+    }
+}
+
+void launch_rerank(const DevIndex& ix, const float* qn, int nq, const uint32_t* pool_vidx,
+                   int pool, int k, uint32_t* out_vidx, float* out_dist, hipStream_t s) {
+    if (nq <= 0) return;
+    hipLaunchKernelGGL(rerank_kernel, dim3(nq), dim3(256), 0, s, ix.vectors, ix.d, qn, nq, pool_vidx,
+                       pool, k, out_vidx, out_dist);
+}
+
+__global__ void finalize_kernel(const uint32_t* __restrict__ vidx, const float* __restrict__ dist,
+                                const uint32_t* __restrict__ doc_ids, int nq, int kin, int k,
+                                int64_t* __restrict__ out_ids, float* __restrict__ out_dists) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (size_t)nq * k) return;
+    const size_t q = e / k, j = e % k;
+    uint32_t v = j < (size_t)kin ? vidx[q * kin + j] : 0xffffffffu;
+    if (v != 0xffffffffu) {
+        out_ids[e] = (int64_t)(doc_ids ? doc_ids[v] : v);
+        out_dists[e] = dist[q * kin + j];
+    } else {
+        out_ids[e] = -1;
+        out_dists[e] = __int_as_float(0x7f800000);
+    }
+}
+
+void launch_finalize(const uint32_t* vidx, const float* dist, const uint32_t* doc_ids, int nq,
+                     int kin, int k, int64_t* out_ids, float* out_dists, hipStream_t s) {
+    size_t total = (size_t)nq * k;
+    if (total == 0) return;
+    hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, vidx,
+                       dist, doc_ids, nq, kin, k, out_ids, out_dists);
+}
+
+}  // namespace vgpu

@@ -1,0 +1,435 @@
+// ADC scan over the probed inverted lists for byte codes (codebook_size != 16),
+// one workgroup (256 threads) per query.
+//
+// Reference: search_approx_internal_observed src/ivf_pq/search.rs:1175-1391;
+// compute_adc_table_into src/ivf_pq/pq.rs:196-266; adc_batch_256_into
+// src/pq_simd.rs:330-369 (sum of LUT[m][code[m]] for m = 0..M-1 from 0.0);
+// finish_top_k_by_distance search.rs:64-75.
+//
+// EXACT mode restates the reference arithmetic: per probed list the residual
+// r = q - c and the table LUT[m][k] = sum_j (r_j - cw_j)^2 (sub, mul, add in
+// order) live in LDS; each candidate sums its M entries in codebook order.
+//
+// FAST mode ranks with the decomposition
+//     ||r - x_r||^2 = ||q - c||^2 + (||x_r||^2 + 2 c.x_r) - 2 q.x_r
+// where the middle term b(x) is stored per list entry at upload and the last
+// term is a per-query table T2[m][k] = -2 q_m.cw_mk built once per query, so
+// no per-(query, list) table is built.  It keeps kk >= k candidates, checks
+// that the kept set provably contains the reference's top-k (gap between the
+// kk-th and k-th approximate distance > 2 tau), rescoring those kk with the
+// EXACT arithmetic; a query that fails the check is flagged and rerun in EXACT
+// mode by the host.
+#include "vgpu_device.h"
+#include "vgpu_launch.h"
+
+namespace vgpu {
+
+#define SCAN_U 2                      // candidates per thread per round
+#define SCAN_ROUND (VGPU_BLOCK * SCAN_U)
+
+struct TopkLds {
+    uint64_t* keys;  // (distance key << 32) | insertion index
+    uint32_t* pos;   // list-major position of the entry
+    uint16_t* probe; // probe slot (which probed list)
+    uint32_t* count;
+    uint32_t* thr;   // distance key threshold: accept fkey(dist) <= thr
+};
+
+// Sort the buffer and keep the best `keep` entries; later candidates must beat
+// the keep-th distance.  All threads call it.
+__device__ void topk_flush(TopkLds& t, int keep) {
+    __syncthreads();
+    int n = (int)*t.count;
+    int n2 = next_pow2(n > 0 ? n : 1);
+    for (int i = n + threadIdx.x; i < n2; i += blockDim.x) {
+        t.keys[i] = ~0ull;
+        t.pos[i] = 0;
+        t.probe[i] = 0;
+    }
+    block_bitonic_sort2(t.keys, t.pos, t.probe, n2);
+    if (threadIdx.x == 0) {
+        if (n >= keep) {
+            *t.thr = (uint32_t)(t.keys[keep - 1] >> 32);
+            *t.count = (uint32_t)keep;
+        }
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ void topk_push(TopkLds& t, bool take, uint32_t fk, uint32_t pos,
+                                          int probe, const uint32_t* __restrict__ list_ids) {
+    int slot = wave_append_slot(take, t.count);
+    if (take) {
+        uint32_t vidx = list_ids[pos];
+        t.keys[slot] = ((uint64_t)fk << 32) | vidx;
+        t.pos[slot] = pos;
+        t.probe[slot] = (uint16_t)probe;
+    }
+}
+
+// Four table lookups from one code word, in codebook order.
+template <int KT>
+__device__ __forceinline__ float add4(float s, uint32_t w, const float* lut, int K) {
+    const int k = KT > 0 ? KT : K;
+    s += lut[w & 0xffu];
+    s += lut[k + ((w >> 8) & 0xffu)];
+    s += lut[2 * k + ((w >> 16) & 0xffu)];
+    s += lut[3 * k + (w >> 24)];
+    return s;
+}
+
+// s + sum_{m=0}^{M-1} lut[m*K + row[m]], m in order.
+template <int MT, int KT>
+__device__ __forceinline__ float adc_sum(const uint8_t* __restrict__ row,
+                                         const float* __restrict__ lut, int M, int K, float s) {
+    const int k = KT > 0 ? KT : K;
+    if constexpr (MT > 0 && MT % 16 == 0) {
+        const uint4* p = reinterpret_cast<const uint4*>(row);
+#pragma unroll
+        for (int v = 0; v < MT / 16; v++) {
+            uint4 x = p[v];
+            s = add4<KT>(s, x.x, lut + (16 * v + 0) * k, K);
+            s = add4<KT>(s, x.y, lut + (16 * v + 4) * k, K);
+            s = add4<KT>(s, x.z, lut + (16 * v + 8) * k, K);
+            s = add4<KT>(s, x.w, lut + (16 * v + 12) * k, K);
+        }
+    } else if constexpr (MT == 8) {
+        uint2 x = *reinterpret_cast<const uint2*>(row);
+        s = add4<KT>(s, x.x, lut, K);
+        s = add4<KT>(s, x.y, lut + 4 * k, K);
+    } else if constexpr (MT == 4) {
+        uint32_t x = *reinterpret_cast<const uint32_t*>(row);
+        s = add4<KT>(s, x, lut, K);
+    } else {
+        for (int m = 0; m < M; m++) s += lut[m * k + row[m]];
+    }
+    return s;
+}
+
+struct ScanLds {
+    float* qs;      // [d]
+    float* rsd;     // [d] EXACT residual
+    float* lut;     // [M*K]
+    uint32_t* lbeg; // [P]
+    uint32_t* llen; // [P]
+    uint32_t* lid;  // [P]
+    uint32_t* pref; // [P+1]
+    float* term0;   // [P]
+    TopkLds tk;
+    uint32_t* misc; // [4]
+};
+
+__host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
+
+__host__ __device__ inline int scan_buf(int kk) {
+    int need = kk + SCAN_ROUND;
+    int b = 1;
+    while (b < need) b <<= 1;
+    return b;
+}
+
+__host__ __device__ inline size_t scan_lds_layout(int d, int M, int K, int P, int buf,
+                                                  size_t* off /* 12 */) {
+    size_t o = 0;
+    off[0] = o; o = align16(o + (size_t)d * 4);          // qs
+    off[1] = o; o = align16(o + (size_t)d * 4);          // rsd
+    off[2] = o; o = align16(o + (size_t)M * K * 4);      // lut
+    off[3] = o; o = align16(o + (size_t)P * 4);          // lbeg
+    off[4] = o; o = align16(o + (size_t)P * 4);          // llen
+    off[5] = o; o = align16(o + (size_t)P * 4);          // lid
+    off[6] = o; o = align16(o + (size_t)(P + 1) * 4);    // pref
+    off[7] = o; o = align16(o + (size_t)P * 4);          // term0
+    off[8] = o; o = align16(o + (size_t)buf * 8);        // keys
+    off[9] = o; o = align16(o + (size_t)buf * 4);        // pos
+    off[10] = o; o = align16(o + (size_t)buf * 2);       // probe
+    off[11] = o; o = align16(o + 16);                    // misc
+    return o;
+}
+
+__device__ inline ScanLds carve(char* smem, int d, int M, int K, int P, int buf) {
+    size_t off[12];
+    scan_lds_layout(d, M, K, P, buf, off);
+    ScanLds s;
+    s.qs = (float*)(smem + off[0]);
+    s.rsd = (float*)(smem + off[1]);
+    s.lut = (float*)(smem + off[2]);
+    s.lbeg = (uint32_t*)(smem + off[3]);
+    s.llen = (uint32_t*)(smem + off[4]);
+    s.lid = (uint32_t*)(smem + off[5]);
+    s.pref = (uint32_t*)(smem + off[6]);
+    s.term0 = (float*)(smem + off[7]);
+    s.tk.keys = (uint64_t*)(smem + off[8]);
+    s.tk.pos = (uint32_t*)(smem + off[9]);
+    s.tk.probe = (uint16_t*)(smem + off[10]);
+    s.misc = (uint32_t*)(smem + off[11]);
+    s.tk.count = s.misc;
+    s.tk.thr = s.misc + 1;
+    return s;
+}
+
+// Common prologue: query vector and probed list ranges into LDS.
+__device__ inline void load_query_and_lists(const DevIndex& ix, const ScanArgs& a, ScanLds& s,
+                                            int q) {
+    const int tid = threadIdx.x, d = ix.d, P = a.P;
+    for (int j = tid; j < d; j += blockDim.x) s.qs[j] = a.qn[(size_t)q * d + j];
+    for (int p = tid; p < P; p += blockDim.x) {
+        uint32_t l = a.probe[(size_t)q * P + p];
+        if (l >= (uint32_t)ix.L) {  // no such list: scanned as empty
+            s.lid[p] = 0;
+            s.lbeg[p] = 0;
+            s.llen[p] = 0;
+            continue;
+        }
+        uint32_t b = ix.offsets[l];
+        s.lid[p] = l;
+        s.lbeg[p] = b;
+        s.llen[p] = ix.offsets[l + 1] - b;
+    }
+    if (tid == 0) {
+        *s.tk.count = 0;
+        *s.tk.thr = 0xffffffffu;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t acc = 0;
+        s.pref[0] = 0;
+        for (int p = 0; p < P; p++) {
+            acc += s.llen[p];
+            s.pref[p + 1] = acc;
+        }
+    }
+}
+
+// Write the first kout sorted entries (insertion index, distance), padding
+// with (0xffffffff, +inf).
+__device__ inline void write_out(const ScanArgs& a, ScanLds& s, int q, int n) {
+    for (int j = threadIdx.x; j < a.kout; j += blockDim.x) {
+        size_t o = (size_t)q * a.kout + j;
+        if (j < n) {
+            a.out_vidx[o] = (uint32_t)s.tk.keys[j];
+            a.out_dist[o] = key_dist(s.tk.keys[j]);
+        } else {
+            a.out_vidx[o] = 0xffffffffu;
+            a.out_dist[o] = __int_as_float(0x7f800000);
+        }
+    }
+}
+
+// The reference's distance of one list entry (pq.rs:232-251 table entries
+// summed in codebook order, pq_simd.rs:349-355): residual r = q - c, then per
+// codebook dist_m = sum_j (r_j - cw_j)^2, total = sum_m dist_m.
+__device__ inline float exact_entry_distance(const DevIndex& ix, const float* qs, uint32_t list,
+                                             uint32_t pos) {
+    const int d = ix.d, M = ix.M, K = ix.K, ds = ix.ds;
+    const float* c = ix.centroids + (size_t)list * d;
+    const uint8_t* row = ix.codes + (size_t)pos * M;
+    float total = 0.0f;
+    for (int m = 0; m < M; m++) {
+        const float* cw = ix.codebooks + ((size_t)m * K + row[m]) * ds;
+        float e = 0.0f;
+        for (int j = 0; j < ds; j++) {
+            float r = qs[m * ds + j] - c[m * ds + j];
+            float diff = r - cw[j];
+            e += diff * diff;
+        }
+        total += e;
+    }
+    return total;
+}
+
+// Error bound between the FAST ranking distance and the exact one, for
+// ||q|| <= qn, ||c|| <= cmax, ||x_r|| <= rmax, ||q - c||^2 <= t0max.
+__device__ inline float fast_tau(int d, int M, int ds, float qn, float cmax, float rmax,
+                                 float t0max) {
+    const float u = 5.9604645e-08f;
+    float rr = sqrtf(t0max) + rmax;
+    float S = 2.0f * (qn + cmax) * rmax + 2.0f * rmax * rmax + 2.0f * rr * rr;
+    return 4.0f * (float)(d + M + ds + 8) * u * S + 1e-30f;
+}
+
+template <int MT, int KT>
+__global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a, int buf) {
+    extern __shared__ __align__(16) char smem[];
+    const int q = blockIdx.x;
+    if (q >= a.nq) return;
+    const int tid = threadIdx.x;
+    const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds, P = a.P;
+    ScanLds s = carve(smem, d, M, K, P, buf);
+    load_query_and_lists(ix, a, s, q);
+    __syncthreads();
+    // ||q - c||^2 per probed list, sequential.
+    for (int p = tid; p < P; p += blockDim.x) {
+        const float* c = ix.centroids + (size_t)s.lid[p] * d;
+        float acc = 0.0f;
+        for (int j = 0; j < d; j++) {
+            float t = s.qs[j] - c[j];
+            acc += t * t;
+        }
+        s.term0[p] = acc;
+    }
+    // Per-query table T2[m][k] = -2 q_m . cw_mk.
+    for (int e = tid; e < M * K; e += blockDim.x) {
+        const int m = e / K;
+        const float* cw = ix.codebooks + (size_t)e * ds;
+        float acc = 0.0f;
+        for (int j = 0; j < ds; j++) acc += s.qs[m * ds + j] * cw[j];
+        s.lut[e] = -2.0f * acc;
+    }
+    __syncthreads();
+    const uint32_t total = s.pref[P];
+    int cur = 0;
+    for (uint32_t base = 0; base < total; base += SCAN_ROUND) {
+        if (*s.tk.count > (uint32_t)(buf - SCAN_ROUND)) topk_flush(s.tk, a.kk);
+        const uint32_t thr = *s.tk.thr;
+#pragma unroll
+        for (int u = 0; u < SCAN_U; u++) {
+            uint32_t t = base + u * VGPU_BLOCK + tid;
+            bool take = false;
+            uint32_t fk = 0, pos = 0;
+            if (t < total) {
+                while (t >= s.pref[cur + 1]) cur++;
+                pos = s.lbeg[cur] + (t - s.pref[cur]);
+                float dist = s.term0[cur] + ix.bias[pos];
+                dist = adc_sum<MT, KT>(ix.codes + (size_t)pos * M, s.lut, M, K, dist);
+                fk = fkey(dist);
+                take = fk <= thr;
+            }
+            topk_push(s.tk, take, fk, pos, cur, ix.list_ids);
+        }
+        __syncthreads();
+    }
+    topk_flush(s.tk, a.kk);
+    const int n = (int)*s.tk.count;
+    // Margin check: every candidate outside the kept set has approximate
+    // distance >= kept[n-1]; if kept[n-1] - kept[k-1] > 2 tau the exact top-k
+    // lies inside the kept set.
+    if (tid == 0) {
+        uint32_t fail = 0;
+        if (total > (uint32_t)n && n >= a.kout && a.kout > 0) {
+            float t0max = 0.0f;
+            for (int p = 0; p < P; p++) t0max = fmaxf(t0max, s.term0[p]);
+            float tau = fast_tau(d, M, ds, a.qnorm[q], ix.cmax, ix.rmax, t0max);
+            float gap = key_dist(s.tk.keys[n - 1]) - key_dist(s.tk.keys[a.kout - 1]);
+            if (!(gap > 2.0f * tau)) fail = 1;
+        }
+        s.misc[2] = fail;
+        if (a.counters) atomicAdd(&a.counters[0], (unsigned long long)total);
+        if (fail) {
+            a.flags[q] = 1u;
+            if (a.counters) atomicAdd(&a.counters[1], 1ull);
+        }
+    }
+    __syncthreads();
+    if (s.misc[2]) return;
+    // Rescore the kept entries with the reference arithmetic.
+    for (int t = tid; t < n; t += blockDim.x) {
+        uint32_t vidx = (uint32_t)s.tk.keys[t];
+        float ex = exact_entry_distance(ix, s.qs, s.lid[s.tk.probe[t]], s.tk.pos[t]);
+        s.tk.keys[t] = cand_key(ex, vidx);
+    }
+    int n2 = next_pow2(n > 0 ? n : 1);
+    for (int t = n + tid; t < n2; t += blockDim.x) {
+        s.tk.keys[t] = ~0ull;
+        s.tk.pos[t] = 0;
+        s.tk.probe[t] = 0;
+    }
+    block_bitonic_sort2(s.tk.keys, s.tk.pos, s.tk.probe, n2);
+    write_out(a, s, q, n < a.kout ? n : a.kout);
+}
+
+template <int MT, int KT>
+__global__ __launch_bounds__(256) void scan8_exact_kernel(DevIndex ix, ScanArgs a, int buf) {
+    extern __shared__ __align__(16) char smem[];
+    const int q = blockIdx.x;
+    if (q >= a.nq) return;
+    if (a.only_flagged && a.flags[q] == 0u) return;
+    const int tid = threadIdx.x;
+    const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds, P = a.P;
+    ScanLds s = carve(smem, d, M, K, P, buf);
+    load_query_and_lists(ix, a, s, q);
+    uint32_t total = 0;
+    for (int p = 0; p < P; p++) {
+        __syncthreads();
+        const uint32_t l = s.lid[p], beg = s.lbeg[p], len = s.llen[p];
+        total += len;
+        if (len == 0) continue;
+        const float* c = ix.centroids + (size_t)l * d;
+        for (int j = tid; j < d; j += blockDim.x) s.rsd[j] = s.qs[j] - c[j];  // search.rs:1242-1245
+        __syncthreads();
+        // pq.rs:232-251 (ds == 1 gives 0 + diff*diff == diff*diff).
+        for (int e = tid; e < M * K; e += blockDim.x) {
+            const int m = e / K;
+            const float* cw = ix.codebooks + (size_t)e * ds;
+            float acc = 0.0f;
+            for (int j = 0; j < ds; j++) {
+                float diff = s.rsd[m * ds + j] - cw[j];
+                acc += diff * diff;
+            }
+            s.lut[e] = acc;
+        }
+        __syncthreads();
+        for (uint32_t base = 0; base < len; base += SCAN_ROUND) {
+            if (*s.tk.count > (uint32_t)(buf - SCAN_ROUND)) topk_flush(s.tk, a.kk);
+            const uint32_t thr = *s.tk.thr;
+#pragma unroll
+            for (int u = 0; u < SCAN_U; u++) {
+                uint32_t i = base + u * VGPU_BLOCK + tid;
+                bool take = false;
+                uint32_t fk = 0, pos = 0;
+                if (i < len) {
+                    pos = beg + i;
+                    float dist = adc_sum<MT, KT>(ix.codes + (size_t)pos * M, s.lut, M, K, 0.0f);
+                    fk = fkey(dist);
+                    take = fk <= thr;
+                }
+                topk_push(s.tk, take, fk, pos, p, ix.list_ids);
+            }
+            __syncthreads();
+        }
+    }
+    topk_flush(s.tk, a.kk);
+    const int n = (int)*s.tk.count;
+    if (tid == 0 && a.counters && !a.only_flagged) atomicAdd(&a.counters[0], (unsigned long long)total);
+    write_out(a, s, q, n < a.kout ? n : a.kout);
+}
+
+size_t scan8_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
+    size_t off[12];
+    return scan_lds_layout(ix.d, ix.M, ix.K, a.P, scan_buf(a.kk), off);
+}
+
+template <int MT, int KT>
+static void launch_mk(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
+    int buf = scan_buf(a.kk);
+    size_t lds = scan8_lds_bytes(ix, a);
+    if (a.exact) {
+        auto k = scan8_exact_kernel<MT, KT>;
+        (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), lds, s, ix, a, buf);
+    } else {
+        auto k = scan8_fast_kernel<MT, KT>;
+        (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), lds, s, ix, a, buf);
+    }
+}
+
+template <int KT>
+static void launch_k(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
+    switch (ix.M) {
+        case 4: launch_mk<4, KT>(ix, a, s); break;
+        case 8: launch_mk<8, KT>(ix, a, s); break;
+        case 16: launch_mk<16, KT>(ix, a, s); break;
+        case 32: launch_mk<32, KT>(ix, a, s); break;
+        case 48: launch_mk<48, KT>(ix, a, s); break;
+        case 64: launch_mk<64, KT>(ix, a, s); break;
+        default: launch_mk<0, KT>(ix, a, s); break;
+    }
+}
+
+void launch_scan8(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
+    if (a.nq <= 0) return;
+    if (ix.K == 256) launch_k<256>(ix, a, s);
+    else launch_k<0>(ix, a, s);
+}
+
+}  // namespace vgpu

@@ -1,0 +1,173 @@
+// Device helpers shared by the gfx950 kernels: total-order float keys, a
+// block-wide bitonic sort in LDS, a block-wide radix select and wave-level
+// append for top-k buffers.  Every kernel runs with 256 threads (4 waves of 64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define VGPU_BLOCK 256
+#define VGPU_WAVE 64
+
+// f32::total_cmp as an unsigned key: u32 order == total_cmp order
+// (src/ivf_pq/search.rs:64-75 sorts with total_cmp; NaN sorts last).
+__device__ __forceinline__ uint32_t fkey(float f) {
+    uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float fkey_to_float(uint32_t k) {
+    uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __uint_as_float(b);
+}
+
+// Candidate key: distance in the high word, vector index in the low word, so
+// u64 order = (distance total_cmp, then lower vector index).
+__device__ __forceinline__ uint64_t cand_key(float dist, uint32_t idx) {
+    return ((uint64_t)fkey(dist) << 32) | idx;
+}
+
+__device__ __forceinline__ float key_dist(uint64_t key) { return fkey_to_float((uint32_t)(key >> 32)); }
+
+// Sequential float32 dot product (src/simd.rs:88-91 order); the library is
+// compiled with -ffp-contract=off so each step rounds the product and the sum.
+__device__ __forceinline__ float seq_dot(const float* a, const float* b, int n) {
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) s += a[i] * b[i];
+    return s;
+}
+
+// Ascending bitonic sort of keys[0..n) (n a power of two) with a payload array.
+// All threads of the block must call it.
+template <typename P>
+__device__ void block_bitonic_sort(uint64_t* keys, P* pay, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (int t = threadIdx.x; t < (n >> 1); t += blockDim.x) {
+                int i = 2 * t - (t & (stride - 1));
+                int j = i + stride;
+                bool asc = (i & size) == 0;
+                uint64_t a = keys[i], b = keys[j];
+                if ((a > b) == asc) {
+                    keys[i] = b;
+                    keys[j] = a;
+                    P pa = pay[i];
+                    pay[i] = pay[j];
+                    pay[j] = pa;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Two payload arrays.
+template <typename P, typename Q>
+__device__ void block_bitonic_sort2(uint64_t* keys, P* pay, Q* pay2, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (int t = threadIdx.x; t < (n >> 1); t += blockDim.x) {
+                int i = 2 * t - (t & (stride - 1));
+                int j = i + stride;
+                bool asc = (i & size) == 0;
+                uint64_t a = keys[i], b = keys[j];
+                if ((a > b) == asc) {
+                    keys[i] = b;
+                    keys[j] = a;
+                    P pa = pay[i];
+                    pay[i] = pay[j];
+                    pay[j] = pa;
+                    Q qa = pay2[i];
+                    pay2[i] = pay2[j];
+                    pay2[j] = qa;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ int next_pow2(int n) {
+    int p = 1;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+// Shared scratch of the radix select: 256 histogram bins + 2 result words.
+struct RadixScratch {
+    uint32_t hist[256];
+    uint32_t bin;
+    uint32_t rem;
+};
+
+// Block-wide radix select: returns the key of 0-based rank `rank` among the
+// keys produced by key_of(i), i in [0, n).  KeyT is uint32_t or uint64_t;
+// digits are 8 bits, most significant first.  key_of is called once per
+// element per pass.  All threads must call it; rank < n.
+template <typename KeyT, typename KeyFn>
+__device__ KeyT block_radix_select(KeyFn key_of, int n, uint32_t rank, RadixScratch* rs) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    KeyT prefix = 0, mask = 0;
+    for (int shift = (int)(sizeof(KeyT) * 8) - 8; shift >= 0; shift -= 8) {
+        __syncthreads();
+        for (int i = tid; i < 256; i += blockDim.x) rs->hist[i] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += blockDim.x) {
+            KeyT k = key_of(i);
+            if ((k & mask) == prefix) atomicAdd(&rs->hist[(uint32_t)(k >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid < 64) {
+            uint32_t h0 = rs->hist[4 * lane], h1 = rs->hist[4 * lane + 1];
+            uint32_t h2 = rs->hist[4 * lane + 2], h3 = rs->hist[4 * lane + 3];
+            uint32_t own = h0 + h1 + h2 + h3;
+            uint32_t s = own;
+            for (int off = 1; off < 64; off <<= 1) {
+                uint32_t t = __shfl_up(s, off, 64);
+                if (lane >= off) s += t;
+            }
+            uint32_t excl = s - own;
+            if (rank >= excl && rank < s) {
+                uint32_t r = rank - excl;
+                uint32_t b = 0;
+                if (r < h0) {
+                    b = 0;
+                } else if (r < h0 + h1) {
+                    b = 1;
+                    r -= h0;
+                } else if (r < h0 + h1 + h2) {
+                    b = 2;
+                    r -= h0 + h1;
+                } else {
+                    b = 3;
+                    r -= h0 + h1 + h2;
+                }
+                rs->bin = 4 * lane + b;
+                rs->rem = r;
+            }
+        }
+        __syncthreads();
+        prefix |= (KeyT)rs->bin << shift;
+        mask |= (KeyT)255u << shift;
+        rank = rs->rem;
+    }
+    __syncthreads();
+    return prefix;
+}
+
+// Wave-aggregated append: lanes with `take` reserve consecutive slots of an
+// LDS counter with one atomic per wave.  Returns the lane's slot (or -1).
+__device__ __forceinline__ int wave_append_slot(bool take, uint32_t* counter) {
+    uint64_t m = __ballot(take);
+    if (m == 0) return -1;
+    uint32_t lo = (uint32_t)m, hi = (uint32_t)(m >> 32);
+    uint32_t below = __builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u));
+    int leader = __ffsll((unsigned long long)m) - 1;
+    uint32_t base = 0;
+    if ((int)(threadIdx.x & 63) == leader) base = atomicAdd(counter, (uint32_t)__popcll(m));
+    base = __shfl(base, leader, 64);
+    return take ? (int)(base + below) : -1;
+}

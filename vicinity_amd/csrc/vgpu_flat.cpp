@@ -1,0 +1,72 @@
+// Flat exact index: database resident in HBM, batched top-k.
+// Reference: brute force over l2_distance_squared / cosine_distance_normalized
+// (src/distance.rs:78-109), as the reference's ground truth
+// (src/ivf_pq/search.rs:3376-3392, tests/common/mod.rs:49-57).
+#include <algorithm>
+#include <cmath>
+
+#include "vgpu_runtime.h"
+
+namespace vgpu {
+
+FlatIndex::FlatIndex(size_t dim, int met) : d(dim), metric(met) {
+    if (dim == 0) throw Error(VGPU_ERR_INVALID_CONFIG, "dimension must be greater than 0");
+    if (met != 0 && met != 1) throw Error(VGPU_ERR_INVALID_CONFIG, "metric must be 0 (L2) or 1 (1 - dot)");
+    VGPU_HIP(hipStreamCreate(&stream));
+    for (auto& e : ev) VGPU_HIP(hipEventCreate(&e));
+}
+
+FlatIndex::~FlatIndex() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (auto& e : ev)
+        if (e) (void)hipEventDestroy(e);
+    if (stream) (void)hipStreamDestroy(stream);
+}
+
+void FlatIndex::add(const float* x, size_t count) {
+    if (n + count >= 0xffffffffull) throw Error(VGPU_ERR_INVALID_PARAMETER, "more than 2^32-1 vectors");
+    host.insert(host.end(), x, x + count * d);
+    for (size_t i = 0; i < count; i++) {
+        double t = 0.0;
+        for (size_t j = 0; j < d; j++) t += (double)x[i * d + j] * x[i * d + j];
+        xmax2 = std::max(xmax2, t);
+    }
+    n += count;
+    d_x.upload(host.data(), n * d, stream);
+    d_xnorm.reserve(n);
+    launch_flat_norms(d_x.p, (int)n, (int)d, d_xnorm.p, stream);
+    VGPU_HIP(hipGetLastError());
+    VGPU_HIP(hipStreamSynchronize(stream));
+}
+
+void FlatIndex::search_device(const float* d_q, size_t nq, size_t k, int64_t* d_ids, float* d_dists,
+                              hipStream_t s) {
+    if (!s) s = stream;
+    if (nq == 0 || k == 0) return;
+    if (k > 112) throw Error(VGPU_ERR_INVALID_PARAMETER, "flat search supports k <= 112");
+    if (n == 0) {
+        launch_finalize(nullptr, nullptr, nullptr, (int)nq, 0, (int)k, d_ids, d_dists, s);
+        VGPU_HIP(hipStreamSynchronize(s));
+        return;
+    }
+    const float xmax = (float)(std::sqrt(xmax2) * 1.0001 + 1e-30);
+    w_qnorm.reserve(nq);
+    w_partial.reserve(flat_partial_count((int)nq, (int)n, (int)k));
+    w_idx.reserve(nq * k);
+    w_dist.reserve(nq * k);
+    w_overflow.reserve(1);
+    VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
+    VGPU_HIP(hipEventRecord(ev[0], s));
+    launch_flat_norms(d_q, (int)nq, (int)d, w_qnorm.p, s);
+    launch_flat_search(d_q, w_qnorm.p, (int)nq, d_x.p, d_xnorm.p, (int)n, (int)d, (int)k, metric, xmax,
+                       w_partial.p, w_idx.p, w_dist.p, w_overflow.p, s);
+    VGPU_HIP(hipEventRecord(ev[1], s));
+    launch_finalize(w_idx.p, w_dist.p, nullptr, (int)nq, (int)k, (int)k, d_ids, d_dists, s);
+    VGPU_HIP(hipEventRecord(ev[2], s));
+    VGPU_HIP(hipGetLastError());
+    VGPU_HIP(hipEventSynchronize(ev[2]));
+    VGPU_HIP(hipEventElapsedTime(&ms_gemm, ev[0], ev[1]));
+    VGPU_HIP(hipEventElapsedTime(&ms_total, ev[0], ev[2]));
+}
+
+}  // namespace vgpu

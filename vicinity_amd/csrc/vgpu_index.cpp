@@ -1,0 +1,606 @@
+// IVF-PQ index object: insert, GPU-assisted build, HBM residency, and the
+// batched search pipeline.
+//
+// Reference: IVFPQIndex src/ivf_pq/search.rs:212-239 (state), add_slice
+// :488-512, build_with_training_config :546-787, build_scan_caches :816-848,
+// search :1087-1093, search_reranked :1117-1158, search_approx_internal_observed
+// :1175-1391; batch shape src/python.rs:744-793.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <numeric>
+
+#include "vgpu_runtime.h"
+
+namespace vgpu {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e == hipSuccess) return;
+    (void)hipGetLastError();
+    int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? VGPU_ERR_OUT_OF_MEMORY
+                                                                           : VGPU_ERR_DEVICE;
+    throw Error(code, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// splitmix64 (Steele, Lea, Flood 2014): the seeded stream of the training
+// sample and of the k-means initial centroids.
+static inline uint64_t splitmix64(uint64_t& s) {
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static inline size_t bounded(uint64_t& s, size_t n) {
+    return (size_t)(((unsigned __int128)splitmix64(s) * (unsigned __int128)n) >> 64);
+}
+
+void draw_distinct(size_t n, size_t count, uint64_t seed, std::vector<uint32_t>& out) {
+    std::vector<uint32_t> perm(n);
+    std::iota(perm.begin(), perm.end(), 0u);
+    uint64_t s = seed;
+    out.resize(count);
+    for (size_t i = 0; i < count; i++) {
+        size_t j = i + bounded(s, n - i);
+        std::swap(perm[i], perm[j]);
+        out[i] = perm[i];
+    }
+}
+
+void sample_indices(size_t n, size_t sample, uint64_t seed, std::vector<uint32_t>& out) {
+    if (sample == 0 || sample >= n) {
+        out.resize(n);
+        std::iota(out.begin(), out.end(), 0u);
+        return;
+    }
+    draw_distinct(n, sample, seed, out);
+    std::sort(out.begin(), out.end());
+}
+
+// search.rs:55-62 / :503-508: sum of squares in order, sqrt, x / norm when
+// norm > 1e-10 (this file is compiled with -ffp-contract=off).
+void normalize_row(const float* x, size_t d, float* out) {
+    float s = 0.0f;
+    for (size_t i = 0; i < d; i++) s += x[i] * x[i];
+    float norm = std::sqrt(s);
+    if (norm > 1e-10f) {
+        for (size_t i = 0; i < d; i++) out[i] = x[i] / norm;
+    } else if (out != x) {
+        std::memcpy(out, x, d * sizeof(float));
+    }
+}
+
+static float row_norm_bound(const float* x, size_t d) {
+    double s = 0.0;
+    for (size_t i = 0; i < d; i++) s += (double)x[i] * (double)x[i];
+    return (float)(std::sqrt(s) * 1.0001 + 1e-30);
+}
+
+IvfpqIndex::IvfpqIndex(size_t dim, const vgpu_ivfpq_params& p) : d(dim), params(p) {
+    if (dim == 0) throw Error(VGPU_ERR_INVALID_CONFIG, "dimension must be greater than 0");
+    if (p.codebook_size > 256)
+        throw Error(VGPU_ERR_INVALID_CONFIG,
+                    "codebook_size must be at most 256 because PQ codes are stored as u8");
+    VGPU_HIP(hipStreamCreate(&stream));
+    for (auto& e : ev) VGPU_HIP(hipEventCreate(&e));
+}
+
+IvfpqIndex::~IvfpqIndex() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (auto& e : ev)
+        if (e) (void)hipEventDestroy(e);
+    if (stream) (void)hipStreamDestroy(stream);
+}
+
+void IvfpqIndex::add(const uint32_t* ids, const float* x, size_t count) {
+    if (built) throw Error(VGPU_ERR_ALREADY_BUILT, "IVF-PQ index: cannot add vectors after build");
+    for (size_t i = 0; i < count * d; i++)
+        if (!std::isfinite(x[i])) throw Error(VGPU_ERR_INVALID_PARAMETER, "vector contains a non-finite value");
+    size_t base = vectors.size();
+    vectors.resize(base + count * d);
+    for (size_t i = 0; i < count; i++) normalize_row(x + i * d, d, vectors.data() + base + i * d);
+    doc_ids.insert(doc_ids.end(), ids, ids + count);
+}
+
+// argmin over centroids of 1 - dot(x, c), lowest index on ties: the coarse
+// GEMM + margin rescoring kernels with nprobe = 1, chunked to bound the score
+// matrix at 1 GiB.
+void IvfpqIndex::assign_cosine(const float* d_x, const float* d_norms, size_t nx,
+                               const float* d_cent, size_t k, float cmax, uint32_t* d_assign,
+                               hipStream_t s) {
+    size_t chunk = std::max<size_t>(1, std::min<size_t>(nx, ((size_t)1 << 28) / std::max<size_t>(k, 1)));
+    chunk = std::min<size_t>(chunk, (size_t)1 << 20);  // grid.y of the GEMM stays < 65536
+    w_dots.reserve(chunk * k);
+    w_overflow.reserve(1);
+    VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
+    for (size_t q0 = 0; q0 < nx; q0 += chunk) {
+        size_t nc = std::min(chunk, nx - q0);
+        launch_coarse_dots(d_x + q0 * d, d_cent, w_dots.p, (int)nc, (int)k, (int)d, s);
+        launch_coarse_select(w_dots.p, d_x + q0 * d, d_norms + q0, d_cent, (int)nc, (int)k, (int)d, 1,
+                             cmax, d_assign + q0, w_overflow.p, s);
+    }
+    VGPU_HIP(hipGetLastError());
+}
+
+// Lloyd k-means with cosine assignment (the role of clump's CosineDistance
+// k-means, src/partitioning/kmeans.rs:64-107): k_eff = min(k, n) seeded
+// distinct starting points; assign on the GPU; stop when no assignment
+// changes; otherwise each non-empty centroid becomes the float64 mean of its
+// members (index order), re-normalised.
+void IvfpqIndex::kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k, uint64_t seed,
+                               size_t max_iter, std::vector<float>& cent) {
+    const size_t ke = std::min(k, nt);
+    std::vector<uint32_t> init;
+    draw_distinct(nt, ke, seed, init);
+    cent.assign(ke * d, 0.0f);
+    for (size_t c = 0; c < ke; c++) std::memcpy(&cent[c * d], &x[(size_t)init[c] * d], d * sizeof(float));
+    std::vector<float> norms(nt);
+    for (size_t i = 0; i < nt; i++) norms[i] = row_norm_bound(&x[i * d], d);
+    DevBuf<float> dx, dn, dc;
+    DevBuf<uint32_t> da;
+    dx.upload(x.data(), nt * d, stream);
+    dn.upload(norms.data(), nt, stream);
+    da.reserve(nt);
+    std::vector<uint32_t> assign(nt), prev(nt);
+    std::vector<double> sums(ke * d);
+    std::vector<uint64_t> counts(ke);
+    for (size_t it = 0; it < max_iter; it++) {
+        float cmax = 0.0f;
+        for (size_t c = 0; c < ke; c++) cmax = std::max(cmax, row_norm_bound(&cent[c * d], d));
+        dc.upload(cent.data(), ke * d, stream);
+        assign_cosine(dx.p, dn.p, nt, dc.p, ke, cmax, da.p, stream);
+        VGPU_HIP(hipMemcpyAsync(assign.data(), da.p, nt * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+        VGPU_HIP(hipStreamSynchronize(stream));
+        if (it > 0 && assign == prev) break;
+        std::fill(sums.begin(), sums.end(), 0.0);
+        std::fill(counts.begin(), counts.end(), 0);
+        for (size_t i = 0; i < nt; i++) {
+            double* sc = &sums[(size_t)assign[i] * d];
+            const float* xi = &x[i * d];
+            for (size_t j = 0; j < d; j++) sc[j] += (double)xi[j];
+            counts[assign[i]]++;
+        }
+        for (size_t c = 0; c < ke; c++) {
+            if (!counts[c]) continue;
+            float* cc = &cent[c * d];
+            for (size_t j = 0; j < d; j++) cc[j] = (float)(sums[c * d + j] / (double)counts[c]);
+            normalize_row(cc, d, cc);
+        }
+        prev.swap(assign);
+    }
+}
+
+// One squared-L2 k-means per subspace (pq.rs:75-124, seed + m), all M run
+// together: one GPU encode pass assigns every subspace; a subspace whose
+// assignment stopped changing is frozen, exactly as if it had been run alone.
+void IvfpqIndex::train_pq(const std::vector<float>& res, size_t nt, size_t Kc, uint64_t seed,
+                          size_t max_iter) {
+    const size_t Ke = std::min(Kc, nt);
+    K = Ke;
+    codebooks.assign(M * Ke * ds, 0.0f);
+    std::vector<uint32_t> init;
+    for (size_t m = 0; m < M; m++) {
+        draw_distinct(nt, Ke, seed + m, init);
+        for (size_t c = 0; c < Ke; c++)
+            std::memcpy(&codebooks[(m * Ke + c) * ds], &res[(size_t)init[c] * d + m * ds], ds * sizeof(float));
+    }
+    DevBuf<float> dres, dcb;
+    DevBuf<uint8_t> dcodes;
+    dres.upload(res.data(), nt * d, stream);
+    dcodes.reserve(nt * M);
+    std::vector<uint8_t> cur(nt * M), prev(nt * M);
+    std::vector<char> frozen(M, 0);
+    std::vector<double> sums(Ke * ds);
+    std::vector<uint64_t> counts(Ke);
+    for (size_t it = 0; it < max_iter; it++) {
+        dcb.upload(codebooks.data(), codebooks.size(), stream);
+        launch_encode(dres.p, (int)nt, (int)d, nullptr, nullptr, dcb.p, (int)M, (int)Ke, (int)ds,
+                      dcodes.p, stream);
+        VGPU_HIP(hipGetLastError());
+        VGPU_HIP(hipMemcpyAsync(cur.data(), dcodes.p, nt * M, hipMemcpyDeviceToHost, stream));
+        VGPU_HIP(hipStreamSynchronize(stream));
+        bool any = false;
+        for (size_t m = 0; m < M; m++) {
+            if (frozen[m]) continue;
+            if (it > 0) {
+                bool same = true;
+                for (size_t i = 0; i < nt && same; i++) same = cur[i * M + m] == prev[i * M + m];
+                if (same) {
+                    frozen[m] = 1;
+                    continue;
+                }
+            }
+            any = true;
+            std::fill(sums.begin(), sums.end(), 0.0);
+            std::fill(counts.begin(), counts.end(), 0);
+            for (size_t i = 0; i < nt; i++) {
+                uint8_t c = cur[i * M + m];
+                const float* xi = &res[i * d + m * ds];
+                for (size_t j = 0; j < ds; j++) sums[c * ds + j] += (double)xi[j];
+                counts[c]++;
+            }
+            for (size_t c = 0; c < Ke; c++) {
+                if (!counts[c]) continue;
+                for (size_t j = 0; j < ds; j++)
+                    codebooks[(m * Ke + c) * ds + j] = (float)(sums[c * ds + j] / (double)counts[c]);
+            }
+        }
+        if (!any) break;
+        prev.swap(cur);
+    }
+}
+
+void IvfpqIndex::build(size_t sample, size_t max_iter) {
+    if (built) return;  // search.rs:550-552
+    const size_t n = this->n();
+    if (n == 0) throw Error(VGPU_ERR_EMPTY_INDEX, "index is empty");
+    if (n < params.codebook_size)
+        throw Error(VGPU_ERR_INVALID_PARAMETER,
+                    "IVF-PQ requires at least codebook_size training vectors (got " +
+                        std::to_string(n) + " vectors, codebook_size = " +
+                        std::to_string(params.codebook_size) + ")");
+    if (max_iter == 0) throw Error(VGPU_ERR_INVALID_CONFIG, "kmeans_max_iter must be greater than 0");
+    std::vector<uint32_t> tidx;
+    sample_indices(n, sample, params.seed, tidx);
+    const size_t nt = tidx.size();
+    size_t min_train = std::max(std::min(params.num_clusters, n), params.codebook_size);
+    if (nt < min_train)
+        throw Error(VGPU_ERR_INVALID_PARAMETER, "IVF-PQ training sample is too small (got " +
+                                                    std::to_string(nt) + ", need at least " +
+                                                    std::to_string(min_train) + ")");
+    if (params.num_clusters == 0)
+        throw Error(VGPU_ERR_INVALID_CONFIG, "dimension and k must both be greater than 0");
+    if (params.num_codebooks == 0 || params.codebook_size == 0)
+        throw Error(VGPU_ERR_INVALID_CONFIG,
+                    "dimension, num_codebooks, codebook_size must all be greater than 0");
+    if (d % params.num_codebooks)
+        throw Error(VGPU_ERR_INVALID_CONFIG, "dimension must be divisible by num_codebooks");
+    if (params.use_opq) throw Error(VGPU_ERR_UNSUPPORTED, "OPQ rotation is not supported on the GPU path");
+    if (n >= 0xffffffffull) throw Error(VGPU_ERR_INVALID_PARAMETER, "more than 2^32-1 vectors");
+    M = params.num_codebooks;
+    ds = d / M;
+
+    std::vector<float> train(nt * d);
+    for (size_t i = 0; i < nt; i++) std::memcpy(&train[i * d], &vectors[(size_t)tidx[i] * d], d * sizeof(float));
+    kmeans_cosine(train, nt, params.num_clusters, params.seed, max_iter, centroids);
+    L = centroids.size() / d;
+
+    // List assignment of every vector (search.rs:621).
+    float cmax = 0.0f;
+    for (size_t c = 0; c < L; c++) cmax = std::max(cmax, row_norm_bound(&centroids[c * d], d));
+    std::vector<float> norms(n);
+    for (size_t i = 0; i < n; i++) norms[i] = row_norm_bound(&vectors[i * d], d);
+    d_vectors.upload(vectors.data(), n * d, stream);
+    d_centroids.upload(centroids.data(), L * d, stream);
+    DevBuf<float> dn;
+    DevBuf<uint32_t> dassign;
+    dn.upload(norms.data(), n, stream);
+    dassign.reserve(n);
+    assign_cosine(d_vectors.p, dn.p, n, d_centroids.p, L, cmax, dassign.p, stream);
+    std::vector<uint32_t> assign(n);
+    VGPU_HIP(hipMemcpyAsync(assign.data(), dassign.p, n * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+    VGPU_HIP(hipStreamSynchronize(stream));
+
+    // Lists: insertion order inside a list (search.rs:624-657).
+    offsets.assign(L + 1, 0);
+    for (size_t i = 0; i < n; i++) offsets[assign[i] + 1]++;
+    for (size_t l = 0; l < L; l++) offsets[l + 1] += offsets[l];
+    list_ids.resize(n);
+    {
+        std::vector<uint64_t> fill(offsets.begin(), offsets.end() - 1);
+        for (size_t i = 0; i < n; i++) list_ids[fill[assign[i]]++] = (uint32_t)i;
+    }
+
+    // Residual PQ training on the sample (search.rs:722-772).
+    std::vector<float> res(nt * d);
+    for (size_t i = 0; i < nt; i++) {
+        const uint32_t v = tidx[i];
+        const float* c = &centroids[(size_t)assign[v] * d];
+        for (size_t j = 0; j < d; j++) res[i * d + j] = vectors[(size_t)v * d + j] - c[j];
+    }
+    train_pq(res, nt, params.codebook_size, params.seed, max_iter);
+
+    // Encode every residual (search.rs:776-781).
+    d_codebooks.upload(codebooks.data(), codebooks.size(), stream);
+    DevBuf<uint8_t> dcodes;
+    dcodes.reserve(n * M);
+    launch_encode(d_vectors.p, (int)n, (int)d, d_centroids.p, dassign.p, d_codebooks.p, (int)M,
+                  (int)K, (int)ds, dcodes.p, stream);
+    VGPU_HIP(hipGetLastError());
+    codes.resize(n * M);
+    VGPU_HIP(hipMemcpyAsync(codes.data(), dcodes.p, n * M, hipMemcpyDeviceToHost, stream));
+    VGPU_HIP(hipStreamSynchronize(stream));
+    has_vectors = true;
+    upload_index();
+    built = true;
+}
+
+void IvfpqIndex::load(const float* cent, size_t Lc, const float* cb, size_t Kc,
+                      const uint64_t* off, const uint32_t* lids, const uint8_t* cds,
+                      const uint32_t* dids, const float* vecs, size_t nv) {
+    if (params.num_codebooks == 0 || d % params.num_codebooks)
+        throw Error(VGPU_ERR_INVALID_CONFIG, "dimension must be divisible by num_codebooks");
+    if (Lc == 0 || Kc == 0 || Kc > 256)
+        throw Error(VGPU_ERR_INVALID_CONFIG, "need num_centroids > 0 and 1 <= codebook_size <= 256");
+    if (nv >= 0xffffffffull) throw Error(VGPU_ERR_INVALID_PARAMETER, "more than 2^32-1 vectors");
+    M = params.num_codebooks;
+    ds = d / M;
+    L = Lc;
+    K = Kc;
+    if (off[0] != 0 || off[L] != nv)
+        throw Error(VGPU_ERR_INVALID_PARAMETER, "list_offsets must start at 0 and end at num_vectors");
+    for (size_t l = 0; l < L; l++)
+        if (off[l + 1] < off[l]) throw Error(VGPU_ERR_INVALID_PARAMETER, "list_offsets must be non-decreasing");
+    std::vector<char> seen(nv, 0);
+    for (size_t i = 0; i < nv; i++) {
+        if (lids[i] >= nv || seen[lids[i]])
+            throw Error(VGPU_ERR_INVALID_PARAMETER, "list_ids must be a permutation of 0..num_vectors");
+        seen[lids[i]] = 1;
+    }
+    for (size_t i = 0; i < nv * M; i++)
+        if (cds[i] >= K) throw Error(VGPU_ERR_INVALID_PARAMETER, "code outside the codebook");
+    centroids.assign(cent, cent + L * d);
+    codebooks.assign(cb, cb + M * K * ds);
+    offsets.assign(off, off + L + 1);
+    list_ids.assign(lids, lids + nv);
+    codes.assign(cds, cds + nv * M);
+    doc_ids.resize(nv);
+    for (size_t i = 0; i < nv; i++) doc_ids[i] = dids ? dids[i] : (uint32_t)i;
+    if (vecs) {
+        vectors.assign(vecs, vecs + nv * d);
+        has_vectors = true;
+    } else {
+        vectors.clear();
+        has_vectors = false;
+    }
+    if (has_vectors) d_vectors.upload(vectors.data(), nv * d, stream);
+    d_centroids.upload(centroids.data(), L * d, stream);
+    d_codebooks.upload(codebooks.data(), codebooks.size(), stream);
+    upload_index();
+    built = true;
+}
+
+// HBM layout of the search path (the list-major caches of
+// build_scan_caches, search.rs:816-848, plus the FAST term).
+void IvfpqIndex::upload_index() {
+    const size_t n = this->n();
+    std::vector<uint32_t> off32(L + 1);
+    for (size_t l = 0; l <= L; l++) off32[l] = (uint32_t)offsets[l];
+    std::vector<uint8_t> lm(n * M);
+    for (size_t p = 0; p < n; p++) std::memcpy(&lm[p * M], &codes[(size_t)list_ids[p] * M], M);
+    d_offsets.upload(off32.data(), L + 1, stream);
+    d_list_ids.upload(list_ids.data(), n, stream);
+    d_doc_ids.upload(doc_ids.data(), n, stream);
+    d_codes.upload(lm.data(), n * M, stream);
+    if (!has_vectors) d_vectors.release();
+
+    double cm = 0.0;
+    for (size_t c = 0; c < L; c++) cm = std::max(cm, (double)row_norm_bound(&centroids[c * d], d));
+    double rr = 0.0;
+    for (size_t m = 0; m < M; m++) {
+        double best = 0.0;
+        for (size_t k = 0; k < K; k++) {
+            double s = 0.0;
+            for (size_t j = 0; j < ds; j++) {
+                double v = codebooks[(m * K + k) * ds + j];
+                s += v * v;
+            }
+            best = std::max(best, s);
+        }
+        rr += best;
+    }
+    dix = DevIndex{};
+    dix.d = (int)d;
+    dix.L = (int)L;
+    dix.M = (int)M;
+    dix.K = (int)K;
+    dix.ds = (int)ds;
+    dix.n = (uint32_t)n;
+    dix.centroids = d_centroids.p;
+    dix.codebooks = d_codebooks.p;
+    dix.offsets = d_offsets.p;
+    dix.list_ids = d_list_ids.p;
+    dix.codes = d_codes.p;
+    dix.doc_ids = d_doc_ids.p;
+    dix.vectors = has_vectors ? d_vectors.p : nullptr;
+    dix.cmax = (float)(cm * 1.0001);
+    dix.rmax = (float)(std::sqrt(rr) * 1.0001 + 1e-30);
+    if (K == 16) {
+        std::vector<uint32_t> poff(L + 1, 0);
+        for (size_t l = 0; l < L; l++) {
+            uint64_t len = offsets[l + 1] - offsets[l];
+            poff[l + 1] = poff[l] + (len >= 16 ? (uint32_t)((len + 31) / 32) : 0u);
+        }
+        d_pack_off.upload(poff.data(), L + 1, stream);
+        d_packed.reserve((size_t)poff[L] * 16 * M + 16);
+        dix.pack_off = d_pack_off.p;
+        dix.packed = d_packed.p;
+        launch_pack4(dix, d_packed.p, stream);
+        d_bias.release();
+    } else {
+        d_bias.reserve(n);
+        dix.bias = d_bias.p;
+        launch_bias(dix, d_bias.p, stream);
+    }
+    VGPU_HIP(hipGetLastError());
+    VGPU_HIP(hipStreamSynchronize(stream));
+}
+
+static int fast_keep(size_t kout) {
+    int kk = 1;
+    while ((size_t)kk < kout + 16) kk <<= 1;
+    return std::max(kk, 32);
+}
+
+void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t nprobe, size_t pool,
+                               int64_t* d_ids, float* d_dists, hipStream_t s) {
+    if (!built) throw Error(VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
+    if (!s) s = stream;
+    stats = vgpu_search_stats{};
+    stats.nq = (uint32_t)nq;
+    if (nq == 0 || k == 0) return;
+    if (pool && !has_vectors)
+        throw Error(VGPU_ERR_UNSUPPORTED, "search_reranked after compact(): raw vectors were dropped");
+    size_t P = nprobe ? nprobe : params.nprobe;
+    P = std::min(P, L);
+    const size_t kout = pool ? std::max(pool, k) : k;
+    if (kout > 2048) throw Error(VGPU_ERR_INVALID_PARAMETER, "k / rerank_pool above 2048 is not supported");
+    if (P > 1024) throw Error(VGPU_ERR_INVALID_PARAMETER, "nprobe above 1024 is not supported");
+    {
+        ScanArgs probe_shape;
+        probe_shape.P = (int)P;
+        probe_shape.kout = (int)kout;
+        probe_shape.kk = K == 16 ? (int)kout : fast_keep(kout);
+        size_t lds = K == 16 ? fastscan_lds_bytes(dix, probe_shape) : scan8_lds_bytes(dix, probe_shape);
+        if (lds > 160 * 1024)
+            throw Error(VGPU_ERR_UNSUPPORTED, "scan working set of " + std::to_string(lds) +
+                                                  " bytes exceeds the 160 KiB of LDS per workgroup");
+    }
+    if (P == 0) {  // no probed list: every row is padding
+        launch_finalize(nullptr, nullptr, nullptr, (int)nq, 0, (int)k, d_ids, d_dists, s);
+        VGPU_HIP(hipGetLastError());
+        VGPU_HIP(hipStreamSynchronize(s));
+        return;
+    }
+    size_t chunk = std::max<size_t>(1, std::min<size_t>(nq, ((size_t)1 << 28) / L));
+    chunk = std::min<size_t>(chunk, 65536);
+    w_qn.reserve(chunk * d);
+    w_qnorm.reserve(chunk);
+    w_dots.reserve(chunk * L);
+    w_probe.reserve(chunk * P);
+    w_vidx.reserve(chunk * kout);
+    w_dist.reserve(chunk * kout);
+    w_vidx2.reserve(chunk * k);
+    w_dist2.reserve(chunk * k);
+    w_flags.reserve(chunk);
+    w_counters.reserve(2);
+    w_overflow.reserve(1);
+    VGPU_HIP(hipMemsetAsync(w_counters.p, 0, 2 * sizeof(unsigned long long), s));
+    VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
+    float t[7] = {0, 0, 0, 0, 0, 0, 0};
+    for (size_t q0 = 0; q0 < nq; q0 += chunk) {
+        const size_t nc = std::min(chunk, nq - q0);
+        if (profiling) VGPU_HIP(hipEventRecord(ev[0], s));
+        launch_normalize(d_q + q0 * d, w_qn.p, w_qnorm.p, (int)nc, (int)d, s);
+        if (profiling) VGPU_HIP(hipEventRecord(ev[1], s));
+        launch_coarse_dots(w_qn.p, d_centroids.p, w_dots.p, (int)nc, (int)L, (int)d, s);
+        if (profiling) VGPU_HIP(hipEventRecord(ev[2], s));
+        launch_coarse_select(w_dots.p, w_qn.p, w_qnorm.p, d_centroids.p, (int)nc, (int)L, (int)d,
+                             (int)P, dix.cmax, w_probe.p, w_overflow.p, s);
+        if (profiling) VGPU_HIP(hipEventRecord(ev[3], s));
+        ScanArgs a;
+        a.qn = w_qn.p;
+        a.qnorm = w_qnorm.p;
+        a.probe = w_probe.p;
+        a.nq = (int)nc;
+        a.P = (int)P;
+        a.kout = (int)kout;
+        a.flags = w_flags.p;
+        a.out_vidx = w_vidx.p;
+        a.out_dist = w_dist.p;
+        a.counters = w_counters.p;
+        if (K == 16) {
+            a.kk = (int)kout;
+            launch_fastscan(dix, a, s);
+            if (profiling) VGPU_HIP(hipEventRecord(ev[4], s));
+        } else if (mode == VGPU_MODE_FAST) {
+            VGPU_HIP(hipMemsetAsync(w_flags.p, 0, nc * sizeof(uint32_t), s));
+            a.kk = fast_keep(kout);
+            a.exact = 0;
+            launch_scan8(dix, a, s);
+            if (profiling) VGPU_HIP(hipEventRecord(ev[4], s));
+            a.kk = (int)kout;
+            a.exact = 1;
+            a.only_flagged = 1;
+            launch_scan8(dix, a, s);
+        } else {
+            a.kk = (int)kout;
+            a.exact = 1;
+            launch_scan8(dix, a, s);
+            if (profiling) VGPU_HIP(hipEventRecord(ev[4], s));
+        }
+        if (profiling) VGPU_HIP(hipEventRecord(ev[5], s));
+        const uint32_t* vout = w_vidx.p;
+        const float* dout = w_dist.p;
+        size_t kin = kout;
+        if (pool) {
+            launch_rerank(dix, w_qn.p, (int)nc, w_vidx.p, (int)kout, (int)k, w_vidx2.p, w_dist2.p, s);
+            vout = w_vidx2.p;
+            dout = w_dist2.p;
+            kin = k;
+        }
+        if (profiling) VGPU_HIP(hipEventRecord(ev[6], s));
+        launch_finalize(vout, dout, d_doc_ids.p, (int)nc, (int)kin, (int)k, d_ids + q0 * k,
+                        d_dists + q0 * k, s);
+        if (profiling) VGPU_HIP(hipEventRecord(ev[7], s));
+        VGPU_HIP(hipGetLastError());
+        if (profiling) {
+            VGPU_HIP(hipEventSynchronize(ev[7]));
+            float ms;
+            for (int i = 0; i < 7; i++) {
+                VGPU_HIP(hipEventElapsedTime(&ms, ev[i], ev[i + 1]));
+                t[i] += ms;
+            }
+        }
+    }
+    unsigned long long cnt[2] = {0, 0};
+    unsigned int ovf = 0;
+    VGPU_HIP(hipMemcpyAsync(cnt, w_counters.p, sizeof(cnt), hipMemcpyDeviceToHost, s));
+    VGPU_HIP(hipMemcpyAsync(&ovf, w_overflow.p, sizeof(ovf), hipMemcpyDeviceToHost, s));
+    VGPU_HIP(hipStreamSynchronize(s));
+    stats.ms_normalize = t[0];
+    stats.ms_coarse = t[1];
+    stats.ms_select = t[2];
+    stats.ms_scan = t[3];
+    stats.ms_fallback = t[4];
+    stats.ms_rerank = t[5];
+    stats.ms_total = t[0] + t[1] + t[2] + t[3] + t[4] + t[5] + t[6];
+    stats.candidates = cnt[0];
+    stats.fallback_queries = (uint32_t)cnt[1];
+    stats.coarse_overflow = ovf;
+    stats.scan_bytes = K == 16 ? cnt[0] * (uint64_t)(M / 2 + 4) : cnt[0] * (uint64_t)(M + 4);
+}
+
+void IvfpqIndex::search_host(const float* q, size_t nq, size_t k, size_t nprobe, size_t pool,
+                             int64_t* ids, float* dists) {
+    for (size_t i = 0; i < nq * d; i++)
+        if (!std::isfinite(q[i])) throw Error(VGPU_ERR_INVALID_PARAMETER, "query contains a non-finite value");
+    if (nq == 0 || k == 0) {
+        if (!built) throw Error(VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
+        return;
+    }
+    w_q.upload(q, nq * d, stream);
+    w_ids.reserve(nq * k);
+    w_odist.reserve(nq * k);
+    search_device(w_q.p, nq, k, nprobe, pool, w_ids.p, w_odist.p, stream);
+    VGPU_HIP(hipMemcpyAsync(ids, w_ids.p, nq * k * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    VGPU_HIP(hipMemcpyAsync(dists, w_odist.p, nq * k * sizeof(float), hipMemcpyDeviceToHost, stream));
+    VGPU_HIP(hipStreamSynchronize(stream));
+}
+
+void IvfpqIndex::probe_host(const float* q, size_t nq, size_t nprobe, uint32_t* lists) {
+    if (!built) throw Error(VGPU_ERR_NOT_BUILT, "IVF-PQ index: probe before build");
+    size_t P = std::min(nprobe, L);
+    if (nq == 0 || P == 0) return;
+    if (P > 1024) throw Error(VGPU_ERR_INVALID_PARAMETER, "nprobe above 1024 is not supported");
+    w_q.upload(q, nq * d, stream);
+    w_qn.reserve(nq * d);
+    w_qnorm.reserve(nq);
+    w_probe.reserve(nq * P);
+    w_overflow.reserve(1);
+    VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), stream));
+    size_t chunk = std::max<size_t>(1, std::min<size_t>(nq, ((size_t)1 << 28) / L));
+    w_dots.reserve(chunk * L);
+    launch_normalize(w_q.p, w_qn.p, w_qnorm.p, (int)nq, (int)d, stream);
+    for (size_t q0 = 0; q0 < nq; q0 += chunk) {
+        size_t nc = std::min(chunk, nq - q0);
+        launch_coarse_dots(w_qn.p + q0 * d, d_centroids.p, w_dots.p, (int)nc, (int)L, (int)d, stream);
+        launch_coarse_select(w_dots.p, w_qn.p + q0 * d, w_qnorm.p + q0, d_centroids.p, (int)nc, (int)L,
+                             (int)d, (int)P, dix.cmax, w_probe.p + q0 * P, w_overflow.p, stream);
+    }
+    VGPU_HIP(hipGetLastError());
+    VGPU_HIP(hipMemcpyAsync(lists, w_probe.p, nq * P * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+    VGPU_HIP(hipStreamSynchronize(stream));
+}
+
+}  // namespace vgpu

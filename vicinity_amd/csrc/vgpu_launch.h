@@ -1,0 +1,87 @@
+// Host-side launchers of the gfx950 kernels (one .hip file per kernel family).
+// Shapes are validated by the callers in vgpu_index.cpp before any launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vgpu {
+
+// HBM-resident IVF-PQ index (all pointers are device memory).
+struct DevIndex {
+    int d = 0, L = 0, M = 0, K = 0, ds = 0;
+    uint32_t n = 0;
+    const float* centroids = nullptr;  // [L*d] row-major
+    const float* codebooks = nullptr;  // [M*K*ds] codebook, codeword, dim
+    const uint32_t* offsets = nullptr; // [L+1] list l = positions [off[l], off[l+1])
+    const uint32_t* list_ids = nullptr;// [n] insertion index at each position
+    const uint8_t* codes = nullptr;    // [n*M] codes at each position (list-major rows)
+    const float* bias = nullptr;       // [n] ||x_r||^2 + 2 c.x_r at each position (K != 16)
+    const uint32_t* doc_ids = nullptr; // [n] by insertion index
+    const float* vectors = nullptr;    // [n*d] by insertion index, normalised (may be null)
+    const uint8_t* packed = nullptr;   // FastScan blocks of every list (K == 16)
+    const uint32_t* pack_off = nullptr;// [L+1] block offset of each list (K == 16)
+    float cmax = 0.f;                  // max ||c||
+    float rmax = 0.f;                  // max ||decoded residual||
+};
+
+struct ScanArgs {
+    const float* qn = nullptr;      // [nq*d] normalised queries
+    const float* qnorm = nullptr;   // [nq] ||q_n||
+    const uint32_t* probe = nullptr;// [nq*P] probed lists, probe order
+    int nq = 0, P = 0;
+    int kout = 0;                   // results kept per query (k, or the rerank pool)
+    int kk = 0;                     // FAST: kept before rescoring (>= kout); EXACT: kout
+    int exact = 0;                  // 1 = EXACT mode
+    int only_flagged = 0;           // run only queries with flags[q] != 0
+    uint32_t* flags = nullptr;      // [nq] FAST margin failures (written), read when only_flagged
+    uint32_t* out_vidx = nullptr;   // [nq*kout] insertion indices, 0xffffffff padding
+    float* out_dist = nullptr;      // [nq*kout]
+    unsigned long long* counters = nullptr; // [0] candidates, [1] fallbacks
+};
+
+void launch_normalize(const float* x, float* out, float* norms, int n, int d, hipStream_t s);
+void launch_coarse_dots(const float* Q, const float* C, float* D, int nq, int L, int d,
+                        hipStream_t s);
+// Probe selection with exact rescoring: probe[q*P..] = the P lists of smallest
+// 1 - dot (ties: lower list index), ascending.  D is overwritten on overflow.
+void launch_coarse_select(float* D, const float* qn, const float* qnorm, const float* C,
+                          int nq, int L, int d, int P, float cmax, uint32_t* probe,
+                          unsigned int* overflow, hipStream_t s);
+
+size_t scan8_lds_bytes(const DevIndex& ix, const ScanArgs& a);
+void launch_scan8(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
+size_t fastscan_lds_bytes(const DevIndex& ix, const ScanArgs& a);
+void launch_fastscan(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
+
+// Exact rerank of the scan's pool: 1 - q.v over stored vectors
+// (search.rs:1148-1156), top-k by (distance, insertion index).
+void launch_rerank(const DevIndex& ix, const float* qn, int nq, const uint32_t* pool_vidx,
+                   int pool, int k, uint32_t* out_vidx, float* out_dist, hipStream_t s);
+// Map insertion indices to doc ids and pad with (-1, +inf) (python.rs:778-785).
+void launch_finalize(const uint32_t* vidx, const float* dist, const uint32_t* doc_ids, int nq,
+                     int kin, int k, int64_t* out_ids, float* out_dists, hipStream_t s);
+
+// Build side.
+// codes[i*M + m] = argmin_k ||x_i,m - c_{assign_i},m - cw_mk||^2 (pq.rs:136-161);
+// centroids/assign may be null (x is then the residual itself).
+void launch_encode(const float* x, int n, int d, const float* centroids, const uint32_t* assign,
+                   const float* codebooks, int M, int K, int ds, uint8_t* codes, hipStream_t s);
+void launch_bias(const DevIndex& ix, float* bias, hipStream_t s);
+void launch_pack4(const DevIndex& ix, uint8_t* packed, hipStream_t s);
+// LUT kernels for tests.
+void launch_adc_tables(const float* codebooks, int M, int K, int ds, const float* r, int nr,
+                       float* tables, hipStream_t s);
+void launch_fastscan_test(const uint8_t* packed, int n, int M, const float* lut, float* out,
+                          hipStream_t s);
+
+// Flat exact search.
+void launch_flat_norms(const float* X, int n, int d, float* norms, hipStream_t s);
+size_t flat_partial_count(int nq, int n, int k);
+// Qsq / Xnorm: squared norms (flat_norms); xmax: max ||x||.
+void launch_flat_search(const float* Q, const float* Qsq, int nq, const float* X,
+                        const float* Xnorm, int n, int d, int k, int metric, float xmax,
+                        uint64_t* partial, uint32_t* out_idx, float* out_dist,
+                        unsigned int* overflow, hipStream_t s);
+
+}  // namespace vgpu

@@ -1,0 +1,152 @@
+// Host runtime: device buffers, HIP error mapping and the IVF-PQ / flat index
+// objects behind the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/vicinity_gpu.h"
+#include "vgpu_launch.h"
+
+namespace vgpu {
+
+// Error carrying a vicinity status code; caught at the C ABI boundary.
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+void hip_check(hipError_t e, const char* what);
+#define VGPU_HIP(expr) ::vgpu::hip_check((expr), #expr)
+
+template <typename T>
+struct DevBuf {
+    T* p = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    ~DevBuf() { release(); }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    // Grow-only allocation (contents are not preserved on growth).
+    void reserve(size_t count) {
+        if (count <= n && p) return;
+        release();
+        size_t bytes = (count ? count : 1) * sizeof(T);
+        hipError_t e = hipMalloc((void**)&p, bytes);
+        if (e != hipSuccess) {
+            p = nullptr;
+            (void)hipGetLastError();
+            throw Error(VGPU_ERR_OUT_OF_MEMORY,
+                        "device allocation of " + std::to_string(bytes) + " bytes failed");
+        }
+        n = count;
+    }
+    void upload(const T* h, size_t count, hipStream_t s) {
+        reserve(count);
+        if (count) VGPU_HIP(hipMemcpyAsync(p, h, count * sizeof(T), hipMemcpyHostToDevice, s));
+    }
+};
+
+// A built IVF-PQ index.  Mirrors the state of IVFPQIndex
+// (src/ivf_pq/search.rs:212-239): the raw normalised vectors and doc ids on
+// the host, the search arrays resident in HBM.
+struct IvfpqIndex {
+    size_t d = 0;
+    vgpu_ivfpq_params params{};
+    int mode = VGPU_MODE_FAST;
+    bool built = false;
+    bool has_vectors = true;
+    bool profiling = false;
+
+    std::vector<float> vectors;     // [n*d] normalised (search.rs:503-508)
+    std::vector<uint32_t> doc_ids;  // [n]
+
+    size_t L = 0, K = 0, M = 0, ds = 0;
+    std::vector<float> centroids;   // [L*d]
+    std::vector<float> codebooks;   // [M*K*ds]
+    std::vector<uint64_t> offsets;  // [L+1]
+    std::vector<uint32_t> list_ids; // [n]
+    std::vector<uint8_t> codes;     // [n*M] insertion order
+
+    hipStream_t stream = nullptr;
+    hipEvent_t ev[8] = {};
+    DevBuf<float> d_centroids, d_codebooks, d_bias, d_vectors;
+    DevBuf<uint32_t> d_offsets, d_list_ids, d_doc_ids, d_pack_off;
+    DevBuf<uint8_t> d_codes, d_packed;
+    DevIndex dix;
+
+    // search workspace
+    DevBuf<float> w_q, w_qn, w_qnorm, w_dots, w_dist, w_dist2, w_odist;
+    DevBuf<uint32_t> w_probe, w_vidx, w_vidx2, w_flags;
+    DevBuf<int64_t> w_ids;
+    DevBuf<unsigned long long> w_counters;
+    DevBuf<unsigned int> w_overflow;
+    vgpu_search_stats stats{};
+    std::mutex mu;
+
+    IvfpqIndex(size_t dim, const vgpu_ivfpq_params& p);
+    ~IvfpqIndex();
+
+    size_t n() const { return doc_ids.size(); }
+    void add(const uint32_t* ids, const float* x, size_t count);
+    void build(size_t sample, size_t max_iter);
+    void load(const float* cent, size_t Lc, const float* cb, size_t Kc, const uint64_t* off,
+              const uint32_t* lids, const uint8_t* cds, const uint32_t* dids, const float* vecs,
+              size_t nv);
+    void upload_index();
+    // Device-pointer batch search on stream s (s may be null = own stream).
+    void search_device(const float* d_q, size_t nq, size_t k, size_t nprobe, size_t pool,
+                       int64_t* d_ids, float* d_dists, hipStream_t s);
+    void search_host(const float* q, size_t nq, size_t k, size_t nprobe, size_t pool,
+                     int64_t* ids, float* dists);
+    void probe_host(const float* q, size_t nq, size_t nprobe, uint32_t* lists);
+
+  private:
+    void kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k, uint64_t seed,
+                       size_t max_iter, std::vector<float>& cent);
+    void assign_cosine(const float* d_x, const float* d_norms, size_t nx, const float* d_cent,
+                       size_t k, float cmax, uint32_t* d_assign, hipStream_t s);
+    void train_pq(const std::vector<float>& res, size_t nt, size_t Kc, uint64_t seed,
+                  size_t max_iter);
+};
+
+struct FlatIndex {
+    size_t d = 0;
+    int metric = 0;
+    size_t n = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev[4] = {};
+    DevBuf<float> d_x, d_xnorm, w_q, w_dist, w_odist, w_qnorm;
+    DevBuf<uint64_t> w_partial;
+    DevBuf<uint32_t> w_idx;
+    DevBuf<int64_t> w_ids;
+    DevBuf<unsigned int> w_overflow;
+    std::vector<float> host;
+    double xmax2 = 0.0;  // max ||x||^2
+    float ms_gemm = 0.f, ms_total = 0.f;
+    std::mutex mu;
+
+    FlatIndex(size_t dim, int met);
+    ~FlatIndex();
+    void add(const float* x, size_t count);
+    void search_device(const float* d_q, size_t nq, size_t k, int64_t* d_ids, float* d_dists,
+                       hipStream_t s);
+};
+
+// Host-side seeded sampling shared with the build (splitmix64 partial
+// Fisher-Yates, ascending sample).
+void sample_indices(size_t n, size_t sample, uint64_t seed, std::vector<uint32_t>& out);
+void draw_distinct(size_t n, size_t count, uint64_t seed, std::vector<uint32_t>& out);
+void normalize_row(const float* x, size_t d, float* out);
+
+}  // namespace vgpu
