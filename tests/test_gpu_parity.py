@@ -311,3 +311,28 @@ def test_flat_search_is_bitexact(vg, oracle):
     ids, dists = fc.search(xq, 7)
     oids, odists = oracle.flat_search(xb, xq, 7, metric=1)
     _assert_same_results(ids, dists, oids, odists)
+
+
+@pytest.mark.parametrize("copies,k", [(40, 9), (700, 5), (700, 100)])
+def test_fast_scan_ties_and_fallback_match_oracle(vg, oracle, copies, k):
+    """Byte codes with heavy exact duplicates: equal approximate distances at
+    the buffer threshold (ties kept), and with 700 copies more ties than the
+    buffer holds, which sends the query to the EXACT kernel.  Both must return
+    the oracle's rows (ties ordered by insertion index)."""
+    from vicinity_amd import IVFPQIndex
+
+    _print_case(f"fast ties copies={copies} k={k}")
+    rng = np.random.default_rng(copies + k)
+    distinct = rng.standard_normal((60, 16)).astype(np.float32)
+    x = np.concatenate([np.repeat(distinct[:1], copies, axis=0), np.repeat(distinct[1:], 20, axis=0)])
+    vecs = oracle.normalize_rows(x)
+    oix, _ = oracle.ivfpq_build(vecs, 4, 4, 256, 9, 0, 10)
+    ix = IVFPQIndex(16, num_clusters=4, num_codebooks=4, codebook_size=256, nprobe=4)
+    ix.load_artifacts(oix.centroids, oix.codebooks, oix.list_offsets, oix.list_ids, oix.codes,
+                      vectors=vecs)
+    q = np.concatenate([distinct[:3], rng.standard_normal((5, 16)).astype(np.float32)])
+    for mode in ["fast", "exact"]:
+        ix.set_mode(mode)
+        ids, dists = ix.batch_search(q, k, nprobe=4)
+        oids, odists = oix.search_batch(q, k, 4)
+        _assert_same_results(ids, dists, oids, odists)

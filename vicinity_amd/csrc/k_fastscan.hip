@@ -121,25 +121,6 @@ __device__ inline void wave_bitonic_sort_keys(uint64_t* keys, int n) {
     wave_sync();
 }
 
-__device__ inline void block_bitonic_sort_keys(uint64_t* keys, int n) {
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            __syncthreads();
-            for (int t = threadIdx.x; t < (n >> 1); t += blockDim.x) {
-                int i = 2 * t - (t & (stride - 1));
-                int j = i + stride;
-                bool asc = (i & size) == 0;
-                uint64_t a = keys[i], b = keys[j];
-                if ((a > b) == asc) {
-                    keys[i] = b;
-                    keys[j] = a;
-                }
-            }
-        }
-    }
-    __syncthreads();
-}
-
 // Per-wave top-k buffer in LDS.
 struct WaveTopk {
     uint64_t* keys;  // [buf]

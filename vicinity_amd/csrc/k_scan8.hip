@@ -10,15 +10,8 @@
 // r = q - c and the table LUT[m][k] = sum_j (r_j - cw_j)^2 (sub, mul, add in
 // order) live in LDS; each candidate sums its M entries in codebook order.
 //
-// FAST mode ranks with the decomposition
-//     ||r - x_r||^2 = ||q - c||^2 + (||x_r||^2 + 2 c.x_r) - 2 q.x_r
-// where the middle term b(x) is stored per list entry at upload and the last
-// term is a per-query table T2[m][k] = -2 q_m.cw_mk built once per query, so
-// no per-(query, list) table is built.  It keeps kk >= k candidates, checks
-// that the kept set provably contains the reference's top-k (gap between the
-// kk-th and k-th approximate distance > 2 tau), rescoring those kk with the
-// EXACT arithmetic; a query that fails the check is flagged and rerun in EXACT
-// mode by the host.
+// This kernel serves EXACT mode and the queries FAST mode (k_scan8_fast.hip)
+// could not prove; it writes the same rows FAST mode would have written.
 #include "vgpu_device.h"
 #include "vgpu_launch.h"
 
@@ -215,128 +208,6 @@ __device__ inline void write_out(const ScanArgs& a, ScanLds& s, int q, int n) {
     }
 }
 
-// The reference's distance of one list entry (pq.rs:232-251 table entries
-// summed in codebook order, pq_simd.rs:349-355): residual r = q - c, then per
-// codebook dist_m = sum_j (r_j - cw_j)^2, total = sum_m dist_m.
-__device__ inline float exact_entry_distance(const DevIndex& ix, const float* qs, uint32_t list,
-                                             uint32_t pos) {
-    const int d = ix.d, M = ix.M, K = ix.K, ds = ix.ds;
-    const float* c = ix.centroids + (size_t)list * d;
-    const uint8_t* row = ix.codes + (size_t)pos * M;
-    float total = 0.0f;
-    for (int m = 0; m < M; m++) {
-        const float* cw = ix.codebooks + ((size_t)m * K + row[m]) * ds;
-        float e = 0.0f;
-        for (int j = 0; j < ds; j++) {
-            float r = qs[m * ds + j] - c[m * ds + j];
-            float diff = r - cw[j];
-            e += diff * diff;
-        }
-        total += e;
-    }
-    return total;
-}
-
-// Error bound between the FAST ranking distance and the exact one, for
-// ||q|| <= qn, ||c|| <= cmax, ||x_r|| <= rmax, ||q - c||^2 <= t0max.
-__device__ inline float fast_tau(int d, int M, int ds, float qn, float cmax, float rmax,
-                                 float t0max) {
-    const float u = 5.9604645e-08f;
-    float rr = sqrtf(t0max) + rmax;
-    float S = 2.0f * (qn + cmax) * rmax + 2.0f * rmax * rmax + 2.0f * rr * rr;
-    return 4.0f * (float)(d + M + ds + 8) * u * S + 1e-30f;
-}
-
-template <int MT, int KT>
-__global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a, int buf) {
-    extern __shared__ __align__(16) char smem[];
-    const int q = blockIdx.x;
-    if (q >= a.nq) return;
-    const int tid = threadIdx.x;
-    const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds, P = a.P;
-    ScanLds s = carve(smem, d, M, K, P, buf);
-    load_query_and_lists(ix, a, s, q);
-    __syncthreads();
-    // ||q - c||^2 per probed list, sequential.
-    for (int p = tid; p < P; p += blockDim.x) {
-        const float* c = ix.centroids + (size_t)s.lid[p] * d;
-        float acc = 0.0f;
-        for (int j = 0; j < d; j++) {
-            float t = s.qs[j] - c[j];
-            acc += t * t;
-        }
-        s.term0[p] = acc;
-    }
-    // Per-query table T2[m][k] = -2 q_m . cw_mk.
-    for (int e = tid; e < M * K; e += blockDim.x) {
-        const int m = e / K;
-        const float* cw = ix.codebooks + (size_t)e * ds;
-        float acc = 0.0f;
-        for (int j = 0; j < ds; j++) acc += s.qs[m * ds + j] * cw[j];
-        s.lut[e] = -2.0f * acc;
-    }
-    __syncthreads();
-    const uint32_t total = s.pref[P];
-    int cur = 0;
-    for (uint32_t base = 0; base < total; base += SCAN_ROUND) {
-        if (*s.tk.count > (uint32_t)(buf - SCAN_ROUND)) topk_flush(s.tk, a.kk);
-        const uint32_t thr = *s.tk.thr;
-#pragma unroll
-        for (int u = 0; u < SCAN_U; u++) {
-            uint32_t t = base + u * VGPU_BLOCK + tid;
-            bool take = false;
-            uint32_t fk = 0, pos = 0;
-            if (t < total) {
-                while (t >= s.pref[cur + 1]) cur++;
-                pos = s.lbeg[cur] + (t - s.pref[cur]);
-                float dist = s.term0[cur] + ix.bias[pos];
-                dist = adc_sum<MT, KT>(ix.codes + (size_t)pos * M, s.lut, M, K, dist);
-                fk = fkey(dist);
-                take = fk <= thr;
-            }
-            topk_push(s.tk, take, fk, pos, cur, ix.list_ids);
-        }
-        __syncthreads();
-    }
-    topk_flush(s.tk, a.kk);
-    const int n = (int)*s.tk.count;
-    // Margin check: every candidate outside the kept set has approximate
-    // distance >= kept[n-1]; if kept[n-1] - kept[k-1] > 2 tau the exact top-k
-    // lies inside the kept set.
-    if (tid == 0) {
-        uint32_t fail = 0;
-        if (total > (uint32_t)n && n >= a.kout && a.kout > 0) {
-            float t0max = 0.0f;
-            for (int p = 0; p < P; p++) t0max = fmaxf(t0max, s.term0[p]);
-            float tau = fast_tau(d, M, ds, a.qnorm[q], ix.cmax, ix.rmax, t0max);
-            float gap = key_dist(s.tk.keys[n - 1]) - key_dist(s.tk.keys[a.kout - 1]);
-            if (!(gap > 2.0f * tau)) fail = 1;
-        }
-        s.misc[2] = fail;
-        if (a.counters) atomicAdd(&a.counters[0], (unsigned long long)total);
-        if (fail) {
-            a.flags[q] = 1u;
-            if (a.counters) atomicAdd(&a.counters[1], 1ull);
-        }
-    }
-    __syncthreads();
-    if (s.misc[2]) return;
-    // Rescore the kept entries with the reference arithmetic.
-    for (int t = tid; t < n; t += blockDim.x) {
-        uint32_t vidx = (uint32_t)s.tk.keys[t];
-        float ex = exact_entry_distance(ix, s.qs, s.lid[s.tk.probe[t]], s.tk.pos[t]);
-        s.tk.keys[t] = cand_key(ex, vidx);
-    }
-    int n2 = next_pow2(n > 0 ? n : 1);
-    for (int t = n + tid; t < n2; t += blockDim.x) {
-        s.tk.keys[t] = ~0ull;
-        s.tk.pos[t] = 0;
-        s.tk.probe[t] = 0;
-    }
-    block_bitonic_sort2(s.tk.keys, s.tk.pos, s.tk.probe, n2);
-    write_out(a, s, q, n < a.kout ? n : a.kout);
-}
-
 template <int MT, int KT>
 __global__ __launch_bounds__(256) void scan8_exact_kernel(DevIndex ix, ScanArgs a, int buf) {
     extern __shared__ __align__(16) char smem[];
@@ -402,15 +273,9 @@ template <int MT, int KT>
 static void launch_mk(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     int buf = scan_buf(a.kk);
     size_t lds = scan8_lds_bytes(ix, a);
-    if (a.exact) {
-        auto k = scan8_exact_kernel<MT, KT>;
-        (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), lds, s, ix, a, buf);
-    } else {
-        auto k = scan8_fast_kernel<MT, KT>;
-        (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), lds, s, ix, a, buf);
-    }
+    auto k = scan8_exact_kernel<MT, KT>;
+    (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), lds, s, ix, a, buf);
 }
 
 template <int KT>
@@ -426,7 +291,7 @@ static void launch_k(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     }
 }
 
-void launch_scan8(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
+void launch_scan8_exact(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     if (a.nq <= 0) return;
     if (ix.K == 256) launch_k<256>(ix, a, s);
     else launch_k<0>(ix, a, s);

@@ -1,0 +1,506 @@
+// FAST-mode ADC scan for byte codes (codebook_size != 16): one workgroup of
+// 256 threads per query, the per-query table resident in LDS, the probed
+// lists streamed from HBM with one round of software prefetch.
+//
+// Reference: search_approx_internal_observed src/ivf_pq/search.rs:1175-1391
+// (per probed list: residual r = q - c, compute_adc_table_into
+// src/ivf_pq/pq.rs:232-251, adc_batch_256_into src/pq_simd.rs:330-369);
+// finish_top_k_by_distance search.rs:64-75.
+//
+// Ranking.  The reference distance of an entry x in list l is
+//     ||r - x_r||^2 = ||q - c||^2 + (||x_r||^2 + 2 c.x_r) - 2 q.x_r .
+// The middle term b(x) is stored per list position at upload, the first is
+// one value per probed list, the last is a per-query table T2[m][k] =
+// -2 q_m.cw_mk, so the scan needs one table per query (not one per probed
+// list) and one 4-byte load per entry besides its codes.  Every approximate
+// distance a is within tau of the reference's float32 distance e
+// (fast_tau, below).
+//
+// Selection.  Entries with fkey(a) <= thr are appended to an LDS buffer;
+// when the buffer fills, a block radix select finds the keep-th smallest key
+// T and the buffer is compacted to the entries <= T, which become the new
+// threshold.  The buffer therefore always holds every scanned entry with
+// key <= thr.  At the end, with A_k the k-th smallest approximate distance,
+// the reference's top-k lies inside R = {a <= A_k + 2 tau}: the k entries with
+// the smallest a have e <= A_k + tau, so the k-th smallest e is at most
+// A_k + tau, and any entry of the exact top-k has a <= e + tau <= A_k + 2 tau.
+// If the buffer provably holds R (A_k + 2 tau <= thr), R is rescored with the
+// reference's arithmetic and sorted by (distance, insertion index);
+// otherwise the query is flagged and rerun by the EXACT kernel.
+#include "vgpu_device.h"
+#include "vgpu_launch.h"
+
+namespace vgpu {
+
+#define FS_U 2                          // entries per thread per round
+#define FS_ROUND (VGPU_BLOCK * FS_U)    // entries per round
+
+// Codes of one list entry held in registers.
+template <int MT>
+struct CodeRow {
+    uint32_t w[MT >= 4 ? MT / 4 : 1];
+};
+
+template <int MT>
+__device__ __forceinline__ void load_row(CodeRow<MT>& r, const uint8_t* __restrict__ p) {
+    if constexpr (MT % 16 == 0) {
+        const uint4* v = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+        for (int i = 0; i < MT / 16; i++) {
+            uint4 x = v[i];
+            r.w[4 * i] = x.x;
+            r.w[4 * i + 1] = x.y;
+            r.w[4 * i + 2] = x.z;
+            r.w[4 * i + 3] = x.w;
+        }
+    } else if constexpr (MT == 8) {
+        uint2 x = *reinterpret_cast<const uint2*>(p);
+        r.w[0] = x.x;
+        r.w[1] = x.y;
+    } else {
+        static_assert(MT == 4, "row width");
+        r.w[0] = *reinterpret_cast<const uint32_t*>(p);
+    }
+}
+
+// sum_m lut[m*K + code_m] with four partial sums (ranking only; the order of
+// the additions is covered by tau).  The table is a static LDS array at a
+// fixed address, so each lookup is one byte-select shift plus an
+// immediate-offset LDS read.
+template <int MT, int KT>
+__device__ __forceinline__ float row_sum(const CodeRow<MT>& r, const float* __restrict__ lut) {
+    static_assert(MT >= 4 && MT % 4 == 0, "row width");
+    const uint32_t w0 = r.w[0];
+    float s0 = lut[0 * KT + (w0 & 0xffu)];
+    float s1 = lut[1 * KT + ((w0 >> 8) & 0xffu)];
+    float s2 = lut[2 * KT + ((w0 >> 16) & 0xffu)];
+    float s3 = lut[3 * KT + (w0 >> 24)];
+#pragma unroll
+    for (int i = 1; i < MT / 4; i++) {
+        const uint32_t w = r.w[i];
+        s0 += lut[(4 * i + 0) * KT + (w & 0xffu)];
+        s1 += lut[(4 * i + 1) * KT + ((w >> 8) & 0xffu)];
+        s2 += lut[(4 * i + 2) * KT + ((w >> 16) & 0xffu)];
+        s3 += lut[(4 * i + 3) * KT + (w >> 24)];
+    }
+    return (s0 + s1) + (s2 + s3);
+}
+
+// Generic M / K: bytes straight from global memory.
+__device__ __forceinline__ float row_sum_generic(const uint8_t* __restrict__ p,
+                                                 const float* __restrict__ lut, int M, int K) {
+    float s0 = 0.0f, s1 = 0.0f;
+    int m = 0;
+    for (; m + 1 < M; m += 2) {
+        s0 += lut[m * K + p[m]];
+        s1 += lut[(m + 1) * K + p[m + 1]];
+    }
+    if (m < M) s0 += lut[m * K + p[m]];
+    return s0 + s1;
+}
+
+// Bound on |a - e| for ||q|| <= qn, ||c|| <= cmax, ||x_r|| <= rmax and
+// ||q - c||^2 <= t0max (u = 2^-24).  With rr = sqrt(t0max) + rmax >= ||r - x_r||:
+//   |e - D| <= (ds + M) u rr^2 + 2u (||q - c|| rr + rr^2)     (reference arithmetic)
+//   |a - D| <= (d + M + ds + 4) u (t0max + rmax^2 + 2 (cmax + qn) rmax)
+// where D is the real-number distance; both are below
+// (d + M + ds + 8) u S with S = 2 (qn + cmax) rmax + 2 rmax^2 + 2 rr^2, which
+// is taken with a factor of 4 to spare.
+__device__ __forceinline__ float fast_tau(int d, int M, int ds, float qn, float cmax, float rmax,
+                                          float t0max) {
+    const float u = 5.9604645e-08f;
+    float rr = sqrtf(t0max) + rmax;
+    float S = 2.0f * (qn + cmax) * rmax + 2.0f * rmax * rmax + 2.0f * rr * rr;
+    return 4.0f * (float)(d + M + ds + 8) * u * S + 1e-30f;
+}
+
+struct FastLds {
+    float* lut;      // [M * max(K, 64)] table, then rescoring scratch
+    uint64_t* keys;  // [buf] (fkey(a) << 32) | position
+    float* qs;       // [d]
+    uint32_t* lid;   // [P]
+    uint32_t* lbeg;  // [P]
+    uint32_t* llen;  // [P]
+    uint32_t* pref;  // [P + 1]
+    float* term0;    // [P] ||q - c||^2
+    RadixScratch* rs;
+    uint32_t* misc;  // [0] count [1] thr [2] fail [3..4] flush flags by round parity
+};
+
+__host__ __device__ inline size_t fs8_align(size_t x) { return (x + 15) & ~(size_t)15; }
+
+__host__ __device__ inline int fs8_buf(int keep) {
+    int need = keep + FS_ROUND;
+    int b = 1;
+    while (b < need) b <<= 1;
+    return b;
+}
+
+// Dynamic LDS layout; the table region is omitted when the kernel holds the
+// table in a static array (static_lut: compile-time M and K = 256).
+__host__ __device__ inline size_t fs8_layout(int d, int M, int K, int P, int buf, bool static_lut,
+                                             size_t* off) {
+    size_t o = 0;
+    const int KL = K > 64 ? K : 64;
+    off[0] = o; o = static_lut ? 0 : fs8_align(o + (size_t)M * KL * 4);  // lut
+    off[1] = o; o = fs8_align(o + (size_t)buf * 8);        // keys
+    off[2] = o; o = fs8_align(o + (size_t)d * 4);          // qs
+    off[3] = o; o = fs8_align(o + (size_t)P * 4);          // lid
+    off[4] = o; o = fs8_align(o + (size_t)P * 4);          // lbeg
+    off[5] = o; o = fs8_align(o + (size_t)P * 4);          // llen
+    off[6] = o; o = fs8_align(o + (size_t)(P + 1) * 4);    // pref
+    off[7] = o; o = fs8_align(o + (size_t)P * 4);          // term0
+    off[8] = o; o = fs8_align(o + sizeof(RadixScratch));   // radix scratch
+    off[9] = o; o = fs8_align(o + 8 * 4);                  // misc
+    return o;
+}
+
+__device__ inline FastLds fs8_carve(char* smem, float* static_lut, int d, int M, int K, int P,
+                                    int buf) {
+    size_t off[10];
+    fs8_layout(d, M, K, P, buf, static_lut != nullptr, off);
+    FastLds s;
+    s.lut = static_lut ? static_lut : (float*)(smem + off[0]);
+    s.keys = (uint64_t*)(smem + off[1]);
+    s.qs = (float*)(smem + off[2]);
+    s.lid = (uint32_t*)(smem + off[3]);
+    s.lbeg = (uint32_t*)(smem + off[4]);
+    s.llen = (uint32_t*)(smem + off[5]);
+    s.pref = (uint32_t*)(smem + off[6]);
+    s.term0 = (float*)(smem + off[7]);
+    s.rs = (RadixScratch*)(smem + off[8]);
+    s.misc = (uint32_t*)(smem + off[9]);
+    return s;
+}
+
+// Keep the buffer entries whose high word is <= T (in place, chunk by chunk:
+// a chunk is read into registers before any of its slots are rewritten, and
+// the compacted prefix never passes the end of the chunk being read).  With
+// `relabel`, each kept key is rewritten as (probe slot << 32) | position.
+__device__ inline uint32_t fs8_compact(FastLds& s, uint32_t n, uint32_t T, bool relabel, int P) {
+    const int tid = threadIdx.x;
+    __syncthreads();
+    if (tid == 0) s.misc[0] = 0;
+    __syncthreads();
+    for (uint32_t c0 = 0; c0 < n; c0 += VGPU_BLOCK) {
+        const uint32_t i = c0 + tid;
+        uint64_t v = i < n ? s.keys[i] : ~0ull;
+        bool take = i < n && (uint32_t)(v >> 32) <= T;
+        __syncthreads();
+        if (take && relabel) {
+            const uint32_t pos = (uint32_t)v;
+            uint32_t p = 0;
+            for (int j = 0; j < P; j++)
+                if (pos - s.lbeg[j] < s.llen[j]) p = (uint32_t)j;
+            v = ((uint64_t)p << 32) | pos;
+        }
+        int slot = wave_append_slot(take, &s.misc[0]);
+        if (take) s.keys[slot] = v;
+        __syncthreads();
+    }
+    return s.misc[0];
+}
+
+// Buffer full: keep the `keep` smallest keys (plus ties); at most `cap`
+// survive, otherwise the query is marked failed.  Clears the flag of `parity`.
+__device__ inline void fs8_flush(FastLds& s, int keep, uint32_t cap, int parity) {
+    __syncthreads();
+    const uint32_t n = s.misc[0];
+    if (threadIdx.x == 0) s.misc[3 + parity] = 0u;
+    if (n <= (uint32_t)keep) {
+        __syncthreads();
+        return;
+    }
+    auto hk = [&](int i) -> uint32_t { return (uint32_t)(s.keys[i] >> 32); };
+    const uint32_t T = block_radix_select<uint32_t>(hk, (int)n, (uint32_t)(keep - 1), s.rs);
+    const uint32_t kept = fs8_compact(s, n, T, false, 0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (kept > cap) {
+            s.misc[0] = cap;
+            s.misc[2] = 1u;
+        }
+        s.misc[1] = T;
+    }
+    __syncthreads();
+}
+
+// Per-thread state of the entries one thread handles in one round.  The
+// loads are unconditional (a slot past the end reads position 0, which exists
+// whenever anything is scanned) so the compiler can wait for one round's
+// loads while the next round's are still in flight.
+template <int MT>
+struct RoundRegs {
+    CodeRow<MT> row[FS_U];
+    float bias[FS_U];
+    float t0[FS_U];    // ||q - c||^2 of the entry's list
+    uint32_t pos[FS_U];// 0xffffffff = no entry
+};
+
+template <int MT>
+__device__ __forceinline__ void fs8_fetch(const DevIndex& ix, const FastLds& s, uint32_t rbase,
+                                          uint32_t total, int& cur, RoundRegs<MT>& g) {
+#pragma unroll
+    for (int u = 0; u < FS_U; u++) {
+        const uint32_t t = rbase + u * VGPU_BLOCK + threadIdx.x;
+        const bool valid = t < total;
+        if (valid)
+            while (t >= s.pref[cur + 1]) cur++;
+        const uint32_t pos = valid ? s.lbeg[cur] + (t - s.pref[cur]) : 0u;
+        g.pos[u] = valid ? pos : 0xffffffffu;
+        g.t0[u] = s.term0[cur];
+        if constexpr (MT > 0) load_row<MT>(g.row[u], ix.codes + (size_t)pos * MT);
+        g.bias[u] = ix.bias[pos];
+    }
+}
+
+// Score one round of entries and append those with fkey(a) <= thr.  A wave
+// whose appends took the buffer past `cap` raises flag misc[3 + parity]: the
+// final count is the largest count any wave saw, so the flag is raised
+// exactly when the buffer needs a flush.  The two parities alternate between
+// rounds, and a raised flag is cleared inside the flush, so a flag is never
+// written while another wave may still be reading it.
+template <int MT, int KT>
+__device__ __forceinline__ void fs8_consume(const DevIndex& ix, FastLds& s, const float* lut_static,
+                                            const RoundRegs<MT>& g, uint32_t thr, uint32_t cap,
+                                            int parity) {
+    uint32_t seen = 0;
+#pragma unroll
+    for (int u = 0; u < FS_U; u++) {
+        const bool ok = g.pos[u] != 0xffffffffu;
+        float dist;
+        if constexpr (MT > 0 && KT > 0) {
+            dist = (g.t0[u] + g.bias[u]) + row_sum<MT, KT>(g.row[u], lut_static);
+        } else {
+            const uint32_t pos = ok ? g.pos[u] : 0u;
+            dist = (g.t0[u] + g.bias[u]) + row_sum_generic(ix.codes + (size_t)pos * ix.M, s.lut, ix.M, ix.K);
+        }
+        const uint32_t fk = fkey(dist);
+        const bool take = ok && fk <= thr;
+        uint32_t after = 0;
+        int slot = wave_append_slot_count(take, &s.misc[0], &after);
+        if (take) s.keys[slot] = ((uint64_t)fk << 32) | g.pos[u];
+        seen = after > seen ? after : seen;
+    }
+    if (seen > cap && (threadIdx.x & 63) == 0) s.misc[3 + parity] = 1u;
+}
+
+template <int MT, int KT>
+__global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a, int buf) {
+    constexpr bool kStatic = MT > 0 && KT >= 64;
+    __shared__ __align__(16) float slut[kStatic ? MT * KT : 1];
+    extern __shared__ __align__(16) char smem[];
+    const int q = blockIdx.x;
+    if (q >= a.nq) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds, P = a.P;
+    FastLds s = fs8_carve(smem, kStatic ? slut : nullptr, d, M, K, P, buf);
+
+    // ---- prologue: query, probed lists, ||q - c||^2, the per-query table.
+    for (int j = tid; j < d; j += VGPU_BLOCK) s.qs[j] = a.qn[(size_t)q * d + j];
+    for (int p = tid; p < P; p += VGPU_BLOCK) {
+        const uint32_t l = a.probe[(size_t)q * P + p];
+        const bool ok = l < (uint32_t)ix.L;  // no such list: scanned as empty
+        const uint32_t b = ok ? ix.offsets[l] : 0u;
+        s.lid[p] = ok ? l : 0u;
+        s.lbeg[p] = b;
+        s.llen[p] = ok ? ix.offsets[l + 1] - b : 0u;
+    }
+    if (tid < 8) s.misc[tid] = tid == 1 ? 0xffffffffu : 0u;  // count 0, thr +inf, flags 0
+    __syncthreads();
+    if (tid < 64) {  // exclusive prefix of the list lengths
+        uint32_t carry = 0;
+        for (int p0 = 0; p0 < P; p0 += 64) {
+            const int p = p0 + lane;
+            const uint32_t own = p < P ? s.llen[p] : 0u;
+            uint32_t x = own;
+            for (int o = 1; o < 64; o <<= 1) {
+                uint32_t y = __shfl_up(x, o, 64);
+                if (lane >= o) x += y;
+            }
+            if (p < P) s.pref[p] = carry + x - own;
+            carry += __shfl(x, 63, 64);
+        }
+        if (lane == 0) s.pref[P] = carry;
+    }
+    {  // ||q - c||^2: eight lanes per probed list
+        const int g = tid >> 3, sub = tid & 7;
+        for (int p0 = 0; p0 < P; p0 += VGPU_BLOCK / 8) {
+            const int p = p0 + g;
+            float acc = 0.0f;
+            if (p < P) {
+                const float* c = ix.centroids + (size_t)s.lid[p] * d;
+                for (int j = sub; j < d; j += 8) {
+                    const float t = s.qs[j] - c[j];
+                    acc = __builtin_fmaf(t, t, acc);
+                }
+            }
+            acc += __shfl_xor(acc, 1, 64);
+            acc += __shfl_xor(acc, 2, 64);
+            acc += __shfl_xor(acc, 4, 64);
+            if (p < P && sub == 0) s.term0[p] = acc;
+        }
+    }
+    // T2[m][k] = -2 q_m . cw_mk
+    for (int e = tid; e < M * K; e += VGPU_BLOCK) {
+        const int m = e / K;
+        const float* cw = ix.codebooks + (size_t)e * ds;
+        const float* qm = s.qs + m * ds;
+        float acc = 0.0f;
+        if (ds == 8) {
+            const float4 c0 = reinterpret_cast<const float4*>(cw)[0];
+            const float4 c1 = reinterpret_cast<const float4*>(cw)[1];
+            acc = __builtin_fmaf(qm[0], c0.x, acc);
+            acc = __builtin_fmaf(qm[1], c0.y, acc);
+            acc = __builtin_fmaf(qm[2], c0.z, acc);
+            acc = __builtin_fmaf(qm[3], c0.w, acc);
+            acc = __builtin_fmaf(qm[4], c1.x, acc);
+            acc = __builtin_fmaf(qm[5], c1.y, acc);
+            acc = __builtin_fmaf(qm[6], c1.z, acc);
+            acc = __builtin_fmaf(qm[7], c1.w, acc);
+        } else if (ds == 2) {
+            const float2 c0 = reinterpret_cast<const float2*>(cw)[0];
+            acc = __builtin_fmaf(qm[0], c0.x, acc);
+            acc = __builtin_fmaf(qm[1], c0.y, acc);
+        } else {
+            for (int j = 0; j < ds; j++) acc = __builtin_fmaf(qm[j], cw[j], acc);
+        }
+        s.lut[e] = -2.0f * acc;
+    }
+    __syncthreads();
+
+    // ---- scan: FS_ROUND entries per round, next round's loads in flight.
+    const uint32_t total = s.pref[P];
+    const int keep = a.kk;
+    const uint32_t cap = (uint32_t)(buf - FS_ROUND);
+    int cur = 0;
+    RoundRegs<MT> ga, gb;
+    if (total > 0) fs8_fetch<MT>(ix, s, 0, total, cur, ga);
+    for (uint32_t rb = 0; rb < total; rb += 2 * FS_ROUND) {
+        fs8_fetch<MT>(ix, s, rb + FS_ROUND, total, cur, gb);
+        fs8_consume<MT, KT>(ix, s, slut, ga, s.misc[1], cap, 0);
+        __syncthreads();
+        if (s.misc[3]) fs8_flush(s, keep, cap, 0);
+        if (rb + FS_ROUND >= total) break;
+        fs8_fetch<MT>(ix, s, rb + 2 * FS_ROUND, total, cur, ga);
+        fs8_consume<MT, KT>(ix, s, slut, gb, s.misc[1], cap, 1);
+        __syncthreads();
+        if (s.misc[4]) fs8_flush(s, keep, cap, 1);
+    }
+    __syncthreads();
+
+    // ---- proof that the buffer holds R, then rescoring.
+    uint32_t n = s.misc[0];
+    const uint32_t thr = s.misc[1];
+    const int kout = a.kout;
+    bool fail = s.misc[2] != 0u;
+    uint32_t bk = 0xffffffffu;
+    if (!fail && n > (uint32_t)kout) {
+        auto hk = [&](int i) -> uint32_t { return (uint32_t)(s.keys[i] >> 32); };
+        const uint32_t Ak = block_radix_select<uint32_t>(hk, (int)n, (uint32_t)(kout - 1), s.rs);
+        float t0max = 0.0f;
+        for (int p = 0; p < P; p++) t0max = fmaxf(t0max, s.term0[p]);
+        const float tau = fast_tau(d, M, ds, a.qnorm[q], ix.cmax, ix.rmax, t0max);
+        const float bound = fkey_to_float(Ak) + 2.0f * tau;
+        bk = fkey(bound);
+        bk = bk < 0xfffffffeu ? bk + 1u : 0xffffffffu;  // one ulp to spare
+        if (thr != 0xffffffffu && bk > thr) fail = true;
+    }
+    if (tid == 0 && a.counters) atomicAdd(&a.counters[0], (unsigned long long)total);
+    if (fail) {
+        if (tid == 0) {
+            a.flags[q] = 1u;
+            if (a.counters) atomicAdd(&a.counters[1], 1ull);
+        }
+        return;
+    }
+    n = fs8_compact(s, n, bk, true, P);  // R, keys relabelled (probe slot, position)
+
+    const int KL = K > 64 ? K : 64;  // rescoring chunk: KL entries x M codebooks
+    for (uint32_t c0 = 0; c0 < n; c0 += (uint32_t)KL) {
+        const uint32_t cn = min((uint32_t)KL, n - c0);
+        for (uint32_t t = tid; t < cn * (uint32_t)M; t += VGPU_BLOCK) {
+            const uint32_t i = c0 + t / (uint32_t)M;
+            const int m = (int)(t % (uint32_t)M);
+            const uint64_t v = s.keys[i];
+            const uint32_t pos = (uint32_t)v, p = (uint32_t)(v >> 32);
+            const uint8_t code = ix.codes[(size_t)pos * M + m];
+            const float* cw = ix.codebooks + ((size_t)m * K + code) * ds;
+            const float* c = ix.centroids + (size_t)s.lid[p] * d + m * ds;
+            const float* qm = s.qs + m * ds;
+            // pq.rs:232-251 on r = q - c (search.rs:1242-1245), no contraction.
+            float e = 0.0f;
+            for (int j = 0; j < ds; j++) {
+                const float r = qm[j] - c[j];
+                const float diff = r - cw[j];
+                e = __fadd_rn(e, __fmul_rn(diff, diff));
+            }
+            s.lut[t] = e;
+        }
+        __syncthreads();
+        for (uint32_t i = c0 + tid; i < c0 + cn; i += VGPU_BLOCK) {
+            const float* em = s.lut + (size_t)(i - c0) * M;
+            float total_e = 0.0f;  // pq_simd.rs:349-355: m = 0..M-1 from 0.0
+            for (int m = 0; m < M; m++) total_e += em[m];
+            const uint32_t pos = (uint32_t)s.keys[i];
+            s.keys[i] = cand_key(total_e, ix.list_ids[pos]);
+        }
+        __syncthreads();
+    }
+    const int n2 = next_pow2(n > 0 ? (int)n : 1);
+    for (int t = (int)n + tid; t < n2; t += VGPU_BLOCK) s.keys[t] = ~0ull;
+    block_bitonic_sort_keys(s.keys, n2);
+    for (int j = tid; j < kout; j += VGPU_BLOCK) {
+        const size_t o = (size_t)q * kout + j;
+        if ((uint32_t)j < n) {
+            a.out_vidx[o] = (uint32_t)s.keys[j];
+            a.out_dist[o] = key_dist(s.keys[j]);
+        } else {
+            a.out_vidx[o] = 0xffffffffu;
+            a.out_dist[o] = __int_as_float(0x7f800000);
+        }
+    }
+}
+
+// Static table bytes of the specialisations (compile-time M, K = 256).
+static size_t static_lut_bytes(const DevIndex& ix) {
+    if (ix.K != 256) return 0;
+    switch (ix.M) {
+        case 4: case 8: case 16: case 32: case 48: case 64: return (size_t)ix.M * 256 * 4;
+        default: return 0;
+    }
+}
+
+size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
+    size_t off[10];
+    const size_t st = static_lut_bytes(ix);
+    return st + fs8_layout(ix.d, ix.M, ix.K, a.P, fs8_buf(a.kk), st != 0, off);
+}
+
+template <int MT, int KT>
+static void launch_fast_mk(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
+    const int buf = fs8_buf(a.kk);
+    size_t off[10];
+    const size_t dyn = fs8_layout(ix.d, ix.M, ix.K, a.P, buf, MT > 0 && KT >= 64, off);
+    auto k = scan8_fast_kernel<MT, KT>;
+    (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn);
+    hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), dyn, s, ix, a, buf);
+}
+
+void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
+    if (a.nq <= 0) return;
+    if (ix.K == 256) {
+        switch (ix.M) {
+            case 4: launch_fast_mk<4, 256>(ix, a, s); return;
+            case 8: launch_fast_mk<8, 256>(ix, a, s); return;
+            case 16: launch_fast_mk<16, 256>(ix, a, s); return;
+            case 32: launch_fast_mk<32, 256>(ix, a, s); return;
+            case 48: launch_fast_mk<48, 256>(ix, a, s); return;
+            case 64: launch_fast_mk<64, 256>(ix, a, s); return;
+            default: break;
+        }
+    }
+    launch_fast_mk<0, 0>(ix, a, s);
+}
+
+}  // namespace vgpu

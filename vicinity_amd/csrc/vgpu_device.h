@@ -1,6 +1,7 @@
 // Device helpers shared by the gfx950 kernels: total-order float keys, a
 // block-wide bitonic sort in LDS, a block-wide radix select and wave-level
-// append for top-k buffers.  Every kernel runs with 256 threads (4 waves of 64).
+// append for top-k buffers.  The block-wide helpers assume 256 threads (4
+// waves of 64), the launch shape of every kernel that calls them.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -44,7 +45,7 @@ __device__ void block_bitonic_sort(uint64_t* keys, P* pay, int n) {
     for (int size = 2; size <= n; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             __syncthreads();
-            for (int t = threadIdx.x; t < (n >> 1); t += blockDim.x) {
+            for (int t = threadIdx.x; t < (n >> 1); t += VGPU_BLOCK) {
                 int i = 2 * t - (t & (stride - 1));
                 int j = i + stride;
                 bool asc = (i & size) == 0;
@@ -68,7 +69,7 @@ __device__ void block_bitonic_sort2(uint64_t* keys, P* pay, Q* pay2, int n) {
     for (int size = 2; size <= n; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             __syncthreads();
-            for (int t = threadIdx.x; t < (n >> 1); t += blockDim.x) {
+            for (int t = threadIdx.x; t < (n >> 1); t += VGPU_BLOCK) {
                 int i = 2 * t - (t & (stride - 1));
                 int j = i + stride;
                 bool asc = (i & size) == 0;
@@ -82,6 +83,26 @@ __device__ void block_bitonic_sort2(uint64_t* keys, P* pay, Q* pay2, int n) {
                     Q qa = pay2[i];
                     pay2[i] = pay2[j];
                     pay2[j] = qa;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Ascending bitonic sort of keys[0..n) (n a power of two), keys only.
+__device__ inline void block_bitonic_sort_keys(uint64_t* keys, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (int t = threadIdx.x; t < (n >> 1); t += VGPU_BLOCK) {
+                int i = 2 * t - (t & (stride - 1));
+                int j = i + stride;
+                bool asc = (i & size) == 0;
+                uint64_t a = keys[i], b = keys[j];
+                if ((a > b) == asc) {
+                    keys[i] = b;
+                    keys[j] = a;
                 }
             }
         }
@@ -113,9 +134,9 @@ __device__ KeyT block_radix_select(KeyFn key_of, int n, uint32_t rank, RadixScra
     KeyT prefix = 0, mask = 0;
     for (int shift = (int)(sizeof(KeyT) * 8) - 8; shift >= 0; shift -= 8) {
         __syncthreads();
-        for (int i = tid; i < 256; i += blockDim.x) rs->hist[i] = 0;
+        for (int i = tid; i < 256; i += VGPU_BLOCK) rs->hist[i] = 0;
         __syncthreads();
-        for (int i = tid; i < n; i += blockDim.x) {
+        for (int i = tid; i < n; i += VGPU_BLOCK) {
             KeyT k = key_of(i);
             if ((k & mask) == prefix) atomicAdd(&rs->hist[(uint32_t)(k >> shift) & 255u], 1u);
         }
@@ -169,5 +190,25 @@ __device__ __forceinline__ int wave_append_slot(bool take, uint32_t* counter) {
     uint32_t base = 0;
     if ((int)(threadIdx.x & 63) == leader) base = atomicAdd(counter, (uint32_t)__popcll(m));
     base = __shfl(base, leader, 64);
+    return take ? (int)(base + below) : -1;
+}
+
+// As wave_append_slot, and *after receives the counter value just after this
+// wave's reservation (the same in every lane; unchanged when no lane takes).
+__device__ __forceinline__ int wave_append_slot_count(bool take, uint32_t* counter,
+                                                      uint32_t* after) {
+    uint64_t m = __ballot(take);
+    if (m == 0) {
+        *after = 0;
+        return -1;
+    }
+    uint32_t lo = (uint32_t)m, hi = (uint32_t)(m >> 32);
+    uint32_t below = __builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u));
+    int leader = __ffsll((unsigned long long)m) - 1;
+    uint32_t cnt = (uint32_t)__popcll(m);
+    uint32_t base = 0;
+    if ((int)(threadIdx.x & 63) == leader) base = atomicAdd(counter, cnt);
+    base = __shfl(base, leader, 64);
+    *after = base + cnt;
     return take ? (int)(base + below) : -1;
 }

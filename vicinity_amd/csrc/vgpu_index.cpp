@@ -451,7 +451,9 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
         probe_shape.P = (int)P;
         probe_shape.kout = (int)kout;
         probe_shape.kk = K == 16 ? (int)kout : fast_keep(kout);
-        size_t lds = K == 16 ? fastscan_lds_bytes(dix, probe_shape) : scan8_lds_bytes(dix, probe_shape);
+        size_t lds = K == 16 ? fastscan_lds_bytes(dix, probe_shape)
+                             : std::max(scan8_fast_lds_bytes(dix, probe_shape),
+                                        scan8_lds_bytes(dix, probe_shape));
         if (lds > 160 * 1024)
             throw Error(VGPU_ERR_UNSUPPORTED, "scan working set of " + std::to_string(lds) +
                                                   " bytes exceeds the 160 KiB of LDS per workgroup");
@@ -507,16 +509,16 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             VGPU_HIP(hipMemsetAsync(w_flags.p, 0, nc * sizeof(uint32_t), s));
             a.kk = fast_keep(kout);
             a.exact = 0;
-            launch_scan8(dix, a, s);
+            launch_scan8_fast(dix, a, s);
             if (profiling) VGPU_HIP(hipEventRecord(ev[4], s));
             a.kk = (int)kout;
             a.exact = 1;
             a.only_flagged = 1;
-            launch_scan8(dix, a, s);
+            launch_scan8_exact(dix, a, s);
         } else {
             a.kk = (int)kout;
             a.exact = 1;
-            launch_scan8(dix, a, s);
+            launch_scan8_exact(dix, a, s);
             if (profiling) VGPU_HIP(hipEventRecord(ev[4], s));
         }
         if (profiling) VGPU_HIP(hipEventRecord(ev[5], s));

@@ -31,7 +31,7 @@ struct ScanArgs {
     const uint32_t* probe = nullptr;// [nq*P] probed lists, probe order
     int nq = 0, P = 0;
     int kout = 0;                   // results kept per query (k, or the rerank pool)
-    int kk = 0;                     // FAST: kept before rescoring (>= kout); EXACT: kout
+    int kk = 0;                     // FAST: entries a flush keeps (> kout); EXACT: kout
     int exact = 0;                  // 1 = EXACT mode
     int only_flagged = 0;           // run only queries with flags[q] != 0
     uint32_t* flags = nullptr;      // [nq] FAST margin failures (written), read when only_flagged
@@ -49,8 +49,13 @@ void launch_coarse_select(float* D, const float* qn, const float* qnorm, const f
                           int nq, int L, int d, int P, float cmax, uint32_t* probe,
                           unsigned int* overflow, hipStream_t s);
 
+// EXACT mode: the reference's per-(query, list) residual table in LDS.
 size_t scan8_lds_bytes(const DevIndex& ix, const ScanArgs& a);
-void launch_scan8(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
+void launch_scan8_exact(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
+// FAST mode: per-query decomposed table, threshold buffer, exact rescoring of
+// the provable candidate set; unprovable queries get flags[q] = 1.
+size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a);
+void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 size_t fastscan_lds_bytes(const DevIndex& ix, const ScanArgs& a);
 void launch_fastscan(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 
