@@ -254,17 +254,22 @@ __device__ __forceinline__ void fs8_fetch(const DevIndex& ix, const FastLds& s, 
     }
 }
 
-// Score one round of entries and append those with fkey(a) <= thr.  A wave
-// whose appends took the buffer past `cap` raises flag misc[3 + parity]: the
-// final count is the largest count any wave saw, so the flag is raised
-// exactly when the buffer needs a flush.  The two parities alternate between
-// rounds, and a raised flag is cleared inside the flush, so a flag is never
-// written while another wave may still be reading it.
+// Score one round of entries and append those with fkey(a) <= thr, with one
+// LDS atomic per wave.  A wave whose appends took the buffer past `cap`
+// raises flag misc[3 + parity]: the final count is the largest count any wave
+// saw, so the flag is raised exactly when the buffer needs a flush.  The two
+// parities alternate between rounds, and a raised flag is cleared inside the
+// flush, so a flag is never written while another wave may still read it.
+// Every thread of the block calls this (all lanes active).
 template <int MT, int KT>
 __device__ __forceinline__ void fs8_consume(const DevIndex& ix, FastLds& s, const float* lut_static,
                                             const RoundRegs<MT>& g, uint32_t thr, uint32_t cap,
                                             int parity) {
-    uint32_t seen = 0;
+    const int lane = threadIdx.x & 63;
+    bool take[FS_U];
+    uint32_t fk[FS_U], before[FS_U];
+    uint64_t mask[FS_U];
+    uint32_t tot = 0;
 #pragma unroll
     for (int u = 0; u < FS_U; u++) {
         const bool ok = g.pos[u] != 0xffffffffu;
@@ -273,27 +278,92 @@ __device__ __forceinline__ void fs8_consume(const DevIndex& ix, FastLds& s, cons
             dist = (g.t0[u] + g.bias[u]) + row_sum<MT, KT>(g.row[u], lut_static);
         } else {
             const uint32_t pos = ok ? g.pos[u] : 0u;
-            dist = (g.t0[u] + g.bias[u]) + row_sum_generic(ix.codes + (size_t)pos * ix.M, s.lut, ix.M, ix.K);
+            dist = (g.t0[u] + g.bias[u]) +
+                   row_sum_generic(ix.codes + (size_t)pos * ix.M, s.lut, ix.M, ix.K);
         }
-        const uint32_t fk = fkey(dist);
-        const bool take = ok && fk <= thr;
-        uint32_t after = 0;
-        int slot = wave_append_slot_count(take, &s.misc[0], &after);
-        if (take) s.keys[slot] = ((uint64_t)fk << 32) | g.pos[u];
-        seen = after > seen ? after : seen;
+        fk[u] = fkey(dist);
+        take[u] = ok && fk[u] <= thr;
+        mask[u] = __ballot(take[u]);
+        before[u] = tot;
+        tot += (uint32_t)__popcll(mask[u]);
     }
-    if (seen > cap && (threadIdx.x & 63) == 0) s.misc[3 + parity] = 1u;
+    if (tot == 0) return;  // wave-uniform
+    uint32_t base = 0;
+    if (lane == 0) base = atomicAdd(&s.misc[0], tot);
+    base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+    for (int u = 0; u < FS_U; u++) {
+        if (take[u]) {
+            const uint32_t below = __builtin_amdgcn_mbcnt_hi(
+                (uint32_t)(mask[u] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask[u], 0u));
+            s.keys[base + before[u] + below] = ((uint64_t)fk[u] << 32) | g.pos[u];
+        }
+    }
+    if (base + tot > cap && lane == 0) s.misc[3 + parity] = 1u;
 }
 
-template <int MT, int KT>
+// DS consecutive floats into registers (vector loads when aligned).
+template <int DS>
+__device__ __forceinline__ void load_vec(const float* __restrict__ p, float* v) {
+    if constexpr (DS % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < DS / 4; i++) {
+            const float4 x = reinterpret_cast<const float4*>(p)[i];
+            v[4 * i] = x.x;
+            v[4 * i + 1] = x.y;
+            v[4 * i + 2] = x.z;
+            v[4 * i + 3] = x.w;
+        }
+    } else if constexpr (DS == 2) {
+        const float2 x = reinterpret_cast<const float2*>(p)[0];
+        v[0] = x.x;
+        v[1] = x.y;
+    } else {
+#pragma unroll
+        for (int j = 0; j < DS; j++) v[j] = p[j];
+    }
+}
+
+// The reference's distance contribution of codebook m for one entry
+// (pq.rs:232-251 on r = q - c, search.rs:1242-1245): sub, sub, mul, add in
+// dimension order, no contraction.
+template <int DS>
+__device__ __forceinline__ float exact_sub_distance(const float* qm, const float* c,
+                                                    const float* cw, int ds) {
+    float e = 0.0f;
+    if constexpr (DS > 0) {
+        float cv[DS], wv[DS];
+        load_vec<DS>(c, cv);
+        load_vec<DS>(cw, wv);
+#pragma unroll
+        for (int j = 0; j < DS; j++) {
+            const float r = __fsub_rn(qm[j], cv[j]);
+            const float diff = __fsub_rn(r, wv[j]);
+            e = __fadd_rn(e, __fmul_rn(diff, diff));
+        }
+    } else {
+        for (int j = 0; j < ds; j++) {
+            const float r = __fsub_rn(qm[j], c[j]);
+            const float diff = __fsub_rn(r, cw[j]);
+            e = __fadd_rn(e, __fmul_rn(diff, diff));
+        }
+    }
+    return e;
+}
+
+// MT, KT, DS: compile-time codebooks, codebook size and subvector dimension
+// (0 = read from the index at run time).
+template <int MT, int KT, int DS>
 __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a, int buf) {
     constexpr bool kStatic = MT > 0 && KT >= 64;
+    constexpr int D = MT * DS;  // compile-time dimension when > 0
     __shared__ __align__(16) float slut[kStatic ? MT * KT : 1];
     extern __shared__ __align__(16) char smem[];
     const int q = blockIdx.x;
     if (q >= a.nq) return;
     const int tid = threadIdx.x, lane = tid & 63;
-    const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds, P = a.P;
+    const int d = D > 0 ? D : ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K;
+    const int ds = DS > 0 ? DS : ix.ds, P = a.P;
     FastLds s = fs8_carve(smem, kStatic ? slut : nullptr, d, M, K, P, buf);
 
     // ---- prologue: query, probed lists, ||q - c||^2, the per-query table.
@@ -323,16 +393,29 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
         }
         if (lane == 0) s.pref[P] = carry;
     }
-    {  // ||q - c||^2: eight lanes per probed list
+    {  // ||q - c||^2: eight lanes per probed list (ranking only: any order)
         const int g = tid >> 3, sub = tid & 7;
         for (int p0 = 0; p0 < P; p0 += VGPU_BLOCK / 8) {
             const int p = p0 + g;
             float acc = 0.0f;
             if (p < P) {
                 const float* c = ix.centroids + (size_t)s.lid[p] * d;
-                for (int j = sub; j < d; j += 8) {
-                    const float t = s.qs[j] - c[j];
-                    acc = __builtin_fmaf(t, t, acc);
+                if constexpr (D > 0 && D % 32 == 0) {
+                    float cv[D / 8];
+#pragma unroll
+                    for (int i = 0; i < D / 32; i++) load_vec<4>(c + 32 * i + 4 * sub, cv + 4 * i);
+#pragma unroll
+                    for (int i = 0; i < D / 32; i++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const float t = s.qs[32 * i + 4 * sub + j] - cv[4 * i + j];
+                            acc = __builtin_fmaf(t, t, acc);
+                        }
+                } else {
+                    for (int j = sub; j < d; j += 8) {
+                        const float t = s.qs[j] - c[j];
+                        acc = __builtin_fmaf(t, t, acc);
+                    }
                 }
             }
             acc += __shfl_xor(acc, 1, 64);
@@ -341,31 +424,35 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
             if (p < P && sub == 0) s.term0[p] = acc;
         }
     }
-    // T2[m][k] = -2 q_m . cw_mk
-    for (int e = tid; e < M * K; e += VGPU_BLOCK) {
-        const int m = e / K;
-        const float* cw = ix.codebooks + (size_t)e * ds;
-        const float* qm = s.qs + m * ds;
-        float acc = 0.0f;
-        if (ds == 8) {
-            const float4 c0 = reinterpret_cast<const float4*>(cw)[0];
-            const float4 c1 = reinterpret_cast<const float4*>(cw)[1];
-            acc = __builtin_fmaf(qm[0], c0.x, acc);
-            acc = __builtin_fmaf(qm[1], c0.y, acc);
-            acc = __builtin_fmaf(qm[2], c0.z, acc);
-            acc = __builtin_fmaf(qm[3], c0.w, acc);
-            acc = __builtin_fmaf(qm[4], c1.x, acc);
-            acc = __builtin_fmaf(qm[5], c1.y, acc);
-            acc = __builtin_fmaf(qm[6], c1.z, acc);
-            acc = __builtin_fmaf(qm[7], c1.w, acc);
-        } else if (ds == 2) {
-            const float2 c0 = reinterpret_cast<const float2*>(cw)[0];
-            acc = __builtin_fmaf(qm[0], c0.x, acc);
-            acc = __builtin_fmaf(qm[1], c0.y, acc);
-        } else {
-            for (int j = 0; j < ds; j++) acc = __builtin_fmaf(qm[j], cw[j], acc);
+    // T2[m][k] = -2 q_m . cw_mk (ranking only: FMA allowed)
+    if constexpr (MT > 0 && KT > 0 && DS > 0 && (MT * KT) % VGPU_BLOCK == 0) {
+        constexpr int NE = MT * KT / VGPU_BLOCK;           // entries per thread
+        constexpr int G = DS >= 8 ? 4 : (NE < 8 ? NE : 8);  // entries whose loads fly together
+        static_assert(NE % G == 0, "table split");
+#pragma unroll
+        for (int g0 = 0; g0 < NE; g0 += G) {
+            float wv[G][DS];
+#pragma unroll
+            for (int i = 0; i < G; i++)
+                load_vec<DS>(ix.codebooks + (size_t)((g0 + i) * VGPU_BLOCK + tid) * DS, wv[i]);
+#pragma unroll
+            for (int i = 0; i < G; i++) {
+                const int e = (g0 + i) * VGPU_BLOCK + tid;
+                const float* qm = s.qs + (e / KT) * DS;
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < DS; j++) acc = __builtin_fmaf(qm[j], wv[i][j], acc);
+                s.lut[e] = -2.0f * acc;
+            }
         }
-        s.lut[e] = -2.0f * acc;
+    } else {
+        for (int e = tid; e < M * K; e += VGPU_BLOCK) {
+            const float* cw = ix.codebooks + (size_t)e * ds;
+            const float* qm = s.qs + (e / K) * ds;
+            float acc = 0.0f;
+            for (int j = 0; j < ds; j++) acc = __builtin_fmaf(qm[j], cw[j], acc);
+            s.lut[e] = -2.0f * acc;
+        }
     }
     __syncthreads();
 
@@ -419,6 +506,7 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     const int KL = K > 64 ? K : 64;  // rescoring chunk: KL entries x M codebooks
     for (uint32_t c0 = 0; c0 < n; c0 += (uint32_t)KL) {
         const uint32_t cn = min((uint32_t)KL, n - c0);
+#pragma unroll 2
         for (uint32_t t = tid; t < cn * (uint32_t)M; t += VGPU_BLOCK) {
             const uint32_t i = c0 + t / (uint32_t)M;
             const int m = (int)(t % (uint32_t)M);
@@ -427,21 +515,13 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
             const uint8_t code = ix.codes[(size_t)pos * M + m];
             const float* cw = ix.codebooks + ((size_t)m * K + code) * ds;
             const float* c = ix.centroids + (size_t)s.lid[p] * d + m * ds;
-            const float* qm = s.qs + m * ds;
-            // pq.rs:232-251 on r = q - c (search.rs:1242-1245), no contraction.
-            float e = 0.0f;
-            for (int j = 0; j < ds; j++) {
-                const float r = qm[j] - c[j];
-                const float diff = r - cw[j];
-                e = __fadd_rn(e, __fmul_rn(diff, diff));
-            }
-            s.lut[t] = e;
+            s.lut[t] = exact_sub_distance<DS>(s.qs + m * ds, c, cw, ds);
         }
         __syncthreads();
         for (uint32_t i = c0 + tid; i < c0 + cn; i += VGPU_BLOCK) {
             const float* em = s.lut + (size_t)(i - c0) * M;
             float total_e = 0.0f;  // pq_simd.rs:349-355: m = 0..M-1 from 0.0
-            for (int m = 0; m < M; m++) total_e += em[m];
+            for (int m = 0; m < M; m++) total_e = __fadd_rn(total_e, em[m]);
             const uint32_t pos = (uint32_t)s.keys[i];
             s.keys[i] = cand_key(total_e, ix.list_ids[pos]);
         }
@@ -477,30 +557,40 @@ size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
     return st + fs8_layout(ix.d, ix.M, ix.K, a.P, fs8_buf(a.kk), st != 0, off);
 }
 
-template <int MT, int KT>
-static void launch_fast_mk(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
+template <int MT, int KT, int DS>
+static void launch_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     const int buf = fs8_buf(a.kk);
     size_t off[10];
     const size_t dyn = fs8_layout(ix.d, ix.M, ix.K, a.P, buf, MT > 0 && KT >= 64, off);
-    auto k = scan8_fast_kernel<MT, KT>;
+    auto k = scan8_fast_kernel<MT, KT, DS>;
     (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn);
     hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), dyn, s, ix, a, buf);
+}
+
+template <int MT>
+static void launch_fast_m(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
+    switch (ix.ds) {  // the subvector widths of the benchmark shapes
+        case 2: launch_fast<MT, 256, 2>(ix, a, s); return;
+        case 4: launch_fast<MT, 256, 4>(ix, a, s); return;
+        case 8: launch_fast<MT, 256, 8>(ix, a, s); return;
+        default: launch_fast<MT, 256, 0>(ix, a, s); return;
+    }
 }
 
 void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     if (a.nq <= 0) return;
     if (ix.K == 256) {
         switch (ix.M) {
-            case 4: launch_fast_mk<4, 256>(ix, a, s); return;
-            case 8: launch_fast_mk<8, 256>(ix, a, s); return;
-            case 16: launch_fast_mk<16, 256>(ix, a, s); return;
-            case 32: launch_fast_mk<32, 256>(ix, a, s); return;
-            case 48: launch_fast_mk<48, 256>(ix, a, s); return;
-            case 64: launch_fast_mk<64, 256>(ix, a, s); return;
+            case 4: launch_fast_m<4>(ix, a, s); return;
+            case 8: launch_fast_m<8>(ix, a, s); return;
+            case 16: launch_fast_m<16>(ix, a, s); return;
+            case 32: launch_fast_m<32>(ix, a, s); return;
+            case 48: launch_fast_m<48>(ix, a, s); return;
+            case 64: launch_fast_m<64>(ix, a, s); return;
             default: break;
         }
     }
-    launch_fast_mk<0, 0>(ix, a, s);
+    launch_fast<0, 0, 0>(ix, a, s);
 }
 
 }  // namespace vgpu
