@@ -114,8 +114,12 @@ def main():
               for key in ("ms_normalize", "ms_coarse", "ms_select", "ms_scan", "ms_fallback",
                           "ms_rerank", "ms_total")}
     fallbacks = int(max(s["fallback_queries"] for s in stats))
+    scan_diag = {"flushes_per_query": round(stats[-1]["fast_flushes"] / nq, 3),
+                 "appends_per_query": round(stats[-1]["fast_appends"] / nq, 1),
+                 "candidates_per_query": round(stats[-1]["candidates"] / nq, 1),
+                 "fallback_ties": int(stats[-1]["fallback_ties"])}
     log(f"{qps:.0f} QPS, {ms_step:.3f} ms/batch, scan {scan_ms:.3f} ms, {achieved:.0f} GB/s, "
-        f"phases {phases}, fallback queries {fallbacks}")
+        f"phases {phases}, fallback queries {fallbacks}, scan {scan_diag}")
 
     gpu_ids = out_ids.cpu().numpy()
     gpu_d = out_d.cpu().numpy()
@@ -156,6 +160,7 @@ def main():
                      "candidates_per_launch": int(cands)},
         "phases_ms": phases,
         "fallback_queries": fallbacks,
+        "scan_diagnostics": scan_diag,
         "cpu_baseline": cpu,
         "parity": parity,
     }

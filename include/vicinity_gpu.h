@@ -72,6 +72,9 @@ typedef struct vgpu_search_stats {
     uint32_t fallback_queries; /* FAST queries recomputed in EXACT mode */
     uint32_t coarse_overflow;  /* queries whose coarse margin set exceeded LDS */
     uint32_t nq;
+    uint64_t fast_flushes;     /* FAST: buffer flushes summed over queries */
+    uint64_t fast_appends;     /* FAST: entries that passed the running threshold */
+    uint32_t fallback_ties;    /* FAST fallbacks caused by more equal distances than the buffer holds */
 } vgpu_search_stats;
 
 typedef struct vgpu_ivfpq vgpu_ivfpq;

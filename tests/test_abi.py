@@ -70,7 +70,8 @@ def test_struct_layouts_match_header():
 
     assert ctypes.sizeof(_lib.Params) == 5 * 8 + 8
     assert ctypes.sizeof(_lib.Info) == 7 * 8 + 3 * 4 + 4
-    assert ctypes.sizeof(_lib.Stats) == 7 * 4 + 4 + 2 * 8 + 3 * 4 + 4
+    # 7 floats, pad, 2 u64, 3 u32, pad, 2 u64 (flushes, appends), 1 u32, pad
+    assert ctypes.sizeof(_lib.Stats) == 7 * 4 + 4 + 2 * 8 + 3 * 4 + 4 + 2 * 8 + 4 + 4
 
 
 def test_datagen_shapes_and_determinism():
@@ -96,3 +97,33 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
     with pytest.raises(ImportError, match="no CPU fallback"):
         _lib.load()
+
+
+def test_ctypes_structs_match_the_c_header_field_by_field(tmp_path):
+    """Compile a probe against include/vicinity_gpu.h with gcc and compare every
+    field offset and struct size with the ctypes mirror."""
+    import shutil
+    import subprocess
+
+    from vicinity_amd import _lib
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    structs = {"vgpu_ivfpq_params": _lib.Params, "vgpu_ivfpq_info": _lib.Info,
+               "vgpu_search_stats": _lib.Stats}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in py._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["return 0;", "}"]
+    src = tmp_path / "probe.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(src)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {tuple(l.split()[:2]): int(l.split()[2]) for l in out if l}
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for field, _ in py._fields_:
+            assert got[(cname, field)] == getattr(py, field).offset, (cname, field)

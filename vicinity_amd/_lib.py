@@ -58,7 +58,9 @@ class Stats(ctypes.Structure):
                 ("ms_fallback", ctypes.c_float), ("ms_rerank", ctypes.c_float),
                 ("ms_total", ctypes.c_float), ("candidates", ctypes.c_uint64),
                 ("scan_bytes", ctypes.c_uint64), ("fallback_queries", ctypes.c_uint32),
-                ("coarse_overflow", ctypes.c_uint32), ("nq", ctypes.c_uint32)]
+                ("coarse_overflow", ctypes.c_uint32), ("nq", ctypes.c_uint32),
+                ("fast_flushes", ctypes.c_uint64), ("fast_appends", ctypes.c_uint64),
+                ("fallback_ties", ctypes.c_uint32)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}

@@ -282,8 +282,13 @@ __global__ __launch_bounds__(256) void fastscan_kernel(DevIndex ix, ScanArgs a, 
     tk.flush();
     // Pad each wave buffer past its kept prefix, then one block sort merges all.
     for (int i = (int)*tk.count + lane; i < wbuf; i += 64) tk.keys[i] = ~0ull;
-    if (lane == 0 && a.counters) atomicAdd(&a.counters[0], (unsigned long long)scanned);
+    if (lane == 0) cnt[4 + wave] = scanned;
     __syncthreads();
+    if (tid == 0) {
+        uint32_t* st = a.qstat + (size_t)q * QSTAT_WORDS;
+        st[0] = cnt[4] + cnt[5] + cnt[6] + cnt[7];
+        st[1] = st[2] = st[3] = 0u;
+    }
     block_bitonic_sort_keys(allkeys, 4 * wbuf);
     for (int j = tid; j < a.kout; j += blockDim.x) {
         size_t o = (size_t)q * a.kout + j;

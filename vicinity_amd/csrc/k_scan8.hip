@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256) void scan8_exact_kernel(DevIndex ix, ScanArgs 
     extern __shared__ __align__(16) char smem[];
     const int q = blockIdx.x;
     if (q >= a.nq) return;
-    if (a.only_flagged && a.flags[q] == 0u) return;
+    if (a.only_flagged && (a.qstat[(size_t)q * QSTAT_WORDS + 3] & 1u) == 0u) return;
     const int tid = threadIdx.x;
     const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds, P = a.P;
     ScanLds s = carve(smem, d, M, K, P, buf);
@@ -260,7 +260,11 @@ __global__ __launch_bounds__(256) void scan8_exact_kernel(DevIndex ix, ScanArgs 
     }
     topk_flush(s.tk, a.kk);
     const int n = (int)*s.tk.count;
-    if (tid == 0 && a.counters && !a.only_flagged) atomicAdd(&a.counters[0], (unsigned long long)total);
+    if (tid == 0 && !a.only_flagged) {
+        uint32_t* st = a.qstat + (size_t)q * QSTAT_WORDS;
+        st[0] = total;
+        st[1] = st[2] = st[3] = 0u;
+    }
     write_out(a, s, q, n < a.kout ? n : a.kout);
 }
 

@@ -124,7 +124,8 @@ struct FastLds {
     uint32_t* pref;  // [P + 1]
     float* term0;    // [P] ||q - c||^2
     RadixScratch* rs;
-    uint32_t* misc;  // [0] count [1] thr [2] fail [3..4] flush flags by round parity
+    uint32_t* misc;  // [0] count [1] thr [2] lost ties [3..4] flush flags by round parity
+                     // [5] entries evicted by flushes [6] flushes
 };
 
 __host__ __device__ inline size_t fs8_align(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -221,6 +222,8 @@ __device__ inline void fs8_flush(FastLds& s, int keep, uint32_t cap, int parity)
             s.misc[2] = 1u;
         }
         s.misc[1] = T;
+        s.misc[5] += n - (kept < cap ? kept : cap);  // entries evicted
+        s.misc[6] += 1u;
     }
     __syncthreads();
 }
@@ -493,14 +496,14 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
         bk = bk < 0xfffffffeu ? bk + 1u : 0xffffffffu;  // one ulp to spare
         if (thr != 0xffffffffu && bk > thr) fail = true;
     }
-    if (tid == 0 && a.counters) atomicAdd(&a.counters[0], (unsigned long long)total);
-    if (fail) {
-        if (tid == 0) {
-            a.flags[q] = 1u;
-            if (a.counters) atomicAdd(&a.counters[1], 1ull);
-        }
-        return;
+    if (tid == 0) {
+        uint32_t* st = a.qstat + (size_t)q * QSTAT_WORDS;
+        st[0] = total;
+        st[1] = s.misc[6];
+        st[2] = s.misc[5] + n;  // appended = evicted + still held
+        st[3] = fail ? (1u | (s.misc[2] ? 2u : 0u)) : 0u;
     }
+    if (fail) return;
     n = fs8_compact(s, n, bk, true, P);  // R, keys relabelled (probe slot, position)
 
     const int KL = K > 64 ? K : 64;  // rescoring chunk: KL entries x M codebooks

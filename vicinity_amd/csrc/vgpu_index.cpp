@@ -426,6 +426,8 @@ void IvfpqIndex::upload_index() {
     VGPU_HIP(hipStreamSynchronize(stream));
 }
 
+static constexpr size_t kNumCounters = 5;
+
 static int fast_keep(size_t kout) {
     int kk = 1;
     while ((size_t)kk < kout + 16) kk <<= 1;
@@ -474,10 +476,10 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
     w_dist.reserve(chunk * kout);
     w_vidx2.reserve(chunk * k);
     w_dist2.reserve(chunk * k);
-    w_flags.reserve(chunk);
-    w_counters.reserve(2);
+    w_qstat.reserve(chunk * QSTAT_WORDS);
+    w_counters.reserve(kNumCounters);
     w_overflow.reserve(1);
-    VGPU_HIP(hipMemsetAsync(w_counters.p, 0, 2 * sizeof(unsigned long long), s));
+    VGPU_HIP(hipMemsetAsync(w_counters.p, 0, kNumCounters * sizeof(unsigned long long), s));
     VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
     float t[7] = {0, 0, 0, 0, 0, 0, 0};
     for (size_t q0 = 0; q0 < nq; q0 += chunk) {
@@ -497,16 +499,14 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
         a.nq = (int)nc;
         a.P = (int)P;
         a.kout = (int)kout;
-        a.flags = w_flags.p;
+        a.qstat = w_qstat.p;
         a.out_vidx = w_vidx.p;
         a.out_dist = w_dist.p;
-        a.counters = w_counters.p;
         if (K == 16) {
             a.kk = (int)kout;
             launch_fastscan(dix, a, s);
             if (profiling) VGPU_HIP(hipEventRecord(ev[4], s));
         } else if (mode == VGPU_MODE_FAST) {
-            VGPU_HIP(hipMemsetAsync(w_flags.p, 0, nc * sizeof(uint32_t), s));
             a.kk = fast_keep(kout);
             a.exact = 0;
             launch_scan8_fast(dix, a, s);
@@ -521,6 +521,7 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             launch_scan8_exact(dix, a, s);
             if (profiling) VGPU_HIP(hipEventRecord(ev[4], s));
         }
+        launch_stats_reduce(w_qstat.p, (int)nc, w_counters.p, s);
         if (profiling) VGPU_HIP(hipEventRecord(ev[5], s));
         const uint32_t* vout = w_vidx.p;
         const float* dout = w_dist.p;
@@ -545,7 +546,7 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             }
         }
     }
-    unsigned long long cnt[2] = {0, 0};
+    unsigned long long cnt[kNumCounters] = {0, 0, 0, 0, 0};
     unsigned int ovf = 0;
     VGPU_HIP(hipMemcpyAsync(cnt, w_counters.p, sizeof(cnt), hipMemcpyDeviceToHost, s));
     VGPU_HIP(hipMemcpyAsync(&ovf, w_overflow.p, sizeof(ovf), hipMemcpyDeviceToHost, s));
@@ -559,6 +560,9 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
     stats.ms_total = t[0] + t[1] + t[2] + t[3] + t[4] + t[5] + t[6];
     stats.candidates = cnt[0];
     stats.fallback_queries = (uint32_t)cnt[1];
+    stats.fast_flushes = cnt[2];
+    stats.fast_appends = cnt[3];
+    stats.fallback_ties = (uint32_t)cnt[4];
     stats.coarse_overflow = ovf;
     stats.scan_bytes = K == 16 ? cnt[0] * (uint64_t)(M / 2 + 4) : cnt[0] * (uint64_t)(M + 4);
 }

@@ -33,11 +33,14 @@ struct ScanArgs {
     int kout = 0;                   // results kept per query (k, or the rerank pool)
     int kk = 0;                     // FAST: entries a flush keeps (> kout); EXACT: kout
     int exact = 0;                  // 1 = EXACT mode
-    int only_flagged = 0;           // run only queries with flags[q] != 0
-    uint32_t* flags = nullptr;      // [nq] FAST margin failures (written), read when only_flagged
+    int only_flagged = 0;           // run only queries whose qstat fallback bit is set
     uint32_t* out_vidx = nullptr;   // [nq*kout] insertion indices, 0xffffffff padding
     float* out_dist = nullptr;      // [nq*kout]
-    unsigned long long* counters = nullptr; // [0] candidates, [1] fallbacks
+    // Per-query statistics, one row of QSTAT_WORDS per query, written with plain
+    // stores (no global atomics): [0] list entries scanned, [1] FAST flushes,
+    // [2] FAST appends, [3] bit 0: FAST could not prove the query (rerun by the
+    // EXACT kernel), bit 1: because of more equal distances than its buffer holds.
+    uint32_t* qstat = nullptr;
 };
 
 void launch_normalize(const float* x, float* out, float* norms, int n, int d, hipStream_t s);
@@ -53,9 +56,16 @@ void launch_coarse_select(float* D, const float* qn, const float* qnorm, const f
 size_t scan8_lds_bytes(const DevIndex& ix, const ScanArgs& a);
 void launch_scan8_exact(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 // FAST mode: per-query decomposed table, threshold buffer, exact rescoring of
-// the provable candidate set; unprovable queries get flags[q] = 1.
+// the provable candidate set; an unprovable query sets bit 0 of its qstat
+// fallback word.
 size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a);
 void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
+
+#define QSTAT_WORDS 4
+// counters[0..4] += sums over the rows of qstat[nq][QSTAT_WORDS]: entries
+// scanned, fallbacks, flushes, appends, fallbacks from ties.  One workgroup.
+void launch_stats_reduce(const uint32_t* qstat, int nq, unsigned long long* counters,
+                         hipStream_t s);
 size_t fastscan_lds_bytes(const DevIndex& ix, const ScanArgs& a);
 void launch_fastscan(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 
