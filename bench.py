@@ -117,7 +117,8 @@ def main():
     scan_diag = {"flushes_per_query": round(stats[-1]["fast_flushes"] / nq, 3),
                  "appends_per_query": round(stats[-1]["fast_appends"] / nq, 1),
                  "candidates_per_query": round(stats[-1]["candidates"] / nq, 1),
-                 "fallback_ties": int(stats[-1]["fallback_ties"])}
+                 "fallback_ties": int(stats[-1]["fallback_ties"]),
+                 "second_passes": int(stats[-1]["fast_retries"])}
     log(f"{qps:.0f} QPS, {ms_step:.3f} ms/batch, scan {scan_ms:.3f} ms, {achieved:.0f} GB/s, "
         f"phases {phases}, fallback queries {fallbacks}, scan {scan_diag}")
 

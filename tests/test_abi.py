@@ -70,7 +70,7 @@ def test_struct_layouts_match_header():
 
     assert ctypes.sizeof(_lib.Params) == 5 * 8 + 8
     assert ctypes.sizeof(_lib.Info) == 7 * 8 + 3 * 4 + 4
-    # 7 floats, pad, 2 u64, 3 u32, pad, 2 u64 (flushes, appends), 1 u32, pad
+    # 7 floats, pad, 2 u64, 3 u32, pad, 2 u64 (flushes, appends), 2 u32
     assert ctypes.sizeof(_lib.Stats) == 7 * 4 + 4 + 2 * 8 + 3 * 4 + 4 + 2 * 8 + 4 + 4
 
 

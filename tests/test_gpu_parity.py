@@ -336,3 +336,34 @@ def test_fast_scan_ties_and_fallback_match_oracle(vg, oracle, copies, k):
         ids, dists = ix.batch_search(q, k, nprobe=4)
         oids, odists = oix.search_batch(q, k, 4)
         _assert_same_results(ids, dists, oids, odists)
+
+
+@pytest.mark.parametrize("copies,expect", [(300, "second_pass"), (900, "exact_rerun")])
+def test_fast_second_pass_and_exact_rerun(vg, oracle, copies, expect):
+    """Near-duplicates (copies of one vector with 1e-6 noise) put hundreds of
+    approximate distances inside the proof window A_k + 2 tau.  With 300 copies
+    the FAST kernel's second pass collects them all; with 900 they overflow its
+    buffer and the query is rerun by the EXACT kernel.  Both must return the
+    oracle's rows, and the statistics must show which path ran."""
+    from vicinity_amd import IVFPQIndex
+
+    _print_case(f"fast second pass copies={copies}")
+    rng = np.random.default_rng(copies)
+    v0 = rng.standard_normal(16).astype(np.float32)
+    near = (v0 + rng.standard_normal((copies, 16)).astype(np.float32) * np.float32(1e-6))
+    x = np.concatenate([near.astype(np.float32), rng.standard_normal((1100, 16)).astype(np.float32)])
+    vecs = oracle.normalize_rows(x)
+    oix, _ = oracle.ivfpq_build(vecs, 4, 4, 256, 13, 0, 10)
+    ix = IVFPQIndex(16, num_clusters=4, num_codebooks=4, codebook_size=256, nprobe=4)
+    ix.load_artifacts(oix.centroids, oix.codebooks, oix.list_offsets, oix.list_ids, oix.codes,
+                      vectors=vecs)
+    q = v0[None, :].copy()
+    ix.set_mode("fast")
+    ids, dists = ix.batch_search(q, 5, nprobe=4)
+    st = ix.last_stats()
+    oids, odists = oix.search_batch(q, 5, 4)
+    _assert_same_results(ids, dists, oids, odists)
+    if expect == "second_pass":
+        assert st["fast_retries"] == 1 and st["fallback_queries"] == 0, st
+    else:
+        assert st["fallback_queries"] == 1, st

@@ -60,7 +60,7 @@ class Stats(ctypes.Structure):
                 ("scan_bytes", ctypes.c_uint64), ("fallback_queries", ctypes.c_uint32),
                 ("coarse_overflow", ctypes.c_uint32), ("nq", ctypes.c_uint32),
                 ("fast_flushes", ctypes.c_uint64), ("fast_appends", ctypes.c_uint64),
-                ("fallback_ties", ctypes.c_uint32)]
+                ("fallback_ties", ctypes.c_uint32), ("fast_retries", ctypes.c_uint32)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}

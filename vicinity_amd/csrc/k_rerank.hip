@@ -80,9 +80,11 @@ void launch_finalize(const uint32_t* vidx, const float* dist, const uint32_t* do
 // Column sums of the per-query statistics rows into 64-bit counters.
 __global__ __launch_bounds__(256) void stats_reduce_kernel(const uint32_t* __restrict__ qstat,
                                                            int nq,
-                                                           unsigned long long* __restrict__ counters) {
-    __shared__ unsigned long long part[5][VGPU_BLOCK];
-    unsigned long long c[5] = {0, 0, 0, 0, 0};
+                                                           unsigned long long* __restrict__ counters,
+                                                           uint32_t* flag_count) {
+    constexpr int NC = NUM_SCAN_COUNTERS;
+    __shared__ unsigned long long part[NC][VGPU_BLOCK];
+    unsigned long long c[NC] = {0, 0, 0, 0, 0, 0};
     for (int q = threadIdx.x; q < nq; q += VGPU_BLOCK) {
         const uint32_t* st = qstat + (size_t)q * QSTAT_WORDS;
         c[0] += st[0];              // entries scanned
@@ -90,21 +92,24 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(const uint32_t* __res
         c[2] += st[1];              // flushes
         c[3] += st[2];              // appends
         c[4] += (st[3] >> 1) & 1u;  // fallbacks from ties
+        c[5] += (st[3] >> 2) & 1u;  // second passes
     }
-    for (int i = 0; i < 5; i++) part[i][threadIdx.x] = c[i];
+    for (int i = 0; i < NC; i++) part[i][threadIdx.x] = c[i];
     __syncthreads();
     for (int w = VGPU_BLOCK / 2; w > 0; w >>= 1) {
         if ((int)threadIdx.x < w)
-            for (int i = 0; i < 5; i++) part[i][threadIdx.x] += part[i][threadIdx.x + w];
+            for (int i = 0; i < NC; i++) part[i][threadIdx.x] += part[i][threadIdx.x + w];
         __syncthreads();
     }
-    if (threadIdx.x < 5) counters[threadIdx.x] += part[threadIdx.x][0];
+    if (threadIdx.x < NC) counters[threadIdx.x] += part[threadIdx.x][0];
+    if (threadIdx.x == 0 && flag_count) *flag_count = 0u;
 }
 
 void launch_stats_reduce(const uint32_t* qstat, int nq, unsigned long long* counters,
-                         hipStream_t s) {
+                         uint32_t* flag_count, hipStream_t s) {
     if (nq <= 0) return;
-    hipLaunchKernelGGL(stats_reduce_kernel, dim3(1), dim3(VGPU_BLOCK), 0, s, qstat, nq, counters);
+    hipLaunchKernelGGL(stats_reduce_kernel, dim3(1), dim3(VGPU_BLOCK), 0, s, qstat, nq, counters,
+                       flag_count);
 }
 
 }  // namespace vgpu

@@ -208,12 +208,9 @@ __device__ inline void write_out(const ScanArgs& a, ScanLds& s, int q, int n) {
     }
 }
 
+// One query with the reference arithmetic; every thread of the block calls it.
 template <int MT, int KT>
-__global__ __launch_bounds__(256) void scan8_exact_kernel(DevIndex ix, ScanArgs a, int buf) {
-    extern __shared__ __align__(16) char smem[];
-    const int q = blockIdx.x;
-    if (q >= a.nq) return;
-    if (a.only_flagged && (a.qstat[(size_t)q * QSTAT_WORDS + 3] & 1u) == 0u) return;
+__device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char* smem, int q) {
     const int tid = threadIdx.x;
     const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds, P = a.P;
     ScanLds s = carve(smem, d, M, K, P, buf);
@@ -268,6 +265,20 @@ __global__ __launch_bounds__(256) void scan8_exact_kernel(DevIndex ix, ScanArgs 
     write_out(a, s, q, n < a.kout ? n : a.kout);
 }
 
+template <int MT, int KT>
+__global__ __launch_bounds__(256) void scan8_exact_kernel(DevIndex ix, ScanArgs a, int buf) {
+    extern __shared__ __align__(16) char smem[];
+    if (!a.only_flagged) {
+        if ((int)blockIdx.x < a.nq) exact_query<MT, KT>(ix, a, buf, smem, blockIdx.x);
+        return;
+    }
+    const uint32_t nf = *a.flag_count;  // written by the FAST kernel before this launch
+    for (uint32_t fi = blockIdx.x; fi < nf; fi += gridDim.x) {
+        __syncthreads();
+        exact_query<MT, KT>(ix, a, buf, smem, (int)a.flag_list[fi]);
+    }
+}
+
 size_t scan8_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
     size_t off[12];
     return scan_lds_layout(ix.d, ix.M, ix.K, a.P, scan_buf(a.kk), off);
@@ -279,7 +290,9 @@ static void launch_mk(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     size_t lds = scan8_lds_bytes(ix, a);
     auto k = scan8_exact_kernel<MT, KT>;
     (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), lds, s, ix, a, buf);
+    // Flagged queries: a small grid walks the list the FAST kernel wrote.
+    const int grid = a.only_flagged ? (a.nq < 256 ? a.nq : 256) : a.nq;
+    hipLaunchKernelGGL(k, dim3(grid), dim3(VGPU_BLOCK), lds, s, ix, a, buf);
 }
 
 template <int KT>

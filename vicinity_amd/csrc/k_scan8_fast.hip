@@ -263,11 +263,13 @@ __device__ __forceinline__ void fs8_fetch(const DevIndex& ix, const FastLds& s, 
 // saw, so the flag is raised exactly when the buffer needs a flush.  The two
 // parities alternate between rounds, and a raised flag is cleared inside the
 // flush, so a flag is never written while another wave may still read it.
-// Every thread of the block calls this (all lanes active).
-template <int MT, int KT>
+// Every thread of the block calls this (all lanes active).  The second pass
+// (RETRY) appends only keys in (lo, thr]: the buffer already holds every key
+// <= lo.
+template <int MT, int KT, bool RETRY>
 __device__ __forceinline__ void fs8_consume(const DevIndex& ix, FastLds& s, const float* lut_static,
-                                            const RoundRegs<MT>& g, uint32_t thr, uint32_t cap,
-                                            int parity) {
+                                            const RoundRegs<MT>& g, uint32_t thr, uint32_t lo,
+                                            uint32_t cap, int parity) {
     const int lane = threadIdx.x & 63;
     bool take[FS_U];
     uint32_t fk[FS_U], before[FS_U];
@@ -285,7 +287,7 @@ __device__ __forceinline__ void fs8_consume(const DevIndex& ix, FastLds& s, cons
                    row_sum_generic(ix.codes + (size_t)pos * ix.M, s.lut, ix.M, ix.K);
         }
         fk[u] = fkey(dist);
-        take[u] = ok && fk[u] <= thr;
+        take[u] = ok && fk[u] <= thr && (!RETRY || fk[u] > lo);
         mask[u] = __ballot(take[u]);
         before[u] = tot;
         tot += (uint32_t)__popcll(mask[u]);
@@ -468,12 +470,12 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     if (total > 0) fs8_fetch<MT>(ix, s, 0, total, cur, ga);
     for (uint32_t rb = 0; rb < total; rb += 2 * FS_ROUND) {
         fs8_fetch<MT>(ix, s, rb + FS_ROUND, total, cur, gb);
-        fs8_consume<MT, KT>(ix, s, slut, ga, s.misc[1], cap, 0);
+        fs8_consume<MT, KT, false>(ix, s, slut, ga, s.misc[1], 0u, cap, 0);
         __syncthreads();
         if (s.misc[3]) fs8_flush(s, keep, cap, 0);
         if (rb + FS_ROUND >= total) break;
         fs8_fetch<MT>(ix, s, rb + 2 * FS_ROUND, total, cur, ga);
-        fs8_consume<MT, KT>(ix, s, slut, gb, s.misc[1], cap, 1);
+        fs8_consume<MT, KT, false>(ix, s, slut, gb, s.misc[1], 0u, cap, 1);
         __syncthreads();
         if (s.misc[4]) fs8_flush(s, keep, cap, 1);
     }
@@ -484,6 +486,7 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     const uint32_t thr = s.misc[1];
     const int kout = a.kout;
     bool fail = s.misc[2] != 0u;
+    bool retried = false;
     uint32_t bk = 0xffffffffu;
     if (!fail && n > (uint32_t)kout) {
         auto hk = [&](int i) -> uint32_t { return (uint32_t)(s.keys[i] >> 32); };
@@ -494,14 +497,45 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
         const float bound = fkey_to_float(Ak) + 2.0f * tau;
         bk = fkey(bound);
         bk = bk < 0xfffffffeu ? bk + 1u : 0xffffffffu;  // one ulp to spare
-        if (thr != 0xffffffffu && bk > thr) fail = true;
+        if (thr != 0xffffffffu && bk > thr) {
+            // Second pass: the buffer holds every key <= thr; add the keys in
+            // (thr, bk] with no flush, so afterwards it holds all of R.  More
+            // than the buffer holds fails the query (EXACT rerun).
+            retried = true;
+            if (tid == 0) {
+                s.misc[1] = bk;
+                s.misc[3] = s.misc[4] = 0u;
+            }
+            __syncthreads();
+            cur = 0;
+            fs8_fetch<MT>(ix, s, 0, total, cur, ga);
+            for (uint32_t rb = 0; rb < total; rb += 2 * FS_ROUND) {
+                fs8_fetch<MT>(ix, s, rb + FS_ROUND, total, cur, gb);
+                fs8_consume<MT, KT, true>(ix, s, slut, ga, bk, thr, cap, 0);
+                __syncthreads();
+                if (s.misc[3]) break;
+                if (rb + FS_ROUND >= total) break;
+                fs8_fetch<MT>(ix, s, rb + 2 * FS_ROUND, total, cur, ga);
+                fs8_consume<MT, KT, true>(ix, s, slut, gb, bk, thr, cap, 1);
+                __syncthreads();
+                if (s.misc[4]) break;
+            }
+            __syncthreads();
+            n = s.misc[0];
+            if (s.misc[3] | s.misc[4]) {
+                fail = true;
+                if (tid == 0) s.misc[2] = 1u;
+            }
+            __syncthreads();
+        }
     }
     if (tid == 0) {
         uint32_t* st = a.qstat + (size_t)q * QSTAT_WORDS;
         st[0] = total;
         st[1] = s.misc[6];
         st[2] = s.misc[5] + n;  // appended = evicted + still held
-        st[3] = fail ? (1u | (s.misc[2] ? 2u : 0u)) : 0u;
+        st[3] = (fail ? (1u | (s.misc[2] ? 2u : 0u)) : 0u) | (retried ? 4u : 0u);
+        if (fail) a.flag_list[atomicAdd(a.flag_count, 1u)] = (uint32_t)q;
     }
     if (fail) return;
     n = fs8_compact(s, n, bk, true, P);  // R, keys relabelled (probe slot, position)

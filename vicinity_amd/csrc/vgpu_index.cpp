@@ -426,7 +426,7 @@ void IvfpqIndex::upload_index() {
     VGPU_HIP(hipStreamSynchronize(stream));
 }
 
-static constexpr size_t kNumCounters = 5;
+static constexpr size_t kNumCounters = NUM_SCAN_COUNTERS;
 
 static int fast_keep(size_t kout) {
     int kk = 1;
@@ -477,9 +477,12 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
     w_vidx2.reserve(chunk * k);
     w_dist2.reserve(chunk * k);
     w_qstat.reserve(chunk * QSTAT_WORDS);
+    w_flag_list.reserve(chunk);
+    w_flag_count.reserve(1);
     w_counters.reserve(kNumCounters);
     w_overflow.reserve(1);
     VGPU_HIP(hipMemsetAsync(w_counters.p, 0, kNumCounters * sizeof(unsigned long long), s));
+    VGPU_HIP(hipMemsetAsync(w_flag_count.p, 0, sizeof(uint32_t), s));
     VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
     float t[7] = {0, 0, 0, 0, 0, 0, 0};
     for (size_t q0 = 0; q0 < nq; q0 += chunk) {
@@ -500,6 +503,8 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
         a.P = (int)P;
         a.kout = (int)kout;
         a.qstat = w_qstat.p;
+        a.flag_list = w_flag_list.p;
+        a.flag_count = w_flag_count.p;
         a.out_vidx = w_vidx.p;
         a.out_dist = w_dist.p;
         if (K == 16) {
@@ -521,7 +526,7 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             launch_scan8_exact(dix, a, s);
             if (profiling) VGPU_HIP(hipEventRecord(ev[4], s));
         }
-        launch_stats_reduce(w_qstat.p, (int)nc, w_counters.p, s);
+        launch_stats_reduce(w_qstat.p, (int)nc, w_counters.p, w_flag_count.p, s);
         if (profiling) VGPU_HIP(hipEventRecord(ev[5], s));
         const uint32_t* vout = w_vidx.p;
         const float* dout = w_dist.p;
@@ -546,7 +551,7 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             }
         }
     }
-    unsigned long long cnt[kNumCounters] = {0, 0, 0, 0, 0};
+    unsigned long long cnt[kNumCounters] = {};
     unsigned int ovf = 0;
     VGPU_HIP(hipMemcpyAsync(cnt, w_counters.p, sizeof(cnt), hipMemcpyDeviceToHost, s));
     VGPU_HIP(hipMemcpyAsync(&ovf, w_overflow.p, sizeof(ovf), hipMemcpyDeviceToHost, s));
@@ -563,6 +568,7 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
     stats.fast_flushes = cnt[2];
     stats.fast_appends = cnt[3];
     stats.fallback_ties = (uint32_t)cnt[4];
+    stats.fast_retries = (uint32_t)cnt[5];
     stats.coarse_overflow = ovf;
     stats.scan_bytes = K == 16 ? cnt[0] * (uint64_t)(M / 2 + 4) : cnt[0] * (uint64_t)(M + 4);
 }

@@ -33,13 +33,16 @@ struct ScanArgs {
     int kout = 0;                   // results kept per query (k, or the rerank pool)
     int kk = 0;                     // FAST: entries a flush keeps (> kout); EXACT: kout
     int exact = 0;                  // 1 = EXACT mode
-    int only_flagged = 0;           // run only queries whose qstat fallback bit is set
+    int only_flagged = 0;           // EXACT: run the queries of flag_list only
+    uint32_t* flag_list = nullptr;  // [nq] queries FAST could not prove (appended by FAST)
+    uint32_t* flag_count = nullptr; // entries of flag_list (zeroed by launch_stats_reduce)
     uint32_t* out_vidx = nullptr;   // [nq*kout] insertion indices, 0xffffffff padding
     float* out_dist = nullptr;      // [nq*kout]
     // Per-query statistics, one row of QSTAT_WORDS per query, written with plain
     // stores (no global atomics): [0] list entries scanned, [1] FAST flushes,
     // [2] FAST appends, [3] bit 0: FAST could not prove the query (rerun by the
-    // EXACT kernel), bit 1: because of more equal distances than its buffer holds.
+    // EXACT kernel), bit 1: because of more equal distances than its buffer holds,
+    // bit 2: FAST needed its second pass.
     uint32_t* qstat = nullptr;
 };
 
@@ -62,10 +65,12 @@ size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a);
 void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 
 #define QSTAT_WORDS 4
-// counters[0..4] += sums over the rows of qstat[nq][QSTAT_WORDS]: entries
-// scanned, fallbacks, flushes, appends, fallbacks from ties.  One workgroup.
+// counters[0..5] += sums over the rows of qstat[nq][QSTAT_WORDS]: entries
+// scanned, fallbacks, flushes, appends, fallbacks from ties, second passes;
+// then *flag_count = 0 (may be null).  One workgroup.
+#define NUM_SCAN_COUNTERS 6
 void launch_stats_reduce(const uint32_t* qstat, int nq, unsigned long long* counters,
-                         hipStream_t s);
+                         uint32_t* flag_count, hipStream_t s);
 size_t fastscan_lds_bytes(const DevIndex& ix, const ScanArgs& a);
 void launch_fastscan(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 
