@@ -367,3 +367,32 @@ def test_fast_second_pass_and_exact_rerun(vg, oracle, copies, expect):
         assert st["fast_retries"] == 1 and st["fallback_queries"] == 0, st
     else:
         assert st["fallback_queries"] == 1, st
+
+
+@pytest.mark.parametrize("d,L,P", [(24, 37, 8), (16, 300, 20), (32, 2000, 40), (16, 13, 13)])
+def test_probe_selection_paths(vg, oracle, d, L, P):
+    """Probe lists through every selection path: L not a multiple of 4, fewer
+    score-holding lanes than probes, and zero queries whose window of exact ties
+    overflows the one-wave kernel (L = 300: block kernel; L = 2000: its 64-bit
+    radix fallback).  Lists must equal the oracle's, ties by lower list index."""
+    from vicinity_amd import IVFPQIndex
+
+    _print_case(f"probe paths d={d} L={L} P={P}")
+    rng = np.random.default_rng(d * L + P)
+    cent = oracle.normalize_rows(rng.standard_normal((L, d)).astype(np.float32))
+    n = 4 * L
+    M, K = 4, 4
+    ds = d // M
+    cb = rng.standard_normal(M * K * ds).astype(np.float32)
+    assign = np.arange(n) % L
+    off, ids = oracle.build_lists(assign.astype(np.uint32), L)
+    codes = rng.integers(0, K, (n, M), dtype=np.uint8)
+    ix = IVFPQIndex(d, num_clusters=L, num_codebooks=M, codebook_size=K, nprobe=P)
+    ix.load_artifacts(cent, cb, off, ids, codes)
+    q = rng.standard_normal((40, d)).astype(np.float32)
+    q[3] = 0.0
+    q[17] = 0.0
+    lists = ix.probe(q, P)
+    oix = oracle.Index(cent, cb, off, ids, codes, np.arange(n, dtype=np.uint32), None, M, K)
+    for i in range(len(q)):
+        assert lists[i].tolist() == oix.probe(q[i], P)[0].tolist(), i

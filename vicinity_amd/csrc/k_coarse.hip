@@ -12,30 +12,49 @@ namespace vgpu {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// One thread per row: s = sum x^2 in order, norm = sqrt(s), x / norm when
+// Sixteen rows per workgroup, staged through LDS (row stride d + 1 keeps the
+// sequential per-row reads free of bank conflicts): s = sum x^2 in order by
+// one lane per row, norm = sqrt(s), then every element x / norm when
 // norm > 1e-10 (search.rs:55-62; divide and sqrt are correctly rounded).
 // norms[i] receives an upper bound of ||out_i|| used by the error margins.
-__global__ void normalize_kernel(const float* __restrict__ x, float* __restrict__ out,
-                                 float* __restrict__ norms, int n, int d) {
-    int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const float* xi = x + (size_t)i * d;
-    float* oi = out + (size_t)i * d;
-    float s = 0.0f;
-    for (int j = 0; j < d; j++) s += xi[j] * xi[j];
-    float nrm = sqrtf(s);
-    if (nrm > 1e-10f) {
-        for (int j = 0; j < d; j++) oi[j] = xi[j] / nrm;
-        if (norms) norms[i] = 1.0001f;
-    } else {
-        for (int j = 0; j < d; j++) oi[j] = xi[j];
-        if (norms) norms[i] = nrm * 1.0001f;
+#define NR_ROWS 16
+
+__global__ __launch_bounds__(256) void normalize_kernel(const float* __restrict__ x,
+                                                        float* __restrict__ out,
+                                                        float* __restrict__ norms, int n, int d) {
+    extern __shared__ float srow[];  // [NR_ROWS][d + 1]
+    __shared__ float snorm[NR_ROWS];
+    const int tid = threadIdx.x;
+    const int r0 = blockIdx.x * NR_ROWS;
+    const int rows = min(NR_ROWS, n - r0);
+    const int st = d + 1;
+    const float* src = x + (size_t)r0 * d;
+    for (int e = tid; e < rows * d; e += VGPU_BLOCK) srow[(e / d) * st + e % d] = src[e];
+    __syncthreads();
+    if (tid < rows) {
+        const float* xr = srow + tid * st;
+        float s = 0.0f;
+        for (int j = 0; j < d; j++) s = __fadd_rn(s, __fmul_rn(xr[j], xr[j]));
+        const float nrm = sqrtf(s);
+        snorm[tid] = nrm;
+        if (norms) norms[r0 + tid] = nrm > 1e-10f ? 1.0001f : nrm * 1.0001f;
+    }
+    __syncthreads();
+    float* dst = out + (size_t)r0 * d;
+    for (int e = tid; e < rows * d; e += VGPU_BLOCK) {
+        const int r = e / d;
+        const float v = srow[r * st + e % d], nrm = snorm[r];
+        dst[e] = nrm > 1e-10f ? v / nrm : v;
     }
 }
 
 void launch_normalize(const float* x, float* out, float* norms, int n, int d, hipStream_t s) {
     if (n <= 0) return;
-    hipLaunchKernelGGL(normalize_kernel, dim3((n + 255) / 256), dim3(256), 0, s, x, out, norms, n, d);
+    const size_t lds = (size_t)NR_ROWS * (d + 1) * sizeof(float);
+    (void)hipFuncSetAttribute((const void*)normalize_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds);
+    hipLaunchKernelGGL(normalize_kernel, dim3((n + NR_ROWS - 1) / NR_ROWS), dim3(VGPU_BLOCK), lds, s,
+                       x, out, norms, n, d);
 }
 
 // ---- coarse GEMM --------------------------------------------------------
@@ -116,6 +135,270 @@ __device__ __forceinline__ float coarse_tau(int d, float qn, float cmax) {
            1e-30f;
 }
 
+// Exact ordering of the window candidates keys[0..cn) (list indices on entry):
+// rescore 1 - dot in the reference's sequential order, sort by (score, list),
+// write the first Pe.  cn <= SEL_CAP.  All threads call it.
+// qs: LDS scratch of at least d floats.
+__device__ inline void select_window_exact(uint64_t* keys, uint32_t cn, const float* qv, float* qs,
+                                           const float* __restrict__ C, int d, int Pe, int P,
+                                           int q, uint32_t* __restrict__ probe) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    for (int j = tid; j < d; j += VGPU_BLOCK) qs[j] = qv[j];
+    __syncthreads();
+    for (uint32_t t = tid; t < cn; t += VGPU_BLOCK) {
+        const uint32_t c = (uint32_t)keys[t];
+        keys[t] = cand_key(1.0f - seq_dot_stream(qs, C + (size_t)c * d, d), c);
+    }
+    __syncthreads();
+    if (cn <= 64) {  // one wave, keys in registers
+        if (tid < 64) {
+            uint64_t k1[1] = {(uint32_t)lane < cn ? keys[lane] : ~0ull};
+            wave_sort_regs<1>(k1);
+            if (lane < Pe) probe[(size_t)q * P + lane] = (uint32_t)k1[0];
+        }
+        return;
+    }
+    if (cn <= 256) {
+        if (tid < 64) {
+            uint64_t k4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) k4[e] = (uint32_t)(e * 64 + lane) < cn ? keys[e * 64 + lane] : ~0ull;
+            wave_sort_regs<4>(k4);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (e * 64 + lane < Pe) probe[(size_t)q * P + e * 64 + lane] = (uint32_t)k4[e];
+        }
+        return;
+    }
+    const int n2 = next_pow2((int)cn);
+    for (int t = (int)cn + tid; t < n2; t += VGPU_BLOCK) keys[t] = ~0ull;
+    block_bitonic_sort_keys(keys, n2);
+    for (int p = tid; p < Pe; p += VGPU_BLOCK) probe[(size_t)q * P + p] = (uint32_t)keys[p];
+}
+
+// Probe selection with the scores of one query held in registers (EPT per
+// thread, L <= 256 * EPT), one read of the score row.  The Pe-th smallest of
+// the 256 per-thread minima, T, bounds the Pe-th smallest score from above (Pe
+// distinct threads hold a score <= T), so every list whose exact score can be
+// among the Pe smallest has approximate score <= T + 2 tau.  Those are rescored
+// exactly and sorted.  Pe <= 256.
+template <int EPT>
+__device__ void select_block_query(float* __restrict__ D, const float* __restrict__ qn,
+                                   const float* __restrict__ qnorm, const float* __restrict__ C,
+                                   int q, int L, int d, int P, float cmax,
+                                   uint32_t* __restrict__ probe, unsigned int* overflow) {
+    __shared__ RadixScratch rs;
+    __shared__ uint64_t keys[SEL_CAP];
+    __shared__ uint32_t pay[SEL_CAP];
+    __shared__ uint32_t mins[VGPU_BLOCK];
+    __shared__ uint32_t cnt, tsel;
+    const int tid = threadIdx.x, lane = tid & 63;
+    float* row = D + (size_t)q * L;
+    const float* qv = qn + (size_t)q * d;
+    const int Pe = P < L ? P : L;
+
+    uint32_t fk[EPT];
+    uint32_t mn = 0xffffffffu;
+    float sv[EPT];  // unconditional loads (clamped index) so all EPT are in flight together
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+        const int i = e * VGPU_BLOCK + tid;
+        sv[e] = row[i < L ? i : L - 1];
+    }
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+        const int i = e * VGPU_BLOCK + tid;
+        fk[e] = i < L ? fkey(1.0f - sv[e]) : 0xffffffffu;
+        mn = fk[e] < mn ? fk[e] : mn;
+    }
+    mins[tid] = mn;
+    if (tid == 0) cnt = 0;
+    __syncthreads();
+    if (tid < 64) {
+        uint64_t k4[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) k4[e] = mins[e * 64 + lane];
+        wave_sort_regs<4>(k4);
+        const int idx = Pe - 1;
+        uint64_t v = k4[0];
+#pragma unroll
+        for (int e = 1; e < 4; e++) v = (idx >> 6) == e ? k4[e] : v;
+        v = __shfl(v, idx & 63, 64);
+        if (lane == 0) tsel = (uint32_t)v;
+    }
+    __syncthreads();
+    const uint32_t T = tsel;
+    const float W = fkey_to_float(T) + 2.0f * coarse_tau(d, qnorm[q], cmax);
+    uint32_t WK = fkey(W);
+    WK = WK < 0xfffffffeu ? WK + 1u : 0xffffffffu;  // one ulp to spare
+    if (WK < T) WK = T;
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+        const int i = e * VGPU_BLOCK + tid;
+        const bool take = i < L && fk[e] <= WK;
+        const int slot = wave_append_slot(take, &cnt);
+        if (take && slot < SEL_CAP) keys[slot] = (uint64_t)i;
+    }
+    __syncthreads();
+    const uint32_t cn = cnt;
+    if (cn <= SEL_CAP) {  // pay doubles as the query's LDS copy (d <= SEL_CAP)
+        select_window_exact(keys, cn, qv, reinterpret_cast<float*>(pay), C, d, Pe, P, q, probe);
+        return;
+    }
+    // Overflow (degenerate inputs such as a zero query): exact scores of all
+    // window candidates replace the row (+inf elsewhere), then an exact
+    // 64-bit radix select.  Each thread rereads only the entries it wrote.
+    if (tid == 0) atomicAdd(overflow, 1u);
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+        const int i = e * VGPU_BLOCK + tid;
+        if (i < L) row[i] = fk[e] <= WK ? 1.0f - seq_dot(qv, C + (size_t)i * d, d)
+                                        : __int_as_float(0x7f800000);
+    }
+    auto ekey = [&](int i) -> uint64_t { return cand_key(row[i], (uint32_t)i); };
+    const uint64_t K64 = block_radix_select<uint64_t>(ekey, L, (uint32_t)(Pe - 1), &rs);
+    if (tid == 0) cnt = 0;
+    __syncthreads();
+    for (int i = tid; i < L; i += VGPU_BLOCK) {
+        const uint64_t k = ekey(i);
+        if (k <= K64) {
+            const uint32_t slot = atomicAdd(&cnt, 1u);
+            if (slot < SEL_CAP) {
+                keys[slot] = k;
+                pay[slot] = (uint32_t)i;
+            }
+        }
+    }
+    __syncthreads();
+    const int n2 = next_pow2(Pe);
+    for (int t = Pe + tid; t < n2; t += VGPU_BLOCK) {
+        keys[t] = ~0ull;
+        pay[t] = 0xffffffffu;
+    }
+    block_bitonic_sort(keys, pay, n2);
+    for (int p = tid; p < Pe; p += VGPU_BLOCK) probe[(size_t)q * P + p] = pay[p];
+}
+
+// One query per workgroup, or (flag_list != null) the queries the wave kernel
+// could not finish, walked by a small grid.
+template <int EPT>
+__global__ __launch_bounds__(256) void coarse_select_reg_kernel(
+    float* __restrict__ D, const float* __restrict__ qn, const float* __restrict__ qnorm,
+    const float* __restrict__ C, int nq, int L, int d, int P, float cmax,
+    uint32_t* __restrict__ probe, unsigned int* overflow, const uint32_t* flag_list,
+    const uint32_t* flag_count) {
+    if (!flag_list) {
+        if ((int)blockIdx.x < nq)
+            select_block_query<EPT>(D, qn, qnorm, C, blockIdx.x, L, d, P, cmax, probe, overflow);
+        return;
+    }
+    const uint32_t nf = *flag_count;  // written by the wave kernel before this launch
+    for (uint32_t i = blockIdx.x; i < nf; i += gridDim.x) {
+        __syncthreads();
+        select_block_query<EPT>(D, qn, qnorm, C, (int)flag_list[i], L, d, P, cmax, probe, overflow);
+    }
+}
+
+// One wave per query (four independent queries per workgroup, no block
+// barriers), for L <= 4096 and Pe <= 64: 64 scores per lane in registers.  The
+// Pe-th smallest of the 64 lane minima bounds the Pe-th smallest score (Pe
+// distinct lanes hold a score at or below it), so every list whose exact score
+// can be among the Pe smallest has approximate score <= that bound + 2 tau.
+// The window is rescored exactly and sorted in registers.  A window of more
+// than WSEL_CAP lists (degenerate inputs) sends the query to the block kernel.
+#define WSEL_CAP 256
+#define WSEL_QD 512
+
+__global__ __launch_bounds__(256) void coarse_select_wave_kernel(
+    const float* __restrict__ D, const float* __restrict__ qn, const float* __restrict__ qnorm,
+    const float* __restrict__ C, int nq, int L, int d, int P, float cmax,
+    uint32_t* __restrict__ probe, uint32_t* __restrict__ flag_list, uint32_t* flag_count) {
+    __shared__ uint64_t wkeys[4][WSEL_CAP];
+    __shared__ float wq[4][WSEL_QD];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = blockIdx.x * 4 + wave;
+    if (q >= nq) return;  // per wave: no block barriers below
+    const float* row = D + (size_t)q * L;
+    const int Pe = P < L ? P : L;
+    // element (t, j) of a lane is score 256 t + 4 lane + j; loads clamped in bounds
+    uint32_t fk[64];
+    uint32_t mn = 0xffffffffu;
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+        const int b = 256 * t + 4 * lane;
+        const int bc = b + 4 <= L ? b : (L >= 4 ? ((L - 4) & ~3) : 0);
+        float x[4];
+        if ((L & 3) == 0 && L >= 4) {
+            const float4 v = *reinterpret_cast<const float4*>(row + bc);
+            x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) x[j] = row[b + j < L ? b + j : L - 1];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            fk[4 * t + j] = b + j < L ? fkey(1.0f - x[j]) : 0xffffffffu;
+            mn = fk[4 * t + j] < mn ? fk[4 * t + j] : mn;
+        }
+    }
+    uint64_t km[1] = {mn};
+    wave_sort_regs<1>(km);
+    const uint32_t T = (uint32_t)__shfl(km[0], Pe - 1, 64);
+    const float W = fkey_to_float(T) + 2.0f * coarse_tau(d, qnorm[q], cmax);
+    uint32_t WK = fkey(W);
+    WK = WK < 0xfffffffeu ? WK + 1u : 0xffffffffu;  // one ulp to spare
+    if (WK < T) WK = T;
+    uint32_t cnt = 0;
+    uint64_t* wk = wkeys[wave];
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const bool take = 256 * t + 4 * lane + j < L && fk[4 * t + j] <= WK;
+            const uint64_t m = __ballot(take);
+            const uint32_t below =
+                __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            if (take && cnt + below < WSEL_CAP) wk[cnt + below] = (uint64_t)(256 * t + 4 * lane + j);
+            cnt += (uint32_t)__popcll(m);
+        }
+    }
+    if (cnt > WSEL_CAP) {
+        if (lane == 0) flag_list[atomicAdd(flag_count, 1u)] = (uint32_t)q;
+        return;
+    }
+    float* qs = wq[wave];
+    for (int j = lane; j < d; j += 64) qs[j] = qn[(size_t)q * d + j];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    uint64_t k4[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t t = e * 64 + lane;
+        k4[e] = ~0ull;
+        if (t < cnt) {
+            const uint32_t c = (uint32_t)wk[t];
+            k4[e] = cand_key(1.0f - seq_dot_stream(qs, C + (size_t)c * d, d), c);
+        }
+    }
+    if (cnt <= 64) {
+        uint64_t k1[1] = {k4[0]};
+        wave_sort_regs<1>(k1);
+        if (lane < Pe) probe[(size_t)q * P + lane] = (uint32_t)k1[0];
+    } else if (cnt <= 128) {
+        uint64_t k2[2] = {k4[0], k4[1]};
+        wave_sort_regs<2>(k2);
+#pragma unroll
+        for (int e = 0; e < 2; e++)
+            if (e * 64 + lane < Pe) probe[(size_t)q * P + e * 64 + lane] = (uint32_t)k2[e];
+    } else {
+        wave_sort_regs<4>(k4);
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (e * 64 + lane < Pe) probe[(size_t)q * P + e * 64 + lane] = (uint32_t)k4[e];
+    }
+}
+
+// Generic selection (any L): radix select over the score row in global memory.
 __global__ __launch_bounds__(256) void coarse_select_kernel(
     float* __restrict__ D, const float* __restrict__ qn, const float* __restrict__ qnorm,
     const float* __restrict__ C, int nq, int L, int d, int P, float cmax,
@@ -199,10 +482,28 @@ __global__ __launch_bounds__(256) void coarse_select_kernel(
 
 void launch_coarse_select(float* D, const float* qn, const float* qnorm, const float* C, int nq,
                           int L, int d, int P, float cmax, uint32_t* probe,
-                          unsigned int* overflow, hipStream_t s) {
+                          unsigned int* overflow, uint32_t* flag_list, uint32_t* flag_count,
+                          hipStream_t s) {
     if (nq <= 0) return;
-    hipLaunchKernelGGL(coarse_select_kernel, dim3(nq), dim3(256), 0, s, D, qn, qnorm, C, nq, L, d,
-                       P, cmax, probe, overflow);
+    const int Pe = P < L ? P : L;
+    if (d > SEL_CAP || Pe > 256 || L > 64 * VGPU_BLOCK) {
+        hipLaunchKernelGGL(coarse_select_kernel, dim3(nq), dim3(256), 0, s, D, qn, qnorm, C, nq, L, d,
+                           P, cmax, probe, overflow);
+        return;
+    }
+    auto block = L <= 16 * VGPU_BLOCK   ? coarse_select_reg_kernel<16>
+                 : L <= 32 * VGPU_BLOCK ? coarse_select_reg_kernel<32>
+                                        : coarse_select_reg_kernel<64>;
+    if (L <= 4096 && Pe <= 64 && d <= WSEL_QD) {
+        (void)hipMemsetAsync(flag_count, 0, sizeof(uint32_t), s);
+        hipLaunchKernelGGL(coarse_select_wave_kernel, dim3((nq + 3) / 4), dim3(256), 0, s, D, qn, qnorm,
+                           C, nq, L, d, P, cmax, probe, flag_list, flag_count);
+        hipLaunchKernelGGL(block, dim3(nq < 128 ? nq : 128), dim3(256), 0, s, D, qn, qnorm, C, nq, L,
+                           d, P, cmax, probe, overflow, flag_list, flag_count);
+        return;
+    }
+    hipLaunchKernelGGL(block, dim3(nq), dim3(256), 0, s, D, qn, qnorm, C, nq, L, d, P, cmax, probe,
+                       overflow, nullptr, nullptr);
 }
 
 }  // namespace vgpu

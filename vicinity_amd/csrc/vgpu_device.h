@@ -38,6 +38,35 @@ __device__ __forceinline__ float seq_dot(const float* a, const float* b, int n) 
     return s;
 }
 
+// The same sequential order with the second operand streamed from global
+// memory 32 floats at a time (eight 16-byte loads in flight per step), for
+// d % 4 == 0 and 16-byte aligned b; other shapes take seq_dot.
+__device__ __forceinline__ float seq_dot_stream(const float* a, const float* __restrict__ b, int d) {
+    if ((d & 3) != 0) return seq_dot(a, b, d);
+    float s = 0.0f;
+    int j0 = 0;
+    for (; j0 + 32 <= d; j0 += 32) {
+        float4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = reinterpret_cast<const float4*>(b + j0)[i];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            s = __fadd_rn(s, __fmul_rn(a[j0 + 4 * i], v[i].x));
+            s = __fadd_rn(s, __fmul_rn(a[j0 + 4 * i + 1], v[i].y));
+            s = __fadd_rn(s, __fmul_rn(a[j0 + 4 * i + 2], v[i].z));
+            s = __fadd_rn(s, __fmul_rn(a[j0 + 4 * i + 3], v[i].w));
+        }
+    }
+    for (; j0 < d; j0 += 4) {
+        const float4 v = reinterpret_cast<const float4*>(b + j0)[0];
+        s = __fadd_rn(s, __fmul_rn(a[j0], v.x));
+        s = __fadd_rn(s, __fmul_rn(a[j0 + 1], v.y));
+        s = __fadd_rn(s, __fmul_rn(a[j0 + 2], v.z));
+        s = __fadd_rn(s, __fmul_rn(a[j0 + 3], v.w));
+    }
+    return s;
+}
+
 // Ascending bitonic sort of keys[0..n) (n a power of two) with a payload array.
 // All threads of the block must call it.
 template <typename P>
@@ -211,4 +240,40 @@ __device__ __forceinline__ int wave_append_slot_count(bool take, uint32_t* count
     base = __shfl(base, leader, 64);
     *after = base + cnt;
     return take ? (int)(base + below) : -1;
+}
+
+// Ascending bitonic sort of 64*E keys held by one wave, E per lane; element
+// e*64 + lane lives in k[e] of that lane.  No LDS, no barriers.
+template <int E>
+__device__ __forceinline__ void wave_sort_regs(uint64_t (&k)[E]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int size = 2; size <= 64 * E; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride >= 64) {
+                const int es = stride >> 6;
+#pragma unroll
+                for (int e = 0; e < E; e++) {
+                    const int f = e ^ es;
+                    if (f > e) {
+                        const bool asc = (((e << 6) | lane) & size) == 0;
+                        const uint64_t a = k[e], b = k[f];
+                        const bool sw = (a > b) == asc;
+                        k[e] = sw ? b : a;
+                        k[f] = sw ? a : b;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; e++) {
+                    const uint64_t o = __shfl_xor(k[e], stride, 64);
+                    const bool asc = (((e << 6) | lane) & size) == 0;
+                    const bool lower = (lane & stride) == 0;
+                    const bool take_min = lower == asc;
+                    k[e] = take_min ? (o < k[e] ? o : k[e]) : (o > k[e] ? o : k[e]);
+                }
+            }
+        }
+    }
 }

@@ -111,13 +111,15 @@ void IvfpqIndex::assign_cosine(const float* d_x, const float* d_norms, size_t nx
     size_t chunk = std::max<size_t>(1, std::min<size_t>(nx, ((size_t)1 << 28) / std::max<size_t>(k, 1)));
     chunk = std::min<size_t>(chunk, (size_t)1 << 20);  // grid.y of the GEMM stays < 65536
     w_dots.reserve(chunk * k);
+    w_cflag_list.reserve(chunk);
+    w_cflag_count.reserve(1);
     w_overflow.reserve(1);
     VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
     for (size_t q0 = 0; q0 < nx; q0 += chunk) {
         size_t nc = std::min(chunk, nx - q0);
         launch_coarse_dots(d_x + q0 * d, d_cent, w_dots.p, (int)nc, (int)k, (int)d, s);
         launch_coarse_select(w_dots.p, d_x + q0 * d, d_norms + q0, d_cent, (int)nc, (int)k, (int)d, 1,
-                             cmax, d_assign + q0, w_overflow.p, s);
+                             cmax, d_assign + q0, w_overflow.p, w_cflag_list.p, w_cflag_count.p, s);
     }
     VGPU_HIP(hipGetLastError());
 }
@@ -471,6 +473,8 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
     w_qn.reserve(chunk * d);
     w_qnorm.reserve(chunk);
     w_dots.reserve(chunk * L);
+    w_cflag_list.reserve(chunk);
+    w_cflag_count.reserve(1);
     w_probe.reserve(chunk * P);
     w_vidx.reserve(chunk * kout);
     w_dist.reserve(chunk * kout);
@@ -493,7 +497,8 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
         launch_coarse_dots(w_qn.p, d_centroids.p, w_dots.p, (int)nc, (int)L, (int)d, s);
         if (profiling) VGPU_HIP(hipEventRecord(ev[2], s));
         launch_coarse_select(w_dots.p, w_qn.p, w_qnorm.p, d_centroids.p, (int)nc, (int)L, (int)d,
-                             (int)P, dix.cmax, w_probe.p, w_overflow.p, s);
+                             (int)P, dix.cmax, w_probe.p, w_overflow.p, w_cflag_list.p,
+                             w_cflag_count.p, s);
         if (profiling) VGPU_HIP(hipEventRecord(ev[3], s));
         ScanArgs a;
         a.qn = w_qn.p;
@@ -603,12 +608,15 @@ void IvfpqIndex::probe_host(const float* q, size_t nq, size_t nprobe, uint32_t* 
     VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), stream));
     size_t chunk = std::max<size_t>(1, std::min<size_t>(nq, ((size_t)1 << 28) / L));
     w_dots.reserve(chunk * L);
+    w_cflag_list.reserve(chunk);
+    w_cflag_count.reserve(1);
     launch_normalize(w_q.p, w_qn.p, w_qnorm.p, (int)nq, (int)d, stream);
     for (size_t q0 = 0; q0 < nq; q0 += chunk) {
         size_t nc = std::min(chunk, nq - q0);
         launch_coarse_dots(w_qn.p + q0 * d, d_centroids.p, w_dots.p, (int)nc, (int)L, (int)d, stream);
         launch_coarse_select(w_dots.p, w_qn.p + q0 * d, w_qnorm.p + q0, d_centroids.p, (int)nc, (int)L,
-                             (int)d, (int)P, dix.cmax, w_probe.p + q0 * P, w_overflow.p, stream);
+                             (int)d, (int)P, dix.cmax, w_probe.p + q0 * P, w_overflow.p,
+                             w_cflag_list.p, w_cflag_count.p, stream);
     }
     VGPU_HIP(hipGetLastError());
     VGPU_HIP(hipMemcpyAsync(lists, w_probe.p, nq * P * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));

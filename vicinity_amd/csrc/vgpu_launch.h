@@ -50,12 +50,13 @@ void launch_normalize(const float* x, float* out, float* norms, int n, int d, hi
 void launch_coarse_dots(const float* Q, const float* C, float* D, int nq, int L, int d,
                         hipStream_t s);
 // Probe selection with exact rescoring: probe[q*P..] = the P lists of smallest
-// 1 - dot (ties: lower list index), ascending.  D is overwritten on overflow.
+// 1 - dot (ties: lower list index), ascending.  D may be overwritten for
+// degenerate rows.  flag_list [nq] / flag_count [1]: device scratch.
 void launch_coarse_select(float* D, const float* qn, const float* qnorm, const float* C,
                           int nq, int L, int d, int P, float cmax, uint32_t* probe,
-                          unsigned int* overflow, hipStream_t s);
+                          unsigned int* overflow, uint32_t* flag_list, uint32_t* flag_count,
+                          hipStream_t s);
 
-// EXACT mode: the reference's per-(query, list) residual table in LDS.
 size_t scan8_lds_bytes(const DevIndex& ix, const ScanArgs& a);
 void launch_scan8_exact(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 // FAST mode: per-query decomposed table, threshold buffer, exact rescoring of
