@@ -33,6 +33,19 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def traffic_from_profile():
+    """HBM bytes per scan launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (calibrated against a copy kernel), or None."""
+    path = os.path.join(ROOT, "profiles", "scan8_fast_ivfpq_1m_d128_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(art, queries, k, nprobe, budget_s=15.0):
     """Oracle search (python.rs batch shape over a thread pool) on a bounded
     query sample; returns (qps, threads, sample_size, ids, dists)."""
@@ -155,7 +168,8 @@ def main():
                    "batch": nq, "mode": args.mode, "train_sample": args.train_sample,
                    "kmeans_iters": args.kmeans_iters},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profile() if args.n == 1_000_000 else None,
                      "kernel": "scan8_fast_kernel<16,256>", "kernel_ms": round(scan_ms, 4),
                      "algorithmic_bytes_per_launch": int(scan_bytes),
                      "candidates_per_launch": int(cands)},
