@@ -51,8 +51,7 @@ __global__ __launch_bounds__(256) void normalize_kernel(const float* __restrict_
 void launch_normalize(const float* x, float* out, float* norms, int n, int d, hipStream_t s) {
     if (n <= 0) return;
     const size_t lds = (size_t)NR_ROWS * (d + 1) * sizeof(float);
-    (void)hipFuncSetAttribute((const void*)normalize_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)lds);
+    ensure_dyn_lds((const void*)normalize_kernel, lds);
     hipLaunchKernelGGL(normalize_kernel, dim3((n + NR_ROWS - 1) / NR_ROWS), dim3(VGPU_BLOCK), lds, s,
                        x, out, norms, n, d);
 }
@@ -495,7 +494,6 @@ void launch_coarse_select(float* D, const float* qn, const float* qnorm, const f
                  : L <= 32 * VGPU_BLOCK ? coarse_select_reg_kernel<32>
                                         : coarse_select_reg_kernel<64>;
     if (L <= 4096 && Pe <= 64 && d <= WSEL_QD) {
-        (void)hipMemsetAsync(flag_count, 0, sizeof(uint32_t), s);
         hipLaunchKernelGGL(coarse_select_wave_kernel, dim3((nq + 3) / 4), dim3(256), 0, s, D, qn, qnorm,
                            C, nq, L, d, P, cmax, probe, flag_list, flag_count);
         hipLaunchKernelGGL(block, dim3(nq < 128 ? nq : 128), dim3(256), 0, s, D, qn, qnorm, C, nq, L,

@@ -311,8 +311,7 @@ size_t fastscan_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
 void launch_fastscan(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     if (a.nq <= 0) return;
     size_t lds = fastscan_lds_bytes(ix, a);
-    (void)hipFuncSetAttribute((const void*)fastscan_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)lds);
+    ensure_dyn_lds((const void*)fastscan_kernel, lds);
     hipLaunchKernelGGL(fastscan_kernel, dim3(a.nq), dim3(VGPU_BLOCK), lds, s, ix, a,
                        fs_wave_buf(a.kout));
 }
@@ -350,8 +349,7 @@ __global__ void fastscan_test_kernel(const uint8_t* __restrict__ packed, int n, 
 void launch_fastscan_test(const uint8_t* packed, int n, int M, const float* lut, float* out,
                           hipStream_t s) {
     size_t lds = fs_align16((size_t)M * 16 * 4) + fs_align16((size_t)M * 16);
-    (void)hipFuncSetAttribute((const void*)fastscan_test_kernel,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    ensure_dyn_lds((const void*)fastscan_test_kernel, lds);
     hipLaunchKernelGGL(fastscan_test_kernel, dim3(1), dim3(64), lds, s, packed, n, M, lut, out);
 }
 

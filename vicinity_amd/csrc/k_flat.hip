@@ -306,8 +306,7 @@ void launch_flat_search(const float* Q, const float* Qsq, int nq, const float* X
     const int kk = flat_keep(k), cap = flat_cap(kk), sp = flat_splits(nq, n, kk);
     const int chunk = (((n + sp - 1) / sp) + FL_N - 1) / FL_N * FL_N;
     size_t lds = 2 * FL_Q * (FL_K + 1) * 4 + (size_t)FL_Q * cap * 8 + 2 * FL_Q * 4;
-    (void)hipFuncSetAttribute((const void*)flat_partial_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)lds);
+    ensure_dyn_lds((const void*)flat_partial_kernel, lds);
     dim3 grid((nq + FL_Q - 1) / FL_Q, sp);
     hipLaunchKernelGGL(flat_partial_kernel, grid, dim3(256), lds, s, Q, X, Xnorm, nq, n, d, metric, kk,
                        cap, sp, chunk, partial);

@@ -77,39 +77,65 @@ void launch_finalize(const uint32_t* vidx, const float* dist, const uint32_t* do
                        dist, doc_ids, nq, kin, k, out_ids, out_dists);
 }
 
-// Column sums of the per-query statistics rows into 64-bit counters.
-__global__ __launch_bounds__(256) void stats_reduce_kernel(const uint32_t* __restrict__ qstat,
-                                                           int nq,
-                                                           unsigned long long* __restrict__ counters,
-                                                           uint32_t* flag_count) {
-    constexpr int NC = NUM_SCAN_COUNTERS;
-    __shared__ unsigned long long part[NC][VGPU_BLOCK];
-    unsigned long long c[NC] = {0, 0, 0, 0, 0, 0};
-    for (int q = threadIdx.x; q < nq; q += VGPU_BLOCK) {
-        const uint32_t* st = qstat + (size_t)q * QSTAT_WORDS;
-        c[0] += st[0];              // entries scanned
-        c[1] += st[3] & 1u;         // fallbacks
-        c[2] += st[1];              // flushes
-        c[3] += st[2];              // appends
-        c[4] += (st[3] >> 1) & 1u;  // fallbacks from ties
-        c[5] += (st[3] >> 2) & 1u;  // second passes
+// End of a search chunk, 64 queries per workgroup: map insertion indices to
+// doc ids with (-1, +inf) padding (python.rs:778-785), add the statistics rows
+// into the counters (one atomic per counter per workgroup; counters sit
+// COUNTER_STRIDE words apart), and clear the two flag-list lengths for the
+// next chunk (both lists were consumed by earlier launches).
+#define FINISH_Q 64
+
+__global__ __launch_bounds__(256) void finish_kernel(
+    const uint32_t* __restrict__ vidx, const float* __restrict__ dist,
+    const uint32_t* __restrict__ doc_ids, int nq, int kin, int k, int64_t* __restrict__ out_ids,
+    float* __restrict__ out_dists, const uint32_t* __restrict__ qstat,
+    unsigned long long* __restrict__ counters, uint32_t* flag_count, uint32_t* cflag_count) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int q0 = blockIdx.x * FINISH_Q;
+    const int nqb = min(FINISH_Q, nq - q0);
+    for (int e = tid; e < nqb * k; e += VGPU_BLOCK) {
+        const int q = q0 + e / k, j = e % k;
+        const uint32_t v = j < kin ? vidx[(size_t)q * kin + j] : 0xffffffffu;
+        const size_t o = (size_t)q * k + j;
+        if (v != 0xffffffffu) {
+            out_ids[o] = (int64_t)(doc_ids ? doc_ids[v] : v);
+            out_dists[o] = dist[(size_t)q * kin + j];
+        } else {
+            out_ids[o] = -1;
+            out_dists[o] = __int_as_float(0x7f800000);
+        }
     }
-    for (int i = 0; i < NC; i++) part[i][threadIdx.x] = c[i];
-    __syncthreads();
-    for (int w = VGPU_BLOCK / 2; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w)
-            for (int i = 0; i < NC; i++) part[i][threadIdx.x] += part[i][threadIdx.x + w];
-        __syncthreads();
+    if (qstat && tid < 64) {
+        uint32_t c[NUM_SCAN_COUNTERS] = {0, 0, 0, 0, 0, 0};
+        if (lane < nqb) {
+            const uint32_t* st = qstat + (size_t)(q0 + lane) * QSTAT_WORDS;
+            c[0] = st[0];              // entries scanned
+            c[1] = st[3] & 1u;         // fallbacks
+            c[2] = st[1];              // flushes
+            c[3] = st[2];              // appends
+            c[4] = (st[3] >> 1) & 1u;  // fallbacks from ties
+            c[5] = (st[3] >> 2) & 1u;  // second passes
+        }
+#pragma unroll
+        for (int i = 0; i < NUM_SCAN_COUNTERS; i++) {
+            unsigned long long v = c[i];
+            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+            if (lane == 0 && v) atomicAdd(&counters[i * COUNTER_STRIDE], v);
+        }
     }
-    if (threadIdx.x < NC) counters[threadIdx.x] += part[threadIdx.x][0];
-    if (threadIdx.x == 0 && flag_count) *flag_count = 0u;
+    if (blockIdx.x == 0 && tid == 0) {
+        if (flag_count) *flag_count = 0u;
+        if (cflag_count) *cflag_count = 0u;
+    }
 }
 
-void launch_stats_reduce(const uint32_t* qstat, int nq, unsigned long long* counters,
-                         uint32_t* flag_count, hipStream_t s) {
+void launch_finish(const uint32_t* vidx, const float* dist, const uint32_t* doc_ids, int nq, int kin,
+                   int k, int64_t* out_ids, float* out_dists, const uint32_t* qstat,
+                   unsigned long long* counters, uint32_t* flag_count, uint32_t* cflag_count,
+                   hipStream_t s) {
     if (nq <= 0) return;
-    hipLaunchKernelGGL(stats_reduce_kernel, dim3(1), dim3(VGPU_BLOCK), 0, s, qstat, nq, counters,
-                       flag_count);
+    hipLaunchKernelGGL(finish_kernel, dim3((nq + FINISH_Q - 1) / FINISH_Q), dim3(VGPU_BLOCK), 0, s, vidx,
+                       dist, doc_ids, nq, kin, k, out_ids, out_dists, qstat, counters, flag_count,
+                       cflag_count);
 }
 
 }  // namespace vgpu

@@ -289,7 +289,7 @@ static void launch_mk(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     int buf = scan_buf(a.kk);
     size_t lds = scan8_lds_bytes(ix, a);
     auto k = scan8_exact_kernel<MT, KT>;
-    (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    ensure_dyn_lds((const void*)k, lds);
     // Flagged queries: a small grid walks the list the FAST kernel wrote.
     const int grid = a.only_flagged ? (a.nq < 256 ? a.nq : 256) : a.nq;
     hipLaunchKernelGGL(k, dim3(grid), dim3(VGPU_BLOCK), lds, s, ix, a, buf);

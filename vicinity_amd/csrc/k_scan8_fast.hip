@@ -600,7 +600,7 @@ static void launch_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     size_t off[10];
     const size_t dyn = fs8_layout(ix.d, ix.M, ix.K, a.P, buf, MT > 0 && KT >= 64, off);
     auto k = scan8_fast_kernel<MT, KT, DS>;
-    (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn);
+    ensure_dyn_lds((const void*)k, dyn);
     hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), dyn, s, ix, a, buf);
 }
 

@@ -9,10 +9,23 @@
 #include <cmath>
 #include <cstring>
 #include <numeric>
+#include <unordered_map>
 
 #include "vgpu_runtime.h"
 
 namespace vgpu {
+
+void ensure_dyn_lds(const void* kernel, size_t bytes) {
+    static std::mutex mu;
+    static std::unordered_map<const void*, size_t> set;
+    std::lock_guard<std::mutex> lock(mu);
+    size_t& cur = set[kernel];
+    if (bytes <= cur) return;
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess)
+        cur = bytes;
+    else
+        (void)hipGetLastError();
+}
 
 void hip_check(hipError_t e, const char* what) {
     if (e == hipSuccess) return;
@@ -87,6 +100,7 @@ IvfpqIndex::IvfpqIndex(size_t dim, const vgpu_ivfpq_params& p) : d(dim), params(
 
 IvfpqIndex::~IvfpqIndex() {
     if (stream) (void)hipStreamSynchronize(stream);
+    if (h_scal) (void)hipHostFree(h_scal);
     for (auto& e : ev)
         if (e) (void)hipEventDestroy(e);
     if (stream) (void)hipStreamDestroy(stream);
@@ -118,6 +132,7 @@ void IvfpqIndex::assign_cosine(const float* d_x, const float* d_norms, size_t nx
     for (size_t q0 = 0; q0 < nx; q0 += chunk) {
         size_t nc = std::min(chunk, nx - q0);
         launch_coarse_dots(d_x + q0 * d, d_cent, w_dots.p, (int)nc, (int)k, (int)d, s);
+        VGPU_HIP(hipMemsetAsync(w_cflag_count.p, 0, sizeof(uint32_t), s));
         launch_coarse_select(w_dots.p, d_x + q0 * d, d_norms + q0, d_cent, (int)nc, (int)k, (int)d, 1,
                              cmax, d_assign + q0, w_overflow.p, w_cflag_list.p, w_cflag_count.p, s);
     }
@@ -428,7 +443,11 @@ void IvfpqIndex::upload_index() {
     VGPU_HIP(hipStreamSynchronize(stream));
 }
 
-static constexpr size_t kNumCounters = NUM_SCAN_COUNTERS;
+// Word offsets in the per-call scalar buffer (64-byte lines apart).
+static constexpr size_t kOverflowWord = NUM_SCAN_COUNTERS * COUNTER_STRIDE;
+static constexpr size_t kFlagWord = kOverflowWord + 8;
+static constexpr size_t kCFlagWord = kFlagWord + 8;
+static constexpr size_t kScalWords = kCFlagWord + 8;
 
 static int fast_keep(size_t kout) {
     int kk = 1;
@@ -482,12 +501,16 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
     w_dist2.reserve(chunk * k);
     w_qstat.reserve(chunk * QSTAT_WORDS);
     w_flag_list.reserve(chunk);
-    w_flag_count.reserve(1);
-    w_counters.reserve(kNumCounters);
-    w_overflow.reserve(1);
-    VGPU_HIP(hipMemsetAsync(w_counters.p, 0, kNumCounters * sizeof(unsigned long long), s));
-    VGPU_HIP(hipMemsetAsync(w_flag_count.p, 0, sizeof(uint32_t), s));
-    VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
+    // Per-call device scalars in one buffer, cleared by one memset: counter i
+    // at word i * COUNTER_STRIDE, then the overflow count and the two
+    // flag-list lengths, each on a cache line of its own.
+    w_scal.reserve(kScalWords);
+    if (!h_scal) VGPU_HIP(hipHostMalloc((void**)&h_scal, kScalWords * sizeof(unsigned long long)));
+    unsigned long long* counters = w_scal.p;
+    unsigned int* overflow = reinterpret_cast<unsigned int*>(w_scal.p + kOverflowWord);
+    uint32_t* flag_count = reinterpret_cast<uint32_t*>(w_scal.p + kFlagWord);
+    uint32_t* cflag_count = reinterpret_cast<uint32_t*>(w_scal.p + kCFlagWord);
+    VGPU_HIP(hipMemsetAsync(w_scal.p, 0, kScalWords * sizeof(unsigned long long), s));
     float t[7] = {0, 0, 0, 0, 0, 0, 0};
     for (size_t q0 = 0; q0 < nq; q0 += chunk) {
         const size_t nc = std::min(chunk, nq - q0);
@@ -497,8 +520,7 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
         launch_coarse_dots(w_qn.p, d_centroids.p, w_dots.p, (int)nc, (int)L, (int)d, s);
         if (profiling) VGPU_HIP(hipEventRecord(ev[2], s));
         launch_coarse_select(w_dots.p, w_qn.p, w_qnorm.p, d_centroids.p, (int)nc, (int)L, (int)d,
-                             (int)P, dix.cmax, w_probe.p, w_overflow.p, w_cflag_list.p,
-                             w_cflag_count.p, s);
+                             (int)P, dix.cmax, w_probe.p, overflow, w_cflag_list.p, cflag_count, s);
         if (profiling) VGPU_HIP(hipEventRecord(ev[3], s));
         ScanArgs a;
         a.qn = w_qn.p;
@@ -509,7 +531,7 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
         a.kout = (int)kout;
         a.qstat = w_qstat.p;
         a.flag_list = w_flag_list.p;
-        a.flag_count = w_flag_count.p;
+        a.flag_count = flag_count;
         a.out_vidx = w_vidx.p;
         a.out_dist = w_dist.p;
         if (K == 16) {
@@ -531,7 +553,6 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             launch_scan8_exact(dix, a, s);
             if (profiling) VGPU_HIP(hipEventRecord(ev[4], s));
         }
-        launch_stats_reduce(w_qstat.p, (int)nc, w_counters.p, w_flag_count.p, s);
         if (profiling) VGPU_HIP(hipEventRecord(ev[5], s));
         const uint32_t* vout = w_vidx.p;
         const float* dout = w_dist.p;
@@ -543,8 +564,8 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             kin = k;
         }
         if (profiling) VGPU_HIP(hipEventRecord(ev[6], s));
-        launch_finalize(vout, dout, d_doc_ids.p, (int)nc, (int)kin, (int)k, d_ids + q0 * k,
-                        d_dists + q0 * k, s);
+        launch_finish(vout, dout, d_doc_ids.p, (int)nc, (int)kin, (int)k, d_ids + q0 * k,
+                      d_dists + q0 * k, w_qstat.p, counters, flag_count, cflag_count, s);
         if (profiling) VGPU_HIP(hipEventRecord(ev[7], s));
         VGPU_HIP(hipGetLastError());
         if (profiling) {
@@ -556,11 +577,12 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             }
         }
     }
-    unsigned long long cnt[kNumCounters] = {};
-    unsigned int ovf = 0;
-    VGPU_HIP(hipMemcpyAsync(cnt, w_counters.p, sizeof(cnt), hipMemcpyDeviceToHost, s));
-    VGPU_HIP(hipMemcpyAsync(&ovf, w_overflow.p, sizeof(ovf), hipMemcpyDeviceToHost, s));
+    VGPU_HIP(hipMemcpyAsync(h_scal, w_scal.p, kScalWords * sizeof(unsigned long long),
+                            hipMemcpyDeviceToHost, s));
     VGPU_HIP(hipStreamSynchronize(s));
+    unsigned long long cnt[NUM_SCAN_COUNTERS];
+    for (int i = 0; i < NUM_SCAN_COUNTERS; i++) cnt[i] = h_scal[i * COUNTER_STRIDE];
+    const unsigned int ovf = reinterpret_cast<const unsigned int*>(h_scal + kOverflowWord)[0];
     stats.ms_normalize = t[0];
     stats.ms_coarse = t[1];
     stats.ms_select = t[2];
@@ -614,6 +636,7 @@ void IvfpqIndex::probe_host(const float* q, size_t nq, size_t nprobe, uint32_t* 
     for (size_t q0 = 0; q0 < nq; q0 += chunk) {
         size_t nc = std::min(chunk, nq - q0);
         launch_coarse_dots(w_qn.p + q0 * d, d_centroids.p, w_dots.p, (int)nc, (int)L, (int)d, stream);
+        VGPU_HIP(hipMemsetAsync(w_cflag_count.p, 0, sizeof(uint32_t), stream));
         launch_coarse_select(w_dots.p, w_qn.p + q0 * d, w_qnorm.p + q0, d_centroids.p, (int)nc, (int)L,
                              (int)d, (int)P, dix.cmax, w_probe.p + q0 * P, w_overflow.p,
                              w_cflag_list.p, w_cflag_count.p, stream);

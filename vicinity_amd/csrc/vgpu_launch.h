@@ -7,6 +7,10 @@
 
 namespace vgpu {
 
+// Raise a kernel's dynamic-LDS limit to at least `bytes`; the attribute is set
+// once per kernel and size increase, not on every launch.
+void ensure_dyn_lds(const void* kernel, size_t bytes);
+
 // HBM-resident IVF-PQ index (all pointers are device memory).
 struct DevIndex {
     int d = 0, L = 0, M = 0, K = 0, ds = 0;
@@ -35,7 +39,7 @@ struct ScanArgs {
     int exact = 0;                  // 1 = EXACT mode
     int only_flagged = 0;           // EXACT: run the queries of flag_list only
     uint32_t* flag_list = nullptr;  // [nq] queries FAST could not prove (appended by FAST)
-    uint32_t* flag_count = nullptr; // entries of flag_list (zeroed by launch_stats_reduce)
+    uint32_t* flag_count = nullptr; // entries of flag_list (zeroed by launch_finish)
     uint32_t* out_vidx = nullptr;   // [nq*kout] insertion indices, 0xffffffff padding
     float* out_dist = nullptr;      // [nq*kout]
     // Per-query statistics, one row of QSTAT_WORDS per query, written with plain
@@ -51,7 +55,8 @@ void launch_coarse_dots(const float* Q, const float* C, float* D, int nq, int L,
                         hipStream_t s);
 // Probe selection with exact rescoring: probe[q*P..] = the P lists of smallest
 // 1 - dot (ties: lower list index), ascending.  D may be overwritten for
-// degenerate rows.  flag_list [nq] / flag_count [1]: device scratch.
+// degenerate rows.  flag_list [nq] / flag_count [1]: device scratch; *flag_count
+// must be 0 on entry and is left holding the number of degenerate rows.
 void launch_coarse_select(float* D, const float* qn, const float* qnorm, const float* C,
                           int nq, int L, int d, int P, float cmax, uint32_t* probe,
                           unsigned int* overflow, uint32_t* flag_list, uint32_t* flag_count,
@@ -66,12 +71,18 @@ size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a);
 void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 
 #define QSTAT_WORDS 4
-// counters[0..5] += sums over the rows of qstat[nq][QSTAT_WORDS]: entries
-// scanned, fallbacks, flushes, appends, fallbacks from ties, second passes;
-// then *flag_count = 0 (may be null).  One workgroup.
+// Search statistics: entries scanned, fallbacks, flushes, appends, fallbacks
+// from ties, second passes; counter i lives at counters[i * COUNTER_STRIDE]
+// (separate cache lines for the per-workgroup atomics).
 #define NUM_SCAN_COUNTERS 6
-void launch_stats_reduce(const uint32_t* qstat, int nq, unsigned long long* counters,
-                         uint32_t* flag_count, hipStream_t s);
+#define COUNTER_STRIDE 8
+// Chunk epilogue: doc-id mapping and padding of (vidx, dist)[nq][kin] into
+// (out_ids, out_dists)[nq][k]; counters += the qstat rows (qstat may be null);
+// *flag_count = *cflag_count = 0 (either may be null).
+void launch_finish(const uint32_t* vidx, const float* dist, const uint32_t* doc_ids, int nq, int kin,
+                   int k, int64_t* out_ids, float* out_dists, const uint32_t* qstat,
+                   unsigned long long* counters, uint32_t* flag_count, uint32_t* cflag_count,
+                   hipStream_t s);
 size_t fastscan_lds_bytes(const DevIndex& ix, const ScanArgs& a);
 void launch_fastscan(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 

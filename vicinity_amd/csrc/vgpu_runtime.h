@@ -87,10 +87,11 @@ struct IvfpqIndex {
 
     // search workspace
     DevBuf<float> w_q, w_qn, w_qnorm, w_dots, w_dist, w_dist2, w_odist;
-    DevBuf<uint32_t> w_probe, w_vidx, w_vidx2, w_qstat, w_flag_list, w_flag_count;
+    DevBuf<uint32_t> w_probe, w_vidx, w_vidx2, w_qstat, w_flag_list;
     DevBuf<uint32_t> w_cflag_list, w_cflag_count;  // coarse selection fallback list
     DevBuf<int64_t> w_ids;
-    DevBuf<unsigned long long> w_counters;
+    DevBuf<unsigned long long> w_scal;           // per-call device scalars (see search_device)
+    unsigned long long* h_scal = nullptr;        // pinned host copy of w_scal
     DevBuf<unsigned int> w_overflow;
     vgpu_search_stats stats{};
     std::mutex mu;
