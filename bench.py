@@ -131,7 +131,8 @@ def main():
                  "appends_per_query": round(stats[-1]["fast_appends"] / nq, 1),
                  "candidates_per_query": round(stats[-1]["candidates"] / nq, 1),
                  "fallback_ties": int(stats[-1]["fallback_ties"]),
-                 "second_passes": int(stats[-1]["fast_retries"])}
+                 "second_passes": int(stats[-1]["fast_retries"]),
+                 "coarse_fallbacks": int(stats[-1]["coarse_overflow"])}
     log(f"{qps:.0f} QPS, {ms_step:.3f} ms/batch, scan {scan_ms:.3f} ms, {achieved:.0f} GB/s, "
         f"phases {phases}, fallback queries {fallbacks}, scan {scan_diag}")
 

@@ -70,7 +70,7 @@ typedef struct vgpu_search_stats {
     uint64_t candidates;     /* sum over queries of scanned list entries */
     uint64_t scan_bytes;     /* algorithmic bytes of the scan: candidates * (code bytes + 4) */
     uint32_t fallback_queries; /* FAST queries recomputed in EXACT mode */
-    uint32_t coarse_overflow;  /* queries whose coarse margin set exceeded LDS */
+    uint32_t coarse_overflow;  /* queries whose probe selection took the exact fallback */
     uint32_t nq;
     uint64_t fast_flushes;     /* FAST: buffer flushes summed over queries */
     uint64_t fast_appends;     /* FAST: entries that passed the running threshold */
@@ -179,6 +179,10 @@ int vgpu_test_fastscan(const uint8_t *packed, size_t n, size_t M, const float *l
 /* Coarse dot products Q.C^T with the MFMA kernel: out f32[nq*L]. */
 int vgpu_test_coarse_dots(const float *q, size_t nq, const float *c, size_t L, size_t d,
                           float *out);
+/* The same products with the search path's split-bfloat16 (bf16x3) MFMA
+ * kernel, d <= 128: out f32[nq*L]. */
+int vgpu_test_coarse_dots_bf16x3(const float *q, size_t nq, const float *c, size_t L, size_t d,
+                                 float *out);
 
 #ifdef __cplusplus
 }

@@ -371,10 +371,10 @@ def test_fast_second_pass_and_exact_rerun(vg, oracle, copies, expect):
 
 @pytest.mark.parametrize("d,L,P", [(24, 37, 8), (16, 300, 20), (32, 2000, 40), (16, 13, 13)])
 def test_probe_selection_paths(vg, oracle, d, L, P):
-    """Probe lists through every selection path: L not a multiple of 4, fewer
-    score-holding lanes than probes, and zero queries whose window of exact ties
-    overflows the one-wave kernel (L = 300: block kernel; L = 2000: its 64-bit
-    radix fallback).  Lists must equal the oracle's, ties by lower list index."""
+    """Probe lists for L not a multiple of the 16-list tile or the 64-list
+    stage, L < 16 and P = L (every list probed), P above 32 (the 16-key lane
+    lists), and zero queries (all scores tie).  Lists must equal the oracle's,
+    ties by lower list index."""
     from vicinity_amd import IVFPQIndex
 
     _print_case(f"probe paths d={d} L={L} P={P}")
@@ -392,6 +392,57 @@ def test_probe_selection_paths(vg, oracle, d, L, P):
     q = rng.standard_normal((40, d)).astype(np.float32)
     q[3] = 0.0
     q[17] = 0.0
+    lists = ix.probe(q, P)
+    oix = oracle.Index(cent, cb, off, ids, codes, np.arange(n, dtype=np.uint32), None, M, K)
+    for i in range(len(q)):
+        assert lists[i].tolist() == oix.probe(q[i], P)[0].tolist(), i
+
+
+@pytest.mark.parametrize("nq,L,d", [(70, 100, 36), (64, 64, 32), (1, 3, 128), (130, 257, 100),
+                                    (200, 4096, 128)])
+def test_coarse_bf16x3_dots_within_bound(vg, nq, L, d):
+    """Split-bfloat16 MFMA dot products (the search path's coarse kernel)
+    against float64, within the bound its proof window uses:
+    (3 * 2^-18 + 7 d u) sum|q_j c_j|.  A wrong operand or output lane layout
+    fails by orders of magnitude."""
+    from vicinity_amd import _lib
+
+    rng = np.random.default_rng(nq * 7 + L + d)
+    q = rng.standard_normal((nq, d)).astype(np.float32)
+    c = rng.standard_normal((L, d)).astype(np.float32)
+    out = np.empty((nq, L), np.float32)
+    _lib.check(_lib.load().vgpu_test_coarse_dots_bf16x3(_lib.ptr(q), nq, _lib.ptr(c), L, d, _lib.ptr(out)))
+    ref = q.astype(np.float64) @ c.astype(np.float64).T
+    absdot = np.abs(q).astype(np.float64) @ np.abs(c).astype(np.float64).T
+    bound = (3 * 2.0 ** -18 + 7 * d * 2.0 ** -24) * absdot
+    err = np.abs(out - ref)
+    assert (err <= bound + 1e-30).all(), float((err / (absdot + 1e-30)).max())
+
+
+@pytest.mark.parametrize("step,copies,P", [(16, 12, 8), (1, 12, 8), (16, 20, 40), (3, 30, 32)])
+def test_probe_ties_through_the_exact_fallback(vg, oracle, step, copies, P):
+    """Copies of one centroid at lists 5, 5 + step, ...: with step 16 they all
+    share one lane's column class and overflow its key list, so the query
+    takes the exact fallback; with other steps the tie window spans lanes.
+    Either way the P lists are the copies in index order (oracle ties by
+    lower index), then the next nearest."""
+    from vicinity_amd import IVFPQIndex
+
+    _print_case(f"probe ties step={step} copies={copies} P={P}")
+    d, L = 32, 700
+    rng = np.random.default_rng(step * 100 + copies + P)
+    cent = oracle.normalize_rows(rng.standard_normal((L, d)).astype(np.float32))
+    base = cent[1].copy()
+    cent[5 + step * np.arange(copies)] = base
+    n = 2 * L
+    M, K = 4, 16
+    cb = rng.standard_normal(M * K * (d // M)).astype(np.float32)
+    off, ids = oracle.build_lists((np.arange(n) % L).astype(np.uint32), L)
+    codes = rng.integers(0, K, (n, M), dtype=np.uint8)
+    ix = IVFPQIndex(d, num_clusters=L, num_codebooks=M, codebook_size=K, nprobe=P)
+    ix.load_artifacts(cent, cb, off, ids, codes)
+    q = (base[None, :] + 0.01 * rng.standard_normal((6, d))).astype(np.float32)
+    q[0] = base
     lists = ix.probe(q, P)
     oix = oracle.Index(cent, cb, off, ids, codes, np.arange(n, dtype=np.uint32), None, M, K)
     for i in range(len(q)):

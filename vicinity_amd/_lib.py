@@ -103,6 +103,7 @@ SIGNATURES = {
     "vgpu_test_normalize": (_i, [_vp, _sz, _sz, _vp]),
     "vgpu_test_fastscan": (_i, [_vp, _sz, _sz, _vp, _vp]),
     "vgpu_test_coarse_dots": (_i, [_vp, _sz, _vp, _sz, _sz, _vp]),
+    "vgpu_test_coarse_dots_bf16x3": (_i, [_vp, _sz, _vp, _sz, _sz, _vp]),
 }
 
 _lib = None

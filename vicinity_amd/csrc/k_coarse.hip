@@ -125,7 +125,7 @@ void launch_coarse_dots(const float* Q, const float* C, float* D, int nq, int L,
 // ---- probe selection ----------------------------------------------------
 #define SEL_CAP 1024
 
-// Error bound of the MFMA score against the sequential one: both are within
+// Error bound of the fp32 scores (MFMA GEMM or approx_dot) against the sequential one: both are within
 // (d + 2) u sum|q_j c_j| <= (d + 2) u ||q|| ||c|| of the real dot product,
 // plus the rounding of 1 - dot; doubled for safety.
 __device__ __forceinline__ float coarse_tau(int d, float qn, float cmax) {
@@ -181,19 +181,18 @@ __device__ inline void select_window_exact(uint64_t* keys, uint32_t cn, const fl
 // distinct threads hold a score <= T), so every list whose exact score can be
 // among the Pe smallest has approximate score <= T + 2 tau.  Those are rescored
 // exactly and sorted.  Pe <= 256.
+// row: the query's L dot products (global or LDS; overwritten for degenerate
+// windows); qv: the normalised query.
 template <int EPT>
-__device__ void select_block_query(float* __restrict__ D, const float* __restrict__ qn,
-                                   const float* __restrict__ qnorm, const float* __restrict__ C,
-                                   int q, int L, int d, int P, float cmax,
-                                   uint32_t* __restrict__ probe, unsigned int* overflow) {
+__device__ void select_block_query(float* row, const float* __restrict__ qv, float qnorm_q,
+                                   const float* __restrict__ C, int q, int L, int d, int P,
+                                   float cmax, uint32_t* __restrict__ probe, unsigned int* overflow) {
     __shared__ RadixScratch rs;
     __shared__ uint64_t keys[SEL_CAP];
     __shared__ uint32_t pay[SEL_CAP];
     __shared__ uint32_t mins[VGPU_BLOCK];
     __shared__ uint32_t cnt, tsel;
     const int tid = threadIdx.x, lane = tid & 63;
-    float* row = D + (size_t)q * L;
-    const float* qv = qn + (size_t)q * d;
     const int Pe = P < L ? P : L;
 
     uint32_t fk[EPT];
@@ -227,7 +226,7 @@ __device__ void select_block_query(float* __restrict__ D, const float* __restric
     }
     __syncthreads();
     const uint32_t T = tsel;
-    const float W = fkey_to_float(T) + 2.0f * coarse_tau(d, qnorm[q], cmax);
+    const float W = fkey_to_float(T) + 2.0f * coarse_tau(d, qnorm_q, cmax);
     uint32_t WK = fkey(W);
     WK = WK < 0xfffffffeu ? WK + 1u : 0xffffffffu;  // one ulp to spare
     if (WK < T) WK = T;
@@ -287,14 +286,63 @@ __global__ __launch_bounds__(256) void coarse_select_reg_kernel(
     uint32_t* __restrict__ probe, unsigned int* overflow, const uint32_t* flag_list,
     const uint32_t* flag_count) {
     if (!flag_list) {
-        if ((int)blockIdx.x < nq)
-            select_block_query<EPT>(D, qn, qnorm, C, blockIdx.x, L, d, P, cmax, probe, overflow);
+        const int q = blockIdx.x;
+        if (q < nq)
+            select_block_query<EPT>(D + (size_t)q * L, qn + (size_t)q * d, qnorm[q], C, q, L, d, P, cmax,
+                                    probe, overflow);
         return;
     }
     const uint32_t nf = *flag_count;  // written by the wave kernel before this launch
     for (uint32_t i = blockIdx.x; i < nf; i += gridDim.x) {
         __syncthreads();
-        select_block_query<EPT>(D, qn, qnorm, C, (int)flag_list[i], L, d, P, cmax, probe, overflow);
+        const int q = (int)flag_list[i];
+        select_block_query<EPT>(D + (size_t)q * L, qn + (size_t)q * d, qnorm[q], C, q, L, d, P, cmax,
+                                probe, overflow);
+    }
+}
+
+// Queries whose fused-kernel candidate set may be incomplete (a lane's key
+// list overflowed: many lists tie or crowd the window): approximate dot
+// products of all L lists (approx_dot, within the same bound coarse_tau
+// covers) go to LDS, then the block selection (window, exact rescoring)
+// runs on them.  The grid walks the flagged list.
+template <int EPT>
+__global__ __launch_bounds__(256) void coarse_exact_flagged_kernel(
+    const float* __restrict__ qn, const float* __restrict__ qnorm, const float* __restrict__ C, int L,
+    int d, int P, float cmax, uint32_t* __restrict__ probe, unsigned int* overflow,
+    const uint32_t* flag_list, const uint32_t* flag_count) {
+    extern __shared__ __align__(16) float qs[];  // [d rounded up to 4] query, then [L] dots
+    float* xrow = qs + ((d + 3) & ~3);
+    const uint32_t nf = *flag_count;  // written by the top-P kernel before this launch
+    for (uint32_t fi = blockIdx.x; fi < nf; fi += gridDim.x) {
+        __syncthreads();
+        const int q = (int)flag_list[fi];
+        for (int j = threadIdx.x; j < d; j += VGPU_BLOCK) qs[j] = qn[(size_t)q * d + j];
+        __syncthreads();
+        for (int i = threadIdx.x; i < L; i += VGPU_BLOCK) xrow[i] = approx_dot(qs, C + (size_t)i * d, d);
+        __syncthreads();
+        select_block_query<EPT>(xrow, qs, qnorm[q], C, q, L, d, P, cmax, probe, overflow);
+    }
+}
+
+void launch_coarse_exact_flagged(const float* qn, const float* qnorm, const float* C, int nq, int L,
+                                 int d, int P, float cmax, uint32_t* probe, unsigned int* overflow,
+                                 const uint32_t* flag_list, const uint32_t* flag_count, hipStream_t s) {
+    if (nq <= 0) return;
+    const size_t lds = ((size_t)L + ((d + 3) & ~3)) * sizeof(float);
+    const dim3 grid(nq < 256 ? nq : 256);
+    if (L <= 16 * VGPU_BLOCK) {
+        ensure_dyn_lds((const void*)coarse_exact_flagged_kernel<16>, lds);
+        hipLaunchKernelGGL(coarse_exact_flagged_kernel<16>, grid, dim3(256), lds, s, qn, qnorm, C, L, d, P,
+                           cmax, probe, overflow, flag_list, flag_count);
+    } else if (L <= 32 * VGPU_BLOCK) {
+        ensure_dyn_lds((const void*)coarse_exact_flagged_kernel<32>, lds);
+        hipLaunchKernelGGL(coarse_exact_flagged_kernel<32>, grid, dim3(256), lds, s, qn, qnorm, C, L, d, P,
+                           cmax, probe, overflow, flag_list, flag_count);
+    } else {
+        ensure_dyn_lds((const void*)coarse_exact_flagged_kernel<64>, lds);
+        hipLaunchKernelGGL(coarse_exact_flagged_kernel<64>, grid, dim3(256), lds, s, qn, qnorm, C, L, d, P,
+                           cmax, probe, overflow, flag_list, flag_count);
     }
 }
 

@@ -1,0 +1,544 @@
+// Coarse quantiser in two kernels, without a query x centroid score matrix:
+//
+//   coarse_fused_kernel  32 queries per workgroup.  Normalises its queries
+//       (search.rs:55-62, writes qn), then makes one pass of bf16x3 MFMA dot
+//       products against every centroid: q.c ~ qh.ch + qh.cl + ql.ch with
+//       x = xh + xl + O(2^-18 |x|) split into bfloat16 halves.  Each (lane, query)
+//       keeps the J largest products of the lane's column class, packed with
+//       their list index into one float key; two waves share a query block and
+//       merge their lists.  The keys above a threshold derived from the P-th
+//       largest key and the error bounds are the query's candidates.
+//   coarse_topp_kernel   one wave per query: rescores the candidates with the
+//       reference's sequential dot (cosine_distance_normalized,
+//       src/distance.rs:104-109), sorts by (score, list) and writes the P
+//       smallest in order (find_nearest_centroids, search.rs:1602-1617).  A
+//       query whose candidate set may be incomplete goes to
+//       launch_coarse_exact_flagged.
+//
+// MFMA layout (v_mfma_f32_16x16x32_bf16, wave64): lane l holds row/column
+// l % 16 and eight consecutive k of group l / 16 for A and B; the result
+// element (4 (l / 16) + i, l % 16) sits in element i of lane l.  A and B use
+// the same dimension-to-(group, slot) assignment, so every dimension is
+// summed exactly once.
+#include "vgpu_device.h"
+#include "vgpu_launch.h"
+
+namespace vgpu {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+// Native 128-bit vector (HIP's uint4 is a struct whose copies stay in memory).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+#define FC_QBW 2               // query blocks (16 queries each) per workgroup
+#define FC_QB (16 * FC_QBW)    // queries per workgroup
+#define FC_NH 2                // waves per query block; each takes its own tiles of a stage
+#define FC_SUB 2               // 16-centroid tiles per wave and stage
+#define FC_ST (FC_NH * FC_SUB) // tiles per stage
+static_assert(FC_QBW * FC_NH * 64 == VGPU_BLOCK, "wave roles");
+
+// Round to nearest even bfloat16 (finite inputs).
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// x = hi + lo + r with |r| <= 2^-18 |x|; returns (hi, lo) bit patterns.
+__device__ __forceinline__ void bf16_split(float x, uint32_t& hi, uint32_t& lo) {
+    hi = bf16_bits(x);
+    const float rem = x - __uint_as_float(hi << 16);  // exact (Sterbenz)
+    lo = bf16_bits(rem);
+}
+
+// Error bound eps of the bf16x3 score against the reference's sequential one
+// for ||q|| <= qn, ||c|| <= cmax (u = 2^-24): the dropped terms (ql.cl and the
+// split remainders) are within 3.01 * 2^-18 sum|q_j c_j|, the fp32
+// accumulation of 3d exact products within 3d 2u (accumulation that
+// truncates), the sequential dot within d u, and 1 - dot rounds within
+// 2u (1 + qn cmax).
+__device__ __forceinline__ float coarse_eps_bf16(int d, float qn, float cmax) {
+    const float u = 5.9604645e-08f;
+    const float qc = qn * cmax;
+    return (3.01f * 3.8146973e-06f + 7.0f * (float)d * u) * qc + 2.0f * u * (1.0f + qc) + 1e-30f;
+}
+
+// Pack centroids into bf16 hi/lo chunks in the order the MFMA tiles read them
+// from LDS, so a pipeline stage is one contiguous copy: chunk
+// Cb[(((tile * 2 + h) * DT + t) * 4 + g) * 16 + c % 16], tile = c / 16, holds
+// the eight dimensions 32 t + 8 g .. + 7 of centroid c (h = 0: hi, 1: lo),
+// zero beyond d and for the padding centroids L .. Lp - 1 (Lp = L rounded up
+// to a whole pipeline stage, so stage loads need no bounds).
+__global__ void coarse_bf16_pack_kernel(const float* __restrict__ C, int L, int Lp, int d, int DT,
+                                        uint4* __restrict__ Cb) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // (c, t, g)
+    if (e >= (size_t)Lp * DT * 4) return;
+    const int g = (int)(e & 3), t = (int)((e >> 2) % DT);
+    const size_t c = e / ((size_t)DT * 4);
+    uint32_t h[8], l[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int j = 32 * t + 8 * g + i;
+        bf16_split(j < d && c < (size_t)L ? C[c * d + j] : 0.0f, h[i], l[i]);
+    }
+    const size_t hi = (((c >> 4) * 2 * DT + t) * 4 + g) * 16 + (c & 15);
+    Cb[hi] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
+    Cb[hi + (size_t)DT * 64] =
+        make_uint4(l[0] | l[1] << 16, l[2] | l[3] << 16, l[4] | l[5] << 16, l[6] | l[7] << 16);
+}
+
+static int fc_padded_lists(int L) { return (L + FC_ST * 16 - 1) / (FC_ST * 16) * (FC_ST * 16); }
+
+size_t coarse_bf16_pack_chunks(int L, int d) { return (size_t)fc_padded_lists(L) * ((d + 31) / 32) * 8; }
+
+void launch_coarse_bf16_pack(const float* C, int L, int d, uint4* Cb, hipStream_t s) {
+    const int DT = (d + 31) / 32, Lp = fc_padded_lists(L);
+    const size_t n = (size_t)Lp * DT * 4;
+    if (n == 0) return;
+    hipLaunchKernelGGL(coarse_bf16_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, C,
+                       L, Lp, d, DT, Cb);
+}
+
+// Dynamic LDS of the fused kernel, in turn: the normalisation tile
+// [FC_QB][d + 1] floats; two pipeline stages of (hi, lo) centroid chunks; the
+// partner waves' key lists [FC_QBW][4][J][64]; then [FC_QB] norms and bounds.
+__host__ __device__ inline size_t fc_stage_chunks(int DT) { return (size_t)FC_ST * DT * 4 * 16; }
+__host__ __device__ inline size_t fc_main_bytes(int d, int DT, int J) {
+    const size_t tile = (size_t)FC_QB * (d + 1) * 4;
+    const size_t stages = 2 * 2 * fc_stage_chunks(DT) * 16;
+    const size_t merge = (size_t)FC_QBW * 4 * J * 64 * 4;
+    size_t m = tile > stages ? tile : stages;
+    return m > merge ? m : merge;
+}
+__host__ __device__ inline size_t fc_lds_bytes(int d, int DT, int J) {
+    return fc_main_bytes(d, DT, J) + FC_QB * 2 * 4;
+}
+
+// One pass over all centroids.  The wave with role (qb, h) = (wave % FC_QBW,
+// wave / FC_QBW) computes, for tiles h * FC_SUB .. + FC_SUB - 1 of every stage
+// of FC_ST 16-centroid tiles, acc = Q_qb . C_tile^T (16 x 16, bf16x3) and hands
+// it to `epi(acc, col_base)`, col_base the tile's first centroid.  Stages are
+// double-buffered in LDS with one barrier each; all threads call this.
+template <int DT, typename Epi>
+__device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, const u32x4 (&ah)[DT],
+                                        const u32x4 (&al)[DT], u32x4* lds, Epi epi) {
+    const u32x4* __restrict__ Cb = reinterpret_cast<const u32x4*>(Cb_in);
+    constexpr int SC = FC_ST * DT * 4 * 16;  // chunks per stage and half
+    constexpr int PER = 2 * SC / VGPU_BLOCK;  // chunks each thread copies per stage
+    static_assert((2 * SC) % VGPU_BLOCK == 0, "stage split");
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    const int h = __builtin_amdgcn_readfirstlane((tid >> 6) / FC_QBW);
+    const int nst = (L + FC_ST * 16 - 1) / (FC_ST * 16);
+    // A stage is 2 SC contiguous chunks of Cb (padded to whole stages), copied
+    // to LDS unchanged: slot i of thread tid is chunk i * VGPU_BLOCK + tid.
+    u32x4 pre[PER];
+#define FC_FETCH(ST)                                                                   \
+    {                                                                                  \
+        const u32x4* __restrict__ sb = Cb + (size_t)(ST) * 2 * SC;                     \
+        _Pragma("unroll") for (int i = 0; i < PER; i++) pre[i] = sb[i * VGPU_BLOCK + tid]; \
+    }
+#define FC_STORE(BUF)                                                                  \
+    _Pragma("unroll") for (int i = 0; i < PER; i++) lds[(size_t)(BUF) * 2 * SC + i * VGPU_BLOCK + tid] = pre[i];
+    FC_FETCH(0)
+    FC_STORE(0)
+    if (nst > 1) { FC_FETCH(1) }
+    for (int st = 0; st < nst; st++) {
+        // Everyone has finished stage st - 1 (buffer (st + 1) & 1) and stage
+        // st's chunks are visible.
+        __syncthreads();
+        if (st + 1 < nst) {
+            FC_STORE((st + 1) & 1)
+            if (st + 2 < nst) { FC_FETCH(st + 2) }
+        }
+        const u32x4* b = lds + (size_t)(st & 1) * 2 * SC;
+        // FC_SUB independent accumulators, interleaved so consecutive MFMAs
+        // never wait on each other.
+        floatx4 acc[FC_SUB];
+#pragma unroll
+        for (int sub = 0; sub < FC_SUB; sub++) acc[sub] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+            bf16x8 bh[FC_SUB], bl[FC_SUB];
+#pragma unroll
+            for (int sub = 0; sub < FC_SUB; sub++) {
+                const int o = (((h * FC_SUB + sub) * 2 * DT + t) * 4 + g) * 16 + c;
+                bh[sub] = __builtin_bit_cast(bf16x8, b[o]);
+                bl[sub] = __builtin_bit_cast(bf16x8, b[o + DT * 64]);
+            }
+            const bf16x8 a_h = __builtin_bit_cast(bf16x8, ah[t]);
+            const bf16x8 a_l = __builtin_bit_cast(bf16x8, al[t]);
+#pragma unroll
+            for (int sub = 0; sub < FC_SUB; sub++)
+                acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bl[sub], acc[sub], 0, 0, 0);
+#pragma unroll
+            for (int sub = 0; sub < FC_SUB; sub++)
+                acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_l, bh[sub], acc[sub], 0, 0, 0);
+#pragma unroll
+            for (int sub = 0; sub < FC_SUB; sub++)
+                acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bh[sub], acc[sub], 0, 0, 0);
+        }
+#pragma unroll
+        for (int sub = 0; sub < FC_SUB; sub++) epi(acc[sub], (st * FC_ST + h * FC_SUB + sub) * 16);
+    }
+#undef FC_FETCH
+#undef FC_STORE
+}
+
+// bf16 hi/lo A operands of one row, element j = x(j), dimensions
+// 32 t + 8 g .. + 7 for lane group g.
+template <int DT, typename X>
+__device__ __forceinline__ void fc_split_rows(X x, int d, int g, u32x4 (&ah)[DT], u32x4 (&al)[DT]) {
+#pragma unroll
+    for (int t = 0; t < DT; t++) {
+        uint32_t hb[8], lb[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int j = 32 * t + 8 * g + i;
+            bf16_split(j < d ? x(j) : 0.0f, hb[i], lb[i]);
+        }
+        ah[t] = u32x4{hb[0] | hb[1] << 16, hb[2] | hb[3] << 16, hb[4] | hb[5] << 16, hb[6] | hb[7] << 16};
+        al[t] = u32x4{lb[0] | lb[1] << 16, lb[2] | lb[3] << 16, lb[4] | lb[5] << 16, lb[6] | lb[7] << 16};
+    }
+}
+
+// Rank k (0-based, ascending) among the 16 J keys held by the 16 lanes of
+// this lane's 16-lane group, J per lane (bitonic sort over element
+// e * 16 + lane % 16; strides below 16 stay inside the group).
+template <int J>
+__device__ __forceinline__ uint32_t group16_rank(uint32_t (&v)[J], int k) {
+    const int l16 = threadIdx.x & 15;
+#pragma unroll
+    for (int size = 2; size <= 16 * J; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride >= 16) {
+                const int es = stride >> 4;
+#pragma unroll
+                for (int e = 0; e < J; e++) {
+                    const int f = e ^ es;
+                    if (f > e) {
+                        const bool asc = (((e << 4) | l16) & size) == 0;
+                        const uint32_t a = v[e], b = v[f];
+                        const bool sw = (a > b) == asc;
+                        v[e] = sw ? b : a;
+                        v[f] = sw ? a : b;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < J; e++) {
+                    const uint32_t o = __shfl_xor(v[e], stride, 64);
+                    const bool asc = (((e << 4) | l16) & size) == 0;
+                    const bool lower = (l16 & stride) == 0;
+                    v[e] = (lower == asc) ? (o < v[e] ? o : v[e]) : (o > v[e] ? o : v[e]);
+                }
+            }
+        }
+    }
+    uint32_t x = v[0];
+#pragma unroll
+    for (int e = 1; e < J; e++) x = (k >> 4) == e ? v[e] : x;
+    return __shfl(x, (threadIdx.x & 48) | (k & 15), 64);
+}
+
+// Insert v into the descending list t[0] >= .. >= t[J-1] (the J largest of
+// the list and v): t_i' = med3(t_{i-1}, t_i, v), updated from the bottom so
+// each step reads the old t_{i-1}; t_0' = max(t_0, v) as med3 against a
+// finite bound above every key.
+template <int J>
+__device__ __forceinline__ void top_insert(float (&t)[J], float v) {
+#pragma unroll
+    for (int i = J - 1; i > 0; i--) t[i] = __builtin_amdgcn_fmed3f(t[i - 1], t[i], v);
+    t[0] = __builtin_amdgcn_fmed3f(t[0], v, 3.0e38f);
+}
+
+// One pass of bf16x3 products.  Every (lane, row) keeps the J largest keys
+// k = (a + 2) with its low IB mantissa bits replaced by the tile index
+// (a = approximate q.c; the lane's column c = lane % 16 completes the list
+// index 16 tile + c).  The partner wave's lists merge in; T = the Pe-th largest
+// of the row's 16 J keys bounds the Pe-th largest approximate dot from below
+// (Pe distinct lists have keys >= T, so approximate dots >= T - 2 - E, E the
+// packing error).  Pe lists then have exact scores within eps of those, so
+// every list among the Pe exact nearest has an approximate dot within 2 eps
+// of T - 2 - E and a key >= T - 2E - 2 eps (taken with a factor 1.25 and a few
+// ulps to spare); those keys form a prefix of each lane's list.  A lane whose J-th key is
+// itself above that threshold may have dropped such a list: the row is then
+// marked overflowed (cand_n = CAP + 1).
+template <int DT, int J>
+__global__ __launch_bounds__(256) void coarse_fused_kernel(
+    const float* __restrict__ Q, int nq, int d, const uint4* __restrict__ Cb, int L, float cmax,
+    int Pe, int IB, int normalize, float* __restrict__ qn_out, float* __restrict__ qnorm_out,
+    uint32_t* __restrict__ cand, uint32_t* __restrict__ cand_n) {
+    extern __shared__ __align__(16) char smem[];
+    constexpr int CAP = 16 * J;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
+    const int qb = wave % FC_QBW, h = wave / FC_QBW;
+    const int q0 = blockIdx.x * FC_QB;
+    const int rows = min(FC_QB, nq - q0);
+    float* tile = reinterpret_cast<float*>(smem);
+    float* snorm = reinterpret_cast<float*>(smem + fc_main_bytes(d, DT, J));  // [FC_QB] norm, [FC_QB] bound
+    const int st = d + 1;
+
+    // ---- normalise (search.rs:55-62): sequential sum of squares per row.
+    const float* src = Q + (size_t)q0 * d;
+    for (int e = tid; e < FC_QB * d; e += VGPU_BLOCK) {
+        const int r = e / d;
+        tile[r * st + e % d] = r < rows ? src[e] : 0.0f;
+    }
+    __syncthreads();
+    if (tid < FC_QB) {
+        const float* xr = tile + tid * st;
+        float s = 0.0f;
+        for (int j = 0; j < d; j++) s = __fadd_rn(s, __fmul_rn(xr[j], xr[j]));
+        const float nrm = sqrtf(s);
+        // without normalisation the rows are used as given; the bound is ||x||
+        snorm[tid] = normalize ? nrm : 0.0f;
+        snorm[FC_QB + tid] = normalize && nrm > 1e-10f ? 1.0001f : nrm * 1.0001f + 1e-30f;
+        if (tid < rows && qnorm_out) qnorm_out[q0 + tid] = snorm[FC_QB + tid];
+    }
+    __syncthreads();
+    if (normalize) {
+        for (int e = tid; e < FC_QB * d; e += VGPU_BLOCK) {
+            const int r = e / d, j = e % d;
+            const float nrm = snorm[r];
+            const float v = tile[r * st + j];
+            const float x = nrm > 1e-10f ? v / nrm : v;
+            tile[r * st + j] = x;
+            if (r < rows) qn_out[(size_t)(q0 + r) * d + j] = x;
+        }
+        __syncthreads();
+    }
+    u32x4 ah[DT], al[DT];
+    {
+        const float* xr = tile + (qb * 16 + c) * st;
+        fc_split_rows<DT>([&](int j) { return xr[j]; }, d, g, ah, al);
+    }
+    __syncthreads();  // the tile region becomes the pipeline buffers
+
+    // ---- the pass: J largest packed keys per (lane, row 4 g + r).
+    const uint32_t kmask = ~((1u << IB) - 1u);
+    float top[4][J];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int j = 0; j < J; j++) top[r][j] = -3.0e38f;  // below every key
+    fc_pass<DT>(Cb, L, ah, al, reinterpret_cast<u32x4*>(smem), [&](const floatx4& acc, int cb) {
+        const uint32_t ti = (uint32_t)cb >> 4;
+        if (cb + 16 <= L) {  // whole tile (uniform branch)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                top_insert<J>(top[r], __uint_as_float((__float_as_uint(acc[r] + 2.0f) & kmask) | ti));
+        } else {
+            const bool valid = cb + c < L;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float k = __uint_as_float((__float_as_uint(acc[r] + 2.0f) & kmask) | ti);
+                top_insert<J>(top[r], valid ? k : -3.0e38f);
+            }
+        }
+    });
+
+    // ---- merge the partner wave's lists (same rows and column class).
+    __syncthreads();  // the pipeline buffers become the merge area
+    float* mg = reinterpret_cast<float*>(smem) + (size_t)qb * 4 * J * 64;
+    if (h == 1) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int j = 0; j < J; j++) mg[(r * J + j) * 64 + lane] = top[r][j];
+    }
+    __syncthreads();
+    if (h == 1) return;  // no barriers below
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int j = 0; j < J; j++) top_insert<J>(top[r], mg[(r * J + j) * 64 + lane]);
+
+    // ---- per row: threshold, overflow test and candidate output.
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int row = qb * 16 + 4 * g + r;
+        uint32_t kv[J];
+#pragma unroll
+        for (int j = 0; j < J; j++) kv[j] = fkey(top[r][j]);
+        const float T = fkey_to_float(group16_rank<J>(kv, CAP - Pe));
+        const float qb_norm = snorm[FC_QB + row];
+        const float qc = qb_norm * cmax;
+        const float u = 5.9604645e-08f;
+        // packing: < 2^IB ulps of a + 2 plus half an ulp of its rounding; every
+        // |a + 2| <= qc + 2 < ub (a power of two) has ulp <= ub u
+        const float ub = __uint_as_float((__float_as_uint(qc + 2.0f) & 0x7f800000u) + 0x00800000u);
+        const float E = ((float)(1u << IB) + 0.5f) * ub * u;
+        const float kthr = T - (2.0f * E + 2.5f * coarse_eps_bf16(d, qb_norm, cmax) + 8.0f * ub * u);
+        uint32_t n = 0;
+#pragma unroll
+        for (int j = 0; j < J; j++) n += top[r][j] >= kthr ? 1u : 0u;
+        const bool over = top[r][J - 1] >= kthr;
+        // exclusive prefix of n over the 16 lanes of the group
+        uint32_t incl = n;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            const uint32_t x = __shfl_up(incl, o, 16);
+            if (c >= o) incl += x;
+        }
+        const uint32_t total = __shfl(incl, (lane & 48) | 15, 64);
+        const bool any_over = __ballot(over) >> (16 * g) & 0xffffull;
+        if (row < rows) {
+            uint32_t* out = cand + (size_t)(q0 + row) * CAP;
+            const uint32_t base = incl - n;
+#pragma unroll
+            for (int j = 0; j < J; j++)
+                if ((uint32_t)j < n && !any_over)
+                    out[base + j] = 16u * (__float_as_uint(top[r][j]) & ~kmask) + (uint32_t)c;
+            if (c == 0) cand_n[q0 + row] = any_over ? (uint32_t)CAP + 1u : total;
+        }
+    }
+}
+
+int coarse_fused_cap(int P) { return P <= 32 ? 128 : 256; }
+
+bool coarse_fused_supported(int d, int P) { return d >= 1 && d <= 128 && P >= 1 && P <= 64; }
+
+template <int DT, int J>
+static void launch_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int Pe,
+                         int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
+                         hipStream_t s) {
+    const size_t lds = fc_lds_bytes(d, DT, J);
+    // index bits: tiles ceil(L / 16) <= 2^IB
+    int IB = 0;
+    while ((1 << IB) < (L + 15) / 16) IB++;
+    auto k = coarse_fused_kernel<DT, J>;
+    ensure_dyn_lds((const void*)k, lds);
+    hipLaunchKernelGGL(k, dim3((nq + FC_QB - 1) / FC_QB), dim3(VGPU_BLOCK), lds, s, Q, nq, d, Cb, L, cmax,
+                       Pe, IB, normalize, qn, qnorm, cand, cand_n);
+}
+
+template <int DT>
+static void launch_fused_j(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int Pe,
+                           int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
+                           hipStream_t s) {
+    if (coarse_fused_cap(Pe) == 128)
+        launch_fused<DT, 8>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s);
+    else
+        launch_fused<DT, 16>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s);
+}
+
+void launch_coarse_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int P,
+                         int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
+                         hipStream_t s) {
+    if (nq <= 0) return;
+    const int Pe = P < L ? P : L;
+    switch ((d + 31) / 32) {
+        case 1: launch_fused_j<1>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s); break;
+        case 2: launch_fused_j<2>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s); break;
+        case 3: launch_fused_j<3>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s); break;
+        default: launch_fused_j<4>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s); break;
+    }
+}
+
+// ---- exact ordering of the candidates, one wave per query ---------------
+#define TP_QD 512
+
+__global__ __launch_bounds__(256) void coarse_topp_kernel(
+    const uint32_t* __restrict__ cand, const uint32_t* __restrict__ cand_n, int CAP,
+    const float* __restrict__ qn, const float* __restrict__ C, int nq, int L, int d, int P,
+    uint32_t* __restrict__ probe, uint32_t* __restrict__ flag_list, uint32_t* flag_count) {
+    __shared__ float wq[4][TP_QD];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = blockIdx.x * 4 + wave;
+    if (q >= nq) return;  // per wave: no block barriers below
+    const int Pe = P < L ? P : L;
+    const uint32_t n = cand_n[q];
+    if (n > (uint32_t)CAP) {
+        if (lane == 0) flag_list[atomicAdd(flag_count, 1u)] = (uint32_t)q;
+        return;
+    }
+    float* qs = wq[wave];
+    for (int j = lane; j < d; j += 64) qs[j] = qn[(size_t)q * d + j];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    uint64_t k4[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t t = e * 64 + lane;
+        k4[e] = ~0ull;
+        if (t < n) {
+            const uint32_t cidx = cand[(size_t)q * CAP + t];
+            k4[e] = cand_key(1.0f - seq_dot_stream(qs, C + (size_t)cidx * d, d), cidx);
+        }
+    }
+    if (n <= 64) {
+        uint64_t k1[1] = {k4[0]};
+        wave_sort_regs<1>(k1);
+        if (lane < Pe) probe[(size_t)q * P + lane] = (uint32_t)k1[0];
+    } else if (n <= 128) {
+        uint64_t k2[2] = {k4[0], k4[1]};
+        wave_sort_regs<2>(k2);
+#pragma unroll
+        for (int e = 0; e < 2; e++)
+            if (e * 64 + lane < Pe) probe[(size_t)q * P + e * 64 + lane] = (uint32_t)k2[e];
+    } else {
+        wave_sort_regs<4>(k4);
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (e * 64 + lane < Pe) probe[(size_t)q * P + e * 64 + lane] = (uint32_t)k4[e];
+    }
+}
+
+void launch_coarse_topp(const uint32_t* cand, const uint32_t* cand_n, int P, const float* qn,
+                        const float* C, int nq, int L, int d, uint32_t* probe, uint32_t* flag_list,
+                        uint32_t* flag_count, hipStream_t s) {
+    if (nq <= 0) return;
+    const int Pe = P < L ? P : L;
+    hipLaunchKernelGGL(coarse_topp_kernel, dim3((nq + 3) / 4), dim3(VGPU_BLOCK), 0, s, cand, cand_n,
+                       coarse_fused_cap(Pe), qn, C, nq, L, d, P, probe, flag_list, flag_count);
+}
+
+// ---- test entry: the bf16x3 dot products of the fused kernel ------------
+// D[q][c] = Q[q] . C[c] through fc_pass (Q already normalised or not).
+template <int DT>
+__global__ __launch_bounds__(256) void coarse_bf16x3_dots_kernel(const float* __restrict__ Q, int nq,
+                                                                 int d, const uint4* __restrict__ Cb,
+                                                                 int L, float* __restrict__ D) {
+    extern __shared__ __align__(16) char smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
+    const int qb = wave % FC_QBW;
+    const int q0 = blockIdx.x * FC_QB;
+    const int row_a = q0 + qb * 16 + c;
+    u32x4 ah[DT], al[DT];
+    fc_split_rows<DT>([&](int j) { return row_a < nq ? Q[(size_t)row_a * d + j] : 0.0f; }, d, g, ah, al);
+    fc_pass<DT>(Cb, L, ah, al, reinterpret_cast<u32x4*>(smem), [&](const floatx4& acc, int cb) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = q0 + qb * 16 + 4 * g + r, col = cb + c;
+            if (row < nq && col < L) D[(size_t)row * L + col] = acc[r];
+        }
+    });
+}
+
+void launch_coarse_bf16x3_dots(const float* Q, int nq, int d, const uint4* Cb, int L, float* D,
+                               hipStream_t s) {
+    if (nq <= 0 || L <= 0) return;
+    const int DT = (d + 31) / 32;
+    const size_t lds = 2 * 2 * fc_stage_chunks(DT) * 16;
+    const dim3 grid((nq + FC_QB - 1) / FC_QB);
+    switch (DT) {
+        case 1:
+            ensure_dyn_lds((const void*)coarse_bf16x3_dots_kernel<1>, lds);
+            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<1>, grid, dim3(256), lds, s, Q, nq, d, Cb, L, D);
+            break;
+        case 2:
+            ensure_dyn_lds((const void*)coarse_bf16x3_dots_kernel<2>, lds);
+            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<2>, grid, dim3(256), lds, s, Q, nq, d, Cb, L, D);
+            break;
+        case 3:
+            ensure_dyn_lds((const void*)coarse_bf16x3_dots_kernel<3>, lds);
+            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<3>, grid, dim3(256), lds, s, Q, nq, d, Cb, L, D);
+            break;
+        default:
+            ensure_dyn_lds((const void*)coarse_bf16x3_dots_kernel<4>, lds);
+            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<4>, grid, dim3(256), lds, s, Q, nq, d, Cb, L, D);
+            break;
+    }
+}
+
+}  // namespace vgpu

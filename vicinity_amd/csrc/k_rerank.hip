@@ -124,7 +124,10 @@ __global__ __launch_bounds__(256) void finish_kernel(
     }
     if (blockIdx.x == 0 && tid == 0) {
         if (flag_count) *flag_count = 0u;
-        if (cflag_count) *cflag_count = 0u;
+        if (cflag_count) {
+            counters[NUM_SCAN_COUNTERS * COUNTER_STRIDE] += *cflag_count;  // exact coarse fallbacks
+            *cflag_count = 0u;
+        }
     }
 }
 

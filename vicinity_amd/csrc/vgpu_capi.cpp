@@ -428,4 +428,19 @@ int vgpu_test_coarse_dots(const float* q, size_t nq, const float* c, size_t L, s
     });
 }
 
+int vgpu_test_coarse_dots_bf16x3(const float* q, size_t nq, const float* c, size_t L, size_t d,
+                                 float* out) {
+    return guard([&] {
+        need(q && c && out && d && L, VGPU_ERR_INVALID_PARAMETER, "bad argument");
+        need(d <= 128, VGPU_ERR_INVALID_PARAMETER, "the bf16x3 coarse kernel takes d <= 128");
+        Tmp<float> qv(q, nq * d), cv(c, L * d), o(nq * L ? nq * L : 1);
+        vgpu::DevBuf<uint4> cb;
+        cb.reserve(vgpu::coarse_bf16_pack_chunks((int)L, (int)d));
+        vgpu::launch_coarse_bf16_pack(cv.p, (int)L, (int)d, cb.p, nullptr);
+        vgpu::launch_coarse_bf16x3_dots(qv.p, (int)nq, (int)d, cb.p, (int)L, o.p, nullptr);
+        VGPU_HIP(hipGetLastError());
+        VGPU_HIP(hipMemcpy(out, o.p, nq * L * sizeof(float), hipMemcpyDeviceToHost));
+    });
+}
+
 }  // extern "C"

@@ -67,6 +67,30 @@ __device__ __forceinline__ float seq_dot_stream(const float* a, const float* __r
     return s;
 }
 
+// a . b in any order: fused multiply-adds into four partial sums, for ranking
+// only.  Within (d / 4 + 2) u sum|a_j b_j| of the real product (u = 2^-24).
+// b is 16-byte aligned when d % 4 == 0.
+__device__ __forceinline__ float approx_dot(const float* a, const float* __restrict__ b, int d) {
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    int j = 0;
+    if ((d & 3) == 0) {
+        for (; j + 16 <= d; j += 16) {
+            float4 v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = reinterpret_cast<const float4*>(b + j)[i];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                s0 = fmaf(a[j + 4 * i], v[i].x, s0);
+                s1 = fmaf(a[j + 4 * i + 1], v[i].y, s1);
+                s2 = fmaf(a[j + 4 * i + 2], v[i].z, s2);
+                s3 = fmaf(a[j + 4 * i + 3], v[i].w, s3);
+            }
+        }
+    }
+    for (; j < d; j++) s0 = fmaf(a[j], b[j], s0);
+    return (s0 + s1) + (s2 + s3);
+}
+
 // Ascending bitonic sort of keys[0..n) (n a power of two) with a payload array.
 // All threads of the block must call it.
 template <typename P>

@@ -117,11 +117,37 @@ void IvfpqIndex::add(const uint32_t* ids, const float* x, size_t count) {
 }
 
 // argmin over centroids of 1 - dot(x, c), lowest index on ties: the coarse
-// GEMM + margin rescoring kernels with nprobe = 1, chunked to bound the score
-// matrix at 1 GiB.
+// kernels with nprobe = 1 on the rows as given (they are already normalised).
+// The fused kernel needs no score matrix; the GEMM fallback (d > 128) is
+// chunked to bound the score matrix at 1 GiB.
 void IvfpqIndex::assign_cosine(const float* d_x, const float* d_norms, size_t nx,
                                const float* d_cent, size_t k, float cmax, uint32_t* d_assign,
                                hipStream_t s) {
+    if (coarse_fused_supported((int)d, 1)) {
+        const size_t chunk = std::min<size_t>(nx, (size_t)1 << 18);
+        const int cap = coarse_fused_cap(1);
+        w_cb16.reserve(coarse_bf16_pack_chunks((int)k, (int)d));
+        w_cand.reserve(chunk * cap);
+        w_cand_n.reserve(chunk);
+        w_cflag_list.reserve(chunk);
+        w_cflag_count.reserve(1);
+        w_overflow.reserve(1);
+        VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
+        launch_coarse_bf16_pack(d_cent, (int)k, (int)d, w_cb16.p, s);
+        for (size_t q0 = 0; q0 < nx; q0 += chunk) {
+            const size_t nc = std::min(chunk, nx - q0);
+            VGPU_HIP(hipMemsetAsync(w_cflag_count.p, 0, sizeof(uint32_t), s));
+            launch_coarse_fused(d_x + q0 * d, (int)nc, (int)d, w_cb16.p, (int)k, cmax, 1, 0, nullptr,
+                                nullptr, w_cand.p, w_cand_n.p, s);
+            launch_coarse_topp(w_cand.p, w_cand_n.p, 1, d_x + q0 * d, d_cent, (int)nc, (int)k, (int)d,
+                               d_assign + q0, w_cflag_list.p, w_cflag_count.p, s);
+            launch_coarse_exact_flagged(d_x + q0 * d, d_norms + q0, d_cent, (int)nc, (int)k, (int)d, 1,
+                                        cmax, d_assign + q0, w_overflow.p, w_cflag_list.p,
+                                        w_cflag_count.p, s);
+        }
+        VGPU_HIP(hipGetLastError());
+        return;
+    }
     size_t chunk = std::max<size_t>(1, std::min<size_t>(nx, ((size_t)1 << 28) / std::max<size_t>(k, 1)));
     chunk = std::min<size_t>(chunk, (size_t)1 << 20);  // grid.y of the GEMM stays < 65536
     w_dots.reserve(chunk * k);
@@ -414,6 +440,9 @@ void IvfpqIndex::upload_index() {
     dix.ds = (int)ds;
     dix.n = (uint32_t)n;
     dix.centroids = d_centroids.p;
+    d_cb16.reserve(coarse_bf16_pack_chunks((int)L, (int)d));
+    launch_coarse_bf16_pack(d_centroids.p, (int)L, (int)d, d_cb16.p, stream);
+    dix.cb16 = d_cb16.p;
     dix.codebooks = d_codebooks.p;
     dix.offsets = d_offsets.p;
     dix.list_ids = d_list_ids.p;
@@ -444,7 +473,7 @@ void IvfpqIndex::upload_index() {
 }
 
 // Word offsets in the per-call scalar buffer (64-byte lines apart).
-static constexpr size_t kOverflowWord = NUM_SCAN_COUNTERS * COUNTER_STRIDE;
+static constexpr size_t kOverflowWord = (NUM_SCAN_COUNTERS + 1) * COUNTER_STRIDE;
 static constexpr size_t kFlagWord = kOverflowWord + 8;
 static constexpr size_t kCFlagWord = kFlagWord + 8;
 static constexpr size_t kScalWords = kCFlagWord + 8;
@@ -491,9 +520,14 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
     chunk = std::min<size_t>(chunk, 65536);
     w_qn.reserve(chunk * d);
     w_qnorm.reserve(chunk);
-    w_dots.reserve(chunk * L);
+    const bool fused = coarse_fused_supported((int)d, (int)P);
+    if (fused) {
+        w_cand.reserve(chunk * coarse_fused_cap((int)P));
+        w_cand_n.reserve(chunk);
+    } else {
+        w_dots.reserve(chunk * L);
+    }
     w_cflag_list.reserve(chunk);
-    w_cflag_count.reserve(1);
     w_probe.reserve(chunk * P);
     w_vidx.reserve(chunk * kout);
     w_dist.reserve(chunk * kout);
@@ -515,12 +549,25 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
     for (size_t q0 = 0; q0 < nq; q0 += chunk) {
         const size_t nc = std::min(chunk, nq - q0);
         if (profiling) VGPU_HIP(hipEventRecord(ev[0], s));
-        launch_normalize(d_q + q0 * d, w_qn.p, w_qnorm.p, (int)nc, (int)d, s);
-        if (profiling) VGPU_HIP(hipEventRecord(ev[1], s));
-        launch_coarse_dots(w_qn.p, d_centroids.p, w_dots.p, (int)nc, (int)L, (int)d, s);
-        if (profiling) VGPU_HIP(hipEventRecord(ev[2], s));
-        launch_coarse_select(w_dots.p, w_qn.p, w_qnorm.p, d_centroids.p, (int)nc, (int)L, (int)d,
-                             (int)P, dix.cmax, w_probe.p, overflow, w_cflag_list.p, cflag_count, s);
+        if (fused) {
+            // normalise + two bf16x3 MFMA passes (ms_coarse), exact top-P of the
+            // candidates and the rare exact fallback (ms_select)
+            if (profiling) VGPU_HIP(hipEventRecord(ev[1], s));
+            launch_coarse_fused(d_q + q0 * d, (int)nc, (int)d, dix.cb16, (int)L, dix.cmax, (int)P, 1,
+                                w_qn.p, w_qnorm.p, w_cand.p, w_cand_n.p, s);
+            if (profiling) VGPU_HIP(hipEventRecord(ev[2], s));
+            launch_coarse_topp(w_cand.p, w_cand_n.p, (int)P, w_qn.p, d_centroids.p, (int)nc, (int)L, (int)d,
+                               w_probe.p, w_cflag_list.p, cflag_count, s);
+            launch_coarse_exact_flagged(w_qn.p, w_qnorm.p, d_centroids.p, (int)nc, (int)L, (int)d, (int)P,
+                                        dix.cmax, w_probe.p, overflow, w_cflag_list.p, cflag_count, s);
+        } else {
+            launch_normalize(d_q + q0 * d, w_qn.p, w_qnorm.p, (int)nc, (int)d, s);
+            if (profiling) VGPU_HIP(hipEventRecord(ev[1], s));
+            launch_coarse_dots(w_qn.p, d_centroids.p, w_dots.p, (int)nc, (int)L, (int)d, s);
+            if (profiling) VGPU_HIP(hipEventRecord(ev[2], s));
+            launch_coarse_select(w_dots.p, w_qn.p, w_qnorm.p, d_centroids.p, (int)nc, (int)L, (int)d,
+                                 (int)P, dix.cmax, w_probe.p, overflow, w_cflag_list.p, cflag_count, s);
+        }
         if (profiling) VGPU_HIP(hipEventRecord(ev[3], s));
         ScanArgs a;
         a.qn = w_qn.p;
@@ -582,7 +629,8 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
     VGPU_HIP(hipStreamSynchronize(s));
     unsigned long long cnt[NUM_SCAN_COUNTERS];
     for (int i = 0; i < NUM_SCAN_COUNTERS; i++) cnt[i] = h_scal[i * COUNTER_STRIDE];
-    const unsigned int ovf = reinterpret_cast<const unsigned int*>(h_scal + kOverflowWord)[0];
+    const unsigned int ovf = reinterpret_cast<const unsigned int*>(h_scal + kOverflowWord)[0] +
+                             (unsigned int)h_scal[NUM_SCAN_COUNTERS * COUNTER_STRIDE];
     stats.ms_normalize = t[0];
     stats.ms_coarse = t[1];
     stats.ms_select = t[2];
@@ -629,9 +677,30 @@ void IvfpqIndex::probe_host(const float* q, size_t nq, size_t nprobe, uint32_t* 
     w_overflow.reserve(1);
     VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), stream));
     size_t chunk = std::max<size_t>(1, std::min<size_t>(nq, ((size_t)1 << 28) / L));
-    w_dots.reserve(chunk * L);
     w_cflag_list.reserve(chunk);
     w_cflag_count.reserve(1);
+    if (coarse_fused_supported((int)d, (int)P)) {
+        chunk = std::min<size_t>(nq, (size_t)1 << 20);
+        w_cflag_list.reserve(chunk);
+        w_cand.reserve(chunk * coarse_fused_cap((int)P));
+        w_cand_n.reserve(chunk);
+        for (size_t q0 = 0; q0 < nq; q0 += chunk) {
+            const size_t nc = std::min(chunk, nq - q0);
+            VGPU_HIP(hipMemsetAsync(w_cflag_count.p, 0, sizeof(uint32_t), stream));
+            launch_coarse_fused(w_q.p + q0 * d, (int)nc, (int)d, dix.cb16, (int)L, dix.cmax, (int)P, 1,
+                                w_qn.p + q0 * d, w_qnorm.p + q0, w_cand.p, w_cand_n.p, stream);
+            launch_coarse_topp(w_cand.p, w_cand_n.p, (int)P, w_qn.p + q0 * d, d_centroids.p, (int)nc, (int)L,
+                               (int)d, w_probe.p + q0 * P, w_cflag_list.p, w_cflag_count.p, stream);
+            launch_coarse_exact_flagged(w_qn.p + q0 * d, w_qnorm.p + q0, d_centroids.p, (int)nc, (int)L,
+                                        (int)d, (int)P, dix.cmax, w_probe.p + q0 * P, w_overflow.p,
+                                        w_cflag_list.p, w_cflag_count.p, stream);
+        }
+        VGPU_HIP(hipGetLastError());
+        VGPU_HIP(hipMemcpyAsync(lists, w_probe.p, nq * P * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+        VGPU_HIP(hipStreamSynchronize(stream));
+        return;
+    }
+    w_dots.reserve(chunk * L);
     launch_normalize(w_q.p, w_qn.p, w_qnorm.p, (int)nq, (int)d, stream);
     for (size_t q0 = 0; q0 < nq; q0 += chunk) {
         size_t nc = std::min(chunk, nq - q0);

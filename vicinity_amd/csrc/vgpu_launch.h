@@ -16,6 +16,7 @@ struct DevIndex {
     int d = 0, L = 0, M = 0, K = 0, ds = 0;
     uint32_t n = 0;
     const float* centroids = nullptr;  // [L*d] row-major
+    const uint4* cb16 = nullptr;       // bf16 hi/lo centroid chunks (launch_coarse_bf16_pack)
     const float* codebooks = nullptr;  // [M*K*ds] codebook, codeword, dim
     const uint32_t* offsets = nullptr; // [L+1] list l = positions [off[l], off[l+1])
     const uint32_t* list_ids = nullptr;// [n] insertion index at each position
@@ -62,6 +63,32 @@ void launch_coarse_select(float* D, const float* qn, const float* qnorm, const f
                           unsigned int* overflow, uint32_t* flag_list, uint32_t* flag_count,
                           hipStream_t s);
 
+// ---- fused coarse quantiser (k_coarse_fused.hip): d <= 128, 1 <= P <= 64.
+bool coarse_fused_supported(int d, int P);
+int coarse_fused_cap(int P);  // candidate row length for P probes
+// bf16 hi/lo copy of the centroids: L * ceil(d/32) * 8 uint4.
+// uint4 chunks of the packed centroids (L padded to whole pipeline stages).
+size_t coarse_bf16_pack_chunks(int L, int d);
+void launch_coarse_bf16_pack(const float* C, int L, int d, uint4* Cb, hipStream_t s);
+// Normalise the raw queries Q (or use them as given, normalize = 0) into qn /
+// qnorm, and write each query's candidate lists: cand[q][coarse_fused_cap(P)],
+// cand_n[q] (a count above the cap means overflow).
+void launch_coarse_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int P,
+                         int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
+                         hipStream_t s);
+// probe[q][0..P) from the candidates by exact score; overflowed queries are
+// appended to flag_list (*flag_count must be 0 on entry).
+void launch_coarse_topp(const uint32_t* cand, const uint32_t* cand_n, int P, const float* qn,
+                        const float* C, int nq, int L, int d, uint32_t* probe, uint32_t* flag_list,
+                        uint32_t* flag_count, hipStream_t s);
+// Exact probe selection for the flagged queries (dot products in LDS).
+void launch_coarse_exact_flagged(const float* qn, const float* qnorm, const float* C, int nq, int L,
+                                 int d, int P, float cmax, uint32_t* probe, unsigned int* overflow,
+                                 const uint32_t* flag_list, const uint32_t* flag_count, hipStream_t s);
+// Test entry: D[q][c] = Q[q] . C[c] with the fused kernel's bf16x3 MFMA.
+void launch_coarse_bf16x3_dots(const float* Q, int nq, int d, const uint4* Cb, int L, float* D,
+                               hipStream_t s);
+
 size_t scan8_lds_bytes(const DevIndex& ix, const ScanArgs& a);
 void launch_scan8_exact(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 // FAST mode: per-query decomposed table, threshold buffer, exact rescoring of
@@ -73,7 +100,8 @@ void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 #define QSTAT_WORDS 4
 // Search statistics: entries scanned, fallbacks, flushes, appends, fallbacks
 // from ties, second passes; counter i lives at counters[i * COUNTER_STRIDE]
-// (separate cache lines for the per-workgroup atomics).
+// (separate cache lines for the per-workgroup atomics); the counter after them
+// (index NUM_SCAN_COUNTERS) counts queries sent to the exact coarse fallback.
 #define NUM_SCAN_COUNTERS 6
 #define COUNTER_STRIDE 8
 // Chunk epilogue: doc-id mapping and padding of (vidx, dist)[nq][kin] into

@@ -81,6 +81,8 @@ struct IvfpqIndex {
     hipStream_t stream = nullptr;
     hipEvent_t ev[8] = {};
     DevBuf<float> d_centroids, d_codebooks, d_bias, d_vectors;
+    DevBuf<uint4> d_cb16, w_cb16;  // bf16 hi/lo centroid copies (search index, build workspace)
+    DevBuf<uint32_t> w_cand, w_cand_n;  // fused coarse candidates
     DevBuf<uint32_t> d_offsets, d_list_ids, d_doc_ids, d_pack_off;
     DevBuf<uint8_t> d_codes, d_packed;
     DevIndex dix;
