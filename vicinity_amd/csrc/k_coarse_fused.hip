@@ -100,12 +100,12 @@ void launch_coarse_bf16_pack(const float* C, int L, int d, uint4* Cb, hipStream_
 
 // Dynamic LDS of the fused kernel, in turn: the normalisation tile
 // [FC_QB][d + 1] floats; two pipeline stages of (hi, lo) centroid chunks; the
-// partner waves' key lists [FC_QBW][4][J][64]; then [FC_QB] norms and bounds.
+// waves' key lists [FC_QBW][FC_NH][4][J][64]; then [FC_QB] norms and bounds.
 __host__ __device__ inline size_t fc_stage_chunks(int DT) { return (size_t)FC_ST * DT * 4 * 16; }
 __host__ __device__ inline size_t fc_main_bytes(int d, int DT, int J) {
     const size_t tile = (size_t)FC_QB * (d + 1) * 4;
     const size_t stages = 2 * 2 * fc_stage_chunks(DT) * 16;
-    const size_t merge = (size_t)FC_QBW * 4 * J * 64 * 4;
+    const size_t merge = (size_t)FC_QBW * FC_NH * 4 * J * 64 * 4;
     size_t m = tile > stages ? tile : stages;
     return m > merge ? m : merge;
 }
@@ -116,8 +116,10 @@ __host__ __device__ inline size_t fc_lds_bytes(int d, int DT, int J) {
 // One pass over all centroids.  The wave with role (qb, h) = (wave % FC_QBW,
 // wave / FC_QBW) computes, for tiles h * FC_SUB .. + FC_SUB - 1 of every stage
 // of FC_ST 16-centroid tiles, acc = Q_qb . C_tile^T (16 x 16, bf16x3) and hands
-// it to `epi(acc, col_base)`, col_base the tile's first centroid.  Stages are
-// double-buffered in LDS with one barrier each; all threads call this.
+// it to `epi(acc, col_base, masked)`, col_base the tile's first centroid and
+// masked = the tile may reach past L (only in the last stage).  Stages are
+// double-buffered in LDS with one barrier each; a stage's epilogue runs after
+// the next stage's MFMAs are issued, so the two overlap.  All threads call this.
 template <int DT, typename Epi>
 __device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, const u32x4 (&ah)[DT],
                                         const u32x4 (&al)[DT], u32x4* lds, Epi epi) {
@@ -141,6 +143,7 @@ __device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, 
     FC_FETCH(0)
     FC_STORE(0)
     if (nst > 1) { FC_FETCH(1) }
+    floatx4 prev[FC_SUB];
     for (int st = 0; st < nst; st++) {
         // Everyone has finished stage st - 1 (buffer (st + 1) & 1) and stage
         // st's chunks are visible.
@@ -176,9 +179,16 @@ __device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, 
             for (int sub = 0; sub < FC_SUB; sub++)
                 acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bh[sub], acc[sub], 0, 0, 0);
         }
+        if (st > 0) {  // stage st - 1 < nst - 1 is whole
 #pragma unroll
-        for (int sub = 0; sub < FC_SUB; sub++) epi(acc[sub], (st * FC_ST + h * FC_SUB + sub) * 16);
+            for (int sub = 0; sub < FC_SUB; sub++) epi(prev[sub], ((st - 1) * FC_ST + h * FC_SUB + sub) * 16, false);
+        }
+#pragma unroll
+        for (int sub = 0; sub < FC_SUB; sub++) prev[sub] = acc[sub];
     }
+    const bool masked = nst * FC_ST * 16 > L;
+#pragma unroll
+    for (int sub = 0; sub < FC_SUB; sub++) epi(prev[sub], ((nst - 1) * FC_ST + h * FC_SUB + sub) * 16, masked);
 #undef FC_FETCH
 #undef FC_STORE
 }
@@ -251,27 +261,31 @@ __device__ __forceinline__ void top_insert(float (&t)[J], float v) {
     t[0] = __builtin_amdgcn_fmed3f(t[0], v, 3.0e38f);
 }
 
-// One pass of bf16x3 products.  Every (lane, row) keeps the J largest keys
-// k = (a + 2) with its low IB mantissa bits replaced by the tile index
+// One pass of bf16x3 products.  Every (wave, lane, row) keeps the J largest
+// keys k = (a + 2) with its low IB mantissa bits replaced by the tile index
 // (a = approximate q.c; the lane's column c = lane % 16 completes the list
-// index 16 tile + c).  The partner wave's lists merge in; T = the Pe-th largest
-// of the row's 16 J keys bounds the Pe-th largest approximate dot from below
-// (Pe distinct lists have keys >= T, so approximate dots >= T - 2 - E, E the
-// packing error).  Pe lists then have exact scores within eps of those, so
-// every list among the Pe exact nearest has an approximate dot within 2 eps
-// of T - 2 - E and a key >= T - 2E - 2 eps (taken with a factor 1.25 and a few
-// ulps to spare); those keys form a prefix of each lane's list.  A lane whose J-th key is
-// itself above that threshold may have dropped such a list: the row is then
-// marked overflowed (cand_n = CAP + 1).
+// index 16 tile + c); the two waves of a query block see disjoint tiles, so a
+// row has 2 x 16 sorted lists of J.  T = the Pe-th largest of the row's 32 J
+// keys bounds the Pe-th largest approximate dot from below (Pe distinct lists
+// have keys >= T, so approximate dots >= T - 2 - E, E the packing error).  Pe
+// lists then have exact scores within eps of those, so every list among the
+// Pe exact nearest has an approximate dot within 2 eps of T - 2 - E and a key
+// >= T - 2E - 2 eps (taken with a factor 1.25 and a few ulps to spare); those
+// keys form a prefix of each list.  A list whose J-th key is itself above that
+// threshold may have dropped such a list: the row is then marked overflowed
+// (cand_n = CAP + 1).  After the pass wave h finishes rows 2h, 2h + 1 of each
+// lane.
 template <int DT, int J>
 __global__ __launch_bounds__(256) void coarse_fused_kernel(
     const float* __restrict__ Q, int nq, int d, const uint4* __restrict__ Cb, int L, float cmax,
     int Pe, int IB, int normalize, float* __restrict__ qn_out, float* __restrict__ qnorm_out,
     uint32_t* __restrict__ cand, uint32_t* __restrict__ cand_n) {
+    static_assert(FC_NH == 2, "two key lists per lane");
     extern __shared__ __align__(16) char smem[];
-    constexpr int CAP = 16 * J;
+    constexpr int CAP = 32 * J;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
-    const int qb = wave % FC_QBW, h = wave / FC_QBW;
+    const int qb = wave % FC_QBW;
+    const int h = __builtin_amdgcn_readfirstlane(wave / FC_QBW);
     const int q0 = blockIdx.x * FC_QB;
     const int rows = min(FC_QB, nq - q0);
     float* tile = reinterpret_cast<float*>(smem);
@@ -321,46 +335,43 @@ __global__ __launch_bounds__(256) void coarse_fused_kernel(
     for (int r = 0; r < 4; r++)
 #pragma unroll
         for (int j = 0; j < J; j++) top[r][j] = -3.0e38f;  // below every key
-    fc_pass<DT>(Cb, L, ah, al, reinterpret_cast<u32x4*>(smem), [&](const floatx4& acc, int cb) {
+    fc_pass<DT>(Cb, L, ah, al, reinterpret_cast<u32x4*>(smem), [&](const floatx4& acc, int cb, bool masked) {
         const uint32_t ti = (uint32_t)cb >> 4;
-        if (cb + 16 <= L) {  // whole tile (uniform branch)
+        const bool valid = !masked || cb + c < L;
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                top_insert<J>(top[r], __uint_as_float((__float_as_uint(acc[r] + 2.0f) & kmask) | ti));
-        } else {
-            const bool valid = cb + c < L;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float k = __uint_as_float((__float_as_uint(acc[r] + 2.0f) & kmask) | ti);
-                top_insert<J>(top[r], valid ? k : -3.0e38f);
-            }
+        for (int r = 0; r < 4; r++) {
+            const float k = __uint_as_float((__float_as_uint(acc[r] + 2.0f) & kmask) | ti);
+            top_insert<J>(top[r], valid ? k : -3.0e38f);
         }
     });
 
-    // ---- merge the partner wave's lists (same rows and column class).
-    __syncthreads();  // the pipeline buffers become the merge area
-    float* mg = reinterpret_cast<float*>(smem) + (size_t)qb * 4 * J * 64;
-    if (h == 1) {
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int j = 0; j < J; j++) mg[(r * J + j) * 64 + lane] = top[r][j];
-    }
-    __syncthreads();
-    if (h == 1) return;  // no barriers below
+    // ---- exchange: every wave's lists to LDS [qb][h][r][j][lane].
+    __syncthreads();  // the pipeline buffers become the exchange area
+    float* mg = reinterpret_cast<float*>(smem);
 #pragma unroll
     for (int r = 0; r < 4; r++)
 #pragma unroll
-        for (int j = 0; j < J; j++) top_insert<J>(top[r], mg[(r * J + j) * 64 + lane]);
+        for (int j = 0; j < J; j++) mg[((((qb * 2 + h) * 4 + r) * J + j) << 6) + lane] = top[r][j];
+    __syncthreads();
 
-    // ---- per row: threshold, overflow test and candidate output.
+    // ---- rows 2h, 2h + 1: threshold, overflow test and candidate output.
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int rr = 0; rr < 2; rr++) {
+        const int r = 2 * h + rr;
         const int row = qb * 16 + 4 * g + r;
-        uint32_t kv[J];
+        float own[J], oth[J];
 #pragma unroll
-        for (int j = 0; j < J; j++) kv[j] = fkey(top[r][j]);
-        const float T = fkey_to_float(group16_rank<J>(kv, CAP - Pe));
+        for (int j = 0; j < J; j++) {
+            own[j] = h ? top[2 + rr][j] : top[rr][j];
+            oth[j] = mg[((((qb * 2 + (1 - h)) * 4 + r) * J + j) << 6) + lane];
+        }
+        uint32_t kv[2 * J];
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            kv[j] = fkey(own[j]);
+            kv[J + j] = fkey(oth[j]);
+        }
+        const float T = fkey_to_float(group16_rank<2 * J>(kv, CAP - Pe));
         const float qb_norm = snorm[FC_QB + row];
         const float qc = qb_norm * cmax;
         const float u = 5.9604645e-08f;
@@ -369,10 +380,14 @@ __global__ __launch_bounds__(256) void coarse_fused_kernel(
         const float ub = __uint_as_float((__float_as_uint(qc + 2.0f) & 0x7f800000u) + 0x00800000u);
         const float E = ((float)(1u << IB) + 0.5f) * ub * u;
         const float kthr = T - (2.0f * E + 2.5f * coarse_eps_bf16(d, qb_norm, cmax) + 8.0f * ub * u);
-        uint32_t n = 0;
+        uint32_t n0 = 0, n1 = 0;
 #pragma unroll
-        for (int j = 0; j < J; j++) n += top[r][j] >= kthr ? 1u : 0u;
-        const bool over = top[r][J - 1] >= kthr;
+        for (int j = 0; j < J; j++) {
+            n0 += own[j] >= kthr ? 1u : 0u;
+            n1 += oth[j] >= kthr ? 1u : 0u;
+        }
+        const uint32_t n = n0 + n1;
+        const bool over = own[J - 1] >= kthr || oth[J - 1] >= kthr;
         // exclusive prefix of n over the 16 lanes of the group
         uint32_t incl = n;
 #pragma unroll
@@ -383,18 +398,26 @@ __global__ __launch_bounds__(256) void coarse_fused_kernel(
         const uint32_t total = __shfl(incl, (lane & 48) | 15, 64);
         const bool any_over = __ballot(over) >> (16 * g) & 0xffffull;
         if (row < rows) {
-            uint32_t* out = cand + (size_t)(q0 + row) * CAP;
-            const uint32_t base = incl - n;
+            uint32_t* out = cand + (size_t)(q0 + row) * CAP + (incl - n);
+            if (!any_over) {
 #pragma unroll
-            for (int j = 0; j < J; j++)
-                if ((uint32_t)j < n && !any_over)
-                    out[base + j] = 16u * (__float_as_uint(top[r][j]) & ~kmask) + (uint32_t)c;
+                for (int j = 0; j < J; j++)
+                    if ((uint32_t)j < n0) out[j] = 16u * (__float_as_uint(own[j]) & ~kmask) + (uint32_t)c;
+#pragma unroll
+                for (int j = 0; j < J; j++)
+                    if ((uint32_t)j < n1) out[n0 + j] = 16u * (__float_as_uint(oth[j]) & ~kmask) + (uint32_t)c;
+            }
             if (c == 0) cand_n[q0 + row] = any_over ? (uint32_t)CAP + 1u : total;
         }
     }
 }
 
-int coarse_fused_cap(int P) { return P <= 32 ? 128 : 256; }
+#define FC_J 8  // keys per (wave, lane, row)
+
+int coarse_fused_cap(int P) {
+    (void)P;
+    return 32 * FC_J;
+}
 
 bool coarse_fused_supported(int d, int P) { return d >= 1 && d <= 128 && P >= 1 && P <= 64; }
 
@@ -416,10 +439,7 @@ template <int DT>
 static void launch_fused_j(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int Pe,
                            int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
                            hipStream_t s) {
-    if (coarse_fused_cap(Pe) == 128)
-        launch_fused<DT, 8>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s);
-    else
-        launch_fused<DT, 16>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s);
+    launch_fused<DT, FC_J>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s);
 }
 
 void launch_coarse_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int P,
@@ -506,7 +526,7 @@ __global__ __launch_bounds__(256) void coarse_bf16x3_dots_kernel(const float* __
     const int row_a = q0 + qb * 16 + c;
     u32x4 ah[DT], al[DT];
     fc_split_rows<DT>([&](int j) { return row_a < nq ? Q[(size_t)row_a * d + j] : 0.0f; }, d, g, ah, al);
-    fc_pass<DT>(Cb, L, ah, al, reinterpret_cast<u32x4*>(smem), [&](const floatx4& acc, int cb) {
+    fc_pass<DT>(Cb, L, ah, al, reinterpret_cast<u32x4*>(smem), [&](const floatx4& acc, int cb, bool) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int row = q0 + qb * 16 + 4 * g + r, col = cb + c;
