@@ -319,7 +319,16 @@ __global__ __launch_bounds__(256) void coarse_exact_flagged_kernel(
         const int q = (int)flag_list[fi];
         for (int j = threadIdx.x; j < d; j += VGPU_BLOCK) qs[j] = qn[(size_t)q * d + j];
         __syncthreads();
-        for (int i = threadIdx.x; i < L; i += VGPU_BLOCK) xrow[i] = approx_dot(qs, C + (size_t)i * d, d);
+        int i0 = threadIdx.x;
+        if ((d & 31) == 0) {  // four rows per thread with their loads in flight together
+            for (; i0 + 3 * VGPU_BLOCK < L; i0 += 4 * VGPU_BLOCK) {
+                float x[4];
+                approx_dot_rows<4>(qs, C + (size_t)i0 * d, (size_t)VGPU_BLOCK * d, d, x);
+#pragma unroll
+                for (int r = 0; r < 4; r++) xrow[i0 + r * VGPU_BLOCK] = x[r];
+            }
+        }
+        for (int i = i0; i < L; i += VGPU_BLOCK) xrow[i] = approx_dot(qs, C + (size_t)i * d, d);
         __syncthreads();
         select_block_query<EPT>(xrow, qs, qnorm[q], C, q, L, d, P, cmax, probe, overflow);
     }

@@ -35,6 +35,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 #define FC_NH 2                // waves per query block; each takes its own tiles of a stage
 #define FC_SUB 2               // 16-centroid tiles per wave and stage
 #define FC_ST (FC_NH * FC_SUB) // tiles per stage
+#define FC_TR 8                // keys per list that enter the rank (<= FC_J)
 static_assert(FC_QBW * FC_NH * 64 == VGPU_BLOCK, "wave roles");
 
 // Round to nearest even bfloat16 (finite inputs).
@@ -123,7 +124,7 @@ __host__ __device__ inline size_t fc_lds_bytes(int d, int DT, int J) {
 template <int DT, typename Epi>
 __device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, const u32x4 (&ah)[DT],
                                         const u32x4 (&al)[DT], u32x4* lds, Epi epi) {
-    const u32x4* __restrict__ Cb = reinterpret_cast<const u32x4*>(Cb_in);
+    const u32x4* Cb = reinterpret_cast<const u32x4*>(Cb_in);
     constexpr int SC = FC_ST * DT * 4 * 16;  // chunks per stage and half
     constexpr int PER = 2 * SC / VGPU_BLOCK;  // chunks each thread copies per stage
     static_assert((2 * SC) % VGPU_BLOCK == 0, "stage split");
@@ -133,11 +134,14 @@ __device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, 
     // A stage is 2 SC contiguous chunks of Cb (padded to whole stages), copied
     // to LDS unchanged: slot i of thread tid is chunk i * VGPU_BLOCK + tid.
     u32x4 pre[PER];
+    // Buffer loads: per-lane offset in a VGPR, stage and slot offsets in
+    // SGPRs, range-checked against the padded size.
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<u32x4*>(Cb), (short)0, nst * 2 * SC * 16, 0x00020000);
+    const uint32_t lofs = (uint32_t)tid * 16u;
 #define FC_FETCH(ST)                                                                   \
-    {                                                                                  \
-        const u32x4* __restrict__ sb = Cb + (size_t)(ST) * 2 * SC;                     \
-        _Pragma("unroll") for (int i = 0; i < PER; i++) pre[i] = sb[i * VGPU_BLOCK + tid]; \
-    }
+    _Pragma("unroll") for (int i = 0; i < PER; i++) pre[i] = __builtin_amdgcn_raw_buffer_load_b128( \
+        rsrc, lofs, (uint32_t)((ST) * 2 * SC * 16 + i * VGPU_BLOCK * 16), 0);
 #define FC_STORE(BUF)                                                                  \
     _Pragma("unroll") for (int i = 0; i < PER; i++) lds[(size_t)(BUF) * 2 * SC + i * VGPU_BLOCK + tid] = pre[i];
     FC_FETCH(0)
@@ -271,7 +275,8 @@ __device__ __forceinline__ void top_insert(float (&t)[J], float v) {
 // lists then have exact scores within eps of those, so every list among the
 // Pe exact nearest has an approximate dot within 2 eps of T - 2 - E and a key
 // >= T - 2E - 2 eps (taken with a factor 1.25 and a few ulps to spare); those
-// keys form a prefix of each list.  A list whose J-th key is itself above that
+// keys form a prefix of each list.  (T is taken over the lists' first FC_TR
+// keys, Pe <= 32 FC_TR.)  A list whose J-th key is itself above that
 // threshold may have dropped such a list: the row is then marked overflowed
 // (cand_n = CAP + 1).  After the pass wave h finishes rows 2h, 2h + 1 of each
 // lane.
@@ -365,13 +370,16 @@ __global__ __launch_bounds__(256) void coarse_fused_kernel(
             own[j] = h ? top[2 + rr][j] : top[rr][j];
             oth[j] = mg[((((qb * 2 + (1 - h)) * 4 + r) * J + j) << 6) + lane];
         }
-        uint32_t kv[2 * J];
+        // T = the Pe-th largest of the lists' first FC_TR keys (a subset, so
+        // Pe distinct lists still have keys >= T; T is below the full rank
+        // only when a list holds more than FC_TR of the top Pe).
+        uint32_t kv[2 * FC_TR];
 #pragma unroll
-        for (int j = 0; j < J; j++) {
+        for (int j = 0; j < FC_TR; j++) {
             kv[j] = fkey(own[j]);
-            kv[J + j] = fkey(oth[j]);
+            kv[FC_TR + j] = fkey(oth[j]);
         }
-        const float T = fkey_to_float(group16_rank<2 * J>(kv, CAP - Pe));
+        const float T = fkey_to_float(group16_rank<2 * FC_TR>(kv, 32 * FC_TR - Pe));
         const float qb_norm = snorm[FC_QB + row];
         const float qc = qb_norm * cmax;
         const float u = 5.9604645e-08f;
