@@ -1,6 +1,6 @@
 // FAST-mode ADC scan for byte codes (codebook_size != 16): one workgroup of
 // 256 threads per query, the per-query table resident in LDS, the probed
-// lists streamed from HBM with one round of software prefetch.
+// lists streamed from HBM with two rounds of software prefetch.
 //
 // Reference: search_approx_internal_observed src/ivf_pq/search.rs:1175-1391
 // (per probed list: residual r = q - c, compute_adc_table_into
@@ -176,8 +176,10 @@ __device__ inline FastLds fs8_carve(char* smem, float* static_lut, int d, int M,
 
 // Keep the buffer entries whose high word is <= T (in place, chunk by chunk:
 // a chunk is read into registers before any of its slots are rewritten, and
-// the compacted prefix never passes the end of the chunk being read).  With
-// `relabel`, each kept key is rewritten as (probe slot << 32) | position.
+// the compacted prefix never passes the end of the chunk being read).  Keys
+// carry t, the entry's index in the concatenated probed lists; with
+// `relabel`, each kept key is rewritten as (probe slot << 32) | position, the
+// slot found by binary search over the list prefix sums.
 __device__ inline uint32_t fs8_compact(FastLds& s, uint32_t n, uint32_t T, bool relabel, int P) {
     const int tid = threadIdx.x;
     __syncthreads();
@@ -189,11 +191,15 @@ __device__ inline uint32_t fs8_compact(FastLds& s, uint32_t n, uint32_t T, bool 
         bool take = i < n && (uint32_t)(v >> 32) <= T;
         __syncthreads();
         if (take && relabel) {
-            const uint32_t pos = (uint32_t)v;
-            uint32_t p = 0;
-            for (int j = 0; j < P; j++)
-                if (pos - s.lbeg[j] < s.llen[j]) p = (uint32_t)j;
-            v = ((uint64_t)p << 32) | pos;
+            // the largest slot p < P with pref[p] <= t is the non-empty list holding t
+            const uint32_t t = (uint32_t)v;
+            uint32_t lo = 0, hi = (uint32_t)P;
+            while (hi - lo > 1u) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (s.pref[mid] <= t) lo = mid;
+                else hi = mid;
+            }
+            v = ((uint64_t)lo << 32) | (s.lbeg[lo] + (t - s.pref[lo]));
         }
         int slot = wave_append_slot(take, &s.misc[0]);
         if (take) s.keys[slot] = v;
@@ -237,7 +243,8 @@ struct RoundRegs {
     CodeRow<MT> row[FS_U];
     float bias[FS_U];
     float t0[FS_U];    // ||q - c||^2 of the entry's list
-    uint32_t pos[FS_U];// 0xffffffff = no entry
+    uint32_t pos[FS_U];// position (code row), generic path only
+    uint32_t t[FS_U];  // index in the concatenated probed lists; 0xffffffff = no entry
 };
 
 template <int MT>
@@ -250,7 +257,8 @@ __device__ __forceinline__ void fs8_fetch(const DevIndex& ix, const FastLds& s, 
         if (valid)
             while (t >= s.pref[cur + 1]) cur++;
         const uint32_t pos = valid ? s.lbeg[cur] + (t - s.pref[cur]) : 0u;
-        g.pos[u] = valid ? pos : 0xffffffffu;
+        g.pos[u] = pos;
+        g.t[u] = valid ? t : 0xffffffffu;
         g.t0[u] = s.term0[cur];
         if constexpr (MT > 0) load_row<MT>(g.row[u], ix.codes + (size_t)pos * MT);
         g.bias[u] = ix.bias[pos];
@@ -277,14 +285,13 @@ __device__ __forceinline__ void fs8_consume(const DevIndex& ix, FastLds& s, cons
     uint32_t tot = 0;
 #pragma unroll
     for (int u = 0; u < FS_U; u++) {
-        const bool ok = g.pos[u] != 0xffffffffu;
+        const bool ok = g.t[u] != 0xffffffffu;
         float dist;
         if constexpr (MT > 0 && KT > 0) {
             dist = (g.t0[u] + g.bias[u]) + row_sum<MT, KT>(g.row[u], lut_static);
         } else {
-            const uint32_t pos = ok ? g.pos[u] : 0u;
             dist = (g.t0[u] + g.bias[u]) +
-                   row_sum_generic(ix.codes + (size_t)pos * ix.M, s.lut, ix.M, ix.K);
+                   row_sum_generic(ix.codes + (size_t)g.pos[u] * ix.M, s.lut, ix.M, ix.K);
         }
         fk[u] = fkey(dist);
         take[u] = ok && fk[u] <= thr && (!RETRY || fk[u] > lo);
@@ -301,7 +308,7 @@ __device__ __forceinline__ void fs8_consume(const DevIndex& ix, FastLds& s, cons
         if (take[u]) {
             const uint32_t below = __builtin_amdgcn_mbcnt_hi(
                 (uint32_t)(mask[u] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask[u], 0u));
-            s.keys[base + before[u] + below] = ((uint64_t)fk[u] << 32) | g.pos[u];
+            s.keys[base + before[u] + below] = ((uint64_t)fk[u] << 32) | g.t[u];
         }
     }
     if (base + tot > cap && lane == 0) s.misc[3 + parity] = 1u;
@@ -461,24 +468,33 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     }
     __syncthreads();
 
-    // ---- scan: FS_ROUND entries per round, next round's loads in flight.
+    // ---- scan: FS_ROUND entries per round, the next two rounds' loads in
+    // flight (a ring of three register sets).  Round r uses flag parity r & 1.
     const uint32_t total = s.pref[P];
     const int keep = a.kk;
     const uint32_t cap = (uint32_t)(buf - FS_ROUND);
     int cur = 0;
-    RoundRegs<MT> ga, gb;
-    if (total > 0) fs8_fetch<MT>(ix, s, 0, total, cur, ga);
-    for (uint32_t rb = 0; rb < total; rb += 2 * FS_ROUND) {
-        fs8_fetch<MT>(ix, s, rb + FS_ROUND, total, cur, gb);
-        fs8_consume<MT, KT, false>(ix, s, slut, ga, s.misc[1], 0u, cap, 0);
-        __syncthreads();
-        if (s.misc[3]) fs8_flush(s, keep, cap, 0);
-        if (rb + FS_ROUND >= total) break;
-        fs8_fetch<MT>(ix, s, rb + 2 * FS_ROUND, total, cur, ga);
-        fs8_consume<MT, KT, false>(ix, s, slut, gb, s.misc[1], 0u, cap, 1);
-        __syncthreads();
-        if (s.misc[4]) fs8_flush(s, keep, cap, 1);
+    RoundRegs<MT> ga, gb, gc;
+    if (total > 0) {
+        fs8_fetch<MT>(ix, s, 0, total, cur, ga);
+        fs8_fetch<MT>(ix, s, FS_ROUND, total, cur, gb);
     }
+#define FS8_STEP(CONSUME, NEXT, R)                                                     \
+    {                                                                                  \
+        const uint32_t rbase = (R) * FS_ROUND;                                         \
+        const int par = (int)((R) & 1u);                                               \
+        fs8_fetch<MT>(ix, s, rbase + 2 * FS_ROUND, total, cur, NEXT);                  \
+        fs8_consume<MT, KT, false>(ix, s, slut, CONSUME, s.misc[1], 0u, cap, par);     \
+        __syncthreads();                                                               \
+        if (s.misc[3 + par]) fs8_flush(s, keep, cap, par);                             \
+        if (rbase + FS_ROUND >= total) break;                                          \
+    }
+    for (uint32_t r = 0; r * FS_ROUND < total; r += 3) {
+        FS8_STEP(ga, gc, r)
+        FS8_STEP(gb, ga, r + 1)
+        FS8_STEP(gc, gb, r + 2)
+    }
+#undef FS8_STEP
     __syncthreads();
 
     // ---- proof that the buffer holds R, then rescoring.
@@ -564,7 +580,46 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
         }
         __syncthreads();
     }
-    const int n2 = next_pow2(n > 0 ? (int)n : 1);
+    if (n <= 256) {  // one wave sorts in registers; no block barriers below
+        if (tid >= 64) return;
+        auto emit = [&](int j, uint64_t key) {
+            const size_t o = (size_t)q * kout + j;
+            if ((uint32_t)j < n) {
+                a.out_vidx[o] = (uint32_t)key;
+                a.out_dist[o] = key_dist(key);
+            } else {
+                a.out_vidx[o] = 0xffffffffu;
+                a.out_dist[o] = __int_as_float(0x7f800000);
+            }
+        };
+        int done = 64;
+        if (n <= 64) {
+            uint64_t k1[1] = {(uint32_t)lane < n ? s.keys[lane] : ~0ull};
+            wave_sort_regs<1>(k1);
+            if (lane < kout) emit(lane, k1[0]);
+        } else if (n <= 128) {
+            uint64_t k2[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) k2[e] = (uint32_t)(e * 64 + lane) < n ? s.keys[e * 64 + lane] : ~0ull;
+            wave_sort_regs<2>(k2);
+#pragma unroll
+            for (int e = 0; e < 2; e++)
+                if (e * 64 + lane < kout) emit(e * 64 + lane, k2[e]);
+            done = 128;
+        } else {
+            uint64_t k4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) k4[e] = (uint32_t)(e * 64 + lane) < n ? s.keys[e * 64 + lane] : ~0ull;
+            wave_sort_regs<4>(k4);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (e * 64 + lane < kout) emit(e * 64 + lane, k4[e]);
+            done = 256;
+        }
+        for (int j = done + lane; j < kout; j += 64) emit(j, ~0ull);  // j >= n: padding
+        return;
+    }
+    const int n2 = next_pow2((int)n);
     for (int t = (int)n + tid; t < n2; t += VGPU_BLOCK) s.keys[t] = ~0ull;
     block_bitonic_sort_keys(s.keys, n2);
     for (int j = tid; j < kout; j += VGPU_BLOCK) {
