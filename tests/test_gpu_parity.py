@@ -338,13 +338,14 @@ def test_fast_scan_ties_and_fallback_match_oracle(vg, oracle, copies, k):
         _assert_same_results(ids, dists, oids, odists)
 
 
-@pytest.mark.parametrize("copies,expect", [(300, "second_pass"), (900, "exact_rerun")])
+@pytest.mark.parametrize("copies,expect", [(200, "second_pass"), (900, "exact_rerun")])
 def test_fast_second_pass_and_exact_rerun(vg, oracle, copies, expect):
     """Near-duplicates (copies of one vector with 1e-6 noise) put hundreds of
-    approximate distances inside the proof window A_k + 2 tau.  With 300 copies
-    the FAST kernel's second pass collects them all; with 900 they overflow its
-    buffer and the query is rerun by the EXACT kernel.  Both must return the
-    oracle's rows, and the statistics must show which path ran."""
+    approximate distances inside the proof window A_k + 2 tau.  With 200 copies
+    the FAST kernel's second pass collects them all (its buffer holds 256 past
+    a flush for k = 5); with 900 they overflow it and the query is rerun by
+    the EXACT kernel.  Both must return the oracle's rows, and the statistics
+    must show which path ran."""
     from vicinity_amd import IVFPQIndex
 
     _print_case(f"fast second pass copies={copies}")

@@ -32,7 +32,7 @@
 
 namespace vgpu {
 
-#define FS_U 2                          // entries per thread per round
+#define FS_U 1                          // entries per thread per round
 #define FS_ROUND (VGPU_BLOCK * FS_U)    // entries per round
 
 // Codes of one list entry held in registers.
@@ -123,6 +123,7 @@ struct FastLds {
     uint32_t* llen;  // [P]
     uint32_t* pref;  // [P + 1]
     float* term0;    // [P] ||q - c||^2
+    uint2* bt;       // [P] (lbeg - pref as u32, bits of term0): one read per entry
     RadixScratch* rs;
     uint32_t* misc;  // [0] count [1] thr [2] lost ties [3..4] flush flags by round parity
                      // [5] entries evicted by flushes [6] flushes
@@ -153,12 +154,13 @@ __host__ __device__ inline size_t fs8_layout(int d, int M, int K, int P, int buf
     off[7] = o; o = fs8_align(o + (size_t)P * 4);          // term0
     off[8] = o; o = fs8_align(o + sizeof(RadixScratch));   // radix scratch
     off[9] = o; o = fs8_align(o + 8 * 4);                  // misc
+    off[10] = o; o = fs8_align(o + (size_t)P * 8);         // bt
     return o;
 }
 
 __device__ inline FastLds fs8_carve(char* smem, float* static_lut, int d, int M, int K, int P,
                                     int buf) {
-    size_t off[10];
+    size_t off[11];
     fs8_layout(d, M, K, P, buf, static_lut != nullptr, off);
     FastLds s;
     s.lut = static_lut ? static_lut : (float*)(smem + off[0]);
@@ -171,6 +173,7 @@ __device__ inline FastLds fs8_carve(char* smem, float* static_lut, int d, int M,
     s.term0 = (float*)(smem + off[7]);
     s.rs = (RadixScratch*)(smem + off[8]);
     s.misc = (uint32_t*)(smem + off[9]);
+    s.bt = (uint2*)(smem + off[10]);
     return s;
 }
 
@@ -237,7 +240,7 @@ __device__ inline void fs8_flush(FastLds& s, int keep, uint32_t cap, int parity)
 // Per-thread state of the entries one thread handles in one round.  The
 // loads are unconditional (a slot past the end reads position 0, which exists
 // whenever anything is scanned) so the compiler can wait for one round's
-// loads while the next round's are still in flight.
+// loads while the next rounds' are still in flight.
 template <int MT>
 struct RoundRegs {
     CodeRow<MT> row[FS_U];
@@ -247,19 +250,33 @@ struct RoundRegs {
     uint32_t t[FS_U];  // index in the concatenated probed lists; 0xffffffff = no entry
 };
 
+// Entry t = rbase + u * VGPU_BLOCK + tid.  Each wave's 64 entries of a slot
+// are consecutive, so the wave keeps one uniform cursor `cw` (the probed list
+// holding the start of its next window; windows only move forward) and a lane
+// finds its list by counting the list starts inside the window (usually none
+// or one).  Empty lists repeat a start and are counted over.
 template <int MT>
 __device__ __forceinline__ void fs8_fetch(const DevIndex& ix, const FastLds& s, uint32_t rbase,
-                                          uint32_t total, int& cur, RoundRegs<MT>& g) {
+                                          uint32_t total, int P, int& cw, RoundRegs<MT>& g) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int u = 0; u < FS_U; u++) {
-        const uint32_t t = rbase + u * VGPU_BLOCK + threadIdx.x;
+        const uint32_t wb = rbase + (uint32_t)u * VGPU_BLOCK + wave * 64u;  // window start
+        const uint32_t t = wb + lane;
         const bool valid = t < total;
-        if (valid)
-            while (t >= s.pref[cur + 1]) cur++;
-        const uint32_t pos = valid ? s.lbeg[cur] + (t - s.pref[cur]) : 0u;
+        while (cw + 1 < P && __builtin_amdgcn_readfirstlane(s.pref[cw + 1]) <= wb) cw++;
+        int lst = cw;
+        for (int j = cw + 1; j < P; j++) {
+            const uint32_t b = __builtin_amdgcn_readfirstlane(s.pref[j]);
+            if (b >= wb + 64u) break;
+            lst += t >= b ? 1 : 0;
+        }
+        const uint2 e = s.bt[lst];
+        const uint32_t pos = valid ? e.x + t : 0u;
         g.pos[u] = pos;
         g.t[u] = valid ? t : 0xffffffffu;
-        g.t0[u] = s.term0[cur];
+        g.t0[u] = __uint_as_float(e.y);
         if constexpr (MT > 0) load_row<MT>(g.row[u], ix.codes + (size_t)pos * MT);
         g.bias[u] = ix.bias[pos];
     }
@@ -466,6 +483,8 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
             s.lut[e] = -2.0f * acc;
         }
     }
+    for (int p = tid; p < P; p += VGPU_BLOCK)
+        s.bt[p] = make_uint2(s.lbeg[p] - s.pref[p], __float_as_uint(s.term0[p]));
     __syncthreads();
 
     // ---- scan: FS_ROUND entries per round, the next two rounds' loads in
@@ -476,14 +495,14 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     int cur = 0;
     RoundRegs<MT> ga, gb, gc;
     if (total > 0) {
-        fs8_fetch<MT>(ix, s, 0, total, cur, ga);
-        fs8_fetch<MT>(ix, s, FS_ROUND, total, cur, gb);
+        fs8_fetch<MT>(ix, s, 0, total, P, cur, ga);
+        fs8_fetch<MT>(ix, s, FS_ROUND, total, P, cur, gb);
     }
 #define FS8_STEP(CONSUME, NEXT, R)                                                     \
     {                                                                                  \
         const uint32_t rbase = (R) * FS_ROUND;                                         \
         const int par = (int)((R) & 1u);                                               \
-        fs8_fetch<MT>(ix, s, rbase + 2 * FS_ROUND, total, cur, NEXT);                  \
+        fs8_fetch<MT>(ix, s, rbase + 2 * FS_ROUND, total, P, cur, NEXT);                  \
         fs8_consume<MT, KT, false>(ix, s, slut, CONSUME, s.misc[1], 0u, cap, par);     \
         __syncthreads();                                                               \
         if (s.misc[3 + par]) fs8_flush(s, keep, cap, par);                             \
@@ -524,14 +543,14 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
             }
             __syncthreads();
             cur = 0;
-            fs8_fetch<MT>(ix, s, 0, total, cur, ga);
+            fs8_fetch<MT>(ix, s, 0, total, P, cur, ga);
             for (uint32_t rb = 0; rb < total; rb += 2 * FS_ROUND) {
-                fs8_fetch<MT>(ix, s, rb + FS_ROUND, total, cur, gb);
+                fs8_fetch<MT>(ix, s, rb + FS_ROUND, total, P, cur, gb);
                 fs8_consume<MT, KT, true>(ix, s, slut, ga, bk, thr, cap, 0);
                 __syncthreads();
                 if (s.misc[3]) break;
                 if (rb + FS_ROUND >= total) break;
-                fs8_fetch<MT>(ix, s, rb + 2 * FS_ROUND, total, cur, ga);
+                fs8_fetch<MT>(ix, s, rb + 2 * FS_ROUND, total, P, cur, ga);
                 fs8_consume<MT, KT, true>(ix, s, slut, gb, bk, thr, cap, 1);
                 __syncthreads();
                 if (s.misc[4]) break;
@@ -644,7 +663,7 @@ static size_t static_lut_bytes(const DevIndex& ix) {
 }
 
 size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
-    size_t off[10];
+    size_t off[11];
     const size_t st = static_lut_bytes(ix);
     return st + fs8_layout(ix.d, ix.M, ix.K, a.P, fs8_buf(a.kk), st != 0, off);
 }
@@ -652,7 +671,7 @@ size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
 template <int MT, int KT, int DS>
 static void launch_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     const int buf = fs8_buf(a.kk);
-    size_t off[10];
+    size_t off[11];
     const size_t dyn = fs8_layout(ix.d, ix.M, ix.K, a.P, buf, MT > 0 && KT >= 64, off);
     auto k = scan8_fast_kernel<MT, KT, DS>;
     ensure_dyn_lds((const void*)k, dyn);
