@@ -240,7 +240,7 @@ __device__ __forceinline__ uint32_t group16_rank(uint32_t (&v)[J], int k) {
             } else {
 #pragma unroll
                 for (int e = 0; e < J; e++) {
-                    const uint32_t o = __shfl_xor(v[e], stride, 64);
+                    const uint32_t o = shfl_xor_u32(v[e], stride);
                     const bool asc = (((e << 4) | l16) & size) == 0;
                     const bool lower = (l16 & stride) == 0;
                     v[e] = (lower == asc) ? (o < v[e] ? o : v[e]) : (o > v[e] ? o : v[e]);

@@ -447,9 +447,9 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
                     }
                 }
             }
-            acc += __shfl_xor(acc, 1, 64);
-            acc += __shfl_xor(acc, 2, 64);
-            acc += __shfl_xor(acc, 4, 64);
+            acc += __uint_as_float(shfl_xor_u32(__float_as_uint(acc), 1));
+            acc += __uint_as_float(shfl_xor_u32(__float_as_uint(acc), 2));
+            acc += __uint_as_float(shfl_xor_u32(__float_as_uint(acc), 4));
             if (p < P && sub == 0) s.term0[p] = acc;
         }
     }

@@ -297,6 +297,32 @@ __device__ __forceinline__ int wave_append_slot_count(bool take, uint32_t* count
     return take ? (int)(base + below) : -1;
 }
 
+// v of lane (lane ^ stride), stride a power of two below 64 (a constant after
+// unrolling).  Strides 1, 2 and 8 are one DPP move (quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_ror:8), 4 is two DPP row shifts and a select, 16
+// a ds_swizzle in bit mode (and 0x1f, xor 16), 32 a ds_bpermute.
+__device__ __forceinline__ uint32_t shfl_xor_u32(uint32_t v, int stride) {
+    const int x = (int)v;
+    switch (stride) {
+        case 1: return (uint32_t)__builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false);
+        case 2: return (uint32_t)__builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false);
+        case 4: {
+            const int up = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0xF, false);  // row_shl:4
+            const int dn = __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+            return (uint32_t)((threadIdx.x & 4) ? dn : up);
+        }
+        case 8: return (uint32_t)__builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, false);
+        case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle(x, 0x401F);
+        default: return (uint32_t)__shfl_xor(x, stride, 64);
+    }
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int stride) {
+    const uint32_t lo = shfl_xor_u32((uint32_t)v, stride);
+    const uint32_t hi = shfl_xor_u32((uint32_t)(v >> 32), stride);
+    return ((uint64_t)hi << 32) | lo;
+}
+
 // Ascending bitonic sort of 64*E keys held by one wave, E per lane; element
 // e*64 + lane lives in k[e] of that lane.  No LDS, no barriers.
 template <int E>
@@ -322,7 +348,7 @@ __device__ __forceinline__ void wave_sort_regs(uint64_t (&k)[E]) {
             } else {
 #pragma unroll
                 for (int e = 0; e < E; e++) {
-                    const uint64_t o = __shfl_xor(k[e], stride, 64);
+                    const uint64_t o = shfl_xor_u64(k[e], stride);
                     const bool asc = (((e << 6) | lane) & size) == 0;
                     const bool lower = (lane & stride) == 0;
                     const bool take_min = lower == asc;
