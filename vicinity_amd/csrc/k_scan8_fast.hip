@@ -211,8 +211,81 @@ __device__ inline uint32_t fs8_compact(FastLds& s, uint32_t n, uint32_t T, bool 
     return s.misc[0];
 }
 
-// Buffer full: keep the `keep` smallest keys (plus ties); at most `cap`
-// survive, otherwise the query is marked failed.  Clears the flag of `parity`.
+// An upper bound U on the rank-th smallest (0-based) high word of the buffer
+// keys (n > rank), from one 256-bin histogram over the 8 bits below the
+// common prefix of the smallest and largest high word: U is the top of the
+// bin holding rank, so every key <= the rank-th is <= U and the keys <= U are
+// those of the bins up to it.  When those number more than `limit`, the exact
+// radix select is taken instead.  All threads call it.
+__device__ uint32_t fs8_select_upper(FastLds& s, uint32_t n, uint32_t rank, uint32_t limit) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t mn = 0xffffffffu, mx = 0u;
+    for (uint32_t i = tid; i < n; i += VGPU_BLOCK) {
+        const uint32_t h = (uint32_t)(s.keys[i] >> 32);
+        mn = h < mn ? h : mn;
+        mx = h > mx ? h : mx;
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t a = shfl_xor_u32(mn, o), b = shfl_xor_u32(mx, o);
+        mn = a < mn ? a : mn;
+        mx = b > mx ? b : mx;
+    }
+    __syncthreads();  // the scratch may still be read by a previous select
+    if (lane == 0) {
+        s.rs->hist[wave] = mn;
+        s.rs->hist[8 + wave] = mx;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < VGPU_BLOCK / 64; w++) {
+        const uint32_t a = s.rs->hist[w], b = s.rs->hist[8 + w];
+        mn = a < mn ? a : mn;
+        mx = b > mx ? b : mx;
+    }
+    if (mn == mx) return mx;
+    const int sbit = 31 - __clz(mn ^ mx);  // highest differing bit
+    const int shift = sbit > 7 ? sbit - 7 : 0;
+    __syncthreads();
+    for (int i = tid; i < 256; i += VGPU_BLOCK) s.rs->hist[i] = 0u;
+    __syncthreads();
+    for (uint32_t i = tid; i < n; i += VGPU_BLOCK)
+        atomicAdd(&s.rs->hist[((uint32_t)(s.keys[i] >> 32) >> shift) & 255u], 1u);
+    __syncthreads();
+    if (tid < 64) {
+        const uint32_t h0 = s.rs->hist[4 * lane], h1 = s.rs->hist[4 * lane + 1];
+        const uint32_t h2 = s.rs->hist[4 * lane + 2], h3 = s.rs->hist[4 * lane + 3];
+        const uint32_t own = h0 + h1 + h2 + h3;
+        uint32_t incl = own;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t x = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += x;
+        }
+        const uint32_t excl = incl - own;
+        if (rank >= excl && rank < incl) {
+            uint32_t b = 3, upto = incl;  // keys in bins <= b
+            if (rank < excl + h0) { b = 0; upto = excl + h0; }
+            else if (rank < excl + h0 + h1) { b = 1; upto = excl + h0 + h1; }
+            else if (rank < excl + h0 + h1 + h2) { b = 2; upto = excl + h0 + h1 + h2; }
+            s.rs->bin = 4 * lane + b;
+            s.rs->rem = upto;
+        }
+    }
+    __syncthreads();
+    const uint32_t b = s.rs->bin, upto = s.rs->rem;
+    if (upto > limit) {  // a heavy bin: exact select
+        auto hk = [&](int i) -> uint32_t { return (uint32_t)(s.keys[i] >> 32); };
+        return block_radix_select<uint32_t>(hk, (int)n, rank, s.rs);
+    }
+    const uint32_t low = (1u << shift) - 1u;
+    const uint32_t base = sbit >= 31 ? 0u : (mn & ~((2u << sbit) - 1u));  // common prefix
+    return base | (b << shift) | low;
+}
+
+// Buffer full: keep the `keep` smallest keys (plus the rest of their
+// histogram bin); at most `cap` survive, otherwise the query is marked failed.
+// Clears the flag of `parity`.
 __device__ inline void fs8_flush(FastLds& s, int keep, uint32_t cap, int parity) {
     __syncthreads();
     const uint32_t n = s.misc[0];
@@ -221,8 +294,7 @@ __device__ inline void fs8_flush(FastLds& s, int keep, uint32_t cap, int parity)
         __syncthreads();
         return;
     }
-    auto hk = [&](int i) -> uint32_t { return (uint32_t)(s.keys[i] >> 32); };
-    const uint32_t T = block_radix_select<uint32_t>(hk, (int)n, (uint32_t)(keep - 1), s.rs);
+    const uint32_t T = fs8_select_upper(s, n, (uint32_t)(keep - 1), cap);
     const uint32_t kept = fs8_compact(s, n, T, false, 0);
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -524,8 +596,8 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     bool retried = false;
     uint32_t bk = 0xffffffffu;
     if (!fail && n > (uint32_t)kout) {
-        auto hk = [&](int i) -> uint32_t { return (uint32_t)(s.keys[i] >> 32); };
-        const uint32_t Ak = block_radix_select<uint32_t>(hk, (int)n, (uint32_t)(kout - 1), s.rs);
+        // an upper bound on A_k: R grows by at most the rest of A_k's bin
+        const uint32_t Ak = fs8_select_upper(s, n, (uint32_t)(kout - 1), 0xffffffffu);
         float t0max = 0.0f;
         for (int p = 0; p < P; p++) t0max = fmaxf(t0max, s.term0[p]);
         const float tau = fast_tau(d, M, ds, a.qnorm[q], ix.cmax, ix.rmax, t0max);
