@@ -647,16 +647,34 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     if (fail) return;
     n = fs8_compact(s, n, bk, true, P);  // R, keys relabelled (probe slot, position)
 
-    const int KL = K > 64 ? K : 64;  // rescoring chunk: KL entries x M codebooks
+    // Rescoring chunks of KL entries: their code rows are staged in the table
+    // region after the KL x M partial distances, so the codeword loads do not
+    // wait on a dependent global load.
+    const int KL = K > 64 ? K / 2 : 32;
+    uint8_t* scodes = reinterpret_cast<uint8_t*>(s.lut + (size_t)KL * M);
     for (uint32_t c0 = 0; c0 < n; c0 += (uint32_t)KL) {
         const uint32_t cn = min((uint32_t)KL, n - c0);
+        if constexpr (MT > 0 && MT % 16 == 0) {  // 16-byte pieces of code rows
+            for (uint32_t t = tid; t < cn * (uint32_t)(MT / 16); t += VGPU_BLOCK) {
+                const uint32_t i = t / (uint32_t)(MT / 16), w = t % (uint32_t)(MT / 16);
+                const uint32_t pos = (uint32_t)s.keys[c0 + i];
+                reinterpret_cast<uint4*>(scodes)[t] =
+                    reinterpret_cast<const uint4*>(ix.codes + (size_t)pos * MT)[w];
+            }
+        } else {
+            for (uint32_t t = tid; t < cn * (uint32_t)M; t += VGPU_BLOCK) {
+                const uint32_t pos = (uint32_t)s.keys[c0 + t / (uint32_t)M];
+                scodes[t] = ix.codes[(size_t)pos * M + t % (uint32_t)M];
+            }
+        }
+        __syncthreads();
 #pragma unroll 2
         for (uint32_t t = tid; t < cn * (uint32_t)M; t += VGPU_BLOCK) {
             const uint32_t i = c0 + t / (uint32_t)M;
             const int m = (int)(t % (uint32_t)M);
             const uint64_t v = s.keys[i];
-            const uint32_t pos = (uint32_t)v, p = (uint32_t)(v >> 32);
-            const uint8_t code = ix.codes[(size_t)pos * M + m];
+            const uint32_t p = (uint32_t)(v >> 32);
+            const uint8_t code = scodes[t];
             const float* cw = ix.codebooks + ((size_t)m * K + code) * ds;
             const float* c = ix.centroids + (size_t)s.lid[p] * d + m * ds;
             s.lut[t] = exact_sub_distance<DS>(s.qs + m * ds, c, cw, ds);
