@@ -647,6 +647,84 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     if (fail) return;
     n = fs8_compact(s, n, bk, true, P);  // R, keys relabelled (probe slot, position)
 
+    // Two threads per entry (codebooks 0 .. M/2 - 1 and M/2 .. M - 1) when the
+    // probed lists' residuals r = q - c fit the idle table region: each thread
+    // loads its half code row, then its codewords in batches; r comes from LDS
+    // (the same single subtraction exact_sub_distance makes).  The first
+    // thread adds its sub-distances in codebook order from 0.0 and continues
+    // with its partner's, handed over by a lane shuffle (pq_simd.rs:349-355).
+    if constexpr (MT == 8 || MT == 16 || MT == 32) {
+        if constexpr (KT > 0 && DS > 0) {
+            if ((size_t)P * D <= (size_t)MT * KT && n <= (uint32_t)(VGPU_BLOCK / 2)) {
+                constexpr int H = MT / 2;                 // codebooks per thread
+                constexpr int CB0 = DS >= 8 ? 4 : 8;
+                constexpr int CB = CB0 < H ? CB0 : H;     // codewords in flight
+                static_assert(H % CB == 0 && H % 4 == 0, "codebook batches");
+                constexpr int HW = H / 4;                 // code words per half row
+                const uint32_t i = (uint32_t)tid >> 1, half = (uint32_t)tid & 1u;
+                const bool act = i < n;
+                const uint64_t v = act ? s.keys[i] : 0ull;
+                const uint32_t pos = (uint32_t)v, p = (uint32_t)(v >> 32);
+                uint32_t cwd[HW];
+#pragma unroll
+                for (int w = 0; w < HW; w++) cwd[w] = 0u;
+                if (act) {
+                    const uint8_t* cp = ix.codes + (size_t)pos * MT + half * H;
+                    if constexpr (HW == 1) cwd[0] = *reinterpret_cast<const uint32_t*>(cp);
+                    else if constexpr (HW == 2) {
+                        const uint2 x = *reinterpret_cast<const uint2*>(cp);
+                        cwd[0] = x.x; cwd[1] = x.y;
+                    } else {
+                        const uint4 x = *reinterpret_cast<const uint4*>(cp);
+                        cwd[0] = x.x; cwd[1] = x.y; cwd[2] = x.z; cwd[3] = x.w;
+                    }
+                }
+                for (int e = tid; e < P * (D / 4); e += VGPU_BLOCK) {  // residual table
+                    const int pp = e / (D / 4), j = 4 * (e % (D / 4));
+                    const float4 c = *reinterpret_cast<const float4*>(ix.centroids + (size_t)s.lid[pp] * D + j);
+                    float* o = s.lut + pp * D + j;
+                    o[0] = __fsub_rn(s.qs[j], c.x);
+                    o[1] = __fsub_rn(s.qs[j + 1], c.y);
+                    o[2] = __fsub_rn(s.qs[j + 2], c.z);
+                    o[3] = __fsub_rn(s.qs[j + 3], c.w);
+                }
+                __syncthreads();
+                float ev[H];
+                const float* rrow = s.lut + (size_t)p * D + half * H * DS;
+#pragma unroll
+                for (int h0 = 0; h0 < H; h0 += CB) {
+                    float wv[CB][DS];
+#pragma unroll
+                    for (int b = 0; b < CB; b++) {
+                        const int h = h0 + b, m = (int)half * H + h;
+                        const uint32_t code = (cwd[h >> 2] >> (8 * (h & 3))) & 0xffu;
+                        load_vec<DS>(ix.codebooks + ((size_t)m * KT + code) * DS, wv[b]);
+                    }
+#pragma unroll
+                    for (int b = 0; b < CB; b++) {
+                        float e = 0.0f;
+#pragma unroll
+                        for (int j = 0; j < DS; j++) {
+                            const float diff = __fsub_rn(rrow[(h0 + b) * DS + j], wv[b][j]);
+                            e = __fadd_rn(e, __fmul_rn(diff, diff));
+                        }
+                        ev[h0 + b] = e;
+                    }
+                }
+                float total_e = 0.0f;  // codebooks 0 .. H - 1 (first thread)
+#pragma unroll
+                for (int h = 0; h < H; h++) total_e = __fadd_rn(total_e, ev[h]);
+#pragma unroll
+                for (int h = 0; h < H; h++)  // then the partner's H .. M - 1
+                    total_e = __fadd_rn(total_e, __uint_as_float(shfl_xor_u32(__float_as_uint(ev[h]), 1)));
+                __syncthreads();  // every key of R read above before any is rewritten
+                if (act && half == 0) s.keys[i] = cand_key(total_e, ix.list_ids[pos]);
+                __syncthreads();
+                goto rescored;
+            }
+        }
+    }
+    {
     // Rescoring chunks of KL entries: their code rows are staged in the table
     // region after the KL x M partial distances, so the codeword loads do not
     // wait on a dependent global load.
@@ -689,6 +767,8 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
         }
         __syncthreads();
     }
+    }
+rescored:
     if (n <= 256) {  // one wave sorts in registers; no block barriers below
         if (tid >= 64) return;
         auto emit = [&](int j, uint64_t key) {
