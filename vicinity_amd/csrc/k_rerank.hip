@@ -77,12 +77,12 @@ void launch_finalize(const uint32_t* vidx, const float* dist, const uint32_t* do
                        dist, doc_ids, nq, kin, k, out_ids, out_dists);
 }
 
-// End of a search chunk, 64 queries per workgroup: map insertion indices to
+// End of a search chunk, FINISH_Q queries per workgroup: map insertion indices to
 // doc ids with (-1, +inf) padding (python.rs:778-785), add the statistics rows
 // into the counters (one atomic per counter per workgroup; counters sit
 // COUNTER_STRIDE words apart), and clear the two flag-list lengths for the
 // next chunk (both lists were consumed by earlier launches).
-#define FINISH_Q 64
+#define FINISH_Q 16
 
 __global__ __launch_bounds__(256) void finish_kernel(
     const uint32_t* __restrict__ vidx, const float* __restrict__ dist,
@@ -92,16 +92,33 @@ __global__ __launch_bounds__(256) void finish_kernel(
     const int tid = threadIdx.x, lane = tid & 63;
     const int q0 = blockIdx.x * FINISH_Q;
     const int nqb = min(FINISH_Q, nq - q0);
-    for (int e = tid; e < nqb * k; e += VGPU_BLOCK) {
-        const int q = q0 + e / k, j = e % k;
-        const uint32_t v = j < kin ? vidx[(size_t)q * kin + j] : 0xffffffffu;
-        const size_t o = (size_t)q * k + j;
-        if (v != 0xffffffffu) {
-            out_ids[o] = (int64_t)(doc_ids ? doc_ids[v] : v);
-            out_dists[o] = dist[(size_t)q * kin + j];
-        } else {
-            out_ids[o] = -1;
-            out_dists[o] = __int_as_float(0x7f800000);
+    const int total = nqb * k;
+    constexpr int U = 4;  // outputs per thread whose loads are in flight together
+    for (int e0 = tid; e0 < total; e0 += U * VGPU_BLOCK) {
+        uint32_t v[U], id[U];
+        float dv[U];
+        size_t src[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int e = e0 + u * VGPU_BLOCK;
+            const int q = q0 + e / k, j = e % k;
+            src[u] = (size_t)q * kin + j;
+            v[u] = e < total && j < kin ? vidx[src[u]] : 0xffffffffu;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const bool ok = v[u] != 0xffffffffu;
+            id[u] = ok && doc_ids ? doc_ids[v[u]] : v[u];
+            dv[u] = ok ? dist[src[u]] : __int_as_float(0x7f800000);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int e = e0 + u * VGPU_BLOCK;
+            if (e < total) {
+                const size_t o = (size_t)(q0 + e / k) * k + e % k;
+                out_ids[o] = v[u] != 0xffffffffu ? (int64_t)id[u] : (int64_t)-1;
+                out_dists[o] = dv[u];
+            }
         }
     }
     if (qstat && tid < 64) {
