@@ -137,7 +137,10 @@ int vgpu_ivfpq_search_batch_device(vgpu_ivfpq *h, const float *d_queries, size_t
                                    size_t dim, size_t k, size_t nprobe, size_t rerank_pool,
                                    int64_t *d_out_ids, float *d_out_dists, void *stream);
 int vgpu_ivfpq_last_stats(const vgpu_ivfpq *h, vgpu_search_stats *out);
-/* Enable per-phase hipEvent timing for later search calls (off by default). */
+/* hipEvent timing of later search calls, read back by vgpu_ivfpq_last_stats:
+ * 0 off (default); 1 every phase (events around each stage, one host wait per
+ * query chunk); 2 the scan kernels only (two events per chunk, read after the
+ * call's final wait; the other phase times read 0). */
 int vgpu_ivfpq_set_profiling(vgpu_ivfpq *h, int enabled);
 
 /* The probed lists of each query in probe order (search.rs:1602-1617),

@@ -27,6 +27,8 @@
 // If the buffer provably holds R (A_k + 2 tau <= thr), R is rescored with the
 // reference's arithmetic and sorted by (distance, insertion index);
 // otherwise the query is flagged and rerun by the EXACT kernel.
+#include <hip/hip_ext.h>
+
 #include "vgpu_device.h"
 #include "vgpu_launch.h"
 
@@ -839,39 +841,44 @@ size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
 }
 
 template <int MT, int KT, int DS>
-static void launch_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
+static void launch_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hipEvent_t t0,
+                        hipEvent_t t1) {
     const int buf = fs8_buf(a.kk);
     size_t off[11];
     const size_t dyn = fs8_layout(ix.d, ix.M, ix.K, a.P, buf, MT > 0 && KT >= 64, off);
     auto k = scan8_fast_kernel<MT, KT, DS>;
     ensure_dyn_lds((const void*)k, dyn);
-    hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), dyn, s, ix, a, buf);
+    if (t0)
+        hipExtLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), (uint32_t)dyn, s, t0, t1, 0u, ix, a, buf);
+    else
+        hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), dyn, s, ix, a, buf);
 }
 
 template <int MT>
-static void launch_fast_m(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
+static void launch_fast_m(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hipEvent_t t0,
+                          hipEvent_t t1) {
     switch (ix.ds) {  // the subvector widths of the benchmark shapes
-        case 2: launch_fast<MT, 256, 2>(ix, a, s); return;
-        case 4: launch_fast<MT, 256, 4>(ix, a, s); return;
-        case 8: launch_fast<MT, 256, 8>(ix, a, s); return;
-        default: launch_fast<MT, 256, 0>(ix, a, s); return;
+        case 2: launch_fast<MT, 256, 2>(ix, a, s, t0, t1); return;
+        case 4: launch_fast<MT, 256, 4>(ix, a, s, t0, t1); return;
+        case 8: launch_fast<MT, 256, 8>(ix, a, s, t0, t1); return;
+        default: launch_fast<MT, 256, 0>(ix, a, s, t0, t1); return;
     }
 }
 
-void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
+void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
     if (a.nq <= 0) return;
     if (ix.K == 256) {
         switch (ix.M) {
-            case 4: launch_fast_m<4>(ix, a, s); return;
-            case 8: launch_fast_m<8>(ix, a, s); return;
-            case 16: launch_fast_m<16>(ix, a, s); return;
-            case 32: launch_fast_m<32>(ix, a, s); return;
-            case 48: launch_fast_m<48>(ix, a, s); return;
-            case 64: launch_fast_m<64>(ix, a, s); return;
+            case 4: launch_fast_m<4>(ix, a, s, t0, t1); return;
+            case 8: launch_fast_m<8>(ix, a, s, t0, t1); return;
+            case 16: launch_fast_m<16>(ix, a, s, t0, t1); return;
+            case 32: launch_fast_m<32>(ix, a, s, t0, t1); return;
+            case 48: launch_fast_m<48>(ix, a, s, t0, t1); return;
+            case 64: launch_fast_m<64>(ix, a, s, t0, t1); return;
             default: break;
         }
     }
-    launch_fast<0, 0, 0>(ix, a, s);
+    launch_fast<0, 0, 0>(ix, a, s, t0, t1);
 }
 
 }  // namespace vgpu

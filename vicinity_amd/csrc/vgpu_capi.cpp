@@ -147,7 +147,8 @@ int vgpu_ivfpq_set_profiling(vgpu_ivfpq* h, int enabled) {
     return guard([&] {
         need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
         std::lock_guard<std::mutex> lk(h->ix->mu);
-        h->ix->profiling = enabled != 0;
+        need(enabled >= 0 && enabled <= 2, VGPU_ERR_INVALID_PARAMETER, "profiling level must be 0, 1 or 2");
+        h->ix->profiling = enabled;
     });
 }
 

@@ -103,6 +103,8 @@ IvfpqIndex::~IvfpqIndex() {
     if (h_scal) (void)hipHostFree(h_scal);
     for (auto& e : ev)
         if (e) (void)hipEventDestroy(e);
+    for (auto& e : sev)
+        if (e) (void)hipEventDestroy(e);
     if (stream) (void)hipStreamDestroy(stream);
 }
 
@@ -546,29 +548,43 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
     uint32_t* cflag_count = reinterpret_cast<uint32_t*>(w_scal.p + kCFlagWord);
     VGPU_HIP(hipMemsetAsync(w_scal.p, 0, kScalWords * sizeof(unsigned long long), s));
     float t[7] = {0, 0, 0, 0, 0, 0, 0};
-    for (size_t q0 = 0; q0 < nq; q0 += chunk) {
+    const bool allp = profiling == 1, scanp = profiling == 2;
+    if (scanp) {
+        const size_t need_ev = 2 * ((nq + chunk - 1) / chunk);
+        while (sev.size() < need_ev) {
+            hipEvent_t e;
+            VGPU_HIP(hipEventCreate(&e));
+            sev.push_back(e);
+        }
+    }
+    size_t ci = 0;  // chunk index
+    for (size_t q0 = 0; q0 < nq; q0 += chunk, ci++) {
         const size_t nc = std::min(chunk, nq - q0);
-        if (profiling) VGPU_HIP(hipEventRecord(ev[0], s));
+        if (allp) VGPU_HIP(hipEventRecord(ev[0], s));
         if (fused) {
             // normalise + two bf16x3 MFMA passes (ms_coarse), exact top-P of the
             // candidates and the rare exact fallback (ms_select)
-            if (profiling) VGPU_HIP(hipEventRecord(ev[1], s));
+            if (allp) VGPU_HIP(hipEventRecord(ev[1], s));
             launch_coarse_fused(d_q + q0 * d, (int)nc, (int)d, dix.cb16, (int)L, dix.cmax, (int)P, 1,
                                 w_qn.p, w_qnorm.p, w_cand.p, w_cand_n.p, s);
-            if (profiling) VGPU_HIP(hipEventRecord(ev[2], s));
+            if (allp) VGPU_HIP(hipEventRecord(ev[2], s));
             launch_coarse_topp(w_cand.p, w_cand_n.p, (int)P, w_qn.p, d_centroids.p, (int)nc, (int)L, (int)d,
                                w_probe.p, w_cflag_list.p, cflag_count, s);
             launch_coarse_exact_flagged(w_qn.p, w_qnorm.p, d_centroids.p, (int)nc, (int)L, (int)d, (int)P,
                                         dix.cmax, w_probe.p, overflow, w_cflag_list.p, cflag_count, s);
         } else {
             launch_normalize(d_q + q0 * d, w_qn.p, w_qnorm.p, (int)nc, (int)d, s);
-            if (profiling) VGPU_HIP(hipEventRecord(ev[1], s));
+            if (allp) VGPU_HIP(hipEventRecord(ev[1], s));
             launch_coarse_dots(w_qn.p, d_centroids.p, w_dots.p, (int)nc, (int)L, (int)d, s);
-            if (profiling) VGPU_HIP(hipEventRecord(ev[2], s));
+            if (allp) VGPU_HIP(hipEventRecord(ev[2], s));
             launch_coarse_select(w_dots.p, w_qn.p, w_qnorm.p, d_centroids.p, (int)nc, (int)L, (int)d,
                                  (int)P, dix.cmax, w_probe.p, overflow, w_cflag_list.p, cflag_count, s);
         }
-        if (profiling) VGPU_HIP(hipEventRecord(ev[3], s));
+        if (allp) VGPU_HIP(hipEventRecord(ev[3], s));
+        // scan-only timing: the FAST kernel's dispatch records the two events
+        // itself; the other scan kernels are bracketed by marker events
+        const bool scan_fast = K != 16 && mode == VGPU_MODE_FAST;
+        if (scanp && !scan_fast) VGPU_HIP(hipEventRecord(sev[2 * ci], s));
         ScanArgs a;
         a.qn = w_qn.p;
         a.qnorm = w_qnorm.p;
@@ -584,12 +600,13 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
         if (K == 16) {
             a.kk = (int)kout;
             launch_fastscan(dix, a, s);
-            if (profiling) VGPU_HIP(hipEventRecord(ev[4], s));
+            if (allp) VGPU_HIP(hipEventRecord(ev[4], s));
+            if (scanp) VGPU_HIP(hipEventRecord(sev[2 * ci + 1], s));
         } else if (mode == VGPU_MODE_FAST) {
             a.kk = fast_keep(kout);
             a.exact = 0;
-            launch_scan8_fast(dix, a, s);
-            if (profiling) VGPU_HIP(hipEventRecord(ev[4], s));
+            launch_scan8_fast(dix, a, s, scanp ? sev[2 * ci] : nullptr, scanp ? sev[2 * ci + 1] : nullptr);
+            if (allp) VGPU_HIP(hipEventRecord(ev[4], s));
             a.kk = (int)kout;
             a.exact = 1;
             a.only_flagged = 1;
@@ -598,9 +615,10 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             a.kk = (int)kout;
             a.exact = 1;
             launch_scan8_exact(dix, a, s);
-            if (profiling) VGPU_HIP(hipEventRecord(ev[4], s));
+            if (allp) VGPU_HIP(hipEventRecord(ev[4], s));
+            if (scanp) VGPU_HIP(hipEventRecord(sev[2 * ci + 1], s));
         }
-        if (profiling) VGPU_HIP(hipEventRecord(ev[5], s));
+        if (allp) VGPU_HIP(hipEventRecord(ev[5], s));
         const uint32_t* vout = w_vidx.p;
         const float* dout = w_dist.p;
         size_t kin = kout;
@@ -610,12 +628,12 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             dout = w_dist2.p;
             kin = k;
         }
-        if (profiling) VGPU_HIP(hipEventRecord(ev[6], s));
+        if (allp) VGPU_HIP(hipEventRecord(ev[6], s));
         launch_finish(vout, dout, d_doc_ids.p, (int)nc, (int)kin, (int)k, d_ids + q0 * k,
                       d_dists + q0 * k, w_qstat.p, counters, flag_count, cflag_count, s);
-        if (profiling) VGPU_HIP(hipEventRecord(ev[7], s));
+        if (allp) VGPU_HIP(hipEventRecord(ev[7], s));
         VGPU_HIP(hipGetLastError());
-        if (profiling) {
+        if (allp) {
             VGPU_HIP(hipEventSynchronize(ev[7]));
             float ms;
             for (int i = 0; i < 7; i++) {
@@ -627,6 +645,13 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
     VGPU_HIP(hipMemcpyAsync(h_scal, w_scal.p, kScalWords * sizeof(unsigned long long),
                             hipMemcpyDeviceToHost, s));
     VGPU_HIP(hipStreamSynchronize(s));
+    if (scanp) {  // the scan kernels of every chunk, read after the final wait
+        for (size_t c = 0; c < ci; c++) {
+            float ms;
+            VGPU_HIP(hipEventElapsedTime(&ms, sev[2 * c], sev[2 * c + 1]));
+            t[3] += ms;
+        }
+    }
     unsigned long long cnt[NUM_SCAN_COUNTERS];
     for (int i = 0; i < NUM_SCAN_COUNTERS; i++) cnt[i] = h_scal[i * COUNTER_STRIDE];
     const unsigned int ovf = reinterpret_cast<const unsigned int*>(h_scal + kOverflowWord)[0] +

@@ -95,7 +95,10 @@ void launch_scan8_exact(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 // the provable candidate set; an unprovable query sets bit 0 of its qstat
 // fallback word.
 size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a);
-void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
+// t0 / t1 (optional): events the kernel's own dispatch records at its start
+// and end (hipExtLaunchKernelGGL), so timing adds no marker packets.
+void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hipEvent_t t0 = nullptr,
+                       hipEvent_t t1 = nullptr);
 
 #define QSTAT_WORDS 4
 // Search statistics: entries scanned, fallbacks, flushes, appends, fallbacks

@@ -66,7 +66,7 @@ struct IvfpqIndex {
     int mode = VGPU_MODE_FAST;
     bool built = false;
     bool has_vectors = true;
-    bool profiling = false;
+    int profiling = 0;  // 0 off, 1 every phase, 2 the scan kernel only
 
     std::vector<float> vectors;     // [n*d] normalised (search.rs:503-508)
     std::vector<uint32_t> doc_ids;  // [n]
@@ -80,6 +80,7 @@ struct IvfpqIndex {
 
     hipStream_t stream = nullptr;
     hipEvent_t ev[8] = {};
+    std::vector<hipEvent_t> sev;  // scan-only timing: two per chunk
     DevBuf<float> d_centroids, d_codebooks, d_bias, d_vectors;
     DevBuf<uint4> d_cb16, w_cb16;  // bf16 hi/lo centroid copies (search index, build workspace)
     DevBuf<uint32_t> w_cand, w_cand_n;  // fused coarse candidates

@@ -162,8 +162,13 @@ class IVFPQIndex:
         m = {"fast": _lib.MODE_FAST, "exact": _lib.MODE_EXACT}[mode]
         _lib.check(self._L.vgpu_ivfpq_set_mode(self._h, m))
 
-    def set_profiling(self, enabled: bool) -> None:
-        _lib.check(self._L.vgpu_ivfpq_set_profiling(self._h, 1 if enabled else 0))
+    def set_profiling(self, enabled) -> None:
+        """False/0 off, True/1 every phase, 2 the scan kernels only (two
+        hipEvents per query chunk, the cheapest timing)."""
+        level = int(enabled)
+        if level not in (0, 1, 2):
+            raise ValueError("profiling level must be 0, 1 or 2")
+        _lib.check(self._L.vgpu_ivfpq_set_profiling(self._h, level))
 
     def compact(self) -> None:
         if not self.is_built:
