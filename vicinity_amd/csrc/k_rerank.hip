@@ -79,58 +79,65 @@ void launch_finalize(const uint32_t* vidx, const float* dist, const uint32_t* do
 
 // End of a search chunk, FINISH_Q queries per workgroup: map insertion indices to
 // doc ids with (-1, +inf) padding (python.rs:778-785), add the statistics rows
-// into the counters (one atomic per counter per workgroup; counters sit
-// COUNTER_STRIDE words apart), and clear the two flag-list lengths for the
-// next chunk (both lists were consumed by earlier launches).
+// into the counters (every FINISH_STATS-th workgroup adds 128 queries' rows,
+// one atomic per counter; counters sit COUNTER_STRIDE words apart), and clear
+// the two flag-list lengths for the next chunk (both lists were consumed by
+// earlier launches).
 #define FINISH_Q 16
+#define FINISH_STATS 8  // workgroups per statistics row block (128 queries)
+static_assert(FINISH_Q * FINISH_STATS == 128, "two queries per lane");
 
 __global__ __launch_bounds__(256) void finish_kernel(
     const uint32_t* __restrict__ vidx, const float* __restrict__ dist,
     const uint32_t* __restrict__ doc_ids, int nq, int kin, int k, int64_t* __restrict__ out_ids,
     float* __restrict__ out_dists, const uint32_t* __restrict__ qstat,
     unsigned long long* __restrict__ counters, uint32_t* flag_count, uint32_t* cflag_count) {
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int q0 = blockIdx.x * FINISH_Q;
     const int nqb = min(FINISH_Q, nq - q0);
-    const int total = nqb * k;
-    constexpr int U = 4;  // outputs per thread whose loads are in flight together
-    for (int e0 = tid; e0 < total; e0 += U * VGPU_BLOCK) {
+    // wave w takes rows w, w + 4, ...; a lane takes columns lane, lane + 64, ...
+    constexpr int U = 8;  // outputs per lane whose loads are in flight together
+    constexpr int RW = FINISH_Q / (VGPU_BLOCK / 64);  // rows per wave
+    for (int c0 = 0; c0 < k; c0 += 64 * (U / RW)) {
         uint32_t v[U], id[U];
         float dv[U];
-        size_t src[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int e = e0 + u * VGPU_BLOCK;
-            const int q = q0 + e / k, j = e % k;
-            src[u] = (size_t)q * kin + j;
-            v[u] = e < total && j < kin ? vidx[src[u]] : 0xffffffffu;
+            const int r = wave + (VGPU_BLOCK / 64) * (u % RW), j = c0 + lane + 64 * (u / RW);
+            v[u] = r < nqb && j < k && j < kin ? vidx[(size_t)(q0 + r) * kin + j] : 0xffffffffu;
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
+            const int r = wave + (VGPU_BLOCK / 64) * (u % RW), j = c0 + lane + 64 * (u / RW);
             const bool ok = v[u] != 0xffffffffu;
             id[u] = ok && doc_ids ? doc_ids[v[u]] : v[u];
-            dv[u] = ok ? dist[src[u]] : __int_as_float(0x7f800000);
+            dv[u] = ok ? dist[(size_t)(q0 + r) * kin + j] : __int_as_float(0x7f800000);
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int e = e0 + u * VGPU_BLOCK;
-            if (e < total) {
-                const size_t o = (size_t)(q0 + e / k) * k + e % k;
+            const int r = wave + (VGPU_BLOCK / 64) * (u % RW), j = c0 + lane + 64 * (u / RW);
+            if (r < nqb && j < k) {
+                const size_t o = (size_t)(q0 + r) * k + j;
                 out_ids[o] = v[u] != 0xffffffffu ? (int64_t)id[u] : (int64_t)-1;
                 out_dists[o] = dv[u];
             }
         }
     }
-    if (qstat && tid < 64) {
+    // statistics: every FINISH_STATS-th workgroup adds 128 queries' rows
+    if (qstat && tid < 64 && blockIdx.x % FINISH_STATS == 0) {
         uint32_t c[NUM_SCAN_COUNTERS] = {0, 0, 0, 0, 0, 0};
-        if (lane < nqb) {
-            const uint32_t* st = qstat + (size_t)(q0 + lane) * QSTAT_WORDS;
-            c[0] = st[0];              // entries scanned
-            c[1] = st[3] & 1u;         // fallbacks
-            c[2] = st[1];              // flushes
-            c[3] = st[2];              // appends
-            c[4] = (st[3] >> 1) & 1u;  // fallbacks from ties
-            c[5] = (st[3] >> 2) & 1u;  // second passes
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int qq = q0 + h * 64 + lane;
+            if (qq < nq) {
+                const uint32_t* st = qstat + (size_t)qq * QSTAT_WORDS;
+                c[0] += st[0];              // entries scanned
+                c[1] += st[3] & 1u;         // fallbacks
+                c[2] += st[1];              // flushes
+                c[3] += st[2];              // appends
+                c[4] += (st[3] >> 1) & 1u;  // fallbacks from ties
+                c[5] += (st[3] >> 2) & 1u;  // second passes
+            }
         }
 #pragma unroll
         for (int i = 0; i < NUM_SCAN_COUNTERS; i++) {
