@@ -119,8 +119,9 @@ __host__ __device__ inline size_t fc_lds_bytes(int d, int DT, int J) {
 // of FC_ST 16-centroid tiles, acc = Q_qb . C_tile^T (16 x 16, bf16x3) and hands
 // it to `epi(acc, col_base, masked)`, col_base the tile's first centroid and
 // masked = the tile may reach past L (only in the last stage).  Stages are
-// double-buffered in LDS with one barrier each; a stage's epilogue runs after
-// the next stage's MFMAs are issued, so the two overlap.  All threads call this.
+// double-buffered in LDS with one barrier each and loaded two stages ahead
+// into registers; a stage's epilogue runs after the next stage's MFMAs are
+// issued, so the two overlap.  All threads call this.
 template <int DT, typename Epi>
 __device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, const u32x4 (&ah)[DT],
                                         const u32x4 (&al)[DT], u32x4* lds, Epi epi) {
@@ -133,63 +134,65 @@ __device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, 
     const int nst = (L + FC_ST * 16 - 1) / (FC_ST * 16);
     // A stage is 2 SC contiguous chunks of Cb (padded to whole stages), copied
     // to LDS unchanged: slot i of thread tid is chunk i * VGPU_BLOCK + tid.
-    u32x4 pre[PER];
     // Buffer loads: per-lane offset in a VGPR, stage and slot offsets in
-    // SGPRs, range-checked against the padded size.
+    // SGPRs.  Only stages below nst are fetched.
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<u32x4*>(Cb), (short)0, nst * 2 * SC * 16, 0x00020000);
     const uint32_t lofs = (uint32_t)tid * 16u;
-#define FC_FETCH(ST)                                                                   \
-    _Pragma("unroll") for (int i = 0; i < PER; i++) pre[i] = __builtin_amdgcn_raw_buffer_load_b128( \
+    // Two register sets: stage st + 1 waits in one while stage st + 2 loads
+    // into the other, so a stage's loads have two stages to arrive.
+    u32x4 pa[PER], pb[PER];
+#define FC_FETCH(SET, ST)                                                              \
+    _Pragma("unroll") for (int i = 0; i < PER; i++) SET[i] = __builtin_amdgcn_raw_buffer_load_b128( \
         rsrc, lofs, (uint32_t)((ST) * 2 * SC * 16 + i * VGPU_BLOCK * 16), 0);
-#define FC_STORE(BUF)                                                                  \
-    _Pragma("unroll") for (int i = 0; i < PER; i++) lds[(size_t)(BUF) * 2 * SC + i * VGPU_BLOCK + tid] = pre[i];
-    FC_FETCH(0)
-    FC_STORE(0)
-    if (nst > 1) { FC_FETCH(1) }
+#define FC_STORE(SET, BUF)                                                             \
+    _Pragma("unroll") for (int i = 0; i < PER; i++) lds[(size_t)(BUF) * 2 * SC + i * VGPU_BLOCK + tid] = SET[i];
     floatx4 prev[FC_SUB];
-    for (int st = 0; st < nst; st++) {
-        // Everyone has finished stage st - 1 (buffer (st + 1) & 1) and stage
-        // st's chunks are visible.
-        __syncthreads();
-        if (st + 1 < nst) {
-            FC_STORE((st + 1) & 1)
-            if (st + 2 < nst) { FC_FETCH(st + 2) }
-        }
-        const u32x4* b = lds + (size_t)(st & 1) * 2 * SC;
-        // FC_SUB independent accumulators, interleaved so consecutive MFMAs
-        // never wait on each other.
-        floatx4 acc[FC_SUB];
-#pragma unroll
-        for (int sub = 0; sub < FC_SUB; sub++) acc[sub] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int t = 0; t < DT; t++) {
-            bf16x8 bh[FC_SUB], bl[FC_SUB];
-#pragma unroll
-            for (int sub = 0; sub < FC_SUB; sub++) {
-                const int o = (((h * FC_SUB + sub) * 2 * DT + t) * 4 + g) * 16 + c;
-                bh[sub] = __builtin_bit_cast(bf16x8, b[o]);
-                bl[sub] = __builtin_bit_cast(bf16x8, b[o + DT * 64]);
-            }
-            const bf16x8 a_h = __builtin_bit_cast(bf16x8, ah[t]);
-            const bf16x8 a_l = __builtin_bit_cast(bf16x8, al[t]);
-#pragma unroll
-            for (int sub = 0; sub < FC_SUB; sub++)
-                acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bl[sub], acc[sub], 0, 0, 0);
-#pragma unroll
-            for (int sub = 0; sub < FC_SUB; sub++)
-                acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_l, bh[sub], acc[sub], 0, 0, 0);
-#pragma unroll
-            for (int sub = 0; sub < FC_SUB; sub++)
-                acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bh[sub], acc[sub], 0, 0, 0);
-        }
-        if (st > 0) {  // stage st - 1 < nst - 1 is whole
-#pragma unroll
-            for (int sub = 0; sub < FC_SUB; sub++) epi(prev[sub], ((st - 1) * FC_ST + h * FC_SUB + sub) * 16, false);
-        }
-#pragma unroll
-        for (int sub = 0; sub < FC_SUB; sub++) prev[sub] = acc[sub];
+    // Stage ST: everyone has finished stage ST - 1 (buffer (ST + 1) & 1) and
+    // stage ST's chunks are visible; SET holds stage ST + 1, then ST + 3.
+#define FC_STEP(ST, SET)                                                               \
+    {                                                                                  \
+        const int st_ = (ST);                                                          \
+        __syncthreads();                                                               \
+        if (st_ + 1 < nst) {                                                           \
+            FC_STORE(SET, (st_ + 1) & 1)                                               \
+            if (st_ + 3 < nst) { FC_FETCH(SET, st_ + 3) }                              \
+        }                                                                              \
+        const u32x4* b = lds + (size_t)(st_ & 1) * 2 * SC;                             \
+        floatx4 acc[FC_SUB];                                                           \
+        _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++) acc[sub] = floatx4{0.f, 0.f, 0.f, 0.f}; \
+        _Pragma("unroll") for (int t = 0; t < DT; t++) {                               \
+            bf16x8 bh[FC_SUB], bl[FC_SUB];                                             \
+            _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++) {                 \
+                const int o = (((h * FC_SUB + sub) * 2 * DT + t) * 4 + g) * 16 + c;    \
+                bh[sub] = __builtin_bit_cast(bf16x8, b[o]);                            \
+                bl[sub] = __builtin_bit_cast(bf16x8, b[o + DT * 64]);                  \
+            }                                                                          \
+            const bf16x8 a_h = __builtin_bit_cast(bf16x8, ah[t]);                      \
+            const bf16x8 a_l = __builtin_bit_cast(bf16x8, al[t]);                      \
+            _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++)                   \
+                acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bl[sub], acc[sub], 0, 0, 0); \
+            _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++)                   \
+                acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_l, bh[sub], acc[sub], 0, 0, 0); \
+            _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++)                   \
+                acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bh[sub], acc[sub], 0, 0, 0); \
+        }                                                                              \
+        if (st_ > 0) { /* stage st_ - 1 < nst - 1 is whole */                          \
+            _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++)                   \
+                epi(prev[sub], ((st_ - 1) * FC_ST + h * FC_SUB + sub) * 16, false);    \
+        }                                                                              \
+        _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++) prev[sub] = acc[sub]; \
     }
+    FC_FETCH(pa, 0)
+    FC_STORE(pa, 0)
+    if (nst > 1) { FC_FETCH(pa, 1) }
+    if (nst > 2) { FC_FETCH(pb, 2) }
+    for (int st = 0; st < nst; st += 2) {
+        FC_STEP(st, pa)
+        if (st + 1 >= nst) break;
+        FC_STEP(st + 1, pb)
+    }
+#undef FC_STEP
     const bool masked = nst * FC_ST * 16 > L;
 #pragma unroll
     for (int sub = 0; sub < FC_SUB; sub++) epi(prev[sub], ((nst - 1) * FC_ST + h * FC_SUB + sub) * 16, masked);
