@@ -76,7 +76,20 @@ def main():
     ap.add_argument("--train-sample", type=int, default=262_144)
     ap.add_argument("--kmeans-iters", type=int, default=25)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only run three 256 MiB device-to-device copies (the reference "
+                         "kernel for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
+    if args.calib_copy:
+        import torch
+
+        a = torch.ones(64 << 20, device="cuda:0")  # 256 MiB of float32
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"three copies of {a.numel() * 4} bytes")
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the index and the "
               "query batch fit one MI355X; multi-GPU query/list sharding is not built.",
