@@ -108,6 +108,36 @@ void launch_bias(const DevIndex& ix, float* bias, hipStream_t s) {
     hipLaunchKernelGGL(bias_kernel, dim3((ix.n + 255) / 256), dim3(256), 0, s, ix, bias);
 }
 
+// One workgroup per list, one thread per 4-byte word of the list's blocks.
+__global__ void tblocks_kernel(DevIndex ix, uint8_t* __restrict__ out) {
+    const int l = blockIdx.x;
+    const uint32_t beg = ix.offsets[l], len = ix.offsets[l + 1] - beg;
+    const uint32_t b0 = ix.tblk_off[l], nb = ix.tblk_off[l + 1] - b0;
+    const uint32_t M = (uint32_t)ix.M, blk = (uint32_t)TBLK_BYTES(M), cb = 16u * M;
+    uint32_t* o = reinterpret_cast<uint32_t*>(out + (size_t)b0 * blk);
+    for (uint32_t w = threadIdx.x; w < nb * blk / 4u; w += blockDim.x) {
+        const uint32_t b = w / (blk / 4u), within = (w % (blk / 4u)) * 4u;
+        uint32_t word = 0u;
+        if (within < cb) {
+            const uint32_t m = within / 16u;
+            for (uint32_t i = 0; i < 4u; i++) {
+                const uint32_t j = within % 16u + i, e = b * 16u + (j ^ (m & 15u));
+                const uint32_t c = e < len ? ix.codes[(size_t)(beg + e) * M + m] : 0u;
+                word |= c << (8u * i);
+            }
+        } else {
+            const uint32_t e = b * 16u + (within - cb) / 4u;
+            word = e < len ? __float_as_uint(ix.bias[beg + e]) : 0u;
+        }
+        o[w] = word;
+    }
+}
+
+void launch_tblocks(const DevIndex& ix, uint8_t* tblocks, hipStream_t s) {
+    if (ix.L <= 0) return;
+    hipLaunchKernelGGL(tblocks_kernel, dim3(ix.L), dim3(256), 0, s, ix, tblocks);
+}
+
 // One workgroup per list; lists shorter than 16 entries have no blocks
 // (they take the exact float path, search.rs:1355-1375).
 __global__ void pack4_kernel(DevIndex ix, uint8_t* __restrict__ packed) {

@@ -16,17 +16,28 @@
 // distance a is within tau of the reference's float32 distance e
 // (fast_tau, below).
 //
-// Selection.  Entries with fkey(a) <= thr are appended to an LDS buffer;
-// when the buffer fills, a block radix select finds the keep-th smallest key
-// T and the buffer is compacted to the entries <= T, which become the new
-// threshold.  The buffer therefore always holds every scanned entry with
-// key <= thr.  At the end, with A_k the k-th smallest approximate distance,
-// the reference's top-k lies inside R = {a <= A_k + 2 tau}: the k entries with
+// Selection.  Each wave keeps its own candidates in its own LDS region:
+// entries with fkey(a) <= F (the wave's filter) are appended; when the region
+// fills, the wave finds the keep-th smallest key T of its region by ballot
+// counts and compacts it to the keys <= T, which become its threshold.  A
+// wave's region therefore always holds every entry it scanned with key <= F.
+// No barrier is needed until the end of the scan.  T also bounds the query's
+// final A_k from above (keep >= k), so every wave may drop entries above
+// T + 2 tau: the waves share the smallest such bound.
+// At the end, with A_k the k-th smallest approximate distance, the
+// reference's top-k lies inside R = {a <= A_k + 2 tau}: the k entries with
 // the smallest a have e <= A_k + tau, so the k-th smallest e is at most
 // A_k + tau, and any entry of the exact top-k has a <= e + tau <= A_k + 2 tau.
-// If the buffer provably holds R (A_k + 2 tau <= thr), R is rescored with the
-// reference's arithmetic and sorted by (distance, insertion index);
-// otherwise the query is flagged and rerun by the EXACT kernel.
+// If the merged regions provably hold R (A_k + 2 tau <= every wave's filter),
+// R is rescored with the reference's arithmetic and sorted by (distance,
+// insertion index); otherwise a second pass adds the missing keys, and a
+// query that still cannot be proved is flagged and rerun by the EXACT kernel.
+//
+// Layouts.  With codebook_size 256 and 16, 32 or 48 codebooks the lists are
+// read from transposed 16-entry blocks (see DevIndex::tblocks), the table is
+// stored code-major so that the 16 lanes of a row read 16 different banks,
+// and a row's 16 lanes exchange partial sums; otherwise one lane scores one
+// list-major code row.
 #include <hip/hip_ext.h>
 
 #include "vgpu_device.h"
@@ -125,19 +136,26 @@ struct FastLds {
     uint32_t* llen;  // [P]
     uint32_t* pref;  // [P + 1]
     float* term0;    // [P] ||q - c||^2
-    uint2* bt;       // [P] (lbeg - pref as u32, bits of term0): one read per entry
+    // [P] per probed slot, one read per entry: x = lbeg - pref (u32), y = bits
+    // of term0; transposed blocks: z = 16 * first block - pref (u32),
+    // w = pref + llen (end of the slot's entries)
+    uint4* bt;
+    uint32_t* tbo;   // [P] first transposed block of each probed list
     RadixScratch* rs;
-    uint32_t* misc;  // [0] count [1] thr [2] lost ties [3..4] flush flags by round parity
-                     // [5] entries evicted by flushes [6] flushes
+    uint32_t* misc;  // [0] count (merged buffer) [2] lost ties [3..4] second-pass flags by
+                     // round parity [5] entries evicted by flushes [6] flushes [7] list
+                     // entries probed [8] shared bound on R [9] bits of max ||q - c||^2
+                     // [16 + w] wave w's kept count [20 + w] wave w's filter
 };
 
 __host__ __device__ inline size_t fs8_align(size_t x) { return (x + 15) & ~(size_t)15; }
 
+// Key buffer: one region per wave, a power of two >= keep + 64 (room for a
+// round of appends above the kept keys).
 __host__ __device__ inline int fs8_buf(int keep) {
-    int need = keep + FS_ROUND;
     int b = 1;
-    while (b < need) b <<= 1;
-    return b;
+    while (b < keep + 64) b <<= 1;
+    return b * (VGPU_BLOCK / 64);
 }
 
 // Dynamic LDS layout; the table region is omitted when the kernel holds the
@@ -151,18 +169,28 @@ __host__ __device__ inline size_t fs8_layout(int d, int M, int K, int P, int buf
     off[2] = o; o = fs8_align(o + (size_t)d * 4);          // qs
     off[3] = o; o = fs8_align(o + (size_t)P * 4);          // lid
     off[4] = o; o = fs8_align(o + (size_t)P * 4);          // lbeg
-    off[5] = o; o = fs8_align(o + (size_t)P * 4);          // llen
     off[6] = o; o = fs8_align(o + (size_t)(P + 1) * 4);    // pref
-    off[7] = o; o = fs8_align(o + (size_t)P * 4);          // term0
     off[8] = o; o = fs8_align(o + sizeof(RadixScratch));   // radix scratch
-    off[9] = o; o = fs8_align(o + 8 * 4);                  // misc
-    off[10] = o; o = fs8_align(o + (size_t)P * 8);         // bt
+    off[9] = o; o = fs8_align(o + 32 * 4);                 // misc
+    off[10] = o; o = fs8_align(o + (size_t)P * 16);        // bt
+    // llen, term0 and tbo are read only before the scan: they share the key
+    // buffer when they fit in it
+    const size_t pa = fs8_align((size_t)P * 4);
+    if (3 * pa <= (size_t)buf * 8) {
+        off[5] = off[1];
+        off[7] = off[1] + pa;
+        off[11] = off[1] + 2 * pa;
+    } else {
+        off[5] = o; o += pa;
+        off[7] = o; o += pa;
+        off[11] = o; o += pa;
+    }
     return o;
 }
 
 __device__ inline FastLds fs8_carve(char* smem, float* static_lut, int d, int M, int K, int P,
                                     int buf) {
-    size_t off[11];
+    size_t off[12];
     fs8_layout(d, M, K, P, buf, static_lut != nullptr, off);
     FastLds s;
     s.lut = static_lut ? static_lut : (float*)(smem + off[0]);
@@ -175,7 +203,8 @@ __device__ inline FastLds fs8_carve(char* smem, float* static_lut, int d, int M,
     s.term0 = (float*)(smem + off[7]);
     s.rs = (RadixScratch*)(smem + off[8]);
     s.misc = (uint32_t*)(smem + off[9]);
-    s.bt = (uint2*)(smem + off[10]);
+    s.bt = (uint4*)(smem + off[10]);
+    s.tbo = (uint32_t*)(smem + off[11]);
     return s;
 }
 
@@ -285,32 +314,6 @@ __device__ uint32_t fs8_select_upper(FastLds& s, uint32_t n, uint32_t rank, uint
     return base | (b << shift) | low;
 }
 
-// Buffer full: keep the `keep` smallest keys (plus the rest of their
-// histogram bin); at most `cap` survive, otherwise the query is marked failed.
-// Clears the flag of `parity`.
-__device__ inline void fs8_flush(FastLds& s, int keep, uint32_t cap, int parity) {
-    __syncthreads();
-    const uint32_t n = s.misc[0];
-    if (threadIdx.x == 0) s.misc[3 + parity] = 0u;
-    if (n <= (uint32_t)keep) {
-        __syncthreads();
-        return;
-    }
-    const uint32_t T = fs8_select_upper(s, n, (uint32_t)(keep - 1), cap);
-    const uint32_t kept = fs8_compact(s, n, T, false, 0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        if (kept > cap) {
-            s.misc[0] = cap;
-            s.misc[2] = 1u;
-        }
-        s.misc[1] = T;
-        s.misc[5] += n - (kept < cap ? kept : cap);  // entries evicted
-        s.misc[6] += 1u;
-    }
-    __syncthreads();
-}
-
 // Per-thread state of the entries one thread handles in one round.  The
 // loads are unconditional (a slot past the end reads position 0, which exists
 // whenever anything is scanned) so the compiler can wait for one round's
@@ -324,29 +327,65 @@ struct RoundRegs {
     uint32_t t[FS_U];  // index in the concatenated probed lists; 0xffffffff = no entry
 };
 
-// Entry t = rbase + u * VGPU_BLOCK + tid.  Each wave's 64 entries of a slot
-// are consecutive, so the wave keeps one uniform cursor `cw` (the probed list
-// holding the start of its next window; windows only move forward) and a lane
-// finds its list by counting the list starts inside the window (usually none
-// or one).  Empty lists repeat a start and are counted over.
+// Slot records of the probed lists held in lane registers when P <= 64:
+// lane p holds pref[p] (0xffffffff for p >= P) and bt[p].
+struct SlotRegs {
+    uint32_t pref;
+    uint4 bt;
+};
+
+__device__ __forceinline__ uint4 readlane4(const uint4& v, int lane) {
+    return make_uint4(__builtin_amdgcn_readlane(v.x, lane), __builtin_amdgcn_readlane(v.y, lane),
+                      __builtin_amdgcn_readlane(v.z, lane), __builtin_amdgcn_readlane(v.w, lane));
+}
+
+// Record of the probed slot holding index x of the window [wb, wb + 64): the
+// last slot p with pref[p] <= x (empty lists repeat a start and are passed
+// over).  With P <= 64 it comes from the lane registers: the slot of the
+// window start is a ballot count, then each list start inside the window
+// (usually none or one) is read out and the lanes at or past it switch to its
+// record.  Otherwise the wave keeps a cursor cw over the LDS prefix sums
+// (windows only move forward) and counts the starts inside the window.
+__device__ __forceinline__ uint4 slot_record(const FastLds& s, const SlotRegs& r, int P, uint32_t wb,
+                                             uint32_t x, int& cw) {
+    if (P <= 64) {
+        const int c = (int)__popcll(__ballot(r.pref <= wb)) - 1;
+        uint4 e = readlane4(r.bt, c);
+        uint64_t inwin = __ballot(r.pref > wb && r.pref < wb + 64u);
+        while (inwin) {
+            const int p = (int)__builtin_ctzll(inwin);
+            inwin &= inwin - 1;
+            const uint32_t b = __builtin_amdgcn_readlane(r.pref, p);
+            const uint4 f = readlane4(r.bt, p);
+            if (x >= b) e = f;
+        }
+        return e;
+    }
+    while (cw + 1 < P && __builtin_amdgcn_readfirstlane(s.pref[cw + 1]) <= wb) cw++;
+    int lst = cw;
+    for (int j = cw + 1; j < P; j++) {
+        const uint32_t b = __builtin_amdgcn_readfirstlane(s.pref[j]);
+        if (b >= wb + 64u) break;
+        lst += x >= b ? 1 : 0;
+    }
+    return s.bt[lst];
+}
+
+// Entry t = rbase + wave * 64 + lane: the waves take interleaved windows of
+// 64 consecutive entries.
 template <int MT>
-__device__ __forceinline__ void fs8_fetch(const DevIndex& ix, const FastLds& s, uint32_t rbase,
-                                          uint32_t total, int P, int& cw, RoundRegs<MT>& g) {
+__device__ __forceinline__ void fs8_fetch(const DevIndex& ix, const FastLds& s, const SlotRegs& sr,
+                                          uint32_t rbase, uint32_t total, int P, int& cw,
+                                          RoundRegs<MT>& g) {
+    static_assert(FS_U == 1, "one window per wave and round");
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-#pragma unroll
-    for (int u = 0; u < FS_U; u++) {
-        const uint32_t wb = rbase + (uint32_t)u * VGPU_BLOCK + wave * 64u;  // window start
+    {
+        constexpr int u = 0;
+        const uint32_t wb = rbase + wave * 64u;  // window start
         const uint32_t t = wb + lane;
         const bool valid = t < total;
-        while (cw + 1 < P && __builtin_amdgcn_readfirstlane(s.pref[cw + 1]) <= wb) cw++;
-        int lst = cw;
-        for (int j = cw + 1; j < P; j++) {
-            const uint32_t b = __builtin_amdgcn_readfirstlane(s.pref[j]);
-            if (b >= wb + 64u) break;
-            lst += t >= b ? 1 : 0;
-        }
-        const uint2 e = s.bt[lst];
+        const uint4 e = slot_record(s, sr, P, wb, t, cw);
         const uint32_t pos = valid ? e.x + t : 0u;
         g.pos[u] = pos;
         g.t[u] = valid ? t : 0xffffffffu;
@@ -356,53 +395,224 @@ __device__ __forceinline__ void fs8_fetch(const DevIndex& ix, const FastLds& s, 
     }
 }
 
-// Score one round of entries and append those with fkey(a) <= thr, with one
-// LDS atomic per wave.  A wave whose appends took the buffer past `cap`
-// raises flag misc[3 + parity]: the final count is the largest count any wave
-// saw, so the flag is raised exactly when the buffer needs a flush.  The two
-// parities alternate between rounds, and a raised flag is cleared inside the
-// flush, so a flag is never written while another wave may still read it.
-// Every thread of the block calls this (all lanes active).  The second pass
-// (RETRY) appends only keys in (lo, thr]: the buffer already holds every key
-// <= lo.
-template <int MT, int KT, bool RETRY>
-__device__ __forceinline__ void fs8_consume(const DevIndex& ix, FastLds& s, const float* lut_static,
-                                            const RoundRegs<MT>& g, uint32_t thr, uint32_t lo,
-                                            uint32_t cap, int parity) {
-    const int lane = threadIdx.x & 63;
-    bool take[FS_U];
-    uint32_t fk[FS_U], before[FS_U];
-    uint64_t mask[FS_U];
-    uint32_t tot = 0;
+// Transposed blocks: the probed lists are concatenated in whole 16-entry
+// blocks (t runs over the padded sequence, pref holds padded starts).  A
+// wave's window of 64 entries is four blocks, one per row of 16 lanes; lane m
+// of a row loads the 16 codes of codebooks m, m + 16, ... of its block (code j
+// of entry j ^ m) and the b(x) of the block's entry m, which is the entry it
+// ends up scoring.  Rows past the end read block 0 (it exists whenever
+// anything is scanned).
+template <int MT>
+__device__ __forceinline__ void fs8t_fetch(const DevIndex& ix, const FastLds& s, const SlotRegs& sr,
+                                           uint32_t rbase, uint32_t total, int P, int& cw,
+                                           RoundRegs<MT>& g) {
+    static_assert(FS_U == 1 && MT % 16 == 0, "one window per wave and round");
+    const uint32_t lane = threadIdx.x & 63u, m = lane & 15u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t wb = rbase + wave * 64u;  // window start
+    const uint32_t tb = wb + (lane & 48u);   // the row's block start
+    const uint32_t t = tb + m;
+    const uint4 e = slot_record(s, sr, P, wb, tb, cw);
+    const uint32_t blk = tb < total ? (e.z + tb) >> 4 : 0u;
+    const uint8_t* bp = ix.tblocks + (size_t)blk * TBLK_BYTES(MT);
 #pragma unroll
-    for (int u = 0; u < FS_U; u++) {
-        const bool ok = g.t[u] != 0xffffffffu;
-        float dist;
-        if constexpr (MT > 0 && KT > 0) {
-            dist = (g.t0[u] + g.bias[u]) + row_sum<MT, KT>(g.row[u], lut_static);
-        } else {
-            dist = (g.t0[u] + g.bias[u]) +
-                   row_sum_generic(ix.codes + (size_t)g.pos[u] * ix.M, s.lut, ix.M, ix.K);
-        }
-        fk[u] = fkey(dist);
-        take[u] = ok && fk[u] <= thr && (!RETRY || fk[u] > lo);
-        mask[u] = __ballot(take[u]);
-        before[u] = tot;
-        tot += (uint32_t)__popcll(mask[u]);
+    for (int gi = 0; gi < MT / 16; gi++) {
+        const uint4 x = *reinterpret_cast<const uint4*>(bp + gi * 256 + m * 16u);
+        g.row[0].w[4 * gi] = x.x;
+        g.row[0].w[4 * gi + 1] = x.y;
+        g.row[0].w[4 * gi + 2] = x.z;
+        g.row[0].w[4 * gi + 3] = x.w;
     }
+    g.bias[0] = *reinterpret_cast<const float*>(bp + 16 * MT + m * 4u);
+    g.t0[0] = __uint_as_float(e.y);
+    g.t[0] = t < e.w ? t : 0xffffffffu;
+}
+
+// a + DPP-moved b (row-local patterns, every source lane active, so no lane
+// takes the bound_ctrl zero; the move folds into the add).
+template <int CTRL>
+__device__ __forceinline__ float add_dpp(float a, float b) {
+    return a + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(b), CTRL, 0xF, 0xF, true));
+}
+
+// Transposed table: T2[m][c] of codebook m = 16 gi + r lives at float
+// ((gi * 256 + c) * NC + copy) * 16 + r, in NC copies; the lanes of row w read
+// copy w % NC, so a half wave (two rows) reads 32 distinct banks when NC = 2.
+// `lutl` is the table plus the lane's (copy * 16 + m).  Lane m's terms v[j]
+// belong to entry j ^ m of its row; four exchange stages with the lanes m ^ 1,
+// m ^ 2, m ^ 7 and m ^ 8 (each halving the registers still needed) leave the
+// sum of entry m in v[0].  Every lane of the wave must be active.
+template <int MT, int NC>
+__device__ __forceinline__ float trow_sum(const CodeRow<MT>& r, const float* __restrict__ lutl) {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+#pragma unroll
+        for (int gi = 0; gi < MT / 16; gi++) {
+            const uint32_t c = (r.w[4 * gi + (j >> 2)] >> (8 * (j & 3))) & 0xffu;
+            const float x = lutl[(gi * 256 + (int)c) * NC * 16];
+            v[j] = gi == 0 ? x : v[j] + x;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; j++)  // keep 0 2 5 7 8 10 13 15 (partner m ^ 1)
+        if (j == 0 || j == 2 || j == 5 || j == 7 || j == 8 || j == 10 || j == 13 || j == 15)
+            v[j] = add_dpp<0xB1>(v[j], v[j ^ 1]);
+    v[0] = add_dpp<0x4E>(v[0], v[2]);   // partner m ^ 2
+    v[7] = add_dpp<0x4E>(v[7], v[5]);
+    v[8] = add_dpp<0x4E>(v[8], v[10]);
+    v[15] = add_dpp<0x4E>(v[15], v[13]);
+    v[0] = add_dpp<0x141>(v[0], v[7]);  // partner m ^ 7 (row_half_mirror)
+    v[8] = add_dpp<0x141>(v[8], v[15]);
+    return add_dpp<0x128>(v[0], v[8]);  // partner m ^ 8 (row_ror:8)
+}
+
+// Approximate distance a of the entry a lane holds in g (every lane of the
+// wave must take part: the transposed sum exchanges values between lanes).
+template <int MT, int KT, int NC>
+__device__ __forceinline__ float entry_dist(const DevIndex& ix, const FastLds& s, const float* lut_static,
+                                            const RoundRegs<MT>& g) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (NC > 0) {
+        const float* lutl = lut_static + (((lane >> 4) & (NC - 1)) * 16 + (lane & 15));
+        return (g.t0[0] + g.bias[0]) + trow_sum<MT, NC>(g.row[0], lutl);
+    } else if constexpr (MT > 0 && KT > 0) {
+        return (g.t0[0] + g.bias[0]) + row_sum<MT, KT>(g.row[0], lut_static);
+    } else {
+        return (g.t0[0] + g.bias[0]) + row_sum_generic(ix.codes + (size_t)g.pos[0] * ix.M, s.lut, ix.M, ix.K);
+    }
+}
+
+// Main pass: append the entries with fkey(a) <= F to the wave's own region
+// `reg` (no atomics: the count is the wave's own).  The region has room for
+// a round (cnt <= capacity - 64 on entry).
+template <int MT, int KT, int NC>
+__device__ __forceinline__ void fs8w_consume(const DevIndex& ix, const FastLds& s, const float* lut_static,
+                                             const RoundRegs<MT>& g, uint32_t F, uint64_t* reg,
+                                             uint32_t& cnt) {
+    const uint32_t fk = fkey(entry_dist<MT, KT, NC>(ix, s, lut_static, g));
+    const bool take = g.t[0] != 0xffffffffu && fk <= F;
+    const uint64_t mask = __ballot(take);
+    if (mask == 0) return;  // wave-uniform
+    if (take) {
+        const uint32_t below =
+            __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+        reg[cnt + below] = ((uint64_t)fk << 32) | g.t[0];
+    }
+    cnt += (uint32_t)__popcll(mask);
+}
+
+// Second pass (after the regions are merged into one buffer): append the keys
+// in (lo, hi] with one LDS atomic per wave.  A wave whose appends took the
+// buffer past `cap` raises flag misc[3 + parity] (the parities alternate
+// between rounds; the caller reads the flag after a barrier).
+template <int MT, int KT, int NC>
+__device__ __forceinline__ void fs8_consume_retry(const DevIndex& ix, FastLds& s, const float* lut_static,
+                                                  const RoundRegs<MT>& g, uint32_t hi, uint32_t lo,
+                                                  uint32_t cap, int parity) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t fk = fkey(entry_dist<MT, KT, NC>(ix, s, lut_static, g));
+    const bool take = g.t[0] != 0xffffffffu && fk <= hi && fk > lo;
+    const uint64_t mask = __ballot(take);
+    const uint32_t tot = (uint32_t)__popcll(mask);
     if (tot == 0) return;  // wave-uniform
     uint32_t base = 0;
     if (lane == 0) base = atomicAdd(&s.misc[0], tot);
     base = __builtin_amdgcn_readfirstlane(base);
-#pragma unroll
-    for (int u = 0; u < FS_U; u++) {
-        if (take[u]) {
-            const uint32_t below = __builtin_amdgcn_mbcnt_hi(
-                (uint32_t)(mask[u] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask[u], 0u));
-            s.keys[base + before[u] + below] = ((uint64_t)fk[u] << 32) | g.t[u];
-        }
+    if (take) {
+        const uint32_t below =
+            __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+        s.keys[base + below] = ((uint64_t)fk << 32) | g.t[0];
     }
     if (base + tot > cap && lane == 0) s.misc[3 + parity] = 1u;
+}
+
+// Wave-level flush of the wave's region reg[0, cnt): T = the rank-th smallest
+// high word (0-based), found bit by bit from the top with ballot counts; the
+// search stops early once every key up to the top of T's current prefix
+// range fits `capw` (T is then that upper end).  The keys <= T are compacted
+// in place (each chunk of 64 is read before any of its slots is rewritten).
+// Returns T; cnt becomes the kept count, or capw with *lost set when more
+// than capw keys are <= T (ties).
+__device__ uint32_t fs8w_flush(uint64_t* reg, uint32_t& cnt, uint32_t rank, uint32_t capw, bool* lost) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t idx = (uint32_t)i * 64u + lane;
+        h[i] = idx < cnt ? (uint32_t)(reg[idx] >> 32) : 0xffffffffu;
+    }
+    // keys (high words) < v, counting the ones past the first 256 from LDS
+    auto below = [&](uint32_t v) -> uint32_t {
+        uint32_t c = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) c += (uint32_t)__popcll(__ballot(h[i] < v));
+        for (uint32_t i0 = 256; i0 < cnt; i0 += 64) {
+            const uint32_t idx = i0 + lane;
+            const uint32_t x = idx < cnt ? (uint32_t)(reg[idx] >> 32) : 0xffffffffu;
+            c += (uint32_t)__popcll(__ballot(x < v));
+        }
+        return c;
+    };
+    uint32_t T = 0;
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t cand = T | (1u << b);
+        if (below(cand) <= rank) T = cand;
+        if ((b & 3) == 0 && b > 0) {  // T's prefix is final down to bit b
+            const uint32_t top = T | ((1u << b) - 1u);
+            if (top != 0xffffffffu && below(top + 1u) <= capw) {
+                T = top;
+                break;
+            }
+        }
+    }
+    uint32_t kept = 0;
+    for (uint32_t i0 = 0; i0 < cnt; i0 += 64) {
+        const uint32_t idx = i0 + lane;
+        const uint64_t v = idx < cnt ? reg[idx] : ~0ull;
+        const bool take = idx < cnt && (uint32_t)(v >> 32) <= T;
+        const uint64_t mask = __ballot(take);
+        if (take) {
+            const uint32_t at = kept + __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+            if (at < capw) reg[at] = v;
+        }
+        kept += (uint32_t)__popcll(mask);
+    }
+    if (kept > capw) {
+        *lost = true;
+        kept = capw;
+    }
+    cnt = kept;
+    return T;
+}
+
+// Dense index i of the merged regions -> LDS slot (region w holds cw[w]
+// keys at w * BW).
+__device__ __forceinline__ uint32_t region_slot(uint32_t i, const uint32_t* off, uint32_t BW) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int v = 1; v < VGPU_BLOCK / 64; v++) w += i >= off[v] ? 1u : 0u;
+    return w * BW + (i - off[w]);
+}
+
+// Merge the waves' regions into keys[0, n) (dense order, chunk by chunk: a
+// slot is rewritten only after every key stored at or before it was read,
+// because region w starts at w * BW >= the keys of the regions before it).
+__device__ inline uint32_t fs8w_merge(FastLds& s, const uint32_t* cnts, uint32_t BW) {
+    uint32_t off[VGPU_BLOCK / 64 + 1];
+    off[0] = 0;
+#pragma unroll
+    for (int w = 0; w < VGPU_BLOCK / 64; w++) off[w + 1] = off[w] + cnts[w];
+    const uint32_t n = off[VGPU_BLOCK / 64];
+    for (uint32_t c0 = 0; c0 < n; c0 += VGPU_BLOCK) {
+        const uint32_t i = c0 + threadIdx.x;
+        const uint64_t v = i < n ? s.keys[region_slot(i, off, BW)] : 0ull;
+        __syncthreads();
+        if (i < n) s.keys[i] = v;
+        __syncthreads();
+    }
+    return n;
 }
 
 // DS consecutive floats into registers (vector loads when aligned).
@@ -455,12 +665,16 @@ __device__ __forceinline__ float exact_sub_distance(const float* qm, const float
 }
 
 // MT, KT, DS: compile-time codebooks, codebook size and subvector dimension
-// (0 = read from the index at run time).
-template <int MT, int KT, int DS>
+// (0 = read from the index at run time).  NC > 0: the lists are read from the
+// transposed blocks, with NC copies of the table.
+template <int MT, int KT, int DS, int NC>
 __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a, int buf) {
+    constexpr bool TR = NC > 0;
+    static_assert(!TR || (MT % 16 == 0 && KT == 256 && DS > 0), "transposed blocks");
     constexpr bool kStatic = MT > 0 && KT >= 64;
     constexpr int D = MT * DS;  // compile-time dimension when > 0
-    __shared__ __align__(16) float slut[kStatic ? MT * KT : 1];
+    constexpr int LUTF = kStatic ? MT * KT * (TR ? NC : 1) : 1;  // static table floats
+    __shared__ __align__(16) float slut[LUTF];
     extern __shared__ __align__(16) char smem[];
     const int q = blockIdx.x;
     if (q >= a.nq) return;
@@ -478,23 +692,102 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
         s.lid[p] = ok ? l : 0u;
         s.lbeg[p] = b;
         s.llen[p] = ok ? ix.offsets[l + 1] - b : 0u;
+        if constexpr (TR) s.tbo[p] = ok ? ix.tblk_off[l] : 0u;
     }
-    if (tid < 8) s.misc[tid] = tid == 1 ? 0xffffffffu : 0u;  // count 0, thr +inf, flags 0
+    if (tid < 32) s.misc[tid] = tid == 8 ? 0xffffffffu : 0u;  // counts 0, no bound yet
+    if constexpr (TR) {
+        // T2[m][k] = -2 q_m . cw_mk (ranking only: FMA allowed), built before
+        // the first barrier from the query in global memory, so its codeword
+        // loads overlap the probed-list loads.  Every load instruction reads
+        // one whole 64-byte line of each of 16 codebooks: lane (m16, j) =
+        // (lane / 4, lane % 4) reads bytes 16 j .. 16 j + 15 of line `sp` of
+        // codebook 16 gi + m16, which hold CPS = 16 / DS codewords.  With
+        // DS = 8 a codeword spans two lanes, whose partial dot products meet
+        // by a lane exchange; its even lane writes it.  The waves take the
+        // lines in turn.
+        static_assert(DS == 2 || DS == 4 || DS == 8, "subvector width");
+        constexpr int CPS = 16 / DS;              // codewords per line
+        constexpr int LINES = KT / CPS;           // lines per codebook
+        constexpr int LW = LINES / (VGPU_BLOCK / 64);  // lines per wave and codebook
+        constexpr int LB = LW < 8 ? LW : 8;       // lines whose loads fly together
+        static_assert(LW % LB == 0, "line batches");
+        const int m16 = lane >> 2, j = lane & 3;
+        const int wv_ = tid >> 6;
+#pragma unroll 1
+        for (int gi = 0; gi < MT / 16; gi++) {
+            const int m = gi * 16 + m16;
+            // the query values this lane multiplies
+            float qv[4];
+            if constexpr (DS == 8) load_vec<4>(a.qn + (size_t)q * D + m * 8 + 4 * (j & 1), qv);
+            else if constexpr (DS == 4) load_vec<4>(a.qn + (size_t)q * D + m * 4, qv);
+            else {
+                load_vec<2>(a.qn + (size_t)q * D + m * 2, qv);
+                qv[2] = qv[0];
+                qv[3] = qv[1];
+            }
+            const float* cb = ix.codebooks + (size_t)m * KT * DS + 4 * j;
+#pragma unroll 1
+            for (int l0 = 0; l0 < LW; l0 += LB) {
+                float4 w[LB];
+#pragma unroll
+                for (int i = 0; i < LB; i++) {
+                    const int sp = (l0 + i) * (VGPU_BLOCK / 64) + wv_;  // line of this load
+                    w[i] = *reinterpret_cast<const float4*>(cb + (size_t)sp * 16);
+                }
+#pragma unroll
+                for (int i = 0; i < LB; i++) {
+                    const int sp = (l0 + i) * (VGPU_BLOCK / 64) + wv_;
+                    if constexpr (DS == 2) {
+                        const float d0 = __builtin_fmaf(qv[1], w[i].y, qv[0] * w[i].x);
+                        const float d1 = __builtin_fmaf(qv[3], w[i].w, qv[2] * w[i].z);
+                        const int k = sp * CPS + 2 * j;
+#pragma unroll
+                        for (int c = 0; c < NC; c++) {
+                            slut[((gi * KT + k) * NC + c) * 16 + m16] = -2.0f * d0;
+                            slut[((gi * KT + k + 1) * NC + c) * 16 + m16] = -2.0f * d1;
+                        }
+                    } else {
+                        float dp = qv[0] * w[i].x;
+                        dp = __builtin_fmaf(qv[1], w[i].y, dp);
+                        dp = __builtin_fmaf(qv[2], w[i].z, dp);
+                        dp = __builtin_fmaf(qv[3], w[i].w, dp);
+                        int k = sp * CPS + j;
+                        if constexpr (DS == 8) {
+                            dp = add_dpp<0xB1>(dp, dp);  // + the partner half (lane j ^ 1)
+                            k = sp * CPS + (j >> 1);
+                        }
+                        if (DS != 8 || (j & 1) == 0) {
+#pragma unroll
+                            for (int c = 0; c < NC; c++) slut[((gi * KT + k) * NC + c) * 16 + m16] = -2.0f * dp;
+                        }
+                    }
+                }
+            }
+        }
+    }
     __syncthreads();
-    if (tid < 64) {  // exclusive prefix of the list lengths
-        uint32_t carry = 0;
+    if (tid < 64) {  // exclusive prefix of the list lengths (whole blocks when transposed)
+        uint32_t carry = 0, entries = 0;
         for (int p0 = 0; p0 < P; p0 += 64) {
             const int p = p0 + lane;
-            const uint32_t own = p < P ? s.llen[p] : 0u;
-            uint32_t x = own;
+            const uint32_t len = p < P ? s.llen[p] : 0u;
+            const uint32_t own = TR ? (len + 15u) & ~15u : len;
+            uint32_t x = own, y = len;
             for (int o = 1; o < 64; o <<= 1) {
-                uint32_t y = __shfl_up(x, o, 64);
-                if (lane >= o) x += y;
+                const uint32_t xs = __shfl_up(x, o, 64), ys = __shfl_up(y, o, 64);
+                if (lane >= o) {
+                    x += xs;
+                    y += ys;
+                }
             }
             if (p < P) s.pref[p] = carry + x - own;
             carry += __shfl(x, 63, 64);
+            entries += __shfl(y, 63, 64);
         }
-        if (lane == 0) s.pref[P] = carry;
+        if (lane == 0) {
+            s.pref[P] = carry;
+            s.misc[7] = entries;
+        }
     }
     {  // ||q - c||^2: eight lanes per probed list (ranking only: any order)
         const int g = tid >> 3, sub = tid & 7;
@@ -527,8 +820,10 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
             if (p < P && sub == 0) s.term0[p] = acc;
         }
     }
-    // T2[m][k] = -2 q_m . cw_mk (ranking only: FMA allowed)
-    if constexpr (MT > 0 && KT > 0 && DS > 0 && (MT * KT) % VGPU_BLOCK == 0) {
+    // T2[m][k] = -2 q_m . cw_mk (ranking only: FMA allowed); the transposed
+    // layout's table is built before the first barrier
+    if constexpr (TR) {
+    } else if constexpr (MT > 0 && KT > 0 && DS > 0 && (MT * KT) % VGPU_BLOCK == 0) {
         constexpr int NE = MT * KT / VGPU_BLOCK;           // entries per thread
         constexpr int G = DS >= 8 ? 4 : (NE < 8 ? NE : 8);  // entries whose loads fly together
         static_assert(NE % G == 0, "table split");
@@ -557,30 +852,72 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
             s.lut[e] = -2.0f * acc;
         }
     }
+    __syncthreads();  // pref (wave 0) and term0 complete
     for (int p = tid; p < P; p += VGPU_BLOCK)
-        s.bt[p] = make_uint2(s.lbeg[p] - s.pref[p], __float_as_uint(s.term0[p]));
-    __syncthreads();
+        s.bt[p] = make_uint4(s.lbeg[p] - s.pref[p], __float_as_uint(s.term0[p]),
+                             TR ? 16u * s.tbo[p] - s.pref[p] : 0u, s.pref[p] + s.llen[p]);
+    if (tid < 64) {  // max ||q - c||^2 for tau
+        float t0max = 0.0f;
+        for (int p = lane; p < P; p += 64) t0max = fmaxf(t0max, s.term0[p]);
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1)
+            t0max = fmaxf(t0max, __uint_as_float(shfl_xor_u32(__float_as_uint(t0max), o)));
+        if (lane == 0) s.misc[9] = __float_as_uint(t0max);
+    }
+    __syncthreads();  // llen, term0 and tbo are dead from here (they may share the key buffer)
 
-    // ---- scan: FS_ROUND entries per round, the next two rounds' loads in
-    // flight (a ring of three register sets).  Round r uses flag parity r & 1.
+    // ---- scan.  Wave w takes the windows rbase + 64 w (rbase = 0, FS_ROUND,
+    // ...) with the next two rounds' loads in flight (a ring of three register
+    // sets) and keeps its own candidates: region keys[w * BW, (w + 1) * BW), its
+    // own count and filter F, and it always holds every entry the wave scanned
+    // with key <= F.  F is the wave's flush threshold or the shared bound
+    // misc[8], whichever is lower.  A flush's T is the keep-th smallest key the
+    // wave has seen (keep >= kout), an upper bound on the query's final A_k, so
+    // no entry above T + 2 tau belongs to R; each flush publishes that bound.
+    // No barrier until the end of the scan.
     const uint32_t total = s.pref[P];
     const int keep = a.kk;
-    const uint32_t cap = (uint32_t)(buf - FS_ROUND);
+    const uint32_t BW = (uint32_t)buf / (VGPU_BLOCK / 64);  // region capacity
+    const uint32_t capw = BW - 64u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane((uint32_t)tid >> 6);
+    uint64_t* reg = s.keys + wave * BW;
+    const float tau = fast_tau(d, M, ds, a.qnorm[q], ix.cmax, ix.rmax, __uint_as_float(s.misc[9]));
+    SlotRegs sr;
+    sr.pref = lane < P ? s.pref[lane] : 0xffffffffu;
+    sr.bt = lane < P ? s.bt[lane] : make_uint4(0u, 0u, 0u, 0u);
+    uint32_t cnt = 0, thr = 0xffffffffu, F = 0xffffffffu, Fused = 0xffffffffu, evicted = 0, flushes = 0;
+    bool lost = false;
     int cur = 0;
     RoundRegs<MT> ga, gb, gc;
+    auto fetch = [&](uint32_t rb, RoundRegs<MT>& g) {
+        if constexpr (TR) fs8t_fetch<MT>(ix, s, sr, rb, total, P, cur, g);
+        else fs8_fetch<MT>(ix, s, sr, rb, total, P, cur, g);
+    };
     if (total > 0) {
-        fs8_fetch<MT>(ix, s, 0, total, P, cur, ga);
-        fs8_fetch<MT>(ix, s, FS_ROUND, total, P, cur, gb);
+        fetch(0, ga);
+        fetch(FS_ROUND, gb);
     }
-#define FS8_STEP(CONSUME, NEXT, R)                                                     \
-    {                                                                                  \
-        const uint32_t rbase = (R) * FS_ROUND;                                         \
-        const int par = (int)((R) & 1u);                                               \
-        fs8_fetch<MT>(ix, s, rbase + 2 * FS_ROUND, total, P, cur, NEXT);                  \
-        fs8_consume<MT, KT, false>(ix, s, slut, CONSUME, s.misc[1], 0u, cap, par);     \
-        __syncthreads();                                                               \
-        if (s.misc[3 + par]) fs8_flush(s, keep, cap, par);                             \
-        if (rbase + FS_ROUND >= total) break;                                          \
+#define FS8_STEP(CONSUME, NEXT, R)                                                           \
+    {                                                                                        \
+        const uint32_t rbase = (R) * FS_ROUND;                                               \
+        fetch(rbase + 2 * FS_ROUND, NEXT);                                                   \
+        const uint32_t shared = __atomic_load_n(&s.misc[8], __ATOMIC_RELAXED);               \
+        Fused = F;                                                                           \
+        fs8w_consume<MT, KT, NC>(ix, s, slut, CONSUME, F, reg, cnt);                         \
+        if (cnt > capw) {                                                                    \
+            const uint32_t before = cnt;                                                     \
+            thr = fs8w_flush(reg, cnt, (uint32_t)keep - 1u, capw, &lost);                    \
+            evicted += before - cnt;                                                         \
+            flushes++;                                                                       \
+            uint32_t ub = fkey(fkey_to_float(thr) + 2.0f * tau);                             \
+            ub = ub < 0xfffffffeu ? ub + 1u : 0xffffffffu;                                   \
+            if (thr < 0xff800000u && lane == 0) atomicMin(&s.misc[8], ub);                   \
+        }                                                                                    \
+        {   /* the next round's filter (the bound read before this round's lookups) */        \
+            const uint32_t sh = __builtin_amdgcn_readfirstlane(shared);                      \
+            F = thr < sh ? thr : sh;                                                         \
+        }                                                                                    \
+        if (rbase + FS_ROUND >= total) break;                                                \
     }
     for (uint32_t r = 0; r * FS_ROUND < total; r += 3) {
         FS8_STEP(ga, gc, r)
@@ -588,11 +925,30 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
         FS8_STEP(gc, gb, r + 2)
     }
 #undef FS8_STEP
+    {
+        const uint32_t G = Fused < thr ? Fused : thr;  // the wave's region holds its entries <= G
+        if (lane == 0) {
+            s.misc[16 + wave] = cnt;
+            s.misc[20 + wave] = G;
+            atomicAdd(&s.misc[5], evicted);
+            atomicAdd(&s.misc[6], flushes);
+            if (lost) s.misc[2] = 1u;
+        }
+    }
     __syncthreads();
 
-    // ---- proof that the buffer holds R, then rescoring.
-    uint32_t n = s.misc[0];
-    const uint32_t thr = s.misc[1];
+    // ---- proof that the merged buffer holds R, then rescoring.
+    uint32_t cnts[VGPU_BLOCK / 64];
+    uint32_t thr_all = 0xffffffffu;  // every wave holds its entries <= thr_all
+#pragma unroll
+    for (int w = 0; w < VGPU_BLOCK / 64; w++) {
+        cnts[w] = s.misc[16 + w];
+        const uint32_t g = s.misc[20 + w];
+        thr_all = g < thr_all ? g : thr_all;
+    }
+    const uint32_t Gw = s.misc[20 + wave];
+    uint32_t n = fs8w_merge(s, cnts, BW);
+    const uint32_t cap = (uint32_t)buf - FS_ROUND;  // second-pass capacity
     const int kout = a.kout;
     bool fail = s.misc[2] != 0u;
     bool retried = false;
@@ -600,32 +956,30 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     if (!fail && n > (uint32_t)kout) {
         // an upper bound on A_k: R grows by at most the rest of A_k's bin
         const uint32_t Ak = fs8_select_upper(s, n, (uint32_t)(kout - 1), 0xffffffffu);
-        float t0max = 0.0f;
-        for (int p = 0; p < P; p++) t0max = fmaxf(t0max, s.term0[p]);
-        const float tau = fast_tau(d, M, ds, a.qnorm[q], ix.cmax, ix.rmax, t0max);
         const float bound = fkey_to_float(Ak) + 2.0f * tau;
         bk = fkey(bound);
         bk = bk < 0xfffffffeu ? bk + 1u : 0xffffffffu;  // one ulp to spare
-        if (thr != 0xffffffffu && bk > thr) {
-            // Second pass: the buffer holds every key <= thr; add the keys in
-            // (thr, bk] with no flush, so afterwards it holds all of R.  More
-            // than the buffer holds fails the query (EXACT rerun).
+        if (thr_all != 0xffffffffu && bk > thr_all) {
+            // Second pass: wave w's entries <= G_w are held; each wave adds
+            // its entries in (G_w, bk] with no flush, so afterwards the buffer
+            // holds all of R.  More than the buffer holds fails the query
+            // (EXACT rerun).
             retried = true;
             if (tid == 0) {
-                s.misc[1] = bk;
+                s.misc[0] = n;
                 s.misc[3] = s.misc[4] = 0u;
             }
             __syncthreads();
             cur = 0;
-            fs8_fetch<MT>(ix, s, 0, total, P, cur, ga);
+            fetch(0, ga);
             for (uint32_t rb = 0; rb < total; rb += 2 * FS_ROUND) {
-                fs8_fetch<MT>(ix, s, rb + FS_ROUND, total, P, cur, gb);
-                fs8_consume<MT, KT, true>(ix, s, slut, ga, bk, thr, cap, 0);
+                fetch(rb + FS_ROUND, gb);
+                fs8_consume_retry<MT, KT, NC>(ix, s, slut, ga, bk, Gw, cap, 0);
                 __syncthreads();
                 if (s.misc[3]) break;
                 if (rb + FS_ROUND >= total) break;
-                fs8_fetch<MT>(ix, s, rb + 2 * FS_ROUND, total, P, cur, ga);
-                fs8_consume<MT, KT, true>(ix, s, slut, gb, bk, thr, cap, 1);
+                fetch(rb + 2 * FS_ROUND, ga);
+                fs8_consume_retry<MT, KT, NC>(ix, s, slut, gb, bk, Gw, cap, 1);
                 __syncthreads();
                 if (s.misc[4]) break;
             }
@@ -640,7 +994,7 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     }
     if (tid == 0) {
         uint32_t* st = a.qstat + (size_t)q * QSTAT_WORDS;
-        st[0] = total;
+        st[0] = s.misc[7];  // list entries, without block padding
         st[1] = s.misc[6];
         st[2] = s.misc[5] + n;  // appended = evicted + still held
         st[3] = (fail ? (1u | (s.misc[2] ? 2u : 0u)) : 0u) | (retried ? 4u : 0u);
@@ -651,15 +1005,17 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
 
     // Two threads per entry (codebooks 0 .. M/2 - 1 and M/2 .. M - 1) when the
     // probed lists' residuals r = q - c fit the idle table region: each thread
-    // loads its half code row, then its codewords in batches; r comes from LDS
-    // (the same single subtraction exact_sub_distance makes).  The first
+    // loads its half code row (and the first thread the entry's insertion
+    // index) together with the residual table, then all its codewords at once
+    // (at most 64 floats); r comes from LDS (the same single subtraction
+    // exact_sub_distance makes).  The first
     // thread adds its sub-distances in codebook order from 0.0 and continues
     // with its partner's, handed over by a lane shuffle (pq_simd.rs:349-355).
     if constexpr (MT == 8 || MT == 16 || MT == 32) {
         if constexpr (KT > 0 && DS > 0) {
-            if ((size_t)P * D <= (size_t)MT * KT && n <= (uint32_t)(VGPU_BLOCK / 2)) {
+            if ((size_t)P * D <= (size_t)LUTF && n <= (uint32_t)(VGPU_BLOCK / 2)) {
                 constexpr int H = MT / 2;                 // codebooks per thread
-                constexpr int CB0 = DS >= 8 ? 4 : 8;
+                constexpr int CB0 = 64 / DS;
                 constexpr int CB = CB0 < H ? CB0 : H;     // codewords in flight
                 static_assert(H % CB == 0 && H % 4 == 0, "codebook batches");
                 constexpr int HW = H / 4;                 // code words per half row
@@ -670,7 +1026,10 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
                 uint32_t cwd[HW];
 #pragma unroll
                 for (int w = 0; w < HW; w++) cwd[w] = 0u;
-                if (act) {
+                const uint32_t vid = act && half == 0 ? ix.list_ids[pos] : 0u;
+                CodeRow<MT> row;  // DS == 8: both lanes of the pair hold the whole row
+                if constexpr (DS == 8) load_row<MT>(row, ix.codes + (size_t)pos * MT);
+                if (DS != 8 && act) {
                     const uint8_t* cp = ix.codes + (size_t)pos * MT + half * H;
                     if constexpr (HW == 1) cwd[0] = *reinterpret_cast<const uint32_t*>(cp);
                     else if constexpr (HW == 2) {
@@ -691,6 +1050,48 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
                     o[3] = __fsub_rn(s.qs[j + 3], c.w);
                 }
                 __syncthreads();
+                float total_e = 0.0f;
+                if constexpr (DS == 8) {
+                    // The pair shares its codewords: for codebooks 2t and 2t + 1
+                    // lane `half` loads dims 4 half .. 4 half + 3 of both (one
+                    // sector each, read by the two lanes together), gives its
+                    // partner the half it lacks (lane 0 scores 2t, lane 1 scores
+                    // 2t + 1), and lane 0 adds the scores in codebook order.
+                    // Both lanes hold the full code row.
+                    float ev[MT / 2];  // this lane's codebooks 2t + half
+                    const float* rrow = s.lut + (size_t)p * D + half * DS;
+#pragma unroll
+                    for (int t = 0; t < MT / 2; t++) {
+                        const uint32_t w = row.w[t >> 1];
+                        const uint32_t c0 = (w >> (16 * (t & 1))) & 0xffu, c1 = (w >> (16 * (t & 1) + 8)) & 0xffu;
+                        const float4 A = *reinterpret_cast<const float4*>(
+                            ix.codebooks + ((size_t)(2 * t) * KT + c0) * DS + 4 * half);
+                        const float4 B = *reinterpret_cast<const float4*>(
+                            ix.codebooks + ((size_t)(2 * t + 1) * KT + c1) * DS + 4 * half);
+                        const float4 snd = half ? A : B;
+                        float4 rcv;
+                        rcv.x = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(snd.x), 0xB1, 0xF, 0xF, true));
+                        rcv.y = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(snd.y), 0xB1, 0xF, 0xF, true));
+                        rcv.z = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(snd.z), 0xB1, 0xF, 0xF, true));
+                        rcv.w = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(snd.w), 0xB1, 0xF, 0xF, true));
+                        const float4 lo = half ? rcv : A, hi = half ? B : rcv;
+                        const float cw[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                        const float* r = rrow + (size_t)(2 * t) * DS;  // codebook 2t + half
+                        float e = 0.0f;
+#pragma unroll
+                        for (int j = 0; j < 8; j++) {
+                            const float diff = __fsub_rn(r[j], cw[j]);
+                            e = __fadd_rn(e, __fmul_rn(diff, diff));
+                        }
+                        ev[t] = e;
+                    }
+#pragma unroll
+                    for (int t = 0; t < MT / 2; t++) {  // lane 0: e_2t, then the partner's e_2t+1
+                        total_e = __fadd_rn(total_e, ev[t]);
+                        total_e = __fadd_rn(total_e, __int_as_float(__builtin_amdgcn_mov_dpp(
+                                                         __float_as_int(ev[t]), 0xB1, 0xF, 0xF, true)));
+                    }
+                } else {
                 float ev[H];
                 const float* rrow = s.lut + (size_t)p * D + half * H * DS;
 #pragma unroll
@@ -713,14 +1114,15 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
                         ev[h0 + b] = e;
                     }
                 }
-                float total_e = 0.0f;  // codebooks 0 .. H - 1 (first thread)
+                // codebooks 0 .. H - 1 (first thread)
 #pragma unroll
                 for (int h = 0; h < H; h++) total_e = __fadd_rn(total_e, ev[h]);
 #pragma unroll
                 for (int h = 0; h < H; h++)  // then the partner's H .. M - 1
                     total_e = __fadd_rn(total_e, __uint_as_float(shfl_xor_u32(__float_as_uint(ev[h]), 1)));
+                }
                 __syncthreads();  // every key of R read above before any is rewritten
-                if (act && half == 0) s.keys[i] = cand_key(total_e, ix.list_ids[pos]);
+                if (act && half == 0) s.keys[i] = cand_key(total_e, vid);
                 __syncthreads();
                 goto rescored;
             }
@@ -825,28 +1227,41 @@ rescored:
     }
 }
 
+bool scan8_fast_blocks_supported(int M, int K, int ds) {
+    return K == 256 && (M == 16 || M == 32 || M == 48) && (ds == 2 || ds == 4 || ds == 8);
+}
+
+// Table copies of the transposed kernels (0: row layout).  One copy: with
+// 16 codebooks two copies would let a half wave read 32 distinct banks, but
+// the doubled table costs more in occupancy than the conflicts it removes.
+static int table_copies(const DevIndex& ix) {
+    return ix.tblocks && scan8_fast_blocks_supported(ix.M, ix.K, ix.ds) ? 1 : 0;
+}
+
 // Static table bytes of the specialisations (compile-time M, K = 256).
 static size_t static_lut_bytes(const DevIndex& ix) {
     if (ix.K != 256) return 0;
+    const int nc = table_copies(ix);
     switch (ix.M) {
-        case 4: case 8: case 16: case 32: case 48: case 64: return (size_t)ix.M * 256 * 4;
+        case 4: case 8: case 16: case 32: case 48: case 64:
+            return (size_t)ix.M * 256 * 4 * (nc ? nc : 1);
         default: return 0;
     }
 }
 
 size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
-    size_t off[11];
+    size_t off[12];
     const size_t st = static_lut_bytes(ix);
     return st + fs8_layout(ix.d, ix.M, ix.K, a.P, fs8_buf(a.kk), st != 0, off);
 }
 
-template <int MT, int KT, int DS>
+template <int MT, int KT, int DS, int NC>
 static void launch_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hipEvent_t t0,
                         hipEvent_t t1) {
     const int buf = fs8_buf(a.kk);
-    size_t off[11];
+    size_t off[12];
     const size_t dyn = fs8_layout(ix.d, ix.M, ix.K, a.P, buf, MT > 0 && KT >= 64, off);
-    auto k = scan8_fast_kernel<MT, KT, DS>;
+    auto k = scan8_fast_kernel<MT, KT, DS, NC>;
     ensure_dyn_lds((const void*)k, dyn);
     if (t0)
         hipExtLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), (uint32_t)dyn, s, t0, t1, 0u, ix, a, buf);
@@ -854,14 +1269,26 @@ static void launch_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hi
         hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), dyn, s, ix, a, buf);
 }
 
+// Compile-time subvector width; the shapes with transposed blocks use them.
+template <int MT, int DS>
+static void launch_fast_ds(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hipEvent_t t0,
+                           hipEvent_t t1) {
+    if constexpr (MT == 16 || MT == 32 || MT == 48) {
+        if (table_copies(ix) == 1) return launch_fast<MT, 256, DS, 1>(ix, a, s, t0, t1);
+        return launch_fast<MT, 256, 0, 0>(ix, a, s, t0, t1);  // blocks missing: row layout
+    } else {
+        launch_fast<MT, 256, DS, 0>(ix, a, s, t0, t1);
+    }
+}
+
 template <int MT>
 static void launch_fast_m(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hipEvent_t t0,
                           hipEvent_t t1) {
     switch (ix.ds) {  // the subvector widths of the benchmark shapes
-        case 2: launch_fast<MT, 256, 2>(ix, a, s, t0, t1); return;
-        case 4: launch_fast<MT, 256, 4>(ix, a, s, t0, t1); return;
-        case 8: launch_fast<MT, 256, 8>(ix, a, s, t0, t1); return;
-        default: launch_fast<MT, 256, 0>(ix, a, s, t0, t1); return;
+        case 2: launch_fast_ds<MT, 2>(ix, a, s, t0, t1); return;
+        case 4: launch_fast_ds<MT, 4>(ix, a, s, t0, t1); return;
+        case 8: launch_fast_ds<MT, 8>(ix, a, s, t0, t1); return;
+        default: launch_fast<MT, 256, 0, 0>(ix, a, s, t0, t1); return;
     }
 }
 
@@ -878,7 +1305,7 @@ void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hip
             default: break;
         }
     }
-    launch_fast<0, 0, 0>(ix, a, s, t0, t1);
+    launch_fast<0, 0, 0, 0>(ix, a, s, t0, t1);
 }
 
 }  // namespace vgpu

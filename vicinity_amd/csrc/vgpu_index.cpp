@@ -469,6 +469,19 @@ void IvfpqIndex::upload_index() {
         d_bias.reserve(n);
         dix.bias = d_bias.p;
         launch_bias(dix, d_bias.p, stream);
+        if (scan8_fast_blocks_supported((int)M, (int)K, (int)ds)) {
+            std::vector<uint32_t> toff(L + 1, 0);
+            for (size_t l = 0; l < L; l++)
+                toff[l + 1] = toff[l] + (uint32_t)((offsets[l + 1] - offsets[l] + 15) / 16);
+            d_tblk_off.upload(toff.data(), L + 1, stream);
+            d_tblocks.reserve((size_t)toff[L] * TBLK_BYTES(M) + TBLK_BYTES(M));
+            dix.tblk_off = d_tblk_off.p;
+            dix.tblocks = d_tblocks.p;
+            launch_tblocks(dix, d_tblocks.p, stream);
+        } else {
+            d_tblocks.release();
+            d_tblk_off.release();
+        }
     }
     VGPU_HIP(hipGetLastError());
     VGPU_HIP(hipStreamSynchronize(stream));

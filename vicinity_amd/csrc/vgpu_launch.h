@@ -26,6 +26,13 @@ struct DevIndex {
     const float* vectors = nullptr;    // [n*d] by insertion index, normalised (may be null)
     const uint8_t* packed = nullptr;   // FastScan blocks of every list (K == 16)
     const uint32_t* pack_off = nullptr;// [L+1] block offset of each list (K == 16)
+    // Transposed 16-entry blocks of every list for the FAST scan (K == 256,
+    // M a multiple of 16; null otherwise): block b of list l is block
+    // tblk_off[l] + b, TBLK_BYTES(M) bytes: codes [m][j] with byte (m, j) the
+    // code of entry j ^ (m & 15) in codebook m, then the 16 entries' b(x).
+    // Entries past the end of the list have code 0 and b(x) 0.
+    const uint8_t* tblocks = nullptr;
+    const uint32_t* tblk_off = nullptr;// [L+1]
     float cmax = 0.f;                  // max ||c||
     float rmax = 0.f;                  // max ||decoded residual||
 };
@@ -131,6 +138,11 @@ void launch_finalize(const uint32_t* vidx, const float* dist, const uint32_t* do
 void launch_encode(const float* x, int n, int d, const float* centroids, const uint32_t* assign,
                    const float* codebooks, int M, int K, int ds, uint8_t* codes, hipStream_t s);
 void launch_bias(const DevIndex& ix, float* bias, hipStream_t s);
+#define TBLK_BYTES(M) (16 * (size_t)(M) + 64)
+// Whether the FAST scan reads transposed blocks for this shape.
+bool scan8_fast_blocks_supported(int M, int K, int ds);
+// Fill ix.tblocks from ix.codes, ix.bias and ix.tblk_off.
+void launch_tblocks(const DevIndex& ix, uint8_t* tblocks, hipStream_t s);
 void launch_pack4(const DevIndex& ix, uint8_t* packed, hipStream_t s);
 // LUT kernels for tests.
 void launch_adc_tables(const float* codebooks, int M, int K, int ds, const float* r, int nr,

@@ -85,7 +85,8 @@ struct IvfpqIndex {
     DevBuf<uint4> d_cb16, w_cb16;  // bf16 hi/lo centroid copies (search index, build workspace)
     DevBuf<uint32_t> w_cand, w_cand_n;  // fused coarse candidates
     DevBuf<uint32_t> d_offsets, d_list_ids, d_doc_ids, d_pack_off;
-    DevBuf<uint8_t> d_codes, d_packed;
+    DevBuf<uint8_t> d_codes, d_packed, d_tblocks;
+    DevBuf<uint32_t> d_tblk_off;
     DevIndex dix;
 
     // search workspace
