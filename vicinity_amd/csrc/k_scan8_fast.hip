@@ -130,7 +130,7 @@ __device__ __forceinline__ float fast_tau(int d, int M, int ds, float qn, float 
 struct FastLds {
     float* lut;      // [M * max(K, 64)] table, then rescoring scratch
     uint64_t* keys;  // [buf] (fkey(a) << 32) | position
-    float* qs;       // [d]
+    float* qs;       // [d] (prologue only)
     uint32_t* lid;   // [P]
     uint32_t* lbeg;  // [P]
     uint32_t* llen;  // [P]
@@ -166,21 +166,22 @@ __host__ __device__ inline size_t fs8_layout(int d, int M, int K, int P, int buf
     const int KL = K > 64 ? K : 64;
     off[0] = o; o = static_lut ? 0 : fs8_align(o + (size_t)M * KL * 4);  // lut
     off[1] = o; o = fs8_align(o + (size_t)buf * 8);        // keys
-    off[2] = o; o = fs8_align(o + (size_t)d * 4);          // qs
     off[3] = o; o = fs8_align(o + (size_t)P * 4);          // lid
     off[4] = o; o = fs8_align(o + (size_t)P * 4);          // lbeg
     off[6] = o; o = fs8_align(o + (size_t)(P + 1) * 4);    // pref
     off[8] = o; o = fs8_align(o + sizeof(RadixScratch));   // radix scratch
     off[9] = o; o = fs8_align(o + 32 * 4);                 // misc
     off[10] = o; o = fs8_align(o + (size_t)P * 16);        // bt
-    // llen, term0 and tbo are read only before the scan: they share the key
-    // buffer when they fit in it
-    const size_t pa = fs8_align((size_t)P * 4);
-    if (3 * pa <= (size_t)buf * 8) {
-        off[5] = off[1];
-        off[7] = off[1] + pa;
-        off[11] = off[1] + 2 * pa;
+    // qs, llen, term0 and tbo are read only before the scan: they share the
+    // key buffer when they fit in it
+    const size_t pa = fs8_align((size_t)P * 4), qa = fs8_align((size_t)d * 4);
+    if (qa + 3 * pa <= (size_t)buf * 8) {
+        off[2] = off[1];
+        off[5] = off[1] + qa;
+        off[7] = off[5] + pa;
+        off[11] = off[7] + pa;
     } else {
+        off[2] = o; o += qa;
         off[5] = o; o += pa;
         off[7] = o; o += pa;
         off[11] = o; o += pa;
@@ -1043,11 +1044,12 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
                 for (int e = tid; e < P * (D / 4); e += VGPU_BLOCK) {  // residual table
                     const int pp = e / (D / 4), j = 4 * (e % (D / 4));
                     const float4 c = *reinterpret_cast<const float4*>(ix.centroids + (size_t)s.lid[pp] * D + j);
+                    const float4 qv = *reinterpret_cast<const float4*>(a.qn + (size_t)q * D + j);
                     float* o = s.lut + pp * D + j;
-                    o[0] = __fsub_rn(s.qs[j], c.x);
-                    o[1] = __fsub_rn(s.qs[j + 1], c.y);
-                    o[2] = __fsub_rn(s.qs[j + 2], c.z);
-                    o[3] = __fsub_rn(s.qs[j + 3], c.w);
+                    o[0] = __fsub_rn(qv.x, c.x);
+                    o[1] = __fsub_rn(qv.y, c.y);
+                    o[2] = __fsub_rn(qv.z, c.z);
+                    o[3] = __fsub_rn(qv.w, c.w);
                 }
                 __syncthreads();
                 float total_e = 0.0f;
@@ -1159,7 +1161,7 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
             const uint8_t code = scodes[t];
             const float* cw = ix.codebooks + ((size_t)m * K + code) * ds;
             const float* c = ix.centroids + (size_t)s.lid[p] * d + m * ds;
-            s.lut[t] = exact_sub_distance<DS>(s.qs + m * ds, c, cw, ds);
+            s.lut[t] = exact_sub_distance<DS>(a.qn + (size_t)q * d + m * ds, c, cw, ds);
         }
         __syncthreads();
         for (uint32_t i = c0 + tid; i < c0 + cn; i += VGPU_BLOCK) {
