@@ -209,20 +209,23 @@ __device__ inline FastLds fs8_carve(char* smem, float* static_lut, int d, int M,
     return s;
 }
 
-// Keep the buffer entries whose high word is <= T (in place, chunk by chunk:
-// a chunk is read into registers before any of its slots are rewritten, and
-// the compacted prefix never passes the end of the chunk being read).  Keys
-// carry t, the entry's index in the concatenated probed lists; with
-// `relabel`, each kept key is rewritten as (probe slot << 32) | position, the
-// slot found by binary search over the list prefix sums.
-__device__ inline uint32_t fs8_compact(FastLds& s, uint32_t n, uint32_t T, bool relabel, int P) {
+// Keep the keys key_at(0 .. n) whose high word is <= T, written densely to
+// keys[0 ..) chunk by chunk: a chunk is read into registers before any slot
+// is rewritten, and the compacted prefix never passes the slot of a key not
+// yet read (key_at(i) is stored at or after keys[i]).  Keys carry t, the
+// entry's index in the concatenated probed lists; with `relabel`, each kept
+// key is rewritten as (probe slot << 32) | position, the slot found by binary
+// search over the list prefix sums.
+template <typename KeyAt>
+__device__ inline uint32_t fs8_compact(FastLds& s, KeyAt key_at, uint32_t n, uint32_t T, bool relabel,
+                                       int P) {
     const int tid = threadIdx.x;
     __syncthreads();
     if (tid == 0) s.misc[0] = 0;
     __syncthreads();
     for (uint32_t c0 = 0; c0 < n; c0 += VGPU_BLOCK) {
         const uint32_t i = c0 + tid;
-        uint64_t v = i < n ? s.keys[i] : ~0ull;
+        uint64_t v = i < n ? key_at(i) : ~0ull;
         bool take = i < n && (uint32_t)(v >> 32) <= T;
         __syncthreads();
         if (take && relabel) {
@@ -249,11 +252,12 @@ __device__ inline uint32_t fs8_compact(FastLds& s, uint32_t n, uint32_t T, bool 
 // bin holding rank, so every key <= the rank-th is <= U and the keys <= U are
 // those of the bins up to it.  When those number more than `limit`, the exact
 // radix select is taken instead.  All threads call it.
-__device__ uint32_t fs8_select_upper(FastLds& s, uint32_t n, uint32_t rank, uint32_t limit) {
+template <typename KeyAt>
+__device__ uint32_t fs8_select_upper(FastLds& s, KeyAt key_at, uint32_t n, uint32_t rank, uint32_t limit) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint32_t mn = 0xffffffffu, mx = 0u;
     for (uint32_t i = tid; i < n; i += VGPU_BLOCK) {
-        const uint32_t h = (uint32_t)(s.keys[i] >> 32);
+        const uint32_t h = (uint32_t)(key_at(i) >> 32);
         mn = h < mn ? h : mn;
         mx = h > mx ? h : mx;
     }
@@ -282,7 +286,7 @@ __device__ uint32_t fs8_select_upper(FastLds& s, uint32_t n, uint32_t rank, uint
     for (int i = tid; i < 256; i += VGPU_BLOCK) s.rs->hist[i] = 0u;
     __syncthreads();
     for (uint32_t i = tid; i < n; i += VGPU_BLOCK)
-        atomicAdd(&s.rs->hist[((uint32_t)(s.keys[i] >> 32) >> shift) & 255u], 1u);
+        atomicAdd(&s.rs->hist[((uint32_t)(key_at(i) >> 32) >> shift) & 255u], 1u);
     __syncthreads();
     if (tid < 64) {
         const uint32_t h0 = s.rs->hist[4 * lane], h1 = s.rs->hist[4 * lane + 1];
@@ -307,7 +311,7 @@ __device__ uint32_t fs8_select_upper(FastLds& s, uint32_t n, uint32_t rank, uint
     __syncthreads();
     const uint32_t b = s.rs->bin, upto = s.rs->rem;
     if (upto > limit) {  // a heavy bin: exact select
-        auto hk = [&](int i) -> uint32_t { return (uint32_t)(s.keys[i] >> 32); };
+        auto hk = [&](int i) -> uint32_t { return (uint32_t)(key_at((uint32_t)i) >> 32); };
         return block_radix_select<uint32_t>(hk, (int)n, rank, s.rs);
     }
     const uint32_t low = (1u << shift) - 1u;
@@ -710,7 +714,7 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
         constexpr int CPS = 16 / DS;              // codewords per line
         constexpr int LINES = KT / CPS;           // lines per codebook
         constexpr int LW = LINES / (VGPU_BLOCK / 64);  // lines per wave and codebook
-        constexpr int LB = LW < 8 ? LW : 8;       // lines whose loads fly together
+        constexpr int LB = LW < 16 ? LW : 16;     // lines whose loads fly together
         static_assert(LW % LB == 0, "line batches");
         const int m16 = lane >> 2, j = lane & 3;
         const int wv_ = tid >> 6;
@@ -948,7 +952,15 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
         thr_all = g < thr_all ? g : thr_all;
     }
     const uint32_t Gw = s.misc[20 + wave];
-    uint32_t n = fs8w_merge(s, cnts, BW);
+    // Dense index i of the waves' keys: wave w's keys are roff[w] .. roff[w + 1],
+    // read in place until a second pass needs them merged.
+    uint32_t roff[VGPU_BLOCK / 64 + 1];
+    roff[0] = 0;
+#pragma unroll
+    for (int w = 0; w < VGPU_BLOCK / 64; w++) roff[w + 1] = roff[w] + cnts[w];
+    uint32_t n = roff[VGPU_BLOCK / 64];
+    bool merged = false;
+    auto key_at = [&](uint32_t i) -> uint64_t { return s.keys[merged ? i : region_slot(i, roff, BW)]; };
     const uint32_t cap = (uint32_t)buf - FS_ROUND;  // second-pass capacity
     const int kout = a.kout;
     bool fail = s.misc[2] != 0u;
@@ -956,7 +968,7 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     uint32_t bk = 0xffffffffu;
     if (!fail && n > (uint32_t)kout) {
         // an upper bound on A_k: R grows by at most the rest of A_k's bin
-        const uint32_t Ak = fs8_select_upper(s, n, (uint32_t)(kout - 1), 0xffffffffu);
+        const uint32_t Ak = fs8_select_upper(s, key_at, n, (uint32_t)(kout - 1), 0xffffffffu);
         const float bound = fkey_to_float(Ak) + 2.0f * tau;
         bk = fkey(bound);
         bk = bk < 0xfffffffeu ? bk + 1u : 0xffffffffu;  // one ulp to spare
@@ -966,6 +978,8 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
             // holds all of R.  More than the buffer holds fails the query
             // (EXACT rerun).
             retried = true;
+            n = fs8w_merge(s, cnts, BW);
+            merged = true;
             if (tid == 0) {
                 s.misc[0] = n;
                 s.misc[3] = s.misc[4] = 0u;
@@ -1002,13 +1016,30 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
         if (fail) a.flag_list[atomicAdd(a.flag_count, 1u)] = (uint32_t)q;
     }
     if (fail) return;
-    n = fs8_compact(s, n, bk, true, P);  // R, keys relabelled (probe slot, position)
+    // The table is no longer needed: the residuals r = q - c of the probed
+    // lists go to its region now (their loads overlap the compaction) when
+    // the two-thread rescoring below may use them.
+    if constexpr ((MT == 8 || MT == 16 || MT == 32) && KT > 0 && DS > 0) {
+        if ((size_t)P * D <= (size_t)LUTF) {
+            for (int e = tid; e < P * (D / 4); e += VGPU_BLOCK) {
+                const int pp = e / (D / 4), j = 4 * (e % (D / 4));
+                const float4 c = *reinterpret_cast<const float4*>(ix.centroids + (size_t)s.lid[pp] * D + j);
+                const float4 qv = *reinterpret_cast<const float4*>(a.qn + (size_t)q * D + j);
+                float* o = s.lut + pp * D + j;
+                o[0] = __fsub_rn(qv.x, c.x);
+                o[1] = __fsub_rn(qv.y, c.y);
+                o[2] = __fsub_rn(qv.z, c.z);
+                o[3] = __fsub_rn(qv.w, c.w);
+            }
+        }
+    }
+    n = fs8_compact(s, key_at, n, bk, true, P);  // R, keys relabelled (probe slot, position)
 
     // Two threads per entry (codebooks 0 .. M/2 - 1 and M/2 .. M - 1) when the
-    // probed lists' residuals r = q - c fit the idle table region: each thread
-    // loads its half code row (and the first thread the entry's insertion
-    // index) together with the residual table, then all its codewords at once
-    // (at most 64 floats); r comes from LDS (the same single subtraction
+    // probed lists' residuals r = q - c fit the idle table region (built
+    // above): each thread loads its half code row (and the first thread the
+    // entry's insertion index), then all its codewords at once (at most 64
+    // floats); r comes from LDS (the same single subtraction
     // exact_sub_distance makes).  The first
     // thread adds its sub-distances in codebook order from 0.0 and continues
     // with its partner's, handed over by a lane shuffle (pq_simd.rs:349-355).
@@ -1041,17 +1072,6 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
                         cwd[0] = x.x; cwd[1] = x.y; cwd[2] = x.z; cwd[3] = x.w;
                     }
                 }
-                for (int e = tid; e < P * (D / 4); e += VGPU_BLOCK) {  // residual table
-                    const int pp = e / (D / 4), j = 4 * (e % (D / 4));
-                    const float4 c = *reinterpret_cast<const float4*>(ix.centroids + (size_t)s.lid[pp] * D + j);
-                    const float4 qv = *reinterpret_cast<const float4*>(a.qn + (size_t)q * D + j);
-                    float* o = s.lut + pp * D + j;
-                    o[0] = __fsub_rn(qv.x, c.x);
-                    o[1] = __fsub_rn(qv.y, c.y);
-                    o[2] = __fsub_rn(qv.z, c.z);
-                    o[3] = __fsub_rn(qv.w, c.w);
-                }
-                __syncthreads();
                 float total_e = 0.0f;
                 if constexpr (DS == 8) {
                     // The pair shares its codewords: for codebooks 2t and 2t + 1
