@@ -45,6 +45,9 @@
 
 namespace vgpu {
 
+// Native 128-bit vector (raw buffer loads).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 #define FS_U 1                          // entries per thread per round
 #define FS_ROUND (VGPU_BLOCK * FS_U)    // entries per round
 
@@ -327,9 +330,9 @@ template <int MT>
 struct RoundRegs {
     CodeRow<MT> row[FS_U];
     float bias[FS_U];
-    float t0[FS_U];    // ||q - c||^2 of the entry's list
+    float t0[FS_U];    // ||q - c||^2 of the entry's list; NaN: no entry (past a list's end)
     uint32_t pos[FS_U];// position (code row), generic path only
-    uint32_t t[FS_U];  // index in the concatenated probed lists; 0xffffffff = no entry
+    uint32_t t[FS_U];  // index in the concatenated probed lists
 };
 
 // Slot records of the probed lists held in lane registers when P <= 64:
@@ -393,8 +396,8 @@ __device__ __forceinline__ void fs8_fetch(const DevIndex& ix, const FastLds& s, 
         const uint4 e = slot_record(s, sr, P, wb, t, cw);
         const uint32_t pos = valid ? e.x + t : 0u;
         g.pos[u] = pos;
-        g.t[u] = valid ? t : 0xffffffffu;
-        g.t0[u] = __uint_as_float(e.y);
+        g.t[u] = t;
+        g.t0[u] = valid ? __uint_as_float(e.y) : __builtin_nanf("");
         if constexpr (MT > 0) load_row<MT>(g.row[u], ix.codes + (size_t)pos * MT);
         g.bias[u] = ix.bias[pos];
     }
@@ -405,12 +408,14 @@ __device__ __forceinline__ void fs8_fetch(const DevIndex& ix, const FastLds& s, 
 // wave's window of 64 entries is four blocks, one per row of 16 lanes; lane m
 // of a row loads the 16 codes of codebooks m, m + 16, ... of its block (code j
 // of entry j ^ m) and the b(x) of the block's entry m, which is the entry it
-// ends up scoring.  Rows past the end read block 0 (it exists whenever
-// anything is scanned).
+// ends up scoring.  Raw buffer loads: the block's byte offset is the slot's
+// e.z plus (MT + 4) tb, split into the window's part `wofs` and the lane's
+// constants lc_code / lc_bias; rows past the end of the lists read zeros or
+// an unrelated block, and their entries are invalid (NaN term).
 template <int MT>
-__device__ __forceinline__ void fs8t_fetch(const DevIndex& ix, const FastLds& s, const SlotRegs& sr,
-                                           uint32_t rbase, uint32_t total, int P, int& cw,
-                                           RoundRegs<MT>& g) {
+__device__ __forceinline__ void fs8t_fetch(__amdgpu_buffer_rsrc_t trs, const FastLds& s, const SlotRegs& sr,
+                                           uint32_t rbase, uint32_t lc_code, uint32_t lc_bias, int P,
+                                           int& cw, RoundRegs<MT>& g) {
     static_assert(FS_U == 1 && MT % 16 == 0, "one window per wave and round");
     const uint32_t lane = threadIdx.x & 63u, m = lane & 15u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -418,19 +423,19 @@ __device__ __forceinline__ void fs8t_fetch(const DevIndex& ix, const FastLds& s,
     const uint32_t tb = wb + (lane & 48u);   // the row's block start
     const uint32_t t = tb + m;
     const uint4 e = slot_record(s, sr, P, wb, tb, cw);
-    const uint32_t blk = tb < total ? (e.z + tb) >> 4 : 0u;
-    const uint8_t* bp = ix.tblocks + (size_t)blk * TBLK_BYTES(MT);
+    const uint32_t wofs = (uint32_t)(MT + 4) * wb;
 #pragma unroll
     for (int gi = 0; gi < MT / 16; gi++) {
-        const uint4 x = *reinterpret_cast<const uint4*>(bp + gi * 256 + m * 16u);
+        // the whole offset in the range-checked VGPR part (soffset is not checked)
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(trs, e.z + wofs + lc_code + (uint32_t)gi * 256u, 0u, 0);
         g.row[0].w[4 * gi] = x.x;
         g.row[0].w[4 * gi + 1] = x.y;
         g.row[0].w[4 * gi + 2] = x.z;
         g.row[0].w[4 * gi + 3] = x.w;
     }
-    g.bias[0] = *reinterpret_cast<const float*>(bp + 16 * MT + m * 4u);
-    g.t0[0] = __uint_as_float(e.y);
-    g.t[0] = t < e.w ? t : 0xffffffffu;
+    g.bias[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(trs, e.z + wofs + lc_bias, 0u, 0));
+    g.t0[0] = t < e.w ? __uint_as_float(e.y) : __builtin_nanf("");
+    g.t[0] = t;
 }
 
 // a + DPP-moved b (row-local patterns, every source lane active, so no lane
@@ -493,18 +498,29 @@ __device__ __forceinline__ float entry_dist(const DevIndex& ix, const FastLds& s
 // a round (cnt <= capacity - 64 on entry).
 template <int MT, int KT, int NC>
 __device__ __forceinline__ void fs8w_consume(const DevIndex& ix, const FastLds& s, const float* lut_static,
-                                             const RoundRegs<MT>& g, uint32_t F, uint64_t* reg,
+                                             const RoundRegs<MT>& g, float Ff, uint64_t* reg,
                                              uint32_t& cnt) {
-    const uint32_t fk = fkey(entry_dist<MT, KT, NC>(ix, s, lut_static, g));
-    const bool take = g.t[0] != 0xffffffffu && fk <= F;
+    const float dist = entry_dist<MT, KT, NC>(ix, s, lut_static, g);
+    const bool take = dist <= Ff;  // NaN (no entry) never
     const uint64_t mask = __ballot(take);
     if (mask == 0) return;  // wave-uniform
     if (take) {
         const uint32_t below =
             __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-        reg[cnt + below] = ((uint64_t)fk << 32) | g.t[0];
+        reg[cnt + below] = ((uint64_t)fkey(dist) << 32) | g.t[0];
     }
     cnt += (uint32_t)__popcll(mask);
+}
+
+// The float threshold equivalent to a key filter F on the approximate
+// distances: x <= filter_float(F) exactly when fkey(x) <= F, for finite x
+// other than -0.0 (an approximate distance is (t0 + b(x)) + sum with
+// t0 = ||q - c||^2 >= +0, so it is never -0.0).
+__device__ __forceinline__ float filter_float(uint32_t F) {
+    uint32_t b = (F & 0x80000000u) ? (F & 0x7fffffffu) : ~F;  // fkey_to_float
+    b = F >= 0xff800000u ? 0x7f800000u : b;                   // every finite distance
+    b = F == 0x7fffffffu ? 0x80000001u : b;                   // the negative ones
+    return __uint_as_float(__builtin_amdgcn_readfirstlane(b));  // wave-uniform
 }
 
 // Second pass (after the regions are merged into one buffer): append the keys
@@ -516,8 +532,9 @@ __device__ __forceinline__ void fs8_consume_retry(const DevIndex& ix, FastLds& s
                                                   const RoundRegs<MT>& g, uint32_t hi, uint32_t lo,
                                                   uint32_t cap, int parity) {
     const int lane = threadIdx.x & 63;
-    const uint32_t fk = fkey(entry_dist<MT, KT, NC>(ix, s, lut_static, g));
-    const bool take = g.t[0] != 0xffffffffu && fk <= hi && fk > lo;
+    const float dist = entry_dist<MT, KT, NC>(ix, s, lut_static, g);
+    const uint32_t fk = fkey(dist);
+    const bool take = dist == dist && fk <= hi && fk > lo;  // NaN: no entry
     const uint64_t mask = __ballot(take);
     const uint32_t tot = (uint32_t)__popcll(mask);
     if (tot == 0) return;  // wave-uniform
@@ -860,7 +877,8 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     __syncthreads();  // pref (wave 0) and term0 complete
     for (int p = tid; p < P; p += VGPU_BLOCK)
         s.bt[p] = make_uint4(s.lbeg[p] - s.pref[p], __float_as_uint(s.term0[p]),
-                             TR ? 16u * s.tbo[p] - s.pref[p] : 0u, s.pref[p] + s.llen[p]);
+                             TR ? (uint32_t)(MT + 4) * (16u * s.tbo[p] - s.pref[p]) : 0u,
+                             s.pref[p] + s.llen[p]);
     if (tid < 64) {  // max ||q - c||^2 for tau
         float t0max = 0.0f;
         for (int p = lane; p < P; p += 64) t0max = fmaxf(t0max, s.term0[p]);
@@ -894,8 +912,16 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     bool lost = false;
     int cur = 0;
     RoundRegs<MT> ga, gb, gc;
+    // transposed blocks (unused by the row layout)
+    const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(ix.tblocks), (short)0, (int)ix.tblk_bytes, 0x00020000);
+    uint32_t lc_code = 0, lc_bias = 0;
+    if constexpr (TR) {
+        lc_code = (uint32_t)(MT + 4) * ((uint32_t)lane & 48u) + ((uint32_t)lane & 15u) * 16u;
+        lc_bias = (uint32_t)(MT + 4) * ((uint32_t)lane & 48u) + 16u * MT + ((uint32_t)lane & 15u) * 4u;
+    }
     auto fetch = [&](uint32_t rb, RoundRegs<MT>& g) {
-        if constexpr (TR) fs8t_fetch<MT>(ix, s, sr, rb, total, P, cur, g);
+        if constexpr (TR) fs8t_fetch<MT>(trs, s, sr, rb, lc_code, lc_bias, P, cur, g);
         else fs8_fetch<MT>(ix, s, sr, rb, total, P, cur, g);
     };
     if (total > 0) {
@@ -908,7 +934,7 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
         fetch(rbase + 2 * FS_ROUND, NEXT);                                                   \
         const uint32_t shared = __atomic_load_n(&s.misc[8], __ATOMIC_RELAXED);               \
         Fused = F;                                                                           \
-        fs8w_consume<MT, KT, NC>(ix, s, slut, CONSUME, F, reg, cnt);                         \
+        fs8w_consume<MT, KT, NC>(ix, s, slut, CONSUME, filter_float(F), reg, cnt);           \
         if (cnt > capw) {                                                                    \
             const uint32_t before = cnt;                                                     \
             thr = fs8w_flush(reg, cnt, (uint32_t)keep - 1u, capw, &lost);                    \

@@ -469,14 +469,16 @@ void IvfpqIndex::upload_index() {
         d_bias.reserve(n);
         dix.bias = d_bias.p;
         launch_bias(dix, d_bias.p, stream);
-        if (scan8_fast_blocks_supported((int)M, (int)K, (int)ds)) {
-            std::vector<uint32_t> toff(L + 1, 0);
-            for (size_t l = 0; l < L; l++)
-                toff[l + 1] = toff[l] + (uint32_t)((offsets[l + 1] - offsets[l] + 15) / 16);
+        std::vector<uint32_t> toff(L + 1, 0);
+        for (size_t l = 0; l < L; l++)
+            toff[l + 1] = toff[l] + (uint32_t)((offsets[l + 1] - offsets[l] + 15) / 16);
+        const size_t tbytes = ((size_t)toff[L] + 1) * TBLK_BYTES(M);  // + one block of slack
+        if (scan8_fast_blocks_supported((int)M, (int)K, (int)ds) && tbytes < ((size_t)1 << 31)) {
             d_tblk_off.upload(toff.data(), L + 1, stream);
-            d_tblocks.reserve((size_t)toff[L] * TBLK_BYTES(M) + TBLK_BYTES(M));
+            d_tblocks.reserve(tbytes);
             dix.tblk_off = d_tblk_off.p;
             dix.tblocks = d_tblocks.p;
+            dix.tblk_bytes = (uint32_t)tbytes;
             launch_tblocks(dix, d_tblocks.p, stream);
         } else {
             d_tblocks.release();

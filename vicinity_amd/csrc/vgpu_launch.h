@@ -33,6 +33,7 @@ struct DevIndex {
     // Entries past the end of the list have code 0 and b(x) 0.
     const uint8_t* tblocks = nullptr;
     const uint32_t* tblk_off = nullptr;// [L+1]
+    uint32_t tblk_bytes = 0;           // bytes of tblocks (< 2^31: 32-bit buffer offsets)
     float cmax = 0.f;                  // max ||c||
     float rmax = 0.f;                  // max ||decoded residual||
 };
