@@ -193,7 +193,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile() if args.n == 1_000_000 else None,
-                     "kernel": "scan8_fast_kernel<16,256>", "kernel_ms": round(scan_ms, 4),
+                     "kernel": "scan8_fast_kernel<16,256,8,1>", "kernel_ms": round(scan_ms, 4),
                      "algorithmic_bytes_per_launch": int(scan_bytes),
                      "candidates_per_launch": int(cands)},
         "phases_ms": phases,
