@@ -422,19 +422,40 @@ __device__ __forceinline__ void fs8t_fetch(__amdgpu_buffer_rsrc_t trs, const Fas
     const uint32_t wb = rbase + wave * 64u;  // window start
     const uint32_t tb = wb + (lane & 48u);   // the row's block start
     const uint32_t t = tb + m;
-    const uint4 e = slot_record(s, sr, P, wb, tb, cw);
     const uint32_t wofs = (uint32_t)(MT + 4) * wb;
+    uint32_t base;  // block byte offset of the lane's row, less (MT + 4) tb
+    float t0;
+    bool uniform = false;
+    if (P <= 64) {
+        // Usually one list covers the whole window (no list starts inside it
+        // and none ends before its last entry): its record is read into
+        // scalars once and the lanes share it.
+        const uint64_t le = __ballot(sr.pref <= wb), lt = __ballot(sr.pref < wb + 64u);
+        const int c = (int)__popcll(le) - 1;
+        const uint32_t ez = __builtin_amdgcn_readlane(sr.bt.z, c), ey = __builtin_amdgcn_readlane(sr.bt.y, c);
+        const uint32_t ew = __builtin_amdgcn_readlane(sr.bt.w, c);
+        if (lt == le && ew >= wb + 64u) {
+            uniform = true;
+            base = ez + wofs;
+            t0 = __uint_as_float(ey);
+        }
+    }
+    if (!uniform) {
+        const uint4 e = slot_record(s, sr, P, wb, tb, cw);
+        base = e.z + wofs;
+        t0 = t < e.w ? __uint_as_float(e.y) : __builtin_nanf("");
+    }
 #pragma unroll
     for (int gi = 0; gi < MT / 16; gi++) {
         // the whole offset in the range-checked VGPR part (soffset is not checked)
-        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(trs, e.z + wofs + lc_code + (uint32_t)gi * 256u, 0u, 0);
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(trs, base + lc_code + (uint32_t)gi * 256u, 0u, 0);
         g.row[0].w[4 * gi] = x.x;
         g.row[0].w[4 * gi + 1] = x.y;
         g.row[0].w[4 * gi + 2] = x.z;
         g.row[0].w[4 * gi + 3] = x.w;
     }
-    g.bias[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(trs, e.z + wofs + lc_bias, 0u, 0));
-    g.t0[0] = t < e.w ? __uint_as_float(e.y) : __builtin_nanf("");
+    g.bias[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(trs, base + lc_bias, 0u, 0));
+    g.t0[0] = t0;
     g.t[0] = t;
 }
 
@@ -452,16 +473,51 @@ __device__ __forceinline__ float add_dpp(float a, float b) {
 // belong to entry j ^ m of its row; four exchange stages with the lanes m ^ 1,
 // m ^ 2, m ^ 7 and m ^ 8 (each halving the registers still needed) leave the
 // sum of entry m in v[0].  Every lane of the wave must be active.
+// c * 64 + off for the code c held in the low (HI = 0) or high (HI = 1)
+// 16-bit half of h (the other half is ignored): one v_mad_u32_u16 with op_sel.
+template <int HI>
+__device__ __forceinline__ uint32_t code_addr(uint32_t h, uint32_t off) {
+    uint32_t a;
+    if constexpr (HI) asm("v_mad_u32_u16 %0, %1, 64, %2 op_sel:[1,0,0,0]" : "=v"(a) : "v"(h), "v"(off));
+    else asm("v_mad_u32_u16 %0, %1, 64, %2" : "=v"(a) : "v"(h), "v"(off));
+    return a;
+}
+
 template <int MT, int NC>
 __device__ __forceinline__ float trow_sum(const CodeRow<MT>& r, const float* __restrict__ lutl) {
     float v[16];
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
+    if constexpr (NC == 1) {
+        // Byte offsets c * 64 + 4 m: codes 0 and 2 of a word are split into
+        // 16-bit halves by a mask, codes 1 and 3 by a byte permute, and each
+        // offset is one multiply-add on a half (1.5 instructions per code).
+        const float* lut0 = lutl - (threadIdx.x & 15);
+        const uint32_t m4 = (threadIdx.x & 15u) * 4u;
 #pragma unroll
         for (int gi = 0; gi < MT / 16; gi++) {
-            const uint32_t c = (r.w[4 * gi + (j >> 2)] >> (8 * (j & 3))) & 0xffu;
-            const float x = lutl[(gi * 256 + (int)c) * NC * 16];
-            v[j] = gi == 0 ? x : v[j] + x;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t w = r.w[4 * gi + i];
+                const uint32_t h02 = w & 0x00ff00ffu;                       // codes 0, 2
+                const uint32_t h13 = __builtin_amdgcn_perm(0u, w, 0x0c030c01u);  // codes 1, 3
+                const uint32_t o[4] = {code_addr<0>(h02, m4), code_addr<0>(h13, m4), code_addr<1>(h02, m4),
+                                       code_addr<1>(h13, m4)};
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const float x = *reinterpret_cast<const float*>(
+                        reinterpret_cast<const char*>(lut0 + gi * 256 * 16) + o[b]);
+                    v[4 * i + b] = gi == 0 ? x : v[4 * i + b] + x;
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+#pragma unroll
+            for (int gi = 0; gi < MT / 16; gi++) {
+                const uint32_t c = (r.w[4 * gi + (j >> 2)] >> (8 * (j & 3))) & 0xffu;
+                const float x = lutl[(gi * 256 + (int)c) * NC * 16];
+                v[j] = gi == 0 ? x : v[j] + x;
+            }
         }
     }
 #pragma unroll
@@ -911,7 +967,7 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     uint32_t cnt = 0, thr = 0xffffffffu, F = 0xffffffffu, Fused = 0xffffffffu, evicted = 0, flushes = 0;
     bool lost = false;
     int cur = 0;
-    RoundRegs<MT> ga, gb, gc;
+    RoundRegs<MT> ga, gb, gc, gd;
     // transposed blocks (unused by the row layout)
     const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(ix.tblocks), (short)0, (int)ix.tblk_bytes, 0x00020000);
@@ -927,11 +983,12 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     if (total > 0) {
         fetch(0, ga);
         fetch(FS_ROUND, gb);
+        fetch(2 * FS_ROUND, gc);
     }
 #define FS8_STEP(CONSUME, NEXT, R)                                                           \
     {                                                                                        \
         const uint32_t rbase = (R) * FS_ROUND;                                               \
-        fetch(rbase + 2 * FS_ROUND, NEXT);                                                   \
+        fetch(rbase + 3 * FS_ROUND, NEXT);                                                   \
         const uint32_t shared = __atomic_load_n(&s.misc[8], __ATOMIC_RELAXED);               \
         Fused = F;                                                                           \
         fs8w_consume<MT, KT, NC>(ix, s, slut, CONSUME, filter_float(F), reg, cnt);           \
@@ -948,12 +1005,24 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
             const uint32_t sh = __builtin_amdgcn_readfirstlane(shared);                      \
             F = thr < sh ? thr : sh;                                                         \
         }                                                                                    \
-        if (rbase + FS_ROUND >= total) break;                                                \
     }
-    for (uint32_t r = 0; r * FS_ROUND < total; r += 3) {
-        FS8_STEP(ga, gc, r)
+    // Whole groups of four rounds in the loop, which has no other exit (an
+    // exit inside would make the loads of its first round look outstanding
+    // at the loop head and drain the ring there), then the last 0 .. 3.
+    const uint32_t nr = (total + FS_ROUND - 1) / FS_ROUND;  // rounds
+    uint32_t r = 0;
+    for (; r + 4 <= nr; r += 4) {
+        FS8_STEP(ga, gd, r)
         FS8_STEP(gb, ga, r + 1)
         FS8_STEP(gc, gb, r + 2)
+        FS8_STEP(gd, gc, r + 3)
+    }
+    if (r < nr) {
+        FS8_STEP(ga, gd, r)
+        if (r + 1 < nr) {
+            FS8_STEP(gb, ga, r + 1)
+            if (r + 2 < nr) FS8_STEP(gc, gb, r + 2)
+        }
     }
 #undef FS8_STEP
     {
@@ -1108,14 +1177,24 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
                     // Both lanes hold the full code row.
                     float ev[MT / 2];  // this lane's codebooks 2t + half
                     const float* rrow = s.lut + (size_t)p * D + half * DS;
+                    constexpr int TB = MT / 2 < 4 ? MT / 2 : 4;  // codebook pairs whose loads fly together
 #pragma unroll
-                    for (int t = 0; t < MT / 2; t++) {
+                    for (int t0 = 0; t0 < MT / 2; t0 += TB) {
+                    float4 Ab[TB], Bb[TB];
+#pragma unroll
+                    for (int tb = 0; tb < TB; tb++) {  // every load of the batch first
+                        const int t = t0 + tb;
                         const uint32_t w = row.w[t >> 1];
                         const uint32_t c0 = (w >> (16 * (t & 1))) & 0xffu, c1 = (w >> (16 * (t & 1) + 8)) & 0xffu;
-                        const float4 A = *reinterpret_cast<const float4*>(
+                        Ab[tb] = *reinterpret_cast<const float4*>(
                             ix.codebooks + ((size_t)(2 * t) * KT + c0) * DS + 4 * half);
-                        const float4 B = *reinterpret_cast<const float4*>(
+                        Bb[tb] = *reinterpret_cast<const float4*>(
                             ix.codebooks + ((size_t)(2 * t + 1) * KT + c1) * DS + 4 * half);
+                    }
+#pragma unroll
+                    for (int tb = 0; tb < TB; tb++) {
+                        const int t = t0 + tb;
+                        const float4 A = Ab[tb], B = Bb[tb];
                         const float4 snd = half ? A : B;
                         float4 rcv;
                         rcv.x = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(snd.x), 0xB1, 0xF, 0xF, true));
@@ -1132,6 +1211,7 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
                             e = __fadd_rn(e, __fmul_rn(diff, diff));
                         }
                         ev[t] = e;
+                    }
                     }
 #pragma unroll
                     for (int t = 0; t < MT / 2; t++) {  // lane 0: e_2t, then the partner's e_2t+1
