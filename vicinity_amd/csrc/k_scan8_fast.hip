@@ -790,11 +790,12 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
         constexpr int LB = LW < 16 ? LW : 16;     // lines whose loads fly together
         static_assert(LW % LB == 0, "line batches");
         const int m16 = lane >> 2, j = lane & 3;
-        const int wv_ = tid >> 6;
+        const int wv_ = (int)__builtin_amdgcn_readfirstlane((uint32_t)tid >> 6);
 #pragma unroll 1
         for (int gi = 0; gi < MT / 16; gi++) {
             const int m = gi * 16 + m16;
-            // the query values this lane multiplies
+            // the query values this lane multiplies, scaled by -2 (exact), so
+            // the dot products below are the table entries themselves
             float qv[4];
             if constexpr (DS == 8) load_vec<4>(a.qn + (size_t)q * D + m * 8 + 4 * (j & 1), qv);
             else if constexpr (DS == 4) load_vec<4>(a.qn + (size_t)q * D + m * 4, qv);
@@ -803,40 +804,47 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
                 qv[2] = qv[0];
                 qv[3] = qv[1];
             }
-            const float* cb = ix.codebooks + (size_t)m * KT * DS + 4 * j;
+#pragma unroll
+            for (int i = 0; i < 4; i++) qv[i] = -2.0f * qv[i];
+            // line sp = (l0 + i) * 4 + wv_: a wave-uniform base, the lane's
+            // fixed byte offset, and a constant step per line
+            const char* cbw = reinterpret_cast<const char*>(ix.codebooks + (size_t)(gi * 16) * KT * DS +
+                                                            (size_t)wv_ * 16);
+            const uint32_t lo = (uint32_t)(m16 * KT * DS + 4 * j) * 4u;
 #pragma unroll 1
             for (int l0 = 0; l0 < LW; l0 += LB) {
+                const char* cbl = cbw + (size_t)l0 * (VGPU_BLOCK / 64) * 64;  // wave-uniform
                 float4 w[LB];
 #pragma unroll
-                for (int i = 0; i < LB; i++) {
-                    const int sp = (l0 + i) * (VGPU_BLOCK / 64) + wv_;  // line of this load
-                    w[i] = *reinterpret_cast<const float4*>(cb + (size_t)sp * 16);
-                }
+                for (int i = 0; i < LB; i++)
+                    w[i] = *reinterpret_cast<const float4*>(cbl + lo + i * (VGPU_BLOCK / 64) * 64);
+                // table row of line l0 * 4 + wv_; line i of the batch is 4 i CPS rows on
+                float* tl = slut + (gi * KT + (l0 * (VGPU_BLOCK / 64) + wv_) * CPS) * NC * 16 + m16;
 #pragma unroll
                 for (int i = 0; i < LB; i++) {
-                    const int sp = (l0 + i) * (VGPU_BLOCK / 64) + wv_;
+                    float* ti = tl + i * (VGPU_BLOCK / 64) * CPS * NC * 16;  // row sp * CPS
                     if constexpr (DS == 2) {
                         const float d0 = __builtin_fmaf(qv[1], w[i].y, qv[0] * w[i].x);
                         const float d1 = __builtin_fmaf(qv[3], w[i].w, qv[2] * w[i].z);
-                        const int k = sp * CPS + 2 * j;
 #pragma unroll
                         for (int c = 0; c < NC; c++) {
-                            slut[((gi * KT + k) * NC + c) * 16 + m16] = -2.0f * d0;
-                            slut[((gi * KT + k + 1) * NC + c) * 16 + m16] = -2.0f * d1;
+                            ti[(2 * j * NC + c) * 16] = d0;
+                            ti[((2 * j + 1) * NC + c) * 16] = d1;
                         }
                     } else {
                         float dp = qv[0] * w[i].x;
                         dp = __builtin_fmaf(qv[1], w[i].y, dp);
                         dp = __builtin_fmaf(qv[2], w[i].z, dp);
                         dp = __builtin_fmaf(qv[3], w[i].w, dp);
-                        int k = sp * CPS + j;
+                        int kj = j;  // codeword of the line
                         if constexpr (DS == 8) {
                             dp = add_dpp<0xB1>(dp, dp);  // + the partner half (lane j ^ 1)
-                            k = sp * CPS + (j >> 1);
+                            asm volatile("" : "+v"(dp));  // every lane adds (the move folds into it)
+                            kj = j >> 1;
                         }
                         if (DS != 8 || (j & 1) == 0) {
 #pragma unroll
-                            for (int c = 0; c < NC; c++) slut[((gi * KT + k) * NC + c) * 16 + m16] = -2.0f * dp;
+                            for (int c = 0; c < NC; c++) ti[(kj * NC + c) * 16] = dp;
                         }
                     }
                 }
