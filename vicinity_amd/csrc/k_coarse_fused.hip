@@ -32,11 +32,13 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 #define FC_QBW 2               // query blocks (16 queries each) per workgroup
 #define FC_QB (16 * FC_QBW)    // queries per workgroup
-#define FC_NH 2                // waves per query block; each takes its own tiles of a stage
-#define FC_SUB 2               // 16-centroid tiles per wave and stage
+#define FC_NH 4                // waves per query block; each takes its own tiles of a stage
+#define FC_SUB 1               // 16-centroid tiles per wave and stage
 #define FC_ST (FC_NH * FC_SUB) // tiles per stage
-#define FC_TR 8                // keys per list that enter the rank (<= FC_J)
-static_assert(FC_QBW * FC_NH * 64 == VGPU_BLOCK, "wave roles");
+#define FC_TR 4                // keys per list that enter the rank (<= FC_J)
+#define FC_THREADS (FC_QBW * FC_NH * 64)  // threads per workgroup
+#define FC_RPW (4 / FC_NH)     // rows of a lane's four that each wave finishes
+static_assert(4 % FC_NH == 0, "wave roles");
 
 // Round to nearest even bfloat16 (finite inputs).
 __device__ __forceinline__ uint32_t bf16_bits(float x) {
@@ -127,36 +129,37 @@ __device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, 
                                         const u32x4 (&al)[DT], u32x4* lds, Epi epi) {
     const u32x4* Cb = reinterpret_cast<const u32x4*>(Cb_in);
     constexpr int SC = FC_ST * DT * 4 * 16;  // chunks per stage and half
-    constexpr int PER = 2 * SC / VGPU_BLOCK;  // chunks each thread copies per stage
-    static_assert((2 * SC) % VGPU_BLOCK == 0, "stage split");
+    constexpr int PER = 2 * SC / FC_THREADS;  // chunks each thread copies per stage
+    static_assert((2 * SC) % FC_THREADS == 0, "stage split");
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
     const int h = __builtin_amdgcn_readfirstlane((tid >> 6) / FC_QBW);
     const int nst = (L + FC_ST * 16 - 1) / (FC_ST * 16);
     // A stage is 2 SC contiguous chunks of Cb (padded to whole stages), copied
-    // to LDS unchanged: slot i of thread tid is chunk i * VGPU_BLOCK + tid.
+    // to LDS unchanged: slot i of thread tid is chunk i * FC_THREADS + tid.
     // Buffer loads: per-lane offset in a VGPR, stage and slot offsets in
     // SGPRs.  Only stages below nst are fetched.
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<u32x4*>(Cb), (short)0, nst * 2 * SC * 16, 0x00020000);
     const uint32_t lofs = (uint32_t)tid * 16u;
-    // Two register sets: stage st + 1 waits in one while stage st + 2 loads
-    // into the other, so a stage's loads have two stages to arrive.
-    u32x4 pa[PER], pb[PER];
+    // One register set: stage st + 1 is stored from it at the start of stage
+    // st and stage st + 2 loads into it, so a stage's loads have one stage
+    // to arrive (the other waves of the CU cover the rest).
+    u32x4 pa[PER];
 #define FC_FETCH(SET, ST)                                                              \
     _Pragma("unroll") for (int i = 0; i < PER; i++) SET[i] = __builtin_amdgcn_raw_buffer_load_b128( \
-        rsrc, lofs, (uint32_t)((ST) * 2 * SC * 16 + i * VGPU_BLOCK * 16), 0);
+        rsrc, lofs, (uint32_t)((ST) * 2 * SC * 16 + i * FC_THREADS * 16), 0);
 #define FC_STORE(SET, BUF)                                                             \
-    _Pragma("unroll") for (int i = 0; i < PER; i++) lds[(size_t)(BUF) * 2 * SC + i * VGPU_BLOCK + tid] = SET[i];
+    _Pragma("unroll") for (int i = 0; i < PER; i++) lds[(size_t)(BUF) * 2 * SC + i * FC_THREADS + tid] = SET[i];
     floatx4 prev[FC_SUB];
     // Stage ST: everyone has finished stage ST - 1 (buffer (ST + 1) & 1) and
-    // stage ST's chunks are visible; SET holds stage ST + 1, then ST + 3.
+    // stage ST's chunks are visible; SET holds stage ST + 1, then ST + 2.
 #define FC_STEP(ST, SET)                                                               \
     {                                                                                  \
         const int st_ = (ST);                                                          \
         __syncthreads();                                                               \
         if (st_ + 1 < nst) {                                                           \
             FC_STORE(SET, (st_ + 1) & 1)                                               \
-            if (st_ + 3 < nst) { FC_FETCH(SET, st_ + 3) }                              \
+            if (st_ + 2 < nst) { FC_FETCH(SET, st_ + 2) }                              \
         }                                                                              \
         const u32x4* b = lds + (size_t)(st_ & 1) * 2 * SC;                             \
         floatx4 acc[FC_SUB];                                                           \
@@ -186,12 +189,7 @@ __device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, 
     FC_FETCH(pa, 0)
     FC_STORE(pa, 0)
     if (nst > 1) { FC_FETCH(pa, 1) }
-    if (nst > 2) { FC_FETCH(pb, 2) }
-    for (int st = 0; st < nst; st += 2) {
-        FC_STEP(st, pa)
-        if (st + 1 >= nst) break;
-        FC_STEP(st + 1, pb)
-    }
+    for (int st = 0; st < nst; st++) FC_STEP(st, pa)
 #undef FC_STEP
     const bool masked = nst * FC_ST * 16 > L;
 #pragma unroll
@@ -271,24 +269,25 @@ __device__ __forceinline__ void top_insert(float (&t)[J], float v) {
 // One pass of bf16x3 products.  Every (wave, lane, row) keeps the J largest
 // keys k = (a + 2) with its low IB mantissa bits replaced by the tile index
 // (a = approximate q.c; the lane's column c = lane % 16 completes the list
-// index 16 tile + c); the two waves of a query block see disjoint tiles, so a
-// row has 2 x 16 sorted lists of J.  T = the Pe-th largest of the row's 32 J
+// index 16 tile + c); the FC_NH waves of a query block see disjoint tiles, so
+// a row has FC_NH x 16 sorted lists of J.  T = the Pe-th largest of the row's
 // keys bounds the Pe-th largest approximate dot from below (Pe distinct lists
 // have keys >= T, so approximate dots >= T - 2 - E, E the packing error).  Pe
 // lists then have exact scores within eps of those, so every list among the
 // Pe exact nearest has an approximate dot within 2 eps of T - 2 - E and a key
 // >= T - 2E - 2 eps (taken with a factor 1.25 and a few ulps to spare); those
 // keys form a prefix of each list.  (T is taken over the lists' first FC_TR
-// keys, Pe <= 32 FC_TR.)  A list whose J-th key is itself above that
-// threshold may have dropped such a list: the row is then marked overflowed
-// (cand_n = CAP + 1).  After the pass wave h finishes rows 2h, 2h + 1 of each
-// lane.
+// keys, Pe <= 16 FC_NH FC_TR.)  A list whose J-th key is itself above that
+// threshold may have dropped such a list, and a row holds at most CAP
+// candidates: the row is then marked overflowed (cand_n = CAP + 1).  After the
+// pass wave h finishes rows FC_RPW h .. + FC_RPW - 1 of each lane; FC_NH waves
+// per query block keep enough waves in flight on a 256-CU part (two per SIMD
+// for a 10k-query batch).
 template <int DT, int J>
-__global__ __launch_bounds__(256) void coarse_fused_kernel(
+__global__ __launch_bounds__(FC_THREADS) void coarse_fused_kernel(
     const float* __restrict__ Q, int nq, int d, const uint4* __restrict__ Cb, int L, float cmax,
     int Pe, int IB, int normalize, float* __restrict__ qn_out, float* __restrict__ qnorm_out,
     uint32_t* __restrict__ cand, uint32_t* __restrict__ cand_n) {
-    static_assert(FC_NH == 2, "two key lists per lane");
     extern __shared__ __align__(16) char smem[];
     constexpr int CAP = 32 * J;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
@@ -302,7 +301,7 @@ __global__ __launch_bounds__(256) void coarse_fused_kernel(
 
     // ---- normalise (search.rs:55-62): sequential sum of squares per row.
     const float* src = Q + (size_t)q0 * d;
-    for (int e = tid; e < FC_QB * d; e += VGPU_BLOCK) {
+    for (int e = tid; e < FC_QB * d; e += FC_THREADS) {
         const int r = e / d;
         tile[r * st + e % d] = r < rows ? src[e] : 0.0f;
     }
@@ -319,7 +318,7 @@ __global__ __launch_bounds__(256) void coarse_fused_kernel(
     }
     __syncthreads();
     if (normalize) {
-        for (int e = tid; e < FC_QB * d; e += VGPU_BLOCK) {
+        for (int e = tid; e < FC_QB * d; e += FC_THREADS) {
             const int r = e / d, j = e % d;
             const float nrm = snorm[r];
             const float v = tile[r * st + j];
@@ -359,30 +358,28 @@ __global__ __launch_bounds__(256) void coarse_fused_kernel(
 #pragma unroll
     for (int r = 0; r < 4; r++)
 #pragma unroll
-        for (int j = 0; j < J; j++) mg[((((qb * 2 + h) * 4 + r) * J + j) << 6) + lane] = top[r][j];
+        for (int j = 0; j < J; j++) mg[((((qb * FC_NH + h) * 4 + r) * J + j) << 6) + lane] = top[r][j];
     __syncthreads();
 
-    // ---- rows 2h, 2h + 1: threshold, overflow test and candidate output.
+    // ---- rows FC_RPW h .. + FC_RPW - 1: threshold, overflow test and output.
 #pragma unroll
-    for (int rr = 0; rr < 2; rr++) {
-        const int r = 2 * h + rr;
+    for (int rr = 0; rr < FC_RPW; rr++) {
+        const int r = FC_RPW * h + rr;
         const int row = qb * 16 + 4 * g + r;
-        float own[J], oth[J];
+        float lst[FC_NH][J];  // the FC_NH waves' lists of this (lane, row)
 #pragma unroll
-        for (int j = 0; j < J; j++) {
-            own[j] = h ? top[2 + rr][j] : top[rr][j];
-            oth[j] = mg[((((qb * 2 + (1 - h)) * 4 + r) * J + j) << 6) + lane];
-        }
+        for (int w = 0; w < FC_NH; w++)
+#pragma unroll
+            for (int j = 0; j < J; j++) lst[w][j] = mg[((((qb * FC_NH + w) * 4 + r) * J + j) << 6) + lane];
         // T = the Pe-th largest of the lists' first FC_TR keys (a subset, so
         // Pe distinct lists still have keys >= T; T is below the full rank
         // only when a list holds more than FC_TR of the top Pe).
-        uint32_t kv[2 * FC_TR];
+        uint32_t kv[FC_NH * FC_TR];
 #pragma unroll
-        for (int j = 0; j < FC_TR; j++) {
-            kv[j] = fkey(own[j]);
-            kv[FC_TR + j] = fkey(oth[j]);
-        }
-        const float T = fkey_to_float(group16_rank<2 * FC_TR>(kv, 32 * FC_TR - Pe));
+        for (int w = 0; w < FC_NH; w++)
+#pragma unroll
+            for (int j = 0; j < FC_TR; j++) kv[w * FC_TR + j] = fkey(lst[w][j]);
+        const float T = fkey_to_float(group16_rank<FC_NH * FC_TR>(kv, 16 * FC_NH * FC_TR - Pe));
         const float qb_norm = snorm[FC_QB + row];
         const float qc = qb_norm * cmax;
         const float u = 5.9604645e-08f;
@@ -391,14 +388,16 @@ __global__ __launch_bounds__(256) void coarse_fused_kernel(
         const float ub = __uint_as_float((__float_as_uint(qc + 2.0f) & 0x7f800000u) + 0x00800000u);
         const float E = ((float)(1u << IB) + 0.5f) * ub * u;
         const float kthr = T - (2.0f * E + 2.5f * coarse_eps_bf16(d, qb_norm, cmax) + 8.0f * ub * u);
-        uint32_t n0 = 0, n1 = 0;
+        uint32_t nw[FC_NH], n = 0;
+        bool over = false;
 #pragma unroll
-        for (int j = 0; j < J; j++) {
-            n0 += own[j] >= kthr ? 1u : 0u;
-            n1 += oth[j] >= kthr ? 1u : 0u;
+        for (int w = 0; w < FC_NH; w++) {
+            nw[w] = 0;
+#pragma unroll
+            for (int j = 0; j < J; j++) nw[w] += lst[w][j] >= kthr ? 1u : 0u;
+            n += nw[w];
+            over = over || lst[w][J - 1] >= kthr;
         }
-        const uint32_t n = n0 + n1;
-        const bool over = own[J - 1] >= kthr || oth[J - 1] >= kthr;
         // exclusive prefix of n over the 16 lanes of the group
         uint32_t incl = n;
 #pragma unroll
@@ -407,16 +406,19 @@ __global__ __launch_bounds__(256) void coarse_fused_kernel(
             if (c >= o) incl += x;
         }
         const uint32_t total = __shfl(incl, (lane & 48) | 15, 64);
-        const bool any_over = __ballot(over) >> (16 * g) & 0xffffull;
+        // a list that may have dropped a member, or more candidates than a row holds
+        const bool any_over = (__ballot(over) >> (16 * g) & 0xffffull) || total > (uint32_t)CAP;
         if (row < rows) {
             uint32_t* out = cand + (size_t)(q0 + row) * CAP + (incl - n);
             if (!any_over) {
+                uint32_t o = 0;
 #pragma unroll
-                for (int j = 0; j < J; j++)
-                    if ((uint32_t)j < n0) out[j] = 16u * (__float_as_uint(own[j]) & ~kmask) + (uint32_t)c;
+                for (int w = 0; w < FC_NH; w++) {
 #pragma unroll
-                for (int j = 0; j < J; j++)
-                    if ((uint32_t)j < n1) out[n0 + j] = 16u * (__float_as_uint(oth[j]) & ~kmask) + (uint32_t)c;
+                    for (int j = 0; j < J; j++)
+                        if ((uint32_t)j < nw[w]) out[o + j] = 16u * (__float_as_uint(lst[w][j]) & ~kmask) + (uint32_t)c;
+                    o += nw[w];
+                }
             }
             if (c == 0) cand_n[q0 + row] = any_over ? (uint32_t)CAP + 1u : total;
         }
@@ -442,7 +444,7 @@ static void launch_fused(const float* Q, int nq, int d, const uint4* Cb, int L, 
     while ((1 << IB) < (L + 15) / 16) IB++;
     auto k = coarse_fused_kernel<DT, J>;
     ensure_dyn_lds((const void*)k, lds);
-    hipLaunchKernelGGL(k, dim3((nq + FC_QB - 1) / FC_QB), dim3(VGPU_BLOCK), lds, s, Q, nq, d, Cb, L, cmax,
+    hipLaunchKernelGGL(k, dim3((nq + FC_QB - 1) / FC_QB), dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, cmax,
                        Pe, IB, normalize, qn, qnorm, cand, cand_n);
 }
 
@@ -527,7 +529,7 @@ void launch_coarse_topp(const uint32_t* cand, const uint32_t* cand_n, int P, con
 // ---- test entry: the bf16x3 dot products of the fused kernel ------------
 // D[q][c] = Q[q] . C[c] through fc_pass (Q already normalised or not).
 template <int DT>
-__global__ __launch_bounds__(256) void coarse_bf16x3_dots_kernel(const float* __restrict__ Q, int nq,
+__global__ __launch_bounds__(FC_THREADS) void coarse_bf16x3_dots_kernel(const float* __restrict__ Q, int nq,
                                                                  int d, const uint4* __restrict__ Cb,
                                                                  int L, float* __restrict__ D) {
     extern __shared__ __align__(16) char smem[];
@@ -555,19 +557,19 @@ void launch_coarse_bf16x3_dots(const float* Q, int nq, int d, const uint4* Cb, i
     switch (DT) {
         case 1:
             ensure_dyn_lds((const void*)coarse_bf16x3_dots_kernel<1>, lds);
-            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<1>, grid, dim3(256), lds, s, Q, nq, d, Cb, L, D);
+            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<1>, grid, dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, D);
             break;
         case 2:
             ensure_dyn_lds((const void*)coarse_bf16x3_dots_kernel<2>, lds);
-            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<2>, grid, dim3(256), lds, s, Q, nq, d, Cb, L, D);
+            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<2>, grid, dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, D);
             break;
         case 3:
             ensure_dyn_lds((const void*)coarse_bf16x3_dots_kernel<3>, lds);
-            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<3>, grid, dim3(256), lds, s, Q, nq, d, Cb, L, D);
+            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<3>, grid, dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, D);
             break;
         default:
             ensure_dyn_lds((const void*)coarse_bf16x3_dots_kernel<4>, lds);
-            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<4>, grid, dim3(256), lds, s, Q, nq, d, Cb, L, D);
+            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<4>, grid, dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, D);
             break;
     }
 }
