@@ -143,6 +143,24 @@ int vgpu_ivfpq_last_stats(const vgpu_ivfpq *h, vgpu_search_stats *out);
  * call's final wait; the other phase times read 0). */
 int vgpu_ivfpq_set_profiling(vgpu_ivfpq *h, int enabled);
 
+/* Filtered search.  IVFPQIndex::with_filtering (search.rs:413-435): switch
+ * per-document categories on, before build (VGPU_ERR_ALREADY_BUILT after). */
+int vgpu_ivfpq_enable_filtering(vgpu_ivfpq *h);
+/* IVFPQIndex::add_metadata (search.rs:439-475), the filter field only: the
+ * document's category 0..63, or -1 when its metadata lacks the field (it then
+ * never matches).  Outside -1..63: VGPU_ERR_INVALID_PARAMETER; filtering off:
+ * VGPU_ERR_UNSUPPORTED.  Lists keep the categories their members had at build
+ * time in their bitmasks (search.rs:626-648); matching reads the current ones. */
+int vgpu_ivfpq_set_category(vgpu_ivfpq *h, uint32_t doc_id, int64_t category);
+/* IVFPQIndex::search_with_filter (search.rs:1407-1549) with
+ * MetadataFilter::Equals(filter field, Int(category)): up to k (doc_id,
+ * distance) pairs of documents carrying the category, ascending; the probe
+ * widens to every list when the probed ones hold fewer than k matches.
+ * Distances use the reference's table arithmetic for every ksub. */
+int vgpu_ivfpq_search_filtered(vgpu_ivfpq *h, const float *query, size_t dim, size_t k,
+                               int64_t category, uint32_t *out_ids, float *out_dists,
+                               size_t *out_len);
+
 /* The probed lists of each query in probe order (search.rs:1602-1617),
  * lists u32[nq*nprobe]; returns the probe count per query in *out_p. */
 int vgpu_ivfpq_probe_batch(vgpu_ivfpq *h, const float *queries, size_t nq, size_t dim,

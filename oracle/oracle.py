@@ -23,6 +23,7 @@ _u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
 _u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
 _u64p = np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
 _i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
 _sz = ctypes.c_size_t
 
@@ -80,6 +81,10 @@ def lib():
         L.or_ivfpq_search_batch.restype = ctypes.c_int
         L.or_ivfpq_search_batch.argtypes = [ctypes.POINTER(_Index), _f32p, _sz, _sz, _sz, _sz,
                                             ctypes.c_int, _i64p, _f32p]
+        L.or_ivfpq_search_filtered.restype = ctypes.c_long
+        L.or_ivfpq_search_filtered.argtypes = [ctypes.POINTER(_Index), _u64p, _i8p, _f32p, _sz,
+                                               _sz, ctypes.c_int, _u32p, _f32p]
+        L.or_list_masks.argtypes = [ctypes.POINTER(_Index), _i8p, _u64p]
         L.or_ivfpq_probe.restype = _sz
         L.or_ivfpq_probe.argtypes = [ctypes.POINTER(_Index), _f32p, _sz, _u32p, _f32p]
         L.or_assign_cosine.argtypes = [_f32p, _sz, _f32p, _sz, _sz, _u32p]
@@ -266,6 +271,26 @@ class Index:
         if rc != 0:
             raise RuntimeError("oracle batch search failed")
         return ids, dists
+
+    def list_masks(self, cat):
+        """search.rs:626-648: per-list category bitmask from per-vector categories."""
+        masks = np.empty(max(self._s.L, 1), np.uint64)
+        lib().or_list_masks(ctypes.byref(self._s), _c(cat, np.int8), masks)
+        return masks[:self._s.L]
+
+    def search_filtered(self, q, k, nprobe, category, cat, list_mask=None):
+        """search.rs:1407-1549: cat = category per vector (-1 none); list_mask defaults
+        to the masks of cat (lists built with the current metadata)."""
+        cat = _c(cat, np.int8)
+        if list_mask is None:
+            list_mask = self.list_masks(cat)
+        ids = np.empty(max(k, 1), np.uint32)
+        dists = np.empty(max(k, 1), np.float32)
+        m = lib().or_ivfpq_search_filtered(ctypes.byref(self._s), _c(list_mask, np.uint64), cat,
+                                           _c(q, np.float32), k, nprobe, category, ids, dists)
+        if m < 0:
+            raise ValueError("category outside 0..63")
+        return ids[:m], dists[:m]
 
     def probe(self, q, nprobe):
         lists = np.empty(max(nprobe, 1), np.uint32)

@@ -9,7 +9,8 @@
  *                          add_slice 488-512, build 546-787, training_indices
  *                          789-814, build_scan_caches 816-848, search 1087-1093,
  *                          search_reranked 1117-1158, search_approx_internal_observed
- *                          1175-1391, find_nearest_centroids 1602-1617
+ *                          1175-1391, search_with_filter 1407-1549,
+ *                          find_nearest_centroids 1602-1617
  *   src/ivf_pq/pq.rs       fit 75-124, quantize 136-161, compute_adc_table_into
  *                          196-266, distance_with_table 272-279, reconstruct 284-290
  *   src/pq_simd.rs         adc_batch_distances_into 99-115, adc_batch_256_into
@@ -36,6 +37,12 @@
  *   or_nearest_centroids                   brute force sort of float64 scores
  *   or_ivfpq_search                        full probe == exhaustive ADC scan
  *                                          over reconstruct (search.rs:2589-2645)
+ *   or_ivfpq_search_filtered / or_list_masks  the widening case of
+ *                                          search.rs:2652-2688 (the three tagged
+ *                                          documents behind nprobe = 1), full
+ *                                          probe == exhaustive scan of the
+ *                                          category over reconstruct, results
+ *                                          carry the category
  *   or_pq_encode                           argmin property (pq.rs:485-551)
  *   or_kmeans / or_ivfpq_build             the reference trains with the `clump`
  *                                          crate (^0.7.0, absent): this k-means
@@ -500,6 +507,80 @@ long or_ivfpq_search_reranked(const or_index *ix, const float *query, size_t k,
     free(qn);
     free(keys);
     return (long)r;
+}
+
+/* search.rs:1407-1549 (search_with_filter, MetadataFilter::Equals on the
+ * filter field): list_mask[L] holds each list's build-time category bitmask
+ * (search.rs:626-648), cat[n] each vector's current category (-1: none).  The
+ * nprobe nearest lists are visited in probe order, lists without the category
+ * bit skipped; each visited list's table (pq.rs:196-266) scores its members of
+ * the category with distance_with_table (pq.rs:272-279, for every ksub: this
+ * path never takes FastScan).  Fewer than k matches with lists left unvisited:
+ * every list is visited in index order, the visited ones skipped
+ * (:1540-1545).  Then top-k (:1548, :64-75). */
+long or_ivfpq_search_filtered(const or_index *ix, const uint64_t *list_mask,
+                              const int8_t *cat, const float *query, size_t k,
+                              size_t nprobe, int category, uint32_t *out_ids,
+                              float *out_dists) {
+    if (category < 0 || category > 63) return -1; /* :1435-1450 */
+    size_t d = ix->d, M = ix->M, K = ix->K, ds = ix->ds, L = ix->L;
+    const uint64_t bit = 1ull << category;
+    float *qn = (float *)malloc(d * sizeof(float));
+    float *res = (float *)malloc(d * sizeof(float));
+    float *table = (float *)malloc(M * K * sizeof(float));
+    uint32_t *order = (uint32_t *)malloc((L ? L : 1) * sizeof(uint32_t));
+    char *scanned = (char *)calloc(L ? L : 1, 1);
+    uint64_t *keys = (uint64_t *)malloc((ix->n ? ix->n : 1) * sizeof(uint64_t));
+    or_normalize(query, d, qn); /* :1462-1468 */
+    size_t P = nprobe < L ? nprobe : L;
+    size_t no = or_nearest_centroids(qn, ix->centroids, L, d, P, order, NULL); /* :1471 */
+    size_t nc = 0;
+    for (;;) {
+        for (size_t o = 0; o < no; o++) {
+            uint32_t l = order[o];
+            if (scanned[l]) continue;
+            scanned[l] = 1;
+            if ((list_mask[l] & bit) == 0) continue; /* :1504-1506 */
+            const float *c = ix->centroids + (size_t)l * d;
+            for (size_t i = 0; i < d; i++) res[i] = qn[i] - c[i]; /* :1509-1512 */
+            or_adc_table(ix->codebooks, M, K, ds, res, table);     /* :1514 */
+            for (uint64_t p = ix->list_offsets[l]; p < ix->list_offsets[l + 1]; p++) {
+                uint32_t v = ix->list_ids[p];
+                if (cat[v] != category) continue; /* metadata_store.matches, :1521 */
+                float dist = or_distance_with_table(table, M, K, ix->codes + (size_t)v * M);
+                keys[nc++] = cand_key(dist, v);
+            }
+        }
+        if (nc >= k || no == L) break; /* :1540 */
+        for (size_t l = 0; l < L; l++) order[l] = (uint32_t)l; /* :1545 */
+        no = L;
+    }
+    size_t m = top_k_keys(keys, nc, k);
+    for (size_t i = 0; i < m; i++) {
+        uint32_t vidx = (uint32_t)keys[i];
+        out_ids[i] = ix->doc_ids ? ix->doc_ids[vidx] : vidx;
+        out_dists[i] = key_dist(keys[i]);
+    }
+    free(qn);
+    free(res);
+    free(table);
+    free(order);
+    free(scanned);
+    free(keys);
+    return (long)m;
+}
+
+/* search.rs:626-648: a list's bitmask is the OR of 1 << category over its
+ * members that carry a category. */
+void or_list_masks(const or_index *ix, const int8_t *cat, uint64_t *list_mask) {
+    for (size_t l = 0; l < ix->L; l++) {
+        uint64_t msk = 0;
+        for (uint64_t p = ix->list_offsets[l]; p < ix->list_offsets[l + 1]; p++) {
+            int c = cat[ix->list_ids[p]];
+            if (c >= 0 && c < 64) msk |= 1ull << c;
+        }
+        list_mask[l] = msk;
+    }
 }
 
 /* ---- batch: python.rs:744-793 (pad with -1 / +inf), run on a thread pool

@@ -92,6 +92,14 @@ long or_ivfpq_search_reranked(const or_index *ix, const float *query, size_t k,
 int or_ivfpq_search_batch(const or_index *ix, const float *queries, size_t nq,
                           size_t k, size_t nprobe, size_t rerank_pool,
                           int threads, int64_t *out_ids, float *out_dists);
+/* search_with_filter with an equality on the filter field: list_mask[L] the
+ * build-time category bitmasks, cat[n] the vectors' categories (-1: none).
+ * Returns the number of results (<= k), -1 for a category outside 0..63. */
+long or_ivfpq_search_filtered(const or_index *ix, const uint64_t *list_mask,
+                              const int8_t *cat, const float *query, size_t k,
+                              size_t nprobe, int category, uint32_t *out_ids,
+                              float *out_dists);
+void or_list_masks(const or_index *ix, const int8_t *cat, uint64_t *list_mask);
 /* The probed lists of one query in probe order (ascending coarse distance). */
 size_t or_ivfpq_probe(const or_index *ix, const float *query, size_t nprobe,
                       uint32_t *lists, float *scores);

@@ -5,6 +5,7 @@ include/vicinity_gpu.h (libvicinity_gpu.so, built by vicinity_amd/csrc).
 """
 
 from ._lib import LIB_PATH, VicinityGpuError, device_available
+from .filtering import MetadataFilter
 from .flat import FlatIndex
 from . import datagen
 from .ivf_pq import MISSING_DISTANCE, MISSING_LABEL, IVFPQIndex, default_codebooks
@@ -12,6 +13,7 @@ from .ivf_pq import MISSING_DISTANCE, MISSING_LABEL, IVFPQIndex, default_codeboo
 __all__ = [
     "IVFPQIndex",
     "FlatIndex",
+    "MetadataFilter",
     "MISSING_LABEL",
     "MISSING_DISTANCE",
     "VicinityGpuError",

@@ -208,11 +208,60 @@ __device__ inline void write_out(const ScanArgs& a, ScanLds& s, int q, int n) {
     }
 }
 
+// Probed list l (slot p, entries beg .. beg + len - 1) with the reference
+// arithmetic: the residual r = q - c (search.rs:1242-1245), the table
+// LUT[m][k] = sum_j (r_j - cw_j)^2 (pq.rs:232-251; ds == 1 gives
+// 0 + diff*diff == diff*diff), then each entry's M entries summed in
+// codebook order (pq.rs:272-279).  With FILT only the entries whose category
+// byte equals cq are candidates (filtering/mod.rs:151-153, 214-218).  Every
+// thread of the block calls it.
+template <int MT, int KT, bool FILT>
+__device__ inline void scan_list(const DevIndex& ix, const ScanArgs& a, ScanLds& s, int buf,
+                                 uint32_t l, uint32_t beg, uint32_t len, int p,
+                                 const uint8_t* __restrict__ ecat, uint8_t cq) {
+    const int tid = threadIdx.x;
+    const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds;
+    const float* c = ix.centroids + (size_t)l * d;
+    for (int j = tid; j < d; j += blockDim.x) s.rsd[j] = s.qs[j] - c[j];
+    __syncthreads();
+    for (int e = tid; e < M * K; e += blockDim.x) {
+        const int m = e / K;
+        const float* cw = ix.codebooks + (size_t)e * ds;
+        float acc = 0.0f;
+        for (int j = 0; j < ds; j++) {
+            float diff = s.rsd[m * ds + j] - cw[j];
+            acc += diff * diff;
+        }
+        s.lut[e] = acc;
+    }
+    __syncthreads();
+    for (uint32_t base = 0; base < len; base += SCAN_ROUND) {
+        if (*s.tk.count > (uint32_t)(buf - SCAN_ROUND)) topk_flush(s.tk, a.kk);
+        const uint32_t thr = *s.tk.thr;
+#pragma unroll
+        for (int u = 0; u < SCAN_U; u++) {
+            uint32_t i = base + u * VGPU_BLOCK + tid;
+            bool take = false;
+            uint32_t fk = 0, pos = 0;
+            if (i < len) {
+                pos = beg + i;
+                if (!FILT || ecat[pos] == cq) {
+                    float dist = adc_sum<MT, KT>(ix.codes + (size_t)pos * M, s.lut, M, K, 0.0f);
+                    fk = fkey(dist);
+                    take = fk <= thr;
+                }
+            }
+            topk_push(s.tk, take, fk, pos, p, ix.list_ids);
+        }
+        __syncthreads();
+    }
+}
+
 // One query with the reference arithmetic; every thread of the block calls it.
 template <int MT, int KT>
 __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char* smem, int q) {
     const int tid = threadIdx.x;
-    const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds, P = a.P;
+    const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, P = a.P;
     ScanLds s = carve(smem, d, M, K, P, buf);
     load_query_and_lists(ix, a, s, q);
     uint32_t total = 0;
@@ -221,39 +270,7 @@ __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char
         const uint32_t l = s.lid[p], beg = s.lbeg[p], len = s.llen[p];
         total += len;
         if (len == 0) continue;
-        const float* c = ix.centroids + (size_t)l * d;
-        for (int j = tid; j < d; j += blockDim.x) s.rsd[j] = s.qs[j] - c[j];  // search.rs:1242-1245
-        __syncthreads();
-        // pq.rs:232-251 (ds == 1 gives 0 + diff*diff == diff*diff).
-        for (int e = tid; e < M * K; e += blockDim.x) {
-            const int m = e / K;
-            const float* cw = ix.codebooks + (size_t)e * ds;
-            float acc = 0.0f;
-            for (int j = 0; j < ds; j++) {
-                float diff = s.rsd[m * ds + j] - cw[j];
-                acc += diff * diff;
-            }
-            s.lut[e] = acc;
-        }
-        __syncthreads();
-        for (uint32_t base = 0; base < len; base += SCAN_ROUND) {
-            if (*s.tk.count > (uint32_t)(buf - SCAN_ROUND)) topk_flush(s.tk, a.kk);
-            const uint32_t thr = *s.tk.thr;
-#pragma unroll
-            for (int u = 0; u < SCAN_U; u++) {
-                uint32_t i = base + u * VGPU_BLOCK + tid;
-                bool take = false;
-                uint32_t fk = 0, pos = 0;
-                if (i < len) {
-                    pos = beg + i;
-                    float dist = adc_sum<MT, KT>(ix.codes + (size_t)pos * M, s.lut, M, K, 0.0f);
-                    fk = fkey(dist);
-                    take = fk <= thr;
-                }
-                topk_push(s.tk, take, fk, pos, p, ix.list_ids);
-            }
-            __syncthreads();
-        }
+        scan_list<MT, KT, false>(ix, a, s, buf, l, beg, len, p, nullptr, 0);
     }
     topk_flush(s.tk, a.kk);
     const int n = (int)*s.tk.count;
@@ -262,6 +279,41 @@ __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char
         st[0] = total;
         st[1] = st[2] = st[3] = 0u;
     }
+    write_out(a, s, q, n < a.kout ? n : a.kout);
+}
+
+// search_with_filter (search.rs:1407-1549), one query per workgroup: the
+// query's lists in slot order (the probed lists carrying its category, then,
+// when it was widened, every other list carrying it; slots >= L are padding),
+// scored like EXACT mode, candidates restricted to the entries whose category
+// is want[q].  The list bounds are read from global memory per slot, so the
+// list count is not bounded by LDS (a widened query takes every list).
+template <int MT, int KT>
+__global__ __launch_bounds__(256) void scan8_filtered_kernel(DevIndex ix, ScanArgs a, int buf,
+                                                             const uint8_t* __restrict__ ecat,
+                                                             const uint8_t* __restrict__ want) {
+    extern __shared__ __align__(16) char smem[];
+    const int q = blockIdx.x;
+    if (q >= a.nq) return;
+    const int tid = threadIdx.x;
+    const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, P = a.P;
+    ScanLds s = carve(smem, d, M, K, 0, buf);
+    for (int j = tid; j < d; j += blockDim.x) s.qs[j] = a.qn[(size_t)q * d + j];
+    if (tid == 0) {
+        *s.tk.count = 0;
+        *s.tk.thr = 0xffffffffu;
+    }
+    const uint8_t cq = want[q];
+    for (int p = 0; p < P; p++) {
+        __syncthreads();
+        const uint32_t l = a.probe[(size_t)q * P + p];  // the same for every thread
+        if (l >= (uint32_t)ix.L) continue;
+        const uint32_t beg = ix.offsets[l], len = ix.offsets[l + 1] - beg;
+        if (len == 0) continue;
+        scan_list<MT, KT, true>(ix, a, s, buf, l, beg, len, p, ecat, cq);
+    }
+    topk_flush(s.tk, a.kk);
+    const int n = (int)*s.tk.count;
     write_out(a, s, q, n < a.kout ? n : a.kout);
 }
 
@@ -312,6 +364,38 @@ void launch_scan8_exact(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     if (a.nq <= 0) return;
     if (ix.K == 256) launch_k<256>(ix, a, s);
     else launch_k<0>(ix, a, s);
+}
+
+template <int MT, int KT>
+static void launch_filtered_mk(const DevIndex& ix, const ScanArgs& a, const uint8_t* ecat,
+                               const uint8_t* want, hipStream_t s) {
+    const int buf = scan_buf(a.kk);
+    size_t off[12];
+    const size_t lds = scan_lds_layout(ix.d, ix.M, ix.K, 0, buf, off);
+    auto k = scan8_filtered_kernel<MT, KT>;
+    ensure_dyn_lds((const void*)k, lds);
+    hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), lds, s, ix, a, buf, ecat, want);
+}
+
+template <int KT>
+static void launch_filtered_k(const DevIndex& ix, const ScanArgs& a, const uint8_t* ecat,
+                              const uint8_t* want, hipStream_t s) {
+    switch (ix.M) {
+        case 4: launch_filtered_mk<4, KT>(ix, a, ecat, want, s); break;
+        case 8: launch_filtered_mk<8, KT>(ix, a, ecat, want, s); break;
+        case 16: launch_filtered_mk<16, KT>(ix, a, ecat, want, s); break;
+        case 32: launch_filtered_mk<32, KT>(ix, a, ecat, want, s); break;
+        case 48: launch_filtered_mk<48, KT>(ix, a, ecat, want, s); break;
+        case 64: launch_filtered_mk<64, KT>(ix, a, ecat, want, s); break;
+        default: launch_filtered_mk<0, KT>(ix, a, ecat, want, s); break;
+    }
+}
+
+void launch_scan8_filtered(const DevIndex& ix, const ScanArgs& a, const uint8_t* ecat,
+                           const uint8_t* want, hipStream_t s) {
+    if (a.nq <= 0) return;
+    if (ix.K == 256) launch_filtered_k<256>(ix, a, ecat, want, s);
+    else launch_filtered_k<0>(ix, a, ecat, want, s);
 }
 
 }  // namespace vgpu

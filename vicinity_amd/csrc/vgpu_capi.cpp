@@ -46,6 +46,9 @@ int guard(F&& f) {
 void need(bool ok, int code, const char* msg) {
     if (!ok) throw Error(code, msg);
 }
+void need(bool ok, int code, const std::string& msg) {
+    if (!ok) throw Error(code, msg);
+}
 
 // Temporary device buffer for the per-kernel test entry points.
 template <typename T>
@@ -258,6 +261,55 @@ int vgpu_ivfpq_last_stats(const vgpu_ivfpq* h, vgpu_search_stats* out) {
     return guard([&] {
         need(h && out, VGPU_ERR_INVALID_PARAMETER, "null argument");
         *out = h->ix->stats;
+    });
+}
+
+int vgpu_ivfpq_enable_filtering(vgpu_ivfpq* h) {
+    return guard([&] {
+        need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
+        std::lock_guard<std::mutex> lk(h->ix->mu);
+        h->ix->enable_filtering();
+    });
+}
+
+int vgpu_ivfpq_set_category(vgpu_ivfpq* h, uint32_t doc_id, int64_t category) {
+    return guard([&] {
+        need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
+        std::lock_guard<std::mutex> lk(h->ix->mu);
+        need(h->ix->filtering, VGPU_ERR_UNSUPPORTED,
+             "filtered search: rebuild the index with IVFPQIndex::with_filtering()");
+        need(category >= -1 && category <= 63, VGPU_ERR_INVALID_PARAMETER,
+             "category ID " + std::to_string(category) + " exceeds bitmask limit of 63; use an integer in 0..63");
+        h->ix->set_category(doc_id, (int)category);
+    });
+}
+
+// One query; the result is truncated at the first padding entry.
+int vgpu_ivfpq_search_filtered(vgpu_ivfpq* h, const float* query, size_t dim, size_t k, int64_t category,
+                               uint32_t* out_ids, float* out_dists, size_t* out_len) {
+    return guard([&] {
+        need(h && out_len && (k == 0 || (query && out_ids && out_dists)), VGPU_ERR_INVALID_PARAMETER,
+             "null argument");
+        std::lock_guard<std::mutex> lk(h->ix->mu);
+        *out_len = 0;
+        need(h->ix->built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
+        check_dim(*h->ix, dim);
+        need(h->ix->filtering, VGPU_ERR_INVALID_PARAMETER,
+             "filter field doesn't match index filter field (None)");
+        need(category >= 0 && category <= 63, VGPU_ERR_INVALID_PARAMETER,
+             "category ID " + std::to_string(category) + " exceeds bitmask limit of 63");
+        if (k == 0) return;
+        std::vector<int64_t> ids(k);
+        std::vector<float> dists(k);
+        const int cat = (int)category;
+        h->ix->search_filtered(query, 1, k, &cat, ids.data(), dists.data());
+        size_t m = 0;
+        while (m < k && ids[m] >= 0) {
+            out_ids[m] = (uint32_t)ids[m];
+            out_dists[m] = dists[m];
+            m++;
+        }
+        *out_len = m;
     });
 }
 

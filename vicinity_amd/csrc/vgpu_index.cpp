@@ -409,6 +409,7 @@ void IvfpqIndex::load(const float* cent, size_t Lc, const float* cb, size_t Kc,
 // build_scan_caches, search.rs:816-848, plus the FAST term).
 void IvfpqIndex::upload_index() {
     const size_t n = this->n();
+    snapshot_list_masks();
     std::vector<uint32_t> off32(L + 1);
     for (size_t l = 0; l <= L; l++) off32[l] = (uint32_t)offsets[l];
     std::vector<uint8_t> lm(n * M);
@@ -752,6 +753,141 @@ void IvfpqIndex::probe_host(const float* q, size_t nq, size_t nprobe, uint32_t* 
     }
     VGPU_HIP(hipGetLastError());
     VGPU_HIP(hipMemcpyAsync(lists, w_probe.p, nq * P * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+    VGPU_HIP(hipStreamSynchronize(stream));
+}
+
+}  // namespace vgpu
+
+namespace vgpu {
+
+// ---- search_with_filter (search.rs:1407-1549) ----------------------------
+
+// IVFPQIndex::with_filtering (search.rs:413-435) makes a filtering index at
+// construction; here it is switched on before the lists exist.
+void IvfpqIndex::enable_filtering() {
+    if (built)
+        throw Error(VGPU_ERR_ALREADY_BUILT, "filtering must be enabled before build (IVFPQIndex::with_filtering)");
+    filtering = true;
+}
+
+// add_metadata (search.rs:439-475), the filter field only: 0..63, or -1 for
+// metadata without the field (such a document never matches).
+void IvfpqIndex::set_category(uint32_t doc_id, int cat) {
+    if (!filtering)
+        throw Error(VGPU_ERR_UNSUPPORTED,
+                    "filtered search: rebuild the index with IVFPQIndex::with_filtering()");
+    if (cat < -1 || cat > 63)
+        throw Error(VGPU_ERR_INVALID_PARAMETER, "category ID " + std::to_string(cat) +
+                                                    " exceeds bitmask limit of 63; use an integer in 0..63");
+    doc_cat[doc_id] = cat;
+    cat_dirty = true;
+}
+
+// search.rs:626-648: list l's bitmask holds the categories of its members
+// when the lists are built (metadata added later does not change it).
+void IvfpqIndex::snapshot_list_masks() {
+    list_mask.assign(L, 0ull);
+    cat_dirty = true;
+    if (!filtering || doc_cat.empty()) return;
+    for (size_t l = 0; l < L; l++)
+        for (uint64_t p = offsets[l]; p < offsets[l + 1]; p++) {
+            const auto it = doc_cat.find(doc_ids[list_ids[p]]);
+            if (it != doc_cat.end() && it->second >= 0) list_mask[l] |= 1ull << it->second;
+        }
+}
+
+// The current category of every list-major entry (what
+// MetadataStore::matches reads, filtering/mod.rs:214-218) and the per-list
+// counts the widening test needs.
+void IvfpqIndex::refresh_categories() {
+    if (!cat_dirty) return;
+    const size_t nv = n();
+    std::vector<uint8_t> ec(nv, 0xff);
+    list_cat_n.assign(L * 64, 0u);
+    for (size_t l = 0; l < L; l++)
+        for (uint64_t p = offsets[l]; p < offsets[l + 1]; p++) {
+            const auto it = doc_cat.find(doc_ids[list_ids[p]]);
+            if (it != doc_cat.end() && it->second >= 0) {
+                ec[p] = (uint8_t)it->second;
+                list_cat_n[l * 64 + (size_t)it->second]++;
+            }
+        }
+    d_ecat.upload(ec.data(), nv, stream);
+    cat_dirty = false;
+}
+
+// The probed lists (nearest first) that carry the query's category are
+// scanned; when their members of that category number fewer than k and some
+// lists were not probed, every other list carrying it follows in index order
+// (search.rs:1486-1545).  Matches are scored with the reference's table
+// arithmetic and the k smallest kept (finish_top_k_by_distance, :64-75).
+void IvfpqIndex::search_filtered(const float* q, size_t nq, size_t k, const int* cats, int64_t* ids,
+                                 float* dists) {
+    if (!built) throw Error(VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
+    if (!filtering)
+        throw Error(VGPU_ERR_INVALID_PARAMETER, "filter field doesn't match index filter field (None)");
+    for (size_t i = 0; i < nq; i++)
+        if (cats[i] < 0 || cats[i] > 63)
+            throw Error(VGPU_ERR_INVALID_PARAMETER, "category ID " + std::to_string(cats[i]) +
+                                                        " exceeds bitmask limit of 63");
+    for (size_t i = 0; i < nq * d; i++)
+        if (!std::isfinite(q[i])) throw Error(VGPU_ERR_INVALID_PARAMETER, "query contains a non-finite value");
+    if (nq == 0 || k == 0) return;
+    const size_t P = std::min((size_t)params.nprobe, L);
+    std::vector<uint32_t> probes(nq * P);
+    probe_host(q, nq, params.nprobe, probes.data());  // leaves the normalised queries in w_qn
+    refresh_categories();
+    std::vector<std::vector<uint32_t>> order(nq);
+    std::vector<char> probed;
+    size_t pmax = 1;
+    for (size_t i = 0; i < nq; i++) {
+        const uint64_t bit = 1ull << cats[i];
+        size_t found = 0;
+        for (size_t p = 0; p < P; p++) {
+            const uint32_t l = probes[i * P + p];
+            if (l < L && (list_mask[l] & bit)) {
+                order[i].push_back(l);
+                found += list_cat_n[(size_t)l * 64 + (size_t)cats[i]];
+            }
+        }
+        if (found < k && P < L) {
+            probed.assign(L, 0);
+            for (size_t p = 0; p < P; p++)
+                if (probes[i * P + p] < L) probed[probes[i * P + p]] = 1;
+            for (size_t l = 0; l < L; l++)
+                if (!probed[l] && (list_mask[l] & bit)) order[i].push_back((uint32_t)l);
+        }
+        pmax = std::max(pmax, order[i].size());
+    }
+    std::vector<uint32_t> slots(nq * pmax, 0xffffffffu);
+    std::vector<uint8_t> want(nq);
+    for (size_t i = 0; i < nq; i++) {
+        std::copy(order[i].begin(), order[i].end(), slots.begin() + i * pmax);
+        want[i] = (uint8_t)cats[i];
+    }
+    w_probe.upload(slots.data(), nq * pmax, stream);
+    w_want.upload(want.data(), nq, stream);
+    w_vidx.reserve(nq * k);
+    w_dist.reserve(nq * k);
+    w_ids.reserve(nq * k);
+    w_odist.reserve(nq * k);
+    ScanArgs a;
+    a.qn = w_qn.p;
+    a.qnorm = w_qnorm.p;
+    a.probe = w_probe.p;
+    a.nq = (int)nq;
+    a.P = (int)pmax;
+    a.kout = (int)k;
+    a.kk = (int)k;
+    a.exact = 1;
+    a.out_vidx = w_vidx.p;
+    a.out_dist = w_dist.p;
+    launch_scan8_filtered(dix, a, d_ecat.p, w_want.p, stream);
+    launch_finish(w_vidx.p, w_dist.p, d_doc_ids.p, (int)nq, (int)k, (int)k, w_ids.p, w_odist.p, nullptr,
+                  nullptr, nullptr, nullptr, stream);
+    VGPU_HIP(hipGetLastError());
+    VGPU_HIP(hipMemcpyAsync(ids, w_ids.p, nq * k * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    VGPU_HIP(hipMemcpyAsync(dists, w_odist.p, nq * k * sizeof(float), hipMemcpyDeviceToHost, stream));
     VGPU_HIP(hipStreamSynchronize(stream));
 }
 

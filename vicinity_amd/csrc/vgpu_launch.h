@@ -99,6 +99,12 @@ void launch_coarse_bf16x3_dots(const float* Q, int nq, int d, const uint4* Cb, i
 
 size_t scan8_lds_bytes(const DevIndex& ix, const ScanArgs& a);
 void launch_scan8_exact(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
+// search_with_filter: a.probe holds a.P list slots per query (slots >= L are
+// padding), ecat[n] the category byte of each list-major entry (0xff: none),
+// want[nq] each query's category; writes a.out_vidx / a.out_dist like EXACT
+// mode (a.kk == a.kout), no statistics rows.
+void launch_scan8_filtered(const DevIndex& ix, const ScanArgs& a, const uint8_t* ecat,
+                           const uint8_t* want, hipStream_t s);
 // FAST mode: per-query decomposed table, threshold buffer, exact rescoring of
 // the provable candidate set; an unprovable query sets bit 0 of its qstat
 // fallback word.

@@ -8,6 +8,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/vicinity_gpu.h"
@@ -100,6 +101,16 @@ struct IvfpqIndex {
     vgpu_search_stats stats{};
     std::mutex mu;
 
+    // search_with_filter state (search.rs:236-238): the category each document
+    // carries in the filter field, per-list bitmasks taken when the lists are
+    // built (search.rs:626-648), and device copies refreshed on demand.
+    bool filtering = false;
+    std::unordered_map<uint32_t, int> doc_cat;  // doc id -> 0..63, or -1 (metadata without the field)
+    std::vector<uint64_t> list_mask;            // [L]
+    std::vector<uint32_t> list_cat_n;           // [L*64] entries per (list, category), current metadata
+    bool cat_dirty = true;
+    DevBuf<uint8_t> d_ecat, w_want;  // category of each list-major entry (0xff: none); per query
+
     IvfpqIndex(size_t dim, const vgpu_ivfpq_params& p);
     ~IvfpqIndex();
 
@@ -116,6 +127,12 @@ struct IvfpqIndex {
     void search_host(const float* q, size_t nq, size_t k, size_t nprobe, size_t pool,
                      int64_t* ids, float* dists);
     void probe_host(const float* q, size_t nq, size_t nprobe, uint32_t* lists);
+    void enable_filtering();
+    void set_category(uint32_t doc_id, int cat);
+    // search_with_filter for nq queries, query i restricted to category cats[i];
+    // rows padded with (-1, +inf) like search_host.
+    void search_filtered(const float* q, size_t nq, size_t k, const int* cats, int64_t* ids,
+                         float* dists);
 
   private:
     void kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k, uint64_t seed,
@@ -124,6 +141,8 @@ struct IvfpqIndex {
                        size_t k, float cmax, uint32_t* d_assign, hipStream_t s);
     void train_pq(const std::vector<float>& res, size_t nt, size_t Kc, uint64_t seed,
                   size_t max_iter);
+    void snapshot_list_masks();
+    void refresh_categories();
 };
 
 struct FlatIndex {

@@ -15,6 +15,7 @@ import ctypes
 import numpy as np
 
 from . import _lib
+from .filtering import MetadataFilter, filter_category, metadata_category
 
 # python.rs:1303-1304 (faiss convention)
 MISSING_LABEL = -1
@@ -60,7 +61,7 @@ class IVFPQIndex:
 
     def __init__(self, dim: int, num_clusters: int = 256, num_codebooks: int | None = None,
                  codebook_size: int = 256, nprobe: int = 1, use_opq: bool = False,
-                 seed: int = 42):
+                 seed: int = 42, filter_field: str | None = None):
         if num_codebooks is None:
             num_codebooks = default_codebooks(dim)
         _validate_shape(dim, num_clusters, num_codebooks, codebook_size, nprobe)
@@ -77,6 +78,11 @@ class IVFPQIndex:
         self._codebook_size = codebook_size
         self._use_opq = use_opq
         self._used_ids: set[int] = set()
+        # search.rs:236-238: the filter field and the documents' metadata
+        self._filter_field = filter_field
+        self._metadata: dict[int, dict] = {}
+        if filter_field is not None:
+            _lib.check(self._L.vgpu_ivfpq_enable_filtering(self._h))
 
     def __del__(self):
         h = getattr(self, "_h", None)
@@ -174,6 +180,49 @@ class IVFPQIndex:
         if not self.is_built:
             raise ValueError("index must be built before compact")
         _lib.check(self._L.vgpu_ivfpq_compact(self._h))
+
+    # ---- filtered search (search.rs:413-475, 1407-1549) ---------------------
+    @classmethod
+    def with_filtering(cls, dim: int, filter_field: str, **params) -> "IVFPQIndex":
+        """IVFPQIndex::with_filtering (search.rs:413-435)."""
+        return cls(dim, filter_field=filter_field, **params)
+
+    def add_metadata(self, doc_id: int, metadata: dict) -> None:
+        """IVFPQIndex::add_metadata (search.rs:439-475): the filter field, if
+        present, must hold an integer category 0..63.  Metadata replaces any
+        earlier entry of the document.  Lists record their members'
+        categories when they are built (search.rs:626-648)."""
+        if self._filter_field is None:
+            raise ValueError("Unsupported: filtered search "
+                             "(rebuild the index with IVFPQIndex::with_filtering())")
+        if not 0 <= int(doc_id) < (1 << 32):
+            raise ValueError(f"doc_id {doc_id} out of range [0, 2**32)")
+        cat = metadata_category(metadata, self._filter_field)
+        _lib.check(self._L.vgpu_ivfpq_set_category(self._h, int(doc_id), cat))
+        self._metadata[int(doc_id)] = dict(metadata)
+
+    def search_with_filter(self, query, k: int, filter: MetadataFilter):
+        """IVFPQIndex::search_with_filter (search.rs:1407-1549): (ids int64[m],
+        dists float32[m]), m <= k, the documents whose filter field equals the
+        filter's category.  The probe widens to every list when the probed
+        ones hold fewer than k matches."""
+        if not self.is_built:
+            raise ValueError("IVF-PQ index: search before build")
+        q = np.asarray(query)
+        if q.ndim != 1 or q.dtype != np.float32:
+            raise ValueError("query must be a 1-D float32 array")
+        if q.shape[0] != self._dim:
+            raise ValueError(f"query dimension mismatch: index expects {self._dim}, "
+                             f"got {q.shape[0]}")
+        cat = filter_category(filter, self._filter_field)
+        q = np.ascontiguousarray(q)
+        ids = np.empty(max(k, 1), np.uint32)
+        dists = np.empty(max(k, 1), np.float32)
+        m = ctypes.c_size_t(0)
+        _lib.check(self._L.vgpu_ivfpq_search_filtered(self._h, _lib.ptr(q), self._dim, k, cat,
+                                                      _lib.ptr(ids), _lib.ptr(dists),
+                                                      ctypes.byref(m)))
+        return ids[:m.value].astype(np.int64), dists[:m.value].copy()
 
     # ---- search -----------------------------------------------------------
     def search(self, query, k: int, nprobe: int | None = None, rerank_pool: int | None = None):
