@@ -161,6 +161,14 @@ int vgpu_ivfpq_search_filtered(vgpu_ivfpq *h, const float *query, size_t dim, si
                                int64_t category, uint32_t *out_ids, float *out_dists,
                                size_t *out_len);
 
+/* The lists' category bitmasks, masks u64[L] (L = the built index's list
+ * count).  No counterpart in the reference's API: they carry
+ * Cluster::filter_bitmask (src/ivf_pq/cluster.rs:24-27) through the snapshot
+ * files, which persist it in clusters.bin (persistence.rs:51-68, :195-248);
+ * set replaces the bitmasks taken at build or load time. */
+int vgpu_ivfpq_get_list_masks(const vgpu_ivfpq *h, uint64_t *masks, size_t L);
+int vgpu_ivfpq_set_list_masks(vgpu_ivfpq *h, const uint64_t *masks, size_t L);
+
 /* The probed lists of each query in probe order (search.rs:1602-1617),
  * lists u32[nq*nprobe]; returns the probe count per query in *out_p. */
 int vgpu_ivfpq_probe_batch(vgpu_ivfpq *h, const float *queries, size_t nq, size_t dim,

@@ -94,6 +94,8 @@ SIGNATURES = {
     "vgpu_ivfpq_set_category": (_i, [_H, ctypes.c_uint32, ctypes.c_int64]),
     "vgpu_ivfpq_search_filtered": (_i, [_H, _vp, _sz, _sz, ctypes.c_int64, _vp, _vp,
                                         ctypes.POINTER(_sz)]),
+    "vgpu_ivfpq_get_list_masks": (_i, [_H, _vp, _sz]),
+    "vgpu_ivfpq_set_list_masks": (_i, [_H, _vp, _sz]),
     "vgpu_ivfpq_probe_batch": (_i, [_H, _vp, _sz, _sz, _sz, _vp, ctypes.POINTER(_sz)]),
     "vgpu_ivfpq_export": (_i, [_H, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vgpu_flat_new": (_i, [_sz, _i, ctypes.POINTER(_H)]),

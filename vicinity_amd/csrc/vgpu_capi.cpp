@@ -313,6 +313,26 @@ int vgpu_ivfpq_search_filtered(vgpu_ivfpq* h, const float* query, size_t dim, si
     });
 }
 
+int vgpu_ivfpq_get_list_masks(const vgpu_ivfpq* h, uint64_t* masks, size_t L) {
+    return guard([&] {
+        need(h && (L == 0 || masks), VGPU_ERR_INVALID_PARAMETER, "null argument");
+        std::lock_guard<std::mutex> lk(h->ix->mu);
+        need(h->ix->built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: list bitmasks before build");
+        need(L == h->ix->L, VGPU_ERR_INVALID_PARAMETER, "list count mismatch");
+        for (size_t l = 0; l < L; l++) masks[l] = l < h->ix->list_mask.size() ? h->ix->list_mask[l] : 0ull;
+    });
+}
+
+int vgpu_ivfpq_set_list_masks(vgpu_ivfpq* h, const uint64_t* masks, size_t L) {
+    return guard([&] {
+        need(h && (L == 0 || masks), VGPU_ERR_INVALID_PARAMETER, "null argument");
+        std::lock_guard<std::mutex> lk(h->ix->mu);
+        need(h->ix->built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: list bitmasks before build");
+        need(L == h->ix->L, VGPU_ERR_INVALID_PARAMETER, "list count mismatch");
+        h->ix->list_mask.assign(masks, masks + L);
+    });
+}
+
 int vgpu_ivfpq_probe_batch(vgpu_ivfpq* h, const float* queries, size_t nq, size_t dim, size_t nprobe,
                            uint32_t* lists, size_t* out_p) {
     return guard([&] {

@@ -16,6 +16,7 @@ import numpy as np
 
 from . import _lib
 from .filtering import MetadataFilter, filter_category, metadata_category
+from .snapshot import read_snapshot, write_snapshot
 
 # python.rs:1303-1304 (faiss convention)
 MISSING_LABEL = -1
@@ -79,6 +80,7 @@ class IVFPQIndex:
         self._use_opq = use_opq
         self._used_ids: set[int] = set()
         # search.rs:236-238: the filter field and the documents' metadata
+        self._seed = seed
         self._filter_field = filter_field
         self._metadata: dict[int, dict] = {}
         if filter_field is not None:
@@ -158,6 +160,51 @@ class IVFPQIndex:
             _lib.ptr(list_offsets), _lib.ptr(list_ids), _lib.ptr(codes), _lib.ptr(doc_ids),
             _lib.ptr(vectors), n))
         self._used_ids = set((doc_ids if doc_ids is not None else np.arange(n)).tolist())
+
+    # ---- snapshots (src/python.rs:655-681, search.rs:906-1084) -------------
+    def save(self, path) -> None:
+        """Save the built index as a directory snapshot in the reference's
+        format (IVFPQIndex::save_to_dir, search.rs:906-1002)."""
+        inf = self._info()
+        if not inf.built:
+            raise ValueError("IVF-PQ index: save before build")
+        art = self.export()
+        L = art["centroids"].shape[0]
+        masks = np.zeros(L, np.uint64)
+        if self._filter_field is not None and L:
+            _lib.check(self._L.vgpu_ivfpq_get_list_masks(self._h, _lib.ptr(masks), L))
+        write_snapshot(
+            path, dimension=self._dim,
+            params={"num_clusters": self._num_clusters, "nprobe": self._nprobe,
+                    "num_codebooks": self._num_codebooks, "codebook_size": self._codebook_size,
+                    "use_opq": self._use_opq, "seed": self._seed},
+            centroids=art["centroids"], codebooks=art["codebooks"], codebook_size=art["K"],
+            num_codebooks=art["M"], list_offsets=art["list_offsets"], list_ids=art["list_ids"],
+            codes=art["codes"], doc_ids=art["doc_ids"], vectors=art["vectors"], list_masks=masks,
+            filter_field=self._filter_field,
+            filter_metadata=self._metadata if self._filter_field is not None else None)
+
+    @staticmethod
+    def load(path) -> "IVFPQIndex":
+        """Load a directory snapshot written by `save` or by the reference
+        (IVFPQIndex::load_from_dir, search.rs:1034-1084): the lists, codes and
+        codebooks as saved, the persisted list bitmasks and filter metadata."""
+        snap = read_snapshot(path)
+        p = snap["params"]
+        if p["use_opq"]:
+            raise ValueError("Unsupported: OPQ snapshots")
+        ix = IVFPQIndex(snap["dimension"], num_clusters=int(p["num_clusters"]),
+                        num_codebooks=int(p["num_codebooks"]),
+                        codebook_size=int(p["codebook_size"]), nprobe=int(p["nprobe"]),
+                        seed=int(p["seed"]), filter_field=snap["filter_field"])
+        for doc, md in snap["filter_metadata"].items():
+            ix.add_metadata(doc, md)
+        ix.load_artifacts(snap["centroids"], snap["codebooks"], snap["list_offsets"],
+                          snap["list_ids"], snap["codes"], snap["doc_ids"], snap["vectors"])
+        if snap["filter_field"] is not None:
+            masks = np.ascontiguousarray(snap["list_masks"], np.uint64)
+            _lib.check(ix._L.vgpu_ivfpq_set_list_masks(ix._h, _lib.ptr(masks), masks.shape[0]))
+        return ix
 
     def set_nprobe(self, nprobe: int) -> None:
         self._nprobe = nprobe
