@@ -3,9 +3,11 @@ MI355X engine through the C ABI.
 
 Mirrors pyvicinity's ``IVFPQIndex`` (src/python.rs:523-793,
 pyvicinity/_core.pyi:197-292): same constructor defaults, argument meaning,
-padding sentinels and ValueError behaviour.  Persistence (save/load) is not
-part of this engine; ``load_artifacts`` takes the arrays of an index built
-elsewhere instead.
+padding sentinels and ValueError behaviour.  ``save`` / ``load`` read and
+write the reference's directory snapshots (src/python.rs:655-681);
+``load_artifacts`` takes the arrays of an index built elsewhere.  Filtered
+search follows the Rust API (``with_filtering``, ``add_metadata``,
+``search_with_filter``, src/ivf_pq/search.rs:413-475, 1407-1549).
 """
 
 from __future__ import annotations
