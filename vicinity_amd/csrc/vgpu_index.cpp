@@ -833,6 +833,13 @@ void IvfpqIndex::search_filtered(const float* q, size_t nq, size_t k, const int*
     for (size_t i = 0; i < nq * d; i++)
         if (!std::isfinite(q[i])) throw Error(VGPU_ERR_INVALID_PARAMETER, "query contains a non-finite value");
     if (nq == 0 || k == 0) return;
+    if (k > 2048) throw Error(VGPU_ERR_INVALID_PARAMETER, "k above 2048 is not supported");
+    {
+        ScanArgs shape;  // the filtered kernel's LDS: the EXACT table and buffer, no per-list arrays
+        shape.kk = (int)k;
+        if (scan8_lds_bytes(dix, shape) > 160 * 1024)
+            throw Error(VGPU_ERR_UNSUPPORTED, "filtered scan working set exceeds the 160 KiB of LDS per workgroup");
+    }
     const size_t P = std::min((size_t)params.nprobe, L);
     std::vector<uint32_t> probes(nq * P);
     probe_host(q, nq, params.nprobe, probes.data());  // leaves the normalised queries in w_qn
