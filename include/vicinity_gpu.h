@@ -47,7 +47,7 @@ extern "C" {
 #define VGPU_MODE_EXACT 1
 
 /* IVFPQParams (src/ivf_pq/search.rs:284-312).  OPQ is not supported
- * (use_opq != 0 -> VGPU_ERR_UNSUPPORTED). */
+ * (use_opq != 0 trains OPQ at build, opq.rs:65-109, for dimension <= 2048). */
 typedef struct vgpu_ivfpq_params {
     size_t num_clusters;  /* nlist */
     size_t nprobe;        /* default probes per query */
@@ -168,6 +168,16 @@ int vgpu_ivfpq_search_filtered(vgpu_ivfpq *h, const float *query, size_t dim, si
  * set replaces the bitmasks taken at build or load time. */
 int vgpu_ivfpq_get_list_masks(const vgpu_ivfpq *h, uint64_t *masks, size_t L);
 int vgpu_ivfpq_set_list_masks(vgpu_ivfpq *h, const uint64_t *masks, size_t L);
+
+/* OPQ rotation R, f32[d*d] row-major (OptimizedProductQuantizer::rotation,
+ * src/ivf_pq/opq.rs:37-38; read by rotation_matrix :151-153).  get writes it
+ * and sets *present = 1, or sets *present = 0 for an index without one
+ * (Quantizer::Product, or OPQ never trained).  set gives an index made with
+ * use_opq the rotation of an index built elsewhere, before vgpu_ivfpq_load
+ * (the Quantizer::Optimized of a snapshot, search.rs:1034-1084); R = NULL
+ * clears it.  Searches then table R (q - c) (opq.rs:120-123). */
+int vgpu_ivfpq_get_rotation(const vgpu_ivfpq *h, float *R, size_t len, int *present);
+int vgpu_ivfpq_set_rotation(vgpu_ivfpq *h, const float *R, size_t len);
 
 /* The probed lists of each query in probe order (search.rs:1602-1617),
  * lists u32[nq*nprobe]; returns the probe count per query in *out_p. */

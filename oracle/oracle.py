@@ -40,7 +40,7 @@ class _Index(ctypes.Structure):
         ("centroids", ctypes.c_void_p), ("codebooks", ctypes.c_void_p),
         ("list_offsets", ctypes.c_void_p), ("list_ids", ctypes.c_void_p),
         ("codes", ctypes.c_void_p), ("doc_ids", ctypes.c_void_p),
-        ("vectors", ctypes.c_void_p),
+        ("vectors", ctypes.c_void_p), ("rotation", ctypes.c_void_p),
     ]
 
 
@@ -94,7 +94,14 @@ def lib():
         L.or_kmeans.argtypes = [_f32p, _sz, _sz, _sz, ctypes.c_int, ctypes.c_uint64, _sz, _f32p]
         L.or_ivfpq_build.restype = ctypes.c_int
         L.or_ivfpq_build.argtypes = [_f32p, _sz, _sz, _sz, _sz, _sz, ctypes.c_uint64, _sz, _sz,
-                                     _f32p, _f32p, _u32p, _u8p, ctypes.POINTER(_sz)]
+                                     ctypes.c_int, _f32p, _f32p, _u32p, _u8p, _f32p,
+                                     ctypes.POINTER(_sz)]
+        L.or_matvec.argtypes = [_f32p, _f32p, _sz, _f32p]
+        L.or_matvec_t.argtypes = [_f32p, _f32p, _sz, _f32p]
+        L.or_polar.argtypes = [_f32p, _sz, _f32p]
+        L.or_opq_fit.restype = ctypes.c_int
+        L.or_opq_fit.argtypes = [_f32p, _sz, _sz, _sz, _sz, _sz, ctypes.c_uint64, _sz, _f32p,
+                                 _f32p, ctypes.POINTER(_sz)]
         L.or_flat_search.restype = ctypes.c_int
         L.or_flat_search.argtypes = [_f32p, _sz, _sz, _f32p, _sz, _sz, ctypes.c_int, ctypes.c_int,
                                      _i64p, _f32p]
@@ -225,6 +232,7 @@ class Index:
     vectors: np.ndarray | None  # f32 [n, d] normalised
     M: int
     K: int
+    rotation: np.ndarray | None = None  # f32 [d, d] OPQ rotation (opq.rs:37-38)
 
     def __post_init__(self):
         self.centroids = _c(self.centroids, np.float32)
@@ -236,11 +244,14 @@ class Index:
             self.doc_ids = _c(self.doc_ids, np.uint32)
         if self.vectors is not None:
             self.vectors = _c(self.vectors, np.float32)
+        if self.rotation is not None:
+            self.rotation = _c(self.rotation, np.float32)
         L, d = self.centroids.shape
         p = lambda a: a.ctypes.data if a is not None else None  # noqa: E731
         self._s = _Index(d, L, self.M, self.K, d // self.M, self.codes.shape[0],
                          p(self.centroids), p(self.codebooks), p(self.list_offsets),
-                         p(self.list_ids), p(self.codes), p(self.doc_ids), p(self.vectors))
+                         p(self.list_ids), p(self.codes), p(self.doc_ids), p(self.vectors),
+                         p(self.rotation))
 
     @property
     def d(self):
@@ -332,8 +343,8 @@ def kmeans(x, k, metric, seed, max_iter):
     return out, it
 
 
-def ivfpq_build(vectors_normalised, L, M, K, seed, sample, max_iter):
-    """Train + assign + encode with this project's k-means; returns Index."""
+def ivfpq_build(vectors_normalised, L, M, K, seed, sample, max_iter, use_opq=False):
+    """Train + assign + encode with this project's k-means; returns (Index, assign)."""
     v = _c(vectors_normalised, np.float32)
     n, d = v.shape
     nt = n if (sample == 0 or sample >= n) else sample
@@ -342,15 +353,53 @@ def ivfpq_build(vectors_normalised, L, M, K, seed, sample, max_iter):
     cb = np.empty(M * K * (d // M), np.float32)
     assign = np.empty(n, np.uint32)
     codes = np.empty((n, M), np.uint8)
+    rot = np.empty((d, d), np.float32)
     ka = _sz()
-    rc = lib().or_ivfpq_build(v, n, d, L, M, K, seed, sample, max_iter, cent, cb, assign, codes,
-                              ctypes.byref(ka))
+    rc = lib().or_ivfpq_build(v, n, d, L, M, K, seed, sample, max_iter, 1 if use_opq else 0, cent,
+                              cb, assign, codes, rot, ctypes.byref(ka))
     if rc != 0:
         raise ValueError("invalid IVF-PQ build shape")
     K_actual = ka.value
     cb = cb[: M * K_actual * (d // M)]
     off, ids = build_lists(assign, Le)
-    return Index(cent, cb, off, ids, codes, np.arange(n, dtype=np.uint32), v, M, K_actual), assign
+    return Index(cent, cb, off, ids, codes, np.arange(n, dtype=np.uint32), v, M, K_actual,
+                 rot if use_opq else None), assign
+
+
+# ---- OPQ (opq.rs) --------------------------------------------------------
+
+def matvec(R, v):
+    R, v = _c(R, np.float32), _c(v, np.float32)
+    out = np.empty(v.size, np.float32)
+    lib().or_matvec(R, v, v.size, out)
+    return out
+
+
+def matvec_t(R, v):
+    R, v = _c(R, np.float32), _c(v, np.float32)
+    out = np.empty(v.size, np.float32)
+    lib().or_matvec_t(R, v, v.size, out)
+    return out
+
+
+def polar(M):
+    M = _c(M, np.float32)
+    out = np.empty_like(M)
+    lib().or_polar(M, M.shape[0], out)
+    return out
+
+
+def opq_fit(data, M, K, iterations, seed, max_iter=100):
+    """(rotation [d, d], codebooks [M*Ke*ds], Ke) of OptimizedProductQuantizer::fit."""
+    data = _c(data, np.float32)
+    n, d = data.shape
+    rot = np.empty((d, d), np.float32)
+    cb = np.empty(M * K * (d // M), np.float32)
+    ka = _sz()
+    rc = lib().or_opq_fit(data, n, d, M, K, iterations, seed, max_iter, rot, cb, ctypes.byref(ka))
+    if rc != 0:
+        raise ValueError(f"need at least {K} training vectors, got {n}")
+    return rot, cb[: M * ka.value * (d // M)], ka.value
 
 
 def flat_search(base, queries, k, metric=0, threads=0):

@@ -405,6 +405,14 @@ size_t or_ivfpq_probe(const or_index *ix, const float *query, size_t nprobe,
     return p;
 }
 
+/* Quantizer::compute_adc_table_into (search.rs:170-181): OPQ rotates the
+ * residual first (opq.rs:120-123, rotate_vector :143-148). */
+static const float *rotated(const or_index *ix, const float *res, float *rres) {
+    if (!ix->rotation) return res;
+    or_matvec(ix->rotation, res, ix->d, rres);
+    return rres;
+}
+
 /* search.rs:1175-1391 up to the candidate list; returns candidate keys
  * (distance, vector index) in *out_keys (malloc'd), count in return. */
 static size_t ivfpq_candidates(const or_index *ix, const float *query,
@@ -412,6 +420,7 @@ static size_t ivfpq_candidates(const or_index *ix, const float *query,
     size_t d = ix->d, M = ix->M, K = ix->K, ds = ix->ds;
     float *qn = (float *)malloc(d * sizeof(float));
     float *res = (float *)malloc(d * sizeof(float));
+    float *rres = (float *)malloc(d * sizeof(float));
     float *table = (float *)malloc(M * K * sizeof(float));
     or_normalize(query, d, qn); /* :1203 */
     size_t P = nprobe < ix->L ? nprobe : ix->L;
@@ -434,7 +443,7 @@ static size_t ivfpq_candidates(const or_index *ix, const float *query,
         uint32_t l = lists[p];
         const float *c = ix->centroids + (size_t)l * d;
         for (size_t i = 0; i < d; i++) res[i] = qn[i] - c[i]; /* :1242-1245 */
-        or_adc_table(ix->codebooks, M, K, ds, res, table);     /* :1255 */
+        or_adc_table(ix->codebooks, M, K, ds, rotated(ix, res, rres), table); /* :1255 */
         uint64_t beg = ix->list_offsets[l], end = ix->list_offsets[l + 1];
         size_t len = (size_t)(end - beg);
         const uint32_t *ids = ix->list_ids + beg;
@@ -457,6 +466,7 @@ static size_t ivfpq_candidates(const or_index *ix, const float *query,
     }
     free(qn);
     free(res);
+    free(rres);
     free(table);
     free(lists);
     free(batch);
@@ -527,6 +537,7 @@ long or_ivfpq_search_filtered(const or_index *ix, const uint64_t *list_mask,
     const uint64_t bit = 1ull << category;
     float *qn = (float *)malloc(d * sizeof(float));
     float *res = (float *)malloc(d * sizeof(float));
+    float *rres = (float *)malloc(d * sizeof(float));
     float *table = (float *)malloc(M * K * sizeof(float));
     uint32_t *order = (uint32_t *)malloc((L ? L : 1) * sizeof(uint32_t));
     char *scanned = (char *)calloc(L ? L : 1, 1);
@@ -543,7 +554,7 @@ long or_ivfpq_search_filtered(const or_index *ix, const uint64_t *list_mask,
             if ((list_mask[l] & bit) == 0) continue; /* :1504-1506 */
             const float *c = ix->centroids + (size_t)l * d;
             for (size_t i = 0; i < d; i++) res[i] = qn[i] - c[i]; /* :1509-1512 */
-            or_adc_table(ix->codebooks, M, K, ds, res, table);     /* :1514 */
+            or_adc_table(ix->codebooks, M, K, ds, rotated(ix, res, rres), table); /* :1514 */
             for (uint64_t p = ix->list_offsets[l]; p < ix->list_offsets[l + 1]; p++) {
                 uint32_t v = ix->list_ids[p];
                 if (cat[v] != category) continue; /* metadata_store.matches, :1521 */
@@ -563,6 +574,7 @@ long or_ivfpq_search_filtered(const or_index *ix, const uint64_t *list_mask,
     }
     free(qn);
     free(res);
+    free(rres);
     free(table);
     free(order);
     free(scanned);
@@ -784,18 +796,37 @@ long or_kmeans(const float *x, size_t n, size_t d, size_t k, int metric,
     return updates;
 }
 
+/* pq.rs:75-124 with this project's k-means: one squared-L2 k-means per
+ * subspace of the rows x[n*d] (seed + m, max_iter).  Returns the codebook
+ * size, min(K, n). */
+static size_t pq_fit(const float *x, size_t n, size_t d, size_t M, size_t K,
+                     uint64_t seed, size_t max_iter, float *codebooks) {
+    size_t ds = d / M, Ke = K < n ? K : n;
+    float *sub = (float *)malloc(n * ds * sizeof(float));
+    for (size_t m = 0; m < M; m++) {
+        for (size_t i = 0; i < n; i++) memcpy(sub + i * ds, x + i * d + m * ds, ds * sizeof(float));
+        or_kmeans(sub, n, ds, Ke, 1, seed + m, max_iter, codebooks + m * Ke * ds);
+    }
+    free(sub);
+    return Ke;
+}
+
 /* search.rs:546-787 with this project's k-means: training sample, cosine
  * coarse k-means (seed), list assignment of all vectors, residuals v - c,
- * one L2 k-means per subspace (seed + m, pq.rs:101-106), encode all
- * residuals.  `vectors` must already be normalised (add_slice rule).
- * Returns 0, or -1 on invalid shapes. */
+ * one L2 k-means per subspace (seed + m, pq.rs:101-106) or, with use_opq,
+ * OPQ training (opq.fit(training, count, 10), search.rs:732-749), then every
+ * residual encoded (opq.quantize rotates it first, opq.rs:112-115).
+ * `vectors` must already be normalised (add_slice rule).  Returns 0, or -1
+ * on invalid shapes. */
 int or_ivfpq_build(const float *vectors, size_t n, size_t d, size_t L,
                    size_t M, size_t K, uint64_t seed, size_t sample,
-                   size_t max_iter, float *centroids, float *codebooks,
-                   uint32_t *assign, uint8_t *codes, size_t *K_actual) {
+                   size_t max_iter, int use_opq, float *centroids,
+                   float *codebooks, uint32_t *assign, uint8_t *codes,
+                   float *rotation, size_t *K_actual) {
     if (n == 0 || M == 0 || d % M || K == 0 || K > 256 || n < K || max_iter == 0) return -1;
     size_t ds = d / M;
     size_t nt = (sample == 0 || sample >= n) ? n : sample;
+    if (use_opq && nt < K) return -1;
     uint32_t *tidx = (uint32_t *)malloc(n * sizeof(uint32_t));
     or_sample_indices(n, sample, seed, tidx);
     float *train = (float *)malloc(nt * d * sizeof(float));
@@ -808,19 +839,188 @@ int or_ivfpq_build(const float *vectors, size_t n, size_t d, size_t L,
         const float *c = centroids + (size_t)assign[i] * d;
         for (size_t j = 0; j < d; j++) res[i * d + j] = vectors[i * d + j] - c[j];
     }
-    float *sub = (float *)malloc(nt * ds * sizeof(float));
-    size_t Ke = K < nt ? K : nt;
-    for (size_t m = 0; m < M; m++) {
-        for (size_t i = 0; i < nt; i++)
-            memcpy(sub + i * ds, res + (size_t)tidx[i] * d + m * ds, ds * sizeof(float));
-        or_kmeans(sub, nt, ds, Ke, 1, seed + m, max_iter, codebooks + m * Ke * ds);
+    for (size_t i = 0; i < nt; i++) /* copy_rows_by_index, search.rs:737-745 */
+        memcpy(train + i * d, res + (size_t)tidx[i] * d, d * sizeof(float));
+    size_t Ke;
+    if (use_opq) {
+        or_opq_fit(train, nt, d, M, K, 10, seed, 100, rotation, codebooks, &Ke);
+        float *rv = (float *)malloc(d * sizeof(float));
+        for (size_t i = 0; i < n; i++) {
+            or_matvec(rotation, res + i * d, d, rv);
+            memcpy(res + i * d, rv, d * sizeof(float));
+        }
+        free(rv);
+    } else {
+        Ke = pq_fit(train, nt, d, M, K, seed, max_iter, codebooks);
     }
     or_pq_encode(codebooks, M, Ke, ds, res, n, codes);
     *K_actual = Ke;
     free(tidx);
     free(train);
     free(res);
-    free(sub);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* OPQ (src/ivf_pq/opq.rs)                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* matrix_vector_multiply, opq.rs:180-191: row i summed from 0.0 in order. */
+void or_matvec(const float *R, const float *v, size_t d, float *out) {
+    for (size_t i = 0; i < d; i++) {
+        const float *row = R + i * d;
+        float s = 0.0f;
+        for (size_t j = 0; j < d; j++) s += row[j] * v[j];
+        out[i] = s;
+    }
+}
+
+/* transpose_matrix_vector_multiply, opq.rs:194-205. */
+void or_matvec_t(const float *R, const float *v, size_t d, float *out) {
+    for (size_t i = 0; i < d; i++) {
+        float s = 0.0f;
+        for (size_t j = 0; j < d; j++) s += R[j * d + i] * v[j];
+        out[i] = s;
+    }
+}
+
+/* The orthogonal polar factor of M (opq.rs:280-294 takes U V^T from an SVD).
+ * One-sided Jacobi (Hestenes; Demmel & Veselic 1992) in float64: column pairs
+ * of A = M are rotated until every pair is orthogonal to 1e-15, the rotations
+ * accumulated in V, so A = U S.  Columns of norm <= 1e-12 of the largest
+ * (M rank-deficient) are completed, in column order, by the unit vector with
+ * the largest component outside the columns so far (Gram-Schmidt, two passes,
+ * lowest index on ties).  R = U V^T rounded to float32. */
+void or_polar(const float *Mf, size_t d, float *R) {
+    double *A = (double *)malloc(d * d * sizeof(double));
+    double *V = (double *)calloc(d * d, sizeof(double));
+    double *U = (double *)calloc(d * d, sizeof(double));
+    double *u = (double *)malloc(d * sizeof(double));
+    double *best = (double *)malloc(d * sizeof(double));
+    double *nrm = (double *)malloc(d * sizeof(double));
+    char *ok = (char *)calloc(d, 1);
+    for (size_t i = 0; i < d * d; i++) A[i] = (double)Mf[i];
+    for (size_t i = 0; i < d; i++) V[i * d + i] = 1.0;
+    for (int sweep = 0; sweep < 64; sweep++) {
+        int changed = 0;
+        for (size_t p = 0; p + 1 < d; p++)
+            for (size_t q = p + 1; q < d; q++) {
+                double a = 0.0, b = 0.0, g = 0.0;
+                for (size_t k = 0; k < d; k++) {
+                    double x = A[k * d + p], y = A[k * d + q];
+                    a += x * x;
+                    b += y * y;
+                    g += x * y;
+                }
+                if (g == 0.0 || fabs(g) <= 1e-15 * sqrt(a * b)) continue;
+                double z = (b - a) / (2.0 * g);
+                double t = (z >= 0.0 ? 1.0 : -1.0) / (fabs(z) + sqrt(1.0 + z * z));
+                double c = 1.0 / sqrt(1.0 + t * t), s = c * t;
+                for (size_t k = 0; k < d; k++) {
+                    double x = A[k * d + p], y = A[k * d + q];
+                    A[k * d + p] = c * x - s * y;
+                    A[k * d + q] = s * x + c * y;
+                    x = V[k * d + p];
+                    y = V[k * d + q];
+                    V[k * d + p] = c * x - s * y;
+                    V[k * d + q] = s * x + c * y;
+                }
+                changed = 1;
+            }
+        if (!changed) break;
+    }
+    double smax = 0.0;
+    for (size_t j = 0; j < d; j++) {
+        double s2 = 0.0;
+        for (size_t k = 0; k < d; k++) s2 += A[k * d + j] * A[k * d + j];
+        nrm[j] = sqrt(s2);
+        if (nrm[j] > smax) smax = nrm[j];
+    }
+    for (size_t j = 0; j < d; j++)
+        if (nrm[j] > 0.0 && nrm[j] > 1e-12 * smax) {
+            ok[j] = 1;
+            for (size_t k = 0; k < d; k++) U[k * d + j] = A[k * d + j] / nrm[j];
+        }
+    for (size_t j = 0; j < d; j++) {
+        if (ok[j]) continue;
+        double bn = -1.0;
+        for (size_t e = 0; e < d; e++) {
+            for (size_t k = 0; k < d; k++) u[k] = k == e ? 1.0 : 0.0;
+            for (int pass = 0; pass < 2; pass++)
+                for (size_t c = 0; c < d; c++) {
+                    if (!ok[c]) continue;
+                    double pr = 0.0;
+                    for (size_t k = 0; k < d; k++) pr += U[k * d + c] * u[k];
+                    for (size_t k = 0; k < d; k++) u[k] -= pr * U[k * d + c];
+                }
+            double s2 = 0.0;
+            for (size_t k = 0; k < d; k++) s2 += u[k] * u[k];
+            if (s2 > bn) {
+                bn = s2;
+                memcpy(best, u, d * sizeof(double));
+            }
+        }
+        bn = sqrt(bn);
+        for (size_t k = 0; k < d; k++) U[k * d + j] = best[k] / bn;
+        ok[j] = 1;
+    }
+    for (size_t i = 0; i < d; i++)
+        for (size_t j = 0; j < d; j++) {
+            double s = 0.0;
+            for (size_t k = 0; k < d; k++) s += U[i * d + k] * V[j * d + k];
+            R[i * d + j] = (float)s;
+        }
+    free(A);
+    free(V);
+    free(U);
+    free(u);
+    free(best);
+    free(nrm);
+    free(ok);
+}
+
+/* OptimizedProductQuantizer::fit (opq.rs:65-109) with
+ * compute_optimal_rotation (:232-295): R starts as the identity; each
+ * iteration fits PQ on the rows rotated by R (the rows as given in the
+ * first), then accumulates in float32, over the first min(n, 5000) rows in
+ * order, M[i][j] += rec_i * x_j where rec = reconstruct(quantize(R x)), and
+ * takes R = polar(M).  The codebooks are those of the last PQ fit, trained
+ * under the rotation before the last update (as in the reference).  The
+ * reference's PQ fits are unseeded (pq.rs:61-63); here each uses seed. */
+int or_opq_fit(const float *data, size_t n, size_t d, size_t M, size_t K,
+               size_t iterations, uint64_t seed, size_t max_iter,
+               float *rotation, float *codebooks, size_t *K_actual) {
+    if (n < K || M == 0 || d == 0 || d % M || iterations == 0) return -1;
+    size_t ds = d / M, ns = n < 5000 ? n : 5000, Ke = 0;
+    float *rot = (float *)malloc(n * d * sizeof(float));
+    float *rv = (float *)malloc(d * sizeof(float));
+    float *rec = (float *)malloc(d * sizeof(float));
+    float *Mx = (float *)malloc(d * d * sizeof(float));
+    uint8_t *code = (uint8_t *)malloc(M);
+    memset(rotation, 0, d * d * sizeof(float));
+    for (size_t i = 0; i < d; i++) rotation[i * d + i] = 1.0f;
+    memcpy(rot, data, n * d * sizeof(float));
+    for (size_t it = 0; it < iterations; it++) {
+        if (it > 0)
+            for (size_t i = 0; i < n; i++) or_matvec(rotation, data + i * d, d, rot + i * d);
+        Ke = pq_fit(rot, n, d, M, K, seed, max_iter, codebooks);
+        memset(Mx, 0, d * d * sizeof(float));
+        for (size_t k = 0; k < ns; k++) {
+            const float *x = data + k * d;
+            or_matvec(rotation, x, d, rv);
+            or_pq_encode(codebooks, M, Ke, ds, rv, 1, code);
+            or_pq_reconstruct(codebooks, M, Ke, ds, code, rec);
+            for (size_t i = 0; i < d; i++)
+                for (size_t j = 0; j < d; j++) Mx[i * d + j] += rec[i] * x[j];
+        }
+        or_polar(Mx, d, rotation);
+    }
+    *K_actual = Ke;
+    free(rot);
+    free(rv);
+    free(rec);
+    free(Mx);
+    free(code);
     return 0;
 }
 

@@ -70,7 +70,9 @@ size_t or_top_k(const uint32_t *idx, const float *dist, size_t n, size_t k,
  *   list_ids   u32[n]            insertion indices, ascending inside a list
  *   codes      u8[n*M]           PQ codes in insertion order (quantized_codes)
  *   doc_ids    u32[n]            insertion index -> caller id
- *   vectors    f32[n*d] or NULL  normalised raw vectors (for rerank)       */
+ *   vectors    f32[n*d] or NULL  normalised raw vectors (for rerank)
+ *   rotation   f32[d*d] or NULL  OPQ rotation R, row-major (opq.rs:37-38);
+ *                                NULL = Quantizer::Product                */
 typedef struct or_index {
     size_t d, L, M, K, ds, n;
     const float *centroids;
@@ -80,6 +82,7 @@ typedef struct or_index {
     const uint8_t *codes;
     const uint32_t *doc_ids;
     const float *vectors;
+    const float *rotation;
 } or_index;
 
 /* Returns the number of results (<= k); negative on error. */
@@ -113,10 +116,27 @@ void or_sample_indices(size_t n, size_t sample, uint64_t seed, uint32_t *out);
 /* metric 0 = cosine (spherical k-means), 1 = squared L2.  Returns iterations. */
 long or_kmeans(const float *x, size_t n, size_t d, size_t k, int metric,
                uint64_t seed, size_t max_iter, float *centroids);
+/* use_opq != 0 trains OPQ on the residuals (search.rs:732-749) and writes
+ * its rotation to rotation[d*d]; otherwise rotation is not touched. */
 int or_ivfpq_build(const float *vectors, size_t n, size_t d, size_t L,
                    size_t M, size_t K, uint64_t seed, size_t sample,
-                   size_t max_iter, float *centroids, float *codebooks,
-                   uint32_t *assign, uint8_t *codes, size_t *K_actual);
+                   size_t max_iter, int use_opq, float *centroids,
+                   float *codebooks, uint32_t *assign, uint8_t *codes,
+                   float *rotation, size_t *K_actual);
+
+/* ---- OPQ (src/ivf_pq/opq.rs) ------------------------------------------ */
+/* out = R v and out = R^T v, R row-major d x d (opq.rs:180-205). */
+void or_matvec(const float *R, const float *v, size_t d, float *out);
+void or_matvec_t(const float *R, const float *v, size_t d, float *out);
+/* The orthogonal factor U V^T of M = U S V^T (opq.rs:280-294), M row-major
+ * d x d float32; computed in float64 by one-sided Jacobi and rounded. */
+void or_polar(const float *M, size_t d, float *R);
+/* OptimizedProductQuantizer::fit (opq.rs:65-109): rotation[d*d] and the
+ * codebooks of the last PQ fit; each PQ fit is this project's k-means with
+ * seed + m and max_iter.  Returns 0, or -1 when n < K (opq.rs:71-76). */
+int or_opq_fit(const float *data, size_t n, size_t d, size_t M, size_t K,
+               size_t iterations, uint64_t seed, size_t max_iter,
+               float *rotation, float *codebooks, size_t *K_actual);
 
 /* ---- flat exact search (src/distance.rs:78-109) ----------------------- */
 int or_flat_search(const float *base, size_t n, size_t d, const float *queries,

@@ -187,3 +187,35 @@ def test_load_rejects_what_the_reference_rejects(tmp_path):
     with pytest.raises(FileNotFoundError):
         read_snapshot(tmp_path / "missing")
     assert not any(name.endswith(tuple(f".tmp.{os.getpid()}")) for name in os.listdir(tmp_path / "size"))
+
+
+def test_opq_quantizer_is_serdes_optimized_variant(tmp_path):
+    # opq.rs:29-41: Quantizer::Optimized { dimension, num_codebooks,
+    # codebook_size (as configured), rotation (row-major or null), pq }
+    a = _arrays(seed=8)
+    rng = np.random.default_rng(2)
+    q, r = np.linalg.qr(rng.standard_normal((a["d"], a["d"])))
+    rot = (q * np.sign(np.diag(r))).astype(np.float32)
+    params = {"num_clusters": a["L"], "nprobe": 2, "num_codebooks": a["M"], "codebook_size": 32,
+              "use_opq": True, "seed": 1}
+    _write(tmp_path, a, params=params, rotation=rot)
+    man = json.loads((tmp_path / "manifest.json").read_text())
+    opt = man["quantizer"]["Optimized"]
+    assert list(opt) == ["dimension", "num_codebooks", "codebook_size", "rotation", "pq"]
+    assert opt["codebook_size"] == 32 and opt["pq"]["codebook_size"] == a["K"]
+    assert list(opt["pq"]) == ["dimension", "num_codebooks", "codebook_size", "subvector_dim",
+                               "codebooks"]
+    s = read_snapshot(tmp_path)
+    assert s["rotation"].tobytes() == rot.tobytes()
+    assert s["codebooks"].tobytes() == a["codebooks"].tobytes()
+    assert s["params"]["use_opq"] is True
+    # a Product snapshot has no rotation; an Optimized one may hold null
+    opt["rotation"] = None
+    (tmp_path / "manifest.json").write_text(json.dumps(man))
+    assert read_snapshot(tmp_path)["rotation"] is None
+    opt["rotation"] = [0.0] * 5
+    (tmp_path / "manifest.json").write_text(json.dumps(man))
+    with pytest.raises(SnapshotFormatError, match="dimension x dimension"):
+        read_snapshot(tmp_path)
+    _write(tmp_path / "plain", a)
+    assert read_snapshot(tmp_path / "plain")["rotation"] is None

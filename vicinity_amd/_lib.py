@@ -96,6 +96,8 @@ SIGNATURES = {
                                         ctypes.POINTER(_sz)]),
     "vgpu_ivfpq_get_list_masks": (_i, [_H, _vp, _sz]),
     "vgpu_ivfpq_set_list_masks": (_i, [_H, _vp, _sz]),
+    "vgpu_ivfpq_get_rotation": (_i, [_H, _vp, _sz, _vp]),
+    "vgpu_ivfpq_set_rotation": (_i, [_H, _vp, _sz]),
     "vgpu_ivfpq_probe_batch": (_i, [_H, _vp, _sz, _sz, _sz, _vp, ctypes.POINTER(_sz)]),
     "vgpu_ivfpq_export": (_i, [_H, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vgpu_flat_new": (_i, [_sz, _i, ctypes.POINTER(_H)]),

@@ -219,8 +219,13 @@ __global__ __launch_bounds__(256) void fastscan_kernel(DevIndex ix, ScanArgs a, 
         if (len == 0) continue;
         const uint32_t beg = ix.offsets[l];
         scanned += len;
-        const float* c = ix.centroids + (size_t)l * d;
-        for (int j = lane; j < d; j += 64) rw[j] = qs[j] - c[j];  // search.rs:1242-1245
+        if (a.rres) {  // OPQ: R (q - c) from the rotation kernel (opq.rs:120-123)
+            const float* rr = a.rres + ((size_t)q * P + p) * d;
+            for (int j = lane; j < d; j += 64) rw[j] = rr[j];
+        } else {
+            const float* c = ix.centroids + (size_t)l * d;
+            for (int j = lane; j < d; j += 64) rw[j] = qs[j] - c[j];  // search.rs:1242-1245
+        }
         wave_sync();
         for (int e = lane; e < M * 16; e += 64) {  // pq.rs:232-251
             const int m = e >> 4;

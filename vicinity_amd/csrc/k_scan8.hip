@@ -209,7 +209,8 @@ __device__ inline void write_out(const ScanArgs& a, ScanLds& s, int q, int n) {
 }
 
 // Probed list l (slot p, entries beg .. beg + len - 1) with the reference
-// arithmetic: the residual r = q - c (search.rs:1242-1245), the table
+// arithmetic: the residual r = q - c (search.rs:1242-1245; with OPQ the
+// rotated residual R r, precomputed per slot in a.rres), the table
 // LUT[m][k] = sum_j (r_j - cw_j)^2 (pq.rs:232-251; ds == 1 gives
 // 0 + diff*diff == diff*diff), then each entry's M entries summed in
 // codebook order (pq.rs:272-279).  With FILT only the entries whose category
@@ -217,12 +218,17 @@ __device__ inline void write_out(const ScanArgs& a, ScanLds& s, int q, int n) {
 // thread of the block calls it.
 template <int MT, int KT, bool FILT>
 __device__ inline void scan_list(const DevIndex& ix, const ScanArgs& a, ScanLds& s, int buf,
-                                 uint32_t l, uint32_t beg, uint32_t len, int p,
+                                 uint32_t l, uint32_t beg, uint32_t len, int q, int p,
                                  const uint8_t* __restrict__ ecat, uint8_t cq) {
     const int tid = threadIdx.x;
     const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds;
-    const float* c = ix.centroids + (size_t)l * d;
-    for (int j = tid; j < d; j += blockDim.x) s.rsd[j] = s.qs[j] - c[j];
+    if (a.rres) {  // OPQ: R (q - c), formed by the rotation kernel (opq.rs:120-123)
+        const float* rr = a.rres + ((size_t)q * a.P + p) * d;
+        for (int j = tid; j < d; j += blockDim.x) s.rsd[j] = rr[j];
+    } else {
+        const float* c = ix.centroids + (size_t)l * d;
+        for (int j = tid; j < d; j += blockDim.x) s.rsd[j] = s.qs[j] - c[j];
+    }
     __syncthreads();
     for (int e = tid; e < M * K; e += blockDim.x) {
         const int m = e / K;
@@ -270,7 +276,7 @@ __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char
         const uint32_t l = s.lid[p], beg = s.lbeg[p], len = s.llen[p];
         total += len;
         if (len == 0) continue;
-        scan_list<MT, KT, false>(ix, a, s, buf, l, beg, len, p, nullptr, 0);
+        scan_list<MT, KT, false>(ix, a, s, buf, l, beg, len, q, p, nullptr, 0);
     }
     topk_flush(s.tk, a.kk);
     const int n = (int)*s.tk.count;
@@ -310,7 +316,7 @@ __global__ __launch_bounds__(256) void scan8_filtered_kernel(DevIndex ix, ScanAr
         if (l >= (uint32_t)ix.L) continue;
         const uint32_t beg = ix.offsets[l], len = ix.offsets[l + 1] - beg;
         if (len == 0) continue;
-        scan_list<MT, KT, true>(ix, a, s, buf, l, beg, len, p, ecat, cq);
+        scan_list<MT, KT, true>(ix, a, s, buf, l, beg, len, q, p, ecat, cq);
     }
     topk_flush(s.tk, a.kk);
     const int n = (int)*s.tk.count;

@@ -333,6 +333,27 @@ int vgpu_ivfpq_set_list_masks(vgpu_ivfpq* h, const uint64_t* masks, size_t L) {
     });
 }
 
+int vgpu_ivfpq_get_rotation(const vgpu_ivfpq* h, float* R, size_t len, int* present) {
+    return guard([&] {
+        need(h && present, VGPU_ERR_INVALID_PARAMETER, "null argument");
+        std::lock_guard<std::mutex> lk(h->ix->mu);
+        const auto& rot = h->ix->rotation;
+        *present = rot.empty() ? 0 : 1;
+        if (rot.empty()) return;
+        need(R && len == rot.size(), VGPU_ERR_INVALID_PARAMETER, "rotation buffer must hold dim * dim floats");
+        std::copy(rot.begin(), rot.end(), R);
+    });
+}
+
+int vgpu_ivfpq_set_rotation(vgpu_ivfpq* h, const float* R, size_t len) {
+    return guard([&] {
+        need(h, VGPU_ERR_INVALID_PARAMETER, "null argument");
+        std::lock_guard<std::mutex> lk(h->ix->mu);
+        need(!R || len == h->ix->d * h->ix->d, VGPU_ERR_INVALID_PARAMETER, "rotation must hold dim * dim floats");
+        h->ix->set_rotation(R);
+    });
+}
+
 int vgpu_ivfpq_probe_batch(vgpu_ivfpq* h, const float* queries, size_t nq, size_t dim, size_t nprobe,
                            uint32_t* lists, size_t* out_p) {
     return guard([&] {

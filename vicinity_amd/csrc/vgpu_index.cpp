@@ -300,7 +300,8 @@ void IvfpqIndex::build(size_t sample, size_t max_iter) {
                     "dimension, num_codebooks, codebook_size must all be greater than 0");
     if (d % params.num_codebooks)
         throw Error(VGPU_ERR_INVALID_CONFIG, "dimension must be divisible by num_codebooks");
-    if (params.use_opq) throw Error(VGPU_ERR_UNSUPPORTED, "OPQ rotation is not supported on the GPU path");
+    if (params.use_opq && d > 2048)
+        throw Error(VGPU_ERR_UNSUPPORTED, "OPQ rotation is limited to dimension <= 2048");
     if (n >= 0xffffffffull) throw Error(VGPU_ERR_INVALID_PARAMETER, "more than 2^32-1 vectors");
     M = params.num_codebooks;
     ds = d / M;
@@ -343,14 +344,35 @@ void IvfpqIndex::build(size_t sample, size_t max_iter) {
         const float* c = &centroids[(size_t)assign[v] * d];
         for (size_t j = 0; j < d; j++) res[i * d + j] = vectors[(size_t)v * d + j] - c[j];
     }
-    train_pq(res, nt, params.codebook_size, params.seed, max_iter);
+    rotation.clear();
+    if (params.use_opq)
+        train_opq(res, nt, params.seed);  // opq.fit(training, count, 10), search.rs:732-749
+    else
+        train_pq(res, nt, params.codebook_size, params.seed, max_iter);
 
-    // Encode every residual (search.rs:776-781).
+    // Encode every residual (search.rs:776-781); OPQ rotates it first
+    // (opq.rs:112-115), a chunk of rows at a time.
     d_codebooks.upload(codebooks.data(), codebooks.size(), stream);
     DevBuf<uint8_t> dcodes;
     dcodes.reserve(n * M);
-    launch_encode(d_vectors.p, (int)n, (int)d, d_centroids.p, dassign.p, d_codebooks.p, (int)M,
-                  (int)K, (int)ds, dcodes.p, stream);
+    if (!rotation.empty()) {
+        d_rotation.upload(rotation.data(), d * d, stream);
+        const size_t chunk = std::max<size_t>(1, std::min<size_t>(n, ((size_t)1 << 28) / d));
+        DevBuf<float> drx;
+        drx.reserve(chunk * d);
+        for (size_t r0 = 0; r0 < n; r0 += chunk) {
+            const size_t nc = std::min(chunk, n - r0);
+            launch_rotate_rows(d_rotation.p, d_vectors.p + r0 * d, 1, d_centroids.p, dassign.p + r0, (int)L,
+                               nc, (int)d, drx.p, stream);
+            launch_encode(drx.p, (int)nc, (int)d, nullptr, nullptr, d_codebooks.p, (int)M, (int)K, (int)ds,
+                          dcodes.p + r0 * M, stream);
+        }
+        VGPU_HIP(hipGetLastError());
+        VGPU_HIP(hipStreamSynchronize(stream));
+    } else {
+        launch_encode(d_vectors.p, (int)n, (int)d, d_centroids.p, dassign.p, d_codebooks.p, (int)M,
+                      (int)K, (int)ds, dcodes.p, stream);
+    }
     VGPU_HIP(hipGetLastError());
     codes.resize(n * M);
     VGPU_HIP(hipMemcpyAsync(codes.data(), dcodes.p, n * M, hipMemcpyDeviceToHost, stream));
@@ -454,6 +476,8 @@ void IvfpqIndex::upload_index() {
     dix.vectors = has_vectors ? d_vectors.p : nullptr;
     dix.cmax = (float)(cm * 1.0001);
     dix.rmax = (float)(std::sqrt(rr) * 1.0001 + 1e-30);
+    if (!rotation.empty()) d_rotation.upload(rotation.data(), d * d, stream);
+    else d_rotation.release();
     if (K == 16) {
         std::vector<uint32_t> poff(L + 1, 0);
         for (size_t l = 0; l < L; l++) {
@@ -466,6 +490,13 @@ void IvfpqIndex::upload_index() {
         dix.packed = d_packed.p;
         launch_pack4(dix, d_packed.p, stream);
         d_bias.release();
+    } else if (!rotation.empty()) {  // OPQ scans in EXACT mode: no FAST arrays
+        d_bias.release();
+        d_tblocks.release();
+        d_tblk_off.release();
+        dix.bias = nullptr;
+        dix.tblocks = nullptr;
+        dix.tblk_off = nullptr;
     } else {
         d_bias.reserve(n);
         dix.bias = d_bias.p;
@@ -534,8 +565,10 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
         VGPU_HIP(hipStreamSynchronize(s));
         return;
     }
+    const bool opq = !rotation.empty();
     size_t chunk = std::max<size_t>(1, std::min<size_t>(nq, ((size_t)1 << 28) / L));
     chunk = std::min<size_t>(chunk, 65536);
+    if (opq) chunk = std::max<size_t>(1, std::min<size_t>(chunk, ((size_t)1 << 28) / (P * d)));
     w_qn.reserve(chunk * d);
     w_qnorm.reserve(chunk);
     const bool fused = coarse_fused_supported((int)d, (int)P);
@@ -599,7 +632,7 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
         if (allp) VGPU_HIP(hipEventRecord(ev[3], s));
         // scan-only timing: the FAST kernel's dispatch records the two events
         // itself; the other scan kernels are bracketed by marker events
-        const bool scan_fast = K != 16 && mode == VGPU_MODE_FAST;
+        const bool scan_fast = K != 16 && mode == VGPU_MODE_FAST && !opq;
         if (scanp && !scan_fast) VGPU_HIP(hipEventRecord(sev[2 * ci], s));
         ScanArgs a;
         a.qn = w_qn.p;
@@ -613,12 +646,13 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
         a.flag_count = flag_count;
         a.out_vidx = w_vidx.p;
         a.out_dist = w_dist.p;
+        if (opq) a.rres = rotate_slots(w_qn.p, nc, P, w_probe.p, s);  // opq.rs:120-123
         if (K == 16) {
             a.kk = (int)kout;
             launch_fastscan(dix, a, s);
             if (allp) VGPU_HIP(hipEventRecord(ev[4], s));
             if (scanp) VGPU_HIP(hipEventRecord(sev[2 * ci + 1], s));
-        } else if (mode == VGPU_MODE_FAST) {
+        } else if (mode == VGPU_MODE_FAST && !opq) {
             a.kk = fast_keep(kout);
             a.exact = 0;
             launch_scan8_fast(dix, a, s, scanp ? sev[2 * ci] : nullptr, scanp ? sev[2 * ci + 1] : nullptr);
@@ -889,6 +923,7 @@ void IvfpqIndex::search_filtered(const float* q, size_t nq, size_t k, const int*
     a.exact = 1;
     a.out_vidx = w_vidx.p;
     a.out_dist = w_dist.p;
+    if (!rotation.empty()) a.rres = rotate_slots(w_qn.p, nq, pmax, w_probe.p, stream);
     launch_scan8_filtered(dix, a, d_ecat.p, w_want.p, stream);
     launch_finish(w_vidx.p, w_dist.p, d_doc_ids.p, (int)nq, (int)k, (int)k, w_ids.p, w_odist.p, nullptr,
                   nullptr, nullptr, nullptr, stream);

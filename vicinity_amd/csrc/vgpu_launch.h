@@ -57,6 +57,10 @@ struct ScanArgs {
     // EXACT kernel), bit 1: because of more equal distances than its buffer holds,
     // bit 2: FAST needed its second pass.
     uint32_t* qstat = nullptr;
+    // OPQ: the rotated residual R (q - c) of every (query, slot), [nq*P*d];
+    // null: the residual q - c (Quantizer::Product).  EXACT, filtered and
+    // FastScan kernels only.
+    const float* rres = nullptr;
 };
 
 void launch_normalize(const float* x, float* out, float* norms, int n, int d, hipStream_t s);
@@ -142,6 +146,16 @@ void launch_finalize(const uint32_t* vidx, const float* dist, const uint32_t* do
 // Build side.
 // codes[i*M + m] = argmin_k ||x_i,m - c_{assign_i},m - cw_mk||^2 (pq.rs:136-161);
 // centroids/assign may be null (x is then the residual itself).
+// ---- OPQ (k_opq.hip) ----
+// out[r] = R x_r (row-major R, d x d), x_r = X[r / xdiv] - C[lists[r]] when C is
+// given (zero for lists[r] >= L), else X[r]; n rows.
+void launch_rotate_rows(const float* R, const float* X, int xdiv, const float* C,
+                        const uint32_t* lists, int L, size_t n, int d, float* out, hipStream_t s);
+size_t rotate_rows_lds_bytes(int d);
+// Mx[d*d] = sum over the first ns rows of reconstruct(codes[k])^T X[k] (float32, in order).
+void launch_procrustes(const uint8_t* codes, const float* cb, int M, int K, int ds, const float* X,
+                       int ns, int d, float* Mx, hipStream_t s);
+
 void launch_encode(const float* x, int n, int d, const float* centroids, const uint32_t* assign,
                    const float* codebooks, int M, int K, int ds, uint8_t* codes, hipStream_t s);
 void launch_bias(const DevIndex& ix, float* bias, hipStream_t s);

@@ -78,11 +78,13 @@ struct IvfpqIndex {
     std::vector<uint64_t> offsets;  // [L+1]
     std::vector<uint32_t> list_ids; // [n]
     std::vector<uint8_t> codes;     // [n*M] insertion order
+    std::vector<float> rotation;    // [d*d] OPQ rotation R, row-major (opq.rs:37-38);
+                                    // empty: Quantizer::Product
 
     hipStream_t stream = nullptr;
     hipEvent_t ev[8] = {};
     std::vector<hipEvent_t> sev;  // scan-only timing: two per chunk
-    DevBuf<float> d_centroids, d_codebooks, d_bias, d_vectors;
+    DevBuf<float> d_centroids, d_codebooks, d_bias, d_vectors, d_rotation;
     DevBuf<uint4> d_cb16, w_cb16;  // bf16 hi/lo centroid copies (search index, build workspace)
     DevBuf<uint32_t> w_cand, w_cand_n;  // fused coarse candidates
     DevBuf<uint32_t> d_offsets, d_list_ids, d_doc_ids, d_pack_off;
@@ -92,6 +94,7 @@ struct IvfpqIndex {
 
     // search workspace
     DevBuf<float> w_q, w_qn, w_qnorm, w_dots, w_dist, w_dist2, w_odist;
+    DevBuf<float> w_rres;  // OPQ: rotated residual of each (query, slot)
     DevBuf<uint32_t> w_probe, w_vidx, w_vidx2, w_qstat, w_flag_list;
     DevBuf<uint32_t> w_cflag_list, w_cflag_count;  // coarse selection fallback list
     DevBuf<int64_t> w_ids;
@@ -121,6 +124,8 @@ struct IvfpqIndex {
               const uint32_t* lids, const uint8_t* cds, const uint32_t* dids, const float* vecs,
               size_t nv);
     void upload_index();
+    // The rotation of an OPQ index built elsewhere (before load); null clears it.
+    void set_rotation(const float* R);
     // Device-pointer batch search on stream s (s may be null = own stream).
     void search_device(const float* d_q, size_t nq, size_t k, size_t nprobe, size_t pool,
                        int64_t* d_ids, float* d_dists, hipStream_t s);
@@ -141,6 +146,10 @@ struct IvfpqIndex {
                        size_t k, float cmax, uint32_t* d_assign, hipStream_t s);
     void train_pq(const std::vector<float>& res, size_t nt, size_t Kc, uint64_t seed,
                   size_t max_iter);
+    void train_opq(const std::vector<float>& res, size_t nt, uint64_t seed);
+    // rotated residuals R (q_i - c_l) of nq queries x P slots into w_rres
+    const float* rotate_slots(const float* d_qn, size_t nq, size_t P, const uint32_t* d_lists,
+                              hipStream_t s);
     void snapshot_list_masks();
     void refresh_categories();
 };
@@ -173,5 +182,8 @@ struct FlatIndex {
 void sample_indices(size_t n, size_t sample, uint64_t seed, std::vector<uint32_t>& out);
 void draw_distinct(size_t n, size_t count, uint64_t seed, std::vector<uint32_t>& out);
 void normalize_row(const float* x, size_t d, float* out);
+// The orthogonal polar factor U V^T of M = U S V^T (d x d, row-major), in
+// float64 by one-sided Jacobi, rounded to float32.
+void polar_factor(const float* M, size_t d, float* R);
 
 }  // namespace vgpu

@@ -141,9 +141,10 @@ class IVFPQIndex:
         _lib.check(self._L.vgpu_ivfpq_build(self._h, training_sample_size or 0, kmeans_max_iter))
 
     def load_artifacts(self, centroids, codebooks, list_offsets, list_ids, codes,
-                       doc_ids=None, vectors=None) -> None:
+                       doc_ids=None, vectors=None, rotation=None) -> None:
         """Upload an index built elsewhere (same arrays as IVFPQIndex holds
-        after build(), search.rs:212-239)."""
+        after build(), search.rs:212-239); `rotation` (d x d) is the OPQ
+        rotation of an index made with use_opq (opq.rs:37-38)."""
         centroids = np.ascontiguousarray(centroids, np.float32)
         codebooks = np.ascontiguousarray(codebooks, np.float32).reshape(-1)
         list_offsets = np.ascontiguousarray(list_offsets, np.uint64)
@@ -157,6 +158,9 @@ class IVFPQIndex:
             doc_ids = np.ascontiguousarray(doc_ids, np.uint32)
         if vectors is not None:
             vectors = np.ascontiguousarray(vectors, np.float32)
+        if rotation is not None:
+            rotation = np.ascontiguousarray(rotation, np.float32).reshape(-1)
+            _lib.check(self._L.vgpu_ivfpq_set_rotation(self._h, _lib.ptr(rotation), rotation.size))
         _lib.check(self._L.vgpu_ivfpq_load(
             self._h, _lib.ptr(centroids), centroids.shape[0], _lib.ptr(codebooks), K,
             _lib.ptr(list_offsets), _lib.ptr(list_ids), _lib.ptr(codes), _lib.ptr(doc_ids),
@@ -184,7 +188,8 @@ class IVFPQIndex:
             num_codebooks=art["M"], list_offsets=art["list_offsets"], list_ids=art["list_ids"],
             codes=art["codes"], doc_ids=art["doc_ids"], vectors=art["vectors"], list_masks=masks,
             filter_field=self._filter_field,
-            filter_metadata=self._metadata if self._filter_field is not None else None)
+            filter_metadata=self._metadata if self._filter_field is not None else None,
+            rotation=art["rotation"])
 
     @staticmethod
     def load(path) -> "IVFPQIndex":
@@ -193,16 +198,16 @@ class IVFPQIndex:
         codebooks as saved, the persisted list bitmasks and filter metadata."""
         snap = read_snapshot(path)
         p = snap["params"]
-        if p["use_opq"]:
-            raise ValueError("Unsupported: OPQ snapshots")
         ix = IVFPQIndex(snap["dimension"], num_clusters=int(p["num_clusters"]),
                         num_codebooks=int(p["num_codebooks"]),
                         codebook_size=int(p["codebook_size"]), nprobe=int(p["nprobe"]),
+                        use_opq=bool(p["use_opq"]) or snap["rotation"] is not None,
                         seed=int(p["seed"]), filter_field=snap["filter_field"])
         for doc, md in snap["filter_metadata"].items():
             ix.add_metadata(doc, md)
         ix.load_artifacts(snap["centroids"], snap["codebooks"], snap["list_offsets"],
-                          snap["list_ids"], snap["codes"], snap["doc_ids"], snap["vectors"])
+                          snap["list_ids"], snap["codes"], snap["doc_ids"], snap["vectors"],
+                          snap["rotation"])
         if snap["filter_field"] is not None:
             masks = np.ascontiguousarray(snap["list_masks"], np.uint64)
             _lib.check(ix._L.vgpu_ivfpq_set_list_masks(ix._h, _lib.ptr(masks), masks.shape[0]))
@@ -344,7 +349,8 @@ class IVFPQIndex:
 
     def export(self) -> dict:
         """The built arrays (centroids, codebooks, list_offsets, list_ids,
-        codes in insertion order, doc_ids, vectors or None)."""
+        codes in insertion order, doc_ids, vectors or None, the OPQ rotation
+        [d, d] or None)."""
         inf = self._info()
         if not inf.built:
             raise ValueError("index must be built before export")
@@ -367,6 +373,11 @@ class IVFPQIndex:
             if out[key] is not None:
                 out[key] = out[key][:n]
         out["M"], out["K"] = M, K
+        rot = np.empty((d, d), np.float32)
+        present = ctypes.c_int(0)
+        _lib.check(self._L.vgpu_ivfpq_get_rotation(self._h, _lib.ptr(rot), rot.size,
+                                                   ctypes.byref(present)))
+        out["rotation"] = rot if present.value else None
         return out
 
     # ---- properties (pyvicinity/_core.pyi:262-292) -------------------------

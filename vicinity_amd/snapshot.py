@@ -3,9 +3,10 @@ vicinity (`IVFPQIndex::save_to_dir`, src/ivf_pq/search.rs:906-1002) loads
 here and the other way round.
 
 Files (src/ivf_pq/persistence.rs, manifest.rs, file_storage.rs):
-- ``manifest.json``: version 1, shapes, the parameters, the product quantizer
+- ``manifest.json``: version 1, shapes, the parameters, the quantizer
   (serde's externally tagged ``{"Product": {...}}``, codebooks flat and
-  codebook-major), the filter field and the documents' filter metadata, sorted
+  codebook-major, or ``{"Optimized": {..., "rotation": [d*d row-major],
+  "pq": {...}}}`` for OPQ, src/ivf_pq/opq.rs:29-41), the filter field and the documents' filter metadata, sorted
   by doc id (search.rs:968-991);
 - ``centroids.bin`` f32, ``doc_ids.bin`` u32, ``codes.bin`` u8 in insertion
   order, ``raw_vectors.bin`` f32 when the vectors are kept; all little-endian;
@@ -125,11 +126,13 @@ def _write_atomic(path: str, data: bytes) -> None:
 
 def write_snapshot(path, *, dimension: int, params: dict, centroids, codebooks, codebook_size: int,
                    num_codebooks: int, list_offsets, list_ids, codes, doc_ids, vectors=None,
-                   list_masks=None, filter_field=None, filter_metadata=None) -> None:
+                   list_masks=None, filter_field=None, filter_metadata=None,
+                   rotation=None) -> None:
     """Write a built index's arrays as a snapshot directory.  `params` holds
     num_clusters, nprobe, num_codebooks, codebook_size, use_opq and seed as
     the index was configured; list_offsets / list_ids are the lists as entry
-    offsets and member indices."""
+    offsets and member indices.  With use_opq the quantizer is written as
+    Quantizer::Optimized holding `rotation` (d x d, or None)."""
     centroids = np.ascontiguousarray(centroids, np.float32).reshape(-1, dimension)
     codebooks = np.ascontiguousarray(codebooks, np.float32).reshape(-1)
     list_offsets = np.asarray(list_offsets, np.uint64)
@@ -160,21 +163,39 @@ def write_snapshot(path, *, dimension: int, params: dict, centroids, codebooks, 
             "use_opq": bool(params.get("use_opq", False)),
             "seed": int(params["seed"]),
         },
-        "quantizer": {"Product": {
-            "dimension": int(dimension),
-            "num_codebooks": int(num_codebooks),
-            "codebook_size": int(codebook_size),
-            "subvector_dim": int(ds),
-            "codebooks": "@CODEBOOKS@",
-        }},
+        "quantizer": None,
         "filter_field": filter_field,
         "filter_metadata": [
             {"doc_id": int(doc), "metadata": metadata_to_json(md)}
             for doc, md in sorted((filter_metadata or {}).items())
         ],
     }
+    product = {
+        "dimension": int(dimension),
+        "num_codebooks": int(num_codebooks),
+        "codebook_size": int(codebook_size),
+        "subvector_dim": int(ds),
+        "codebooks": "@CODEBOOKS@",
+    }
+    if params.get("use_opq", False):
+        # OptimizedProductQuantizer (opq.rs:31-41): its own codebook_size stays
+        # the configured one; the inner pq's is the trained one.
+        manifest["quantizer"] = {"Optimized": {
+            "dimension": int(dimension),
+            "num_codebooks": int(num_codebooks),
+            "codebook_size": int(params["codebook_size"]),
+            "rotation": None if rotation is None else "@ROTATION@",
+            "pq": product,
+        }}
+    else:
+        manifest["quantizer"] = {"Product": product}
     text = json.dumps(manifest, indent=2)
     text = text.replace('"@CODEBOOKS@"', "[" + ", ".join(_f32_text(v) for v in codebooks) + "]")
+    if rotation is not None:
+        rot = np.ascontiguousarray(rotation, np.float32).reshape(-1)
+        if rot.size != dimension * dimension:
+            raise ValueError("rotation must hold dimension * dimension floats")
+        text = text.replace('"@ROTATION@"', "[" + ", ".join(_f32_text(v) for v in rot) + "]")
     _write_atomic(os.path.join(path, "manifest.json"), text.encode("utf-8"))
     _write_atomic(os.path.join(path, "centroids.bin"), centroids.astype("<f4").tobytes())
     _write_atomic(os.path.join(path, "doc_ids.bin"), doc_ids.astype("<u4").tobytes())
@@ -250,9 +271,21 @@ def read_snapshot(path) -> dict:
         if comps != want:
             raise SnapshotFormatError(
                 f"IVF-PQ generation component inventory mismatch: expected {want}, got {comps}")
-    if not isinstance(quant, dict) or list(quant) != ["Product"]:
-        raise SnapshotFormatError("only product quantizers are supported (OPQ is not)")
-    pq = quant["Product"]
+    rotation = None
+    if isinstance(quant, dict) and list(quant) == ["Product"]:
+        pq = quant["Product"]
+    elif isinstance(quant, dict) and list(quant) == ["Optimized"]:
+        try:
+            pq = quant["Optimized"]["pq"]
+            rot = quant["Optimized"]["rotation"]
+        except (KeyError, TypeError) as e:
+            raise SnapshotFormatError(f"manifest field missing: {e}") from None
+        if rot is not None:
+            if len(rot) != dim * dim:
+                raise SnapshotFormatError("OPQ rotation is not dimension x dimension")
+            rotation = np.array([f32_from_decimal(str(t)) for t in rot], np.float32).reshape(dim, dim)
+    else:
+        raise SnapshotFormatError("unknown quantizer (expected Product or Optimized)")
     M, K, ds = int(pq["num_codebooks"]), int(pq["codebook_size"]), int(pq["subvector_dim"])
     cb_tokens = pq["codebooks"]
     if len(cb_tokens) != M * K * ds or M * ds != dim:
@@ -315,5 +348,5 @@ def read_snapshot(path) -> dict:
         "centroids": centroids, "codebooks": codebooks, "doc_ids": doc_ids, "codes": codes,
         "vectors": vectors, "list_offsets": np.asarray(offsets[:L + 1], np.uint64),
         "list_ids": list_ids.astype(np.uint32), "list_masks": np.asarray(masks[:L], np.uint64),
-        "filter_field": filter_field, "filter_metadata": filter_metadata,
+        "filter_field": filter_field, "filter_metadata": filter_metadata, "rotation": rotation,
     }
