@@ -53,7 +53,8 @@ def cpu_baseline(art, queries, k, nprobe, budget_s=15.0):
 
     orc.build()
     oix = orc.Index(art["centroids"], art["codebooks"], art["list_offsets"], art["list_ids"],
-                    art["codes"], art["doc_ids"], art["vectors"], art["M"], art["K"])
+                    art["codes"], art["doc_ids"], art["vectors"], art["M"], art["K"],
+                    art["rotation"])
     threads = min(os.cpu_count() or 1, 16)
     probe = 200
     t0 = time.perf_counter()
@@ -76,6 +77,9 @@ def main():
     ap.add_argument("--train-sample", type=int, default=262_144)
     ap.add_argument("--kmeans-iters", type=int, default=25)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--opq", action="store_true",
+                    help="build with use_opq (OPQ rotation, EXACT-mode scan of rotated residual "
+                         "tables) instead of the headline product quantizer")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run three 256 MiB device-to-device copies (the reference "
                          "kernel for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -109,7 +113,8 @@ def main():
     log(f"data {w.base.shape} in {time.perf_counter() - t0:.1f}s")
     t0 = time.perf_counter()
     ix = v.IVFPQIndex(128, num_clusters=p["num_clusters"], num_codebooks=p["num_codebooks"],
-                      codebook_size=p["codebook_size"], nprobe=p["nprobe"], seed=42)
+                      codebook_size=p["codebook_size"], nprobe=p["nprobe"], use_opq=args.opq,
+                      seed=42)
     ix.add_items(w.base)
     ix.build(training_sample_size=args.train_sample, kmeans_max_iter=args.kmeans_iters)
     log(f"build in {time.perf_counter() - t0:.1f}s")
@@ -186,14 +191,19 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded Gaussian mixture, vicinity_amd/datagen.py)",
-        "config": {"workload": w.name, "n": args.n, "d": 128, "nlist": p["num_clusters"],
+        "config": {"workload": w.name + ("_opq" if args.opq else ""), "n": args.n, "d": 128, "nlist": p["num_clusters"],
                    "M": p["num_codebooks"], "ksub": p["codebook_size"], "nprobe": nprobe, "k": k,
-                   "batch": nq, "mode": args.mode, "train_sample": args.train_sample,
+                   "batch": nq, "mode": "exact" if args.opq else args.mode,
+                   "use_opq": args.opq, "train_sample": args.train_sample,
                    "kmeans_iters": args.kmeans_iters},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profile() if args.n == 1_000_000 else None,
-                     "kernel": "scan8_fast_kernel<16,256,8,1>", "kernel_ms": round(scan_ms, 4),
+                     "traffic": (traffic_from_profile()
+                                 if args.n == 1_000_000 and not args.opq and args.mode == "fast"
+                                 else None),
+                     "kernel": ("scan8_exact_kernel<16,256>" if args.opq or args.mode == "exact"
+                                else "scan8_fast_kernel<16,256,8,1>"),
+                     "kernel_ms": round(scan_ms, 4),
                      "algorithmic_bytes_per_launch": int(scan_bytes),
                      "candidates_per_launch": int(cands)},
         "phases_ms": phases,

@@ -216,10 +216,11 @@ __device__ inline void write_out(const ScanArgs& a, ScanLds& s, int q, int n) {
 // codebook order (pq.rs:272-279).  With FILT only the entries whose category
 // byte equals cq are candidates (filtering/mod.rs:151-153, 214-218).  Every
 // thread of the block calls it.
-template <int MT, int KT, bool FILT>
+template <int MT, int KT, bool FILT, int CWD>
 __device__ inline void scan_list(const DevIndex& ix, const ScanArgs& a, ScanLds& s, int buf,
                                  uint32_t l, uint32_t beg, uint32_t len, int q, int p,
-                                 const uint8_t* __restrict__ ecat, uint8_t cq) {
+                                 const uint8_t* __restrict__ ecat, uint8_t cq,
+                                 const float (&cw)[CWD != 0 ? MT * (CWD > 0 ? CWD : -CWD) : 1]) {
     const int tid = threadIdx.x;
     const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds;
     if (a.rres) {  // OPQ: R (q - c), formed by the rotation kernel (opq.rs:120-123)
@@ -230,15 +231,35 @@ __device__ inline void scan_list(const DevIndex& ix, const ScanArgs& a, ScanLds&
         for (int j = tid; j < d; j += blockDim.x) s.rsd[j] = s.qs[j] - c[j];
     }
     __syncthreads();
-    for (int e = tid; e < M * K; e += blockDim.x) {
-        const int m = e / K;
-        const float* cw = ix.codebooks + (size_t)e * ds;
-        float acc = 0.0f;
-        for (int j = 0; j < ds; j++) {
-            float diff = s.rsd[m * ds + j] - cw[j];
-            acc += diff * diff;
+    if constexpr (CWD != 0) {  // thread t: code t of every codebook, codewords in registers
+        constexpr int W = CWD > 0 ? CWD : -CWD;
+        const int dsx = CWD > 0 ? ds : W;  // CWD < 0: ds == W, every index known
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < W; j++) {
+                if (j < dsx) {
+                    float diff = s.rsd[m * dsx + j] - cw[m * W + j];
+                    acc += diff * diff;
+                }
+            }
+            s.lut[m * 256 + tid] = acc;
+            // one codebook's residual slice live at a time (hoisting every
+            // LDS read ahead of the arithmetic would double the registers)
+            __builtin_amdgcn_sched_barrier(0);
         }
-        s.lut[e] = acc;
+    } else {
+        for (int e = tid; e < M * K; e += blockDim.x) {
+            const int m = e / K;
+            const float* cwp = ix.codebooks + (size_t)e * ds;
+            float acc = 0.0f;
+            for (int j = 0; j < ds; j++) {
+                float diff = s.rsd[m * ds + j] - cwp[j];
+                acc += diff * diff;
+            }
+            s.lut[e] = acc;
+        }
     }
     __syncthreads();
     for (uint32_t base = 0; base < len; base += SCAN_ROUND) {
@@ -263,12 +284,32 @@ __device__ inline void scan_list(const DevIndex& ix, const ScanArgs& a, ScanLds&
     }
 }
 
+// Codeword t of every codebook into registers (ksub 256, 256 threads):
+// CWD > 0 holds ds <= CWD floats per codeword, CWD < 0 exactly ds = -CWD.  The
+// per-list tables then read no codebook memory.
+template <int MT, int CWD>
+__device__ inline void load_codewords(const DevIndex& ix,
+                                      float (&cw)[CWD != 0 ? MT * (CWD > 0 ? CWD : -CWD) : 1]) {
+    if constexpr (CWD != 0) {
+        constexpr int W = CWD > 0 ? CWD : -CWD;
+        const int t = threadIdx.x, ds = CWD > 0 ? ix.ds : W;
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            const float* src = ix.codebooks + ((size_t)m * 256 + t) * ds;
+#pragma unroll
+            for (int j = 0; j < W; j++) cw[m * W + j] = j < ds ? src[j] : 0.0f;
+        }
+    }
+}
+
 // One query with the reference arithmetic; every thread of the block calls it.
-template <int MT, int KT>
+template <int MT, int KT, int CWD>
 __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char* smem, int q) {
     const int tid = threadIdx.x;
     const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, P = a.P;
     ScanLds s = carve(smem, d, M, K, P, buf);
+    float cw[CWD != 0 ? MT * (CWD > 0 ? CWD : -CWD) : 1];
+    load_codewords<MT, CWD>(ix, cw);
     load_query_and_lists(ix, a, s, q);
     uint32_t total = 0;
     for (int p = 0; p < P; p++) {
@@ -276,7 +317,7 @@ __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char
         const uint32_t l = s.lid[p], beg = s.lbeg[p], len = s.llen[p];
         total += len;
         if (len == 0) continue;
-        scan_list<MT, KT, false>(ix, a, s, buf, l, beg, len, q, p, nullptr, 0);
+        scan_list<MT, KT, false, CWD>(ix, a, s, buf, l, beg, len, q, p, nullptr, 0, cw);
     }
     topk_flush(s.tk, a.kk);
     const int n = (int)*s.tk.count;
@@ -294,7 +335,7 @@ __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char
 // scored like EXACT mode, candidates restricted to the entries whose category
 // is want[q].  The list bounds are read from global memory per slot, so the
 // list count is not bounded by LDS (a widened query takes every list).
-template <int MT, int KT>
+template <int MT, int KT, int CWD>
 __global__ __launch_bounds__(256) void scan8_filtered_kernel(DevIndex ix, ScanArgs a, int buf,
                                                              const uint8_t* __restrict__ ecat,
                                                              const uint8_t* __restrict__ want) {
@@ -304,6 +345,8 @@ __global__ __launch_bounds__(256) void scan8_filtered_kernel(DevIndex ix, ScanAr
     const int tid = threadIdx.x;
     const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, P = a.P;
     ScanLds s = carve(smem, d, M, K, 0, buf);
+    float cw[CWD != 0 ? MT * (CWD > 0 ? CWD : -CWD) : 1];
+    load_codewords<MT, CWD>(ix, cw);
     for (int j = tid; j < d; j += blockDim.x) s.qs[j] = a.qn[(size_t)q * d + j];
     if (tid == 0) {
         *s.tk.count = 0;
@@ -316,25 +359,34 @@ __global__ __launch_bounds__(256) void scan8_filtered_kernel(DevIndex ix, ScanAr
         if (l >= (uint32_t)ix.L) continue;
         const uint32_t beg = ix.offsets[l], len = ix.offsets[l + 1] - beg;
         if (len == 0) continue;
-        scan_list<MT, KT, true>(ix, a, s, buf, l, beg, len, q, p, ecat, cq);
+        scan_list<MT, KT, true, CWD>(ix, a, s, buf, l, beg, len, q, p, ecat, cq, cw);
     }
     topk_flush(s.tk, a.kk);
     const int n = (int)*s.tk.count;
     write_out(a, s, q, n < a.kout ? n : a.kout);
 }
 
-template <int MT, int KT>
+template <int MT, int KT, int CWD>
 __global__ __launch_bounds__(256) void scan8_exact_kernel(DevIndex ix, ScanArgs a, int buf) {
     extern __shared__ __align__(16) char smem[];
-    if (!a.only_flagged) {
-        if ((int)blockIdx.x < a.nq) exact_query<MT, KT>(ix, a, buf, smem, blockIdx.x);
-        return;
-    }
-    const uint32_t nf = *a.flag_count;  // written by the FAST kernel before this launch
-    for (uint32_t fi = blockIdx.x; fi < nf; fi += gridDim.x) {
+    // Every query of the batch (block q takes query q), or the flagged queries
+    // the FAST kernel listed before this launch (blocks stride over the list).
+    // One call site, so the query body is inlined once.
+    const uint32_t nf = a.only_flagged ? *a.flag_count : (uint32_t)a.nq;
+    const uint32_t step = a.only_flagged ? gridDim.x : nf;
+    for (uint32_t fi = blockIdx.x; fi < nf; fi += step) {
         __syncthreads();
-        exact_query<MT, KT>(ix, a, buf, smem, (int)a.flag_list[fi]);
+        const int q = a.only_flagged ? (int)a.flag_list[fi] : (int)fi;
+        exact_query<MT, KT, CWD>(ix, a, buf, smem, q);
     }
+}
+
+// Codewords held per thread: ksub 256 with a fixed codebook count and
+// d <= 128 (M * ds floats per thread); 0 = read the codebooks per list.  The
+// kernels take -cw_regs when ds is exactly that width.
+template <int MT, int KT>
+constexpr int cw_regs() {
+    return (KT == 256 && MT > 0 && MT <= 64) ? 128 / MT : 0;
 }
 
 size_t scan8_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
@@ -346,7 +398,10 @@ template <int MT, int KT>
 static void launch_mk(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     int buf = scan_buf(a.kk);
     size_t lds = scan8_lds_bytes(ix, a);
-    auto k = scan8_exact_kernel<MT, KT>;
+    constexpr int CWD = cw_regs<MT, KT>();
+    auto k = (CWD > 0 && ix.ds == CWD)  ? scan8_exact_kernel<MT, KT, -CWD>
+             : (CWD > 0 && ix.ds < CWD) ? scan8_exact_kernel<MT, KT, CWD>
+                                        : scan8_exact_kernel<MT, KT, 0>;
     ensure_dyn_lds((const void*)k, lds);
     // Flagged queries: a small grid walks the list the FAST kernel wrote.
     const int grid = a.only_flagged ? (a.nq < 256 ? a.nq : 256) : a.nq;
@@ -378,7 +433,10 @@ static void launch_filtered_mk(const DevIndex& ix, const ScanArgs& a, const uint
     const int buf = scan_buf(a.kk);
     size_t off[12];
     const size_t lds = scan_lds_layout(ix.d, ix.M, ix.K, 0, buf, off);
-    auto k = scan8_filtered_kernel<MT, KT>;
+    constexpr int CWD = cw_regs<MT, KT>();
+    auto k = (CWD > 0 && ix.ds == CWD)  ? scan8_filtered_kernel<MT, KT, -CWD>
+             : (CWD > 0 && ix.ds < CWD) ? scan8_filtered_kernel<MT, KT, CWD>
+                                        : scan8_filtered_kernel<MT, KT, 0>;
     ensure_dyn_lds((const void*)k, lds);
     hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), lds, s, ix, a, buf, ecat, want);
 }

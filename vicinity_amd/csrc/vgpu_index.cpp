@@ -629,6 +629,9 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             launch_coarse_select(w_dots.p, w_qn.p, w_qnorm.p, d_centroids.p, (int)nc, (int)L, (int)d,
                                  (int)P, dix.cmax, w_probe.p, overflow, w_cflag_list.p, cflag_count, s);
         }
+        // OPQ: the rotated residual of every (query, probe) slot (opq.rs:120-123),
+        // timed with the selection
+        const float* rres = opq ? rotate_slots(w_qn.p, nc, P, w_probe.p, s) : nullptr;
         if (allp) VGPU_HIP(hipEventRecord(ev[3], s));
         // scan-only timing: the FAST kernel's dispatch records the two events
         // itself; the other scan kernels are bracketed by marker events
@@ -646,7 +649,7 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
         a.flag_count = flag_count;
         a.out_vidx = w_vidx.p;
         a.out_dist = w_dist.p;
-        if (opq) a.rres = rotate_slots(w_qn.p, nc, P, w_probe.p, s);  // opq.rs:120-123
+        a.rres = rres;
         if (K == 16) {
             a.kk = (int)kout;
             launch_fastscan(dix, a, s);
