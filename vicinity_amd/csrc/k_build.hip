@@ -189,4 +189,84 @@ void launch_adc_tables(const float* codebooks, int M, int K, int ds, const float
                        codebooks, M, K, ds, r, nr, tables);
 }
 
+// Lloyd update of every active key (k-means centroid, or codeword c of
+// subspace m): the float64 sum of its members' rows in index order, the mean
+// cast to float, and with NORM the row normalised like normalize_row (float
+// sum of squares in order, sqrt, divide when the norm exceeds 1e-10).  An empty
+// key keeps its row.  One wave per key: lanes test 64 rows per step, a ballot
+// lists the members, and each member's row is added in row order, lane j owning
+// dims j, j + 64, ...  Labels: u32 per row (U8 false) or the code byte of
+// subspace m at labels[i * M + m] (U8 true).  Rows: x[i * d + col0], w floats
+// wide (w <= 256); out rows are w floats at out[key * w].
+template <bool U8, bool NORM>
+__global__ __launch_bounds__(256) void kmeans_update_kernel(const float* __restrict__ x, int n, int d,
+                                                            int w, int M, const void* __restrict__ labels,
+                                                            int K, const uint8_t* __restrict__ active,
+                                                            float* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int key = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (key >= M * K) return;
+    const int m = key / K, c = key - m * K;
+    if (active && !active[m]) return;
+    const size_t col0 = U8 ? (size_t)m * w : 0;
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    uint32_t count = 0;
+    for (int i0 = 0; i0 < n; i0 += 64) {
+        const int i = i0 + lane;
+        bool mine = false;
+        if (i < n) {
+            mine = U8 ? ((const uint8_t*)labels)[(size_t)i * M + m] == (uint8_t)c
+                      : ((const uint32_t*)labels)[i] == (uint32_t)c;
+        }
+        uint64_t b = __ballot(mine);
+        count += (uint32_t)__popcll(b);
+        while (b) {
+            const int src = __ffsll((unsigned long long)b) - 1;
+            b &= b - 1;
+            const float* xr = x + (size_t)(i0 + src) * d + col0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int j = lane + 64 * t;
+                if (j < w) acc[t] += (double)xr[j];
+            }
+        }
+    }
+    if (count == 0) return;
+    float f[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) f[t] = (float)(acc[t] / (double)count);
+    if constexpr (NORM) {
+        float s2 = 0.0f;
+        for (int j = 0; j < w; j++) {  // uniform loop: every lane forms the same sum
+            const float v = __shfl(f[j >> 6], j & 63, 64);
+            s2 += v * v;
+        }
+        const float nrm = sqrtf(s2);
+        if (nrm > 1e-10f) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) f[t] = f[t] / nrm;
+        }
+    }
+    float* o = out + (size_t)key * w;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int j = lane + 64 * t;
+        if (j < w) o[j] = f[t];
+    }
+}
+
+void launch_kmeans_update(const float* x, int n, int d, int w, int M, const void* labels, bool u8,
+                          int K, const uint8_t* active, bool normalize, float* out, hipStream_t s) {
+    const dim3 grid((unsigned)(((size_t)M * K + 3) / 4));
+    if (u8)
+        hipLaunchKernelGGL((kmeans_update_kernel<true, false>), grid, dim3(256), 0, s, x, n, d, w, M,
+                           labels, K, active, out);
+    else if (normalize)
+        hipLaunchKernelGGL((kmeans_update_kernel<false, true>), grid, dim3(256), 0, s, x, n, d, w, M,
+                           labels, K, active, out);
+    else
+        hipLaunchKernelGGL((kmeans_update_kernel<false, false>), grid, dim3(256), 0, s, x, n, d, w, M,
+                           labels, K, active, out);
+}
+
 }  // namespace vgpu

@@ -171,7 +171,9 @@ void IvfpqIndex::assign_cosine(const float* d_x, const float* d_norms, size_t nx
 // k-means, src/partitioning/kmeans.rs:64-107): k_eff = min(k, n) seeded
 // distinct starting points; assign on the GPU; stop when no assignment
 // changes; otherwise each non-empty centroid becomes the float64 mean of its
-// members (index order), re-normalised.
+// members (index order), re-normalised.  Both steps run on the GPU for
+// d <= 256 (the update kernel's row width); the host keeps the assignment
+// test and the centroid norm bound.
 void IvfpqIndex::kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k, uint64_t seed,
                                size_t max_iter, std::vector<float>& cent) {
     const size_t ke = std::min(k, nt);
@@ -189,14 +191,25 @@ void IvfpqIndex::kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k,
     std::vector<uint32_t> assign(nt), prev(nt);
     std::vector<double> sums(ke * d);
     std::vector<uint64_t> counts(ke);
+    const bool gpu_update = d <= 256;
+    dc.upload(cent.data(), ke * d, stream);
     for (size_t it = 0; it < max_iter; it++) {
         float cmax = 0.0f;
         for (size_t c = 0; c < ke; c++) cmax = std::max(cmax, row_norm_bound(&cent[c * d], d));
-        dc.upload(cent.data(), ke * d, stream);
+        if (!gpu_update) dc.upload(cent.data(), ke * d, stream);
         assign_cosine(dx.p, dn.p, nt, dc.p, ke, cmax, da.p, stream);
         VGPU_HIP(hipMemcpyAsync(assign.data(), da.p, nt * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
         VGPU_HIP(hipStreamSynchronize(stream));
         if (it > 0 && assign == prev) break;
+        if (gpu_update) {
+            launch_kmeans_update(dx.p, (int)nt, (int)d, (int)d, 1, da.p, false, (int)ke, nullptr, true, dc.p,
+                                 stream);
+            VGPU_HIP(hipGetLastError());
+            VGPU_HIP(hipMemcpyAsync(cent.data(), dc.p, ke * d * sizeof(float), hipMemcpyDeviceToHost, stream));
+            VGPU_HIP(hipStreamSynchronize(stream));
+            prev.swap(assign);
+            continue;
+        }
         std::fill(sums.begin(), sums.end(), 0.0);
         std::fill(counts.begin(), counts.end(), 0);
         for (size_t i = 0; i < nt; i++) {
@@ -218,6 +231,7 @@ void IvfpqIndex::kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k,
 // One squared-L2 k-means per subspace (pq.rs:75-124, seed + m), all M run
 // together: one GPU encode pass assigns every subspace; a subspace whose
 // assignment stopped changing is frozen, exactly as if it had been run alone.
+// The codeword means run on the GPU (float64, member order) for ds <= 256.
 void IvfpqIndex::train_pq(const std::vector<float>& res, size_t nt, size_t Kc, uint64_t seed,
                           size_t max_iter) {
     const size_t Ke = std::min(Kc, nt);
@@ -230,15 +244,17 @@ void IvfpqIndex::train_pq(const std::vector<float>& res, size_t nt, size_t Kc, u
             std::memcpy(&codebooks[(m * Ke + c) * ds], &res[(size_t)init[c] * d + m * ds], ds * sizeof(float));
     }
     DevBuf<float> dres, dcb;
-    DevBuf<uint8_t> dcodes;
+    DevBuf<uint8_t> dcodes, dactive;
     dres.upload(res.data(), nt * d, stream);
     dcodes.reserve(nt * M);
-    std::vector<uint8_t> cur(nt * M), prev(nt * M);
+    std::vector<uint8_t> cur(nt * M), prev(nt * M), active(M);
     std::vector<char> frozen(M, 0);
     std::vector<double> sums(Ke * ds);
     std::vector<uint64_t> counts(Ke);
+    const bool gpu_update = ds <= 256;
+    dcb.upload(codebooks.data(), codebooks.size(), stream);
     for (size_t it = 0; it < max_iter; it++) {
-        dcb.upload(codebooks.data(), codebooks.size(), stream);
+        if (!gpu_update) dcb.upload(codebooks.data(), codebooks.size(), stream);
         launch_encode(dres.p, (int)nt, (int)d, nullptr, nullptr, dcb.p, (int)M, (int)Ke, (int)ds,
                       dcodes.p, stream);
         VGPU_HIP(hipGetLastError());
@@ -246,6 +262,7 @@ void IvfpqIndex::train_pq(const std::vector<float>& res, size_t nt, size_t Kc, u
         VGPU_HIP(hipStreamSynchronize(stream));
         bool any = false;
         for (size_t m = 0; m < M; m++) {
+            active[m] = 0;
             if (frozen[m]) continue;
             if (it > 0) {
                 bool same = true;
@@ -256,6 +273,8 @@ void IvfpqIndex::train_pq(const std::vector<float>& res, size_t nt, size_t Kc, u
                 }
             }
             any = true;
+            active[m] = 1;
+            if (gpu_update) continue;
             std::fill(sums.begin(), sums.end(), 0.0);
             std::fill(counts.begin(), counts.end(), 0);
             for (size_t i = 0; i < nt; i++) {
@@ -271,7 +290,18 @@ void IvfpqIndex::train_pq(const std::vector<float>& res, size_t nt, size_t Kc, u
             }
         }
         if (!any) break;
+        if (gpu_update) {
+            dactive.upload(active.data(), M, stream);
+            launch_kmeans_update(dres.p, (int)nt, (int)d, (int)ds, (int)M, dcodes.p, true, (int)Ke, dactive.p,
+                                 false, dcb.p, stream);
+            VGPU_HIP(hipGetLastError());
+        }
         prev.swap(cur);
+    }
+    if (gpu_update) {
+        VGPU_HIP(hipMemcpyAsync(codebooks.data(), dcb.p, codebooks.size() * sizeof(float),
+                                hipMemcpyDeviceToHost, stream));
+        VGPU_HIP(hipStreamSynchronize(stream));
     }
 }
 

@@ -156,6 +156,14 @@ size_t rotate_rows_lds_bytes(int d);
 void launch_procrustes(const uint8_t* codes, const float* cb, int M, int K, int ds, const float* X,
                        int ns, int d, float* Mx, hipStream_t s);
 
+// k-means update of every key (M subspaces x K, or M = 1): float64 member sums in
+// row order, mean cast to float, optionally normalised; empty keys keep their
+// row; subspaces with active[m] == 0 are skipped (active may be null).  u8:
+// labels[i * M + m] code bytes over row slices x[i * d + m * w .. + w);
+// otherwise u32 labels[i] over whole rows (w = d <= 256).
+void launch_kmeans_update(const float* x, int n, int d, int w, int M, const void* labels, bool u8,
+                          int K, const uint8_t* active, bool normalize, float* out, hipStream_t s);
+
 void launch_encode(const float* x, int n, int d, const float* centroids, const uint32_t* assign,
                    const float* codebooks, int M, int K, int ds, uint8_t* codes, hipStream_t s);
 void launch_bias(const DevIndex& ix, float* bias, hipStream_t s);
