@@ -161,3 +161,23 @@ def test_opq_snapshot_round_trip(k64, tmp_path):
     assert loaded.export()["rotation"].tobytes() == ix.export()["rotation"].tobytes()
     after = loaded.batch_search(q, 10, rerank_pool=30)
     _same(before[0], before[1], after[0], after[1])
+
+
+@pytest.mark.parametrize("d,M,K,L", [
+    (18, 3, 32, 8),     # d % 4 != 0: the rotation's scalar path
+    (200, 8, 100, 12),  # d > 128 and ksub 100: the table read from the codebooks per list
+    (300, 10, 64, 10),  # d > 256: several rotation outputs per thread
+])
+def test_opq_shapes_build_and_search_bitexact(vg, oracle, d, M, K, L):
+    _print_case(f"OPQ shape d={d} M={M} ksub={K} nlist={L}")
+    ix, base, rng = _build(vg, 1200, d, L, M, K, 21, d)
+    art = ix.export()
+    oix, _ = oracle.ivfpq_build(oracle.normalize_rows(base), L, M, K, 21, 0, 10, use_opq=True)
+    assert art["rotation"].tobytes() == oix.rotation.tobytes()
+    assert art["codebooks"].tobytes() == oix.codebooks.tobytes()
+    assert np.array_equal(art["codes"], oix.codes)
+    q = rng.standard_normal((80, d)).astype(np.float32)
+    for k, nprobe, pool in ((10, 4, 0), (25, L, 0), (5, 3, 20)):
+        ids, dists = ix.batch_search(q, k, nprobe=nprobe, rerank_pool=pool or None)
+        oids, odists = _oracle_index(oracle, art).search_batch(q, k, nprobe, pool)
+        _same(ids, dists, oids, odists)
