@@ -125,6 +125,14 @@ def load() -> ctypes.CDLL:
             raise ImportError(
                 f"{LIB_PATH} is missing: build it with `make -C vicinity_amd/csrc` "
                 "(there is no CPU fallback)")
+        # PyTorch's ROCm wheel carries its own HIP and HSA runtimes.  Loading
+        # torch first makes this library bind to those same runtimes; loaded
+        # the other way round, the process holds two HSA runtimes and the
+        # second to initialise finds no device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         lib = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)

@@ -231,9 +231,32 @@ __device__ inline void scan_list(const DevIndex& ix, const ScanArgs& a, ScanLds&
         for (int j = tid; j < d; j += blockDim.x) s.rsd[j] = s.qs[j] - c[j];
     }
     __syncthreads();
-    if constexpr (CWD != 0) {  // thread t: code t of every codebook, codewords in registers
-        constexpr int W = CWD > 0 ? CWD : -CWD;
-        const int dsx = CWD > 0 ? ds : W;  // CWD < 0: ds == W, every index known
+    if constexpr (CWD < 0) {  // ds == W: codewords in registers, the next slice read ahead
+        constexpr int W = -CWD;
+        float rc[W], rn[W];
+#pragma unroll
+        for (int j = 0; j < W; j++) rc[j] = s.rsd[j];
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            if (m + 1 < MT) {
+#pragma unroll
+                for (int j = 0; j < W; j++) rn[j] = s.rsd[(m + 1) * W + j];
+            }
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < W; j++) {
+                float diff = rc[j] - cw[m * W + j];
+                acc += diff * diff;
+            }
+            s.lut[m * 256 + tid] = acc;
+#pragma unroll
+            for (int j = 0; j < W; j++) rc[j] = rn[j];
+            // two slices live at a time: the compiler may not hoist further reads
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else if constexpr (CWD > 0) {  // ds < CWD: codewords in registers, guarded
+        constexpr int W = CWD;
+        const int dsx = ds;
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             float acc = 0.0f;
