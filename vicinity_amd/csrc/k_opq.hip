@@ -10,7 +10,7 @@
 
 namespace vgpu {
 
-constexpr int ROT_RB = 8;  // rows per row group
+constexpr int ROT_RB = 16;  // rows per row group
 
 // out[r][i] = sum_j R[i][j] * x_r[j], j ascending from 0.0, each product and
 // each sum rounded (matrix_vector_multiply; this file is built without FMA
