@@ -945,19 +945,26 @@ void IvfpqIndex::search_filtered(const float* q, size_t nq, size_t k, const int*
     w_dist.reserve(nq * k);
     w_ids.reserve(nq * k);
     w_odist.reserve(nq * k);
-    ScanArgs a;
-    a.qn = w_qn.p;
-    a.qnorm = w_qnorm.p;
-    a.probe = w_probe.p;
-    a.nq = (int)nq;
-    a.P = (int)pmax;
-    a.kout = (int)k;
-    a.kk = (int)k;
-    a.exact = 1;
-    a.out_vidx = w_vidx.p;
-    a.out_dist = w_dist.p;
-    if (!rotation.empty()) a.rres = rotate_slots(w_qn.p, nq, pmax, w_probe.p, stream);
-    launch_scan8_filtered(dix, a, d_ecat.p, w_want.p, stream);
+    // OPQ rotates every (query, slot) residual first; queries go in chunks that
+    // bound that buffer at 2^28 floats (a widened query has up to L slots).
+    const bool opq = !rotation.empty();
+    const size_t chunk = opq ? std::max<size_t>(1, ((size_t)1 << 28) / (pmax * d)) : nq;
+    for (size_t q0 = 0; q0 < nq; q0 += chunk) {
+        const size_t nc = std::min(chunk, nq - q0);
+        ScanArgs a;
+        a.qn = w_qn.p + q0 * d;
+        a.qnorm = w_qnorm.p;  // not read by the filtered kernel
+        a.probe = w_probe.p + q0 * pmax;
+        a.nq = (int)nc;
+        a.P = (int)pmax;
+        a.kout = (int)k;
+        a.kk = (int)k;
+        a.exact = 1;
+        a.out_vidx = w_vidx.p + q0 * k;
+        a.out_dist = w_dist.p + q0 * k;
+        if (opq) a.rres = rotate_slots(a.qn, nc, pmax, a.probe, stream);
+        launch_scan8_filtered(dix, a, d_ecat.p, w_want.p + q0, stream);
+    }
     launch_finish(w_vidx.p, w_dist.p, d_doc_ids.p, (int)nq, (int)k, (int)k, w_ids.p, w_odist.p, nullptr,
                   nullptr, nullptr, nullptr, stream);
     VGPU_HIP(hipGetLastError());
