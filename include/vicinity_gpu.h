@@ -46,8 +46,9 @@ extern "C" {
 #define VGPU_MODE_FAST 0
 #define VGPU_MODE_EXACT 1
 
-/* IVFPQParams (src/ivf_pq/search.rs:284-312).  OPQ is not supported
- * (use_opq != 0 trains OPQ at build, opq.rs:65-109, for dimension <= 2048). */
+/* IVFPQParams (src/ivf_pq/search.rs:284-312).  use_opq != 0 trains OPQ at
+ * build (opq.rs:65-109) for dimension <= 2048; searches then scan in EXACT
+ * mode on rotated residual tables. */
 typedef struct vgpu_ivfpq_params {
     size_t num_clusters;  /* nlist */
     size_t nprobe;        /* default probes per query */

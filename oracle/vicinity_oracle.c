@@ -11,6 +11,9 @@
  *                          search_reranked 1117-1158, search_approx_internal_observed
  *                          1175-1391, search_with_filter 1407-1549,
  *                          find_nearest_centroids 1602-1617
+ *   src/ivf_pq/opq.rs      fit 65-109, quantize 112-115, approximate_distance_table
+ *                          120-123, matrix products 180-205, compute_optimal_rotation
+ *                          232-295
  *   src/ivf_pq/pq.rs       fit 75-124, quantize 136-161, compute_adc_table_into
  *                          196-266, distance_with_table 272-279, reconstruct 284-290
  *   src/pq_simd.rs         adc_batch_distances_into 99-115, adc_batch_256_into
@@ -44,6 +47,17 @@
  *                                          category over reconstruct, results
  *                                          carry the category
  *   or_pq_encode                           argmin property (pq.rs:485-551)
+ *   or_matvec / or_matvec_t                KATs opq.rs:362-385, float64 products,
+ *                                          a permutation exactly
+ *   or_polar                               numpy (LAPACK) SVD U V^T, R^T M
+ *                                          symmetric PSD, M = Q D gives Q; the
+ *                                          reference's nalgebra 0.35 float32 SVD
+ *                                          (absent) is unpinned to the last bit
+ *   or_opq_fit                             the reference's OPQ tests
+ *                                          (opq.rs:309-453, tests/opq_vs_pq.rs
+ *                                          MAE bounds), the last rotation is
+ *                                          polar of the last fit; its PQ fits are
+ *                                          seeded here, unseeded in the reference
  *   or_kmeans / or_ivfpq_build             the reference trains with the `clump`
  *                                          crate (^0.7.0, absent): this k-means
  *                                          is this project's own definition and
