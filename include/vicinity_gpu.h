@@ -10,10 +10,11 @@
  * Status codes map onto vicinity's RetrieveError (src/error.rs:17-80).  The
  * message of the last failure on the calling thread is vgpu_last_error().
  *
- * Threading: one handle may be searched from several threads (calls on one
- * handle are serialised internally, like the Python binding's search_lock,
- * src/python.rs:155); add/build/load/free need exclusive access, as the
- * reference's &mut self methods do.
+ * Threading: one handle may be searched from several threads at once, as the
+ * reference's search(&self) may (src/ivf_pq/search.rs:1087): each call
+ * borrows its own device workspace and, when it passes no stream, its own
+ * stream.  add/build/load/setters wait for running searches and exclude new
+ * ones, as the reference's &mut self methods do; free needs exclusive access.
  */
 #ifndef VICINITY_GPU_H
 #define VICINITY_GPU_H
@@ -64,8 +65,8 @@ typedef struct vgpu_ivfpq_info {
     int built, has_vectors, mode;
 } vgpu_ivfpq_info;
 
-/* Per-call device timings (ms, hipEvents on the handle's stream) and
- * counters of the last search_batch on a handle. */
+/* Per-call device timings (ms, hipEvents on the call's stream) and
+ * counters of the search that finished last on a handle. */
 typedef struct vgpu_search_stats {
     float ms_normalize, ms_coarse, ms_select, ms_scan, ms_fallback, ms_rerank, ms_total;
     uint64_t candidates;     /* sum over queries of scanned list entries */
@@ -132,8 +133,8 @@ int vgpu_ivfpq_search_reranked(vgpu_ivfpq *h, const float *query, size_t dim, si
 int vgpu_ivfpq_search_batch(vgpu_ivfpq *h, const float *queries, size_t nq, size_t dim, size_t k,
                             size_t nprobe, size_t rerank_pool, int64_t *out_ids,
                             float *out_dists);
-/* Same with device pointers on `stream` (a hipStream_t, NULL = the handle's
- * stream); returns after enqueueing and waiting for completion. */
+/* Same with device pointers on `stream` (a hipStream_t; NULL = the stream
+ * of the call's borrowed workspace); returns after the search completes. */
 int vgpu_ivfpq_search_batch_device(vgpu_ivfpq *h, const float *d_queries, size_t nq,
                                    size_t dim, size_t k, size_t nprobe, size_t rerank_pool,
                                    int64_t *d_out_ids, float *d_out_dists, void *stream);
@@ -161,6 +162,15 @@ int vgpu_ivfpq_set_category(vgpu_ivfpq *h, uint32_t doc_id, int64_t category);
 int vgpu_ivfpq_search_filtered(vgpu_ivfpq *h, const float *query, size_t dim, size_t k,
                                int64_t category, uint32_t *out_ids, float *out_dists,
                                size_t *out_len);
+
+/* search_with_filter for a batch: query i restricted to categories[i]
+ * (0..63), rows (nq, k) padded with (-1, +inf) like search_batch
+ * (python.rs:778-785).  The reference has the one-query form only
+ * (search.rs:1407-1549); each row equals that query's
+ * vgpu_ivfpq_search_filtered result. */
+int vgpu_ivfpq_search_filtered_batch(vgpu_ivfpq *h, const float *queries, size_t nq, size_t dim,
+                                     size_t k, const int64_t *categories, int64_t *out_ids,
+                                     float *out_dists);
 
 /* The lists' category bitmasks, masks u64[L] (L = the built index's list
  * count).  No counterpart in the reference's API: they carry
@@ -205,6 +215,22 @@ int vgpu_flat_search_batch_device(vgpu_flat *h, const float *d_queries, size_t n
 int vgpu_flat_last_ms(const vgpu_flat *h, float *ms_gemm, float *ms_total);
 
 /* ---- per-kernel test entry points (host buffers) -------------------------- */
+/* Host steps of the build, no device needed.  Inverted lists from list
+ * labels (search.rs:624-657): offsets u64[L+1], list_ids u32[n]; a label >= L
+ * (what a faulty device would return) is VGPU_ERR_DEVICE. */
+int vgpu_test_host_lists(const uint32_t *assign, size_t n, size_t L, uint64_t *offsets,
+                         uint32_t *list_ids);
+/* The host cosine k-means update of centroids f32[k*d] in place (float64
+ * member means in row order, re-normalised; empty keys keep their row); a
+ * label >= k is VGPU_ERR_DEVICE. */
+int vgpu_test_host_centroid_update(const float *x, size_t n, size_t d, const uint32_t *assign,
+                                   size_t k, float *centroids);
+/* The OPQ polar factor U V^T of M f32[d*d] (compute_optimal_rotation,
+ * opq.rs:280-294) into R f32[d*d]. */
+int vgpu_test_polar_factor(const float *m, size_t d, float *r);
+/* Bound on the rotated residuals (floats) one pass of a filtered search
+ * under OPQ holds; queries beyond it go in further passes (default 2^28). */
+int vgpu_test_set_rres_limit(vgpu_ivfpq *h, size_t floats);
 /* compute_adc_table_into (pq.rs:196-266) for nr residuals: tables f32[nr*M*K]. */
 int vgpu_test_adc_tables(const float *codebooks, size_t M, size_t K, size_t ds,
                          const float *residuals, size_t nr, float *tables);

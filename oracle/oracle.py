@@ -34,6 +34,17 @@ def build() -> str:
     return _LIB_PATH
 
 
+def use_native() -> str:
+    """Build the -march=native copy for this host (bit-identical results) and
+    make it the library every later call loads; call before the first use."""
+    global _LIB_PATH
+    if _lib is not None:
+        raise RuntimeError("the oracle library is already loaded")
+    subprocess.run(["make", "-s", "-C", _HERE, "native"], check=True)
+    _LIB_PATH = os.path.join(_HERE, "_build", "native", "libvicinity_oracle.so")
+    return _LIB_PATH
+
+
 class _Index(ctypes.Structure):
     _fields_ = [
         ("d", _sz), ("L", _sz), ("M", _sz), ("K", _sz), ("ds", _sz), ("n", _sz),

@@ -37,6 +37,11 @@
  *                                          limit 780-795, range KAT 1160-1187,
  *                                          error bound 1206-1318
  *   or_top_k                               KAT search.rs:2047-2069, brute sort
+ *   or_flat_search                         closed forms (distance.rs:78-83,
+ *                                          104-109 values), metric branches that
+ *                                          rank in opposite orders, ties by index,
+ *                                          k > n padding, float64 brute force,
+ *                                          each distance = its pair's primitive
  *   or_nearest_centroids                   brute force sort of float64 scores
  *   or_ivfpq_search                        full probe == exhaustive ADC scan
  *                                          over reconstruct (search.rs:2589-2645)
@@ -906,22 +911,27 @@ void or_matvec_t(const float *R, const float *v, size_t d, float *out) {
  * the largest component outside the columns so far (Gram-Schmidt, two passes,
  * lowest index on ties).  R = U V^T rounded to float32. */
 void or_polar(const float *Mf, size_t d, float *R) {
-    double *A = (double *)malloc(d * d * sizeof(double));
-    double *V = (double *)calloc(d * d, sizeof(double));
-    double *U = (double *)calloc(d * d, sizeof(double));
+    /* A, V and U are stored transposed (column j is row j); every sum runs
+     * over k in ascending order. */
+    double *At = (double *)malloc(d * d * sizeof(double));
+    double *Vt = (double *)calloc(d * d, sizeof(double));
+    double *Ut = (double *)calloc(d * d, sizeof(double));
+    double *S = (double *)calloc(d * d, sizeof(double));
     double *u = (double *)malloc(d * sizeof(double));
     double *best = (double *)malloc(d * sizeof(double));
     double *nrm = (double *)malloc(d * sizeof(double));
     char *ok = (char *)calloc(d, 1);
-    for (size_t i = 0; i < d * d; i++) A[i] = (double)Mf[i];
-    for (size_t i = 0; i < d; i++) V[i * d + i] = 1.0;
+    for (size_t k = 0; k < d; k++)
+        for (size_t j = 0; j < d; j++) At[j * d + k] = (double)Mf[k * d + j];
+    for (size_t i = 0; i < d; i++) Vt[i * d + i] = 1.0;
     for (int sweep = 0; sweep < 64; sweep++) {
         int changed = 0;
         for (size_t p = 0; p + 1 < d; p++)
             for (size_t q = p + 1; q < d; q++) {
+                double *ap = At + p * d, *aq = At + q * d;
                 double a = 0.0, b = 0.0, g = 0.0;
                 for (size_t k = 0; k < d; k++) {
-                    double x = A[k * d + p], y = A[k * d + q];
+                    double x = ap[k], y = aq[k];
                     a += x * x;
                     b += y * y;
                     g += x * y;
@@ -930,14 +940,16 @@ void or_polar(const float *Mf, size_t d, float *R) {
                 double z = (b - a) / (2.0 * g);
                 double t = (z >= 0.0 ? 1.0 : -1.0) / (fabs(z) + sqrt(1.0 + z * z));
                 double c = 1.0 / sqrt(1.0 + t * t), s = c * t;
+                double *vp = Vt + p * d, *vq = Vt + q * d;
                 for (size_t k = 0; k < d; k++) {
-                    double x = A[k * d + p], y = A[k * d + q];
-                    A[k * d + p] = c * x - s * y;
-                    A[k * d + q] = s * x + c * y;
-                    x = V[k * d + p];
-                    y = V[k * d + q];
-                    V[k * d + p] = c * x - s * y;
-                    V[k * d + q] = s * x + c * y;
+                    double x = ap[k], y = aq[k];
+                    ap[k] = c * x - s * y;
+                    aq[k] = s * x + c * y;
+                }
+                for (size_t k = 0; k < d; k++) {
+                    double x = vp[k], y = vq[k];
+                    vp[k] = c * x - s * y;
+                    vq[k] = s * x + c * y;
                 }
                 changed = 1;
             }
@@ -946,14 +958,14 @@ void or_polar(const float *Mf, size_t d, float *R) {
     double smax = 0.0;
     for (size_t j = 0; j < d; j++) {
         double s2 = 0.0;
-        for (size_t k = 0; k < d; k++) s2 += A[k * d + j] * A[k * d + j];
+        for (size_t k = 0; k < d; k++) s2 += At[j * d + k] * At[j * d + k];
         nrm[j] = sqrt(s2);
         if (nrm[j] > smax) smax = nrm[j];
     }
     for (size_t j = 0; j < d; j++)
         if (nrm[j] > 0.0 && nrm[j] > 1e-12 * smax) {
             ok[j] = 1;
-            for (size_t k = 0; k < d; k++) U[k * d + j] = A[k * d + j] / nrm[j];
+            for (size_t k = 0; k < d; k++) Ut[j * d + k] = At[j * d + k] / nrm[j];
         }
     for (size_t j = 0; j < d; j++) {
         if (ok[j]) continue;
@@ -963,9 +975,10 @@ void or_polar(const float *Mf, size_t d, float *R) {
             for (int pass = 0; pass < 2; pass++)
                 for (size_t c = 0; c < d; c++) {
                     if (!ok[c]) continue;
+                    const double *uc = Ut + c * d;
                     double pr = 0.0;
-                    for (size_t k = 0; k < d; k++) pr += U[k * d + c] * u[k];
-                    for (size_t k = 0; k < d; k++) u[k] -= pr * U[k * d + c];
+                    for (size_t k = 0; k < d; k++) pr += uc[k] * u[k];
+                    for (size_t k = 0; k < d; k++) u[k] -= pr * uc[k];
                 }
             double s2 = 0.0;
             for (size_t k = 0; k < d; k++) s2 += u[k] * u[k];
@@ -975,18 +988,20 @@ void or_polar(const float *Mf, size_t d, float *R) {
             }
         }
         bn = sqrt(bn);
-        for (size_t k = 0; k < d; k++) U[k * d + j] = best[k] / bn;
+        for (size_t k = 0; k < d; k++) Ut[j * d + k] = best[k] / bn;
         ok[j] = 1;
     }
-    for (size_t i = 0; i < d; i++)
-        for (size_t j = 0; j < d; j++) {
-            double s = 0.0;
-            for (size_t k = 0; k < d; k++) s += U[i * d + k] * V[j * d + k];
-            R[i * d + j] = (float)s;
+    /* R[i][j] = sum over k ascending of U[i][k] V[j][k] */
+    for (size_t k = 0; k < d; k++)
+        for (size_t i = 0; i < d; i++) {
+            double ui = Ut[k * d + i];
+            for (size_t j = 0; j < d; j++) S[i * d + j] += ui * Vt[k * d + j];
         }
-    free(A);
-    free(V);
-    free(U);
+    for (size_t i = 0; i < d * d; i++) R[i] = (float)S[i];
+    free(At);
+    free(Vt);
+    free(Ut);
+    free(S);
     free(u);
     free(best);
     free(nrm);

@@ -142,3 +142,48 @@ def test_config_flat_100k_d96(oracle):
     oids, odists = oracle.flat_search(w.base, w.queries[qs], 10, metric=0)
     assert np.array_equal(ids[qs], oids)
     assert dists[qs].tobytes() == odists.tobytes()
+
+
+def test_config_1m_d128_headline(oracle):
+    """The configuration the benchmark is quoted on, built exactly as
+    bench.py builds it: 1M x 128 Gaussian mixture (datagen.ivfpq_1m), nlist
+    4096, M 16 x 8, ksub 256, nprobe 32, k 100, training sample 262,144, 25
+    k-means iterations.  The whole 10k batch equals the oracle on the exported
+    arrays (ids, float32 bits); the build's assignments and codes are the
+    oracle's argmins on 4,000 sampled vectors; EXACT mode equals FAST."""
+    from vicinity_amd import IVFPQIndex, datagen
+
+    _print_case("1M x 128 headline: generate")
+    w = datagen.ivfpq_1m()
+    p = w.params
+    _print_case("1M x 128 headline: build")
+    ix = IVFPQIndex(128, num_clusters=p["num_clusters"], num_codebooks=p["num_codebooks"],
+                    codebook_size=p["codebook_size"], nprobe=p["nprobe"], seed=42)
+    ix.add_items(w.base)
+    ix.build(training_sample_size=262_144, kmeans_max_iter=25)
+    k, nprobe = p["k"], p["nprobe"]
+    _print_case("1M x 128 headline: search 10k")
+    ids, dists = ix.batch_search(w.queries, k, nprobe=nprobe)
+    st = ix.last_stats()
+    _check_rows(ids, dists, k)
+    art = ix.export()
+    _print_case("1M x 128 headline: oracle on all 10k queries")
+    oix = oracle.Index(art["centroids"], art["codebooks"], art["list_offsets"], art["list_ids"],
+                       art["codes"], art["doc_ids"], None, art["M"], art["K"])
+    oids, odists = oix.search_batch(w.queries, k, nprobe, threads=16)
+    assert np.array_equal(ids, oids)
+    assert dists.tobytes() == odists.tobytes()
+    # the probe sets themselves (search.rs:1602-1617) on a sample
+    rng = np.random.default_rng(10)
+    qs = rng.choice(len(w.queries), 500, replace=False)
+    probes = ix.probe(w.queries[qs], nprobe)
+    for row, qi in zip(probes, qs):
+        assert row.tolist() == oix.probe(w.queries[qi], nprobe)[0].tolist()
+    _print_case("1M x 128 headline: build argmins")
+    _check_build(oracle, art, art["vectors"], rng.choice(len(w.base), 4000, replace=False))
+    _print_case("1M x 128 headline: exact mode")
+    ix.set_mode("exact")
+    eids, edists = ix.batch_search(w.queries[:2000], k, nprobe=nprobe)
+    assert np.array_equal(eids, ids[:2000])
+    assert edists.tobytes() == dists[:2000].tobytes()
+    assert st["nq"] == len(w.queries) and st["candidates"] > 0

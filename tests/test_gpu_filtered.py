@@ -167,3 +167,44 @@ def test_filter_errors(vg, k256):
     with pytest.raises(ValueError, match="doesn't match"):
         plain.search_with_filter(rng.random(16, dtype=np.float32), 5,
                                  MetadataFilter.equals("group", 1))
+
+
+def test_nprobe_zero_widens_on_a_fresh_handle_and_after_a_search(vg, oracle):
+    """set_nprobe(0) probes no list, so every list that carries the category
+    is a widening candidate (search.rs:1486-1545).  The queries must still be
+    normalised for the scan, on a handle that never searched and on one whose
+    last search left other queries in its buffers."""
+    from vicinity_amd import MetadataFilter, _lib
+
+    _print_case("filtered search with nprobe 0 (fresh handle, then after a search)")
+    ix, rng = _build(vg, 2000, 32, 16, 8, 256, 3, 5)
+    art = ix.export()
+    oix, cat = _oracle_index(oracle, art), _categories(art, _group_of)
+    L = _lib.load()
+    _lib.check(L.vgpu_ivfpq_set_nprobe(ix._h, 0))
+    queries = rng.standard_normal((6, 32)).astype(np.float32)
+    for t, q in enumerate(queries):
+        if t == 3:  # a plain search in between refills the workspace with other queries
+            ix.batch_search(rng.standard_normal((64, 32)).astype(np.float32), 10, nprobe=4)
+        g = t % 7
+        ids, dists = ix.search_with_filter(q, 20, MetadataFilter.equals("group", g))
+        oids, odists = oix.search_filtered(q, 20, 0, g, cat)
+        assert ids.tolist() == oids.tolist(), t
+        assert dists.tobytes() == odists.tobytes(), t
+        assert len(ids) == 20
+
+
+def test_batched_filter_rows_equal_single_queries(k256):
+    from vicinity_amd import MetadataFilter
+
+    ix, art, oix, cat, rng = k256
+    _print_case("batched filtered search vs one query at a time")
+    qs = rng.standard_normal((40, 32)).astype(np.float32)
+    filters = [MetadataFilter.equals("group", t % 7) for t in range(40)]
+    for k in (1, 17, 700):
+        ids, dists = ix.batch_search_with_filter(qs, k, filters)
+        for t in range(40):
+            sids, sd = ix.search_with_filter(qs[t], k, filters[t])
+            m = len(sids)
+            assert ids[t, :m].tolist() == sids.tolist() and dists[t, :m].tobytes() == sd.tobytes()
+            assert (ids[t, m:] == -1).all() and np.isinf(dists[t, m:]).all()

@@ -141,12 +141,30 @@ def test_opq_filtered_search_is_bitexact(vg, oracle):
     art = ix.export()
     oix = _oracle_index(oracle, art)
     cat = np.array([(d - 70_000) % 5 if d - 70_000 > 2 else 9 for d in art["doc_ids"]], np.int8)
+    qs, gs = [], []
     for t in range(12):
         g = 9 if t % 4 == 0 else t % 5  # 9: three documents, the probe widens
         q = rng.standard_normal(16).astype(np.float32)
         ids, dists = ix.search_with_filter(q, 10, MetadataFilter.equals("g", g))
         oids, odists = oix.search_filtered(q, 10, 2, g, cat)
         assert ids.tolist() == oids.tolist() and dists.tobytes() == odists.tobytes()
+        qs.append(q)
+        gs.append(g)
+    # A batch whose rotated residuals go in several passes: a query's slots
+    # are the lists that carry its category (two or three here), 16 floats
+    # each, and the bound holds seven slots, so a pass takes two or three
+    # queries and the 12 queries take four to six passes.
+    from vicinity_amd import _lib
+
+    _print_case("OPQ filtered batch in several rotation passes")
+    _lib.check(_lib.load().vgpu_test_set_rres_limit(ix._h, 7 * 16))
+    ids, dists = ix.batch_search_with_filter(np.stack(qs), 10,
+                                             [MetadataFilter.equals("g", g) for g in gs])
+    for t in range(12):
+        oids, odists = oix.search_filtered(qs[t], 10, 2, gs[t], cat)
+        m = len(oids)
+        assert ids[t, :m].tolist() == oids.tolist() and dists[t, :m].tobytes() == odists.tobytes()
+        assert (ids[t, m:] == -1).all()
 
 
 def test_opq_snapshot_round_trip(k64, tmp_path):

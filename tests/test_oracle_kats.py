@@ -467,3 +467,91 @@ def test_reranked_distances_are_exact_cosine(oracle):
     assert ids[0] == 3
     for i, dd in zip(ids, d):
         assert dd == np.float32(1.0) - oracle.dot(q, x[i])
+
+
+# ---- flat exact search: src/distance.rs:78-83, 104-109; ground truth
+# ---- search.rs:3376-3392 (brute force, ascending, ties by index) ---------
+
+def test_flat_search_closed_forms(oracle):
+    # l2_distance_squared: [1,2,3] to [4,5,6] is 27, to 0 is 14, to itself 0.
+    base = np.array([[4, 5, 6], [1, 2, 3], [0, 0, 0]], np.float32)
+    ids, d = oracle.flat_search(base, np.array([[1, 2, 3]], np.float32), 3, metric=0)
+    assert ids.tolist() == [[1, 2, 0]] and d.tolist() == [[0.0, 14.0, 27.0]]
+    # cosine_distance_normalized = 1 - dot on unit vectors.
+    h = np.float32(np.sqrt(np.float32(0.5)))
+    unit = np.array([[1, 0], [0, 1], [h, h]], np.float32)
+    ids, d = oracle.flat_search(unit, np.array([[1, 0]], np.float32), 3, metric=1)
+    assert ids.tolist() == [[0, 2, 1]]
+    assert d.tolist() == [[0.0, float(np.float32(1) - h), 1.0]]
+
+
+def test_flat_search_metric_branches_differ(oracle):
+    # Unnormalised rows where squared L2 and 1 - dot rank in opposite orders:
+    # a wrong metric branch fails one of the two assertions.
+    base = np.array([[10, 0], [0.9, 0.1]], np.float32)
+    q = np.array([[1, 0]], np.float32)
+    assert oracle.flat_search(base, q, 2, metric=0)[0].tolist() == [[1, 0]]
+    assert oracle.flat_search(base, q, 2, metric=1)[0].tolist() == [[0, 1]]
+
+
+def test_flat_search_ties_padding_and_threads(oracle):
+    rng = np.random.default_rng(5)
+    base = rng.standard_normal((40, 6)).astype(np.float32)
+    base[[3, 7, 11, 30]] = base[20]  # five equal rows: ties go to the lower index
+    q = base[20:21].copy()
+    for metric in (0, 1):
+        ids, d = oracle.flat_search(base, q, 5, metric=metric)
+        if metric == 0:
+            assert ids.tolist() == [[3, 7, 11, 20, 30]]
+            assert (d == 0).all()
+        else:  # the equal rows keep index order wherever they fall in the row
+            tied = [i for i in ids[0].tolist() if i in (3, 7, 11, 20, 30)]
+            assert tied == sorted(tied)
+    # k > n pads with (-1, +inf) (python.rs:778-785 convention)
+    ids, d = oracle.flat_search(base[:4], q, 7, metric=0)
+    assert ids[0, 4:].tolist() == [-1, -1, -1] and np.isinf(d[0, 4:]).all()
+    assert sorted(ids[0, :4].tolist()) == [0, 1, 2, 3]
+    # one thread and many give the same rows
+    qs = rng.standard_normal((9, 6)).astype(np.float32)
+    a = oracle.flat_search(base, qs, 6, metric=0, threads=1)
+    b = oracle.flat_search(base, qs, 6, metric=0, threads=4)
+    assert np.array_equal(a[0], b[0]) and a[1].tobytes() == b[1].tobytes()
+
+
+@pytest.mark.parametrize("metric", [0, 1])
+def test_flat_search_equals_float64_brute_force(oracle, metric):
+    """Each returned distance is the sequential float32 primitive of its own
+    (query, id) pair (a stride or pairing mistake fails), and the ranking
+    equals float64 brute force wherever the float64 gap exceeds the float32
+    rounding bound of the sums (d * 2^-23 * the sum of magnitudes)."""
+    rng = np.random.default_rng(11 + metric)
+    n, d, nq, k = 300, 19, 7, 12
+    base = rng.standard_normal((n, d)).astype(np.float32)
+    qs = rng.standard_normal((nq, d)).astype(np.float32)
+    if metric == 1:
+        base = oracle.normalize_rows(base)
+        qs = oracle.normalize_rows(qs)
+    ids, dist = oracle.flat_search(base, qs, k, metric=metric)
+    for i in range(nq):
+        for j in range(k):
+            x = base[ids[i, j]]
+            prim = oracle.l2sq(qs[i], x) if metric == 0 else np.float32(1) - oracle.dot(qs[i], x)
+            assert dist[i, j] == np.float32(prim)
+        q64, b64 = qs[i].astype(np.float64), base.astype(np.float64)
+        if metric == 0:
+            exact = ((b64 - q64) ** 2).sum(axis=1)
+            mag = ((b64 - q64) ** 2).sum(axis=1)
+        else:
+            exact = 1.0 - b64 @ q64
+            mag = np.abs(b64 * q64).sum(axis=1) + 1.0
+        bound = d * 2.0 ** -23 * mag
+        assert np.all(np.abs(dist[i].astype(np.float64) - exact[ids[i]]) <= bound[ids[i]])
+        order = np.argsort(exact, kind="stable")
+        # every id the float64 ranking puts clearly inside the top-k is returned
+        kth = exact[order[k - 1]]
+        clear = order[: k][exact[order[:k]] < kth - 2 * bound.max()]
+        assert set(clear.tolist()) <= set(ids[i].tolist())
+        # and nothing clearly outside it is
+        outside = np.where(exact > kth + 2 * bound.max())[0]
+        assert not set(outside.tolist()) & set(ids[i].tolist())
+        assert np.all(np.diff(dist[i]) >= 0)

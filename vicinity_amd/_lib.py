@@ -94,6 +94,7 @@ SIGNATURES = {
     "vgpu_ivfpq_set_category": (_i, [_H, ctypes.c_uint32, ctypes.c_int64]),
     "vgpu_ivfpq_search_filtered": (_i, [_H, _vp, _sz, _sz, ctypes.c_int64, _vp, _vp,
                                         ctypes.POINTER(_sz)]),
+    "vgpu_ivfpq_search_filtered_batch": (_i, [_H, _vp, _sz, _sz, _sz, _vp, _vp, _vp]),
     "vgpu_ivfpq_get_list_masks": (_i, [_H, _vp, _sz]),
     "vgpu_ivfpq_set_list_masks": (_i, [_H, _vp, _sz]),
     "vgpu_ivfpq_get_rotation": (_i, [_H, _vp, _sz, _vp]),
@@ -106,6 +107,10 @@ SIGNATURES = {
     "vgpu_flat_search_batch": (_i, [_H, _vp, _sz, _sz, _sz, _vp, _vp]),
     "vgpu_flat_search_batch_device": (_i, [_H, _vp, _sz, _sz, _sz, _vp, _vp, _vp]),
     "vgpu_flat_last_ms": (_i, [_H, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]),
+    "vgpu_test_host_lists": (_i, [_vp, _sz, _sz, _vp, _vp]),
+    "vgpu_test_host_centroid_update": (_i, [_vp, _sz, _sz, _vp, _sz, _vp]),
+    "vgpu_test_polar_factor": (_i, [_vp, _sz, _vp]),
+    "vgpu_test_set_rres_limit": (_i, [_H, _sz]),
     "vgpu_test_adc_tables": (_i, [_vp, _sz, _sz, _sz, _vp, _sz, _vp]),
     "vgpu_test_pq_encode": (_i, [_vp, _sz, _sz, _sz, _vp, _sz, _vp]),
     "vgpu_test_normalize": (_i, [_vp, _sz, _sz, _vp]),

@@ -165,4 +165,16 @@ void launch_finish(const uint32_t* vidx, const float* dist, const uint32_t* doc_
                        cflag_count);
 }
 
+// Clear n 64-bit words (the per-call scalars) with a kernel, not a
+// memset, so a captured stream records a kernel node.
+__global__ void zero_words_kernel(unsigned long long* __restrict__ p, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0ull;
+}
+
+void launch_zero_words(unsigned long long* p, size_t n, hipStream_t s) {
+    if (n == 0) return;
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);
+}
+
 }  // namespace vgpu

@@ -1,8 +1,11 @@
 // extern "C" boundary: argument checks, exception -> status mapping and the
 // thread-local error message.  Every entry point is declared in
 // include/vicinity_gpu.h with the reference interface it replaces.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
+#include <shared_mutex>
 #include <string>
 
 #include "vgpu_runtime.h"
@@ -102,7 +105,7 @@ void vgpu_ivfpq_free(vgpu_ivfpq* h) {
 int vgpu_ivfpq_add(vgpu_ivfpq* h, const uint32_t* doc_ids, const float* vectors, size_t n) {
     return guard([&] {
         need(h && (n == 0 || (doc_ids && vectors)), VGPU_ERR_INVALID_PARAMETER, "null argument");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::unique_lock<std::shared_mutex> lk(h->ix->mu);
         h->ix->add(doc_ids, vectors, n);
     });
 }
@@ -110,7 +113,7 @@ int vgpu_ivfpq_add(vgpu_ivfpq* h, const uint32_t* doc_ids, const float* vectors,
 int vgpu_ivfpq_build(vgpu_ivfpq* h, size_t training_sample_size, size_t kmeans_max_iter) {
     return guard([&] {
         need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::unique_lock<std::shared_mutex> lk(h->ix->mu);
         h->ix->build(training_sample_size, kmeans_max_iter);
     });
 }
@@ -122,7 +125,7 @@ int vgpu_ivfpq_load(vgpu_ivfpq* h, const float* centroids, size_t num_centroids,
     return guard([&] {
         need(h && centroids && codebooks && list_offsets && (num_vectors == 0 || (list_ids && codes)),
              VGPU_ERR_INVALID_PARAMETER, "null argument");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::unique_lock<std::shared_mutex> lk(h->ix->mu);
         need(!h->ix->built, VGPU_ERR_ALREADY_BUILT, "IVF-PQ index is already built");
         h->ix->load(centroids, num_centroids, codebooks, codebook_size, list_offsets, list_ids, codes,
                     doc_ids, vectors, num_vectors);
@@ -132,7 +135,7 @@ int vgpu_ivfpq_load(vgpu_ivfpq* h, const float* centroids, size_t num_centroids,
 int vgpu_ivfpq_set_nprobe(vgpu_ivfpq* h, size_t nprobe) {
     return guard([&] {
         need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::unique_lock<std::shared_mutex> lk(h->ix->mu);
         h->ix->params.nprobe = nprobe;
     });
 }
@@ -141,7 +144,7 @@ int vgpu_ivfpq_set_mode(vgpu_ivfpq* h, int mode) {
     return guard([&] {
         need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
         need(mode == VGPU_MODE_FAST || mode == VGPU_MODE_EXACT, VGPU_ERR_INVALID_PARAMETER, "unknown mode");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::unique_lock<std::shared_mutex> lk(h->ix->mu);
         h->ix->mode = mode;
     });
 }
@@ -149,7 +152,7 @@ int vgpu_ivfpq_set_mode(vgpu_ivfpq* h, int mode) {
 int vgpu_ivfpq_set_profiling(vgpu_ivfpq* h, int enabled) {
     return guard([&] {
         need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::unique_lock<std::shared_mutex> lk(h->ix->mu);
         need(enabled >= 0 && enabled <= 2, VGPU_ERR_INVALID_PARAMETER, "profiling level must be 0, 1 or 2");
         h->ix->profiling = enabled;
     });
@@ -158,7 +161,7 @@ int vgpu_ivfpq_set_profiling(vgpu_ivfpq* h, int enabled) {
 int vgpu_ivfpq_compact(vgpu_ivfpq* h) {
     return guard([&] {
         need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::unique_lock<std::shared_mutex> lk(h->ix->mu);
         need(h->ix->built, VGPU_ERR_INVALID_PARAMETER, "index must be built before compact");
         h->ix->vectors.clear();
         h->ix->vectors.shrink_to_fit();
@@ -171,6 +174,7 @@ int vgpu_ivfpq_compact(vgpu_ivfpq* h) {
 int vgpu_ivfpq_get_info(const vgpu_ivfpq* h, vgpu_ivfpq_info* out) {
     return guard([&] {
         need(h && out, VGPU_ERR_INVALID_PARAMETER, "null argument");
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
         const IvfpqIndex& ix = *h->ix;
         out->dimension = ix.d;
         out->num_vectors = ix.n();
@@ -197,7 +201,7 @@ int vgpu_ivfpq_search_batch(vgpu_ivfpq* h, const float* queries, size_t nq, size
     return guard([&] {
         need(h && (nq == 0 || k == 0 || (queries && out_ids && out_dists)), VGPU_ERR_INVALID_PARAMETER,
              "null argument");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
         need(h->ix->built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
         check_dim(*h->ix, dim);
         h->ix->search_host(queries, nq, k, nprobe, rerank_pool, out_ids, out_dists);
@@ -210,12 +214,11 @@ int vgpu_ivfpq_search_batch_device(vgpu_ivfpq* h, const float* d_queries, size_t
     return guard([&] {
         need(h && (nq == 0 || k == 0 || (d_queries && d_out_ids && d_out_dists)),
              VGPU_ERR_INVALID_PARAMETER, "null argument");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
         need(h->ix->built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
         check_dim(*h->ix, dim);
         h->ix->search_device(d_queries, nq, k, nprobe, rerank_pool, d_out_ids, d_out_dists,
                              (hipStream_t)stream);
-        VGPU_HIP(hipStreamSynchronize(stream ? (hipStream_t)stream : h->ix->stream));
     });
 }
 
@@ -226,7 +229,7 @@ static int search_one(vgpu_ivfpq* h, const float* query, size_t dim, size_t k, s
     return guard([&] {
         need(h && out_len && (k == 0 || (query && out_ids && out_dists)), VGPU_ERR_INVALID_PARAMETER,
              "null argument");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
         *out_len = 0;
         need(h->ix->built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
         check_dim(*h->ix, dim);
@@ -260,14 +263,14 @@ int vgpu_ivfpq_search_reranked(vgpu_ivfpq* h, const float* query, size_t dim, si
 int vgpu_ivfpq_last_stats(const vgpu_ivfpq* h, vgpu_search_stats* out) {
     return guard([&] {
         need(h && out, VGPU_ERR_INVALID_PARAMETER, "null argument");
-        *out = h->ix->stats;
+        *out = h->ix->last_stats();
     });
 }
 
 int vgpu_ivfpq_enable_filtering(vgpu_ivfpq* h) {
     return guard([&] {
         need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::unique_lock<std::shared_mutex> lk(h->ix->mu);
         h->ix->enable_filtering();
     });
 }
@@ -275,7 +278,7 @@ int vgpu_ivfpq_enable_filtering(vgpu_ivfpq* h) {
 int vgpu_ivfpq_set_category(vgpu_ivfpq* h, uint32_t doc_id, int64_t category) {
     return guard([&] {
         need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::unique_lock<std::shared_mutex> lk(h->ix->mu);
         need(h->ix->filtering, VGPU_ERR_UNSUPPORTED,
              "filtered search: rebuild the index with IVFPQIndex::with_filtering()");
         need(category >= -1 && category <= 63, VGPU_ERR_INVALID_PARAMETER,
@@ -290,7 +293,7 @@ int vgpu_ivfpq_search_filtered(vgpu_ivfpq* h, const float* query, size_t dim, si
     return guard([&] {
         need(h && out_len && (k == 0 || (query && out_ids && out_dists)), VGPU_ERR_INVALID_PARAMETER,
              "null argument");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
         *out_len = 0;
         need(h->ix->built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
         check_dim(*h->ix, dim);
@@ -313,10 +316,31 @@ int vgpu_ivfpq_search_filtered(vgpu_ivfpq* h, const float* query, size_t dim, si
     });
 }
 
+int vgpu_ivfpq_search_filtered_batch(vgpu_ivfpq* h, const float* queries, size_t nq, size_t dim, size_t k,
+                                     const int64_t* categories, int64_t* out_ids, float* out_dists) {
+    return guard([&] {
+        need(h && (nq == 0 || k == 0 || (queries && categories && out_ids && out_dists)),
+             VGPU_ERR_INVALID_PARAMETER, "null argument");
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
+        need(h->ix->built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
+        check_dim(*h->ix, dim);
+        need(h->ix->filtering, VGPU_ERR_INVALID_PARAMETER,
+             "filter field doesn't match index filter field (None)");
+        std::vector<int> cats(nq);
+        for (size_t i = 0; i < nq; i++) {
+            need(categories[i] >= 0 && categories[i] <= 63, VGPU_ERR_INVALID_PARAMETER,
+                 "category ID " + std::to_string(categories[i]) + " exceeds bitmask limit of 63");
+            cats[i] = (int)categories[i];
+        }
+        if (nq == 0 || k == 0) return;
+        h->ix->search_filtered(queries, nq, k, cats.data(), out_ids, out_dists);
+    });
+}
+
 int vgpu_ivfpq_get_list_masks(const vgpu_ivfpq* h, uint64_t* masks, size_t L) {
     return guard([&] {
         need(h && (L == 0 || masks), VGPU_ERR_INVALID_PARAMETER, "null argument");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
         need(h->ix->built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: list bitmasks before build");
         need(L == h->ix->L, VGPU_ERR_INVALID_PARAMETER, "list count mismatch");
         for (size_t l = 0; l < L; l++) masks[l] = l < h->ix->list_mask.size() ? h->ix->list_mask[l] : 0ull;
@@ -326,7 +350,7 @@ int vgpu_ivfpq_get_list_masks(const vgpu_ivfpq* h, uint64_t* masks, size_t L) {
 int vgpu_ivfpq_set_list_masks(vgpu_ivfpq* h, const uint64_t* masks, size_t L) {
     return guard([&] {
         need(h && (L == 0 || masks), VGPU_ERR_INVALID_PARAMETER, "null argument");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::unique_lock<std::shared_mutex> lk(h->ix->mu);
         need(h->ix->built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: list bitmasks before build");
         need(L == h->ix->L, VGPU_ERR_INVALID_PARAMETER, "list count mismatch");
         h->ix->list_mask.assign(masks, masks + L);
@@ -336,7 +360,7 @@ int vgpu_ivfpq_set_list_masks(vgpu_ivfpq* h, const uint64_t* masks, size_t L) {
 int vgpu_ivfpq_get_rotation(const vgpu_ivfpq* h, float* R, size_t len, int* present) {
     return guard([&] {
         need(h && present, VGPU_ERR_INVALID_PARAMETER, "null argument");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
         const auto& rot = h->ix->rotation;
         *present = rot.empty() ? 0 : 1;
         if (rot.empty()) return;
@@ -348,7 +372,7 @@ int vgpu_ivfpq_get_rotation(const vgpu_ivfpq* h, float* R, size_t len, int* pres
 int vgpu_ivfpq_set_rotation(vgpu_ivfpq* h, const float* R, size_t len) {
     return guard([&] {
         need(h, VGPU_ERR_INVALID_PARAMETER, "null argument");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::unique_lock<std::shared_mutex> lk(h->ix->mu);
         need(!R || len == h->ix->d * h->ix->d, VGPU_ERR_INVALID_PARAMETER, "rotation must hold dim * dim floats");
         h->ix->set_rotation(R);
     });
@@ -358,7 +382,7 @@ int vgpu_ivfpq_probe_batch(vgpu_ivfpq* h, const float* queries, size_t nq, size_
                            uint32_t* lists, size_t* out_p) {
     return guard([&] {
         need(h && out_p && (nq == 0 || (queries && lists)), VGPU_ERR_INVALID_PARAMETER, "null argument");
-        std::lock_guard<std::mutex> lk(h->ix->mu);
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
         need(h->ix->built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: probe before build");
         check_dim(*h->ix, dim);
         *out_p = std::min(nprobe, h->ix->L);
@@ -372,6 +396,7 @@ int vgpu_ivfpq_export(const vgpu_ivfpq* h, float* centroids, float* codebooks, u
                       uint32_t* list_ids, uint8_t* codes, uint32_t* doc_ids, float* vectors) {
     return guard([&] {
         need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
         const IvfpqIndex& ix = *h->ix;
         need(ix.built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: export before build");
         auto cp = [](void* dst, const void* src, size_t bytes) {
@@ -463,6 +488,40 @@ int vgpu_flat_last_ms(const vgpu_flat* h, float* ms_gemm, float* ms_total) {
 }
 
 /* ---- per-kernel test entry points ---------------------------------------- */
+
+int vgpu_test_host_lists(const uint32_t* assign, size_t n, size_t L, uint64_t* offsets, uint32_t* list_ids) {
+    return guard([&] {
+        need((n == 0 || (assign && list_ids)) && offsets && L, VGPU_ERR_INVALID_PARAMETER, "bad argument");
+        std::vector<uint64_t> off;
+        std::vector<uint32_t> ids;
+        vgpu::build_lists(assign, n, L, off, ids);
+        std::copy(off.begin(), off.end(), offsets);
+        std::copy(ids.begin(), ids.end(), list_ids);
+    });
+}
+
+int vgpu_test_host_centroid_update(const float* x, size_t n, size_t d, const uint32_t* assign, size_t k,
+                                   float* centroids) {
+    return guard([&] {
+        need((n == 0 || (x && assign)) && centroids && d && k, VGPU_ERR_INVALID_PARAMETER, "bad argument");
+        vgpu::centroid_update(x, n, d, assign, k, centroids);
+    });
+}
+
+int vgpu_test_polar_factor(const float* m, size_t d, float* r) {
+    return guard([&] {
+        need(m && r && d, VGPU_ERR_INVALID_PARAMETER, "bad argument");
+        vgpu::polar_factor(m, d, r);
+    });
+}
+
+int vgpu_test_set_rres_limit(vgpu_ivfpq* h, size_t floats) {
+    return guard([&] {
+        need(h && floats, VGPU_ERR_INVALID_PARAMETER, "bad argument");
+        std::unique_lock<std::shared_mutex> lk(h->ix->mu);
+        h->ix->rres_limit = floats;
+    });
+}
 
 int vgpu_test_adc_tables(const float* codebooks, size_t M, size_t K, size_t ds, const float* residuals,
                          size_t nr, float* tables) {

@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstring>
 #include <numeric>
+#include <type_traits>
 #include <unordered_map>
 
 #include "vgpu_runtime.h"
@@ -83,6 +84,61 @@ void normalize_row(const float* x, size_t d, float* out) {
     }
 }
 
+// Labels read back from the device index host arrays: one outside 0..L-1
+// means the device returned garbage, reported as a device error instead of
+// being used as an index.
+template <typename T>
+static void check_labels(const T* labels, size_t n, size_t stride, size_t L, const char* what) {
+    for (size_t i = 0; i < n; i++)
+        if ((size_t)labels[i * stride] >= L)
+            throw Error(VGPU_ERR_DEVICE, std::string(what) + ": row " + std::to_string(i) + " has label " +
+                                             std::to_string((size_t)labels[i * stride]) + ", outside 0.." +
+                                             std::to_string(L - 1));
+}
+
+// Inverted lists from list labels (search.rs:624-657): list l holds the rows
+// labelled l in insertion order; offsets[L + 1], list_ids[n].
+void build_lists(const uint32_t* assign, size_t n, size_t L, std::vector<uint64_t>& offsets,
+                 std::vector<uint32_t>& list_ids) {
+    check_labels(assign, n, 1, L, "list assignment");
+    offsets.assign(L + 1, 0);
+    for (size_t i = 0; i < n; i++) offsets[assign[i] + 1]++;
+    for (size_t l = 0; l < L; l++) offsets[l + 1] += offsets[l];
+    list_ids.resize(n);
+    std::vector<uint64_t> fill(offsets.begin(), offsets.end() - 1);
+    for (size_t i = 0; i < n; i++) list_ids[fill[assign[i]]++] = (uint32_t)i;
+}
+
+// Lloyd update on the host (rows wider than the update kernel's 256
+// floats): every non-empty key becomes the float64 mean of its members in
+// row order, cast to float, re-normalised when `normalize`; empty keys keep
+// their row.  Row i's slice is x[i * ld + off .. + w), its label
+// labels[i * lstride]; out[k * w].
+template <typename T>
+static void host_mean_update(const float* x, size_t n, size_t ld, size_t off, size_t w, const T* labels,
+                             size_t lstride, size_t k, bool normalize, float* out) {
+    check_labels(labels, n, lstride, k, "k-means labels");
+    std::vector<double> sums(k * w, 0.0);
+    std::vector<uint64_t> counts(k, 0);
+    for (size_t i = 0; i < n; i++) {
+        const size_t c = (size_t)labels[i * lstride];
+        double* sc = &sums[c * w];
+        const float* xi = &x[i * ld + off];
+        for (size_t j = 0; j < w; j++) sc[j] += (double)xi[j];
+        counts[c]++;
+    }
+    for (size_t c = 0; c < k; c++) {
+        if (!counts[c]) continue;
+        float* cc = &out[c * w];
+        for (size_t j = 0; j < w; j++) cc[j] = (float)(sums[c * w + j] / (double)counts[c]);
+        if (normalize) normalize_row(cc, w, cc);
+    }
+}
+
+void centroid_update(const float* x, size_t n, size_t d, const uint32_t* assign, size_t k, float* cent) {
+    host_mean_update(x, n, d, 0, d, assign, 1, k, true, cent);
+}
+
 static float row_norm_bound(const float* x, size_t d) {
     double s = 0.0;
     for (size_t i = 0; i < d; i++) s += (double)x[i] * (double)x[i];
@@ -94,17 +150,13 @@ IvfpqIndex::IvfpqIndex(size_t dim, const vgpu_ivfpq_params& p) : d(dim), params(
     if (p.codebook_size > 256)
         throw Error(VGPU_ERR_INVALID_CONFIG,
                     "codebook_size must be at most 256 because PQ codes are stored as u8");
-    VGPU_HIP(hipStreamCreate(&stream));
-    for (auto& e : ev) VGPU_HIP(hipEventCreate(&e));
+    VGPU_HIP(hipGetDevice(&device));
+    VGPU_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
 }
 
 IvfpqIndex::~IvfpqIndex() {
+    ws_pool.clear();
     if (stream) (void)hipStreamSynchronize(stream);
-    if (h_scal) (void)hipHostFree(h_scal);
-    for (auto& e : ev)
-        if (e) (void)hipEventDestroy(e);
-    for (auto& e : sev)
-        if (e) (void)hipEventDestroy(e);
     if (stream) (void)hipStreamDestroy(stream);
 }
 
@@ -128,41 +180,41 @@ void IvfpqIndex::assign_cosine(const float* d_x, const float* d_norms, size_t nx
     if (coarse_fused_supported((int)d, 1)) {
         const size_t chunk = std::min<size_t>(nx, (size_t)1 << 18);
         const int cap = coarse_fused_cap(1);
-        w_cb16.reserve(coarse_bf16_pack_chunks((int)k, (int)d));
-        w_cand.reserve(chunk * cap);
-        w_cand_n.reserve(chunk);
-        w_cflag_list.reserve(chunk);
-        w_cflag_count.reserve(1);
-        w_overflow.reserve(1);
-        VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
-        launch_coarse_bf16_pack(d_cent, (int)k, (int)d, w_cb16.p, s);
+        b_cb16.reserve(coarse_bf16_pack_chunks((int)k, (int)d));
+        b_cand.reserve(chunk * cap);
+        b_cand_n.reserve(chunk);
+        b_cflag_list.reserve(chunk);
+        b_cflag_count.reserve(1);
+        b_overflow.reserve(1);
+        VGPU_HIP(hipMemsetAsync(b_overflow.p, 0, sizeof(unsigned int), s));
+        launch_coarse_bf16_pack(d_cent, (int)k, (int)d, b_cb16.p, s);
         for (size_t q0 = 0; q0 < nx; q0 += chunk) {
             const size_t nc = std::min(chunk, nx - q0);
-            VGPU_HIP(hipMemsetAsync(w_cflag_count.p, 0, sizeof(uint32_t), s));
-            launch_coarse_fused(d_x + q0 * d, (int)nc, (int)d, w_cb16.p, (int)k, cmax, 1, 0, nullptr,
-                                nullptr, w_cand.p, w_cand_n.p, s);
-            launch_coarse_topp(w_cand.p, w_cand_n.p, 1, d_x + q0 * d, d_cent, (int)nc, (int)k, (int)d,
-                               d_assign + q0, w_cflag_list.p, w_cflag_count.p, s);
+            VGPU_HIP(hipMemsetAsync(b_cflag_count.p, 0, sizeof(uint32_t), s));
+            launch_coarse_fused(d_x + q0 * d, (int)nc, (int)d, b_cb16.p, (int)k, cmax, 1, 0, nullptr,
+                                nullptr, b_cand.p, b_cand_n.p, s);
+            launch_coarse_topp(b_cand.p, b_cand_n.p, 1, d_x + q0 * d, d_cent, (int)nc, (int)k, (int)d,
+                               d_assign + q0, b_cflag_list.p, b_cflag_count.p, s);
             launch_coarse_exact_flagged(d_x + q0 * d, d_norms + q0, d_cent, (int)nc, (int)k, (int)d, 1,
-                                        cmax, d_assign + q0, w_overflow.p, w_cflag_list.p,
-                                        w_cflag_count.p, s);
+                                        cmax, d_assign + q0, b_overflow.p, b_cflag_list.p,
+                                        b_cflag_count.p, s);
         }
         VGPU_HIP(hipGetLastError());
         return;
     }
     size_t chunk = std::max<size_t>(1, std::min<size_t>(nx, ((size_t)1 << 28) / std::max<size_t>(k, 1)));
     chunk = std::min<size_t>(chunk, (size_t)1 << 20);  // grid.y of the GEMM stays < 65536
-    w_dots.reserve(chunk * k);
-    w_cflag_list.reserve(chunk);
-    w_cflag_count.reserve(1);
-    w_overflow.reserve(1);
-    VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
+    b_dots.reserve(chunk * k);
+    b_cflag_list.reserve(chunk);
+    b_cflag_count.reserve(1);
+    b_overflow.reserve(1);
+    VGPU_HIP(hipMemsetAsync(b_overflow.p, 0, sizeof(unsigned int), s));
     for (size_t q0 = 0; q0 < nx; q0 += chunk) {
         size_t nc = std::min(chunk, nx - q0);
-        launch_coarse_dots(d_x + q0 * d, d_cent, w_dots.p, (int)nc, (int)k, (int)d, s);
-        VGPU_HIP(hipMemsetAsync(w_cflag_count.p, 0, sizeof(uint32_t), s));
-        launch_coarse_select(w_dots.p, d_x + q0 * d, d_norms + q0, d_cent, (int)nc, (int)k, (int)d, 1,
-                             cmax, d_assign + q0, w_overflow.p, w_cflag_list.p, w_cflag_count.p, s);
+        launch_coarse_dots(d_x + q0 * d, d_cent, b_dots.p, (int)nc, (int)k, (int)d, s);
+        VGPU_HIP(hipMemsetAsync(b_cflag_count.p, 0, sizeof(uint32_t), s));
+        launch_coarse_select(b_dots.p, d_x + q0 * d, d_norms + q0, d_cent, (int)nc, (int)k, (int)d, 1,
+                             cmax, d_assign + q0, b_overflow.p, b_cflag_list.p, b_cflag_count.p, s);
     }
     VGPU_HIP(hipGetLastError());
 }
@@ -189,8 +241,6 @@ void IvfpqIndex::kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k,
     dn.upload(norms.data(), nt, stream);
     da.reserve(nt);
     std::vector<uint32_t> assign(nt), prev(nt);
-    std::vector<double> sums(ke * d);
-    std::vector<uint64_t> counts(ke);
     const bool gpu_update = d <= 256;
     dc.upload(cent.data(), ke * d, stream);
     for (size_t it = 0; it < max_iter; it++) {
@@ -200,6 +250,7 @@ void IvfpqIndex::kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k,
         assign_cosine(dx.p, dn.p, nt, dc.p, ke, cmax, da.p, stream);
         VGPU_HIP(hipMemcpyAsync(assign.data(), da.p, nt * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
         VGPU_HIP(hipStreamSynchronize(stream));
+        check_labels(assign.data(), nt, 1, ke, "k-means assignment");
         if (it > 0 && assign == prev) break;
         if (gpu_update) {
             launch_kmeans_update(dx.p, (int)nt, (int)d, (int)d, 1, da.p, false, (int)ke, nullptr, true, dc.p,
@@ -210,20 +261,7 @@ void IvfpqIndex::kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k,
             prev.swap(assign);
             continue;
         }
-        std::fill(sums.begin(), sums.end(), 0.0);
-        std::fill(counts.begin(), counts.end(), 0);
-        for (size_t i = 0; i < nt; i++) {
-            double* sc = &sums[(size_t)assign[i] * d];
-            const float* xi = &x[i * d];
-            for (size_t j = 0; j < d; j++) sc[j] += (double)xi[j];
-            counts[assign[i]]++;
-        }
-        for (size_t c = 0; c < ke; c++) {
-            if (!counts[c]) continue;
-            float* cc = &cent[c * d];
-            for (size_t j = 0; j < d; j++) cc[j] = (float)(sums[c * d + j] / (double)counts[c]);
-            normalize_row(cc, d, cc);
-        }
+        centroid_update(x.data(), nt, d, assign.data(), ke, cent.data());
         prev.swap(assign);
     }
 }
@@ -249,8 +287,6 @@ void IvfpqIndex::train_pq(const std::vector<float>& res, size_t nt, size_t Kc, u
     dcodes.reserve(nt * M);
     std::vector<uint8_t> cur(nt * M), prev(nt * M), active(M);
     std::vector<char> frozen(M, 0);
-    std::vector<double> sums(Ke * ds);
-    std::vector<uint64_t> counts(Ke);
     const bool gpu_update = ds <= 256;
     dcb.upload(codebooks.data(), codebooks.size(), stream);
     for (size_t it = 0; it < max_iter; it++) {
@@ -260,6 +296,7 @@ void IvfpqIndex::train_pq(const std::vector<float>& res, size_t nt, size_t Kc, u
         VGPU_HIP(hipGetLastError());
         VGPU_HIP(hipMemcpyAsync(cur.data(), dcodes.p, nt * M, hipMemcpyDeviceToHost, stream));
         VGPU_HIP(hipStreamSynchronize(stream));
+        check_labels(cur.data(), nt * M, 1, Ke, "PQ codes");
         bool any = false;
         for (size_t m = 0; m < M; m++) {
             active[m] = 0;
@@ -275,19 +312,8 @@ void IvfpqIndex::train_pq(const std::vector<float>& res, size_t nt, size_t Kc, u
             any = true;
             active[m] = 1;
             if (gpu_update) continue;
-            std::fill(sums.begin(), sums.end(), 0.0);
-            std::fill(counts.begin(), counts.end(), 0);
-            for (size_t i = 0; i < nt; i++) {
-                uint8_t c = cur[i * M + m];
-                const float* xi = &res[i * d + m * ds];
-                for (size_t j = 0; j < ds; j++) sums[c * ds + j] += (double)xi[j];
-                counts[c]++;
-            }
-            for (size_t c = 0; c < Ke; c++) {
-                if (!counts[c]) continue;
-                for (size_t j = 0; j < ds; j++)
-                    codebooks[(m * Ke + c) * ds + j] = (float)(sums[c * ds + j] / (double)counts[c]);
-            }
+            host_mean_update(res.data(), nt, d, m * ds, ds, cur.data() + m, M, Ke, false,
+                             &codebooks[m * Ke * ds]);
         }
         if (!any) break;
         if (gpu_update) {
@@ -357,15 +383,9 @@ void IvfpqIndex::build(size_t sample, size_t max_iter) {
     VGPU_HIP(hipMemcpyAsync(assign.data(), dassign.p, n * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
     VGPU_HIP(hipStreamSynchronize(stream));
 
-    // Lists: insertion order inside a list (search.rs:624-657).
-    offsets.assign(L + 1, 0);
-    for (size_t i = 0; i < n; i++) offsets[assign[i] + 1]++;
-    for (size_t l = 0; l < L; l++) offsets[l + 1] += offsets[l];
-    list_ids.resize(n);
-    {
-        std::vector<uint64_t> fill(offsets.begin(), offsets.end() - 1);
-        for (size_t i = 0; i < n; i++) list_ids[fill[assign[i]]++] = (uint32_t)i;
-    }
+    // Lists: insertion order inside a list (search.rs:624-657); the labels are
+    // range-checked there, before the residuals below index the centroids.
+    build_lists(assign.data(), n, L, offsets, list_ids);
 
     // Residual PQ training on the sample (search.rs:722-772).
     std::vector<float> res(nt * d);
@@ -407,6 +427,7 @@ void IvfpqIndex::build(size_t sample, size_t max_iter) {
     codes.resize(n * M);
     VGPU_HIP(hipMemcpyAsync(codes.data(), dcodes.p, n * M, hipMemcpyDeviceToHost, stream));
     VGPU_HIP(hipStreamSynchronize(stream));
+    check_labels(codes.data(), n * M, 1, K, "PQ codes");
     has_vectors = true;
     upload_index();
     built = true;
@@ -551,37 +572,84 @@ void IvfpqIndex::upload_index() {
     VGPU_HIP(hipStreamSynchronize(stream));
 }
 
-// Word offsets in the per-call scalar buffer (64-byte lines apart).
-static constexpr size_t kOverflowWord = (NUM_SCAN_COUNTERS + 1) * COUNTER_STRIDE;
-static constexpr size_t kFlagWord = kOverflowWord + 8;
-static constexpr size_t kCFlagWord = kFlagWord + 8;
-static constexpr size_t kScalWords = kCFlagWord + 8;
-
 static int fast_keep(size_t kout) {
     int kk = 1;
     while ((size_t)kk < kout + 16) kk <<= 1;
     return std::max(kk, 32);
 }
 
-void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t nprobe, size_t pool,
-                               int64_t* d_ids, float* d_dists, hipStream_t s) {
-    if (!built) throw Error(VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
-    if (!s) s = stream;
-    stats = vgpu_search_stats{};
-    stats.nq = (uint32_t)nq;
-    if (nq == 0 || k == 0) return;
+SearchWs::SearchWs() {
+    // non-blocking: no implicit wait on the null stream (default priority)
+    VGPU_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+    for (auto& e : ev) VGPU_HIP(hipEventCreate(&e));
+    VGPU_HIP(hipHostMalloc((void**)&h_scal, kScalWords * sizeof(unsigned long long)));
+}
+
+SearchWs::~SearchWs() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    if (h_scal) (void)hipHostFree(h_scal);
+    for (auto& e : ev)
+        if (e) (void)hipEventDestroy(e);
+    for (auto& e : sev)
+        if (e) (void)hipEventDestroy(e);
+    if (stream) (void)hipStreamDestroy(stream);
+}
+
+std::unique_ptr<SearchWs> IvfpqIndex::take_ws() {
+    {
+        std::lock_guard<std::mutex> lk(pool_mu);
+        if (!ws_pool.empty()) {
+            auto ws = std::move(ws_pool.back());
+            ws_pool.pop_back();
+            return ws;
+        }
+    }
+    return std::make_unique<SearchWs>();
+}
+
+void IvfpqIndex::give_ws(std::unique_ptr<SearchWs> ws) {
+    std::lock_guard<std::mutex> lk(pool_mu);
+    ws_pool.push_back(std::move(ws));
+}
+
+namespace {
+// Returns a borrowed workspace to the pool when the call ends, thrown or
+// not, after the work queued on it (on the call's stream) has finished.
+struct WsLease {
+    IvfpqIndex& ix;
+    std::unique_ptr<SearchWs> ws;
+    hipStream_t used = nullptr;  // the stream the call queued its work on
+    WsLease(IvfpqIndex& i, std::unique_ptr<SearchWs> w) : ix(i), ws(std::move(w)) {}
+    ~WsLease() {
+        if (ws) {
+            (void)hipStreamSynchronize(used ? used : ws->stream);
+            ix.give_ws(std::move(ws));
+        }
+    }
+    SearchWs* operator->() { return ws.get(); }
+};
+}  // namespace
+
+vgpu_search_stats IvfpqIndex::last_stats() {
+    std::lock_guard<std::mutex> lk(stats_mu);
+    return stats;
+}
+
+SearchPlan IvfpqIndex::plan_search(size_t nq, size_t k, size_t nprobe, size_t pool) const {
+    SearchPlan pl;
     if (pool && !has_vectors)
         throw Error(VGPU_ERR_UNSUPPORTED, "search_reranked after compact(): raw vectors were dropped");
-    size_t P = nprobe ? nprobe : params.nprobe;
-    P = std::min(P, L);
-    const size_t kout = pool ? std::max(pool, k) : k;
-    if (kout > 2048) throw Error(VGPU_ERR_INVALID_PARAMETER, "k / rerank_pool above 2048 is not supported");
-    if (P > 1024) throw Error(VGPU_ERR_INVALID_PARAMETER, "nprobe above 1024 is not supported");
-    {
+    pl.P = std::min(nprobe ? nprobe : params.nprobe, L);  // search.rs:1610
+    pl.k = k;
+    pl.pool = pool;
+    pl.kout = pool ? std::max(pool, k) : k;  // search.rs:1144
+    if (pl.kout > 2048) throw Error(VGPU_ERR_INVALID_PARAMETER, "k / rerank_pool above 2048 is not supported");
+    if (pl.P > 1024) throw Error(VGPU_ERR_INVALID_PARAMETER, "nprobe above 1024 is not supported");
+    if (pl.P) {
         ScanArgs probe_shape;
-        probe_shape.P = (int)P;
-        probe_shape.kout = (int)kout;
-        probe_shape.kk = K == 16 ? (int)kout : fast_keep(kout);
+        probe_shape.P = (int)pl.P;
+        probe_shape.kout = (int)pl.kout;
+        probe_shape.kk = K == 16 ? (int)pl.kout : fast_keep(pl.kout);
         size_t lds = K == 16 ? fastscan_lds_bytes(dix, probe_shape)
                              : std::max(scan8_fast_lds_bytes(dix, probe_shape),
                                         scan8_lds_bytes(dix, probe_shape));
@@ -589,106 +657,141 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             throw Error(VGPU_ERR_UNSUPPORTED, "scan working set of " + std::to_string(lds) +
                                                   " bytes exceeds the 160 KiB of LDS per workgroup");
     }
+    pl.opq = !rotation.empty();
+    pl.fused = coarse_fused_supported((int)d, (int)pl.P);
+    size_t chunk = std::max<size_t>(1, std::min<size_t>(nq, ((size_t)1 << 28) / std::max<size_t>(L, 1)));
+    chunk = std::min<size_t>(chunk, 65536);
+    if (pl.opq && pl.P)
+        chunk = std::max<size_t>(1, std::min<size_t>(chunk, ((size_t)1 << 28) / (pl.P * d)));
+    pl.chunk = chunk;
+    return pl;
+}
+
+size_t IvfpqIndex::ws_layout(const SearchPlan& pl, uint8_t* base, WsPtrs* out) const {
+    size_t off = 0;
+    auto carve = [&](auto*& p, size_t count) {
+        using T = std::remove_reference_t<decltype(*p)>;
+        off = (off + 255) & ~(size_t)255;
+        if (base) p = reinterpret_cast<T*>(base + off);
+        off += std::max<size_t>(count, 1) * sizeof(T);
+    };
+    WsPtrs w;
+    const size_t c = pl.chunk;
+    carve(w.scal, kScalWords);
+    carve(w.qn, c * d);
+    carve(w.qnorm, c);
+    if (pl.fused) {
+        carve(w.cand, c * (size_t)coarse_fused_cap((int)pl.P));
+        carve(w.cand_n, c);
+    } else if (pl.P) {
+        carve(w.dots, c * L);
+    }
+    carve(w.cflag_list, c);
+    carve(w.probe, c * std::max<size_t>(pl.P, 1));
+    carve(w.vidx, c * pl.kout);
+    carve(w.dist, c * pl.kout);
+    if (pl.pool) {
+        carve(w.vidx2, c * pl.k);
+        carve(w.dist2, c * pl.k);
+    }
+    carve(w.qstat, c * QSTAT_WORDS);
+    carve(w.flag_list, c);
+    if (pl.opq) carve(w.rres, c * pl.P * d);
+    if (out) *out = w;
+    return (off + 255) & ~(size_t)255;
+}
+
+// Normalise (search.rs:55-62) and probe (search.rs:1602-1617) nq <= chunk
+// queries.  The fused path normalises in its prologue; P == 0 only normalises.
+void IvfpqIndex::coarse_probe(const float* d_q, size_t nq, size_t P, const SearchPlan& pl,
+                              const WsPtrs& w, hipStream_t s, hipEvent_t mid) {
+    unsigned int* overflow = reinterpret_cast<unsigned int*>(w.scal + kOverflowWord);
+    uint32_t* cflag_count = reinterpret_cast<uint32_t*>(w.scal + kCFlagWord);
+    if (P == 0) {
+        launch_normalize(d_q, w.qn, w.qnorm, (int)nq, (int)d, s);
+        return;
+    }
+    if (pl.fused) {
+        launch_coarse_fused(d_q, (int)nq, (int)d, dix.cb16, (int)L, dix.cmax, (int)P, 1, w.qn, w.qnorm,
+                            w.cand, w.cand_n, s);
+        if (mid) VGPU_HIP(hipEventRecord(mid, s));
+        launch_coarse_topp(w.cand, w.cand_n, (int)P, w.qn, d_centroids.p, (int)nq, (int)L, (int)d, w.probe,
+                           w.cflag_list, cflag_count, s);
+        launch_coarse_exact_flagged(w.qn, w.qnorm, d_centroids.p, (int)nq, (int)L, (int)d, (int)P, dix.cmax,
+                                    w.probe, overflow, w.cflag_list, cflag_count, s);
+    } else {
+        launch_normalize(d_q, w.qn, w.qnorm, (int)nq, (int)d, s);
+        launch_coarse_dots(w.qn, d_centroids.p, w.dots, (int)nq, (int)L, (int)d, s);
+        if (mid) VGPU_HIP(hipEventRecord(mid, s));
+        launch_coarse_select(w.dots, w.qn, w.qnorm, d_centroids.p, (int)nq, (int)L, (int)d, (int)P, dix.cmax,
+                             w.probe, overflow, w.cflag_list, cflag_count, s);
+    }
+}
+
+void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, const WsPtrs& w,
+                            int64_t* d_ids, float* d_dists, hipStream_t s, SearchWs* ws,
+                            vgpu_search_stats* st) {
+    const size_t P = pl.P, k = pl.k, kout = pl.kout, chunk = pl.chunk;
+    unsigned long long* counters = w.scal;
+    uint32_t* flag_count = reinterpret_cast<uint32_t*>(w.scal + kFlagWord);
+    uint32_t* cflag_count = reinterpret_cast<uint32_t*>(w.scal + kCFlagWord);
+    launch_zero_words(w.scal, kScalWords, s);
     if (P == 0) {  // no probed list: every row is padding
         launch_finalize(nullptr, nullptr, nullptr, (int)nq, 0, (int)k, d_ids, d_dists, s);
         VGPU_HIP(hipGetLastError());
         VGPU_HIP(hipStreamSynchronize(s));
         return;
     }
-    const bool opq = !rotation.empty();
-    size_t chunk = std::max<size_t>(1, std::min<size_t>(nq, ((size_t)1 << 28) / L));
-    chunk = std::min<size_t>(chunk, 65536);
-    if (opq) chunk = std::max<size_t>(1, std::min<size_t>(chunk, ((size_t)1 << 28) / (P * d)));
-    w_qn.reserve(chunk * d);
-    w_qnorm.reserve(chunk);
-    const bool fused = coarse_fused_supported((int)d, (int)P);
-    if (fused) {
-        w_cand.reserve(chunk * coarse_fused_cap((int)P));
-        w_cand_n.reserve(chunk);
-    } else {
-        w_dots.reserve(chunk * L);
-    }
-    w_cflag_list.reserve(chunk);
-    w_probe.reserve(chunk * P);
-    w_vidx.reserve(chunk * kout);
-    w_dist.reserve(chunk * kout);
-    w_vidx2.reserve(chunk * k);
-    w_dist2.reserve(chunk * k);
-    w_qstat.reserve(chunk * QSTAT_WORDS);
-    w_flag_list.reserve(chunk);
-    // Per-call device scalars in one buffer, cleared by one memset: counter i
-    // at word i * COUNTER_STRIDE, then the overflow count and the two
-    // flag-list lengths, each on a cache line of its own.
-    w_scal.reserve(kScalWords);
-    if (!h_scal) VGPU_HIP(hipHostMalloc((void**)&h_scal, kScalWords * sizeof(unsigned long long)));
-    unsigned long long* counters = w_scal.p;
-    unsigned int* overflow = reinterpret_cast<unsigned int*>(w_scal.p + kOverflowWord);
-    uint32_t* flag_count = reinterpret_cast<uint32_t*>(w_scal.p + kFlagWord);
-    uint32_t* cflag_count = reinterpret_cast<uint32_t*>(w_scal.p + kCFlagWord);
-    VGPU_HIP(hipMemsetAsync(w_scal.p, 0, kScalWords * sizeof(unsigned long long), s));
     float t[7] = {0, 0, 0, 0, 0, 0, 0};
-    const bool allp = profiling == 1, scanp = profiling == 2;
+    const int prof = ws ? profiling : 0;
+    const bool allp = prof == 1, scanp = prof == 2;
     if (scanp) {
         const size_t need_ev = 2 * ((nq + chunk - 1) / chunk);
-        while (sev.size() < need_ev) {
+        while (ws->sev.size() < need_ev) {
             hipEvent_t e;
             VGPU_HIP(hipEventCreate(&e));
-            sev.push_back(e);
+            ws->sev.push_back(e);
         }
     }
+    hipEvent_t* ev = ws ? ws->ev : nullptr;
     size_t ci = 0;  // chunk index
     for (size_t q0 = 0; q0 < nq; q0 += chunk, ci++) {
         const size_t nc = std::min(chunk, nq - q0);
         if (allp) VGPU_HIP(hipEventRecord(ev[0], s));
-        if (fused) {
-            // normalise + two bf16x3 MFMA passes (ms_coarse), exact top-P of the
-            // candidates and the rare exact fallback (ms_select)
-            if (allp) VGPU_HIP(hipEventRecord(ev[1], s));
-            launch_coarse_fused(d_q + q0 * d, (int)nc, (int)d, dix.cb16, (int)L, dix.cmax, (int)P, 1,
-                                w_qn.p, w_qnorm.p, w_cand.p, w_cand_n.p, s);
-            if (allp) VGPU_HIP(hipEventRecord(ev[2], s));
-            launch_coarse_topp(w_cand.p, w_cand_n.p, (int)P, w_qn.p, d_centroids.p, (int)nc, (int)L, (int)d,
-                               w_probe.p, w_cflag_list.p, cflag_count, s);
-            launch_coarse_exact_flagged(w_qn.p, w_qnorm.p, d_centroids.p, (int)nc, (int)L, (int)d, (int)P,
-                                        dix.cmax, w_probe.p, overflow, w_cflag_list.p, cflag_count, s);
-        } else {
-            launch_normalize(d_q + q0 * d, w_qn.p, w_qnorm.p, (int)nc, (int)d, s);
-            if (allp) VGPU_HIP(hipEventRecord(ev[1], s));
-            launch_coarse_dots(w_qn.p, d_centroids.p, w_dots.p, (int)nc, (int)L, (int)d, s);
-            if (allp) VGPU_HIP(hipEventRecord(ev[2], s));
-            launch_coarse_select(w_dots.p, w_qn.p, w_qnorm.p, d_centroids.p, (int)nc, (int)L, (int)d,
-                                 (int)P, dix.cmax, w_probe.p, overflow, w_cflag_list.p, cflag_count, s);
-        }
+        // normalise + bf16x3 MFMA pass or score GEMM (ms_coarse), exact top-P
+        // of the candidates and the rare exact fallback (ms_select)
+        if (allp) VGPU_HIP(hipEventRecord(ev[1], s));
+        coarse_probe(d_q + q0 * d, nc, P, pl, w, s, allp ? ev[2] : nullptr);
         // OPQ: the rotated residual of every (query, probe) slot (opq.rs:120-123),
         // timed with the selection
-        const float* rres = opq ? rotate_slots(w_qn.p, nc, P, w_probe.p, s) : nullptr;
+        if (pl.opq) rotate_slots(w.qn, nc, P, w.probe, w.rres, s);
         if (allp) VGPU_HIP(hipEventRecord(ev[3], s));
         // scan-only timing: the FAST kernel's dispatch records the two events
         // itself; the other scan kernels are bracketed by marker events
-        const bool scan_fast = K != 16 && mode == VGPU_MODE_FAST && !opq;
-        if (scanp && !scan_fast) VGPU_HIP(hipEventRecord(sev[2 * ci], s));
+        const bool scan_fast = K != 16 && mode == VGPU_MODE_FAST && !pl.opq;
+        if (scanp && !scan_fast) VGPU_HIP(hipEventRecord(ws->sev[2 * ci], s));
         ScanArgs a;
-        a.qn = w_qn.p;
-        a.qnorm = w_qnorm.p;
-        a.probe = w_probe.p;
+        a.qn = w.qn;
+        a.qnorm = w.qnorm;
+        a.probe = w.probe;
         a.nq = (int)nc;
         a.P = (int)P;
         a.kout = (int)kout;
-        a.qstat = w_qstat.p;
-        a.flag_list = w_flag_list.p;
+        a.qstat = w.qstat;
+        a.flag_list = w.flag_list;
         a.flag_count = flag_count;
-        a.out_vidx = w_vidx.p;
-        a.out_dist = w_dist.p;
-        a.rres = rres;
+        a.out_vidx = w.vidx;
+        a.out_dist = w.dist;
+        a.rres = pl.opq ? w.rres : nullptr;
         if (K == 16) {
             a.kk = (int)kout;
             launch_fastscan(dix, a, s);
             if (allp) VGPU_HIP(hipEventRecord(ev[4], s));
-            if (scanp) VGPU_HIP(hipEventRecord(sev[2 * ci + 1], s));
-        } else if (mode == VGPU_MODE_FAST && !opq) {
+            if (scanp) VGPU_HIP(hipEventRecord(ws->sev[2 * ci + 1], s));
+        } else if (scan_fast) {
             a.kk = fast_keep(kout);
             a.exact = 0;
-            launch_scan8_fast(dix, a, s, scanp ? sev[2 * ci] : nullptr, scanp ? sev[2 * ci + 1] : nullptr);
+            launch_scan8_fast(dix, a, s, scanp ? ws->sev[2 * ci] : nullptr, scanp ? ws->sev[2 * ci + 1] : nullptr);
             if (allp) VGPU_HIP(hipEventRecord(ev[4], s));
             a.kk = (int)kout;
             a.exact = 1;
@@ -699,21 +802,21 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             a.exact = 1;
             launch_scan8_exact(dix, a, s);
             if (allp) VGPU_HIP(hipEventRecord(ev[4], s));
-            if (scanp) VGPU_HIP(hipEventRecord(sev[2 * ci + 1], s));
+            if (scanp) VGPU_HIP(hipEventRecord(ws->sev[2 * ci + 1], s));
         }
         if (allp) VGPU_HIP(hipEventRecord(ev[5], s));
-        const uint32_t* vout = w_vidx.p;
-        const float* dout = w_dist.p;
+        const uint32_t* vout = w.vidx;
+        const float* dout = w.dist;
         size_t kin = kout;
-        if (pool) {
-            launch_rerank(dix, w_qn.p, (int)nc, w_vidx.p, (int)kout, (int)k, w_vidx2.p, w_dist2.p, s);
-            vout = w_vidx2.p;
-            dout = w_dist2.p;
+        if (pl.pool) {
+            launch_rerank(dix, w.qn, (int)nc, w.vidx, (int)kout, (int)k, w.vidx2, w.dist2, s);
+            vout = w.vidx2;
+            dout = w.dist2;
             kin = k;
         }
         if (allp) VGPU_HIP(hipEventRecord(ev[6], s));
-        launch_finish(vout, dout, d_doc_ids.p, (int)nc, (int)kin, (int)k, d_ids + q0 * k,
-                      d_dists + q0 * k, w_qstat.p, counters, flag_count, cflag_count, s);
+        launch_finish(vout, dout, d_doc_ids.p, (int)nc, (int)kin, (int)k, d_ids + q0 * k, d_dists + q0 * k,
+                      w.qstat, counters, flag_count, cflag_count, s);
         if (allp) VGPU_HIP(hipEventRecord(ev[7], s));
         VGPU_HIP(hipGetLastError());
         if (allp) {
@@ -725,13 +828,17 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
             }
         }
     }
-    VGPU_HIP(hipMemcpyAsync(h_scal, w_scal.p, kScalWords * sizeof(unsigned long long),
-                            hipMemcpyDeviceToHost, s));
+    if (!ws) {
+        VGPU_HIP(hipStreamSynchronize(s));
+        return;
+    }
+    unsigned long long* h_scal = ws->h_scal;
+    VGPU_HIP(hipMemcpyAsync(h_scal, w.scal, kScalWords * sizeof(unsigned long long), hipMemcpyDeviceToHost, s));
     VGPU_HIP(hipStreamSynchronize(s));
     if (scanp) {  // the scan kernels of every chunk, read after the final wait
         for (size_t c = 0; c < ci; c++) {
             float ms;
-            VGPU_HIP(hipEventElapsedTime(&ms, sev[2 * c], sev[2 * c + 1]));
+            VGPU_HIP(hipEventElapsedTime(&ms, ws->sev[2 * c], ws->sev[2 * c + 1]));
             t[3] += ms;
         }
     }
@@ -739,88 +846,122 @@ void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t npr
     for (int i = 0; i < NUM_SCAN_COUNTERS; i++) cnt[i] = h_scal[i * COUNTER_STRIDE];
     const unsigned int ovf = reinterpret_cast<const unsigned int*>(h_scal + kOverflowWord)[0] +
                              (unsigned int)h_scal[NUM_SCAN_COUNTERS * COUNTER_STRIDE];
-    stats.ms_normalize = t[0];
-    stats.ms_coarse = t[1];
-    stats.ms_select = t[2];
-    stats.ms_scan = t[3];
-    stats.ms_fallback = t[4];
-    stats.ms_rerank = t[5];
-    stats.ms_total = t[0] + t[1] + t[2] + t[3] + t[4] + t[5] + t[6];
-    stats.candidates = cnt[0];
-    stats.fallback_queries = (uint32_t)cnt[1];
-    stats.fast_flushes = cnt[2];
-    stats.fast_appends = cnt[3];
-    stats.fallback_ties = (uint32_t)cnt[4];
-    stats.fast_retries = (uint32_t)cnt[5];
-    stats.coarse_overflow = ovf;
-    stats.scan_bytes = K == 16 ? cnt[0] * (uint64_t)(M / 2 + 4) : cnt[0] * (uint64_t)(M + 4);
+    st->ms_normalize = t[0];
+    st->ms_coarse = t[1];
+    st->ms_select = t[2];
+    st->ms_scan = t[3];
+    st->ms_fallback = t[4];
+    st->ms_rerank = t[5];
+    st->ms_total = t[0] + t[1] + t[2] + t[3] + t[4] + t[5] + t[6];
+    st->candidates = cnt[0];
+    st->fallback_queries = (uint32_t)cnt[1];
+    st->fast_flushes = cnt[2];
+    st->fast_appends = cnt[3];
+    st->fallback_ties = (uint32_t)cnt[4];
+    st->fast_retries = (uint32_t)cnt[5];
+    st->coarse_overflow = ovf;
+    st->scan_bytes = K == 16 ? cnt[0] * (uint64_t)(M / 2 + 4) : cnt[0] * (uint64_t)(M + 4);
+}
+
+void IvfpqIndex::search_device(const float* d_q, size_t nq, size_t k, size_t nprobe, size_t pool,
+                               int64_t* d_ids, float* d_dists, hipStream_t s) {
+    if (!built) throw Error(VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
+    vgpu_search_stats st{};
+    st.nq = (uint32_t)nq;
+    if (nq == 0 || k == 0) {
+        std::lock_guard<std::mutex> lk(stats_mu);
+        stats = st;
+        return;
+    }
+    const SearchPlan pl = plan_search(nq, k, nprobe, pool);
+    WsLease ws(*this, take_ws());
+    if (!s) s = ws->stream;
+    ws.used = s;
+    const size_t bytes = ws_layout(pl, nullptr, nullptr);
+    ws->arena.reserve(bytes);
+    WsPtrs w;
+    ws_layout(pl, ws->arena.p, &w);
+    run_search(d_q, nq, pl, w, d_ids, d_dists, s, ws.ws.get(), &st);
+    std::lock_guard<std::mutex> lk(stats_mu);
+    stats = st;
+}
+
+void IvfpqIndex::search_device_in(const float* d_q, size_t nq, size_t k, size_t nprobe, size_t pool,
+                                  int64_t* d_ids, float* d_dists, hipStream_t s, uint8_t* arena,
+                                  size_t bytes) {
+    if (!built) throw Error(VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
+    if (nq == 0 || k == 0) return;
+    SearchPlan pl = plan_search(nq, k, nprobe, pool);
+    // the largest chunk whose arena fits the caller's bytes
+    size_t lo = 0, hi = pl.chunk;
+    while (lo < hi) {
+        const size_t mid = (lo + hi + 1) / 2;
+        SearchPlan t = pl;
+        t.chunk = mid;
+        if (ws_layout(t, nullptr, nullptr) <= bytes) lo = mid;
+        else hi = mid - 1;
+    }
+    if (lo == 0) {
+        SearchPlan one = pl;
+        one.chunk = 1;
+        throw Error(VGPU_ERR_INVALID_PARAMETER,
+                    "allocation-free search needs " + std::to_string(ws_layout(one, nullptr, nullptr)) +
+                        " bytes of scratch for one query at this shape; the scratch holds " +
+                        std::to_string(bytes));
+    }
+    pl.chunk = lo;
+    WsPtrs w;
+    ws_layout(pl, arena, &w);
+    run_search(d_q, nq, pl, w, d_ids, d_dists, s ? s : stream, nullptr, nullptr);
 }
 
 void IvfpqIndex::search_host(const float* q, size_t nq, size_t k, size_t nprobe, size_t pool,
                              int64_t* ids, float* dists) {
     for (size_t i = 0; i < nq * d; i++)
         if (!std::isfinite(q[i])) throw Error(VGPU_ERR_INVALID_PARAMETER, "query contains a non-finite value");
-    if (nq == 0 || k == 0) {
-        if (!built) throw Error(VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
-        return;
-    }
-    w_q.upload(q, nq * d, stream);
-    w_ids.reserve(nq * k);
-    w_odist.reserve(nq * k);
-    search_device(w_q.p, nq, k, nprobe, pool, w_ids.p, w_odist.p, stream);
-    VGPU_HIP(hipMemcpyAsync(ids, w_ids.p, nq * k * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
-    VGPU_HIP(hipMemcpyAsync(dists, w_odist.p, nq * k * sizeof(float), hipMemcpyDeviceToHost, stream));
-    VGPU_HIP(hipStreamSynchronize(stream));
+    if (!built) throw Error(VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
+    if (nq == 0 || k == 0) return;
+    const SearchPlan pl = plan_search(nq, k, nprobe, pool);
+    WsLease ws(*this, take_ws());
+    hipStream_t s = ws->stream;
+    ws->q.upload(q, nq * d, s);
+    ws->ids.reserve(nq * k);
+    ws->odist.reserve(nq * k);
+    ws->arena.reserve(ws_layout(pl, nullptr, nullptr));
+    WsPtrs w;
+    ws_layout(pl, ws->arena.p, &w);
+    vgpu_search_stats st{};
+    st.nq = (uint32_t)nq;
+    run_search(ws->q.p, nq, pl, w, ws->ids.p, ws->odist.p, s, ws.ws.get(), &st);
+    VGPU_HIP(hipMemcpyAsync(ids, ws->ids.p, nq * k * sizeof(int64_t), hipMemcpyDeviceToHost, s));
+    VGPU_HIP(hipMemcpyAsync(dists, ws->odist.p, nq * k * sizeof(float), hipMemcpyDeviceToHost, s));
+    VGPU_HIP(hipStreamSynchronize(s));
+    std::lock_guard<std::mutex> lk(stats_mu);
+    stats = st;
 }
 
 void IvfpqIndex::probe_host(const float* q, size_t nq, size_t nprobe, uint32_t* lists) {
     if (!built) throw Error(VGPU_ERR_NOT_BUILT, "IVF-PQ index: probe before build");
-    size_t P = std::min(nprobe, L);
+    const size_t P = std::min(nprobe, L);
     if (nq == 0 || P == 0) return;
     if (P > 1024) throw Error(VGPU_ERR_INVALID_PARAMETER, "nprobe above 1024 is not supported");
-    w_q.upload(q, nq * d, stream);
-    w_qn.reserve(nq * d);
-    w_qnorm.reserve(nq);
-    w_probe.reserve(nq * P);
-    w_overflow.reserve(1);
-    VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), stream));
-    size_t chunk = std::max<size_t>(1, std::min<size_t>(nq, ((size_t)1 << 28) / L));
-    w_cflag_list.reserve(chunk);
-    w_cflag_count.reserve(1);
-    if (coarse_fused_supported((int)d, (int)P)) {
-        chunk = std::min<size_t>(nq, (size_t)1 << 20);
-        w_cflag_list.reserve(chunk);
-        w_cand.reserve(chunk * coarse_fused_cap((int)P));
-        w_cand_n.reserve(chunk);
-        for (size_t q0 = 0; q0 < nq; q0 += chunk) {
-            const size_t nc = std::min(chunk, nq - q0);
-            VGPU_HIP(hipMemsetAsync(w_cflag_count.p, 0, sizeof(uint32_t), stream));
-            launch_coarse_fused(w_q.p + q0 * d, (int)nc, (int)d, dix.cb16, (int)L, dix.cmax, (int)P, 1,
-                                w_qn.p + q0 * d, w_qnorm.p + q0, w_cand.p, w_cand_n.p, stream);
-            launch_coarse_topp(w_cand.p, w_cand_n.p, (int)P, w_qn.p + q0 * d, d_centroids.p, (int)nc, (int)L,
-                               (int)d, w_probe.p + q0 * P, w_cflag_list.p, w_cflag_count.p, stream);
-            launch_coarse_exact_flagged(w_qn.p + q0 * d, w_qnorm.p + q0, d_centroids.p, (int)nc, (int)L,
-                                        (int)d, (int)P, dix.cmax, w_probe.p + q0 * P, w_overflow.p,
-                                        w_cflag_list.p, w_cflag_count.p, stream);
-        }
-        VGPU_HIP(hipGetLastError());
-        VGPU_HIP(hipMemcpyAsync(lists, w_probe.p, nq * P * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
-        VGPU_HIP(hipStreamSynchronize(stream));
-        return;
-    }
-    w_dots.reserve(chunk * L);
-    launch_normalize(w_q.p, w_qn.p, w_qnorm.p, (int)nq, (int)d, stream);
-    for (size_t q0 = 0; q0 < nq; q0 += chunk) {
-        size_t nc = std::min(chunk, nq - q0);
-        launch_coarse_dots(w_qn.p + q0 * d, d_centroids.p, w_dots.p, (int)nc, (int)L, (int)d, stream);
-        VGPU_HIP(hipMemsetAsync(w_cflag_count.p, 0, sizeof(uint32_t), stream));
-        launch_coarse_select(w_dots.p, w_qn.p + q0 * d, w_qnorm.p + q0, d_centroids.p, (int)nc, (int)L,
-                             (int)d, (int)P, dix.cmax, w_probe.p + q0 * P, w_overflow.p,
-                             w_cflag_list.p, w_cflag_count.p, stream);
+    SearchPlan pl = plan_search(nq, 1, P, 0);
+    WsLease ws(*this, take_ws());
+    hipStream_t s = ws->stream;
+    ws->q.upload(q, nq * d, s);
+    ws->arena.reserve(ws_layout(pl, nullptr, nullptr));
+    WsPtrs w;
+    ws_layout(pl, ws->arena.p, &w);
+    launch_zero_words(w.scal, kScalWords, s);
+    uint32_t* cflag_count = reinterpret_cast<uint32_t*>(w.scal + kCFlagWord);
+    for (size_t q0 = 0; q0 < nq; q0 += pl.chunk) {
+        const size_t nc = std::min(pl.chunk, nq - q0);
+        launch_zero_words(reinterpret_cast<unsigned long long*>(cflag_count), 1, s);
+        coarse_probe(ws->q.p + q0 * d, nc, P, pl, w, s, nullptr);
+        VGPU_HIP(hipMemcpyAsync(lists + q0 * P, w.probe, nc * P * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
     }
     VGPU_HIP(hipGetLastError());
-    VGPU_HIP(hipMemcpyAsync(lists, w_probe.p, nq * P * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
-    VGPU_HIP(hipStreamSynchronize(stream));
+    VGPU_HIP(hipStreamSynchronize(s));
 }
 
 }  // namespace vgpu
@@ -866,7 +1007,8 @@ void IvfpqIndex::snapshot_list_masks() {
 // The current category of every list-major entry (what
 // MetadataStore::matches reads, filtering/mod.rs:214-218) and the per-list
 // counts the widening test needs.
-void IvfpqIndex::refresh_categories() {
+void IvfpqIndex::refresh_categories(hipStream_t s) {
+    std::lock_guard<std::mutex> lk(cat_mu);
     if (!cat_dirty) return;
     const size_t nv = n();
     std::vector<uint8_t> ec(nv, 0xff);
@@ -879,7 +1021,8 @@ void IvfpqIndex::refresh_categories() {
                 list_cat_n[l * 64 + (size_t)it->second]++;
             }
         }
-    d_ecat.upload(ec.data(), nv, stream);
+    d_ecat.upload(ec.data(), nv, s);
+    VGPU_HIP(hipStreamSynchronize(s));
     cat_dirty = false;
 }
 
@@ -907,10 +1050,33 @@ void IvfpqIndex::search_filtered(const float* q, size_t nq, size_t k, const int*
         if (scan8_lds_bytes(dix, shape) > 160 * 1024)
             throw Error(VGPU_ERR_UNSUPPORTED, "filtered scan working set exceeds the 160 KiB of LDS per workgroup");
     }
-    const size_t P = std::min((size_t)params.nprobe, L);
+    // probe with the index's nprobe (which may be 0: then every list that
+    // carries the category is a widening candidate)
+    const SearchPlan pl = plan_search(nq, 1, 0, 0);
+    const size_t P = pl.P;
+    WsLease ws(*this, take_ws());
+    hipStream_t s = ws->stream;
+    ws->q.upload(q, nq * d, s);
+    ws->arena.reserve(ws_layout(pl, nullptr, nullptr));
+    WsPtrs w;
+    ws_layout(pl, ws->arena.p, &w);
+    ws->fqn.reserve(nq * d);
     std::vector<uint32_t> probes(nq * P);
-    probe_host(q, nq, params.nprobe, probes.data());  // leaves the normalised queries in w_qn
-    refresh_categories();
+    launch_zero_words(w.scal, kScalWords, s);
+    uint32_t* cflag_count = reinterpret_cast<uint32_t*>(w.scal + kCFlagWord);
+    for (size_t q0 = 0; q0 < nq; q0 += pl.chunk) {
+        const size_t nc = std::min(pl.chunk, nq - q0);
+        launch_zero_words(reinterpret_cast<unsigned long long*>(cflag_count), 1, s);
+        coarse_probe(ws->q.p + q0 * d, nc, P, pl, w, s, nullptr);
+        VGPU_HIP(hipMemcpyAsync(ws->fqn.p + q0 * d, w.qn, nc * d * sizeof(float), hipMemcpyDeviceToDevice, s));
+        if (P)
+            VGPU_HIP(hipMemcpyAsync(probes.data() + q0 * P, w.probe, nc * P * sizeof(uint32_t),
+                                    hipMemcpyDeviceToHost, s));
+    }
+    VGPU_HIP(hipGetLastError());
+    VGPU_HIP(hipStreamSynchronize(s));
+    check_labels(probes.data(), nq * P, 1, L, "probed lists");
+    refresh_categories(s);
     std::vector<std::vector<uint32_t>> order(nq);
     std::vector<char> probed;
     size_t pmax = 1;
@@ -919,15 +1085,14 @@ void IvfpqIndex::search_filtered(const float* q, size_t nq, size_t k, const int*
         size_t found = 0;
         for (size_t p = 0; p < P; p++) {
             const uint32_t l = probes[i * P + p];
-            if (l < L && (list_mask[l] & bit)) {
+            if (list_mask[l] & bit) {
                 order[i].push_back(l);
                 found += list_cat_n[(size_t)l * 64 + (size_t)cats[i]];
             }
         }
         if (found < k && P < L) {
             probed.assign(L, 0);
-            for (size_t p = 0; p < P; p++)
-                if (probes[i * P + p] < L) probed[probes[i * P + p]] = 1;
+            for (size_t p = 0; p < P; p++) probed[probes[i * P + p]] = 1;
             for (size_t l = 0; l < L; l++)
                 if (!probed[l] && (list_mask[l] & bit)) order[i].push_back((uint32_t)l);
         }
@@ -939,38 +1104,42 @@ void IvfpqIndex::search_filtered(const float* q, size_t nq, size_t k, const int*
         std::copy(order[i].begin(), order[i].end(), slots.begin() + i * pmax);
         want[i] = (uint8_t)cats[i];
     }
-    w_probe.upload(slots.data(), nq * pmax, stream);
-    w_want.upload(want.data(), nq, stream);
-    w_vidx.reserve(nq * k);
-    w_dist.reserve(nq * k);
-    w_ids.reserve(nq * k);
-    w_odist.reserve(nq * k);
+    ws->slots.upload(slots.data(), nq * pmax, s);
+    ws->want.upload(want.data(), nq, s);
+    ws->fvidx.reserve(nq * k);
+    ws->fdist.reserve(nq * k);
+    ws->ids.reserve(nq * k);
+    ws->odist.reserve(nq * k);
     // OPQ rotates every (query, slot) residual first; queries go in chunks that
-    // bound that buffer at 2^28 floats (a widened query has up to L slots).
+    // bound that buffer at rres_limit floats (a widened query has up to L slots).
     const bool opq = !rotation.empty();
-    const size_t chunk = opq ? std::max<size_t>(1, ((size_t)1 << 28) / (pmax * d)) : nq;
+    const size_t chunk = opq ? std::max<size_t>(1, rres_limit / (pmax * d)) : nq;
+    if (opq) ws->frres.reserve(std::min(chunk, nq) * pmax * d);
     for (size_t q0 = 0; q0 < nq; q0 += chunk) {
         const size_t nc = std::min(chunk, nq - q0);
         ScanArgs a;
-        a.qn = w_qn.p + q0 * d;
-        a.qnorm = w_qnorm.p;  // not read by the filtered kernel
-        a.probe = w_probe.p + q0 * pmax;
+        a.qn = ws->fqn.p + q0 * d;
+        a.qnorm = nullptr;  // not read by the filtered kernel
+        a.probe = ws->slots.p + q0 * pmax;
         a.nq = (int)nc;
         a.P = (int)pmax;
         a.kout = (int)k;
         a.kk = (int)k;
         a.exact = 1;
-        a.out_vidx = w_vidx.p + q0 * k;
-        a.out_dist = w_dist.p + q0 * k;
-        if (opq) a.rres = rotate_slots(a.qn, nc, pmax, a.probe, stream);
-        launch_scan8_filtered(dix, a, d_ecat.p, w_want.p + q0, stream);
+        a.out_vidx = ws->fvidx.p + q0 * k;
+        a.out_dist = ws->fdist.p + q0 * k;
+        if (opq) {
+            rotate_slots(a.qn, nc, pmax, a.probe, ws->frres.p, s);
+            a.rres = ws->frres.p;
+        }
+        launch_scan8_filtered(dix, a, d_ecat.p, ws->want.p + q0, s);
     }
-    launch_finish(w_vidx.p, w_dist.p, d_doc_ids.p, (int)nq, (int)k, (int)k, w_ids.p, w_odist.p, nullptr,
-                  nullptr, nullptr, nullptr, stream);
+    launch_finish(ws->fvidx.p, ws->fdist.p, d_doc_ids.p, (int)nq, (int)k, (int)k, ws->ids.p, ws->odist.p,
+                  nullptr, nullptr, nullptr, nullptr, s);
     VGPU_HIP(hipGetLastError());
-    VGPU_HIP(hipMemcpyAsync(ids, w_ids.p, nq * k * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
-    VGPU_HIP(hipMemcpyAsync(dists, w_odist.p, nq * k * sizeof(float), hipMemcpyDeviceToHost, stream));
-    VGPU_HIP(hipStreamSynchronize(stream));
+    VGPU_HIP(hipMemcpyAsync(ids, ws->ids.p, nq * k * sizeof(int64_t), hipMemcpyDeviceToHost, s));
+    VGPU_HIP(hipMemcpyAsync(dists, ws->odist.p, nq * k * sizeof(float), hipMemcpyDeviceToHost, s));
+    VGPU_HIP(hipStreamSynchronize(s));
 }
 
 }  // namespace vgpu

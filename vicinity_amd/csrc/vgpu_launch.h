@@ -139,6 +139,8 @@ void launch_fastscan(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 // (search.rs:1148-1156), top-k by (distance, insertion index).
 void launch_rerank(const DevIndex& ix, const float* qn, int nq, const uint32_t* pool_vidx,
                    int pool, int k, uint32_t* out_vidx, float* out_dist, hipStream_t s);
+// Zero n 64-bit words on stream s (a kernel, graph-capture safe).
+void launch_zero_words(unsigned long long* p, size_t n, hipStream_t s);
 // Map insertion indices to doc ids and pad with (-1, +inf) (python.rs:778-785).
 void launch_finalize(const uint32_t* vidx, const float* dist, const uint32_t* doc_ids, int nq,
                      int kin, int k, int64_t* out_ids, float* out_dists, hipStream_t s);

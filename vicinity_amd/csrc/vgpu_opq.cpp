@@ -20,19 +20,24 @@ namespace vgpu {
 // <= 1e-12 of the largest (M rank-deficient) are completed in column order by
 // the unit vector with the largest component outside the columns so far
 // (Gram-Schmidt, two passes, lowest index on ties).  R = U V^T, rounded.
-// opq.rs:280-294 takes the same factor from nalgebra's SVD.
+// opq.rs:280-294 takes the same factor from nalgebra's SVD.  A, V and U are
+// stored transposed (column j is row j), so a column pair is two contiguous
+// rows; every sum still runs over k in ascending order.
 void polar_factor(const float* Mf, size_t d, float* R) {
-    std::vector<double> A(d * d), V(d * d, 0.0), U(d * d, 0.0), u(d), best(d), nrm(d);
+    std::vector<double> At(d * d), Vt(d * d, 0.0), Ut(d * d, 0.0), u(d), best(d), nrm(d), S(d * d, 0.0);
     std::vector<char> ok(d, 0);
-    for (size_t i = 0; i < d * d; i++) A[i] = (double)Mf[i];
-    for (size_t i = 0; i < d; i++) V[i * d + i] = 1.0;
+    for (size_t k = 0; k < d; k++)
+        for (size_t j = 0; j < d; j++) At[j * d + k] = (double)Mf[k * d + j];
+    for (size_t i = 0; i < d; i++) Vt[i * d + i] = 1.0;
     for (int sweep = 0; sweep < 64; sweep++) {
         bool changed = false;
         for (size_t p = 0; p + 1 < d; p++)
             for (size_t q = p + 1; q < d; q++) {
+                double* ap = &At[p * d];
+                double* aq = &At[q * d];
                 double a = 0.0, b = 0.0, g = 0.0;
                 for (size_t k = 0; k < d; k++) {
-                    const double x = A[k * d + p], y = A[k * d + q];
+                    const double x = ap[k], y = aq[k];
                     a += x * x;
                     b += y * y;
                     g += x * y;
@@ -41,14 +46,17 @@ void polar_factor(const float* Mf, size_t d, float* R) {
                 const double z = (b - a) / (2.0 * g);
                 const double t = (z >= 0.0 ? 1.0 : -1.0) / (std::fabs(z) + std::sqrt(1.0 + z * z));
                 const double c = 1.0 / std::sqrt(1.0 + t * t), sn = c * t;
+                double* vp = &Vt[p * d];
+                double* vq = &Vt[q * d];
                 for (size_t k = 0; k < d; k++) {
-                    double x = A[k * d + p], y = A[k * d + q];
-                    A[k * d + p] = c * x - sn * y;
-                    A[k * d + q] = sn * x + c * y;
-                    x = V[k * d + p];
-                    y = V[k * d + q];
-                    V[k * d + p] = c * x - sn * y;
-                    V[k * d + q] = sn * x + c * y;
+                    const double x = ap[k], y = aq[k];
+                    ap[k] = c * x - sn * y;
+                    aq[k] = sn * x + c * y;
+                }
+                for (size_t k = 0; k < d; k++) {
+                    const double x = vp[k], y = vq[k];
+                    vp[k] = c * x - sn * y;
+                    vq[k] = sn * x + c * y;
                 }
                 changed = true;
             }
@@ -57,14 +65,14 @@ void polar_factor(const float* Mf, size_t d, float* R) {
     double smax = 0.0;
     for (size_t j = 0; j < d; j++) {
         double s2 = 0.0;
-        for (size_t k = 0; k < d; k++) s2 += A[k * d + j] * A[k * d + j];
+        for (size_t k = 0; k < d; k++) s2 += At[j * d + k] * At[j * d + k];
         nrm[j] = std::sqrt(s2);
         if (nrm[j] > smax) smax = nrm[j];
     }
     for (size_t j = 0; j < d; j++)
         if (nrm[j] > 0.0 && nrm[j] > 1e-12 * smax) {
             ok[j] = 1;
-            for (size_t k = 0; k < d; k++) U[k * d + j] = A[k * d + j] / nrm[j];
+            for (size_t k = 0; k < d; k++) Ut[j * d + k] = At[j * d + k] / nrm[j];
         }
     for (size_t j = 0; j < d; j++) {
         if (ok[j]) continue;
@@ -74,9 +82,10 @@ void polar_factor(const float* Mf, size_t d, float* R) {
             for (int pass = 0; pass < 2; pass++)
                 for (size_t c = 0; c < d; c++) {
                     if (!ok[c]) continue;
+                    const double* uc = &Ut[c * d];
                     double pr = 0.0;
-                    for (size_t k = 0; k < d; k++) pr += U[k * d + c] * u[k];
-                    for (size_t k = 0; k < d; k++) u[k] -= pr * U[k * d + c];
+                    for (size_t k = 0; k < d; k++) pr += uc[k] * u[k];
+                    for (size_t k = 0; k < d; k++) u[k] -= pr * uc[k];
                 }
             double s2 = 0.0;
             for (size_t k = 0; k < d; k++) s2 += u[k] * u[k];
@@ -86,15 +95,20 @@ void polar_factor(const float* Mf, size_t d, float* R) {
             }
         }
         bn = std::sqrt(bn);
-        for (size_t k = 0; k < d; k++) U[k * d + j] = best[k] / bn;
+        for (size_t k = 0; k < d; k++) Ut[j * d + k] = best[k] / bn;
         ok[j] = 1;
     }
-    for (size_t i = 0; i < d; i++)
-        for (size_t j = 0; j < d; j++) {
-            double s = 0.0;
-            for (size_t k = 0; k < d; k++) s += U[i * d + k] * V[j * d + k];
-            R[i * d + j] = (float)s;
+    // R[i][j] = sum over k ascending of U[i][k] V[j][k] = Ut[k][i] Vt[k][j]
+    for (size_t k = 0; k < d; k++) {
+        const double* uk = &Ut[k * d];
+        const double* vk = &Vt[k * d];
+        for (size_t i = 0; i < d; i++) {
+            const double ui = uk[i];
+            double* si = &S[i * d];
+            for (size_t j = 0; j < d; j++) si[j] += ui * vk[j];
         }
+    }
+    for (size_t i = 0; i < d * d; i++) R[i] = (float)S[i];
 }
 
 // OptimizedProductQuantizer::fit(res, nt, 10) (opq.rs:65-109): R starts as
@@ -153,14 +167,11 @@ void IvfpqIndex::set_rotation(const float* R) {
 }
 
 // R (q_i - c_l) for every slot (i, p), l = d_lists[i * P + p] (slots >= L
-// give zero rows, never scanned), into w_rres; returns the buffer.
-const float* IvfpqIndex::rotate_slots(const float* d_qn, size_t nq, size_t P, const uint32_t* d_lists,
-                                      hipStream_t s) {
-    w_rres.reserve(nq * P * d);
-    launch_rotate_rows(d_rotation.p, d_qn, (int)P, d_centroids.p, d_lists, (int)L, nq * P, (int)d, w_rres.p,
-                       s);
+// give zero rows, never scanned), into out[nq * P * d].
+void IvfpqIndex::rotate_slots(const float* d_qn, size_t nq, size_t P, const uint32_t* d_lists, float* out,
+                              hipStream_t s) {
+    launch_rotate_rows(d_rotation.p, d_qn, (int)P, d_centroids.p, d_lists, (int)L, nq * P, (int)d, out, s);
     VGPU_HIP(hipGetLastError());
-    return w_rres.p;
 }
 
 }  // namespace vgpu

@@ -5,7 +5,9 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <memory>
 #include <mutex>
+#include <shared_mutex>
 #include <stdexcept>
 #include <string>
 #include <unordered_map>
@@ -58,12 +60,69 @@ struct DevBuf {
     }
 };
 
+// Sizes of one search call's device workspace: per query chunk, the
+// normalised queries, coarse candidates or score rows, probe lists, scan
+// results and statistics rows, plus the per-call scalars.
+struct SearchPlan {
+    size_t P = 0;      // probes per query (after min(nprobe, L))
+    size_t kout = 0;   // results the scan keeps per query (k, or the rerank pool)
+    size_t k = 0;      // results returned per query
+    size_t pool = 0;   // rerank pool (0: no rerank)
+    size_t chunk = 0;  // queries per launch sequence
+    bool fused = false, opq = false;
+};
+
+// Device pointers of one call's workspace, carved from one arena
+// (ws_layout): a pooled SearchWs arena, or the static scratch of the
+// allocation-free entry point.
+struct WsPtrs {
+    float *qn = nullptr, *qnorm = nullptr, *dots = nullptr, *dist = nullptr, *dist2 = nullptr,
+          *rres = nullptr;
+    uint32_t *cand = nullptr, *cand_n = nullptr, *cflag_list = nullptr, *probe = nullptr,
+             *vidx = nullptr, *vidx2 = nullptr, *qstat = nullptr, *flag_list = nullptr;
+    unsigned long long* scal = nullptr;  // per-call scalars (counters, flag-list lengths)
+};
+
+// Per-call device scalars: counter i at word i * COUNTER_STRIDE, then the
+// overflow count and the two flag-list lengths, each on a cache line of its own.
+constexpr size_t kOverflowWord = (NUM_SCAN_COUNTERS + 1) * COUNTER_STRIDE;
+constexpr size_t kFlagWord = kOverflowWord + 8;
+constexpr size_t kCFlagWord = kFlagWord + 8;
+constexpr size_t kScalWords = kCFlagWord + 8;
+
+// Workspace of one search call.  A handle keeps a pool of these: each call
+// borrows one for its whole duration, so concurrent searches on one handle
+// use separate buffers and, unless the caller passes a stream, separate
+// streams.  The arena grows to the largest plan seen and is reused.
+struct SearchWs {
+    hipStream_t stream = nullptr;
+    hipEvent_t ev[8] = {};
+    std::vector<hipEvent_t> sev;  // scan-only timing: two per chunk
+    DevBuf<uint8_t> arena;
+    DevBuf<float> q, odist;       // host-buffer entry points: staged queries and distances
+    DevBuf<int64_t> ids;          // host-buffer entry points: staged ids
+    DevBuf<uint32_t> slots;       // filtered search: per-query list slots
+    DevBuf<uint8_t> want;         // filtered search: per-query category
+    DevBuf<float> fqn, fdist, frres;  // filtered search: queries, distances, rotated residuals
+    DevBuf<uint32_t> fvidx;           // filtered search: insertion indices
+    unsigned long long* h_scal = nullptr;  // pinned host copy of the per-call scalars
+    SearchWs();
+    ~SearchWs();
+    SearchWs(const SearchWs&) = delete;
+    SearchWs& operator=(const SearchWs&) = delete;
+};
+
 // A built IVF-PQ index.  Mirrors the state of IVFPQIndex
 // (src/ivf_pq/search.rs:212-239): the raw normalised vectors and doc ids on
 // the host, the search arrays resident in HBM.
+//
+// Locking: searches, probes and reads take `mu` shared (the reference's
+// search takes &self, so concurrent searches are legal); add, build, load
+// and setters take it exclusively (the reference's &mut self methods).
 struct IvfpqIndex {
     size_t d = 0;
     vgpu_ivfpq_params params{};
+    int device = 0;  // the HIP device current at construction
     int mode = VGPU_MODE_FAST;
     bool built = false;
     bool has_vectors = true;
@@ -81,38 +140,37 @@ struct IvfpqIndex {
     std::vector<float> rotation;    // [d*d] OPQ rotation R, row-major (opq.rs:37-38);
                                     // empty: Quantizer::Product
 
-    hipStream_t stream = nullptr;
-    hipEvent_t ev[8] = {};
-    std::vector<hipEvent_t> sev;  // scan-only timing: two per chunk
+    hipStream_t stream = nullptr;   // build, upload and the allocation-free search
     DevBuf<float> d_centroids, d_codebooks, d_bias, d_vectors, d_rotation;
-    DevBuf<uint4> d_cb16, w_cb16;  // bf16 hi/lo centroid copies (search index, build workspace)
-    DevBuf<uint32_t> w_cand, w_cand_n;  // fused coarse candidates
+    DevBuf<uint4> d_cb16;           // bf16 hi/lo centroid copy of the search index
     DevBuf<uint32_t> d_offsets, d_list_ids, d_doc_ids, d_pack_off;
     DevBuf<uint8_t> d_codes, d_packed, d_tblocks;
     DevBuf<uint32_t> d_tblk_off;
     DevIndex dix;
 
-    // search workspace
-    DevBuf<float> w_q, w_qn, w_qnorm, w_dots, w_dist, w_dist2, w_odist;
-    DevBuf<float> w_rres;  // OPQ: rotated residual of each (query, slot)
-    DevBuf<uint32_t> w_probe, w_vidx, w_vidx2, w_qstat, w_flag_list;
-    DevBuf<uint32_t> w_cflag_list, w_cflag_count;  // coarse selection fallback list
-    DevBuf<int64_t> w_ids;
-    DevBuf<unsigned long long> w_scal;           // per-call device scalars (see search_device)
-    unsigned long long* h_scal = nullptr;        // pinned host copy of w_scal
-    DevBuf<unsigned int> w_overflow;
+    // build workspace (k-means assignment), used under the exclusive lock
+    DevBuf<uint4> b_cb16;
+    DevBuf<float> b_dots;
+    DevBuf<uint32_t> b_cand, b_cand_n, b_cflag_list, b_cflag_count;
+    DevBuf<unsigned int> b_overflow;
+
+    std::shared_mutex mu;
+    std::mutex pool_mu;                              // the free workspaces
+    std::vector<std::unique_ptr<SearchWs>> ws_pool;
+    std::mutex stats_mu;                             // stats of the last finished search
     vgpu_search_stats stats{};
-    std::mutex mu;
 
     // search_with_filter state (search.rs:236-238): the category each document
     // carries in the filter field, per-list bitmasks taken when the lists are
-    // built (search.rs:626-648), and device copies refreshed on demand.
+    // built (search.rs:626-648), and device copies refreshed on demand (under
+    // cat_mu, by the first filtered search after a change).
     bool filtering = false;
     std::unordered_map<uint32_t, int> doc_cat;  // doc id -> 0..63, or -1 (metadata without the field)
     std::vector<uint64_t> list_mask;            // [L]
     std::vector<uint32_t> list_cat_n;           // [L*64] entries per (list, category), current metadata
     bool cat_dirty = true;
-    DevBuf<uint8_t> d_ecat, w_want;  // category of each list-major entry (0xff: none); per query
+    std::mutex cat_mu;
+    DevBuf<uint8_t> d_ecat;  // category of each list-major entry (0xff: none)
 
     IvfpqIndex(size_t dim, const vgpu_ivfpq_params& p);
     ~IvfpqIndex();
@@ -126,9 +184,19 @@ struct IvfpqIndex {
     void upload_index();
     // The rotation of an OPQ index built elsewhere (before load); null clears it.
     void set_rotation(const float* R);
-    // Device-pointer batch search on stream s (s may be null = own stream).
+    // The probe count, plan and shape checks of a search of nq queries.
+    SearchPlan plan_search(size_t nq, size_t k, size_t nprobe, size_t pool) const;
+    // Bytes of a plan's workspace arena; with a base, also the pointers into it.
+    size_t ws_layout(const SearchPlan& pl, uint8_t* base, WsPtrs* out) const;
+    // Device-pointer batch search on stream s (null: the borrowed workspace's
+    // stream); waits for completion.
     void search_device(const float* d_q, size_t nq, size_t k, size_t nprobe, size_t pool,
                        int64_t* d_ids, float* d_dists, hipStream_t s);
+    // The same over a caller-provided arena of `bytes` bytes (no allocation,
+    // no statistics): queries go in chunks that fit it.
+    void search_device_in(const float* d_q, size_t nq, size_t k, size_t nprobe, size_t pool,
+                          int64_t* d_ids, float* d_dists, hipStream_t s, uint8_t* arena,
+                          size_t bytes);
     void search_host(const float* q, size_t nq, size_t k, size_t nprobe, size_t pool,
                      int64_t* ids, float* dists);
     void probe_host(const float* q, size_t nq, size_t nprobe, uint32_t* lists);
@@ -138,8 +206,26 @@ struct IvfpqIndex {
     // rows padded with (-1, +inf) like search_host.
     void search_filtered(const float* q, size_t nq, size_t k, const int* cats, int64_t* ids,
                          float* dists);
+    vgpu_search_stats last_stats();
+
+    // Borrow a workspace from the pool (a new one when all are in use).
+    std::unique_ptr<SearchWs> take_ws();
+    void give_ws(std::unique_ptr<SearchWs> ws);
+    // Filtered search under OPQ rotates at most this many floats of residuals
+    // per pass (queries go in chunks); settable for tests.
+    size_t rres_limit = (size_t)1 << 28;
 
   private:
+    // Every chunk of one search: coarse, select, scan, rerank and finish.
+    // ws (may be null) supplies the profiling events and the pinned scalar
+    // copy; *st receives the statistics when ws is given.
+    void run_search(const float* d_q, size_t nq, const SearchPlan& pl, const WsPtrs& w,
+                    int64_t* d_ids, float* d_dists, hipStream_t s, SearchWs* ws,
+                    vgpu_search_stats* st);
+    // Normalise and probe nq queries into w.qn / w.qnorm / w.probe (P may be 0).
+    // mid (may be null) is recorded between the scoring and the selection.
+    void coarse_probe(const float* d_q, size_t nq, size_t P, const SearchPlan& pl, const WsPtrs& w,
+                      hipStream_t s, hipEvent_t mid);
     void kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k, uint64_t seed,
                        size_t max_iter, std::vector<float>& cent);
     void assign_cosine(const float* d_x, const float* d_norms, size_t nx, const float* d_cent,
@@ -147,11 +233,11 @@ struct IvfpqIndex {
     void train_pq(const std::vector<float>& res, size_t nt, size_t Kc, uint64_t seed,
                   size_t max_iter);
     void train_opq(const std::vector<float>& res, size_t nt, uint64_t seed);
-    // rotated residuals R (q_i - c_l) of nq queries x P slots into w_rres
-    const float* rotate_slots(const float* d_qn, size_t nq, size_t P, const uint32_t* d_lists,
-                              hipStream_t s);
+    // rotated residuals R (q_i - c_l) of nq queries x P slots into out[nq * P * d]
+    void rotate_slots(const float* d_qn, size_t nq, size_t P, const uint32_t* d_lists, float* out,
+                      hipStream_t s);
     void snapshot_list_masks();
-    void refresh_categories();
+    void refresh_categories(hipStream_t s);
 };
 
 struct FlatIndex {
@@ -182,6 +268,14 @@ struct FlatIndex {
 void sample_indices(size_t n, size_t sample, uint64_t seed, std::vector<uint32_t>& out);
 void draw_distinct(size_t n, size_t count, uint64_t seed, std::vector<uint32_t>& out);
 void normalize_row(const float* x, size_t d, float* out);
+// Inverted lists from per-row list labels (insertion order inside a list);
+// a label >= L raises VGPU_ERR_DEVICE.
+void build_lists(const uint32_t* assign, size_t n, size_t L, std::vector<uint64_t>& offsets,
+                 std::vector<uint32_t>& list_ids);
+// Host cosine k-means update (float64 member means in row order, cast,
+// re-normalised; empty keys keep their row) of cent[k * d]; a label >= k
+// raises VGPU_ERR_DEVICE.
+void centroid_update(const float* x, size_t n, size_t d, const uint32_t* assign, size_t k, float* cent);
 // The orthogonal polar factor U V^T of M = U S V^T (d x d, row-major), in
 // float64 by one-sided Jacobi, rounded to float32.
 void polar_factor(const float* M, size_t d, float* R);

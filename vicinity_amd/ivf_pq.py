@@ -278,6 +278,34 @@ class IVFPQIndex:
                                                       ctypes.byref(m)))
         return ids[:m.value].astype(np.int64), dists[:m.value].copy()
 
+    def batch_search_with_filter(self, queries, k: int, filters):
+        """search_with_filter for a batch: ``filters`` is one MetadataFilter
+        for every query or one per query.  Returns (ids int64[nq, k], dists
+        float32[nq, k]) padded with (MISSING_LABEL, MISSING_DISTANCE); row i
+        equals search_with_filter(queries[i], k, filter_i)."""
+        if not self.is_built:
+            raise ValueError("IVF-PQ index: search before build")
+        q = np.asarray(queries)
+        if q.ndim != 2:
+            raise ValueError("queries must be a 2-D array")
+        if q.shape[1] != self._dim:
+            raise ValueError(f"queries dimension mismatch: index expects {self._dim}, "
+                             f"got {q.shape[1]}")
+        q = _f32_2d(q, "queries")
+        nq = q.shape[0]
+        if isinstance(filters, MetadataFilter):
+            filters = [filters] * nq
+        if len(filters) != nq:
+            raise ValueError(f"{len(filters)} filters for {nq} queries")
+        cats = np.array([filter_category(f, self._filter_field) for f in filters], np.int64)
+        ids = np.full((nq, k), MISSING_LABEL, np.int64)
+        dists = np.full((nq, k), MISSING_DISTANCE, np.float32)
+        _lib.check(self._L.vgpu_ivfpq_search_filtered_batch(
+            self._h, _lib.ptr(q) if nq else None, nq, self._dim, k,
+            _lib.ptr(cats) if nq else None, _lib.ptr(ids) if ids.size else None,
+            _lib.ptr(dists) if dists.size else None))
+        return ids, dists
+
     # ---- search -----------------------------------------------------------
     def search(self, query, k: int, nprobe: int | None = None, rerank_pool: int | None = None):
         """python.rs:709-738: (ids int64[m], dists float32[m]), m <= k."""
