@@ -138,6 +138,21 @@ int vgpu_ivfpq_search_batch(vgpu_ivfpq *h, const float *queries, size_t nq, size
 int vgpu_ivfpq_search_batch_device(vgpu_ivfpq *h, const float *d_queries, size_t nq,
                                    size_t dim, size_t k, size_t nprobe, size_t rerank_pool,
                                    int64_t *d_out_ids, float *d_out_dists, void *stream);
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  vgpu_ivfpq_search_batch_device without any device or
+ * pinned-host allocation: the workspace is a 64 MiB device array inside the library (one
+ * per GPU, held until the process ends), and a batch goes in query chunks
+ * that fit it; a shape whose single query does not fit (about 2.5 KB per
+ * query at d 128, nprobe 32, k 100) is VGPU_ERR_INVALID_PARAMETER.  Every
+ * call on one GPU shares that array, whatever the handle: calls that overlap
+ * on one GPU race.  The index's device must be current.  stream NULL = the
+ * handle's own stream; returns after the search completes; does not update
+ * vgpu_ivfpq_last_stats or the profiling timers. */
+int vgpu_ivfpq_search_batch_device_noalloc(vgpu_ivfpq *h, const float *d_queries, size_t nq,
+                                           size_t dim, size_t k, size_t nprobe,
+                                           size_t rerank_pool, int64_t *d_out_ids,
+                                           float *d_out_dists, void *stream);
 int vgpu_ivfpq_last_stats(const vgpu_ivfpq *h, vgpu_search_stats *out);
 /* hipEvent timing of later search calls, read back by vgpu_ivfpq_last_stats:
  * 0 off (default); 1 every phase (events around each stage, one host wait per

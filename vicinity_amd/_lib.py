@@ -88,6 +88,8 @@ SIGNATURES = {
     "vgpu_ivfpq_search_reranked": (_i, [_H, _vp, _sz, _sz, _sz, _vp, _vp, ctypes.POINTER(_sz)]),
     "vgpu_ivfpq_search_batch": (_i, [_H, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp]),
     "vgpu_ivfpq_search_batch_device": (_i, [_H, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _vp]),
+    "vgpu_ivfpq_search_batch_device_noalloc": (_i, [_H, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp,
+                                                    _vp]),
     "vgpu_ivfpq_last_stats": (_i, [_H, ctypes.POINTER(Stats)]),
     "vgpu_ivfpq_set_profiling": (_i, [_H, _i]),
     "vgpu_ivfpq_enable_filtering": (_i, [_H]),

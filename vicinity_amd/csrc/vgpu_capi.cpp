@@ -222,6 +222,22 @@ int vgpu_ivfpq_search_batch_device(vgpu_ivfpq* h, const float* d_queries, size_t
     });
 }
 
+int vgpu_ivfpq_search_batch_device_noalloc(vgpu_ivfpq* h, const float* d_queries, size_t nq, size_t dim,
+                                           size_t k, size_t nprobe, size_t rerank_pool, int64_t* d_out_ids,
+                                           float* d_out_dists, void* stream) {
+    return guard([&] {
+        need(h && (nq == 0 || k == 0 || (d_queries && d_out_ids && d_out_dists)),
+             VGPU_ERR_INVALID_PARAMETER, "null argument");
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
+        need(h->ix->built, VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
+        check_dim(*h->ix, dim);
+        if (nq == 0 || k == 0) return;
+        uint8_t* scratch = vgpu::noalloc_scratch(h->ix->device);
+        h->ix->search_device_in(d_queries, nq, k, nprobe, rerank_pool, d_out_ids, d_out_dists,
+                                (hipStream_t)stream, scratch, NOALLOC_SCRATCH_BYTES);
+    });
+}
+
 // One query through the batch path; the result is truncated at the first
 // padding entry (the reference returns fewer than k pairs in that case).
 static int search_one(vgpu_ivfpq* h, const float* query, size_t dim, size_t k, size_t pool,

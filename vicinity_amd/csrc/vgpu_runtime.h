@@ -263,6 +263,12 @@ struct FlatIndex {
                        hipStream_t s);
 };
 
+// Bytes of the allocation-free search's device scratch (one array per GPU).
+#define NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+// The scratch array's device address on `device`, which must be current;
+// looked up once per device (hipGetSymbolAddress) and kept.
+uint8_t* noalloc_scratch(int device);
+
 // Host-side seeded sampling shared with the build (splitmix64 partial
 // Fisher-Yates, ascending sample).
 void sample_indices(size_t n, size_t sample, uint64_t seed, std::vector<uint32_t>& out);
