@@ -36,6 +36,7 @@ sys.path.insert(0, ROOT)
 METRIC = "IVF-PQ QPS @ fixed nprobe, 1M×d128 batch 10k; ADC-scan HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
+BF16_PEAK_TFLOPS = 2500.0
 
 
 def log(msg):
@@ -308,7 +309,9 @@ def run_flat(args, w):
     qps = nq * args.steps / dt
     gemm_ms = float(np.mean(gemm))
     tflops = 2.0 * n * d * nq / (gemm_ms * 1e-3) / 1e12
-    log(f"{qps:.0f} QPS, {ms_step:.3f} ms/batch, ranking {gemm_ms:.3f} ms = {tflops:.1f} TFLOP/s")
+    fallbacks = fx.last_fallbacks()
+    log(f"{qps:.0f} QPS, {ms_step:.3f} ms/batch, ranking {gemm_ms:.3f} ms = {tflops:.1f} TFLOP/s, "
+        f"{fallbacks} exhaustive fallbacks")
     gpu_ids = out_ids.cpu().numpy()
     gpu_d = out_d.cpu().numpy()
     cpu = parity = None
@@ -335,11 +338,21 @@ def run_flat(args, w):
     config = {"workload": w.name, "n": n, "d": d, "k": k, "batch": nq, "metric": "l2"}
     line = base_line(args, f"flat exact top-{k} QPS, {w.name} batch {nq // 1000}k; ranking GEMM "
                            "TFLOP/s vs fp32 MFMA peak", qps, "queries/s", ms_step, "f32", config)
+    rank_bf16 = d <= 128 and k <= 32
     line.update({
+        # achieved: the fp32 product work 2 n d per query over the ranking
+        # kernel's time, against the fp32 MFMA peak; the kernel computes it as
+        # three bf16 MFMA products (bf16x3), whose own rate is mfma_bf16_frac of
+        # the bf16 dense peak
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
-                     "traffic": None, "kernel": "flat_partial_kernel", "kernel_ms": round(gemm_ms, 4),
+                     "traffic": None,
+                     "kernel": f"flat_rank_kernel<{(d + 31) // 32}>" if rank_bf16 else "flat_partial_kernel",
+                     "kernel_ms": round(gemm_ms, 4),
+                     "mfma_dtype": "bf16x3" if rank_bf16 else "f32",
+                     "mfma_bf16_frac": round(3 * tflops / BF16_PEAK_TFLOPS, 4) if rank_bf16 else None,
                      "algorithmic_flops_per_launch": int(2 * n * d * nq)},
+        "exhaustive_fallbacks": fallbacks,
         "cpu_baseline": cpu,
         "parity": parity,
     })

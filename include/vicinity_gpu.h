@@ -227,7 +227,14 @@ int vgpu_flat_search_batch(vgpu_flat *h, const float *queries, size_t nq, size_t
                            int64_t *out_ids, float *out_dists);
 int vgpu_flat_search_batch_device(vgpu_flat *h, const float *d_queries, size_t nq, size_t dim,
                                   size_t k, int64_t *d_out_ids, float *d_out_dists, void *stream);
+/* Device time of the last search: ms_gemm the ranking kernel (bf16x3 MFMA
+ * for d <= 128 and k <= 32, fp32 MFMA otherwise), ms_total ranking through
+ * merge, exact rescoring, fallback and output. */
 int vgpu_flat_last_ms(const vgpu_flat *h, float *ms_gemm, float *ms_total);
+/* Queries of the last flat search whose kept candidates could not be proved
+ * to hold the exact top-k, and which were answered by an exhaustive exact
+ * scan instead (their results are exact either way). */
+int vgpu_flat_last_fallbacks(const vgpu_flat *h, uint32_t *queries);
 
 /* ---- per-kernel test entry points (host buffers) -------------------------- */
 /* Host steps of the build, no device needed.  Inverted lists from list

@@ -109,6 +109,7 @@ SIGNATURES = {
     "vgpu_flat_search_batch": (_i, [_H, _vp, _sz, _sz, _sz, _vp, _vp]),
     "vgpu_flat_search_batch_device": (_i, [_H, _vp, _sz, _sz, _sz, _vp, _vp, _vp]),
     "vgpu_flat_last_ms": (_i, [_H, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]),
+    "vgpu_flat_last_fallbacks": (_i, [_H, ctypes.POINTER(ctypes.c_uint32)]),
     "vgpu_test_host_lists": (_i, [_vp, _sz, _sz, _vp, _vp]),
     "vgpu_test_host_centroid_update": (_i, [_vp, _sz, _sz, _vp, _sz, _vp]),
     "vgpu_test_polar_factor": (_i, [_vp, _sz, _vp]),

@@ -7,20 +7,29 @@
 // src/distance.rs:104-109 (1 - dot); brute-force ground truth
 // src/ivf_pq/search.rs:3376-3392.
 //
-// Ranking distance (metric 0): ||x||^2 - 2 q.x (||q||^2 is constant per query).
-// Each block takes 64 queries and one slice of the database; every database
-// tile of 64 vectors is one 64x64 MFMA tile whose scores are filtered against
-// the per-query threshold into per-query LDS buffers; a full buffer is sorted
-// by one wave and cut to the kept count.  The merge kernel gathers the slices,
+// Ranking distance (metric 0): ||x||^2 - 2 q.x (||q||^2 is constant per query);
+// metric 1: 1 - q.x.  A ranking kernel keeps, for every (query, database
+// slice), the kk smallest ranking keys; the merge kernel gathers the slices,
 // checks that the kept set provably contains the exact top-k (gap > 2 tau)
 // and rescores it; a query that fails the check is searched exhaustively with
 // the exact arithmetic.
+//
+// flat_rank_kernel (d <= 128): bf16x3 MFMA products (q.x ~ qh.xh + qh.xl +
+// ql.xh, as the coarse quantiser), 128 queries per workgroup held in
+// registers, the slice's vectors streamed through LDS two 16-vector tiles at
+// a time (pre-split into bf16 hi/lo, tile-major).  Each score is compared
+// with its row's threshold in registers; the rare ones below it are appended
+// to the row's LDS buffer, which the row's 16 lanes cut back to the kk
+// smallest by a bitonic sort when it fills.  flat_partial_kernel (any d) is
+// the fp32 MFMA path with per-row LDS thresholds.
 #include "vgpu_device.h"
 #include "vgpu_launch.h"
 
 namespace vgpu {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 #define FL_Q 64
 #define FL_N 64
@@ -170,7 +179,272 @@ __global__ __launch_bounds__(256) void flat_partial_kernel(
     }
 }
 
-#define FL_BUF 1024
+
+// ---- bf16x3 ranking kernel (d <= 128) ------------------------------------
+
+#define FR_TPS 2    // database tiles (16 vectors each) per pipeline stage
+#define FR_QBW 2    // query blocks (16 queries each) per wave
+#define FR_ROWS (4 * FR_QBW * 16)  // queries per workgroup
+#define FR_J 4      // keys each lane keeps per row (and sorts per lane at the end)
+#define FR_BIG 3.0e38f
+
+// Round to nearest even bfloat16 bits (finite inputs); x = hi + lo + r with
+// |r| <= 2^-18 |x|.
+__device__ __forceinline__ uint32_t fr_bf16_bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Bound on |ranking key + ||q||^2 (metric 0) - exact distance| with the
+// exact distance l2_distance_squared / 1 - seq_dot in float32
+// (u = 2^-24, |q| <= qn, |x| <= xn): the bf16x3 product is within
+// (3.01 2^-18 + 7 d u) |q||x| of q.x, ||x||^2 within d u ||x||^2, one rounding
+// of the score, the reference's sum within (d + 1) u (|q| + |x|)^2 (or
+// d u |q||x| + 2u (1 + |q||x|) for 1 - dot), taken twice; plus the packing:
+// a key is the score with its low ib mantissa bits replaced by a tile index,
+// within 2^ib ulps of |score| <= ||x||^2 + 2 |q||x| (or 1 + |q||x|).
+__host__ __device__ inline float flat_bf16_tau(int d, int metric, float qn, float xn, int ib) {
+    const float u = 5.9604645e-08f;
+    const float qx = qn * xn;
+    const float dot = (3.01f * 3.8146973e-06f + 7.0f * (float)d * u) * qx;
+    const float smax = metric == 1 ? 1.0f + qx : xn * xn + 2.0f * qx;
+    const float pack = ((float)(1u << ib) + 1.0f) * 2.0f * u * smax;
+    if (metric == 1) return 2.0f * (dot + (float)d * u * qx + 2.0f * u * (1.0f + qx)) + pack + 1e-30f;
+    const float s = qn + xn;
+    return 2.0f * (2.0f * dot + (float)d * u * xn * xn + u * (xn * xn + 2.0f * qx) +
+                   (float)(d + 1) * u * s * s) + pack + 1e-30f;
+}
+
+// Ascending list of the FR_J smallest keys: t_i' = med3(t_{i-1}, t_i, v) from
+// the bottom, t_0' = min(t_0, v).
+__device__ __forceinline__ void fr_insert(float (&t)[FR_J], float v) {
+#pragma unroll
+    for (int i = FR_J - 1; i > 0; i--) t[i] = __builtin_amdgcn_fmed3f(t[i - 1], t[i], v);
+    t[0] = fminf(t[0], v);
+}
+
+// Ascending bitonic sort of the 16 FR_J keys of a lane group (element
+// e * 16 + lane % 16 in k[e]).
+__device__ __forceinline__ void fr_group_sort(uint64_t (&k)[FR_J]) {
+    const int c = threadIdx.x & 15;
+#pragma unroll
+    for (int size = 2; size <= 16 * FR_J; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride >= 16) {
+                const int es = stride >> 4;
+#pragma unroll
+                for (int e = 0; e < FR_J; e++) {
+                    const int f = e ^ es;
+                    if (f > e) {
+                        const bool asc = (((e << 4) | c) & size) == 0;
+                        const uint64_t a = k[e], b = k[f];
+                        const bool sw = (a > b) == asc;
+                        k[e] = sw ? b : a;
+                        k[f] = sw ? a : b;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < FR_J; e++) {
+                    const uint64_t o = shfl_xor_u64(k[e], stride);
+                    const bool asc = (((e << 4) | c) & size) == 0;
+                    const bool lower = (c & stride) == 0;
+                    k[e] = (lower == asc) ? (o < k[e] ? o : k[e]) : (o > k[e] ? o : k[e]);
+                }
+            }
+        }
+    }
+}
+
+// Workgroup (4 waves) = FR_ROWS queries x one database slice of tiles
+// [blockIdx.y * tps, ..) (tps <= 2^ib).  Wave w holds query blocks
+// FR_QBW w .. + FR_QBW - 1 (bf16 hi/lo A operands in registers); every stage
+// of FR_TPS tiles is copied to LDS once and multiplied by all of them.  The
+// lane of group g (lanes 16 g .. + 15) and column c scores rows 4 g .. + 3 of
+// each of its query blocks against vector 16 tile + c and keeps, per row, the
+// FR_J smallest keys (score with the low ib mantissa bits replaced by the
+// tile's index in the slice).  At the end each row's 16 lanes sort their
+// 16 FR_J keys as (fkey, vector index); the slice writes the kk smallest and
+// a bound every key it dropped is at or above: the kk-th kept key and the
+// FR_J-th key of every full lane list.
+template <int DT>
+__global__ __launch_bounds__(256) void flat_rank_kernel(
+    const float* __restrict__ Q, int nq, int d, const uint4* __restrict__ Xb_in,
+    const float* __restrict__ Xnorm, int n, int metric, int kk, int tps, int ib, int splits,
+    uint64_t* __restrict__ partial, uint32_t* __restrict__ pbound) {
+    extern __shared__ __align__(16) char smem[];
+    constexpr int TC = 2 * DT * 64;  // 16-byte chunks per tile (hi, then lo)
+    constexpr int SC = FR_TPS * TC;  // chunks per stage
+    constexpr int PER = SC / VGPU_BLOCK;
+    static_assert(SC % VGPU_BLOCK == 0, "stage split");
+    u32x4* stage = reinterpret_cast<u32x4*>(smem);                // [2][SC]
+    float* snorm = reinterpret_cast<float*>(smem + 2 * SC * 16);  // [2][FR_TPS * 16]
+    const u32x4* Xb = reinterpret_cast<const u32x4*>(Xb_in);
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q0 = blockIdx.x * FR_ROWS, sl = blockIdx.y;
+    const int ntiles = (n + 15) / 16;
+    const int tile0 = sl * tps, tile1 = min(ntiles, tile0 + tps);
+    const int nst = tile1 > tile0 ? (tile1 - tile0 + FR_TPS - 1) / FR_TPS : 0;
+    const uint32_t kmask = ~((1u << ib) - 1u);
+
+    // A operands: row (FR_QBW wave + qb) * 16 + c of the block, dimensions
+    // 32 t + 8 g .. + 7 (zero past d; rows past nq repeat the last query and
+    // are never written).
+    u32x4 ah[FR_QBW][DT], al[FR_QBW][DT];
+#pragma unroll
+    for (int qb = 0; qb < FR_QBW; qb++) {
+        const int row = min(q0 + (FR_QBW * wave + qb) * 16 + c, nq - 1);
+        const float* qr = Q + (size_t)row * d;
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+            uint32_t hb[8], lb[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int j = 32 * t + 8 * g + i;
+                const float x = j < d ? qr[j] : 0.0f;
+                hb[i] = fr_bf16_bits(x);
+                lb[i] = fr_bf16_bits(x - __uint_as_float(hb[i] << 16));
+            }
+            ah[qb][t] = u32x4{hb[0] | hb[1] << 16, hb[2] | hb[3] << 16, hb[4] | hb[5] << 16, hb[6] | hb[7] << 16};
+            al[qb][t] = u32x4{lb[0] | lb[1] << 16, lb[2] | lb[3] << 16, lb[4] | lb[5] << 16, lb[6] | lb[7] << 16};
+        }
+    }
+    float lst[FR_QBW][4][FR_J];
+#pragma unroll
+    for (int qb = 0; qb < FR_QBW; qb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int j = 0; j < FR_J; j++) lst[qb][r][j] = FR_BIG;
+
+    // Stage st: tiles tile0 + FR_TPS st .. + FR_TPS - 1 (chunks contiguous in
+    // the packed copy, which is padded to whole groups of four tiles).
+    u32x4 pre[PER];
+    float pn = 0.0f;
+    auto fetch = [&](int st) {
+        const size_t base = (size_t)(tile0 + FR_TPS * st) * TC;
+#pragma unroll
+        for (int i = 0; i < PER; i++) pre[i] = Xb[base + (size_t)i * VGPU_BLOCK + tid];
+        const int v = (tile0 + FR_TPS * st) * 16 + tid;
+        pn = tid < FR_TPS * 16 && v < n ? Xnorm[v] : 0.0f;
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < PER; i++) stage[(size_t)buf * SC + i * VGPU_BLOCK + tid] = pre[i];
+        if (tid < FR_TPS * 16) snorm[buf * FR_TPS * 16 + tid] = pn;
+    };
+    // Scores of stage st into the lane's lists.
+    auto epilogue = [&](const floatx4 (&acc)[FR_TPS][FR_QBW], const float (&xn)[FR_TPS], int st) {
+#pragma unroll
+        for (int i = 0; i < FR_TPS; i++) {
+            const int ti = FR_TPS * st + i;  // tile index in the slice, < 2^ib
+            const bool colok = tile0 + ti < tile1 && (tile0 + ti) * 16 + c < n;
+#pragma unroll
+            for (int qb = 0; qb < FR_QBW; qb++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float v = metric == 0 ? xn[i] - 2.0f * acc[i][qb][r] : 1.0f - acc[i][qb][r];
+                    const float key = __uint_as_float((__float_as_uint(v) & kmask) | (uint32_t)ti);
+                    fr_insert(lst[qb][r], colok ? key : FR_BIG);
+                }
+        }
+    };
+
+    floatx4 prev[FR_TPS][FR_QBW];
+    float prevn[FR_TPS];
+    if (nst > 0) {
+        fetch(0);
+        store(0);
+        if (nst > 1) fetch(1);
+    }
+    for (int st = 0; st < nst; st++) {
+        __syncthreads();  // stage st visible; buffer (st + 1) & 1 no longer read
+        if (st + 1 < nst) {
+            store((st + 1) & 1);
+            if (st + 2 < nst) fetch(st + 2);
+        }
+        const u32x4* b = stage + (size_t)(st & 1) * SC;
+        floatx4 acc[FR_TPS][FR_QBW];
+        float xn[FR_TPS];
+#pragma unroll
+        for (int i = 0; i < FR_TPS; i++) {
+            xn[i] = snorm[(st & 1) * FR_TPS * 16 + i * 16 + c];
+#pragma unroll
+            for (int qb = 0; qb < FR_QBW; qb++) acc[i][qb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+#pragma unroll
+            for (int i = 0; i < FR_TPS; i++) {
+                const int o = i * TC + (t * 4 + g) * 16 + c;
+                const bf16x8 bh = __builtin_bit_cast(bf16x8, b[o]);
+                const bf16x8 bl = __builtin_bit_cast(bf16x8, b[o + DT * 64]);
+#pragma unroll
+                for (int qb = 0; qb < FR_QBW; qb++) {
+                    const bf16x8 a_h = __builtin_bit_cast(bf16x8, ah[qb][t]);
+                    const bf16x8 a_l = __builtin_bit_cast(bf16x8, al[qb][t]);
+                    acc[i][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bl, acc[i][qb], 0, 0, 0);
+                    acc[i][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_l, bh, acc[i][qb], 0, 0, 0);
+                    acc[i][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bh, acc[i][qb], 0, 0, 0);
+                }
+            }
+        }
+        if (st > 0) epilogue(prev, prevn, st - 1);
+#pragma unroll
+        for (int i = 0; i < FR_TPS; i++) {
+            prevn[i] = xn[i];
+#pragma unroll
+            for (int qb = 0; qb < FR_QBW; qb++) prev[i][qb] = acc[i][qb];
+        }
+    }
+    if (nst > 0) epilogue(prev, prevn, nst - 1);
+
+    // Per row: sort the group's keys, write the kk smallest and the bound.
+#pragma unroll 1
+    for (int j = 0; j < 4 * FR_QBW; j++) {
+        const int qb = j >> 2, r = j & 3;
+        float t[FR_J];
+#pragma unroll
+        for (int e = 0; e < FR_J; e++) {  // the lane's list of row slot j (registers: unrolled select)
+            float x = lst[0][0][e];
+#pragma unroll
+            for (int jj = 1; jj < 4 * FR_QBW; jj++) x = jj == j ? lst[jj >> 2][jj & 3][e] : x;
+            t[e] = x;
+        }
+        uint64_t k[FR_J];
+#pragma unroll
+        for (int e = 0; e < FR_J; e++) {
+            const uint32_t bits = __float_as_uint(t[e]);
+            const uint32_t col = (uint32_t)((tile0 + (int)(bits & ~kmask)) * 16 + c);
+            k[e] = t[e] < FR_BIG ? ((uint64_t)fkey(t[e]) << 32) | col : ~0ull;
+        }
+        uint32_t lb = t[FR_J - 1] < FR_BIG ? fkey(t[FR_J - 1]) : 0xffffffffu;  // a full list dropped keys >= it
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            const uint32_t x = shfl_xor_u32(lb, o);
+            lb = x < lb ? x : lb;
+        }
+        fr_group_sort(k);
+        uint64_t kth = k[0];
+#pragma unroll
+        for (int e = 1; e < FR_J; e++) kth = ((kk - 1) >> 4) == e ? k[e] : kth;
+        const int src = (lane & 48) | ((kk - 1) & 15);
+        const uint32_t kth_hi = (uint32_t)__shfl((int)(uint32_t)(kth >> 32), src, 64);
+        const uint32_t bound = kth_hi < lb ? kth_hi : lb;
+        const int qrow = q0 + (FR_QBW * wave + qb) * 16 + 4 * g + r;
+        if (qrow < nq) {
+            uint64_t* out = partial + ((size_t)qrow * splits + sl) * kk;
+#pragma unroll
+            for (int e = 0; e < FR_J; e++)
+                if (e * 16 + c < kk) out[e * 16 + c] = k[e];
+            if (c == 0) pbound[(size_t)qrow * splits + sl] = bound;
+        }
+    }
+}
+
+#define FL_BUF 2048
 #define FL_ROUND 512
 
 __device__ inline float flat_exact(const float* q, const float* x, int d, int metric) {
@@ -185,11 +459,56 @@ __device__ inline float flat_exact(const float* q, const float* x, int d, int me
     return 1.0f - seq_dot(q, x, d);
 }
 
+// Exact top-k of query qv over vectors [j0, j1) with a threshold-filtered LDS
+// buffer: keys (fkey(dist), index) sorted ascending in keys[0 ..) on return;
+// returns how many (all threads).  keys / pay hold FL_BUF entries.
+__device__ int flat_exact_range(const float* qv, const float* __restrict__ X, int j0, int j1, int d, int k,
+                                int metric, uint64_t* keys, uint32_t* pay, uint32_t* misc) {
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        misc[2] = 0;
+        misc[3] = 0xffffffffu;
+    }
+    __syncthreads();
+    for (int base = j0; base < j1; base += FL_ROUND) {
+        if ((int)misc[2] > FL_BUF - FL_ROUND) {
+            int m = (int)misc[2];
+            int m2 = next_pow2(m);
+            for (int i = m + tid; i < m2; i += blockDim.x) keys[i] = ~0ull;
+            block_bitonic_sort(keys, pay, m2);
+            if (tid == 0 && m >= k) {
+                misc[3] = (uint32_t)(keys[k - 1] >> 32);
+                misc[2] = (uint32_t)k;
+            }
+            __syncthreads();
+        }
+        const uint32_t th = misc[3];
+        for (int u = 0; u < FL_ROUND / 256; u++) {
+            int j = base + u * 256 + tid;
+            bool take = false;
+            uint64_t key = 0;
+            if (j < j1) {
+                float dist = flat_exact(qv, X + (size_t)j * d, d, metric);
+                key = cand_key(dist, (uint32_t)j);
+                take = (uint32_t)(key >> 32) <= th;
+            }
+            int slot = wave_append_slot(take, &misc[2]);
+            if (take) keys[slot] = key;
+        }
+        __syncthreads();
+    }
+    int m = (int)misc[2];
+    int m2 = next_pow2(m > 0 ? m : 1);
+    for (int i = m + tid; i < m2; i += blockDim.x) keys[i] = ~0ull;
+    block_bitonic_sort(keys, pay, m2);
+    return m;
+}
+
 __global__ __launch_bounds__(256) void flat_merge_kernel(
     const uint64_t* __restrict__ partial, int splits, int kk, const float* __restrict__ Q,
     const float* __restrict__ Qsq, const float* __restrict__ X, int nq, int n, int d, int k,
-    int metric, float xmax, uint32_t* __restrict__ out_idx, float* __restrict__ out_dist,
-    unsigned int* overflow) {
+    int metric, float xmax, const uint32_t* __restrict__ pbound, int ib, uint32_t* __restrict__ out_idx,
+    float* __restrict__ out_dist, unsigned int* overflow, uint32_t* __restrict__ flag_list) {
     __shared__ uint64_t keys[FL_BUF];
     __shared__ uint32_t pay[FL_BUF];
     __shared__ uint32_t misc[4];
@@ -203,25 +522,63 @@ __global__ __launch_bounds__(256) void flat_merge_kernel(
         pay[i] = 0;
     }
     block_bitonic_sort(keys, pay, n2);
+    // Proof.  A_k = the k-th smallest kept ranking key; the k kept entries with
+    // the smallest keys have exact distances <= A_k + tau, so every member of
+    // the exact top-k has a key <= bound = A_k + 2 tau.  An entry a slice
+    // dropped has a key >= that slice's bound (pbound, or its kk-th kept key)
+    // >= B, the smallest over the slices.  B > bound: the kept entries with
+    // keys <= bound hold the exact top-k (ties included), and they are
+    // rescored.  Fewer than k kept entries: every slice kept all it saw.
     if (tid == 0) {
-        int have = 0;
-        while (have < kk && keys[have] != ~0ull) have++;
-        uint32_t fail = 0;
-        if (n > have && have >= k) {
+        int m = 0, hi = tot;  // valid keys (the ~0 padding sorts last)
+        while (m < hi) {
+            const int mid = (m + hi) >> 1;
+            if (keys[mid] != ~0ull) m = mid + 1;
+            else hi = mid;
+        }
+        uint32_t fail = 0, rescore = (uint32_t)m;
+        if (m >= k) {
             const float u = 5.9604645e-08f;
             const float qmax = sqrtf(Qsq[q]) * 1.0001f + 1e-30f;
-            float tau = metric == 0 ? 4.0f * (float)(d + 8) * u * (qmax + xmax) * (qmax + xmax)
-                                    : 4.0f * (float)(d + 8) * u * (1.0f + qmax * xmax);
-            float gap = key_dist(keys[have - 1]) - key_dist(keys[k - 1]);
-            if (!(gap > 2.0f * tau)) fail = 1;
+            const float tau = pbound ? flat_bf16_tau(d, metric, qmax, xmax, ib)
+                                     : metric == 0 ? 4.0f * (float)(d + 8) * u * (qmax + xmax) * (qmax + xmax)
+                                                   : 4.0f * (float)(d + 8) * u * (1.0f + qmax * xmax);
+            uint32_t fb = fkey(key_dist(keys[k - 1]) + 2.0f * tau);
+            fb = fb < 0xfffffffeu ? fb + 1u : 0xffffffffu;  // one ulp up: the bound is not rounded down
+            uint32_t B = 0xffffffffu;
+            for (int sl = 0; sl < splits; sl++) {
+                uint32_t b = 0xffffffffu;
+                if (pbound) {
+                    b = pbound[(size_t)q * splits + sl];
+                } else {
+                    const uint64_t last = partial[((size_t)q * splits + sl) * kk + kk - 1];
+                    if (last != ~0ull) b = (uint32_t)(last >> 32);
+                }
+                B = b < B ? b : B;
+            }
+            if (!(B > fb)) {
+                fail = 1;
+            } else {
+                int lo = 0;
+                hi = m;  // keys whose high word is <= fb
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if ((uint32_t)(keys[mid] >> 32) <= fb) lo = mid + 1;
+                    else hi = mid;
+                }
+                rescore = (uint32_t)lo;
+            }
         }
-        misc[0] = (uint32_t)have;
+        misc[0] = rescore;
         misc[1] = fail;
-        if (fail) atomicAdd(overflow, 1u);
+        // an unproved query is answered by the exhaustive exact scan, spread
+        // over many workgroups by launch_flat_fallback
+        if (fail) flag_list[atomicAdd(overflow, 1u)] = (uint32_t)q;
     }
     __syncthreads();
     const int have = (int)misc[0];
-    if (!misc[1]) {
+    if (misc[1]) return;
+    {
         for (int i = tid; i < n2; i += blockDim.x) {
             if (i < have) {
                 uint32_t idx = (uint32_t)keys[i];
@@ -231,44 +588,6 @@ __global__ __launch_bounds__(256) void flat_merge_kernel(
             }
         }
         block_bitonic_sort(keys, pay, n2);
-    } else {
-        // Exhaustive exact scan with a threshold-filtered LDS buffer.
-        if (tid == 0) {
-            misc[2] = 0;
-            misc[3] = 0xffffffffu;
-        }
-        __syncthreads();
-        for (int base = 0; base < n; base += FL_ROUND) {
-            if ((int)misc[2] > FL_BUF - FL_ROUND) {
-                int m = (int)misc[2];
-                int m2 = next_pow2(m);
-                for (int i = m + tid; i < m2; i += blockDim.x) keys[i] = ~0ull;
-                block_bitonic_sort(keys, pay, m2);
-                if (tid == 0 && m >= k) {
-                    misc[3] = (uint32_t)(keys[k - 1] >> 32);
-                    misc[2] = (uint32_t)k;
-                }
-                __syncthreads();
-            }
-            const uint32_t th = misc[3];
-            for (int u = 0; u < FL_ROUND / 256; u++) {
-                int j = base + u * 256 + tid;
-                bool take = false;
-                uint64_t key = 0;
-                if (j < n) {
-                    float dist = flat_exact(qv, X + (size_t)j * d, d, metric);
-                    key = cand_key(dist, (uint32_t)j);
-                    take = (uint32_t)(key >> 32) <= th;
-                }
-                int slot = wave_append_slot(take, &misc[2]);
-                if (take) keys[slot] = key;
-            }
-            __syncthreads();
-        }
-        int m = (int)misc[2];
-        int m2 = next_pow2(m > 0 ? m : 1);
-        for (int i = m + tid; i < m2; i += blockDim.x) keys[i] = ~0ull;
-        block_bitonic_sort(keys, pay, m2);
     }
     for (int j = tid; j < k; j += blockDim.x) {
         size_t o = (size_t)q * k + j;
@@ -283,6 +602,65 @@ __global__ __launch_bounds__(256) void flat_merge_kernel(
     }
 }
 
+// Exhaustive exact fallback of the unproved queries, spread over the GPU:
+// workgroup (s, i) finds the exact top-k of query flag_list[i] among vectors
+// [s len, (s + 1) len) and writes its k smallest keys (padded with ~0); the
+// finish kernel merges a query's slices and writes its output row.
+__global__ __launch_bounds__(256) void flat_exact_slice_kernel(
+    const uint32_t* __restrict__ flag_list, const float* __restrict__ Q, const float* __restrict__ X, int n,
+    int d, int k, int metric, int len, uint64_t* __restrict__ out_keys) {
+    __shared__ uint64_t keys[FL_BUF];
+    __shared__ uint32_t pay[FL_BUF];
+    __shared__ uint32_t misc[4];
+    const int s = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
+    const uint32_t q = flag_list[i];
+    const int j0 = s * len, j1 = min(n, j0 + len);
+    const int m = flat_exact_range(Q + (size_t)q * d, X, j0, j1, d, k, metric, keys, pay, misc);
+    for (int j = tid; j < k; j += blockDim.x)
+        out_keys[((size_t)i * gridDim.x + s) * k + j] = j < m ? keys[j] : ~0ull;
+}
+
+__global__ __launch_bounds__(256) void flat_exact_finish_kernel(
+    const uint32_t* __restrict__ flag_list, int slices, int k, const uint64_t* __restrict__ in_keys,
+    uint32_t* __restrict__ out_idx, float* __restrict__ out_dist) {
+    __shared__ uint64_t keys[FL_BUF];
+    __shared__ uint32_t pay[FL_BUF];
+    const int i = blockIdx.x, tid = threadIdx.x;
+    const uint32_t q = flag_list[i];
+    const int tot = slices * k, n2 = next_pow2(tot);
+    for (int j = tid; j < n2; j += blockDim.x) {
+        keys[j] = j < tot ? in_keys[(size_t)i * tot + j] : ~0ull;
+        pay[j] = 0;
+    }
+    block_bitonic_sort(keys, pay, n2);
+    for (int j = tid; j < k; j += blockDim.x) {
+        const size_t o = (size_t)q * k + j;
+        const uint64_t key = keys[j];
+        out_idx[o] = key != ~0ull ? (uint32_t)key : 0xffffffffu;
+        out_dist[o] = key != ~0ull ? key_dist(key) : __int_as_float(0x7f800000);
+    }
+}
+
+int flat_fallback_slices(int n, int k) {
+    int sl = FL_BUF / k;
+    sl = sl > 64 ? 64 : sl;
+    const int most = (n + 255) / 256;  // at least 256 vectors per slice
+    return sl < most ? sl : (most > 0 ? most : 1);
+}
+
+void launch_flat_fallback(const uint32_t* flag_list, int nflag, const float* Q, const float* X, int n, int d,
+                          int k, int metric, uint64_t* keys, uint32_t* out_idx, float* out_dist,
+                          hipStream_t s) {
+    const int sl = flat_fallback_slices(n, k), len = (n + sl - 1) / sl;
+    for (int f0 = 0; f0 < nflag; f0 += 65535) {  // grid.y limit
+        const int nf = nflag - f0 < 65535 ? nflag - f0 : 65535;
+        hipLaunchKernelGGL(flat_exact_slice_kernel, dim3(sl, nf), dim3(256), 0, s, flag_list + f0, Q, X, n, d,
+                           k, metric, len, keys + (size_t)f0 * sl * k);
+        hipLaunchKernelGGL(flat_exact_finish_kernel, dim3(nf), dim3(256), 0, s, flag_list + f0, sl, k,
+                           keys + (size_t)f0 * sl * k, out_idx, out_dist);
+    }
+}
+
 // Database slices per query block: enough blocks to fill the GPU, slices of
 // at least 4 tiles, and splits * kk merge entries within the merge buffer.
 static int flat_splits(int nq, int n, int kk) {
@@ -294,15 +672,75 @@ static int flat_splits(int nq, int n, int kk) {
     return sp;
 }
 
-size_t flat_partial_count(int nq, int n, int k) {
+// The bf16x3 ranking kernel serves d <= 128 and k <= 32; it keeps
+// kk = k + 16 rounded up to 4 (at most the 64 keys a row's lanes hold) per
+// slice, plus one bound word per (query, slice) after the keys.
+static bool flat_rank_ok(int d, int k) { return d >= 1 && d <= 128 && k >= 1 && k <= 32; }
+static int flat_rank_keep(int k) { return (k + 16 + 3) & ~3; }
+
+// Slices for the ranking kernel: an even number of tiles each (stages are
+// tile pairs), enough workgroups for four waves of two per CU on 256 CUs,
+// slices of at least 64 tiles, and splits * kk merge entries within the
+// merge buffer; ib = the bits of a tile index within a slice.
+static int flat_rank_splits(int nq, int n, int kk, int* tps, int* ib) {
+    const int qb = (nq + FR_ROWS - 1) / FR_ROWS, ntiles = (n + 15) / 16;
+    int sp = 1;
+    while (qb * sp < 2048 && 2 * sp * kk <= FL_BUF && ntiles / (2 * sp) >= 64) sp <<= 1;
+    int t = (ntiles + sp - 1) / sp;
+    t += t & 1;
+    int b = 1;
+    while ((1 << b) < t) b++;
+    *tps = t;
+    *ib = b;
+    return (ntiles + t - 1) / t;
+}
+
+size_t flat_partial_count(int nq, int n, int d, int k) {
+    if (flat_rank_ok(d, k)) {
+        int tps, ib;
+        const int kk = flat_rank_keep(k);
+        const size_t slots = (size_t)nq * flat_rank_splits(nq, n, kk, &tps, &ib);
+        return slots * kk + (slots + 1) / 2;
+    }
     return (size_t)nq * flat_splits(nq, n, flat_keep(k)) * flat_keep(k);
 }
 
-void launch_flat_search(const float* Q, const float* Qsq, int nq, const float* X,
+size_t flat_pack_chunks(int n, int d) { return d <= 128 ? coarse_bf16_pack_chunks(n, d) : 0; }
+
+void launch_flat_pack(const float* X, int n, int d, uint4* Xb, hipStream_t s) {
+    if (d <= 128 && n > 0) launch_coarse_bf16_pack(X, n, d, Xb, s);
+}
+
+template <int DT>
+static void launch_rank(const float* Q, int nq, int d, const uint4* Xb, const float* Xnorm, int n, int metric,
+                        int kk, int tps, int ib, int sp, uint64_t* partial, uint32_t* pbound, hipStream_t s) {
+    const size_t lds = 2 * (size_t)FR_TPS * 2 * DT * 64 * 16 + 2 * FR_TPS * 16 * 4;
+    ensure_dyn_lds((const void*)flat_rank_kernel<DT>, lds);
+    dim3 grid((nq + FR_ROWS - 1) / FR_ROWS, sp);
+    hipLaunchKernelGGL(flat_rank_kernel<DT>, grid, dim3(VGPU_BLOCK), lds, s, Q, nq, d, Xb, Xnorm, n, metric, kk,
+                       tps, ib, sp, partial, pbound);
+}
+
+void launch_flat_search(const float* Q, const float* Qsq, int nq, const float* X, const uint4* Xb,
                         const float* Xnorm, int n, int d, int k, int metric, float xmax,
                         uint64_t* partial, uint32_t* out_idx, float* out_dist,
-                        unsigned int* overflow, hipStream_t s) {
+                        unsigned int* overflow, uint32_t* flag_list, hipStream_t s, hipEvent_t ranked) {
     if (nq <= 0) return;
+    if (Xb && flat_rank_ok(d, k)) {
+        int tps, ib;
+        const int kk = flat_rank_keep(k), sp = flat_rank_splits(nq, n, kk, &tps, &ib);
+        uint32_t* pbound = reinterpret_cast<uint32_t*>(partial + (size_t)nq * sp * kk);
+        switch ((d + 31) / 32) {
+            case 1: launch_rank<1>(Q, nq, d, Xb, Xnorm, n, metric, kk, tps, ib, sp, partial, pbound, s); break;
+            case 2: launch_rank<2>(Q, nq, d, Xb, Xnorm, n, metric, kk, tps, ib, sp, partial, pbound, s); break;
+            case 3: launch_rank<3>(Q, nq, d, Xb, Xnorm, n, metric, kk, tps, ib, sp, partial, pbound, s); break;
+            default: launch_rank<4>(Q, nq, d, Xb, Xnorm, n, metric, kk, tps, ib, sp, partial, pbound, s); break;
+        }
+        if (ranked) (void)hipEventRecord(ranked, s);
+        hipLaunchKernelGGL(flat_merge_kernel, dim3(nq), dim3(256), 0, s, partial, sp, kk, Q, Qsq, X, nq, n,
+                           d, k, metric, xmax, pbound, ib, out_idx, out_dist, overflow, flag_list);
+        return;
+    }
     const int kk = flat_keep(k), cap = flat_cap(kk), sp = flat_splits(nq, n, kk);
     const int chunk = (((n + sp - 1) / sp) + FL_N - 1) / FL_N * FL_N;
     size_t lds = 2 * FL_Q * (FL_K + 1) * 4 + (size_t)FL_Q * cap * 8 + 2 * FL_Q * 4;
@@ -310,8 +748,9 @@ void launch_flat_search(const float* Q, const float* Qsq, int nq, const float* X
     dim3 grid((nq + FL_Q - 1) / FL_Q, sp);
     hipLaunchKernelGGL(flat_partial_kernel, grid, dim3(256), lds, s, Q, X, Xnorm, nq, n, d, metric, kk,
                        cap, sp, chunk, partial);
+    if (ranked) (void)hipEventRecord(ranked, s);
     hipLaunchKernelGGL(flat_merge_kernel, dim3(nq), dim3(256), 0, s, partial, sp, kk, Q, Qsq, X, nq, n,
-                       d, k, metric, xmax, out_idx, out_dist, overflow);
+                       d, k, metric, xmax, nullptr, 0, out_idx, out_dist, overflow, flag_list);
 }
 
 }  // namespace vgpu

@@ -498,8 +498,17 @@ int vgpu_flat_search_batch_device(vgpu_flat* h, const float* d_queries, size_t n
 int vgpu_flat_last_ms(const vgpu_flat* h, float* ms_gemm, float* ms_total) {
     return guard([&] {
         need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
+        std::lock_guard<std::mutex> lk(h->fx->mu);
         if (ms_gemm) *ms_gemm = h->fx->ms_gemm;
         if (ms_total) *ms_total = h->fx->ms_total;
+    });
+}
+
+int vgpu_flat_last_fallbacks(const vgpu_flat* h, uint32_t* queries) {
+    return guard([&] {
+        need(h && queries, VGPU_ERR_INVALID_PARAMETER, "null argument");
+        std::lock_guard<std::mutex> lk(h->fx->mu);
+        *queries = h->fx->fallbacks;
     });
 }
 

@@ -35,6 +35,10 @@ void FlatIndex::add(const float* x, size_t count) {
     d_x.upload(host.data(), n * d, stream);
     d_xnorm.reserve(n);
     launch_flat_norms(d_x.p, (int)n, (int)d, d_xnorm.p, stream);
+    if (flat_pack_chunks((int)n, (int)d)) {
+        d_xb.reserve(flat_pack_chunks((int)n, (int)d));
+        launch_flat_pack(d_x.p, (int)n, (int)d, d_xb.p, stream);
+    }
     VGPU_HIP(hipGetLastError());
     VGPU_HIP(hipStreamSynchronize(stream));
 }
@@ -51,21 +55,30 @@ void FlatIndex::search_device(const float* d_q, size_t nq, size_t k, int64_t* d_
     }
     const float xmax = (float)(std::sqrt(xmax2) * 1.0001 + 1e-30);
     w_qnorm.reserve(nq);
-    w_partial.reserve(flat_partial_count((int)nq, (int)n, (int)k));
+    w_partial.reserve(flat_partial_count((int)nq, (int)n, (int)d, (int)k));
     w_idx.reserve(nq * k);
     w_dist.reserve(nq * k);
     w_overflow.reserve(1);
+    w_flag.reserve(nq);
     VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
-    VGPU_HIP(hipEventRecord(ev[0], s));
     launch_flat_norms(d_q, (int)nq, (int)d, w_qnorm.p, s);
-    launch_flat_search(d_q, w_qnorm.p, (int)nq, d_x.p, d_xnorm.p, (int)n, (int)d, (int)k, metric, xmax,
-                       w_partial.p, w_idx.p, w_dist.p, w_overflow.p, s);
+    VGPU_HIP(hipEventRecord(ev[0], s));
+    launch_flat_search(d_q, w_qnorm.p, (int)nq, d_x.p, d_xb.n ? d_xb.p : nullptr, d_xnorm.p, (int)n, (int)d,
+                       (int)k, metric, xmax, w_partial.p, w_idx.p, w_dist.p, w_overflow.p, w_flag.p, s, ev[3]);
+    // the unproved queries (rare): exhaustive exact scan over many workgroups
+    VGPU_HIP(hipMemcpyAsync(&fallbacks, w_overflow.p, sizeof(unsigned int), hipMemcpyDeviceToHost, s));
+    VGPU_HIP(hipStreamSynchronize(s));
+    if (fallbacks) {
+        w_fbkeys.reserve((size_t)fallbacks * flat_fallback_slices((int)n, (int)k) * k);
+        launch_flat_fallback(w_flag.p, (int)fallbacks, d_q, d_x.p, (int)n, (int)d, (int)k, metric, w_fbkeys.p,
+                             w_idx.p, w_dist.p, s);
+    }
     VGPU_HIP(hipEventRecord(ev[1], s));
     launch_finalize(w_idx.p, w_dist.p, nullptr, (int)nq, (int)k, (int)k, d_ids, d_dists, s);
     VGPU_HIP(hipEventRecord(ev[2], s));
     VGPU_HIP(hipGetLastError());
-    VGPU_HIP(hipEventSynchronize(ev[2]));
-    VGPU_HIP(hipEventElapsedTime(&ms_gemm, ev[0], ev[1]));
+    VGPU_HIP(hipStreamSynchronize(s));
+    VGPU_HIP(hipEventElapsedTime(&ms_gemm, ev[0], ev[3]));
     VGPU_HIP(hipEventElapsedTime(&ms_total, ev[0], ev[2]));
 }
 

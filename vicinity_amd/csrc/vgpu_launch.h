@@ -183,11 +183,27 @@ void launch_fastscan_test(const uint8_t* packed, int n, int M, const float* lut,
 
 // Flat exact search.
 void launch_flat_norms(const float* X, int n, int d, float* norms, hipStream_t s);
-size_t flat_partial_count(int nq, int n, int k);
-// Qsq / Xnorm: squared norms (flat_norms); xmax: max ||x||.
-void launch_flat_search(const float* Q, const float* Qsq, int nq, const float* X,
+size_t flat_partial_count(int nq, int n, int d, int k);
+// bf16 hi/lo copy of the database for the ranking kernel (d <= 128; 0 chunks
+// otherwise), in the coarse quantiser's tile-major layout.
+size_t flat_pack_chunks(int n, int d);
+void launch_flat_pack(const float* X, int n, int d, uint4* Xb, hipStream_t s);
+// Qsq / Xnorm: squared norms (flat_norms); xmax: max ||x||; Xb: the packed
+// copy (null: the fp32 ranking path for every shape); `ranked` (optional) is
+// recorded between the ranking kernel and the merge.
+// Queries whose kept candidates cannot be proved to hold the exact top-k are
+// appended to flag_list (*overflow, zero on entry, counts them) and their
+// rows are left for launch_flat_fallback.
+void launch_flat_search(const float* Q, const float* Qsq, int nq, const float* X, const uint4* Xb,
                         const float* Xnorm, int n, int d, int k, int metric, float xmax,
                         uint64_t* partial, uint32_t* out_idx, float* out_dist,
-                        unsigned int* overflow, hipStream_t s);
+                        unsigned int* overflow, uint32_t* flag_list, hipStream_t s,
+                        hipEvent_t ranked = nullptr);
+// Exhaustive exact top-k rows of the nflag queries of flag_list;
+// keys: scratch of nflag * flat_fallback_slices(n, k) * k entries.
+int flat_fallback_slices(int n, int k);
+void launch_flat_fallback(const uint32_t* flag_list, int nflag, const float* Q, const float* X, int n, int d,
+                          int k, int metric, uint64_t* keys, uint32_t* out_idx, float* out_dist,
+                          hipStream_t s);
 
 }  // namespace vgpu

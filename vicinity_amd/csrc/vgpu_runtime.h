@@ -247,13 +247,15 @@ struct FlatIndex {
     hipStream_t stream = nullptr;
     hipEvent_t ev[4] = {};
     DevBuf<float> d_x, d_xnorm, w_q, w_dist, w_odist, w_qnorm;
-    DevBuf<uint64_t> w_partial;
-    DevBuf<uint32_t> w_idx;
+    DevBuf<uint4> d_xb;  // bf16 hi/lo copy for the ranking kernel (d <= 128)
+    DevBuf<uint64_t> w_partial, w_fbkeys;
+    DevBuf<uint32_t> w_idx, w_flag;
     DevBuf<int64_t> w_ids;
     DevBuf<unsigned int> w_overflow;
     std::vector<float> host;
     double xmax2 = 0.0;  // max ||x||^2
     float ms_gemm = 0.f, ms_total = 0.f;
+    unsigned int fallbacks = 0;  // queries of the last search that took the exhaustive exact scan
     std::mutex mu;
 
     FlatIndex(size_t dim, int met);

@@ -63,6 +63,12 @@ class FlatIndex:
             out_dists.data_ptr(), s))
         return out_ids, out_dists
 
+    def last_fallbacks(self) -> int:
+        """Queries of the last search answered by the exhaustive exact scan."""
+        q = ctypes.c_uint32()
+        _lib.check(self._L.vgpu_flat_last_fallbacks(self._h, ctypes.byref(q)))
+        return q.value
+
     def last_ms(self):
         g, t = ctypes.c_float(), ctypes.c_float()
         _lib.check(self._L.vgpu_flat_last_ms(self._h, ctypes.byref(g), ctypes.byref(t)))
