@@ -293,6 +293,7 @@ __global__ __launch_bounds__(256) void flat_rank_kernel(
     // 32 t + 8 g .. + 7 (zero past d; rows past nq repeat the last query and
     // are never written).
     u32x4 ah[FR_QBW][DT], al[FR_QBW][DT];
+    const float qsc = metric == 0 ? -2.0f : -1.0f;
 #pragma unroll
     for (int qb = 0; qb < FR_QBW; qb++) {
         const int row = min(q0 + (FR_QBW * wave + qb) * 16 + c, nq - 1);
@@ -303,7 +304,9 @@ __global__ __launch_bounds__(256) void flat_rank_kernel(
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int j = 32 * t + 8 * g + i;
-                const float x = j < d ? qr[j] : 0.0f;
+                // scaled by -2 (metric 0) or -1 (exact), so an accumulator is
+                // the score less ||x||^2 (or less 1)
+                const float x = j < d ? qsc * qr[j] : 0.0f;
                 hb[i] = fr_bf16_bits(x);
                 lb[i] = fr_bf16_bits(x - __uint_as_float(hb[i] << 16));
             }
@@ -335,17 +338,20 @@ __global__ __launch_bounds__(256) void flat_rank_kernel(
         for (int i = 0; i < PER; i++) stage[(size_t)buf * SC + i * VGPU_BLOCK + tid] = pre[i];
         if (tid < FR_TPS * 16) snorm[buf * FR_TPS * 16 + tid] = pn;
     };
-    // Scores of stage st into the lane's lists.
-    auto epilogue = [&](const floatx4 (&acc)[FR_TPS][FR_QBW], const float (&xn)[FR_TPS], int st) {
+    // Scores of stage st into the lane's lists: score = base + acc with base
+    // ||x||^2 (metric 0) or 1 (the product is -2 q.x or -q.x); only the
+    // slice's last stage can hold columns past its tiles or past n.
+    auto epilogue = [&](const floatx4 (&acc)[FR_TPS][FR_QBW], const float (&xn)[FR_TPS], int st, bool last) {
 #pragma unroll
         for (int i = 0; i < FR_TPS; i++) {
             const int ti = FR_TPS * st + i;  // tile index in the slice, < 2^ib
-            const bool colok = tile0 + ti < tile1 && (tile0 + ti) * 16 + c < n;
+            const bool colok = !last || (tile0 + ti < tile1 && (tile0 + ti) * 16 + c < n);
+            const float base = metric == 0 ? xn[i] : 1.0f;
 #pragma unroll
             for (int qb = 0; qb < FR_QBW; qb++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const float v = metric == 0 ? xn[i] - 2.0f * acc[i][qb][r] : 1.0f - acc[i][qb][r];
+                    const float v = base + acc[i][qb][r];
                     const float key = __uint_as_float((__float_as_uint(v) & kmask) | (uint32_t)ti);
                     fr_insert(lst[qb][r], colok ? key : FR_BIG);
                 }
@@ -391,7 +397,7 @@ __global__ __launch_bounds__(256) void flat_rank_kernel(
                 }
             }
         }
-        if (st > 0) epilogue(prev, prevn, st - 1);
+        if (st > 0) epilogue(prev, prevn, st - 1, false);
 #pragma unroll
         for (int i = 0; i < FR_TPS; i++) {
             prevn[i] = xn[i];
@@ -399,7 +405,7 @@ __global__ __launch_bounds__(256) void flat_rank_kernel(
             for (int qb = 0; qb < FR_QBW; qb++) prev[i][qb] = acc[i][qb];
         }
     }
-    if (nst > 0) epilogue(prev, prevn, nst - 1);
+    if (nst > 0) epilogue(prev, prevn, nst - 1, true);
 
     // Per row: sort the group's keys, write the kk smallest and the bound.
 #pragma unroll 1
@@ -602,6 +608,110 @@ __global__ __launch_bounds__(256) void flat_merge_kernel(
     }
 }
 
+// Merge of the ranking kernel's slices, one wave per query (four per
+// workgroup), keys in registers: key i = e * 64 + lane in k[e].  The proof is
+// flat_merge_kernel's: A_k by a bitwise search over the keys' high words
+// (ballot counts), B the smallest slice bound; the keys <= A_k + 2 tau (at
+// most FM_R) are compacted through LDS, rescored with the reference's
+// arithmetic and sorted in registers.  More than FM_R such keys, or no
+// proof: the query goes to the exhaustive fallback.
+#define FM_R 256
+template <int E>
+__global__ __launch_bounds__(256) void flat_merge_wave_kernel(
+    const uint64_t* __restrict__ partial, const uint32_t* __restrict__ pbound, int splits, int kk,
+    const float* __restrict__ Q, const float* __restrict__ Qsq, const float* __restrict__ X, int nq, int d,
+    int k, int metric, float xmax, int ib, uint32_t* __restrict__ out_idx, float* __restrict__ out_dist,
+    unsigned int* overflow, uint32_t* __restrict__ flag_list) {
+    __shared__ uint64_t rbuf[4][FM_R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = blockIdx.x * 4 + wave;
+    if (q >= nq) return;
+    const int tot = splits * kk;
+    uint64_t kv[E];
+    const uint64_t* src = partial + (size_t)q * tot;
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const int i = e * 64 + lane;
+        kv[e] = i < tot ? src[i] : ~0ull;
+    }
+    int m = 0;  // valid keys (padding is ~0)
+#pragma unroll
+    for (int e = 0; e < E; e++) m += (int)__popcll(__ballot(kv[e] != ~0ull));
+    uint32_t fb = 0xffffffffu;  // keys whose high word is <= fb are rescored
+    if (m >= k) {
+        uint32_t T = 0;  // the (k-1)-th smallest high word: the largest v with < k words below it
+        for (int b = 31; b >= 0; b--) {
+            const uint32_t cand = T | (1u << b);
+            int below = 0;
+#pragma unroll
+            for (int e = 0; e < E; e++) below += (int)__popcll(__ballot((uint32_t)(kv[e] >> 32) < cand));
+            if (below <= k - 1) T = cand;
+        }
+        const float u = 5.9604645e-08f;
+        const float qmax = sqrtf(Qsq[q]) * 1.0001f + 1e-30f;
+        const float tau = flat_bf16_tau(d, metric, qmax, xmax, ib);
+        fb = fkey(fkey_to_float(T) + 2.0f * tau);
+        fb = fb < 0xfffffffeu ? fb + 1u : 0xffffffffu;  // one ulp up: the bound is not rounded down
+        (void)u;
+        uint32_t B = 0xffffffffu;
+        for (int sl = lane; sl < splits; sl += 64) {
+            const uint32_t b = pbound[(size_t)q * splits + sl];
+            B = b < B ? b : B;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint32_t x = (uint32_t)__shfl_xor((int)B, o, 64);
+            B = x < B ? x : B;
+        }
+        if (!(B > fb)) {
+            if (lane == 0) flag_list[atomicAdd(overflow, 1u)] = (uint32_t)q;
+            return;
+        }
+    }
+    // compact the keys <= fb into this wave's LDS row
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const bool take = kv[e] != ~0ull && (uint32_t)(kv[e] >> 32) <= fb;
+        const uint64_t mk = __ballot(take);
+        const uint32_t pos = cnt + __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
+        if (take && pos < FM_R) rbuf[wave][pos] = kv[e];
+        cnt += (uint32_t)__popcll(mk);
+    }
+    if (cnt > FM_R) {  // more near-ties than the rescoring holds
+        if (lane == 0) flag_list[atomicAdd(overflow, 1u)] = (uint32_t)q;
+        return;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const float* qv = Q + (size_t)q * d;
+    auto rescore = [&](uint32_t i) -> uint64_t {
+        if (i >= cnt) return ~0ull;
+        const uint32_t idx = (uint32_t)rbuf[wave][i];
+        return cand_key(flat_exact(qv, X + (size_t)idx * d, d, metric), idx);
+    };
+    auto emit = [&](int j, uint64_t key) {
+        if (j < k) {
+            const size_t o = (size_t)q * k + j;
+            out_idx[o] = key != ~0ull ? (uint32_t)key : 0xffffffffu;
+            out_dist[o] = key != ~0ull ? key_dist(key) : __int_as_float(0x7f800000);
+        }
+    };
+    if (cnt <= 64) {  // the usual case: one key per lane
+        uint64_t r1[1] = {rescore((uint32_t)lane)};
+        wave_sort_regs<1>(r1);
+        emit(lane, r1[0]);
+        return;
+    }
+    uint64_t r[FM_R / 64];
+#pragma unroll
+    for (int e = 0; e < FM_R / 64; e++) r[e] = rescore((uint32_t)(e * 64 + lane));
+    wave_sort_regs<FM_R / 64>(r);
+#pragma unroll
+    for (int e = 0; e < FM_R / 64; e++) emit(e * 64 + lane, r[e]);
+}
+
 // Exhaustive exact fallback of the unproved queries, spread over the GPU:
 // workgroup (s, i) finds the exact top-k of query flag_list[i] among vectors
 // [s len, (s + 1) len) and writes its k smallest keys (padded with ~0); the
@@ -643,7 +753,7 @@ __global__ __launch_bounds__(256) void flat_exact_finish_kernel(
 
 int flat_fallback_slices(int n, int k) {
     int sl = FL_BUF / k;
-    sl = sl > 64 ? 64 : sl;
+    sl = sl > 256 ? 256 : sl;
     const int most = (n + 255) / 256;  // at least 256 vectors per slice
     return sl < most ? sl : (most > 0 ? most : 1);
 }
@@ -737,8 +847,20 @@ void launch_flat_search(const float* Q, const float* Qsq, int nq, const float* X
             default: launch_rank<4>(Q, nq, d, Xb, Xnorm, n, metric, kk, tps, ib, sp, partial, pbound, s); break;
         }
         if (ranked) (void)hipEventRecord(ranked, s);
-        hipLaunchKernelGGL(flat_merge_kernel, dim3(nq), dim3(256), 0, s, partial, sp, kk, Q, Qsq, X, nq, n,
-                           d, k, metric, xmax, pbound, ib, out_idx, out_dist, overflow, flag_list);
+        const int tot = sp * kk;
+        const dim3 mg((nq + 3) / 4);
+        if (tot <= 256)
+            hipLaunchKernelGGL(flat_merge_wave_kernel<4>, mg, dim3(256), 0, s, partial, pbound, sp, kk, Q, Qsq, X,
+                               nq, d, k, metric, xmax, ib, out_idx, out_dist, overflow, flag_list);
+        else if (tot <= 512)
+            hipLaunchKernelGGL(flat_merge_wave_kernel<8>, mg, dim3(256), 0, s, partial, pbound, sp, kk, Q, Qsq, X,
+                               nq, d, k, metric, xmax, ib, out_idx, out_dist, overflow, flag_list);
+        else if (tot <= 1024)
+            hipLaunchKernelGGL(flat_merge_wave_kernel<16>, mg, dim3(256), 0, s, partial, pbound, sp, kk, Q, Qsq,
+                               X, nq, d, k, metric, xmax, ib, out_idx, out_dist, overflow, flag_list);
+        else
+            hipLaunchKernelGGL(flat_merge_wave_kernel<32>, mg, dim3(256), 0, s, partial, pbound, sp, kk, Q, Qsq,
+                               X, nq, d, k, metric, xmax, ib, out_idx, out_dist, overflow, flag_list);
         return;
     }
     const int kk = flat_keep(k), cap = flat_cap(kk), sp = flat_splits(nq, n, kk);
