@@ -127,3 +127,28 @@ def test_ctypes_structs_match_the_c_header_field_by_field(tmp_path):
         assert got[(cname, "size")] == ctypes.sizeof(py), cname
         for field, _ in py._fields_:
             assert got[(cname, field)] == getattr(py, field).offset, (cname, field)
+
+
+def test_static_archive_links_into_a_c_program(tmp_path):
+    """libvicinity_gpu.a (what a Rust build.rs links statically) resolves
+    every declared entry point and runs the host-side checks of a C program
+    linked against it."""
+    import shutil
+    import subprocess
+
+    archive = os.path.join(ROOT, "vicinity_amd", "libvicinity_gpu.a")
+    assert os.path.exists(archive), "run make -C vicinity_amd/csrc"
+    nm = shutil.which("nm")
+    if nm:
+        out = subprocess.run([nm, "-g", "--defined-only", archive], capture_output=True,
+                             text=True, check=True).stdout
+        defined = set(re.findall(r" T (vgpu_[a-z0-9_]+)$", out, flags=re.M))
+        assert set(_declared_symbols()) <= defined
+    exe = str(tmp_path / "link_check")
+    subprocess.run(["gcc", "-O1", "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "static_link", "link_check.c"), archive,
+                    "-L/opt/rocm/lib", "-lamdhip64", "-lstdc++", "-lm", "-lpthread",
+                    "-Wl,-rpath,/opt/rocm/lib", "-o", exe], check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "static link ok" in r.stdout
