@@ -250,6 +250,22 @@ int vgpu_test_host_centroid_update(const float *x, size_t n, size_t d, const uin
 /* The OPQ polar factor U V^T of M f32[d*d] (compute_optimal_rotation,
  * opq.rs:280-294) into R f32[d*d]. */
 int vgpu_test_polar_factor(const float *m, size_t d, float *r);
+/* The error bounds behind the exactness proofs, evaluated on the host by
+ * the same code the kernels run (test hooks with no reference counterpart;
+ * no device call): FAST ranking value against the ADC distance
+ * (search.rs:1318-1354), bf16x3 and fp32 coarse scores against the
+ * sequential dot (search.rs:1602-1617), flat bf16x3 key against
+ * l2_distance_squared / 1 - dot (distance.rs:78-109). */
+int vgpu_test_bound_fast_tau(size_t d, size_t M, size_t ds, float qn, float cmax, float rmax,
+                             float t0max, float *out);
+int vgpu_test_bound_coarse(size_t d, float qn, float cmax, float *out_bf16x3, float *out_fp32);
+int vgpu_test_bound_flat(size_t d, int metric, float qn, float xn, int ib, float *out);
+/* Device-allocation failure injection (a test hook with no reference
+ * counterpart): after `after` more device allocations by the library succeed,
+ * the next `count` fail with VGPU_ERR_OUT_OF_MEMORY, as hipMalloc's
+ * out-of-memory would (the reference's allocation failure is a process
+ * abort).  count 0 disarms.  Process-wide. */
+int vgpu_test_fail_device_allocations(size_t after, size_t count);
 /* Bound on the rotated residuals (floats) one pass of a filtered search
  * under OPQ holds; queries beyond it go in further passes (default 2^28). */
 int vgpu_test_set_rres_limit(vgpu_ivfpq *h, size_t floats);

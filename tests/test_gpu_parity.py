@@ -404,7 +404,7 @@ def test_probe_selection_paths(vg, oracle, d, L, P):
 def test_coarse_bf16x3_dots_within_bound(vg, nq, L, d):
     """Split-bfloat16 MFMA dot products (the search path's coarse kernel)
     against float64, within the bound its proof window uses:
-    (3 * 2^-18 + 7 d u) sum|q_j c_j|.  A wrong operand or output lane layout
+    (3.01 * 2^-16 + 7 d u) sum|q_j c_j|.  A wrong operand or output lane layout
     fails by orders of magnitude."""
     from vicinity_amd import _lib
 
@@ -415,7 +415,7 @@ def test_coarse_bf16x3_dots_within_bound(vg, nq, L, d):
     _lib.check(_lib.load().vgpu_test_coarse_dots_bf16x3(_lib.ptr(q), nq, _lib.ptr(c), L, d, _lib.ptr(out)))
     ref = q.astype(np.float64) @ c.astype(np.float64).T
     absdot = np.abs(q).astype(np.float64) @ np.abs(c).astype(np.float64).T
-    bound = (3 * 2.0 ** -18 + 7 * d * 2.0 ** -24) * absdot
+    bound = (3.01 * 2.0 ** -16 + 7 * d * 2.0 ** -24) * absdot
     err = np.abs(out - ref)
     assert (err <= bound + 1e-30).all(), float((err / (absdot + 1e-30)).max())
 

@@ -70,6 +70,8 @@ _sz = ctypes.c_size_t
 _vp = ctypes.c_void_p
 _H = ctypes.c_void_p
 _i = ctypes.c_int
+_ci = ctypes.c_int
+_f = ctypes.c_float
 
 # name -> (restype, argtypes); every symbol declared in include/vicinity_gpu.h.
 SIGNATURES = {
@@ -114,6 +116,10 @@ SIGNATURES = {
     "vgpu_test_host_centroid_update": (_i, [_vp, _sz, _sz, _vp, _sz, _vp]),
     "vgpu_test_polar_factor": (_i, [_vp, _sz, _vp]),
     "vgpu_test_set_rres_limit": (_i, [_H, _sz]),
+    "vgpu_test_fail_device_allocations": (_i, [_sz, _sz]),
+    "vgpu_test_bound_fast_tau": (_i, [_sz, _sz, _sz, _f, _f, _f, _f, _vp]),
+    "vgpu_test_bound_coarse": (_i, [_sz, _f, _f, _vp, _vp]),
+    "vgpu_test_bound_flat": (_i, [_sz, _ci, _f, _f, _ci, _vp]),
     "vgpu_test_adc_tables": (_i, [_vp, _sz, _sz, _sz, _vp, _sz, _vp]),
     "vgpu_test_pq_encode": (_i, [_vp, _sz, _sz, _sz, _vp, _sz, _vp]),
     "vgpu_test_normalize": (_i, [_vp, _sz, _sz, _vp]),

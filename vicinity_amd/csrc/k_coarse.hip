@@ -6,6 +6,7 @@
 // search.rs:1602-1617 with cosine_distance_normalized src/distance.rs:104-109
 // (score 1 - dot(q, c), nprobe smallest, ascending).
 #include "vgpu_device.h"
+#include "vgpu_bounds.h"
 #include "vgpu_launch.h"
 
 namespace vgpu {
@@ -124,15 +125,6 @@ void launch_coarse_dots(const float* Q, const float* C, float* D, int nq, int L,
 
 // ---- probe selection ----------------------------------------------------
 #define SEL_CAP 1024
-
-// Error bound of the fp32 scores (MFMA GEMM or approx_dot) against the sequential one: both are within
-// (d + 2) u sum|q_j c_j| <= (d + 2) u ||q|| ||c|| of the real dot product,
-// plus the rounding of 1 - dot; doubled for safety.
-__device__ __forceinline__ float coarse_tau(int d, float qn, float cmax) {
-    const float u = 5.9604645e-08f;
-    return 2.0f * ((2.0f * (float)d + 8.0f) * u * qn * cmax + 4.0f * u * (1.0f + qn * cmax)) +
-           1e-30f;
-}
 
 // Exact ordering of the window candidates keys[0..cn) (list indices on entry):
 // rescore 1 - dot in the reference's sequential order, sort by (score, list),
@@ -339,7 +331,8 @@ void launch_coarse_exact_flagged(const float* qn, const float* qnorm, const floa
                                  const uint32_t* flag_list, const uint32_t* flag_count, hipStream_t s) {
     if (nq <= 0) return;
     const size_t lds = ((size_t)L + ((d + 3) & ~3)) * sizeof(float);
-    const dim3 grid(nq < 256 ? nq : 256);
+    // flagged queries are rare: a small grid keeps the usual empty launch cheap
+    const dim3 grid(nq < 64 ? nq : 64);
     if (L <= 16 * VGPU_BLOCK) {
         ensure_dyn_lds((const void*)coarse_exact_flagged_kernel<16>, lds);
         hipLaunchKernelGGL(coarse_exact_flagged_kernel<16>, grid, dim3(256), lds, s, qn, qnorm, C, L, d, P,

@@ -295,17 +295,7 @@ __global__ __launch_bounds__(256) void fastscan_kernel(DevIndex ix, ScanArgs a, 
         st[1] = st[2] = st[3] = 0u;
     }
     block_bitonic_sort_keys(allkeys, 4 * wbuf);
-    for (int j = tid; j < a.kout; j += blockDim.x) {
-        size_t o = (size_t)q * a.kout + j;
-        uint64_t key = allkeys[j];
-        if (key != ~0ull) {
-            a.out_vidx[o] = (uint32_t)key;
-            a.out_dist[o] = key_dist(key);
-        } else {
-            a.out_vidx[o] = 0xffffffffu;
-            a.out_dist[o] = __int_as_float(0x7f800000);
-        }
-    }
+    for (int j = tid; j < a.kout; j += blockDim.x) scan_emit(a, q, j, allkeys[j], allkeys[j] != ~0ull);
 }
 
 size_t fastscan_lds_bytes(const DevIndex& ix, const ScanArgs& a) {

@@ -23,6 +23,7 @@
 // smallest by a bitonic sort when it fills.  flat_partial_kernel (any d) is
 // the fp32 MFMA path with per-row LDS thresholds.
 #include "vgpu_device.h"
+#include "vgpu_bounds.h"
 #include "vgpu_launch.h"
 
 namespace vgpu {
@@ -189,30 +190,10 @@ __global__ __launch_bounds__(256) void flat_partial_kernel(
 #define FR_BIG 3.0e38f
 
 // Round to nearest even bfloat16 bits (finite inputs); x = hi + lo + r with
-// |r| <= 2^-18 |x|.
+// |r| <= 2^-16 |x|.
 __device__ __forceinline__ uint32_t fr_bf16_bits(float x) {
     const uint32_t u = __float_as_uint(x);
     return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
-
-// Bound on |ranking key + ||q||^2 (metric 0) - exact distance| with the
-// exact distance l2_distance_squared / 1 - seq_dot in float32
-// (u = 2^-24, |q| <= qn, |x| <= xn): the bf16x3 product is within
-// (3.01 2^-18 + 7 d u) |q||x| of q.x, ||x||^2 within d u ||x||^2, one rounding
-// of the score, the reference's sum within (d + 1) u (|q| + |x|)^2 (or
-// d u |q||x| + 2u (1 + |q||x|) for 1 - dot), taken twice; plus the packing:
-// a key is the score with its low ib mantissa bits replaced by a tile index,
-// within 2^ib ulps of |score| <= ||x||^2 + 2 |q||x| (or 1 + |q||x|).
-__host__ __device__ inline float flat_bf16_tau(int d, int metric, float qn, float xn, int ib) {
-    const float u = 5.9604645e-08f;
-    const float qx = qn * xn;
-    const float dot = (3.01f * 3.8146973e-06f + 7.0f * (float)d * u) * qx;
-    const float smax = metric == 1 ? 1.0f + qx : xn * xn + 2.0f * qx;
-    const float pack = ((float)(1u << ib) + 1.0f) * 2.0f * u * smax;
-    if (metric == 1) return 2.0f * (dot + (float)d * u * qx + 2.0f * u * (1.0f + qx)) + pack + 1e-30f;
-    const float s = qn + xn;
-    return 2.0f * (2.0f * dot + (float)d * u * xn * xn + u * (xn * xn + 2.0f * qx) +
-                   (float)(d + 1) * u * s * s) + pack + 1e-30f;
 }
 
 // Ascending list of the FR_J smallest keys: t_i' = med3(t_{i-1}, t_i, v) from
@@ -621,7 +602,7 @@ __global__ __launch_bounds__(256) void flat_merge_wave_kernel(
     const uint64_t* __restrict__ partial, const uint32_t* __restrict__ pbound, int splits, int kk,
     const float* __restrict__ Q, const float* __restrict__ Qsq, const float* __restrict__ X, int nq, int d,
     int k, int metric, float xmax, int ib, uint32_t* __restrict__ out_idx, float* __restrict__ out_dist,
-    unsigned int* overflow, uint32_t* __restrict__ flag_list) {
+    unsigned int* overflow, uint32_t* __restrict__ flag_list, uint32_t* __restrict__ fbv) {
     __shared__ uint64_t rbuf[4][FM_R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = blockIdx.x * 4 + wave;
@@ -664,7 +645,10 @@ __global__ __launch_bounds__(256) void flat_merge_wave_kernel(
             B = x < B ? x : B;
         }
         if (!(B > fb)) {
-            if (lane == 0) flag_list[atomicAdd(overflow, 1u)] = (uint32_t)q;
+            if (lane == 0) {
+                fbv[q] = fb;
+                flag_list[atomicAdd(overflow, 1u)] = (uint32_t)q;
+            }
             return;
         }
     }
@@ -680,7 +664,10 @@ __global__ __launch_bounds__(256) void flat_merge_wave_kernel(
         cnt += (uint32_t)__popcll(mk);
     }
     if (cnt > FM_R) {  // more near-ties than the rescoring holds
-        if (lane == 0) flag_list[atomicAdd(overflow, 1u)] = (uint32_t)q;
+        if (lane == 0) {
+            fbv[q] = fb;
+            flag_list[atomicAdd(overflow, 1u)] = (uint32_t)q;
+        }
         return;
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -710,6 +697,40 @@ __global__ __launch_bounds__(256) void flat_merge_wave_kernel(
     wave_sort_regs<FM_R / 64>(r);
 #pragma unroll
     for (int e = 0; e < FM_R / 64; e++) emit(e * 64 + lane, r[e]);
+}
+
+// Database slices per query block: enough blocks to fill the GPU, slices of
+// at least 4 tiles, and splits * kk merge entries within the merge buffer.
+static int flat_splits(int nq, int n, int kk) {
+    int qb = (nq + FL_Q - 1) / FL_Q;
+    int sp = 1;
+    while (sp < FL_SPLITS_MAX && qb * sp < 2048 && 2 * sp * kk <= FL_BUF &&
+           (n + sp * 2 - 1) / (sp * 2) >= 4 * FL_N)
+        sp <<= 1;
+    return sp;
+}
+
+// The bf16x3 ranking kernel serves d <= 128 and k <= 32; it keeps
+// kk = k + 16 rounded up to 4 (at most the 64 keys a row's lanes hold) per
+// slice, plus one bound word per (query, slice) after the keys.
+static bool flat_rank_ok(int d, int k) { return d >= 1 && d <= 128 && k >= 1 && k <= 32; }
+static int flat_rank_keep(int k) { return (k + 16 + 3) & ~3; }
+
+// Slices for the ranking kernel: an even number of tiles each (stages are
+// tile pairs), enough workgroups for four waves of two per CU on 256 CUs,
+// slices of at least 64 tiles, and splits * kk merge entries within the
+// merge buffer; ib = the bits of a tile index within a slice.
+static int flat_rank_splits(int nq, int n, int kk, int* tps, int* ib) {
+    const int qb = (nq + FR_ROWS - 1) / FR_ROWS, ntiles = (n + 15) / 16;
+    int sp = 1;
+    while (qb * sp < 2048 && 2 * sp * kk <= FL_BUF && ntiles / (2 * sp) >= 64) sp <<= 1;
+    int t = (ntiles + sp - 1) / sp;
+    t += t & 1;
+    int b = 1;
+    while ((1 << b) < t) b++;
+    *tps = t;
+    *ib = b;
+    return (ntiles + t - 1) / t;
 }
 
 // Exhaustive exact fallback of the unproved queries, spread over the GPU:
@@ -751,11 +772,72 @@ __global__ __launch_bounds__(256) void flat_exact_finish_kernel(
     }
 }
 
+// Fallback of the ranking path, workgroup (s, i) for query q = flag_list[i]
+// and ranking slice s (tiles s tps ..): a slice whose bound exceeds the
+// query's rescoring threshold fb (fbv[q]) dropped no key <= fb, so its kept
+// keys <= fb are rescored; a slice whose bound does not is scanned
+// exhaustively with the exact arithmetic.  Either way the slice's k smallest
+// exact keys go to out_keys for flat_exact_finish_kernel: slices that could
+// not have hidden a result are not rescanned.
+__global__ __launch_bounds__(256) void flat_rank_fallback_kernel(
+    const uint32_t* __restrict__ flag_list, const uint32_t* __restrict__ fbv,
+    const uint64_t* __restrict__ partial, const uint32_t* __restrict__ pbound, int splits, int kk, int tps,
+    const float* __restrict__ Q, const float* __restrict__ X, int n, int d, int k, int metric,
+    uint64_t* __restrict__ out_keys) {
+    __shared__ uint64_t keys[FL_BUF];
+    __shared__ uint32_t pay[FL_BUF];
+    __shared__ uint32_t misc[4];
+    const int s = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
+    const uint32_t q = flag_list[i];
+    const uint32_t fb = fbv[q];
+    uint64_t* out = out_keys + ((size_t)i * splits + s) * k;
+    if (pbound[(size_t)q * splits + s] > fb) {
+        if (tid >= 64) return;  // kk <= 64 kept keys: one wave
+        const uint64_t* src = partial + ((size_t)q * splits + s) * kk;
+        uint64_t r[1] = {~0ull};
+        if (tid < kk) {
+            const uint64_t key = src[tid];
+            if (key != ~0ull && (uint32_t)(key >> 32) <= fb) {
+                const uint32_t idx = (uint32_t)key;
+                r[0] = cand_key(flat_exact(Q + (size_t)q * d, X + (size_t)idx * d, d, metric), idx);
+            }
+        }
+        wave_sort_regs<1>(r);
+        if (tid < k) out[tid] = r[0];
+        return;
+    }
+    const int j0 = s * tps * 16, j1 = min(n, (s + 1) * tps * 16);
+    const int m = j0 < j1 ? flat_exact_range(Q + (size_t)q * d, X, j0, j1, d, k, metric, keys, pay, misc) : 0;
+    for (int j = tid; j < k; j += blockDim.x) out[j] = j < m ? keys[j] : ~0ull;
+}
+
 int flat_fallback_slices(int n, int k) {
     int sl = FL_BUF / k;
     sl = sl > 256 ? 256 : sl;
     const int most = (n + 255) / 256;  // at least 256 vectors per slice
     return sl < most ? sl : (most > 0 ? most : 1);
+}
+
+void launch_flat_rank_fallback(const uint32_t* flag_list, int nflag, const uint32_t* fbv,
+                               const uint64_t* partial, int nq, int n, int d, int k, int metric,
+                               const float* Q, const float* X, uint64_t* keys, uint32_t* out_idx,
+                               float* out_dist, hipStream_t s) {
+    int tps, ib;
+    const int kk = flat_rank_keep(k), sp = flat_rank_splits(nq, n, kk, &tps, &ib);
+    const uint32_t* pbound = reinterpret_cast<const uint32_t*>(partial + (size_t)nq * sp * kk);
+    for (int f0 = 0; f0 < nflag; f0 += 65535) {  // grid.y limit
+        const int nf = nflag - f0 < 65535 ? nflag - f0 : 65535;
+        hipLaunchKernelGGL(flat_rank_fallback_kernel, dim3(sp, nf), dim3(256), 0, s, flag_list + f0, fbv, partial,
+                           pbound, sp, kk, tps, Q, X, n, d, k, metric, keys + (size_t)f0 * sp * k);
+        hipLaunchKernelGGL(flat_exact_finish_kernel, dim3(nf), dim3(256), 0, s, flag_list + f0, sp, k,
+                           keys + (size_t)f0 * sp * k, out_idx, out_dist);
+    }
+}
+
+int flat_rank_fallback_slices(int nq, int n, int d, int k) {
+    if (!flat_rank_ok(d, k)) return 0;
+    int tps, ib;
+    return flat_rank_splits(nq, n, flat_rank_keep(k), &tps, &ib);
 }
 
 void launch_flat_fallback(const uint32_t* flag_list, int nflag, const float* Q, const float* X, int n, int d,
@@ -771,39 +853,6 @@ void launch_flat_fallback(const uint32_t* flag_list, int nflag, const float* Q, 
     }
 }
 
-// Database slices per query block: enough blocks to fill the GPU, slices of
-// at least 4 tiles, and splits * kk merge entries within the merge buffer.
-static int flat_splits(int nq, int n, int kk) {
-    int qb = (nq + FL_Q - 1) / FL_Q;
-    int sp = 1;
-    while (sp < FL_SPLITS_MAX && qb * sp < 2048 && 2 * sp * kk <= FL_BUF &&
-           (n + sp * 2 - 1) / (sp * 2) >= 4 * FL_N)
-        sp <<= 1;
-    return sp;
-}
-
-// The bf16x3 ranking kernel serves d <= 128 and k <= 32; it keeps
-// kk = k + 16 rounded up to 4 (at most the 64 keys a row's lanes hold) per
-// slice, plus one bound word per (query, slice) after the keys.
-static bool flat_rank_ok(int d, int k) { return d >= 1 && d <= 128 && k >= 1 && k <= 32; }
-static int flat_rank_keep(int k) { return (k + 16 + 3) & ~3; }
-
-// Slices for the ranking kernel: an even number of tiles each (stages are
-// tile pairs), enough workgroups for four waves of two per CU on 256 CUs,
-// slices of at least 64 tiles, and splits * kk merge entries within the
-// merge buffer; ib = the bits of a tile index within a slice.
-static int flat_rank_splits(int nq, int n, int kk, int* tps, int* ib) {
-    const int qb = (nq + FR_ROWS - 1) / FR_ROWS, ntiles = (n + 15) / 16;
-    int sp = 1;
-    while (qb * sp < 2048 && 2 * sp * kk <= FL_BUF && ntiles / (2 * sp) >= 64) sp <<= 1;
-    int t = (ntiles + sp - 1) / sp;
-    t += t & 1;
-    int b = 1;
-    while ((1 << b) < t) b++;
-    *tps = t;
-    *ib = b;
-    return (ntiles + t - 1) / t;
-}
 
 size_t flat_partial_count(int nq, int n, int d, int k) {
     if (flat_rank_ok(d, k)) {
@@ -834,7 +883,8 @@ static void launch_rank(const float* Q, int nq, int d, const uint4* Xb, const fl
 void launch_flat_search(const float* Q, const float* Qsq, int nq, const float* X, const uint4* Xb,
                         const float* Xnorm, int n, int d, int k, int metric, float xmax,
                         uint64_t* partial, uint32_t* out_idx, float* out_dist,
-                        unsigned int* overflow, uint32_t* flag_list, hipStream_t s, hipEvent_t ranked) {
+                        unsigned int* overflow, uint32_t* flag_list, uint32_t* fbv, hipStream_t s,
+                        hipEvent_t ranked) {
     if (nq <= 0) return;
     if (Xb && flat_rank_ok(d, k)) {
         int tps, ib;
@@ -851,16 +901,16 @@ void launch_flat_search(const float* Q, const float* Qsq, int nq, const float* X
         const dim3 mg((nq + 3) / 4);
         if (tot <= 256)
             hipLaunchKernelGGL(flat_merge_wave_kernel<4>, mg, dim3(256), 0, s, partial, pbound, sp, kk, Q, Qsq, X,
-                               nq, d, k, metric, xmax, ib, out_idx, out_dist, overflow, flag_list);
+                               nq, d, k, metric, xmax, ib, out_idx, out_dist, overflow, flag_list, fbv);
         else if (tot <= 512)
             hipLaunchKernelGGL(flat_merge_wave_kernel<8>, mg, dim3(256), 0, s, partial, pbound, sp, kk, Q, Qsq, X,
-                               nq, d, k, metric, xmax, ib, out_idx, out_dist, overflow, flag_list);
+                               nq, d, k, metric, xmax, ib, out_idx, out_dist, overflow, flag_list, fbv);
         else if (tot <= 1024)
             hipLaunchKernelGGL(flat_merge_wave_kernel<16>, mg, dim3(256), 0, s, partial, pbound, sp, kk, Q, Qsq,
-                               X, nq, d, k, metric, xmax, ib, out_idx, out_dist, overflow, flag_list);
+                               X, nq, d, k, metric, xmax, ib, out_idx, out_dist, overflow, flag_list, fbv);
         else
             hipLaunchKernelGGL(flat_merge_wave_kernel<32>, mg, dim3(256), 0, s, partial, pbound, sp, kk, Q, Qsq,
-                               X, nq, d, k, metric, xmax, ib, out_idx, out_dist, overflow, flag_list);
+                               X, nq, d, k, metric, xmax, ib, out_idx, out_dist, overflow, flag_list, fbv);
         return;
     }
     const int kk = flat_keep(k), cap = flat_cap(kk), sp = flat_splits(nq, n, kk);

@@ -78,7 +78,9 @@ void launch_finalize(const uint32_t* vidx, const float* dist, const uint32_t* do
 }
 
 // End of a search chunk, FINISH_Q queries per workgroup: map insertion indices to
-// doc ids with (-1, +inf) padding (python.rs:778-785), add the statistics rows
+// doc ids with (-1, +inf) padding (python.rs:778-785; skipped when vidx is null:
+// the scan wrote the final rows, and each workgroup then takes the statistics
+// of 128 queries), add the statistics rows
 // into the counters (every FINISH_STATS-th workgroup adds 128 queries' rows,
 // one atomic per counter; counters sit COUNTER_STRIDE words apart), and clear
 // the two flag-list lengths for the next chunk (both lists were consumed by
@@ -93,12 +95,13 @@ __global__ __launch_bounds__(256) void finish_kernel(
     float* __restrict__ out_dists, const uint32_t* __restrict__ qstat,
     unsigned long long* __restrict__ counters, uint32_t* flag_count, uint32_t* cflag_count) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int q0 = blockIdx.x * FINISH_Q;
+    const bool map = vidx != nullptr;
+    const int q0 = blockIdx.x * (map ? FINISH_Q : FINISH_Q * FINISH_STATS);
     const int nqb = min(FINISH_Q, nq - q0);
     // wave w takes rows w, w + 4, ...; a lane takes columns lane, lane + 64, ...
     constexpr int U = 8;  // outputs per lane whose loads are in flight together
     constexpr int RW = FINISH_Q / (VGPU_BLOCK / 64);  // rows per wave
-    for (int c0 = 0; c0 < k; c0 += 64 * (U / RW)) {
+    for (int c0 = 0; map && c0 < k; c0 += 64 * (U / RW)) {
         uint32_t v[U], id[U];
         float dv[U];
 #pragma unroll
@@ -124,7 +127,7 @@ __global__ __launch_bounds__(256) void finish_kernel(
         }
     }
     // statistics: every FINISH_STATS-th workgroup adds 128 queries' rows
-    if (qstat && tid < 64 && blockIdx.x % FINISH_STATS == 0) {
+    if (qstat && tid < 64 && (!map || blockIdx.x % FINISH_STATS == 0)) {
         uint32_t c[NUM_SCAN_COUNTERS] = {0, 0, 0, 0, 0, 0};
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -160,7 +163,8 @@ void launch_finish(const uint32_t* vidx, const float* dist, const uint32_t* doc_
                    unsigned long long* counters, uint32_t* flag_count, uint32_t* cflag_count,
                    hipStream_t s) {
     if (nq <= 0) return;
-    hipLaunchKernelGGL(finish_kernel, dim3((nq + FINISH_Q - 1) / FINISH_Q), dim3(VGPU_BLOCK), 0, s, vidx,
+    const int per = vidx ? FINISH_Q : FINISH_Q * FINISH_STATS;
+    hipLaunchKernelGGL(finish_kernel, dim3((nq + per - 1) / per), dim3(VGPU_BLOCK), 0, s, vidx,
                        dist, doc_ids, nq, kin, k, out_ids, out_dists, qstat, counters, flag_count,
                        cflag_count);
 }

@@ -193,19 +193,9 @@ __device__ inline void load_query_and_lists(const DevIndex& ix, const ScanArgs& 
     }
 }
 
-// Write the first kout sorted entries (insertion index, distance), padding
-// with (0xffffffff, +inf).
+// Write the first kout sorted entries, padded (scan_emit).
 __device__ inline void write_out(const ScanArgs& a, ScanLds& s, int q, int n) {
-    for (int j = threadIdx.x; j < a.kout; j += blockDim.x) {
-        size_t o = (size_t)q * a.kout + j;
-        if (j < n) {
-            a.out_vidx[o] = (uint32_t)s.tk.keys[j];
-            a.out_dist[o] = key_dist(s.tk.keys[j]);
-        } else {
-            a.out_vidx[o] = 0xffffffffu;
-            a.out_dist[o] = __int_as_float(0x7f800000);
-        }
-    }
+    for (int j = threadIdx.x; j < a.kout; j += blockDim.x) scan_emit(a, q, j, s.tk.keys[j], j < n);
 }
 
 // Probed list l (slot p, entries beg .. beg + len - 1) with the reference
@@ -427,7 +417,8 @@ static void launch_mk(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
                                         : scan8_exact_kernel<MT, KT, 0>;
     ensure_dyn_lds((const void*)k, lds);
     // Flagged queries: a small grid walks the list the FAST kernel wrote.
-    const int grid = a.only_flagged ? (a.nq < 256 ? a.nq : 256) : a.nq;
+    // flagged queries are rare: a small grid keeps the usual empty launch cheap
+    const int grid = a.only_flagged ? (a.nq < 64 ? a.nq : 64) : a.nq;
     hipLaunchKernelGGL(k, dim3(grid), dim3(VGPU_BLOCK), lds, s, ix, a, buf);
 }
 

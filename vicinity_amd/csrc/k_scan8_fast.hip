@@ -41,6 +41,7 @@
 #include <hip/hip_ext.h>
 
 #include "vgpu_device.h"
+#include "vgpu_bounds.h"
 #include "vgpu_launch.h"
 
 namespace vgpu {
@@ -113,21 +114,6 @@ __device__ __forceinline__ float row_sum_generic(const uint8_t* __restrict__ p,
     }
     if (m < M) s0 += lut[m * K + p[m]];
     return s0 + s1;
-}
-
-// Bound on |a - e| for ||q|| <= qn, ||c|| <= cmax, ||x_r|| <= rmax and
-// ||q - c||^2 <= t0max (u = 2^-24).  With rr = sqrt(t0max) + rmax >= ||r - x_r||:
-//   |e - D| <= (ds + M) u rr^2 + 2u (||q - c|| rr + rr^2)     (reference arithmetic)
-//   |a - D| <= (d + M + ds + 4) u (t0max + rmax^2 + 2 (cmax + qn) rmax)
-// where D is the real-number distance; both are below
-// (d + M + ds + 8) u S with S = 2 (qn + cmax) rmax + 2 rmax^2 + 2 rr^2, which
-// is taken with a factor of 4 to spare.
-__device__ __forceinline__ float fast_tau(int d, int M, int ds, float qn, float cmax, float rmax,
-                                          float t0max) {
-    const float u = 5.9604645e-08f;
-    float rr = sqrtf(t0max) + rmax;
-    float S = 2.0f * (qn + cmax) * rmax + 2.0f * rmax * rmax + 2.0f * rr * rr;
-    return 4.0f * (float)(d + M + ds + 8) * u * S + 1e-30f;
 }
 
 struct FastLds {
@@ -1311,16 +1297,7 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
 rescored:
     if (n <= 256) {  // one wave sorts in registers; no block barriers below
         if (tid >= 64) return;
-        auto emit = [&](int j, uint64_t key) {
-            const size_t o = (size_t)q * kout + j;
-            if ((uint32_t)j < n) {
-                a.out_vidx[o] = (uint32_t)key;
-                a.out_dist[o] = key_dist(key);
-            } else {
-                a.out_vidx[o] = 0xffffffffu;
-                a.out_dist[o] = __int_as_float(0x7f800000);
-            }
-        };
+        auto emit = [&](int j, uint64_t key) { scan_emit(a, q, j, key, (uint32_t)j < n); };
         int done = 64;
         if (n <= 64) {
             uint64_t k1[1] = {(uint32_t)lane < n ? s.keys[lane] : ~0ull};
@@ -1351,16 +1328,7 @@ rescored:
     const int n2 = next_pow2((int)n);
     for (int t = (int)n + tid; t < n2; t += VGPU_BLOCK) s.keys[t] = ~0ull;
     block_bitonic_sort_keys(s.keys, n2);
-    for (int j = tid; j < kout; j += VGPU_BLOCK) {
-        const size_t o = (size_t)q * kout + j;
-        if ((uint32_t)j < n) {
-            a.out_vidx[o] = (uint32_t)s.keys[j];
-            a.out_dist[o] = key_dist(s.keys[j]);
-        } else {
-            a.out_vidx[o] = 0xffffffffu;
-            a.out_dist[o] = __int_as_float(0x7f800000);
-        }
-    }
+    for (int j = tid; j < kout; j += VGPU_BLOCK) scan_emit(a, q, j, s.keys[j], (uint32_t)j < n);
 }
 
 bool scan8_fast_blocks_supported(int M, int K, int ds) {

@@ -8,6 +8,7 @@
 #include <shared_mutex>
 #include <string>
 
+#include "vgpu_bounds.h"
 #include "vgpu_runtime.h"
 
 using vgpu::Error;
@@ -538,6 +539,34 @@ int vgpu_test_polar_factor(const float* m, size_t d, float* r) {
         need(m && r && d, VGPU_ERR_INVALID_PARAMETER, "bad argument");
         vgpu::polar_factor(m, d, r);
     });
+}
+
+int vgpu_test_bound_fast_tau(size_t d, size_t M, size_t ds, float qn, float cmax, float rmax,
+                             float t0max, float* out) {
+    return guard([&] {
+        need(out && d && M && ds, VGPU_ERR_INVALID_PARAMETER, "bad argument");
+        *out = vgpu::fast_tau((int)d, (int)M, (int)ds, qn, cmax, rmax, t0max);
+    });
+}
+
+int vgpu_test_bound_coarse(size_t d, float qn, float cmax, float* out_bf16x3, float* out_fp32) {
+    return guard([&] {
+        need(out_bf16x3 && out_fp32 && d, VGPU_ERR_INVALID_PARAMETER, "bad argument");
+        *out_bf16x3 = vgpu::coarse_eps_bf16((int)d, qn, cmax);
+        *out_fp32 = vgpu::coarse_tau((int)d, qn, cmax);
+    });
+}
+
+int vgpu_test_bound_flat(size_t d, int metric, float qn, float xn, int ib, float* out) {
+    return guard([&] {
+        need(out && d && (metric == 0 || metric == 1) && ib >= 0 && ib < 24,
+             VGPU_ERR_INVALID_PARAMETER, "bad argument");
+        *out = vgpu::flat_bf16_tau((int)d, metric, qn, xn, ib);
+    });
+}
+
+int vgpu_test_fail_device_allocations(size_t after, size_t count) {
+    return guard([&] { vgpu::arm_alloc_failures((long long)after, (long long)count); });
 }
 
 int vgpu_test_set_rres_limit(vgpu_ivfpq* h, size_t floats) {

@@ -25,6 +25,8 @@ FlatIndex::~FlatIndex() {
 
 void FlatIndex::add(const float* x, size_t count) {
     if (n + count >= 0xffffffffull) throw Error(VGPU_ERR_INVALID_PARAMETER, "more than 2^32-1 vectors");
+    const size_t n0 = n;
+    const double xmax0 = xmax2;
     host.insert(host.end(), x, x + count * d);
     for (size_t i = 0; i < count; i++) {
         double t = 0.0;
@@ -32,20 +34,44 @@ void FlatIndex::add(const float* x, size_t count) {
         xmax2 = std::max(xmax2, t);
     }
     n += count;
-    d_x.upload(host.data(), n * d, stream);
-    d_xnorm.reserve(n);
-    launch_flat_norms(d_x.p, (int)n, (int)d, d_xnorm.p, stream);
-    if (flat_pack_chunks((int)n, (int)d)) {
-        d_xb.reserve(flat_pack_chunks((int)n, (int)d));
-        launch_flat_pack(d_x.p, (int)n, (int)d, d_xb.p, stream);
+    try {
+        sync_device();
+    } catch (...) {
+        // A failed allocation has released the buffer it was growing: go
+        // back to the previous rows and rebuild their device copy.
+        host.resize(n0 * d);
+        n = n0;
+        xmax2 = xmax0;
+        try {
+            sync_device();
+        } catch (...) {
+            stale = true;
+        }
+        throw;
     }
-    VGPU_HIP(hipGetLastError());
-    VGPU_HIP(hipStreamSynchronize(stream));
+}
+
+void FlatIndex::sync_device() {
+    stale = true;
+    if (n) {
+        d_x.upload(host.data(), n * d, stream);
+        d_xnorm.reserve(n);
+        launch_flat_norms(d_x.p, (int)n, (int)d, d_xnorm.p, stream);
+        if (flat_pack_chunks((int)n, (int)d)) {
+            d_xb.reserve(flat_pack_chunks((int)n, (int)d));
+            launch_flat_pack(d_x.p, (int)n, (int)d, d_xb.p, stream);
+        }
+        VGPU_HIP(hipGetLastError());
+        VGPU_HIP(hipStreamSynchronize(stream));
+    }
+    stale = false;
 }
 
 void FlatIndex::search_device(const float* d_q, size_t nq, size_t k, int64_t* d_ids, float* d_dists,
                               hipStream_t s) {
     if (!s) s = stream;
+    if (stale)
+        throw Error(VGPU_ERR_DEVICE, "the device copy of the flat index was lost in a failed add; add again");
     if (nq == 0 || k == 0) return;
     if (k > 112) throw Error(VGPU_ERR_INVALID_PARAMETER, "flat search supports k <= 112");
     if (n == 0) {
@@ -60,18 +86,27 @@ void FlatIndex::search_device(const float* d_q, size_t nq, size_t k, int64_t* d_
     w_dist.reserve(nq * k);
     w_overflow.reserve(1);
     w_flag.reserve(nq);
+    w_fb.reserve(nq);
     VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
     launch_flat_norms(d_q, (int)nq, (int)d, w_qnorm.p, s);
     VGPU_HIP(hipEventRecord(ev[0], s));
     launch_flat_search(d_q, w_qnorm.p, (int)nq, d_x.p, d_xb.n ? d_xb.p : nullptr, d_xnorm.p, (int)n, (int)d,
-                       (int)k, metric, xmax, w_partial.p, w_idx.p, w_dist.p, w_overflow.p, w_flag.p, s, ev[3]);
-    // the unproved queries (rare): exhaustive exact scan over many workgroups
+                       (int)k, metric, xmax, w_partial.p, w_idx.p, w_dist.p, w_overflow.p, w_flag.p, w_fb.p, s,
+                       ev[3]);
+    // the unproved queries (rare): exact scans over many workgroups
     VGPU_HIP(hipMemcpyAsync(&fallbacks, w_overflow.p, sizeof(unsigned int), hipMemcpyDeviceToHost, s));
     VGPU_HIP(hipStreamSynchronize(s));
     if (fallbacks) {
-        w_fbkeys.reserve((size_t)fallbacks * flat_fallback_slices((int)n, (int)k) * k);
-        launch_flat_fallback(w_flag.p, (int)fallbacks, d_q, d_x.p, (int)n, (int)d, (int)k, metric, w_fbkeys.p,
-                             w_idx.p, w_dist.p, s);
+        const int rsl = d_xb.n ? flat_rank_fallback_slices((int)nq, (int)n, (int)d, (int)k) : 0;
+        if (rsl) {
+            w_fbkeys.reserve((size_t)fallbacks * rsl * k);
+            launch_flat_rank_fallback(w_flag.p, (int)fallbacks, w_fb.p, w_partial.p, (int)nq, (int)n, (int)d,
+                                      (int)k, metric, d_q, d_x.p, w_fbkeys.p, w_idx.p, w_dist.p, s);
+        } else {
+            w_fbkeys.reserve((size_t)fallbacks * flat_fallback_slices((int)n, (int)k) * k);
+            launch_flat_fallback(w_flag.p, (int)fallbacks, d_q, d_x.p, (int)n, (int)d, (int)k, metric,
+                                 w_fbkeys.p, w_idx.p, w_dist.p, s);
+        }
     }
     VGPU_HIP(hipEventRecord(ev[1], s));
     launch_finalize(w_idx.p, w_dist.p, nullptr, (int)nq, (int)k, (int)k, d_ids, d_dists, s);

@@ -6,6 +6,7 @@
 // search :1087-1093, search_reranked :1117-1158, search_approx_internal_observed
 // :1175-1391; batch shape src/python.rs:744-793.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
 #include <numeric>
@@ -34,6 +35,27 @@ void hip_check(hipError_t e, const char* what) {
     int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? VGPU_ERR_OUT_OF_MEMORY
                                                                            : VGPU_ERR_DEVICE;
     throw Error(code, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+namespace {
+std::atomic<long long> g_fail_after{0}, g_fail_count{0};
+}
+
+void arm_alloc_failures(long long after, long long count) {
+    g_fail_count.store(0);
+    g_fail_after.store(after < 0 ? 0 : after);
+    g_fail_count.store(count < 0 ? 0 : count);
+}
+
+bool alloc_should_fail() {
+    if (g_fail_count.load(std::memory_order_relaxed) <= 0) return false;
+    long long a = g_fail_after.load();
+    while (a > 0)
+        if (g_fail_after.compare_exchange_weak(a, a - 1)) return false;
+    long long c = g_fail_count.load();
+    while (c > 0)
+        if (g_fail_count.compare_exchange_weak(c, c - 1)) return true;
+    return false;
 }
 
 // splitmix64 (Steele, Lea, Flood 2014): the seeded stream of the training
@@ -782,6 +804,11 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
         a.flag_count = flag_count;
         a.out_vidx = w.vidx;
         a.out_dist = w.dist;
+        if (!pl.pool) {  // no rerank: the scan kernels write the final rows
+            a.out_ids = d_ids + q0 * k;
+            a.out_dists = d_dists + q0 * k;
+            a.doc_ids = d_doc_ids.p;
+        }
         a.rres = pl.opq ? w.rres : nullptr;
         if (K == 16) {
             a.kk = (int)kout;
@@ -805,8 +832,8 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
             if (scanp) VGPU_HIP(hipEventRecord(ws->sev[2 * ci + 1], s));
         }
         if (allp) VGPU_HIP(hipEventRecord(ev[5], s));
-        const uint32_t* vout = w.vidx;
-        const float* dout = w.dist;
+        const uint32_t* vout = nullptr;  // rows already final
+        const float* dout = nullptr;
         size_t kin = kout;
         if (pl.pool) {
             launch_rerank(dix, w.qn, (int)nc, w.vidx, (int)kout, (int)k, w.vidx2, w.dist2, s);

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "vgpu_device.h"
+
 namespace vgpu {
 
 // Raise a kernel's dynamic-LDS limit to at least `bytes`; the attribute is set
@@ -51,6 +53,11 @@ struct ScanArgs {
     uint32_t* flag_count = nullptr; // entries of flag_list (zeroed by launch_finish)
     uint32_t* out_vidx = nullptr;   // [nq*kout] insertion indices, 0xffffffff padding
     float* out_dist = nullptr;      // [nq*kout]
+    // Final rows instead (no rerank, kout = k): doc ids (insertion indices
+    // when doc_ids is null) with (-1, +inf) padding, python.rs:778-785.
+    int64_t* out_ids = nullptr;     // [nq*kout]
+    float* out_dists = nullptr;     // [nq*kout]
+    const uint32_t* doc_ids = nullptr;
     // Per-query statistics, one row of QSTAT_WORDS per query, written with plain
     // stores (no global atomics): [0] list entries scanned, [1] FAST flushes,
     // [2] FAST appends, [3] bit 0: FAST could not prove the query (rerun by the
@@ -62,6 +69,22 @@ struct ScanArgs {
     // FastScan kernels only.
     const float* rres = nullptr;
 };
+
+// Writes result j of query q from a (distance, insertion index) key, or
+// padding when !valid: the final (doc id, distance) row when a.out_ids is set,
+// else the (insertion index, distance) row for a later rerank.
+__device__ __forceinline__ void scan_emit(const ScanArgs& a, int q, int j, uint64_t key, bool valid) {
+    const size_t o = (size_t)q * a.kout + j;
+    const uint32_t v = (uint32_t)key;
+    const float dist = valid ? key_dist(key) : __int_as_float(0x7f800000);
+    if (a.out_ids) {
+        a.out_ids[o] = valid ? (int64_t)(a.doc_ids ? a.doc_ids[v] : v) : (int64_t)-1;
+        a.out_dists[o] = dist;
+    } else {
+        a.out_vidx[o] = valid ? v : 0xffffffffu;
+        a.out_dist[o] = dist;
+    }
+}
 
 void launch_normalize(const float* x, float* out, float* norms, int n, int d, hipStream_t s);
 void launch_coarse_dots(const float* Q, const float* C, float* D, int nq, int L, int d,
@@ -197,8 +220,18 @@ void launch_flat_pack(const float* X, int n, int d, uint4* Xb, hipStream_t s);
 void launch_flat_search(const float* Q, const float* Qsq, int nq, const float* X, const uint4* Xb,
                         const float* Xnorm, int n, int d, int k, int metric, float xmax,
                         uint64_t* partial, uint32_t* out_idx, float* out_dist,
-                        unsigned int* overflow, uint32_t* flag_list, hipStream_t s,
+                        unsigned int* overflow, uint32_t* flag_list, uint32_t* fbv, hipStream_t s,
                         hipEvent_t ranked = nullptr);
+// The bf16x3 ranking path's fallback for the nflag queries of flag_list
+// (fbv: their rescoring thresholds, written by the merge): only the slices
+// whose bound does not clear the threshold are scanned exhaustively.  keys:
+// scratch of nflag * flat_rank_fallback_slices(...) * k entries; 0 slices =
+// the ranking path is not used for this shape.
+int flat_rank_fallback_slices(int nq, int n, int d, int k);
+void launch_flat_rank_fallback(const uint32_t* flag_list, int nflag, const uint32_t* fbv,
+                               const uint64_t* partial, int nq, int n, int d, int k, int metric,
+                               const float* Q, const float* X, uint64_t* keys, uint32_t* out_idx,
+                               float* out_dist, hipStream_t s);
 // Exhaustive exact top-k rows of the nflag queries of flag_list;
 // keys: scratch of nflag * flat_fallback_slices(n, k) * k entries.
 int flat_fallback_slices(int n, int k);

@@ -27,6 +27,12 @@ struct Error : std::runtime_error {
 void hip_check(hipError_t e, const char* what);
 #define VGPU_HIP(expr) ::vgpu::hip_check((expr), #expr)
 
+// Device-allocation failure injection, a test hook: once armed with
+// (after, count), the next `after` DevBuf allocations go through and the
+// `count` after them fail as out-of-memory without calling hipMalloc.
+void arm_alloc_failures(long long after, long long count);
+bool alloc_should_fail();
+
 template <typename T>
 struct DevBuf {
     T* p = nullptr;
@@ -45,6 +51,9 @@ struct DevBuf {
         if (count <= n && p) return;
         release();
         size_t bytes = (count ? count : 1) * sizeof(T);
+        if (alloc_should_fail())
+            throw Error(VGPU_ERR_OUT_OF_MEMORY,
+                        "device allocation of " + std::to_string(bytes) + " bytes failed (injected)");
         hipError_t e = hipMalloc((void**)&p, bytes);
         if (e != hipSuccess) {
             p = nullptr;
@@ -249,18 +258,21 @@ struct FlatIndex {
     DevBuf<float> d_x, d_xnorm, w_q, w_dist, w_odist, w_qnorm;
     DevBuf<uint4> d_xb;  // bf16 hi/lo copy for the ranking kernel (d <= 128)
     DevBuf<uint64_t> w_partial, w_fbkeys;
-    DevBuf<uint32_t> w_idx, w_flag;
+    DevBuf<uint32_t> w_idx, w_flag, w_fb;
     DevBuf<int64_t> w_ids;
     DevBuf<unsigned int> w_overflow;
     std::vector<float> host;
     double xmax2 = 0.0;  // max ||x||^2
     float ms_gemm = 0.f, ms_total = 0.f;
     unsigned int fallbacks = 0;  // queries of the last search that took the exhaustive exact scan
+    bool stale = false;  // a failed add could not restore the device copy of the n rows
     std::mutex mu;
 
     FlatIndex(size_t dim, int met);
     ~FlatIndex();
+    // Appends count rows; on failure the index keeps its previous n rows.
     void add(const float* x, size_t count);
+    void sync_device();  // device copy, norms and bf16 pack of host rows 0..n
     void search_device(const float* d_q, size_t nq, size_t k, int64_t* d_ids, float* d_dists,
                        hipStream_t s);
 };
