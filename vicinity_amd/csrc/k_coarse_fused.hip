@@ -3,7 +3,7 @@
 //   coarse_fused_kernel  32 queries per workgroup.  Normalises its queries
 //       (search.rs:55-62, writes qn), then makes one pass of bf16x3 MFMA dot
 //       products against every centroid: q.c ~ qh.ch + qh.cl + ql.ch with
-//       x = xh + xl + O(2^-18 |x|) split into bfloat16 halves.  Each (lane, query)
+//       x = xh + xl + O(2^-16 |x|) split into bfloat16 halves.  Each (lane, query)
 //       keeps the J largest products of the lane's column class, packed with
 //       their list index into one float key; two waves share a query block and
 //       merge their lists.  The keys above a threshold derived from the P-th
@@ -46,7 +46,8 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
     return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
-// x = hi + lo + r with |r| <= 2^-18 |x|; returns (hi, lo) bit patterns.
+// x = hi + lo + r with |r| <= 2^-16 |x| (each rounding to bfloat16 is within
+// 2^-8 relative); returns (hi, lo) bit patterns.
 __device__ __forceinline__ void bf16_split(float x, uint32_t& hi, uint32_t& lo) {
     hi = bf16_bits(x);
     const float rem = x - __uint_as_float(hi << 16);  // exact (Sterbenz)
