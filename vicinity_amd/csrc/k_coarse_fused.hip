@@ -21,6 +21,7 @@
 // the same dimension-to-(group, slot) assignment, so every dimension is
 // summed exactly once.
 #include "vgpu_device.h"
+#include "vgpu_bounds.h"
 #include "vgpu_launch.h"
 
 namespace vgpu {
@@ -52,18 +53,6 @@ __device__ __forceinline__ void bf16_split(float x, uint32_t& hi, uint32_t& lo) 
     hi = bf16_bits(x);
     const float rem = x - __uint_as_float(hi << 16);  // exact (Sterbenz)
     lo = bf16_bits(rem);
-}
-
-// Error bound eps of the bf16x3 score against the reference's sequential one
-// for ||q|| <= qn, ||c|| <= cmax (u = 2^-24): the dropped terms (ql.cl and the
-// split remainders) are within 3.01 * 2^-18 sum|q_j c_j|, the fp32
-// accumulation of 3d exact products within 3d 2u (accumulation that
-// truncates), the sequential dot within d u, and 1 - dot rounds within
-// 2u (1 + qn cmax).
-__device__ __forceinline__ float coarse_eps_bf16(int d, float qn, float cmax) {
-    const float u = 5.9604645e-08f;
-    const float qc = qn * cmax;
-    return (3.01f * 3.8146973e-06f + 7.0f * (float)d * u) * qc + 2.0f * u * (1.0f + qc) + 1e-30f;
 }
 
 // Pack centroids into bf16 hi/lo chunks in the order the MFMA tiles read them
