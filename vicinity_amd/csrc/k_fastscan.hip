@@ -32,13 +32,16 @@ __device__ __forceinline__ uint32_t round_to_u8(float v) {
 }
 
 // Four byte lookups: sel holds four indices 0..15 (one per byte) into the
-// 16-byte table t0..t3.
+// 16-byte table t0..t3.  The byte mask of the indices >= 8 comes from
+// v_perm_b32's sign-replicating selectors (8..11 give 0xff when bit 15, 31,
+// 47 or 63 of the source pair is set): sel << 4 puts bit 3 of bytes 1 and 3
+// at bits 15 and 31, sel << 12 bit 3 of bytes 0 and 2 at bits 47 and 63.
 __device__ __forceinline__ uint32_t lookup16(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3,
                                              uint32_t sel) {
     uint32_t i7 = sel & 0x07070707u;
     uint32_t lo = __builtin_amdgcn_perm(t1, t0, i7);  // entries 0..7
     uint32_t hi = __builtin_amdgcn_perm(t3, t2, i7);  // entries 8..15
-    uint32_t m = ((sel >> 3) & 0x01010101u) * 0xffu;
+    uint32_t m = __builtin_amdgcn_perm(sel << 12, sel << 4, 0x090b080au);
     return (hi & m) | (lo & ~m);
 }
 
@@ -263,11 +266,20 @@ __global__ __launch_bounds__(256) void fastscan_kernel(DevIndex ix, ScanArgs a, 
             uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
             if (b < nb) {
                 const uint32_t* src = (const uint32_t*)(blocks + (size_t)b * 16 * M) + w;
-                for (int m = 0; m < M; m++) {
-                    uint32_t x = src[m * 4];
-                    fs_accumulate(x, qw[m * 4], qw[m * 4 + 1], qw[m * 4 + 2], qw[m * 4 + 3], a0, a1,
-                                  a2, a3);
+                // eight codebooks' code words in flight at a time
+                int m = 0;
+                for (; m + 8 <= M; m += 8) {
+                    uint32_t x[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) x[u] = src[(m + u) * 4];
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+                        fs_accumulate(x[u], qw[(m + u) * 4], qw[(m + u) * 4 + 1], qw[(m + u) * 4 + 2],
+                                      qw[(m + u) * 4 + 3], a0, a1, a2, a3);
                 }
+                for (; m < M; m++)
+                    fs_accumulate(src[m * 4], qw[m * 4], qw[m * 4 + 1], qw[m * 4 + 2], qw[m * 4 + 3], a0, a1,
+                                  a2, a3);
             }
 #pragma unroll
             for (int cc = 0; cc < 8; cc++) {
