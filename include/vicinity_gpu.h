@@ -216,6 +216,39 @@ int vgpu_ivfpq_export(const vgpu_ivfpq *h, float *centroids, float *codebooks,
                       uint64_t *list_offsets, uint32_t *list_ids, uint8_t *codes,
                       uint32_t *doc_ids, float *vectors);
 
+/* ---- file-backed search: IVFPQFileSearcher (src/ivf_pq/search.rs:247-282,
+ * :1620-2041) --------------------------------------------------------------
+ * The routing metadata in memory (what load_from_parts, search.rs:1679-1762,
+ * parses from the snapshot: centroids, codebooks, the clusters as
+ * list_offsets/list_ids, doc ids, the OPQ rotation or NULL); the PQ codes
+ * (list_codes.bin + list_offsets.bin, else codes.bin) and raw_vectors.bin
+ * stay in the snapshot directory `dir` and are read per search call.  A
+ * call probes with the full index's centroids, reads the codes of the union
+ * of the probed lists into HBM and scans them there; a reranked call reads
+ * the raw vectors of the approximate candidates only.  Results equal the
+ * in-memory index's on the same snapshot.  One call at a time per handle. */
+typedef struct vgpu_ivfpq_file vgpu_ivfpq_file;
+/* IVFPQFileSearchDiagnostics (search.rs:263-282), per query. */
+typedef struct vgpu_file_diagnostics {
+    uint64_t probed_lists, scanned_vectors, code_reads, code_bytes, retained_candidates,
+        raw_vector_reads, raw_vector_bytes, reranked_candidates;
+} vgpu_file_diagnostics;
+int vgpu_ivfpq_file_open(size_t dimension, const vgpu_ivfpq_params *params, const float *centroids,
+                         size_t num_centroids, const float *codebooks, size_t codebook_size,
+                         const uint64_t *list_offsets, const uint32_t *list_ids,
+                         const uint32_t *doc_ids, size_t num_vectors, const float *rotation,
+                         const char *dir, int raw_vectors_present, vgpu_ivfpq_file **out);
+void vgpu_ivfpq_file_free(vgpu_ivfpq_file *h);
+int vgpu_ivfpq_file_set_nprobe(vgpu_ivfpq_file *h, size_t nprobe); /* search.rs:1765-1768 */
+/* search / search_reranked / batch of them (search.rs:1800-1891): nprobe 0 =
+ * the searcher's, rerank_pool 0 = no rerank; rows padded with (-1, +inf);
+ * diag (NULL allowed) receives nq rows. */
+int vgpu_ivfpq_file_search_batch(vgpu_ivfpq_file *h, const float *queries, size_t nq, size_t dim,
+                                 size_t k, size_t nprobe, size_t rerank_pool, int64_t *out_ids,
+                                 float *out_dists, vgpu_file_diagnostics *diag);
+/* File reads of the last search call (positional reads and bytes). */
+int vgpu_ivfpq_file_last_io(const vgpu_ivfpq_file *h, uint64_t *reads, uint64_t *bytes);
+
 /* ---- flat exact search (src/distance.rs:78-109) ---------------------------
  * metric 0: squared L2 ||q||^2 - 2 q.x + ||x||^2 ranking, distances rescored
  * with l2_distance_squared; metric 1: 1 - q.x (cosine_distance_normalized). */
@@ -232,8 +265,9 @@ int vgpu_flat_search_batch_device(vgpu_flat *h, const float *d_queries, size_t n
  * merge, exact rescoring, fallback and output. */
 int vgpu_flat_last_ms(const vgpu_flat *h, float *ms_gemm, float *ms_total);
 /* Queries of the last flat search whose kept candidates could not be proved
- * to hold the exact top-k, and which were answered by an exhaustive exact
- * scan instead (their results are exact either way). */
+ * to hold the exact top-k; the database slices that could hide a result were
+ * then scanned exhaustively with the exact arithmetic (their results are
+ * exact either way). */
 int vgpu_flat_last_fallbacks(const vgpu_flat *h, uint32_t *queries);
 
 /* ---- per-kernel test entry points (host buffers) -------------------------- */

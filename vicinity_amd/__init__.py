@@ -6,12 +6,14 @@ include/vicinity_gpu.h (libvicinity_gpu.so, built by vicinity_amd/csrc).
 
 from ._lib import LIB_PATH, VicinityGpuError, device_available
 from .filtering import MetadataFilter
+from .file_searcher import IVFPQFileSearcher
 from .flat import FlatIndex
 from . import datagen
 from .ivf_pq import MISSING_DISTANCE, MISSING_LABEL, IVFPQIndex, default_codebooks
 
 __all__ = [
     "IVFPQIndex",
+    "IVFPQFileSearcher",
     "FlatIndex",
     "MetadataFilter",
     "MISSING_LABEL",

@@ -52,6 +52,16 @@ class Info(ctypes.Structure):
                 ("has_vectors", ctypes.c_int), ("mode", ctypes.c_int)]
 
 
+class FileDiagnostics(ctypes.Structure):
+    """IVFPQFileSearchDiagnostics (search.rs:263-282)."""
+    _fields_ = [(name, ctypes.c_uint64) for name in (
+        "probed_lists", "scanned_vectors", "code_reads", "code_bytes", "retained_candidates",
+        "raw_vector_reads", "raw_vector_bytes", "reranked_candidates")]
+
+    def as_dict(self) -> dict:
+        return {name: int(getattr(self, name)) for name, _ in self._fields_}
+
+
 class Stats(ctypes.Structure):
     _fields_ = [("ms_normalize", ctypes.c_float), ("ms_coarse", ctypes.c_float),
                 ("ms_select", ctypes.c_float), ("ms_scan", ctypes.c_float),
@@ -105,6 +115,12 @@ SIGNATURES = {
     "vgpu_ivfpq_set_rotation": (_i, [_H, _vp, _sz]),
     "vgpu_ivfpq_probe_batch": (_i, [_H, _vp, _sz, _sz, _sz, _vp, ctypes.POINTER(_sz)]),
     "vgpu_ivfpq_export": (_i, [_H, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "vgpu_ivfpq_file_open": (_i, [_sz, ctypes.POINTER(Params), _vp, _sz, _vp, _sz, _vp, _vp, _vp, _sz, _vp,
+                                  ctypes.c_char_p, _i, ctypes.POINTER(_H)]),
+    "vgpu_ivfpq_file_free": (None, [_H]),
+    "vgpu_ivfpq_file_set_nprobe": (_i, [_H, _sz]),
+    "vgpu_ivfpq_file_search_batch": (_i, [_H, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _vp]),
+    "vgpu_ivfpq_file_last_io": (_i, [_H, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
     "vgpu_flat_new": (_i, [_sz, _i, ctypes.POINTER(_H)]),
     "vgpu_flat_free": (None, [_H]),
     "vgpu_flat_add": (_i, [_H, _vp, _sz]),

@@ -53,6 +53,13 @@ void launch_rerank(const DevIndex& ix, const float* qn, int nq, const uint32_t* 
                        pool, k, out_vidx, out_dist);
 }
 
+void launch_rerank_vectors(const float* vectors, int d, const float* qn, int nq, const uint32_t* pool_rows,
+                           int pool, int k, uint32_t* out_rows, float* out_dist, hipStream_t s) {
+    if (nq <= 0) return;
+    hipLaunchKernelGGL(rerank_kernel, dim3(nq), dim3(256), 0, s, vectors, d, qn, nq, pool_rows, pool, k,
+                       out_rows, out_dist);
+}
+
 __global__ void finalize_kernel(const uint32_t* __restrict__ vidx, const float* __restrict__ dist,
                                 const uint32_t* __restrict__ doc_ids, int nq, int kin, int k,
                                 int64_t* __restrict__ out_ids, float* __restrict__ out_dists) {

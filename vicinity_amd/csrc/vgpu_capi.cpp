@@ -541,6 +541,68 @@ int vgpu_test_polar_factor(const float* m, size_t d, float* r) {
     });
 }
 
+struct vgpu_ivfpq_file {
+    vgpu::FileIvfpq* fx;
+};
+
+int vgpu_ivfpq_file_open(size_t dimension, const vgpu_ivfpq_params* params, const float* centroids,
+                         size_t num_centroids, const float* codebooks, size_t codebook_size,
+                         const uint64_t* list_offsets, const uint32_t* list_ids, const uint32_t* doc_ids,
+                         size_t num_vectors, const float* rotation, const char* dir, int raw_vectors_present,
+                         vgpu_ivfpq_file** out) {
+    return guard([&] {
+        need(params && centroids && codebooks && list_offsets && dir && out, VGPU_ERR_INVALID_PARAMETER,
+             "null argument");
+        *out = nullptr;
+        auto* h = new vgpu_ivfpq_file{nullptr};
+        try {
+            h->fx = new vgpu::FileIvfpq(dimension, *params, centroids, num_centroids, codebooks, codebook_size,
+                                        list_offsets, list_ids, doc_ids, num_vectors, rotation, dir,
+                                        raw_vectors_present != 0);
+        } catch (...) {
+            delete h;
+            throw;
+        }
+        *out = h;
+    });
+}
+
+void vgpu_ivfpq_file_free(vgpu_ivfpq_file* h) {
+    if (!h) return;
+    delete h->fx;
+    delete h;
+}
+
+int vgpu_ivfpq_file_set_nprobe(vgpu_ivfpq_file* h, size_t nprobe) {
+    return guard([&] {
+        need(h, VGPU_ERR_INVALID_PARAMETER, "null handle");
+        std::lock_guard<std::mutex> lk(h->fx->mu);
+        h->fx->params.nprobe = nprobe;
+    });
+}
+
+int vgpu_ivfpq_file_search_batch(vgpu_ivfpq_file* h, const float* queries, size_t nq, size_t dim, size_t k,
+                                 size_t nprobe, size_t rerank_pool, int64_t* out_ids, float* out_dists,
+                                 vgpu_file_diagnostics* diag) {
+    return guard([&] {
+        need(h && (nq == 0 || queries) && (nq * k == 0 || (out_ids && out_dists)), VGPU_ERR_INVALID_PARAMETER,
+             "null argument");
+        std::lock_guard<std::mutex> lk(h->fx->mu);
+        need(dim == h->fx->d, VGPU_ERR_DIMENSION_MISMATCH, "query dimension does not match the index");
+        need(k <= 2048 && rerank_pool <= 2048, VGPU_ERR_INVALID_PARAMETER, "k / rerank_pool above 2048 is not supported");
+        h->fx->search(queries, nq, k, nprobe, rerank_pool, out_ids, out_dists, diag);
+    });
+}
+
+int vgpu_ivfpq_file_last_io(const vgpu_ivfpq_file* h, uint64_t* reads, uint64_t* bytes) {
+    return guard([&] {
+        need(h && reads && bytes, VGPU_ERR_INVALID_PARAMETER, "null argument");
+        std::lock_guard<std::mutex> lk(h->fx->mu);
+        *reads = h->fx->io_reads;
+        *bytes = h->fx->io_bytes;
+    });
+}
+
 int vgpu_test_bound_fast_tau(size_t d, size_t M, size_t ds, float qn, float cmax, float rmax,
                              float t0max, float* out) {
     return guard([&] {

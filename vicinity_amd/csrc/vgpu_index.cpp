@@ -752,7 +752,7 @@ void IvfpqIndex::coarse_probe(const float* d_q, size_t nq, size_t P, const Searc
 
 void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, const WsPtrs& w,
                             int64_t* d_ids, float* d_dists, hipStream_t s, SearchWs* ws,
-                            vgpu_search_stats* st) {
+                            vgpu_search_stats* st, const uint32_t* d_given) {
     const size_t P = pl.P, k = pl.k, kout = pl.kout, chunk = pl.chunk;
     unsigned long long* counters = w.scal;
     uint32_t* flag_count = reinterpret_cast<uint32_t*>(w.scal + kFlagWord);
@@ -783,10 +783,17 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
         // normalise + bf16x3 MFMA pass or score GEMM (ms_coarse), exact top-P
         // of the candidates and the rare exact fallback (ms_select)
         if (allp) VGPU_HIP(hipEventRecord(ev[1], s));
-        coarse_probe(d_q + q0 * d, nc, P, pl, w, s, allp ? ev[2] : nullptr);
+        const uint32_t* probe = w.probe;
+        if (d_given) {
+            launch_normalize(d_q + q0 * d, w.qn, w.qnorm, (int)nc, (int)d, s);
+            if (allp) VGPU_HIP(hipEventRecord(ev[2], s));
+            probe = d_given + q0 * P;
+        } else {
+            coarse_probe(d_q + q0 * d, nc, P, pl, w, s, allp ? ev[2] : nullptr);
+        }
         // OPQ: the rotated residual of every (query, probe) slot (opq.rs:120-123),
         // timed with the selection
-        if (pl.opq) rotate_slots(w.qn, nc, P, w.probe, w.rres, s);
+        if (pl.opq) rotate_slots(w.qn, nc, P, probe, w.rres, s);
         if (allp) VGPU_HIP(hipEventRecord(ev[3], s));
         // scan-only timing: the FAST kernel's dispatch records the two events
         // itself; the other scan kernels are bracketed by marker events
@@ -795,7 +802,7 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
         ScanArgs a;
         a.qn = w.qn;
         a.qnorm = w.qnorm;
-        a.probe = w.probe;
+        a.probe = probe;
         a.nq = (int)nc;
         a.P = (int)P;
         a.kout = (int)kout;
@@ -960,6 +967,34 @@ void IvfpqIndex::search_host(const float* q, size_t nq, size_t k, size_t nprobe,
     vgpu_search_stats st{};
     st.nq = (uint32_t)nq;
     run_search(ws->q.p, nq, pl, w, ws->ids.p, ws->odist.p, s, ws.ws.get(), &st);
+    VGPU_HIP(hipMemcpyAsync(ids, ws->ids.p, nq * k * sizeof(int64_t), hipMemcpyDeviceToHost, s));
+    VGPU_HIP(hipMemcpyAsync(dists, ws->odist.p, nq * k * sizeof(float), hipMemcpyDeviceToHost, s));
+    VGPU_HIP(hipStreamSynchronize(s));
+    std::lock_guard<std::mutex> lk(stats_mu);
+    stats = st;
+}
+
+void IvfpqIndex::search_host_probed(const float* q, size_t nq, size_t P, const uint32_t* probes,
+                                    size_t k, int64_t* ids, float* dists) {
+    if (!built) throw Error(VGPU_ERR_NOT_BUILT, "IVF-PQ index: search before build");
+    if (nq == 0 || k == 0) return;
+    if (P > L) throw Error(VGPU_ERR_INVALID_PARAMETER, "more probes than lists");
+    for (size_t i = 0; i < nq * P; i++)
+        if (probes[i] >= L) throw Error(VGPU_ERR_INVALID_PARAMETER, "probe list out of range");
+    const SearchPlan pl = plan_search(nq, k, P, 0);
+    WsLease ws(*this, take_ws());
+    hipStream_t s = ws->stream;
+    ws->q.upload(q, nq * d, s);
+    if (P) ws->gprobe.upload(probes, nq * P, s);
+    else ws->gprobe.reserve(1);
+    ws->ids.reserve(nq * k);
+    ws->odist.reserve(nq * k);
+    ws->arena.reserve(ws_layout(pl, nullptr, nullptr));
+    WsPtrs w;
+    ws_layout(pl, ws->arena.p, &w);
+    vgpu_search_stats st{};
+    st.nq = (uint32_t)nq;
+    run_search(ws->q.p, nq, pl, w, ws->ids.p, ws->odist.p, s, ws.ws.get(), &st, ws->gprobe.p);
     VGPU_HIP(hipMemcpyAsync(ids, ws->ids.p, nq * k * sizeof(int64_t), hipMemcpyDeviceToHost, s));
     VGPU_HIP(hipMemcpyAsync(dists, ws->odist.p, nq * k * sizeof(float), hipMemcpyDeviceToHost, s));
     VGPU_HIP(hipStreamSynchronize(s));

@@ -162,6 +162,10 @@ void launch_fastscan(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 // (search.rs:1148-1156), top-k by (distance, insertion index).
 void launch_rerank(const DevIndex& ix, const float* qn, int nq, const uint32_t* pool_vidx,
                    int pool, int k, uint32_t* out_vidx, float* out_dist, hipStream_t s);
+// The same over rows of a given vector array (pool_rows index it; ties go to
+// the lower row): the file-backed searcher's candidate vectors.
+void launch_rerank_vectors(const float* vectors, int d, const float* qn, int nq, const uint32_t* pool_rows,
+                           int pool, int k, uint32_t* out_rows, float* out_dist, hipStream_t s);
 // Zero n 64-bit words on stream s (a kernel, graph-capture safe).
 void launch_zero_words(unsigned long long* p, size_t n, hipStream_t s);
 // Map insertion indices to doc ids and pad with (-1, +inf) (python.rs:778-785).

@@ -114,6 +114,7 @@ struct SearchWs {
     DevBuf<uint8_t> want;         // filtered search: per-query category
     DevBuf<float> fqn, fdist, frres;  // filtered search: queries, distances, rotated residuals
     DevBuf<uint32_t> fvidx;           // filtered search: insertion indices
+    DevBuf<uint32_t> gprobe;          // given probe lists (file-backed search)
     unsigned long long* h_scal = nullptr;  // pinned host copy of the per-call scalars
     SearchWs();
     ~SearchWs();
@@ -209,6 +210,12 @@ struct IvfpqIndex {
     void search_host(const float* q, size_t nq, size_t k, size_t nprobe, size_t pool,
                      int64_t* ids, float* dists);
     void probe_host(const float* q, size_t nq, size_t nprobe, uint32_t* lists);
+    // search_host over given probe lists (probes[q*P..], P per query, every
+    // list < L) instead of the coarse quantiser's: the file-backed searcher
+    // probes with the full index's centroids and scans a batch index of the
+    // probed lists.
+    void search_host_probed(const float* q, size_t nq, size_t P, const uint32_t* probes, size_t k,
+                            int64_t* ids, float* dists);
     void enable_filtering();
     void set_category(uint32_t doc_id, int cat);
     // search_with_filter for nq queries, query i restricted to category cats[i];
@@ -228,9 +235,10 @@ struct IvfpqIndex {
     // Every chunk of one search: coarse, select, scan, rerank and finish.
     // ws (may be null) supplies the profiling events and the pinned scalar
     // copy; *st receives the statistics when ws is given.
+    // d_given (may be null): probe lists to use instead of the coarse step's.
     void run_search(const float* d_q, size_t nq, const SearchPlan& pl, const WsPtrs& w,
                     int64_t* d_ids, float* d_dists, hipStream_t s, SearchWs* ws,
-                    vgpu_search_stats* st);
+                    vgpu_search_stats* st, const uint32_t* d_given = nullptr);
     // Normalise and probe nq queries into w.qn / w.qnorm / w.probe (P may be 0).
     // mid (may be null) is recorded between the scoring and the selection.
     void coarse_probe(const float* d_q, size_t nq, size_t P, const SearchPlan& pl, const WsPtrs& w,
@@ -275,6 +283,45 @@ struct FlatIndex {
     void sync_device();  // device copy, norms and bf16 pack of host rows 0..n
     void search_device(const float* d_q, size_t nq, size_t k, int64_t* d_ids, float* d_dists,
                        hipStream_t s);
+};
+
+// A file descriptor closed with its owner (also when a constructor throws).
+struct UniqueFd {
+    int v = -1;
+    UniqueFd() = default;
+    UniqueFd(const UniqueFd&) = delete;
+    UniqueFd& operator=(const UniqueFd&) = delete;
+    ~UniqueFd();
+};
+
+// IVFPQFileSearcher (search.rs:247-262): routing metadata in memory, codes
+// and raw vectors read from the snapshot directory per batch.  One batch at a
+// time per handle (the reference's search takes &mut self).
+struct FileIvfpq {
+    size_t d = 0, L = 0, M = 0, K = 0, n = 0;
+    vgpu_ivfpq_params params;
+    std::string dir;
+    std::vector<uint64_t> offsets;     // [L+1] list offsets into list_ids
+    std::vector<uint32_t> list_ids;    // [n] snapshot vector index per list entry
+    std::vector<uint32_t> doc_ids;     // [n]
+    std::vector<float> centroids, codebooks;
+    std::vector<uint64_t> lc_offsets;  // list_offsets.bin (bytes into list_codes.bin)
+    UniqueFd fd_codes, fd_list_codes, fd_raw;
+    std::unique_ptr<IvfpqIndex> meta;   // centroids only: the probe lists
+    std::unique_ptr<IvfpqIndex> batch;  // the probed lists of the current batch
+    hipStream_t stream = nullptr;
+    DevBuf<float> d_vecs, d_q, d_qn, d_outd;
+    DevBuf<uint32_t> d_rows, d_outrow;
+    uint64_t io_bytes = 0, io_reads = 0;  // file reads of the last search
+    std::mutex mu;
+
+    FileIvfpq(size_t dim, const vgpu_ivfpq_params& p, const float* cent, size_t Lc, const float* cb,
+              size_t Kc, const uint64_t* off, const uint32_t* lids, const uint32_t* dids, size_t nv,
+              const float* rot, const std::string& directory, bool raw_present);
+    ~FileIvfpq();
+    void load_batch(const std::vector<uint32_t>& uni, std::vector<uint32_t>& members);
+    void search(const float* q, size_t nq, size_t k, size_t nprobe, size_t pool, int64_t* ids,
+                float* dists, vgpu_file_diagnostics* diag);
 };
 
 // Bytes of the allocation-free search's device scratch (one array per GPU).

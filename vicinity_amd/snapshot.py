@@ -227,6 +227,12 @@ _COMPONENTS = ["centroids.bin", "clusters.bin", "codes.bin", "doc_ids.bin", "lis
                "list_offsets.bin"]  # manifest.rs:64-79
 
 
+def _check_size(path: str, nbytes: int) -> None:
+    size = os.path.getsize(path)
+    if size != nbytes:
+        raise SnapshotFormatError(f"{os.path.basename(path)} size mismatch: expected {nbytes} bytes, got {size}")
+
+
 def _read_exact(path: str, dtype, count: int) -> np.ndarray:
     """persistence.rs:117-174: the file holds exactly `count` values."""
     with open(path, "rb") as f:
@@ -237,9 +243,11 @@ def _read_exact(path: str, dtype, count: int) -> np.ndarray:
     return np.frombuffer(data, dtype=dtype).astype(np.dtype(dtype).newbyteorder("="), copy=True)
 
 
-def read_snapshot(path) -> dict:
+def read_snapshot(path, arrays: bool = True) -> dict:
     """Parse and check a snapshot directory; returns the manifest fields and
-    the arrays (lists as entry offsets + member indices)."""
+    the arrays (lists as entry offsets + member indices).  With arrays=False
+    the codes and raw vectors are not read (their files' sizes are checked):
+    what the file-backed searcher keeps in memory (search.rs:1679-1762)."""
     with open(os.path.join(path, "manifest.json"), "rb") as f:
         raw = f.read()
     try:
@@ -302,11 +310,16 @@ def read_snapshot(path) -> dict:
 
     doc_ids = _read_exact(os.path.join(path, "doc_ids.bin"), "<u4", n)
     centroids = _read_exact(os.path.join(path, "centroids.bin"), "<f4", L * dim).reshape(L, dim)
-    codes = _read_exact(os.path.join(path, "codes.bin"), np.uint8,
-                        n * int(params["num_codebooks"])).reshape(n, -1)
-    vectors = None
-    if present:
-        vectors = _read_exact(os.path.join(path, "raw_vectors.bin"), "<f4", n * dim).reshape(n, dim)
+    codes = vectors = None
+    if arrays:
+        codes = _read_exact(os.path.join(path, "codes.bin"), np.uint8,
+                            n * int(params["num_codebooks"])).reshape(n, -1)
+        if present:
+            vectors = _read_exact(os.path.join(path, "raw_vectors.bin"), "<f4", n * dim).reshape(n, dim)
+    else:
+        _check_size(os.path.join(path, "codes.bin"), n * int(params["num_codebooks"]))
+        if present:
+            _check_size(os.path.join(path, "raw_vectors.bin"), n * dim * 4)
     # clusters.bin (persistence.rs:201-248)
     with open(os.path.join(path, "clusters.bin"), "rb") as f:
         blob = f.read()
@@ -349,4 +362,5 @@ def read_snapshot(path) -> dict:
         "vectors": vectors, "list_offsets": np.asarray(offsets[:L + 1], np.uint64),
         "list_ids": list_ids.astype(np.uint32), "list_masks": np.asarray(masks[:L], np.uint64),
         "filter_field": filter_field, "filter_metadata": filter_metadata, "rotation": rotation,
+        "raw_vectors_present": bool(present),
     }
