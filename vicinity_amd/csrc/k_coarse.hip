@@ -529,6 +529,57 @@ __global__ __launch_bounds__(256) void coarse_select_kernel(
     for (int p = tid; p < Pe; p += blockDim.x) probe[(size_t)q * P + p] = pay[p];
 }
 
+// Selection of more than SEL_CAP lists (P up to L <= SEL_WIDE_MAX): the exact
+// score of every list (the reference's sequential 1 - dot,
+// cosine_distance_normalized) into the row, an exact 64-bit radix select of
+// the Pe-th (score, list) key, then the Pe keys at or below it sorted in LDS
+// (search.rs:1602-1617 with nprobe up to num_clusters).
+__global__ __launch_bounds__(256) void coarse_select_wide_kernel(float* __restrict__ D,
+                                                                 const float* __restrict__ qn,
+                                                                 const float* __restrict__ C, int nq,
+                                                                 int L, int d, int P,
+                                                                 uint32_t* __restrict__ probe) {
+    extern __shared__ __align__(16) uint64_t wide_keys[];  // [next_pow2(Pe)]
+    __shared__ RadixScratch rs;
+    __shared__ uint32_t cnt;
+    const int tid = threadIdx.x;
+    const int q = blockIdx.x;
+    if (q >= nq) return;
+    float* row = D + (size_t)q * L;
+    const float* qv = qn + (size_t)q * d;
+    const int Pe = P < L ? P : L;
+    for (int i = tid; i < L; i += blockDim.x) row[i] = 1.0f - seq_dot(qv, C + (size_t)i * d, d);
+    __threadfence_block();
+    __syncthreads();
+    auto ekey = [&](int i) -> uint64_t { return cand_key(row[i], (uint32_t)i); };
+    const uint64_t K64 = Pe < L ? block_radix_select<uint64_t>(ekey, L, (uint32_t)(Pe - 1), &rs) : ~0ull;
+    if (tid == 0) cnt = 0;
+    __syncthreads();
+    for (int i = tid; i < L; i += blockDim.x) {
+        const uint64_t k = ekey(i);
+        if (k <= K64) {
+            const uint32_t slot = atomicAdd(&cnt, 1u);
+            if (slot < (uint32_t)Pe) wide_keys[slot] = k;
+        }
+    }
+    __syncthreads();
+    const int n2 = next_pow2(Pe);
+    for (int t = Pe + tid; t < n2; t += blockDim.x) wide_keys[t] = ~0ull;
+    block_bitonic_sort_keys(wide_keys, n2);
+    for (int p = tid; p < Pe; p += blockDim.x) probe[(size_t)q * P + p] = (uint32_t)wide_keys[p];
+}
+
+void launch_coarse_select_wide(float* D, const float* qn, const float* C, int nq, int L, int d, int P,
+                               uint32_t* probe, hipStream_t s) {
+    if (nq <= 0) return;
+    const int Pe = P < L ? P : L;
+    size_t n2 = 1;
+    while (n2 < (size_t)Pe) n2 <<= 1;
+    const size_t lds = n2 * sizeof(uint64_t);
+    ensure_dyn_lds((const void*)coarse_select_wide_kernel, lds);
+    hipLaunchKernelGGL(coarse_select_wide_kernel, dim3(nq), dim3(256), lds, s, D, qn, C, nq, L, d, P, probe);
+}
+
 void launch_coarse_select(float* D, const float* qn, const float* qnorm, const float* C, int nq,
                           int L, int d, int P, float cmax, uint32_t* probe,
                           unsigned int* overflow, uint32_t* flag_list, uint32_t* flag_count,

@@ -170,7 +170,12 @@ __host__ __device__ inline int fs_wave_buf(int keep) {
 
 __host__ __device__ inline size_t fs_align16(size_t x) { return (x + 15) & ~(size_t)15; }
 
+// Probe slots staged in LDS per query; a wider probe reads each slot's list
+// from global memory when its wave takes it.
+#define FS_LDS_P 1024
+
 __host__ __device__ inline size_t fs_lds_layout(int d, int M, int P, int wbuf, size_t* off) {
+    if (P > FS_LDS_P) P = 0;
     size_t o = 0;
     off[0] = o; o = fs_align16(o + (size_t)d * 4);            // qs
     off[1] = o; o = fs_align16(o + (size_t)4 * d * 4);        // residual per wave
@@ -194,13 +199,14 @@ __global__ __launch_bounds__(256) void fastscan_kernel(DevIndex ix, ScanArgs a, 
     float* rw = (float*)(smem + off[1]) + wave * d;
     float* lutf = (float*)(smem + off[2]) + wave * M * 16;
     uint8_t* qlut = (uint8_t*)(smem + off[3]) + wave * M * 16;
+    const bool wide = P > FS_LDS_P;
     uint32_t* lid = (uint32_t*)(smem + off[4]);
-    uint32_t* llen = lid + P;
+    uint32_t* llen = lid + (wide ? 0 : P);
     uint64_t* allkeys = (uint64_t*)(smem + off[5]);
     uint32_t* cnt = (uint32_t*)(smem + off[6]);
 
     for (int j = tid; j < d; j += blockDim.x) qs[j] = a.qn[(size_t)q * d + j];
-    for (int p = tid; p < P; p += blockDim.x) {
+    for (int p = tid; p < (wide ? 0 : P); p += blockDim.x) {
         uint32_t l = a.probe[(size_t)q * P + p];
         bool ok = l < (uint32_t)ix.L;  // no such list: scanned as empty
         lid[p] = ok ? l : 0u;
@@ -218,7 +224,16 @@ __global__ __launch_bounds__(256) void fastscan_kernel(DevIndex ix, ScanArgs a, 
     uint32_t scanned = 0;
 
     for (int p = wave; p < P; p += 4) {
-        const uint32_t l = lid[p], len = llen[p];
+        uint32_t l, len;
+        if (wide) {
+            const uint32_t g = a.probe[(size_t)q * P + p];
+            const bool ok = g < (uint32_t)ix.L;  // no such list: scanned as empty
+            l = ok ? g : 0u;
+            len = ok ? ix.offsets[g + 1] - ix.offsets[g] : 0u;
+        } else {
+            l = lid[p];
+            len = llen[p];
+        }
         if (len == 0) continue;
         const uint32_t beg = ix.offsets[l];
         scanned += len;

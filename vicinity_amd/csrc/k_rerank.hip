@@ -10,19 +10,19 @@
 
 namespace vgpu {
 
-#define RERANK_CAP 2048
-
+// One workgroup per query; the pool's keys and a payload row in dynamic LDS
+// (next_pow2(pool) of each; pool <= RERANK_MAX).
 __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ vectors, int d,
                                                      const float* __restrict__ qn, int nq,
                                                      const uint32_t* __restrict__ pool_vidx,
                                                      int pool, int k, uint32_t* __restrict__ out_vidx,
                                                      float* __restrict__ out_dist) {
-    __shared__ uint64_t keys[RERANK_CAP];
-    __shared__ uint32_t pay[RERANK_CAP];
+    extern __shared__ __align__(16) uint64_t keys[];
     const int q = blockIdx.x;
     if (q >= nq) return;
     const float* qv = qn + (size_t)q * d;
     const int n2 = next_pow2(pool);
+    uint32_t* pay = reinterpret_cast<uint32_t*>(keys + n2);
     for (int t = threadIdx.x; t < n2; t += blockDim.x) {
         uint64_t key = ~0ull;
         if (t < pool) {
@@ -46,17 +46,23 @@ __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ v
     }
 }
 
+static size_t rerank_lds(int pool) {
+    size_t n2 = 1;
+    while (n2 < (size_t)pool) n2 <<= 1;
+    return n2 * (sizeof(uint64_t) + sizeof(uint32_t));
+}
+
 void launch_rerank(const DevIndex& ix, const float* qn, int nq, const uint32_t* pool_vidx,
                    int pool, int k, uint32_t* out_vidx, float* out_dist, hipStream_t s) {
-    if (nq <= 0) return;
-    hipLaunchKernelGGL(rerank_kernel, dim3(nq), dim3(256), 0, s, ix.vectors, ix.d, qn, nq, pool_vidx,
-                       pool, k, out_vidx, out_dist);
+    launch_rerank_vectors(ix.vectors, ix.d, qn, nq, pool_vidx, pool, k, out_vidx, out_dist, s);
 }
 
 void launch_rerank_vectors(const float* vectors, int d, const float* qn, int nq, const uint32_t* pool_rows,
                            int pool, int k, uint32_t* out_rows, float* out_dist, hipStream_t s) {
     if (nq <= 0) return;
-    hipLaunchKernelGGL(rerank_kernel, dim3(nq), dim3(256), 0, s, vectors, d, qn, nq, pool_rows, pool, k,
+    const size_t lds = rerank_lds(pool);
+    ensure_dyn_lds((const void*)rerank_kernel, lds);
+    hipLaunchKernelGGL(rerank_kernel, dim3(nq), dim3(256), lds, s, vectors, d, qn, nq, pool_rows, pool, k,
                        out_rows, out_dist);
 }
 

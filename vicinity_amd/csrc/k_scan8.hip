@@ -20,6 +20,10 @@ namespace vgpu {
 #define SCAN_U 2                      // candidates per thread per round
 #define SCAN_ROUND (VGPU_BLOCK * SCAN_U)
 
+// Probe slots kept in LDS per query; a wider probe (nprobe up to nlist) reads
+// each slot's list from global memory when it is scanned.
+#define SCAN_LDS_P 1024
+
 struct TopkLds {
     uint64_t* keys;  // (distance key << 32) | insertion index
     uint32_t* pos;   // list-major position of the entry
@@ -160,10 +164,11 @@ __device__ inline ScanLds carve(char* smem, int d, int M, int K, int P, int buf)
     return s;
 }
 
-// Common prologue: query vector and probed list ranges into LDS.
+// Common prologue: query vector and probed list ranges into LDS (the ranges
+// only for at most SCAN_LDS_P probes: wider probes are read per slot).
 __device__ inline void load_query_and_lists(const DevIndex& ix, const ScanArgs& a, ScanLds& s,
                                             int q) {
-    const int tid = threadIdx.x, d = ix.d, P = a.P;
+    const int tid = threadIdx.x, d = ix.d, P = a.P > SCAN_LDS_P ? 0 : a.P;
     for (int j = tid; j < d; j += blockDim.x) s.qs[j] = a.qn[(size_t)q * d + j];
     for (int p = tid; p < P; p += blockDim.x) {
         uint32_t l = a.probe[(size_t)q * P + p];
@@ -320,14 +325,25 @@ template <int MT, int KT, int CWD>
 __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char* smem, int q) {
     const int tid = threadIdx.x;
     const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, P = a.P;
-    ScanLds s = carve(smem, d, M, K, P, buf);
+    const bool wide = P > SCAN_LDS_P;
+    ScanLds s = carve(smem, d, M, K, wide ? 0 : P, buf);
     float cw[CWD != 0 ? MT * (CWD > 0 ? CWD : -CWD) : 1];
     load_codewords<MT, CWD>(ix, cw);
     load_query_and_lists(ix, a, s, q);
     uint32_t total = 0;
     for (int p = 0; p < P; p++) {
         __syncthreads();
-        const uint32_t l = s.lid[p], beg = s.lbeg[p], len = s.llen[p];
+        uint32_t l, beg, len;
+        if (wide) {  // the same for every thread
+            l = a.probe[(size_t)q * P + p];
+            const bool ok = l < (uint32_t)ix.L;
+            beg = ok ? ix.offsets[l] : 0u;
+            len = ok ? ix.offsets[l + 1] - beg : 0u;
+        } else {
+            l = s.lid[p];
+            beg = s.lbeg[p];
+            len = s.llen[p];
+        }
         total += len;
         if (len == 0) continue;
         scan_list<MT, KT, false, CWD>(ix, a, s, buf, l, beg, len, q, p, nullptr, 0, cw);
@@ -404,7 +420,7 @@ constexpr int cw_regs() {
 
 size_t scan8_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
     size_t off[12];
-    return scan_lds_layout(ix.d, ix.M, ix.K, a.P, scan_buf(a.kk), off);
+    return scan_lds_layout(ix.d, ix.M, ix.K, a.P > SCAN_LDS_P ? 0 : a.P, scan_buf(a.kk), off);
 }
 
 template <int MT, int KT>

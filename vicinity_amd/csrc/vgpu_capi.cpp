@@ -589,7 +589,6 @@ int vgpu_ivfpq_file_search_batch(vgpu_ivfpq_file* h, const float* queries, size_
              "null argument");
         std::lock_guard<std::mutex> lk(h->fx->mu);
         need(dim == h->fx->d, VGPU_ERR_DIMENSION_MISMATCH, "query dimension does not match the index");
-        need(k <= 2048 && rerank_pool <= 2048, VGPU_ERR_INVALID_PARAMETER, "k / rerank_pool above 2048 is not supported");
         h->fx->search(queries, nq, k, nprobe, rerank_pool, out_ids, out_dists, diag);
     });
 }

@@ -665,19 +665,33 @@ SearchPlan IvfpqIndex::plan_search(size_t nq, size_t k, size_t nprobe, size_t po
     pl.k = k;
     pl.pool = pool;
     pl.kout = pool ? std::max(pool, k) : k;  // search.rs:1144
-    if (pl.kout > 2048) throw Error(VGPU_ERR_INVALID_PARAMETER, "k / rerank_pool above 2048 is not supported");
-    if (pl.P > 1024) throw Error(VGPU_ERR_INVALID_PARAMETER, "nprobe above 1024 is not supported");
+    if (pool && pl.kout > RERANK_MAX)
+        throw Error(VGPU_ERR_UNSUPPORTED, "rerank_pool above " + std::to_string(RERANK_MAX) + " is not supported");
+    pl.wide = pl.P > 1024 || pl.kout > 2048;
+    if (pl.P > SEL_WIDE_MAX)  // min(nprobe, nlist) lists sorted in LDS
+        throw Error(VGPU_ERR_UNSUPPORTED, "probing more than " + std::to_string(SEL_WIDE_MAX) +
+                                              " lists is not supported");
     if (pl.P) {
         ScanArgs probe_shape;
         probe_shape.P = (int)pl.P;
         probe_shape.kout = (int)pl.kout;
-        probe_shape.kk = K == 16 ? (int)pl.kout : fast_keep(pl.kout);
-        size_t lds = K == 16 ? fastscan_lds_bytes(dix, probe_shape)
-                             : std::max(scan8_fast_lds_bytes(dix, probe_shape),
-                                        scan8_lds_bytes(dix, probe_shape));
+        size_t lds;
+        if (K == 16) {
+            probe_shape.kk = (int)pl.kout;
+            lds = fastscan_lds_bytes(dix, probe_shape);
+        } else if (pl.wide) {  // EXACT only
+            probe_shape.kk = (int)pl.kout;
+            lds = scan8_lds_bytes(dix, probe_shape);
+        } else {
+            probe_shape.kk = fast_keep(pl.kout);
+            lds = scan8_fast_lds_bytes(dix, probe_shape);
+            probe_shape.kk = (int)pl.kout;
+            lds = std::max(lds, scan8_lds_bytes(dix, probe_shape));
+        }
         if (lds > 160 * 1024)
-            throw Error(VGPU_ERR_UNSUPPORTED, "scan working set of " + std::to_string(lds) +
-                                                  " bytes exceeds the 160 KiB of LDS per workgroup");
+            throw Error(VGPU_ERR_UNSUPPORTED, "k of " + std::to_string(pl.kout) + " needs a scan working set of " +
+                                                  std::to_string(lds) +
+                                                  " bytes, above the 160 KiB of LDS per workgroup");
     }
     pl.opq = !rotation.empty();
     pl.fused = coarse_fused_supported((int)d, (int)pl.P);
@@ -741,6 +755,10 @@ void IvfpqIndex::coarse_probe(const float* d_q, size_t nq, size_t P, const Searc
                            w.cflag_list, cflag_count, s);
         launch_coarse_exact_flagged(w.qn, w.qnorm, d_centroids.p, (int)nq, (int)L, (int)d, (int)P, dix.cmax,
                                     w.probe, overflow, w.cflag_list, cflag_count, s);
+    } else if (P > 1024) {  // every list's exact score, then the P smallest
+        launch_normalize(d_q, w.qn, w.qnorm, (int)nq, (int)d, s);
+        if (mid) VGPU_HIP(hipEventRecord(mid, s));
+        launch_coarse_select_wide(w.dots, w.qn, d_centroids.p, (int)nq, (int)L, (int)d, (int)P, w.probe, s);
     } else {
         launch_normalize(d_q, w.qn, w.qnorm, (int)nq, (int)d, s);
         launch_coarse_dots(w.qn, d_centroids.p, w.dots, (int)nq, (int)L, (int)d, s);
@@ -797,7 +815,7 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
         if (allp) VGPU_HIP(hipEventRecord(ev[3], s));
         // scan-only timing: the FAST kernel's dispatch records the two events
         // itself; the other scan kernels are bracketed by marker events
-        const bool scan_fast = K != 16 && mode == VGPU_MODE_FAST && !pl.opq;
+        const bool scan_fast = K != 16 && mode == VGPU_MODE_FAST && !pl.opq && !pl.wide;
         if (scanp && !scan_fast) VGPU_HIP(hipEventRecord(ws->sev[2 * ci], s));
         ScanArgs a;
         a.qn = w.qn;
@@ -1006,7 +1024,6 @@ void IvfpqIndex::probe_host(const float* q, size_t nq, size_t nprobe, uint32_t* 
     if (!built) throw Error(VGPU_ERR_NOT_BUILT, "IVF-PQ index: probe before build");
     const size_t P = std::min(nprobe, L);
     if (nq == 0 || P == 0) return;
-    if (P > 1024) throw Error(VGPU_ERR_INVALID_PARAMETER, "nprobe above 1024 is not supported");
     SearchPlan pl = plan_search(nq, 1, P, 0);
     WsLease ws(*this, take_ws());
     hipStream_t s = ws->stream;
@@ -1105,7 +1122,6 @@ void IvfpqIndex::search_filtered(const float* q, size_t nq, size_t k, const int*
     for (size_t i = 0; i < nq * d; i++)
         if (!std::isfinite(q[i])) throw Error(VGPU_ERR_INVALID_PARAMETER, "query contains a non-finite value");
     if (nq == 0 || k == 0) return;
-    if (k > 2048) throw Error(VGPU_ERR_INVALID_PARAMETER, "k above 2048 is not supported");
     {
         ScanArgs shape;  // the filtered kernel's LDS: the EXACT table and buffer, no per-list arrays
         shape.kk = (int)k;

@@ -93,6 +93,11 @@ void launch_coarse_dots(const float* Q, const float* C, float* D, int nq, int L,
 // 1 - dot (ties: lower list index), ascending.  D may be overwritten for
 // degenerate rows.  flag_list [nq] / flag_count [1]: device scratch; *flag_count
 // must be 0 on entry and is left holding the number of degenerate rows.
+// Probe selection of more than 1024 lists (up to SEL_WIDE_MAX): exact scores of
+// every list into D (nq x L), then the P smallest (score, list) in order.
+#define SEL_WIDE_MAX 16384
+void launch_coarse_select_wide(float* D, const float* qn, const float* C, int nq, int L, int d, int P,
+                               uint32_t* probe, hipStream_t s);
 void launch_coarse_select(float* D, const float* qn, const float* qnorm, const float* C,
                           int nq, int L, int d, int P, float cmax, uint32_t* probe,
                           unsigned int* overflow, uint32_t* flag_list, uint32_t* flag_count,
@@ -160,6 +165,8 @@ void launch_fastscan(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 
 // Exact rerank of the scan's pool: 1 - q.v over stored vectors
 // (search.rs:1148-1156), top-k by (distance, insertion index).
+// Largest rerank pool (the pool's keys sit in LDS).
+#define RERANK_MAX 8192
 void launch_rerank(const DevIndex& ix, const float* qn, int nq, const uint32_t* pool_vidx,
                    int pool, int k, uint32_t* out_vidx, float* out_dist, hipStream_t s);
 // The same over rows of a given vector array (pool_rows index it; ties go to

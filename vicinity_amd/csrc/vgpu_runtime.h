@@ -79,6 +79,9 @@ struct SearchPlan {
     size_t pool = 0;   // rerank pool (0: no rerank)
     size_t chunk = 0;  // queries per launch sequence
     bool fused = false, opq = false;
+    // nprobe above 1024 or kout above 2048: probes chosen from exact scores of
+    // every list, scans in EXACT (or FastScan) mode with per-slot list reads
+    bool wide = false;
 };
 
 // Device pointers of one call's workspace, carved from one arena
