@@ -82,3 +82,35 @@ def test_flat_wide_rows_take_the_fp32_path(oracle):
     ids, dists = fx.search(q, 10)
     oids, odists = oracle.flat_search(base, q, 10, metric=0)
     _check(ids, dists, oids, odists)
+
+
+@pytest.mark.parametrize("metric", [0, 1])
+def test_flat_fallback_rescans_crowded_lanes(oracle, metric):
+    """Near-copies of one vector crowded into single ranking lanes (more than
+    the four keys a lane keeps, so the merge cannot prove the result and the
+    fallback rescans those lanes' columns) beside near-copies spread one per
+    lane in another slice (kept keys, rescored) and exact duplicates (ties
+    broken by index).  40000 rows make 32 slices of 80 tiles: vector
+    16 (80 s + t) + c is slice s, lane c."""
+    from vicinity_amd import FlatIndex
+
+    _print_case(f"flat crowded lanes metric={metric}")
+    rng = np.random.default_rng(71 + metric)
+    n, d = 40_000, 64
+    base = rng.standard_normal((n, d)).astype(np.float32)
+    v = base[17].copy()
+    near = lambda m, s: v + s * rng.standard_normal((m, d)).astype(np.float32)  # noqa: E731
+    base[(160 + np.arange(12)) * 16 + 5] = near(12, 1e-4)      # slice 2, lane 5
+    base[(560 + 3) * 16 + np.arange(6)] = near(6, 1e-4)       # slice 7, lanes 0-5
+    base[(1600 + 2 * np.arange(5)) * 16 + 9] = v              # slice 20, lane 9
+    q = np.concatenate([near(4, 1e-3), rng.standard_normal((20, d)).astype(np.float32)])
+    if metric == 1:
+        base = oracle.normalize_rows(base)
+        q = oracle.normalize_rows(q)
+    fx = FlatIndex(d, "l2" if metric == 0 else "cosine")
+    fx.add(base)
+    for k in (10, 32, 3):
+        ids, dists = fx.search(q, k)
+        oids, odists = oracle.flat_search(base, q, k, metric=metric)
+        _check(ids, dists, oids, odists)
+        assert fx.last_fallbacks() >= 4, k

@@ -204,40 +204,6 @@ __device__ __forceinline__ void fr_insert(float (&t)[FR_J], float v) {
     t[0] = fminf(t[0], v);
 }
 
-// Ascending bitonic sort of the 16 FR_J keys of a lane group (element
-// e * 16 + lane % 16 in k[e]).
-__device__ __forceinline__ void fr_group_sort(uint64_t (&k)[FR_J]) {
-    const int c = threadIdx.x & 15;
-#pragma unroll
-    for (int size = 2; size <= 16 * FR_J; size <<= 1) {
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            if (stride >= 16) {
-                const int es = stride >> 4;
-#pragma unroll
-                for (int e = 0; e < FR_J; e++) {
-                    const int f = e ^ es;
-                    if (f > e) {
-                        const bool asc = (((e << 4) | c) & size) == 0;
-                        const uint64_t a = k[e], b = k[f];
-                        const bool sw = (a > b) == asc;
-                        k[e] = sw ? b : a;
-                        k[f] = sw ? a : b;
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < FR_J; e++) {
-                    const uint64_t o = shfl_xor_u64(k[e], stride);
-                    const bool asc = (((e << 4) | c) & size) == 0;
-                    const bool lower = (c & stride) == 0;
-                    k[e] = (lower == asc) ? (o < k[e] ? o : k[e]) : (o > k[e] ? o : k[e]);
-                }
-            }
-        }
-    }
-}
-
 // Workgroup (4 waves) = FR_ROWS queries x one database slice of tiles
 // [blockIdx.y * tps, ..) (tps <= 2^ib).  Wave w holds query blocks
 // FR_QBW w .. + FR_QBW - 1 (bf16 hi/lo A operands in registers); every stage
@@ -245,10 +211,10 @@ __device__ __forceinline__ void fr_group_sort(uint64_t (&k)[FR_J]) {
 // lane of group g (lanes 16 g .. + 15) and column c scores rows 4 g .. + 3 of
 // each of its query blocks against vector 16 tile + c and keeps, per row, the
 // FR_J smallest keys (score with the low ib mantissa bits replaced by the
-// tile's index in the slice).  At the end each row's 16 lanes sort their
-// 16 FR_J keys as (fkey, vector index); the slice writes the kk smallest and
-// a bound every key it dropped is at or above: the kk-th kept key and the
-// FR_J-th key of every full lane list.
+// tile's index in the slice).  At the end each row's 16 lanes write their
+// 16 FR_J keys as (fkey, vector index), unsorted (the merge selects), and a
+// bound every key the slice dropped is at or above: the FR_J-th key of every
+// full lane list.
 template <int DT>
 __global__ __launch_bounds__(256) void flat_rank_kernel(
     const float* __restrict__ Q, int nq, int d, const uint4* __restrict__ Xb_in,
@@ -388,45 +354,30 @@ __global__ __launch_bounds__(256) void flat_rank_kernel(
     }
     if (nst > 0) epilogue(prev, prevn, nst - 1, true);
 
-    // Per row: sort the group's keys, write the kk smallest and the bound.
-#pragma unroll 1
+    // Per row: every lane's FR_J keys as (fkey, vector index), ~0 past a
+    // short list, and the bound every dropped key is at or above: the
+    // FR_J-th key of every full lane list (all 16 FR_J keys are kept, kk =
+    // 16 FR_J, so no key of the lists themselves is dropped).
+#pragma unroll
     for (int j = 0; j < 4 * FR_QBW; j++) {
         const int qb = j >> 2, r = j & 3;
-        float t[FR_J];
-#pragma unroll
-        for (int e = 0; e < FR_J; e++) {  // the lane's list of row slot j (registers: unrolled select)
-            float x = lst[0][0][e];
-#pragma unroll
-            for (int jj = 1; jj < 4 * FR_QBW; jj++) x = jj == j ? lst[jj >> 2][jj & 3][e] : x;
-            t[e] = x;
-        }
-        uint64_t k[FR_J];
-#pragma unroll
-        for (int e = 0; e < FR_J; e++) {
-            const uint32_t bits = __float_as_uint(t[e]);
-            const uint32_t col = (uint32_t)((tile0 + (int)(bits & ~kmask)) * 16 + c);
-            k[e] = t[e] < FR_BIG ? ((uint64_t)fkey(t[e]) << 32) | col : ~0ull;
-        }
-        uint32_t lb = t[FR_J - 1] < FR_BIG ? fkey(t[FR_J - 1]) : 0xffffffffu;  // a full list dropped keys >= it
+        const float tl = lst[qb][r][FR_J - 1];
+        uint32_t lb = tl < FR_BIG ? fkey(tl) : 0xffffffffu;
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) {
             const uint32_t x = shfl_xor_u32(lb, o);
             lb = x < lb ? x : lb;
         }
-        fr_group_sort(k);
-        uint64_t kth = k[0];
-#pragma unroll
-        for (int e = 1; e < FR_J; e++) kth = ((kk - 1) >> 4) == e ? k[e] : kth;
-        const int src = (lane & 48) | ((kk - 1) & 15);
-        const uint32_t kth_hi = (uint32_t)__shfl((int)(uint32_t)(kth >> 32), src, 64);
-        const uint32_t bound = kth_hi < lb ? kth_hi : lb;
         const int qrow = q0 + (FR_QBW * wave + qb) * 16 + 4 * g + r;
         if (qrow < nq) {
             uint64_t* out = partial + ((size_t)qrow * splits + sl) * kk;
 #pragma unroll
-            for (int e = 0; e < FR_J; e++)
-                if (e * 16 + c < kk) out[e * 16 + c] = k[e];
-            if (c == 0) pbound[(size_t)qrow * splits + sl] = bound;
+            for (int e = 0; e < FR_J; e++) {
+                const float t = lst[qb][r][e];
+                const uint32_t col = (uint32_t)((tile0 + (int)(__float_as_uint(t) & ~kmask)) * 16 + c);
+                out[e * 16 + c] = t < FR_BIG ? ((uint64_t)fkey(t) << 32) | col : ~0ull;
+            }
+            if (c == 0) pbound[(size_t)qrow * splits + sl] = lb;
         }
     }
 }
@@ -434,22 +385,18 @@ __global__ __launch_bounds__(256) void flat_rank_kernel(
 #define FL_BUF 2048
 #define FL_ROUND 512
 
-__device__ inline float flat_exact(const float* q, const float* x, int d, int metric) {
-    if (metric == 0) {
-        float s = 0.0f;
-        for (int j = 0; j < d; j++) {
-            float t = q[j] - x[j];
-            s += t * t;
-        }
-        return s;
-    }
-    return 1.0f - seq_dot(q, x, d);
+// The reference's distance of query q to row x (rows 16-byte aligned): squared
+// L2 or 1 - dot, summed in index order.
+__device__ inline float flat_exact(const float* q, const float* __restrict__ x, int d, int metric) {
+    return metric == 0 ? seq_l2_stream(q, x, d) : 1.0f - seq_dot_stream(q, x, d);
 }
 
-// Exact top-k of query qv over vectors [j0, j1) with a threshold-filtered LDS
-// buffer: keys (fkey(dist), index) sorted ascending in keys[0 ..) on return;
-// returns how many (all threads).  keys / pay hold FL_BUF entries.
-__device__ int flat_exact_range(const float* qv, const float* __restrict__ X, int j0, int j1, int d, int k,
+// Exact top-k of query qv over the vectors item(0 .. W - 1) names (an index,
+// or 0xffffffff to skip the item) with a threshold-filtered LDS buffer: keys
+// (fkey(dist), index) sorted ascending in keys[0 ..) on return; returns how
+// many (all threads).  keys / pay hold FL_BUF entries.
+template <class Item>
+__device__ int flat_exact_items(const float* qv, const float* __restrict__ X, int W, Item item, int d, int k,
                                 int metric, uint64_t* keys, uint32_t* pay, uint32_t* misc) {
     const int tid = threadIdx.x;
     if (tid == 0) {
@@ -457,7 +404,7 @@ __device__ int flat_exact_range(const float* qv, const float* __restrict__ X, in
         misc[3] = 0xffffffffu;
     }
     __syncthreads();
-    for (int base = j0; base < j1; base += FL_ROUND) {
+    for (int base = 0; base < W; base += FL_ROUND) {
         if ((int)misc[2] > FL_BUF - FL_ROUND) {
             int m = (int)misc[2];
             int m2 = next_pow2(m);
@@ -471,12 +418,12 @@ __device__ int flat_exact_range(const float* qv, const float* __restrict__ X, in
         }
         const uint32_t th = misc[3];
         for (int u = 0; u < FL_ROUND / 256; u++) {
-            int j = base + u * 256 + tid;
+            const int i = base + u * 256 + tid;
+            const uint32_t j = i < W ? item(i) : 0xffffffffu;
             bool take = false;
             uint64_t key = 0;
-            if (j < j1) {
-                float dist = flat_exact(qv, X + (size_t)j * d, d, metric);
-                key = cand_key(dist, (uint32_t)j);
+            if (j != 0xffffffffu) {
+                key = cand_key(flat_exact(qv, X + (size_t)j * d, d, metric), j);
                 take = (uint32_t)(key >> 32) <= th;
             }
             int slot = wave_append_slot(take, &misc[2]);
@@ -489,6 +436,13 @@ __device__ int flat_exact_range(const float* qv, const float* __restrict__ X, in
     for (int i = m + tid; i < m2; i += blockDim.x) keys[i] = ~0ull;
     block_bitonic_sort(keys, pay, m2);
     return m;
+}
+
+// flat_exact_items over vectors [j0, j1).
+__device__ int flat_exact_range(const float* qv, const float* __restrict__ X, int j0, int j1, int d, int k,
+                                int metric, uint64_t* keys, uint32_t* pay, uint32_t* misc) {
+    return flat_exact_items(qv, X, j1 > j0 ? j1 - j0 : 0, [=](int i) { return (uint32_t)(j0 + i); }, d, k,
+                            metric, keys, pay, misc);
 }
 
 __global__ __launch_bounds__(256) void flat_merge_kernel(
@@ -604,6 +558,7 @@ __global__ __launch_bounds__(256) void flat_merge_wave_kernel(
     int k, int metric, float xmax, int ib, uint32_t* __restrict__ out_idx, float* __restrict__ out_dist,
     unsigned int* overflow, uint32_t* __restrict__ flag_list, uint32_t* __restrict__ fbv) {
     __shared__ uint64_t rbuf[4][FM_R];
+    __shared__ float qsh[4][128];  // d <= 128
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = blockIdx.x * 4 + wave;
     if (q >= nq) return;
@@ -670,9 +625,10 @@ __global__ __launch_bounds__(256) void flat_merge_wave_kernel(
         }
         return;
     }
+    const float* qv = qsh[wave];
+    for (int j = lane; j < d; j += 64) qsh[wave][j] = Q[(size_t)q * d + j];
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    const float* qv = Q + (size_t)q * d;
     auto rescore = [&](uint32_t i) -> uint64_t {
         if (i >= cnt) return ~0ull;
         const uint32_t idx = (uint32_t)rbuf[wave][i];
@@ -710,11 +666,14 @@ static int flat_splits(int nq, int n, int kk) {
     return sp;
 }
 
-// The bf16x3 ranking kernel serves d <= 128 and k <= 32; it keeps
-// kk = k + 16 rounded up to 4 (at most the 64 keys a row's lanes hold) per
-// slice, plus one bound word per (query, slice) after the keys.
+// The bf16x3 ranking kernel serves d <= 128 and k <= 32; every slice keeps
+// all 16 FR_J keys of a row's lane lists, plus one bound word per (query,
+// slice) after the keys.
 static bool flat_rank_ok(int d, int k) { return d >= 1 && d <= 128 && k >= 1 && k <= 32; }
-static int flat_rank_keep(int k) { return (k + 16 + 3) & ~3; }
+static int flat_rank_keep(int k) {
+    (void)k;
+    return 16 * FR_J;
+}
 
 // Slices for the ranking kernel: an even number of tiles each (stages are
 // tile pairs), enough workgroups for four waves of two per CU on 256 CUs,
@@ -773,12 +732,15 @@ __global__ __launch_bounds__(256) void flat_exact_finish_kernel(
 }
 
 // Fallback of the ranking path, workgroup (s, i) for query q = flag_list[i]
-// and ranking slice s (tiles s tps ..): a slice whose bound exceeds the
-// query's rescoring threshold fb (fbv[q]) dropped no key <= fb, so its kept
-// keys <= fb are rescored; a slice whose bound does not is scanned
-// exhaustively with the exact arithmetic.  Either way the slice's k smallest
-// exact keys go to out_keys for flat_exact_finish_kernel: slices that could
-// not have hidden a result are not rescanned.
+// and ranking slice s (tiles s tps ..), fb = the query's rescoring threshold
+// fbv[q].  Lane c of a slice's row kept the FR_J smallest keys of vectors
+// 16 (s tps + t) + c (t < tps) at partial[e 16 + c], sorted in e; a lane whose
+// list is not full dropped nothing, and one whose FR_J-th key exceeds fb
+// dropped no key <= fb.  The other lanes' columns are scanned with the exact
+// arithmetic, and the kept keys <= fb of the rest are rescored: every vector
+// with a key <= fb (the superset of the exact top-k the merge proved) is
+// scored exactly, so the slice's k smallest exact keys, written to out_keys
+// for flat_exact_finish_kernel, hold its share of the exact top-k.
 __global__ __launch_bounds__(256) void flat_rank_fallback_kernel(
     const uint32_t* __restrict__ flag_list, const uint32_t* __restrict__ fbv,
     const uint64_t* __restrict__ partial, const uint32_t* __restrict__ pbound, int splits, int kk, int tps,
@@ -787,27 +749,52 @@ __global__ __launch_bounds__(256) void flat_rank_fallback_kernel(
     __shared__ uint64_t keys[FL_BUF];
     __shared__ uint32_t pay[FL_BUF];
     __shared__ uint32_t misc[4];
+    __shared__ float qs[128];  // d <= 128
+    __shared__ uint32_t rescan[16];
     const int s = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
     const uint32_t q = flag_list[i];
     const uint32_t fb = fbv[q];
+    const uint64_t* src = partial + ((size_t)q * splits + s) * kk;
     uint64_t* out = out_keys + ((size_t)i * splits + s) * k;
+    for (int j = tid; j < d; j += blockDim.x) qs[j] = Q[(size_t)q * d + j];
+    __syncthreads();
     if (pbound[(size_t)q * splits + s] > fb) {
         if (tid >= 64) return;  // kk <= 64 kept keys: one wave
-        const uint64_t* src = partial + ((size_t)q * splits + s) * kk;
         uint64_t r[1] = {~0ull};
         if (tid < kk) {
             const uint64_t key = src[tid];
             if (key != ~0ull && (uint32_t)(key >> 32) <= fb) {
                 const uint32_t idx = (uint32_t)key;
-                r[0] = cand_key(flat_exact(Q + (size_t)q * d, X + (size_t)idx * d, d, metric), idx);
+                r[0] = cand_key(flat_exact(qs, X + (size_t)idx * d, d, metric), idx);
             }
         }
         wave_sort_regs<1>(r);
         if (tid < k) out[tid] = r[0];
         return;
     }
-    const int j0 = s * tps * 16, j1 = min(n, (s + 1) * tps * 16);
-    const int m = j0 < j1 ? flat_exact_range(Q + (size_t)q * d, X, j0, j1, d, k, metric, keys, pay, misc) : 0;
+    // the lanes to rescan: full list (FR_J-th key present) with that key <= fb
+    uint32_t nres = 0, resmask = 0;
+    for (int c = 0; c < 16; c++) {
+        const uint64_t last = src[(FR_J - 1) * 16 + c];
+        if (last != ~0ull && (uint32_t)(last >> 32) <= fb) {
+            if (tid == 0) rescan[nres] = (uint32_t)c;
+            nres++;
+            resmask |= 1u << c;
+        }
+    }
+    __syncthreads();
+    const int scan = (int)nres * tps, tile0 = s * tps;
+    auto item = [&](int it) -> uint32_t {
+        if (it < scan) {
+            const int t = it % tps;
+            const uint32_t v = (uint32_t)((tile0 + t) * 16) + rescan[it / tps];
+            return v < (uint32_t)n ? v : 0xffffffffu;
+        }
+        const uint64_t key = src[it - scan];
+        const bool kept = key != ~0ull && (uint32_t)(key >> 32) <= fb && !((resmask >> ((it - scan) & 15)) & 1u);
+        return kept ? (uint32_t)key : 0xffffffffu;
+    };
+    const int m = flat_exact_items(qs, X, scan + kk, item, d, k, metric, keys, pay, misc);
     for (int j = tid; j < k; j += blockDim.x) out[j] = j < m ? keys[j] : ~0ull;
 }
 

@@ -67,6 +67,44 @@ __device__ __forceinline__ float seq_dot_stream(const float* a, const float* __r
     return s;
 }
 
+// sum_j (a_j - b_j)^2 in index order, each difference, square and sum
+// rounded (the reference's squared-L2 loop), b streamed as seq_dot_stream
+// streams it; d % 4 == 0 and 16-byte aligned b, other shapes one float at a time.
+__device__ __forceinline__ float seq_l2_stream(const float* a, const float* __restrict__ b, int d) {
+    float s = 0.0f;
+    int j0 = 0;
+    if ((d & 3) == 0) {
+        for (; j0 + 32 <= d; j0 += 32) {
+            float4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = reinterpret_cast<const float4*>(b + j0)[i];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float t0 = __fsub_rn(a[j0 + 4 * i], v[i].x), t1 = __fsub_rn(a[j0 + 4 * i + 1], v[i].y);
+                const float t2 = __fsub_rn(a[j0 + 4 * i + 2], v[i].z), t3 = __fsub_rn(a[j0 + 4 * i + 3], v[i].w);
+                s = __fadd_rn(s, __fmul_rn(t0, t0));
+                s = __fadd_rn(s, __fmul_rn(t1, t1));
+                s = __fadd_rn(s, __fmul_rn(t2, t2));
+                s = __fadd_rn(s, __fmul_rn(t3, t3));
+            }
+        }
+        for (; j0 < d; j0 += 4) {
+            const float4 v = reinterpret_cast<const float4*>(b + j0)[0];
+            const float t0 = __fsub_rn(a[j0], v.x), t1 = __fsub_rn(a[j0 + 1], v.y);
+            const float t2 = __fsub_rn(a[j0 + 2], v.z), t3 = __fsub_rn(a[j0 + 3], v.w);
+            s = __fadd_rn(s, __fmul_rn(t0, t0));
+            s = __fadd_rn(s, __fmul_rn(t1, t1));
+            s = __fadd_rn(s, __fmul_rn(t2, t2));
+            s = __fadd_rn(s, __fmul_rn(t3, t3));
+        }
+    }
+    for (; j0 < d; j0++) {
+        const float t = __fsub_rn(a[j0], b[j0]);
+        s = __fadd_rn(s, __fmul_rn(t, t));
+    }
+    return s;
+}
+
 // a . b in any order: fused multiply-adds into four partial sums, for ranking
 // only.  Within (d / 4 + 2) u sum|a_j b_j| of the real product (u = 2^-24).
 // b is 16-byte aligned when d % 4 == 0.
