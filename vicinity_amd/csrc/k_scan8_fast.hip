@@ -731,8 +731,118 @@ __device__ __forceinline__ float exact_sub_distance(const float* qm, const float
 // MT, KT, DS: compile-time codebooks, codebook size and subvector dimension
 // (0 = read from the index at run time).  NC > 0: the lists are read from the
 // transposed blocks, with NC copies of the table.
+// Exact distance (the reference's arithmetic, pq_simd.rs:349-355) of the list
+// entry whose code row both lanes half = 0, 1 of a pair hold: lane `half`
+// takes codebooks M/2 half .. (or, DS = 8, codebooks 2t + half, at most TBW
+// codewords' loads in flight), with the residual r = q - c of the entry's
+// probe slot p at res + p * D (LDS); the first lane adds the sub-distances in
+// codebook order from 0.0 and continues with its partner's, handed over by a
+// lane exchange, and returns the distance (the second lane's return value is
+// unused).  Both lanes of every pair must take part.
+template <int MT, int KT, int DS, int TBW>
+__device__ __forceinline__ float fs8_pair_distance(const DevIndex& ix, const float* __restrict__ res,
+                                                   uint32_t p, const CodeRow<MT>& row, uint32_t half) {
+    constexpr int D = MT * DS;
+    constexpr int H = MT / 2;                 // codebooks per thread
+    constexpr int CB0 = 64 / DS;
+    constexpr int CB = CB0 < H ? CB0 : H;     // codewords in flight
+    static_assert(H % CB == 0 && H % 4 == 0, "codebook batches");
+    constexpr int HW = H / 4;                 // code words per half row
+    uint32_t cwd[HW];
+#pragma unroll
+    for (int w = 0; w < HW; w++) cwd[w] = row.w[half * HW + w];
+    float total_e = 0.0f;
+    if constexpr (DS == 8) {
+        // The pair shares its codewords: for codebooks 2t and 2t + 1 lane
+        // `half` loads dims 4 half .. 4 half + 3 of both (the two lanes of a
+        // load read one codeword, one cache access), gives its partner the
+        // half it lacks (lane 0 scores 2t, lane 1 scores 2t + 1) and takes its
+        // residual slice from LDS; lane 0 then adds the scores in codebook
+        // order.  Raw buffer loads at 32-bit offsets.
+        const __amdgpu_buffer_rsrc_t cbr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(ix.codebooks), (short)0, MT * KT * DS * 4, 0x00020000);
+        float ev[MT / 2];  // this lane's codebooks 2t + half
+        const float* rrow = res + (size_t)p * D + half * DS;
+        const uint32_t hoff = half * 16u;
+        constexpr int TB = MT / 2 < TBW ? MT / 2 : TBW;  // codebook pairs whose loads fly together
+#pragma unroll
+        for (int t0 = 0; t0 < MT / 2; t0 += TB) {
+            u32x4 Ab[TB], Bb[TB];
+#pragma unroll
+            for (int tb = 0; tb < TB; tb++) {  // every load of the batch first
+                const int t = t0 + tb;
+                const uint32_t w = row.w[t >> 1];
+                const uint32_t c0 = (w >> (16 * (t & 1))) & 0xffu, c1 = (w >> (16 * (t & 1) + 8)) & 0xffu;
+                Ab[tb] = __builtin_amdgcn_raw_buffer_load_b128(
+                    cbr, c0 * (uint32_t)(DS * 4) + hoff + (uint32_t)(2 * t * KT * DS * 4), 0u, 0);
+                Bb[tb] = __builtin_amdgcn_raw_buffer_load_b128(
+                    cbr, c1 * (uint32_t)(DS * 4) + hoff + (uint32_t)((2 * t + 1) * KT * DS * 4), 0u, 0);
+            }
+#pragma unroll
+            for (int tb = 0; tb < TB; tb++) {
+                const int t = t0 + tb;
+                const u32x4 A = Ab[tb], B = Bb[tb];
+                const u32x4 snd = half ? A : B;
+                u32x4 rcv;
+                rcv.x = (uint32_t)__builtin_amdgcn_mov_dpp((int)snd.x, 0xB1, 0xF, 0xF, true);
+                rcv.y = (uint32_t)__builtin_amdgcn_mov_dpp((int)snd.y, 0xB1, 0xF, 0xF, true);
+                rcv.z = (uint32_t)__builtin_amdgcn_mov_dpp((int)snd.z, 0xB1, 0xF, 0xF, true);
+                rcv.w = (uint32_t)__builtin_amdgcn_mov_dpp((int)snd.w, 0xB1, 0xF, 0xF, true);
+                const u32x4 lo = half ? rcv : A, hi = half ? B : rcv;
+                const float cw[8] = {__uint_as_float(lo.x), __uint_as_float(lo.y), __uint_as_float(lo.z),
+                                     __uint_as_float(lo.w), __uint_as_float(hi.x), __uint_as_float(hi.y),
+                                     __uint_as_float(hi.z), __uint_as_float(hi.w)};
+                const float* r = rrow + (size_t)(2 * t) * DS;  // codebook 2t + half
+                float e = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float diff = __fsub_rn(r[j], cw[j]);
+                    e = __fadd_rn(e, __fmul_rn(diff, diff));
+                }
+                ev[t] = e;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < MT / 2; t++) {  // lane 0: e_2t, then the partner's e_2t+1
+            total_e = __fadd_rn(total_e, ev[t]);
+            total_e = __fadd_rn(total_e, __int_as_float(__builtin_amdgcn_mov_dpp(
+                                             __float_as_int(ev[t]), 0xB1, 0xF, 0xF, true)));
+        }
+    } else {
+    float ev[H];
+    const float* rrow = res + (size_t)p * D + half * H * DS;
+#pragma unroll
+    for (int h0 = 0; h0 < H; h0 += CB) {
+        float wv[CB][DS];
+#pragma unroll
+        for (int b = 0; b < CB; b++) {
+            const int h = h0 + b, m = (int)half * H + h;
+            const uint32_t code = (cwd[h >> 2] >> (8 * (h & 3))) & 0xffu;
+            load_vec<DS>(ix.codebooks + ((size_t)m * KT + code) * DS, wv[b]);
+        }
+#pragma unroll
+        for (int b = 0; b < CB; b++) {
+            float e = 0.0f;
+#pragma unroll
+            for (int j = 0; j < DS; j++) {
+                const float diff = __fsub_rn(rrow[(h0 + b) * DS + j], wv[b][j]);
+                e = __fadd_rn(e, __fmul_rn(diff, diff));
+            }
+            ev[h0 + b] = e;
+        }
+    }
+    // codebooks 0 .. H - 1 (first thread)
+#pragma unroll
+    for (int h = 0; h < H; h++) total_e = __fadd_rn(total_e, ev[h]);
+#pragma unroll
+    for (int h = 0; h < H; h++)  // then the partner's H .. M - 1
+        total_e = __fadd_rn(total_e, __uint_as_float(shfl_xor_u32(__float_as_uint(ev[h]), 1)));
+    }
+    return total_e;
+}
+
 template <int MT, int KT, int DS, int NC>
-__global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a, int buf) {
+__global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArgs a, int buf) {
     constexpr bool TR = NC > 0;
     static_assert(!TR || (MT % 16 == 0 && KT == 256 && DS > 0), "transposed blocks");
     constexpr bool kStatic = MT > 0 && KT >= 64;
@@ -1107,18 +1217,34 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     if (fail) return;
     // The table is no longer needed: the residuals r = q - c of the probed
     // lists go to its region now (their loads overlap the compaction) when
-    // the two-thread rescoring below may use them.
+    // the two-thread rescoring below may use them.  Thread t stages
+    // dimensions 4 (t % (D / 4)) .. + 3 of slots t / (D / 4), + SPT, ...: the
+    // slot ids are read first and every centroid load is in flight at once
+    // (a store to the table region could otherwise hold back the next id read).
     if constexpr ((MT == 8 || MT == 16 || MT == 32) && KT > 0 && DS > 0) {
         if ((size_t)P * D <= (size_t)LUTF) {
-            for (int e = tid; e < P * (D / 4); e += VGPU_BLOCK) {
-                const int pp = e / (D / 4), j = 4 * (e % (D / 4));
-                const float4 c = *reinterpret_cast<const float4*>(ix.centroids + (size_t)s.lid[pp] * D + j);
-                const float4 qv = *reinterpret_cast<const float4*>(a.qn + (size_t)q * D + j);
-                float* o = s.lut + pp * D + j;
-                o[0] = __fsub_rn(qv.x, c.x);
-                o[1] = __fsub_rn(qv.y, c.y);
-                o[2] = __fsub_rn(qv.z, c.z);
-                o[3] = __fsub_rn(qv.w, c.w);
+            constexpr int SPT = VGPU_BLOCK / (D / 4);         // slots per pass
+            constexpr int SMAX = (LUTF / D + SPT - 1) / SPT;  // passes for P D <= LUTF
+            static_assert(VGPU_BLOCK % (D / 4) == 0, "staging split");
+            const int j = 4 * (tid % (D / 4)), pp0 = tid / (D / 4);
+            uint32_t lr[SMAX];
+#pragma unroll
+            for (int it = 0; it < SMAX; it++) lr[it] = pp0 + it * SPT < P ? s.lid[pp0 + it * SPT] : 0u;
+            const float4 qv = *reinterpret_cast<const float4*>(a.qn + (size_t)q * D + j);
+            float4 c[SMAX];
+#pragma unroll
+            for (int it = 0; it < SMAX; it++)
+                if (pp0 + it * SPT < P) c[it] = *reinterpret_cast<const float4*>(ix.centroids + (size_t)lr[it] * D + j);
+#pragma unroll
+            for (int it = 0; it < SMAX; it++) {
+                const int pp = pp0 + it * SPT;
+                if (pp < P) {
+                    float* o = s.lut + pp * D + j;
+                    o[0] = __fsub_rn(qv.x, c[it].x);
+                    o[1] = __fsub_rn(qv.y, c[it].y);
+                    o[2] = __fsub_rn(qv.z, c[it].z);
+                    o[3] = __fsub_rn(qv.w, c[it].w);
+                }
             }
         }
     }
@@ -1135,114 +1261,15 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     if constexpr (MT == 8 || MT == 16 || MT == 32) {
         if constexpr (KT > 0 && DS > 0) {
             if ((size_t)P * D <= (size_t)LUTF && n <= (uint32_t)(VGPU_BLOCK / 2)) {
-                constexpr int H = MT / 2;                 // codebooks per thread
-                constexpr int CB0 = 64 / DS;
-                constexpr int CB = CB0 < H ? CB0 : H;     // codewords in flight
-                static_assert(H % CB == 0 && H % 4 == 0, "codebook batches");
-                constexpr int HW = H / 4;                 // code words per half row
                 const uint32_t i = (uint32_t)tid >> 1, half = (uint32_t)tid & 1u;
                 const bool act = i < n;
                 const uint64_t v = act ? s.keys[i] : 0ull;
-                const uint32_t pos = (uint32_t)v, p = (uint32_t)(v >> 32);
-                uint32_t cwd[HW];
-#pragma unroll
-                for (int w = 0; w < HW; w++) cwd[w] = 0u;
-                const uint32_t vid = act && half == 0 ? ix.list_ids[pos] : 0u;
-                CodeRow<MT> row;  // DS == 8: both lanes of the pair hold the whole row
-                if constexpr (DS == 8) load_row<MT>(row, ix.codes + (size_t)pos * MT);
-                if (DS != 8 && act) {
-                    const uint8_t* cp = ix.codes + (size_t)pos * MT + half * H;
-                    if constexpr (HW == 1) cwd[0] = *reinterpret_cast<const uint32_t*>(cp);
-                    else if constexpr (HW == 2) {
-                        const uint2 x = *reinterpret_cast<const uint2*>(cp);
-                        cwd[0] = x.x; cwd[1] = x.y;
-                    } else {
-                        const uint4 x = *reinterpret_cast<const uint4*>(cp);
-                        cwd[0] = x.x; cwd[1] = x.y; cwd[2] = x.z; cwd[3] = x.w;
-                    }
-                }
-                float total_e = 0.0f;
-                if constexpr (DS == 8) {
-                    // The pair shares its codewords: for codebooks 2t and 2t + 1
-                    // lane `half` loads dims 4 half .. 4 half + 3 of both (one
-                    // sector each, read by the two lanes together), gives its
-                    // partner the half it lacks (lane 0 scores 2t, lane 1 scores
-                    // 2t + 1), and lane 0 adds the scores in codebook order.
-                    // Both lanes hold the full code row.
-                    float ev[MT / 2];  // this lane's codebooks 2t + half
-                    const float* rrow = s.lut + (size_t)p * D + half * DS;
-                    constexpr int TB = MT / 2 < 4 ? MT / 2 : 4;  // codebook pairs whose loads fly together
-#pragma unroll
-                    for (int t0 = 0; t0 < MT / 2; t0 += TB) {
-                    float4 Ab[TB], Bb[TB];
-#pragma unroll
-                    for (int tb = 0; tb < TB; tb++) {  // every load of the batch first
-                        const int t = t0 + tb;
-                        const uint32_t w = row.w[t >> 1];
-                        const uint32_t c0 = (w >> (16 * (t & 1))) & 0xffu, c1 = (w >> (16 * (t & 1) + 8)) & 0xffu;
-                        Ab[tb] = *reinterpret_cast<const float4*>(
-                            ix.codebooks + ((size_t)(2 * t) * KT + c0) * DS + 4 * half);
-                        Bb[tb] = *reinterpret_cast<const float4*>(
-                            ix.codebooks + ((size_t)(2 * t + 1) * KT + c1) * DS + 4 * half);
-                    }
-#pragma unroll
-                    for (int tb = 0; tb < TB; tb++) {
-                        const int t = t0 + tb;
-                        const float4 A = Ab[tb], B = Bb[tb];
-                        const float4 snd = half ? A : B;
-                        float4 rcv;
-                        rcv.x = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(snd.x), 0xB1, 0xF, 0xF, true));
-                        rcv.y = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(snd.y), 0xB1, 0xF, 0xF, true));
-                        rcv.z = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(snd.z), 0xB1, 0xF, 0xF, true));
-                        rcv.w = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(snd.w), 0xB1, 0xF, 0xF, true));
-                        const float4 lo = half ? rcv : A, hi = half ? B : rcv;
-                        const float cw[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-                        const float* r = rrow + (size_t)(2 * t) * DS;  // codebook 2t + half
-                        float e = 0.0f;
-#pragma unroll
-                        for (int j = 0; j < 8; j++) {
-                            const float diff = __fsub_rn(r[j], cw[j]);
-                            e = __fadd_rn(e, __fmul_rn(diff, diff));
-                        }
-                        ev[t] = e;
-                    }
-                    }
-#pragma unroll
-                    for (int t = 0; t < MT / 2; t++) {  // lane 0: e_2t, then the partner's e_2t+1
-                        total_e = __fadd_rn(total_e, ev[t]);
-                        total_e = __fadd_rn(total_e, __int_as_float(__builtin_amdgcn_mov_dpp(
-                                                         __float_as_int(ev[t]), 0xB1, 0xF, 0xF, true)));
-                    }
-                } else {
-                float ev[H];
-                const float* rrow = s.lut + (size_t)p * D + half * H * DS;
-#pragma unroll
-                for (int h0 = 0; h0 < H; h0 += CB) {
-                    float wv[CB][DS];
-#pragma unroll
-                    for (int b = 0; b < CB; b++) {
-                        const int h = h0 + b, m = (int)half * H + h;
-                        const uint32_t code = (cwd[h >> 2] >> (8 * (h & 3))) & 0xffu;
-                        load_vec<DS>(ix.codebooks + ((size_t)m * KT + code) * DS, wv[b]);
-                    }
-#pragma unroll
-                    for (int b = 0; b < CB; b++) {
-                        float e = 0.0f;
-#pragma unroll
-                        for (int j = 0; j < DS; j++) {
-                            const float diff = __fsub_rn(rrow[(h0 + b) * DS + j], wv[b][j]);
-                            e = __fadd_rn(e, __fmul_rn(diff, diff));
-                        }
-                        ev[h0 + b] = e;
-                    }
-                }
-                // codebooks 0 .. H - 1 (first thread)
-#pragma unroll
-                for (int h = 0; h < H; h++) total_e = __fadd_rn(total_e, ev[h]);
-#pragma unroll
-                for (int h = 0; h < H; h++)  // then the partner's H .. M - 1
-                    total_e = __fadd_rn(total_e, __uint_as_float(shfl_xor_u32(__float_as_uint(ev[h]), 1)));
-                }
+                const uint32_t vid = act && half == 0 ? ix.list_ids[(uint32_t)v] : 0u;
+                CodeRow<MT> row;  // both lanes of the pair hold the whole row (entry 0 when inactive)
+                load_row<MT>(row, ix.codes + (size_t)(uint32_t)v * MT);
+                // fewer codewords in flight for wide rows (registers)
+                const float total_e = fs8_pair_distance<MT, KT, DS, MT <= 16 ? 4 : 2>(
+                    ix, s.lut, (uint32_t)(v >> 32), row, half);
                 __syncthreads();  // every key of R read above before any is rewritten
                 if (act && half == 0) s.keys[i] = cand_key(total_e, vid);
                 __syncthreads();
@@ -1295,34 +1322,34 @@ __global__ __launch_bounds__(256) void scan8_fast_kernel(DevIndex ix, ScanArgs a
     }
     }
 rescored:
-    if (n <= 256) {  // one wave sorts in registers; no block barriers below
-        if (tid >= 64) return;
-        auto emit = [&](int j, uint64_t key) { scan_emit(a, q, j, key, (uint32_t)j < n); };
-        int done = 64;
-        if (n <= 64) {
-            uint64_t k1[1] = {(uint32_t)lane < n ? s.keys[lane] : ~0ull};
-            wave_sort_regs<1>(k1);
-            if (lane < kout) emit(lane, k1[0]);
-        } else if (n <= 128) {
-            uint64_t k2[2];
-#pragma unroll
-            for (int e = 0; e < 2; e++) k2[e] = (uint32_t)(e * 64 + lane) < n ? s.keys[e * 64 + lane] : ~0ull;
-            wave_sort_regs<2>(k2);
-#pragma unroll
-            for (int e = 0; e < 2; e++)
-                if (e * 64 + lane < kout) emit(e * 64 + lane, k2[e]);
-            done = 128;
-        } else {
-            uint64_t k4[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) k4[e] = (uint32_t)(e * 64 + lane) < n ? s.keys[e * 64 + lane] : ~0ull;
-            wave_sort_regs<4>(k4);
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (e * 64 + lane < kout) emit(e * 64 + lane, k4[e]);
-            done = 256;
+    if (n <= (uint32_t)VGPU_BLOCK) {
+        // Each thread takes one key and writes it at its position in the
+        // ascending order, the number of smaller keys (the keys are distinct:
+        // one per vector); its doc id load flies during the count.
+        if (tid == 0 && (n & 1u)) s.keys[n] = ~0ull;  // even count for the pairwise reads; above every key
+        __syncthreads();
+        if ((uint32_t)tid < n) {
+            const uint64_t ki = s.keys[tid];
+            const uint32_t vi = (uint32_t)ki;
+            const uint32_t doc = a.out_ids && a.doc_ids ? a.doc_ids[vi] : vi;
+            uint32_t r = 0;
+#pragma unroll 8
+            for (uint32_t jj = 0; jj < n; jj += 2) {
+                const ulonglong2 kj = *reinterpret_cast<const ulonglong2*>(s.keys + jj);
+                r += (kj.x < ki ? 1u : 0u) + (kj.y < ki ? 1u : 0u);
+            }
+            if (r < (uint32_t)kout) {
+                const size_t o = (size_t)q * kout + r;
+                if (a.out_ids) {
+                    a.out_ids[o] = (int64_t)doc;
+                    a.out_dists[o] = key_dist(ki);
+                } else {
+                    a.out_vidx[o] = vi;
+                    a.out_dist[o] = key_dist(ki);
+                }
+            }
         }
-        for (int j = done + lane; j < kout; j += 64) emit(j, ~0ull);  // j >= n: padding
+        for (int j = (int)n + tid; j < kout; j += VGPU_BLOCK) scan_emit(a, q, j, ~0ull, false);  // padding
         return;
     }
     const int n2 = next_pow2((int)n);
@@ -1411,5 +1438,6 @@ void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hip
     }
     launch_fast<0, 0, 0, 0>(ix, a, s, t0, t1);
 }
+
 
 }  // namespace vgpu
