@@ -750,7 +750,7 @@ __device__ __forceinline__ float fs8_pair_distance(const DevIndex& ix, const flo
     constexpr int HW = H / 4;                 // code words per half row
     uint32_t cwd[HW];
 #pragma unroll
-    for (int w = 0; w < HW; w++) cwd[w] = row.w[half * HW + w];
+    for (int w = 0; w < HW; w++) cwd[w] = half ? row.w[HW + w] : row.w[w];  // no dynamic register index
     float total_e = 0.0f;
     if constexpr (DS == 8) {
         // The pair shares its codewords: for codebooks 2t and 2t + 1 lane
@@ -858,80 +858,101 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
     FastLds s = fs8_carve(smem, kStatic ? slut : nullptr, d, M, K, P, buf);
 
     // ---- prologue: query, probed lists, ||q - c||^2, the per-query table.
-    for (int j = tid; j < d; j += VGPU_BLOCK) s.qs[j] = a.qn[(size_t)q * d + j];
-    for (int p = tid; p < P; p += VGPU_BLOCK) {
-        const uint32_t l = a.probe[(size_t)q * P + p];
+    // Round trip 1: the thread's first probed slot and (blocks) the query
+    // slices and first codebook lines of the table; round trip 2: that slot's
+    // list record with the next codebook lines.  Slots past the first 256 are
+    // read afterwards.
+    const uint32_t l0id = tid < P ? a.probe[(size_t)q * P + tid] : 0u;
+    // a probed slot's list record (list, begin, end, block offset): loads,
+    // then (once they are back) LDS stores
+    uint32_t rl = 0, rb = 0, re = 0, rt = 0;
+    auto rec_load = [&](uint32_t l) {
         const bool ok = l < (uint32_t)ix.L;  // no such list: scanned as empty
-        const uint32_t b = ok ? ix.offsets[l] : 0u;
-        s.lid[p] = ok ? l : 0u;
-        s.lbeg[p] = b;
-        s.llen[p] = ok ? ix.offsets[l + 1] - b : 0u;
-        if constexpr (TR) s.tbo[p] = ok ? ix.tblk_off[l] : 0u;
-    }
+        rl = ok ? l : 0u;
+        rb = ok ? ix.offsets[l] : 0u;
+        re = ok ? ix.offsets[l + 1] : 0u;
+        if constexpr (TR) rt = ok ? ix.tblk_off[l] : 0u;
+    };
+    auto rec_store = [&](int p) {
+        s.lid[p] = rl;
+        s.lbeg[p] = rb;
+        s.llen[p] = re - rb;
+        if constexpr (TR) s.tbo[p] = rt;
+    };
     if (tid < 32) s.misc[tid] = tid == 8 ? 0xffffffffu : 0u;  // counts 0, no bound yet
     if constexpr (TR) {
         // T2[m][k] = -2 q_m . cw_mk (ranking only: FMA allowed), built before
-        // the first barrier from the query in global memory, so its codeword
-        // loads overlap the probed-list loads.  Every load instruction reads
-        // one whole 64-byte line of each of 16 codebooks: lane (m16, j) =
-        // (lane / 4, lane % 4) reads bytes 16 j .. 16 j + 15 of line `sp` of
-        // codebook 16 gi + m16, which hold CPS = 16 / DS codewords.  With
-        // DS = 8 a codeword spans two lanes, whose partial dot products meet
-        // by a lane exchange; its even lane writes it.  The waves take the
-        // lines in turn.
+        // the first barrier from the query in global memory.  Every load
+        // instruction reads one whole 64-byte line of each of 16 codebooks:
+        // lane (m16, j) = (lane / 4, lane % 4) reads bytes 16 j .. 16 j + 15
+        // of line `sp` of codebook 16 gi + m16, which hold CPS = 16 / DS
+        // codewords.  With DS = 8 a codeword spans two lanes, whose partial
+        // dot products meet by a lane exchange; its even lane writes it.  The
+        // waves take the lines in turn, in batches of LB lines whose loads fly
+        // together; batch b + 1 is issued once batch b is consumed.
         static_assert(DS == 2 || DS == 4 || DS == 8, "subvector width");
         constexpr int CPS = 16 / DS;              // codewords per line
         constexpr int LINES = KT / CPS;           // lines per codebook
         constexpr int LW = LINES / (VGPU_BLOCK / 64);  // lines per wave and codebook
-        constexpr int LB = LW < 16 ? LW : 16;     // lines whose loads fly together
+        constexpr int LB = LW < 8 ? LW : 8;       // lines whose loads fly together
         static_assert(LW % LB == 0, "line batches");
+        constexpr int NGI = MT / 16, NBL = LW / LB;
         const int m16 = lane >> 2, j = lane & 3;
         const int wv_ = (int)__builtin_amdgcn_readfirstlane((uint32_t)tid >> 6);
-#pragma unroll 1
-        for (int gi = 0; gi < MT / 16; gi++) {
+        // the query values this lane multiplies for each codebook group
+        float qv[NGI][4];
+#pragma unroll
+        for (int gi = 0; gi < NGI; gi++) {
             const int m = gi * 16 + m16;
-            // the query values this lane multiplies, scaled by -2 (exact), so
-            // the dot products below are the table entries themselves
-            float qv[4];
-            if constexpr (DS == 8) load_vec<4>(a.qn + (size_t)q * D + m * 8 + 4 * (j & 1), qv);
-            else if constexpr (DS == 4) load_vec<4>(a.qn + (size_t)q * D + m * 4, qv);
+            if constexpr (DS == 8) load_vec<4>(a.qn + (size_t)q * D + m * 8 + 4 * (j & 1), qv[gi]);
+            else if constexpr (DS == 4) load_vec<4>(a.qn + (size_t)q * D + m * 4, qv[gi]);
             else {
-                load_vec<2>(a.qn + (size_t)q * D + m * 2, qv);
-                qv[2] = qv[0];
-                qv[3] = qv[1];
+                load_vec<2>(a.qn + (size_t)q * D + m * 2, qv[gi]);
+                qv[gi][2] = qv[gi][0];
+                qv[gi][3] = qv[gi][1];
             }
+        }
+        // line sp = (l0 + i) * 4 + wv_ of group gi: a wave-uniform base, the
+        // lane's fixed byte offset, and a constant step per line
+        const uint32_t lo = (uint32_t)(m16 * KT * DS + 4 * j) * 4u;
+        float4 w[LB];
+        auto batch = [&](int gi, int l0) {
+            const char* cbl = reinterpret_cast<const char*>(ix.codebooks + (size_t)(gi * 16) * KT * DS +
+                                                            (size_t)wv_ * 16) +
+                              (size_t)l0 * (VGPU_BLOCK / 64) * 64;  // wave-uniform
 #pragma unroll
-            for (int i = 0; i < 4; i++) qv[i] = -2.0f * qv[i];
-            // line sp = (l0 + i) * 4 + wv_: a wave-uniform base, the lane's
-            // fixed byte offset, and a constant step per line
-            const char* cbw = reinterpret_cast<const char*>(ix.codebooks + (size_t)(gi * 16) * KT * DS +
-                                                            (size_t)wv_ * 16);
-            const uint32_t lo = (uint32_t)(m16 * KT * DS + 4 * j) * 4u;
+            for (int i = 0; i < LB; i++)
+                w[i] = *reinterpret_cast<const float4*>(cbl + lo + i * (VGPU_BLOCK / 64) * 64);
+        };
+        batch(0, 0);
+        if (tid < P) rec_load(l0id);  // in flight with the next batch; stored after its issue
+#pragma unroll
+        for (int gi = 0; gi < NGI; gi++) {
+            // scaled by -2 (exact), so the dot products below are the table entries themselves
+            float qg[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) qg[i] = -2.0f * qv[gi][i];
 #pragma unroll 1
-            for (int l0 = 0; l0 < LW; l0 += LB) {
-                const char* cbl = cbw + (size_t)l0 * (VGPU_BLOCK / 64) * 64;  // wave-uniform
-                float4 w[LB];
-#pragma unroll
-                for (int i = 0; i < LB; i++)
-                    w[i] = *reinterpret_cast<const float4*>(cbl + lo + i * (VGPU_BLOCK / 64) * 64);
+            for (int bl = 0; bl < NBL; bl++) {
+                const int l0 = bl * LB;
                 // table row of line l0 * 4 + wv_; line i of the batch is 4 i CPS rows on
                 float* tl = slut + (gi * KT + (l0 * (VGPU_BLOCK / 64) + wv_) * CPS) * NC * 16 + m16;
 #pragma unroll
                 for (int i = 0; i < LB; i++) {
                     float* ti = tl + i * (VGPU_BLOCK / 64) * CPS * NC * 16;  // row sp * CPS
                     if constexpr (DS == 2) {
-                        const float d0 = __builtin_fmaf(qv[1], w[i].y, qv[0] * w[i].x);
-                        const float d1 = __builtin_fmaf(qv[3], w[i].w, qv[2] * w[i].z);
+                        const float d0 = __builtin_fmaf(qg[1], w[i].y, qg[0] * w[i].x);
+                        const float d1 = __builtin_fmaf(qg[3], w[i].w, qg[2] * w[i].z);
 #pragma unroll
                         for (int c = 0; c < NC; c++) {
                             ti[(2 * j * NC + c) * 16] = d0;
                             ti[((2 * j + 1) * NC + c) * 16] = d1;
                         }
                     } else {
-                        float dp = qv[0] * w[i].x;
-                        dp = __builtin_fmaf(qv[1], w[i].y, dp);
-                        dp = __builtin_fmaf(qv[2], w[i].z, dp);
-                        dp = __builtin_fmaf(qv[3], w[i].w, dp);
+                        float dp = qg[0] * w[i].x;
+                        dp = __builtin_fmaf(qg[1], w[i].y, dp);
+                        dp = __builtin_fmaf(qg[2], w[i].z, dp);
+                        dp = __builtin_fmaf(qg[3], w[i].w, dp);
                         int kj = j;  // codeword of the line
                         if constexpr (DS == 8) {
                             dp = add_dpp<0xB1>(dp, dp);  // + the partner half (lane j ^ 1)
@@ -944,8 +965,36 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
                         }
                     }
                 }
+                if (bl + 1 < NBL) batch(gi, l0 + LB);
+                else if (gi + 1 < NGI) batch(gi + 1, 0);
+                if (gi == 0 && bl == 0 && tid < P) rec_store(tid);
             }
         }
+        // the query itself from the slices just loaded: wave 0's lanes with
+        // j < 2 (DS = 8) or j = 0 hold each dimension once
+        if (tid < 64 && (DS == 8 ? j < 2 : j == 0)) {
+#pragma unroll
+            for (int gi = 0; gi < NGI; gi++) {
+                const int m = gi * 16 + m16;
+                if constexpr (DS == 8) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) s.qs[m * 8 + 4 * j + i] = qv[gi][i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < DS; i++) s.qs[m * DS + i] = qv[gi][i];
+                }
+            }
+        }
+    } else {
+        if (tid < P) {
+            rec_load(l0id);
+            rec_store(tid);
+        }
+        for (int jj = tid; jj < d; jj += VGPU_BLOCK) s.qs[jj] = a.qn[(size_t)q * d + jj];
+    }
+    for (int p = tid + VGPU_BLOCK; p < P; p += VGPU_BLOCK) {
+        rec_load(a.probe[(size_t)q * P + p]);
+        rec_store(p);
     }
     __syncthreads();
     if (tid < 64) {  // exclusive prefix of the list lengths (whole blocks when transposed)
