@@ -45,15 +45,15 @@ def log(msg):
 
 def traffic_from_profile(name):
     """HBM bytes per scan launch from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary profiles/<kernel>_<workload>_traffic.md (calibrated
-    against a copy kernel), or None."""
-    path = os.path.join(ROOT, "profiles", f"{name}_traffic.md")
-    try:
-        for line in open(path):
-            if line.startswith("traffic_bytes_per_launch"):
-                return int(line.split("=")[1])
-    except OSError:
-        pass
+    WRITE_SIZE summary profiles/<kernel>_<workload>_traffic.md or
+    profiles/<kernel>_<workload>.md (calibrated against a copy kernel), or None."""
+    for fname in (f"{name}_traffic.md", f"{name}.md"):
+        try:
+            for line in open(os.path.join(ROOT, "profiles", fname)):
+                if line.startswith("traffic_bytes_per_launch"):
+                    return int(line.split("=")[1])
+        except OSError:
+            pass
     return None
 
 
@@ -185,7 +185,7 @@ def run_ivfpq(args, w):
     # roofline's launch duration); the per-phase breakdown comes from a
     # separate, untimed pass with every-phase events.
     ix.set_profiling(2)
-    k, nprobe, pool = p["k"], p["nprobe"], p.get("rerank_pool")
+    k, nprobe, pool = p["k"], args.nprobe or p["nprobe"], p.get("rerank_pool")
     nq = w.queries.shape[0]
     q = torch.from_numpy(w.queries).to("cuda:0")
     out_ids = torch.empty((nq, k), dtype=torch.int64, device="cuda:0")
@@ -370,6 +370,8 @@ def main():
     ap.add_argument("--n", type=int, default=None, help="base vectors (default: the workload's)")
     ap.add_argument("--train-sample", type=int, default=None)
     ap.add_argument("--kmeans-iters", type=int, default=None)
+    ap.add_argument("--nprobe", type=int, default=None,
+                    help="probed lists per query (default: the workload's; other values are profiling runs)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-recall", action="store_true")
     ap.add_argument("--opq", action="store_true",
