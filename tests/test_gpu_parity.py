@@ -448,3 +448,32 @@ def test_probe_ties_through_the_exact_fallback(vg, oracle, step, copies, P):
     oix = oracle.Index(cent, cb, off, ids, codes, np.arange(n, dtype=np.uint32), None, M, K)
     for i in range(len(q)):
         assert lists[i].tolist() == oix.probe(q[i], P)[0].tolist(), i
+
+
+def test_many_flagged_probe_queries(vg, oracle):
+    """More queries through the coarse exact fallback than its grid-wide
+    path takes (64): 100 queries near a centroid copied 12 times in one lane's
+    column class, among 60 ordinary queries, over 2000 lists (8 slices of
+    256).  Probe lists equal the oracle's, in order."""
+    from vicinity_amd import IVFPQIndex
+
+    _print_case("probe ties: 100 flagged queries of 160, L 2000")
+    d, L, P, copies = 32, 2000, 16, 12
+    rng = np.random.default_rng(77)
+    cent = oracle.normalize_rows(rng.standard_normal((L, d)).astype(np.float32))
+    base = cent[1].copy()
+    cent[5 + 16 * np.arange(copies)] = base
+    n = 2 * L
+    M, K = 4, 16
+    cb = rng.standard_normal(M * K * (d // M)).astype(np.float32)
+    off, ids = oracle.build_lists((np.arange(n) % L).astype(np.uint32), L)
+    codes = rng.integers(0, K, (n, M), dtype=np.uint8)
+    ix = IVFPQIndex(d, num_clusters=L, num_codebooks=M, codebook_size=K, nprobe=P)
+    ix.load_artifacts(cent, cb, off, ids, codes)
+    near = (base[None, :] + 0.01 * rng.standard_normal((100, d))).astype(np.float32)
+    q = np.concatenate([near[:50], rng.standard_normal((60, d)).astype(np.float32), near[50:]])
+    oix = oracle.Index(cent, cb, off, ids, codes, np.arange(n, dtype=np.uint32), None, M, K)
+    for rep in range(2):  # the second call reuses the slice counters the first one reset
+        lists = ix.probe(q, P)
+        for i in range(len(q)):
+            assert lists[i].tolist() == oix.probe(q[i], P)[0].tolist(), (rep, i)

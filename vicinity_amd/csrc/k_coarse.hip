@@ -296,17 +296,47 @@ __global__ __launch_bounds__(256) void coarse_select_reg_kernel(
 // Queries whose fused-kernel candidate set may be incomplete (a lane's key
 // list overflowed: many lists tie or crowd the window): approximate dot
 // products of all L lists (approx_dot, within the same bound coarse_tau
-// covers) go to LDS, then the block selection (window, exact rescoring)
-// runs on them.  The grid walks the flagged list.
+// covers), then the block selection (window, exact rescoring) on them.
+// With a scratch row per query (fdots, COARSE_FLAG_PAR rows of L), the first
+// COARSE_FLAG_PAR flagged queries spread their dot products over the grid in
+// slices of 256 lists; the workgroup that finishes a query's last slice
+// (counted in fdone[fi], which it resets) runs the selection on the row.
+// Flagged queries past those, or all of them without scratch, are one
+// workgroup each: their dot products go to LDS.  The grid walks the flagged
+// list.
 template <int EPT>
 __global__ __launch_bounds__(256) void coarse_exact_flagged_kernel(
     const float* __restrict__ qn, const float* __restrict__ qnorm, const float* __restrict__ C, int L,
     int d, int P, float cmax, uint32_t* __restrict__ probe, unsigned int* overflow,
-    const uint32_t* flag_list, const uint32_t* flag_count) {
+    const uint32_t* flag_list, const uint32_t* flag_count, float* __restrict__ fdots, uint32_t* fdone) {
     extern __shared__ __align__(16) float qs[];  // [d rounded up to 4] query, then [L] dots
+    __shared__ uint32_t last;
     float* xrow = qs + ((d + 3) & ~3);
     const uint32_t nf = *flag_count;  // written by the top-P kernel before this launch
-    for (uint32_t fi = blockIdx.x; fi < nf; fi += gridDim.x) {
+    const uint32_t npar = fdots ? (nf < COARSE_FLAG_PAR ? nf : COARSE_FLAG_PAR) : 0u;
+    const int S = (L + VGPU_BLOCK - 1) / VGPU_BLOCK;  // slices of 256 lists
+    for (uint32_t it = blockIdx.x; it < npar * (uint32_t)S; it += gridDim.x) {
+        __syncthreads();
+        const uint32_t fi = it / (uint32_t)S;
+        const int c = (int)(it % (uint32_t)S) * VGPU_BLOCK + threadIdx.x;
+        const int q = (int)flag_list[fi];
+        for (int j = threadIdx.x; j < d; j += VGPU_BLOCK) qs[j] = qn[(size_t)q * d + j];
+        __syncthreads();
+        float* row = fdots + (size_t)fi * L;
+        if (c < L) row[c] = approx_dot(qs, C + (size_t)c * d, d);
+        __threadfence();  // the slice is visible before it is counted
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            last = atomicAdd(&fdone[fi], 1u) == (uint32_t)(S - 1) ? 1u : 0u;
+            if (last) atomicExch(&fdone[fi], 0u);  // every slice counted: ready for the next launch
+        }
+        __syncthreads();
+        if (last) {
+            __threadfence();  // the other workgroups' slices
+            select_block_query<EPT>(row, qs, qnorm[q], C, q, L, d, P, cmax, probe, overflow);
+        }
+    }
+    for (uint32_t fi = npar + blockIdx.x; fi < nf; fi += gridDim.x) {
         __syncthreads();
         const int q = (int)flag_list[fi];
         for (int j = threadIdx.x; j < d; j += VGPU_BLOCK) qs[j] = qn[(size_t)q * d + j];
@@ -328,23 +358,25 @@ __global__ __launch_bounds__(256) void coarse_exact_flagged_kernel(
 
 void launch_coarse_exact_flagged(const float* qn, const float* qnorm, const float* C, int nq, int L,
                                  int d, int P, float cmax, uint32_t* probe, unsigned int* overflow,
-                                 const uint32_t* flag_list, const uint32_t* flag_count, hipStream_t s) {
+                                 const uint32_t* flag_list, const uint32_t* flag_count, hipStream_t s,
+                                 float* fdots, uint32_t* fdone) {
     if (nq <= 0) return;
     const size_t lds = ((size_t)L + ((d + 3) & ~3)) * sizeof(float);
     // flagged queries are rare: a small grid keeps the usual empty launch cheap
-    const dim3 grid(nq < 64 ? nq : 64);
+    const int gmax = fdots ? 256 : 64;
+    const dim3 grid(nq < gmax ? nq : gmax);
     if (L <= 16 * VGPU_BLOCK) {
         ensure_dyn_lds((const void*)coarse_exact_flagged_kernel<16>, lds);
         hipLaunchKernelGGL(coarse_exact_flagged_kernel<16>, grid, dim3(256), lds, s, qn, qnorm, C, L, d, P,
-                           cmax, probe, overflow, flag_list, flag_count);
+                           cmax, probe, overflow, flag_list, flag_count, fdots, fdone);
     } else if (L <= 32 * VGPU_BLOCK) {
         ensure_dyn_lds((const void*)coarse_exact_flagged_kernel<32>, lds);
         hipLaunchKernelGGL(coarse_exact_flagged_kernel<32>, grid, dim3(256), lds, s, qn, qnorm, C, L, d, P,
-                           cmax, probe, overflow, flag_list, flag_count);
+                           cmax, probe, overflow, flag_list, flag_count, fdots, fdone);
     } else {
         ensure_dyn_lds((const void*)coarse_exact_flagged_kernel<64>, lds);
         hipLaunchKernelGGL(coarse_exact_flagged_kernel<64>, grid, dim3(256), lds, s, qn, qnorm, C, L, d, P,
-                           cmax, probe, overflow, flag_list, flag_count);
+                           cmax, probe, overflow, flag_list, flag_count, fdots, fdone);
     }
 }
 

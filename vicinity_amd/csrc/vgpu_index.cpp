@@ -719,6 +719,7 @@ size_t IvfpqIndex::ws_layout(const SearchPlan& pl, uint8_t* base, WsPtrs* out) c
     if (pl.fused) {
         carve(w.cand, c * (size_t)coarse_fused_cap((int)pl.P));
         carve(w.cand_n, c);
+        carve(w.fdots, (size_t)COARSE_FLAG_PAR * L);
     } else if (pl.P) {
         carve(w.dots, c * L);
     }
@@ -754,7 +755,8 @@ void IvfpqIndex::coarse_probe(const float* d_q, size_t nq, size_t P, const Searc
         launch_coarse_topp(w.cand, w.cand_n, (int)P, w.qn, d_centroids.p, (int)nq, (int)L, (int)d, w.probe,
                            w.cflag_list, cflag_count, s);
         launch_coarse_exact_flagged(w.qn, w.qnorm, d_centroids.p, (int)nq, (int)L, (int)d, (int)P, dix.cmax,
-                                    w.probe, overflow, w.cflag_list, cflag_count, s);
+                                    w.probe, overflow, w.cflag_list, cflag_count, s, w.fdots,
+                                    reinterpret_cast<uint32_t*>(w.scal + kFDoneWord));
     } else if (P > 1024) {  // every list's exact score, then the P smallest
         launch_normalize(d_q, w.qn, w.qnorm, (int)nq, (int)d, s);
         if (mid) VGPU_HIP(hipEventRecord(mid, s));

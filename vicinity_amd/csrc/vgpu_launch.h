@@ -122,9 +122,14 @@ void launch_coarse_topp(const uint32_t* cand, const uint32_t* cand_n, int P, con
                         const float* C, int nq, int L, int d, uint32_t* probe, uint32_t* flag_list,
                         uint32_t* flag_count, hipStream_t s);
 // Exact probe selection for the flagged queries (dot products in LDS).
+// fdots (COARSE_FLAG_PAR rows of L floats) and fdone (COARSE_FLAG_PAR zeroed
+// counters) spread the first flagged queries' dot products over the grid;
+// null: one workgroup per flagged query.
+#define COARSE_FLAG_PAR 64
 void launch_coarse_exact_flagged(const float* qn, const float* qnorm, const float* C, int nq, int L,
                                  int d, int P, float cmax, uint32_t* probe, unsigned int* overflow,
-                                 const uint32_t* flag_list, const uint32_t* flag_count, hipStream_t s);
+                                 const uint32_t* flag_list, const uint32_t* flag_count, hipStream_t s,
+                                 float* fdots = nullptr, uint32_t* fdone = nullptr);
 // Test entry: D[q][c] = Q[q] . C[c] with the fused kernel's bf16x3 MFMA.
 void launch_coarse_bf16x3_dots(const float* Q, int nq, int d, const uint4* Cb, int L, float* D,
                                hipStream_t s);

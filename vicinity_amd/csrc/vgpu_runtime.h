@@ -92,6 +92,7 @@ struct WsPtrs {
           *rres = nullptr;
     uint32_t *cand = nullptr, *cand_n = nullptr, *cflag_list = nullptr, *probe = nullptr,
              *vidx = nullptr, *vidx2 = nullptr, *qstat = nullptr, *flag_list = nullptr;
+    float* fdots = nullptr;  // coarse fallback: dot-product rows of the first flagged queries
     unsigned long long* scal = nullptr;  // per-call scalars (counters, flag-list lengths)
 };
 
@@ -100,7 +101,8 @@ struct WsPtrs {
 constexpr size_t kOverflowWord = (NUM_SCAN_COUNTERS + 1) * COUNTER_STRIDE;
 constexpr size_t kFlagWord = kOverflowWord + 8;
 constexpr size_t kCFlagWord = kFlagWord + 8;
-constexpr size_t kScalWords = kCFlagWord + 8;
+constexpr size_t kFDoneWord = kCFlagWord + 8;  // COARSE_FLAG_PAR uint32 slice counters
+constexpr size_t kScalWords = kFDoneWord + COARSE_FLAG_PAR / 2;
 
 // Workspace of one search call.  A handle keeps a pool of these: each call
 // borrows one for its whole duration, so concurrent searches on one handle
