@@ -1,6 +1,6 @@
 // Coarse quantiser in two kernels, without a query x centroid score matrix:
 //
-//   coarse_fused_kernel  32 queries per workgroup.  Normalises its queries
+//   coarse_fused_kernel  48 queries per workgroup.  Normalises its queries
 //       (search.rs:55-62, writes qn), then makes one pass of bf16x3 MFMA dot
 //       products against every centroid: q.c ~ qh.ch + qh.cl + ql.ch with
 //       x = xh + xl + O(2^-16 |x|) split into bfloat16 halves.  Each (lane, query)
@@ -31,7 +31,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // Native 128-bit vector (HIP's uint4 is a struct whose copies stay in memory).
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-#define FC_QBW 2               // query blocks (16 queries each) per workgroup
+#define FC_QBW 3               // query blocks (16 queries each) per workgroup
 #define FC_QB (16 * FC_QBW)    // queries per workgroup
 #define FC_NH 4                // waves per query block; each takes its own tiles of a stage
 #define FC_SUB 1               // 16-centroid tiles per wave and stage
@@ -119,8 +119,10 @@ __device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, 
                                         const u32x4 (&al)[DT], u32x4* lds, Epi epi) {
     const u32x4* Cb = reinterpret_cast<const u32x4*>(Cb_in);
     constexpr int SC = FC_ST * DT * 4 * 16;  // chunks per stage and half
-    constexpr int PER = 2 * SC / FC_THREADS;  // chunks each thread copies per stage
-    static_assert((2 * SC) % FC_THREADS == 0, "stage split");
+    // chunks each thread copies per stage; with 768 threads the last slot is
+    // only partly used, so a thread copies slot i only when it exists
+    constexpr int PER = (2 * SC + FC_THREADS - 1) / FC_THREADS;
+    constexpr bool EXACT_SPLIT = (2 * SC) % FC_THREADS == 0;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
     const int h = __builtin_amdgcn_readfirstlane((tid >> 6) / FC_QBW);
     const int nst = (L + FC_ST * 16 - 1) / (FC_ST * 16);
@@ -136,10 +138,10 @@ __device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, 
     // to arrive (the other waves of the CU cover the rest).
     u32x4 pa[PER];
 #define FC_FETCH(SET, ST)                                                              \
-    _Pragma("unroll") for (int i = 0; i < PER; i++) SET[i] = __builtin_amdgcn_raw_buffer_load_b128( \
+    _Pragma("unroll") for (int i = 0; i < PER; i++) if (EXACT_SPLIT || i * FC_THREADS + tid < 2 * SC) SET[i] = __builtin_amdgcn_raw_buffer_load_b128( \
         rsrc, lofs, (uint32_t)((ST) * 2 * SC * 16 + i * FC_THREADS * 16), 0);
 #define FC_STORE(SET, BUF)                                                             \
-    _Pragma("unroll") for (int i = 0; i < PER; i++) lds[(size_t)(BUF) * 2 * SC + i * FC_THREADS + tid] = SET[i];
+    _Pragma("unroll") for (int i = 0; i < PER; i++) if (EXACT_SPLIT || i * FC_THREADS + tid < 2 * SC) lds[(size_t)(BUF) * 2 * SC + i * FC_THREADS + tid] = SET[i];
     floatx4 prev[FC_SUB];
     // Stage ST: everyone has finished stage ST - 1 (buffer (ST + 1) & 1) and
     // stage ST's chunks are visible; SET holds stage ST + 1, then ST + 2.
@@ -270,9 +272,10 @@ __device__ __forceinline__ void top_insert(float (&t)[J], float v) {
 // keys, Pe <= 16 FC_NH FC_TR.)  A list whose J-th key is itself above that
 // threshold may have dropped such a list, and a row holds at most CAP
 // candidates: the row is then marked overflowed (cand_n = CAP + 1).  After the
-// pass wave h finishes rows FC_RPW h .. + FC_RPW - 1 of each lane; FC_NH waves
-// per query block keep enough waves in flight on a 256-CU part (two per SIMD
-// for a 10k-query batch).
+// pass wave h finishes rows FC_RPW h .. + FC_RPW - 1 of each lane.  Three
+// query blocks of FC_NH waves (48 queries, 12 waves) per workgroup: a 10k
+// batch is 209 workgroups, one per CU with none left over (with 32 queries,
+// 313 workgroups left 57 CUs running two and the launch waited for them).
 template <int DT, int J>
 __global__ __launch_bounds__(FC_THREADS) void coarse_fused_kernel(
     const float* __restrict__ Q, int nq, int d, const uint4* __restrict__ Cb, int L, float cmax,
