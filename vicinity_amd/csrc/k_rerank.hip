@@ -10,8 +10,10 @@
 
 namespace vgpu {
 
-// One workgroup per query; the pool's keys and a payload row in dynamic LDS
-// (next_pow2(pool) of each; pool <= RERANK_MAX).
+// One workgroup per query; the pool's keys, a payload row (next_pow2(pool)
+// of each; pool <= RERANK_MAX) and the query in dynamic LDS.  Each thread
+// streams its candidate's row 32 floats at a time (seq_dot_stream: the same
+// sequential sum).
 __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ vectors, int d,
                                                      const float* __restrict__ qn, int nq,
                                                      const uint32_t* __restrict__ pool_vidx,
@@ -20,14 +22,16 @@ __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ v
     extern __shared__ __align__(16) uint64_t keys[];
     const int q = blockIdx.x;
     if (q >= nq) return;
-    const float* qv = qn + (size_t)q * d;
     const int n2 = next_pow2(pool);
     uint32_t* pay = reinterpret_cast<uint32_t*>(keys + n2);
+    float* qs = reinterpret_cast<float*>(pay + n2);  // [d]
+    for (int j = threadIdx.x; j < d; j += blockDim.x) qs[j] = qn[(size_t)q * d + j];
+    __syncthreads();
     for (int t = threadIdx.x; t < n2; t += blockDim.x) {
         uint64_t key = ~0ull;
         if (t < pool) {
             uint32_t v = pool_vidx[(size_t)q * pool + t];
-            if (v != 0xffffffffu) key = cand_key(1.0f - seq_dot(qv, vectors + (size_t)v * d, d), v);
+            if (v != 0xffffffffu) key = cand_key(1.0f - seq_dot_stream(qs, vectors + (size_t)v * d, d), v);
         }
         keys[t] = key;
         pay[t] = 0;
@@ -46,10 +50,10 @@ __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ v
     }
 }
 
-static size_t rerank_lds(int pool) {
+static size_t rerank_lds(int pool, int d) {
     size_t n2 = 1;
     while (n2 < (size_t)pool) n2 <<= 1;
-    return n2 * (sizeof(uint64_t) + sizeof(uint32_t));
+    return n2 * (sizeof(uint64_t) + sizeof(uint32_t)) + (size_t)d * sizeof(float);
 }
 
 void launch_rerank(const DevIndex& ix, const float* qn, int nq, const uint32_t* pool_vidx,
@@ -60,7 +64,7 @@ void launch_rerank(const DevIndex& ix, const float* qn, int nq, const uint32_t* 
 void launch_rerank_vectors(const float* vectors, int d, const float* qn, int nq, const uint32_t* pool_rows,
                            int pool, int k, uint32_t* out_rows, float* out_dist, hipStream_t s) {
     if (nq <= 0) return;
-    const size_t lds = rerank_lds(pool);
+    const size_t lds = rerank_lds(pool, d);
     ensure_dyn_lds((const void*)rerank_kernel, lds);
     hipLaunchKernelGGL(rerank_kernel, dim3(nq), dim3(256), lds, s, vectors, d, qn, nq, pool_rows, pool, k,
                        out_rows, out_dist);
