@@ -84,17 +84,18 @@ def test_flat_wide_rows_take_the_fp32_path(oracle):
     _check(ids, dists, oids, odists)
 
 
-@pytest.mark.parametrize("metric", [0, 1])
-def test_flat_fallback_rescans_crowded_lanes(oracle, metric):
+@pytest.mark.parametrize("metric,nnear", [(0, 4), (1, 4), (0, 300)])
+def test_flat_fallback_rescans_crowded_lanes(oracle, metric, nnear):
     """Near-copies of one vector crowded into single ranking lanes (more than
     the four keys a lane keeps, so the merge cannot prove the result and the
     fallback rescans those lanes' columns) beside near-copies spread one per
     lane in another slice (kept keys, rescored) and exact duplicates (ties
     broken by index).  40000 rows make 32 slices of 80 tiles: vector
-    16 (80 s + t) + c is slice s, lane c."""
+    16 (80 s + t) + c is slice s, lane c.  300 such queries pass the 256 the
+    device-driven fallback takes, so the rest run after the final wait."""
     from vicinity_amd import FlatIndex
 
-    _print_case(f"flat crowded lanes metric={metric}")
+    _print_case(f"flat crowded lanes metric={metric} near queries={nnear}")
     rng = np.random.default_rng(71 + metric)
     n, d = 40_000, 64
     base = rng.standard_normal((n, d)).astype(np.float32)
@@ -103,7 +104,7 @@ def test_flat_fallback_rescans_crowded_lanes(oracle, metric):
     base[(160 + np.arange(12)) * 16 + 5] = near(12, 1e-4)      # slice 2, lane 5
     base[(560 + 3) * 16 + np.arange(6)] = near(6, 1e-4)       # slice 7, lanes 0-5
     base[(1600 + 2 * np.arange(5)) * 16 + 9] = v              # slice 20, lane 9
-    q = np.concatenate([near(4, 1e-3), rng.standard_normal((20, d)).astype(np.float32)])
+    q = np.concatenate([near(nnear, 1e-3), rng.standard_normal((20, d)).astype(np.float32)])
     if metric == 1:
         base = oracle.normalize_rows(base)
         q = oracle.normalize_rows(q)
@@ -113,4 +114,4 @@ def test_flat_fallback_rescans_crowded_lanes(oracle, metric):
         ids, dists = fx.search(q, k)
         oids, odists = oracle.flat_search(base, q, k, metric=metric)
         _check(ids, dists, oids, odists)
-        assert fx.last_fallbacks() >= 4, k
+        assert fx.last_fallbacks() >= nnear, k

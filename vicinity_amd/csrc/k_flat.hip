@@ -562,6 +562,23 @@ __global__ __launch_bounds__(256) void flat_merge_wave_kernel(
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = blockIdx.x * 4 + wave;
     if (q >= nq) return;
+    // the query to LDS (rescoring) and, without Qsq, its squared norm for the
+    // error bound (any order: the bound takes sqrt(.) * 1.0001)
+    const float* qv = qsh[wave];
+    float qsq = 0.0f;
+    for (int j = lane; j < d; j += 64) {
+        const float x = Q[(size_t)q * d + j];
+        qsh[wave][j] = x;
+        qsq = __builtin_fmaf(x, x, qsq);
+    }
+    if (Qsq) {
+        qsq = Qsq[q];
+    } else {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) qsq += __uint_as_float(shfl_xor_u32(__float_as_uint(qsq), o));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
     const int tot = splits * kk;
     uint64_t kv[E];
     const uint64_t* src = partial + (size_t)q * tot;
@@ -584,7 +601,7 @@ __global__ __launch_bounds__(256) void flat_merge_wave_kernel(
             if (below <= k - 1) T = cand;
         }
         const float u = 5.9604645e-08f;
-        const float qmax = sqrtf(Qsq[q]) * 1.0001f + 1e-30f;
+        const float qmax = sqrtf(qsq) * 1.0001f + 1e-30f;
         const float tau = flat_bf16_tau(d, metric, qmax, xmax, ib);
         fb = fkey(fkey_to_float(T) + 2.0f * tau);
         fb = fb < 0xfffffffeu ? fb + 1u : 0xffffffffu;  // one ulp up: the bound is not rounded down
@@ -625,10 +642,6 @@ __global__ __launch_bounds__(256) void flat_merge_wave_kernel(
         }
         return;
     }
-    const float* qv = qsh[wave];
-    for (int j = lane; j < d; j += 64) qsh[wave][j] = Q[(size_t)q * d + j];
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
     auto rescore = [&](uint32_t i) -> uint64_t {
         if (i >= cnt) return ~0ull;
         const uint32_t idx = (uint32_t)rbuf[wave][i];
@@ -710,12 +723,15 @@ __global__ __launch_bounds__(256) void flat_exact_slice_kernel(
         out_keys[((size_t)i * gridDim.x + s) * k + j] = j < m ? keys[j] : ~0ull;
 }
 
+// nflag_dev (optional): the flagged-query count on the device; workgroups
+// past it (or past the grid) have nothing to do.
 __global__ __launch_bounds__(256) void flat_exact_finish_kernel(
     const uint32_t* __restrict__ flag_list, int slices, int k, const uint64_t* __restrict__ in_keys,
-    uint32_t* __restrict__ out_idx, float* __restrict__ out_dist) {
+    uint32_t* __restrict__ out_idx, float* __restrict__ out_dist, const unsigned int* nflag_dev) {
     __shared__ uint64_t keys[FL_BUF];
     __shared__ uint32_t pay[FL_BUF];
     const int i = blockIdx.x, tid = threadIdx.x;
+    if (nflag_dev && (unsigned int)i >= *nflag_dev) return;
     const uint32_t q = flag_list[i];
     const int tot = slices * k, n2 = next_pow2(tot);
     for (int j = tid; j < n2; j += blockDim.x) {
@@ -745,7 +761,8 @@ __global__ __launch_bounds__(256) void flat_rank_fallback_kernel(
     const uint32_t* __restrict__ flag_list, const uint32_t* __restrict__ fbv,
     const uint64_t* __restrict__ partial, const uint32_t* __restrict__ pbound, int splits, int kk, int tps,
     const float* __restrict__ Q, const float* __restrict__ X, int n, int d, int k, int metric,
-    uint64_t* __restrict__ out_keys) {
+    uint64_t* __restrict__ out_keys, const unsigned int* nflag_dev) {
+    if (nflag_dev && blockIdx.y >= *nflag_dev) return;  // uniform: no flagged query for this row
     __shared__ uint64_t keys[FL_BUF];
     __shared__ uint32_t pay[FL_BUF];
     __shared__ uint32_t misc[4];
@@ -815,10 +832,24 @@ void launch_flat_rank_fallback(const uint32_t* flag_list, int nflag, const uint3
     for (int f0 = 0; f0 < nflag; f0 += 65535) {  // grid.y limit
         const int nf = nflag - f0 < 65535 ? nflag - f0 : 65535;
         hipLaunchKernelGGL(flat_rank_fallback_kernel, dim3(sp, nf), dim3(256), 0, s, flag_list + f0, fbv, partial,
-                           pbound, sp, kk, tps, Q, X, n, d, k, metric, keys + (size_t)f0 * sp * k);
+                           pbound, sp, kk, tps, Q, X, n, d, k, metric, keys + (size_t)f0 * sp * k, nullptr);
         hipLaunchKernelGGL(flat_exact_finish_kernel, dim3(nf), dim3(256), 0, s, flag_list + f0, sp, k,
-                           keys + (size_t)f0 * sp * k, out_idx, out_dist);
+                           keys + (size_t)f0 * sp * k, out_idx, out_dist, nullptr);
     }
+}
+
+void launch_flat_rank_fallback_dev(const uint32_t* flag_list, const unsigned int* nflag_dev, int cap,
+                                   const uint32_t* fbv, const uint64_t* partial, int nq, int n, int d, int k,
+                                   int metric, const float* Q, const float* X, uint64_t* keys, uint32_t* out_idx,
+                                   float* out_dist, hipStream_t s) {
+    if (cap <= 0) return;
+    int tps, ib;
+    const int kk = flat_rank_keep(k), sp = flat_rank_splits(nq, n, kk, &tps, &ib);
+    const uint32_t* pbound = reinterpret_cast<const uint32_t*>(partial + (size_t)nq * sp * kk);
+    hipLaunchKernelGGL(flat_rank_fallback_kernel, dim3(sp, cap), dim3(256), 0, s, flag_list, fbv, partial, pbound,
+                       sp, kk, tps, Q, X, n, d, k, metric, keys, nflag_dev);
+    hipLaunchKernelGGL(flat_exact_finish_kernel, dim3(cap), dim3(256), 0, s, flag_list, sp, k, keys, out_idx,
+                       out_dist, nflag_dev);
 }
 
 int flat_rank_fallback_slices(int nq, int n, int d, int k) {
@@ -836,7 +867,7 @@ void launch_flat_fallback(const uint32_t* flag_list, int nflag, const float* Q, 
         hipLaunchKernelGGL(flat_exact_slice_kernel, dim3(sl, nf), dim3(256), 0, s, flag_list + f0, Q, X, n, d,
                            k, metric, len, keys + (size_t)f0 * sl * k);
         hipLaunchKernelGGL(flat_exact_finish_kernel, dim3(nf), dim3(256), 0, s, flag_list + f0, sl, k,
-                           keys + (size_t)f0 * sl * k, out_idx, out_dist);
+                           keys + (size_t)f0 * sl * k, out_idx, out_dist, nullptr);
     }
 }
 

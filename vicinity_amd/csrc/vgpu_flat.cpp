@@ -9,6 +9,9 @@
 
 namespace vgpu {
 
+// Flagged queries the ranking path's fallback takes with the count read on the device
+constexpr size_t kFlatFallbackCap = 256;
+
 FlatIndex::FlatIndex(size_t dim, int met) : d(dim), metric(met) {
     if (dim == 0) throw Error(VGPU_ERR_INVALID_CONFIG, "dimension must be greater than 0");
     if (met != 0 && met != 1) throw Error(VGPU_ERR_INVALID_CONFIG, "metric must be 0 (L2) or 1 (1 - dot)");
@@ -88,21 +91,26 @@ void FlatIndex::search_device(const float* d_q, size_t nq, size_t k, int64_t* d_
     w_flag.reserve(nq);
     w_fb.reserve(nq);
     VGPU_HIP(hipMemsetAsync(w_overflow.p, 0, sizeof(unsigned int), s));
-    launch_flat_norms(d_q, (int)nq, (int)d, w_qnorm.p, s);
+    // the bf16x3 ranking path computes the query norms in its merge
+    const int rsl = d_xb.n ? flat_rank_fallback_slices((int)nq, (int)n, (int)d, (int)k) : 0;
+    if (!rsl) launch_flat_norms(d_q, (int)nq, (int)d, w_qnorm.p, s);
     VGPU_HIP(hipEventRecord(ev[0], s));
-    launch_flat_search(d_q, w_qnorm.p, (int)nq, d_x.p, d_xb.n ? d_xb.p : nullptr, d_xnorm.p, (int)n, (int)d,
-                       (int)k, metric, xmax, w_partial.p, w_idx.p, w_dist.p, w_overflow.p, w_flag.p, w_fb.p, s,
-                       ev[3]);
-    // the unproved queries (rare): exact scans over many workgroups
-    VGPU_HIP(hipMemcpyAsync(&fallbacks, w_overflow.p, sizeof(unsigned int), hipMemcpyDeviceToHost, s));
-    VGPU_HIP(hipStreamSynchronize(s));
-    if (fallbacks) {
-        const int rsl = d_xb.n ? flat_rank_fallback_slices((int)nq, (int)n, (int)d, (int)k) : 0;
-        if (rsl) {
-            w_fbkeys.reserve((size_t)fallbacks * rsl * k);
-            launch_flat_rank_fallback(w_flag.p, (int)fallbacks, w_fb.p, w_partial.p, (int)nq, (int)n, (int)d,
+    launch_flat_search(d_q, rsl ? nullptr : w_qnorm.p, (int)nq, d_x.p, d_xb.n ? d_xb.p : nullptr, d_xnorm.p,
+                       (int)n, (int)d, (int)k, metric, xmax, w_partial.p, w_idx.p, w_dist.p, w_overflow.p, w_flag.p,
+                       w_fb.p, s, ev[3]);
+    // the unproved queries (rare): exact scans over many workgroups.  The
+    // ranking path runs the first kFlatFallbackCap of them with the count
+    // read on the device (no host round trip), the rest after the final
+    // wait; the other path reads the count first.
+    const int cap = rsl ? (int)std::min<size_t>(nq, kFlatFallbackCap) : 0;
+    if (rsl) {
+        w_fbkeys.reserve((size_t)cap * rsl * k);
+        launch_flat_rank_fallback_dev(w_flag.p, w_overflow.p, cap, w_fb.p, w_partial.p, (int)nq, (int)n, (int)d,
                                       (int)k, metric, d_q, d_x.p, w_fbkeys.p, w_idx.p, w_dist.p, s);
-        } else {
+    } else {
+        VGPU_HIP(hipMemcpyAsync(&fallbacks, w_overflow.p, sizeof(unsigned int), hipMemcpyDeviceToHost, s));
+        VGPU_HIP(hipStreamSynchronize(s));
+        if (fallbacks) {
             w_fbkeys.reserve((size_t)fallbacks * flat_fallback_slices((int)n, (int)k) * k);
             launch_flat_fallback(w_flag.p, (int)fallbacks, d_q, d_x.p, (int)n, (int)d, (int)k, metric,
                                  w_fbkeys.p, w_idx.p, w_dist.p, s);
@@ -111,8 +119,19 @@ void FlatIndex::search_device(const float* d_q, size_t nq, size_t k, int64_t* d_
     VGPU_HIP(hipEventRecord(ev[1], s));
     launch_finalize(w_idx.p, w_dist.p, nullptr, (int)nq, (int)k, (int)k, d_ids, d_dists, s);
     VGPU_HIP(hipEventRecord(ev[2], s));
+    if (rsl) VGPU_HIP(hipMemcpyAsync(&fallbacks, w_overflow.p, sizeof(unsigned int), hipMemcpyDeviceToHost, s));
     VGPU_HIP(hipGetLastError());
     VGPU_HIP(hipStreamSynchronize(s));
+    if (rsl && fallbacks > (unsigned int)cap) {  // more than the device-driven pass took
+        const int rest = (int)fallbacks - cap;
+        w_fbkeys.reserve((size_t)rest * rsl * k);
+        launch_flat_rank_fallback(w_flag.p + cap, rest, w_fb.p, w_partial.p, (int)nq, (int)n, (int)d, (int)k,
+                                  metric, d_q, d_x.p, w_fbkeys.p, w_idx.p, w_dist.p, s);
+        launch_finalize(w_idx.p, w_dist.p, nullptr, (int)nq, (int)k, (int)k, d_ids, d_dists, s);
+        VGPU_HIP(hipEventRecord(ev[2], s));
+        VGPU_HIP(hipGetLastError());
+        VGPU_HIP(hipStreamSynchronize(s));
+    }
     VGPU_HIP(hipEventElapsedTime(&ms_gemm, ev[0], ev[3]));
     VGPU_HIP(hipEventElapsedTime(&ms_total, ev[0], ev[2]));
 }

@@ -233,6 +233,8 @@ void launch_flat_pack(const float* X, int n, int d, uint4* Xb, hipStream_t s);
 // Queries whose kept candidates cannot be proved to hold the exact top-k are
 // appended to flag_list (*overflow, zero on entry, counts them) and their
 // rows are left for launch_flat_fallback.
+// Qsq: the queries' squared norms; the bf16x3 ranking path (Xb) takes null
+// and computes them in its merge.
 void launch_flat_search(const float* Q, const float* Qsq, int nq, const float* X, const uint4* Xb,
                         const float* Xnorm, int n, int d, int k, int metric, float xmax,
                         uint64_t* partial, uint32_t* out_idx, float* out_dist,
@@ -248,6 +250,12 @@ void launch_flat_rank_fallback(const uint32_t* flag_list, int nflag, const uint3
                                const uint64_t* partial, int nq, int n, int d, int k, int metric,
                                const float* Q, const float* X, uint64_t* keys, uint32_t* out_idx,
                                float* out_dist, hipStream_t s);
+// The same for the first min(*nflag_dev, cap) flagged queries, the count read
+// on the device (no host round trip); keys: cap * slices * k entries.
+void launch_flat_rank_fallback_dev(const uint32_t* flag_list, const unsigned int* nflag_dev, int cap,
+                                   const uint32_t* fbv, const uint64_t* partial, int nq, int n, int d, int k,
+                                   int metric, const float* Q, const float* X, uint64_t* keys, uint32_t* out_idx,
+                                   float* out_dist, hipStream_t s);
 // Exhaustive exact top-k rows of the nflag queries of flag_list;
 // keys: scratch of nflag * flat_fallback_slices(n, k) * k entries.
 int flat_fallback_slices(int n, int k);
