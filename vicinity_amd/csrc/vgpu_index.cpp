@@ -264,6 +264,8 @@ void IvfpqIndex::kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k,
     da.reserve(nt);
     std::vector<uint32_t> assign(nt), prev(nt);
     const bool gpu_update = d <= 256;
+    DevBuf<uint32_t> dks;  // member lists of the update
+    if (gpu_update) dks.reserve(kmeans_update_scratch_words((int)nt, 1, (int)ke));
     dc.upload(cent.data(), ke * d, stream);
     for (size_t it = 0; it < max_iter; it++) {
         float cmax = 0.0f;
@@ -275,9 +277,8 @@ void IvfpqIndex::kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k,
         check_labels(assign.data(), nt, 1, ke, "k-means assignment");
         if (it > 0 && assign == prev) break;
         if (gpu_update) {
-            launch_kmeans_update(dx.p, (int)nt, (int)d, (int)d, 1, da.p, false, (int)ke, nullptr, true, dc.p,
-                                 stream);
-            VGPU_HIP(hipGetLastError());
+            VGPU_HIP(launch_kmeans_update(dx.p, (int)nt, (int)d, (int)d, 1, da.p, false, (int)ke, nullptr, true,
+                                          dc.p, dks.p, dks.n, stream));
             VGPU_HIP(hipMemcpyAsync(cent.data(), dc.p, ke * d * sizeof(float), hipMemcpyDeviceToHost, stream));
             VGPU_HIP(hipStreamSynchronize(stream));
             prev.swap(assign);
@@ -310,6 +311,8 @@ void IvfpqIndex::train_pq(const std::vector<float>& res, size_t nt, size_t Kc, u
     std::vector<uint8_t> cur(nt * M), prev(nt * M), active(M);
     std::vector<char> frozen(M, 0);
     const bool gpu_update = ds <= 256;
+    DevBuf<uint32_t> dks;  // member lists of the update
+    if (gpu_update) dks.reserve(kmeans_update_scratch_words((int)nt, (int)M, (int)Ke));
     dcb.upload(codebooks.data(), codebooks.size(), stream);
     for (size_t it = 0; it < max_iter; it++) {
         if (!gpu_update) dcb.upload(codebooks.data(), codebooks.size(), stream);
@@ -340,9 +343,8 @@ void IvfpqIndex::train_pq(const std::vector<float>& res, size_t nt, size_t Kc, u
         if (!any) break;
         if (gpu_update) {
             dactive.upload(active.data(), M, stream);
-            launch_kmeans_update(dres.p, (int)nt, (int)d, (int)ds, (int)M, dcodes.p, true, (int)Ke, dactive.p,
-                                 false, dcb.p, stream);
-            VGPU_HIP(hipGetLastError());
+            VGPU_HIP(launch_kmeans_update(dres.p, (int)nt, (int)d, (int)ds, (int)M, dcodes.p, true, (int)Ke,
+                                          dactive.p, false, dcb.p, dks.p, dks.n, stream));
         }
         prev.swap(cur);
     }

@@ -201,9 +201,13 @@ void launch_procrustes(const uint8_t* codes, const float* cb, int M, int K, int 
 // row order, mean cast to float, optionally normalised; empty keys keep their
 // row; subspaces with active[m] == 0 are skipped (active may be null).  u8:
 // labels[i * M + m] code bytes over row slices x[i * d + m * w .. + w);
-// otherwise u32 labels[i] over whole rows (w = d <= 256).
-void launch_kmeans_update(const float* x, int n, int d, int w, int M, const void* labels, bool u8,
-                          int K, const uint8_t* active, bool normalize, float* out, hipStream_t s);
+// otherwise u32 labels[i] over whole rows (w = d <= 256).  Labels must be
+// below K.  The member lists live in scratch (device words, at least
+// kmeans_update_scratch_words(n, M, K); hipErrorInvalidValue when fewer).
+size_t kmeans_update_scratch_words(int n, int M, int K);
+hipError_t launch_kmeans_update(const float* x, int n, int d, int w, int M, const void* labels, bool u8,
+                                int K, const uint8_t* active, bool normalize, float* out, uint32_t* scratch,
+                                size_t scratch_words, hipStream_t s);
 
 void launch_encode(const float* x, int n, int d, const float* centroids, const uint32_t* assign,
                    const float* codebooks, int M, int K, int ds, uint8_t* codes, hipStream_t s);
