@@ -127,8 +127,8 @@ def cpu_baseline(art, queries, k, nprobe, pool=0, budget_s=15.0):
     return out, n, ids, dists
 
 
-IVFPQ_RUNS = {  # workload -> (training sample, k-means iterations)
-    "ivfpq_small": (0, 10),
+IVFPQ_RUNS = {  # workload -> (training sample or None for every vector, k-means iterations)
+    "ivfpq_small": (None, 10),
     "ivfpq_1m": (262_144, 25),
     "ivfpq_10m": (262_144, 10),
     "ivfpq_4bit": (262_144, 10),
