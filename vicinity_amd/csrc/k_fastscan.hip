@@ -147,12 +147,14 @@ struct WaveTopk {
         wave_sync();
     }
 
-    // Push one candidate per lane (take may differ by lane).
-    __device__ void push(bool take, float dist, uint32_t vidx) {
+    // Push one candidate per lane (take may differ by lane); the insertion
+    // index ids[pos] is read only for a candidate that passes the filter.
+    __device__ void push(bool take, float dist, const uint32_t* __restrict__ ids, uint32_t pos) {
         uint32_t fk = fkey(dist);
         take = take && fk <= thr;
         uint64_t m = __ballot(take);
         if (m == 0) return;
+        const uint32_t vidx = take ? ids[pos] : 0u;
         if ((int)*count > buf - 64) flush();
         take = take && fk <= thr;
         int slot = wave_append_slot(take, count);
@@ -260,14 +262,11 @@ __global__ __launch_bounds__(256) void fastscan_kernel(DevIndex ix, ScanArgs a, 
             // Exact float path: m-ordered sum (pq.rs:272-279).
             bool take = (uint32_t)lane < len;
             float dist = 0.0f;
-            uint32_t vidx = 0;
             if (take) {
-                const uint32_t pos = beg + lane;
-                const uint8_t* row = ix.codes + (size_t)pos * M;
+                const uint8_t* row = ix.codes + (size_t)(beg + lane) * M;
                 for (int m = 0; m < M; m++) dist += lutf[m * 16 + row[m]];
-                vidx = ix.list_ids[pos];
             }
-            tk.push(take, dist, vidx);
+            tk.push(take, dist, ix.list_ids, beg + lane);
             continue;
         }
         float scale, base_offset;
@@ -299,14 +298,9 @@ __global__ __launch_bounds__(256) void fastscan_kernel(DevIndex ix, ScanArgs a, 
 #pragma unroll
             for (int cc = 0; cc < 8; cc++) {
                 const uint32_t vi = b * 32 + (cc < 4 ? 4 * w + cc : 16 + 4 * w + (cc - 4));
-                bool take = b < nb && vi < len;
-                float dist = 0.0f;
-                uint32_t vidx = 0;
-                if (take) {
-                    dist = (float)fs_acc(cc, a0, a1, a2, a3) * scale + base_offset;
-                    vidx = ix.list_ids[beg + vi];
-                }
-                tk.push(take, dist, vidx);
+                const bool take = b < nb && vi < len;
+                const float dist = take ? (float)fs_acc(cc, a0, a1, a2, a3) * scale + base_offset : 0.0f;
+                tk.push(take, dist, ix.list_ids, beg + vi);
             }
         }
         wave_sync();
