@@ -182,14 +182,22 @@ __host__ __device__ inline size_t fs_lds_layout(int d, int M, int P, int wbuf, s
     off[0] = o; o = fs_align16(o + (size_t)d * 4);            // qs
     off[1] = o; o = fs_align16(o + (size_t)4 * d * 4);        // residual per wave
     off[2] = o; o = fs_align16(o + (size_t)4 * M * 16 * 4);   // float LUT per wave
-    off[3] = o; o = fs_align16(o + (size_t)4 * M * 16);       // byte LUT per wave
+    off[3] = o; o = fs_align16(o + (size_t)4 * 2 * M * 16);   // two byte LUTs per wave
     off[4] = o; o = fs_align16(o + (size_t)P * 4 * 2);        // lid, llen
     off[5] = o; o = fs_align16(o + (size_t)4 * wbuf * 8);     // wave buffers (contiguous)
     off[6] = o; o = fs_align16(o + 16 * 4);                   // counters
     return o;
 }
 
-__global__ __launch_bounds__(256) void fastscan_kernel(DevIndex ix, ScanArgs a, int wbuf) {
+// A list of a wave's block stream: its first stream block, blocks, entries,
+// first packed block, quantisation and table slot.
+struct FsList {
+    uint32_t sst = 0, nb = 0, beg = 0, len = 0, pack = 0;
+    float scale = 0.0f, base_offset = 0.0f;
+    int slot = 0;
+};
+
+__global__ __launch_bounds__(256, 5) void fastscan_kernel(DevIndex ix, ScanArgs a, int wbuf) {
     extern __shared__ __align__(16) char smem[];
     const int q = blockIdx.x;
     if (q >= a.nq) return;
@@ -200,7 +208,7 @@ __global__ __launch_bounds__(256) void fastscan_kernel(DevIndex ix, ScanArgs a, 
     float* qs = (float*)(smem + off[0]);
     float* rw = (float*)(smem + off[1]) + wave * d;
     float* lutf = (float*)(smem + off[2]) + wave * M * 16;
-    uint8_t* qlut = (uint8_t*)(smem + off[3]) + wave * M * 16;
+    uint8_t* qlut = (uint8_t*)(smem + off[3]) + wave * 2 * M * 16;  // [2][M * 16]
     const bool wide = P > FS_LDS_P;
     uint32_t* lid = (uint32_t*)(smem + off[4]);
     uint32_t* llen = lid + (wide ? 0 : P);
@@ -225,84 +233,120 @@ __global__ __launch_bounds__(256) void fastscan_kernel(DevIndex ix, ScanArgs a, 
     tk.keep = a.kout;
     uint32_t scanned = 0;
 
-    for (int p = wave; p < P; p += 4) {
-        uint32_t l, len;
-        if (wide) {
-            const uint32_t g = a.probe[(size_t)q * P + p];
-            const bool ok = g < (uint32_t)ix.L;  // no such list: scanned as empty
-            l = ok ? g : 0u;
-            len = ok ? ix.offsets[g + 1] - ix.offsets[g] : 0u;
-        } else {
-            l = lid[p];
-            len = llen[p];
-        }
-        if (len == 0) continue;
-        const uint32_t beg = ix.offsets[l];
-        scanned += len;
-        if (a.rres) {  // OPQ: R (q - c) from the rotation kernel (opq.rs:120-123)
-            const float* rr = a.rres + ((size_t)q * P + p) * d;
-            for (int j = lane; j < d; j += 64) rw[j] = rr[j];
-        } else {
-            const float* c = ix.centroids + (size_t)l * d;
-            for (int j = lane; j < d; j += 64) rw[j] = qs[j] - c[j];  // search.rs:1242-1245
-        }
-        wave_sync();
-        for (int e = lane; e < M * 16; e += 64) {  // pq.rs:232-251
-            const int m = e >> 4;
-            const float* cw = ix.codebooks + (size_t)e * ds;
-            float acc = 0.0f;
-            for (int j = 0; j < ds; j++) {
-                float diff = rw[m * ds + j] - cw[j];
-                acc += diff * diff;
+    // The wave's lists p = wave, wave + 4, ... in order.  Lists of 16 or more
+    // entries form one stream of 32-entry blocks; each 16-block round takes the
+    // next blocks of the stream from at most two lists (`prv`, `cur`), whose
+    // quantised tables sit in the wave's two table slots.  A list's table is
+    // built when the blocks ahead of the round run short and the older list's
+    // blocks are all scanned (its slot is then free).  Shorter lists take the
+    // exact float path as their table is built.
+    FsList prv, cur;
+    prv.slot = 0;
+    cur.slot = 1;
+    uint32_t s0 = 0;  // next stream block to scan
+    int p = wave;     // next list to prepare
+    for (;;) {
+        while (p < P && cur.sst + cur.nb - s0 < 16 && prv.sst + prv.nb <= s0) {
+            uint32_t l, len;
+            if (wide) {
+                const uint32_t g = a.probe[(size_t)q * P + p];
+                const bool ok = g < (uint32_t)ix.L;  // no such list: scanned as empty
+                l = ok ? g : 0u;
+                len = ok ? ix.offsets[g + 1] - ix.offsets[g] : 0u;
+            } else {
+                l = lid[p];
+                len = llen[p];
             }
-            lutf[e] = acc;
-        }
-        wave_sync();
-        if (len < 16) {
-            // Exact float path: m-ordered sum (pq.rs:272-279).
-            bool take = (uint32_t)lane < len;
-            float dist = 0.0f;
-            if (take) {
-                const uint8_t* row = ix.codes + (size_t)(beg + lane) * M;
-                for (int m = 0; m < M; m++) dist += lutf[m * 16 + row[m]];
+            l = __builtin_amdgcn_readfirstlane(l);  // wave-uniform: scalar registers
+            len = __builtin_amdgcn_readfirstlane(len);
+            const int pp = p;
+            p += 4;
+            if (len == 0) continue;
+            const uint32_t beg = ix.offsets[l];
+            scanned += len;
+            if (a.rres) {  // OPQ: R (q - c) from the rotation kernel (opq.rs:120-123)
+                const float* rr = a.rres + ((size_t)q * P + pp) * d;
+                for (int j = lane; j < d; j += 64) rw[j] = rr[j];
+            } else {
+                const float* c = ix.centroids + (size_t)l * d;
+                for (int j = lane; j < d; j += 64) rw[j] = qs[j] - c[j];  // search.rs:1242-1245
             }
-            tk.push(take, dist, ix.list_ids, beg + lane);
-            continue;
-        }
-        float scale, base_offset;
-        fs_quantize(lutf, qlut, M, scale, base_offset);
-        wave_sync();
-        const uint32_t* qw = (const uint32_t*)qlut;
-        const uint32_t nb = ix.pack_off[l + 1] - ix.pack_off[l];
-        const uint8_t* blocks = ix.packed + (size_t)ix.pack_off[l] * 16 * M;
-        for (uint32_t b0 = 0; b0 < nb; b0 += 16) {
-            const uint32_t b = b0 + (lane >> 2), w = lane & 3;
-            uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
-            if (b < nb) {
-                const uint32_t* src = (const uint32_t*)(blocks + (size_t)b * 16 * M) + w;
-                // eight codebooks' code words in flight at a time
-                int m = 0;
-                for (; m + 8 <= M; m += 8) {
-                    uint32_t x[8];
-#pragma unroll
-                    for (int u = 0; u < 8; u++) x[u] = src[(m + u) * 4];
-#pragma unroll
-                    for (int u = 0; u < 8; u++)
-                        fs_accumulate(x[u], qw[(m + u) * 4], qw[(m + u) * 4 + 1], qw[(m + u) * 4 + 2],
-                                      qw[(m + u) * 4 + 3], a0, a1, a2, a3);
+            wave_sync();
+            for (int e = lane; e < M * 16; e += 64) {  // pq.rs:232-251
+                const int m = e >> 4;
+                const float* cw = ix.codebooks + (size_t)e * ds;
+                float acc = 0.0f;
+                for (int j = 0; j < ds; j++) {
+                    float diff = rw[m * ds + j] - cw[j];
+                    acc += diff * diff;
                 }
-                for (; m < M; m++)
-                    fs_accumulate(src[m * 4], qw[m * 4], qw[m * 4 + 1], qw[m * 4 + 2], qw[m * 4 + 3], a0, a1,
-                                  a2, a3);
+                lutf[e] = acc;
             }
-#pragma unroll
-            for (int cc = 0; cc < 8; cc++) {
-                const uint32_t vi = b * 32 + (cc < 4 ? 4 * w + cc : 16 + 4 * w + (cc - 4));
-                const bool take = b < nb && vi < len;
-                const float dist = take ? (float)fs_acc(cc, a0, a1, a2, a3) * scale + base_offset : 0.0f;
-                tk.push(take, dist, ix.list_ids, beg + vi);
+            wave_sync();
+            if (len < 16) {
+                // Exact float path: m-ordered sum (pq.rs:272-279).
+                bool take = (uint32_t)lane < len;
+                float dist = 0.0f;
+                if (take) {
+                    const uint8_t* row = ix.codes + (size_t)(beg + lane) * M;
+                    for (int m = 0; m < M; m++) dist += lutf[m * 16 + row[m]];
+                }
+                tk.push(take, dist, ix.list_ids, beg + lane);
+                wave_sync();  // lutf is rewritten for the next list
+                continue;
             }
+            // the older list is done: its slot takes the new list
+            const int slot = prv.slot;
+            prv = cur;
+            cur.slot = slot;
+            cur.sst = prv.sst + prv.nb;
+            cur.nb = ix.pack_off[l + 1] - ix.pack_off[l];
+            cur.beg = beg;
+            cur.len = len;
+            cur.pack = ix.pack_off[l];
+            float sc, bo;
+            fs_quantize(lutf, qlut + slot * M * 16, M, sc, bo);
+            cur.scale = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(sc)));
+            cur.base_offset = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(bo)));
+            wave_sync();
         }
+        const uint32_t s_end = cur.sst + cur.nb;
+        if (s0 >= s_end) break;  // every list prepared and scanned
+        // lane quad b scans stream block s0 + b of its list: 4 lanes x one code
+        // dword of each codebook row (8 entries per lane)
+        const uint32_t sb = s0 + (lane >> 2), w = lane & 3;
+        const bool in_cur = sb >= cur.sst;
+        const bool valid = sb < s_end;
+        const uint32_t bl = valid ? sb - (in_cur ? cur.sst : prv.sst) : 0u;  // block within its list
+        const uint32_t lbeg = in_cur ? cur.beg : prv.beg, llen_b = in_cur ? cur.len : prv.len;
+        const float scale = in_cur ? cur.scale : prv.scale, base_offset = in_cur ? cur.base_offset : prv.base_offset;
+        const uint32_t* qw = (const uint32_t*)(qlut + (in_cur ? cur.slot : prv.slot) * M * 16);
+        uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+        if (valid) {
+            const uint32_t* src =
+                (const uint32_t*)(ix.packed + ((size_t)(in_cur ? cur.pack : prv.pack) + bl) * 16 * M) + w;
+            // eight codebooks' code words in flight at a time
+            int m = 0;
+            for (; m + 8 <= M; m += 8) {
+                uint32_t x[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) x[u] = src[(m + u) * 4];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    fs_accumulate(x[u], qw[(m + u) * 4], qw[(m + u) * 4 + 1], qw[(m + u) * 4 + 2],
+                                  qw[(m + u) * 4 + 3], a0, a1, a2, a3);
+            }
+            for (; m < M; m++)
+                fs_accumulate(src[m * 4], qw[m * 4], qw[m * 4 + 1], qw[m * 4 + 2], qw[m * 4 + 3], a0, a1, a2, a3);
+        }
+#pragma unroll
+        for (int cc = 0; cc < 8; cc++) {
+            const uint32_t vi = bl * 32 + (cc < 4 ? 4 * w + cc : 16 + 4 * w + (cc - 4));
+            const bool take = valid && vi < llen_b;
+            const float dist = take ? (float)fs_acc(cc, a0, a1, a2, a3) * scale + base_offset : 0.0f;
+            tk.push(take, dist, ix.list_ids, lbeg + vi);
+        }
+        s0 = min(s0 + 16u, s_end);
         wave_sync();
     }
     tk.flush();
