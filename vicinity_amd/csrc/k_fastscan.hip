@@ -103,6 +103,56 @@ __device__ inline void fs_quantize(const float* lutf, uint8_t* qlut, int M, floa
     base_offset = mn * (float)M;
 }
 
+// Codebooks of at most this many bytes are staged in LDS once per query for
+// the table builds; larger ones are read from global memory.
+#define FS_CB_LDS 16384
+#define FS_CW 8  // codebooks whose code words a lane loads together
+__host__ __device__ inline bool fs_cb_in_lds(int M, int ds) { return (size_t)M * 16 * ds * 4 <= FS_CB_LDS; }
+
+// Entry e = m * 16 + c of the float table of residual rw:
+// sum_j (r_mj - cw_mcj)^2 in j order (pq.rs:232-251).
+__device__ __forceinline__ float fs_lut_value(const float* rw, const float* cb, int ds, int e) {
+    const float* cw = cb + (size_t)e * ds;
+    const float* r = rw + (e >> 4) * ds;
+    float acc = 0.0f;
+    for (int j = 0; j < ds; j++) {
+        float diff = r[j] - cw[j];
+        acc += diff * diff;
+    }
+    return acc;
+}
+
+// The quantised table of one list by one wave, as fs_quantize makes it from
+// the float table, with the float entries recomputed in a second pass
+// instead of kept: min and max, then the bytes.
+__device__ inline void fs_build_qlut(const float* rw, const float* cb, int M, int ds, uint8_t* qlut,
+                                     float& scale, float& base_offset) {
+    const int lane = threadIdx.x & 63;
+    float mn = __int_as_float(0x7f800000), mx = __int_as_float(0xff800000);
+    for (int e = lane; e < M * 16; e += 64) {
+        const float v = fs_lut_value(rw, cb, ds, e);
+        if (v < mn) mn = v;
+        if (v > mx) mx = v;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        float omn = __shfl_xor(mn, off, 64), omx = __shfl_xor(mx, off, 64);
+        if (omn < mn) mn = omn;
+        if (omx > mx) mx = omx;
+    }
+    float range = mx - mn;
+    float sc, inv;
+    if (range < 1.1920929e-07f) {
+        sc = 1.0f;
+        inv = 0.0f;
+    } else {
+        sc = range / 255.0f;
+        inv = 255.0f / range;
+    }
+    for (int e = lane; e < M * 16; e += 64) qlut[e] = (uint8_t)round_to_u8((fs_lut_value(rw, cb, ds, e) - mn) * inv);
+    scale = sc;
+    base_offset = mn * (float)M;
+}
+
 // Ascending bitonic sort of keys[0..n) by one wave (n a power of two).
 __device__ inline void wave_bitonic_sort_keys(uint64_t* keys, int n) {
     const int lane = threadIdx.x & 63;
@@ -176,12 +226,12 @@ __host__ __device__ inline size_t fs_align16(size_t x) { return (x + 15) & ~(siz
 // from global memory when its wave takes it.
 #define FS_LDS_P 1024
 
-__host__ __device__ inline size_t fs_lds_layout(int d, int M, int P, int wbuf, size_t* off) {
+__host__ __device__ inline size_t fs_lds_layout(int d, int M, int ds, int P, int wbuf, size_t* off) {
     if (P > FS_LDS_P) P = 0;
     size_t o = 0;
     off[0] = o; o = fs_align16(o + (size_t)d * 4);            // qs
     off[1] = o; o = fs_align16(o + (size_t)4 * d * 4);        // residual per wave
-    off[2] = o; o = fs_align16(o + (size_t)4 * M * 16 * 4);   // float LUT per wave
+    off[2] = o; o = fs_align16(o + (fs_cb_in_lds(M, ds) ? (size_t)M * 16 * ds * 4 : 0));  // codebooks
     off[3] = o; o = fs_align16(o + (size_t)4 * 2 * M * 16);   // two byte LUTs per wave
     off[4] = o; o = fs_align16(o + (size_t)P * 4 * 2);        // lid, llen
     off[5] = o; o = fs_align16(o + (size_t)4 * wbuf * 8);     // wave buffers (contiguous)
@@ -197,17 +247,19 @@ struct FsList {
     int slot = 0;
 };
 
-__global__ __launch_bounds__(256, 5) void fastscan_kernel(DevIndex ix, ScanArgs a, int wbuf) {
+__global__ __launch_bounds__(256, 6) void fastscan_kernel(DevIndex ix, ScanArgs a, int wbuf) {
     extern __shared__ __align__(16) char smem[];
     const int q = blockIdx.x;
     if (q >= a.nq) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
     const int d = ix.d, M = ix.M, ds = ix.ds, P = a.P;
     size_t off[7];
-    fs_lds_layout(d, M, P, wbuf, off);
+    fs_lds_layout(d, M, ds, P, wbuf, off);
     float* qs = (float*)(smem + off[0]);
     float* rw = (float*)(smem + off[1]) + wave * d;
-    float* lutf = (float*)(smem + off[2]) + wave * M * 16;
+    const bool cbl = fs_cb_in_lds(M, ds);
+    float* cbs = (float*)(smem + off[2]);  // the codebooks when cbl
     uint8_t* qlut = (uint8_t*)(smem + off[3]) + wave * 2 * M * 16;  // [2][M * 16]
     const bool wide = P > FS_LDS_P;
     uint32_t* lid = (uint32_t*)(smem + off[4]);
@@ -222,6 +274,8 @@ __global__ __launch_bounds__(256, 5) void fastscan_kernel(DevIndex ix, ScanArgs 
         lid[p] = ok ? l : 0u;
         llen[p] = ok ? ix.offsets[l + 1] - ix.offsets[l] : 0u;
     }
+    if (cbl)
+        for (int i = tid; i < M * 16 * ds; i += blockDim.x) cbs[i] = ix.codebooks[i];
     if (tid < 4) cnt[tid] = 0;
     __syncthreads();
 
@@ -272,27 +326,19 @@ __global__ __launch_bounds__(256, 5) void fastscan_kernel(DevIndex ix, ScanArgs 
                 for (int j = lane; j < d; j += 64) rw[j] = qs[j] - c[j];  // search.rs:1242-1245
             }
             wave_sync();
-            for (int e = lane; e < M * 16; e += 64) {  // pq.rs:232-251
-                const int m = e >> 4;
-                const float* cw = ix.codebooks + (size_t)e * ds;
-                float acc = 0.0f;
-                for (int j = 0; j < ds; j++) {
-                    float diff = rw[m * ds + j] - cw[j];
-                    acc += diff * diff;
-                }
-                lutf[e] = acc;
-            }
-            wave_sync();
             if (len < 16) {
-                // Exact float path: m-ordered sum (pq.rs:272-279).
+                // Exact float path: m-ordered sum of the float table (pq.rs:272-279).
                 bool take = (uint32_t)lane < len;
                 float dist = 0.0f;
                 if (take) {
                     const uint8_t* row = ix.codes + (size_t)(beg + lane) * M;
-                    for (int m = 0; m < M; m++) dist += lutf[m * 16 + row[m]];
+                    if (cbl)
+                        for (int m = 0; m < M; m++) dist += fs_lut_value(rw, cbs, ds, m * 16 + row[m]);
+                    else
+                        for (int m = 0; m < M; m++) dist += fs_lut_value(rw, ix.codebooks, ds, m * 16 + row[m]);
                 }
                 tk.push(take, dist, ix.list_ids, beg + lane);
-                wave_sync();  // lutf is rewritten for the next list
+                wave_sync();  // rw is rewritten for the next list
                 continue;
             }
             // the older list is done: its slot takes the new list
@@ -305,7 +351,8 @@ __global__ __launch_bounds__(256, 5) void fastscan_kernel(DevIndex ix, ScanArgs 
             cur.len = len;
             cur.pack = ix.pack_off[l];
             float sc, bo;
-            fs_quantize(lutf, qlut + slot * M * 16, M, sc, bo);
+            if (cbl) fs_build_qlut(rw, cbs, M, ds, qlut + slot * M * 16, sc, bo);
+            else fs_build_qlut(rw, ix.codebooks, M, ds, qlut + slot * M * 16, sc, bo);
             cur.scale = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(sc)));
             cur.base_offset = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(bo)));
             wave_sync();
@@ -325,14 +372,14 @@ __global__ __launch_bounds__(256, 5) void fastscan_kernel(DevIndex ix, ScanArgs 
         if (valid) {
             const uint32_t* src =
                 (const uint32_t*)(ix.packed + ((size_t)(in_cur ? cur.pack : prv.pack) + bl) * 16 * M) + w;
-            // eight codebooks' code words in flight at a time
+            // FS_CW codebooks' code words in flight at a time
             int m = 0;
-            for (; m + 8 <= M; m += 8) {
-                uint32_t x[8];
+            for (; m + FS_CW <= M; m += FS_CW) {
+                uint32_t x[FS_CW];
 #pragma unroll
-                for (int u = 0; u < 8; u++) x[u] = src[(m + u) * 4];
+                for (int u = 0; u < FS_CW; u++) x[u] = src[(m + u) * 4];
 #pragma unroll
-                for (int u = 0; u < 8; u++)
+                for (int u = 0; u < FS_CW; u++)
                     fs_accumulate(x[u], qw[(m + u) * 4], qw[(m + u) * 4 + 1], qw[(m + u) * 4 + 2],
                                   qw[(m + u) * 4 + 3], a0, a1, a2, a3);
             }
@@ -365,7 +412,7 @@ __global__ __launch_bounds__(256, 5) void fastscan_kernel(DevIndex ix, ScanArgs 
 
 size_t fastscan_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
     size_t off[7];
-    return fs_lds_layout(ix.d, ix.M, a.P, fs_wave_buf(a.kout), off);
+    return fs_lds_layout(ix.d, ix.M, ix.ds, a.P, fs_wave_buf(a.kout), off);
 }
 
 void launch_fastscan(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
