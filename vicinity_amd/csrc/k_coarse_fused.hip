@@ -418,12 +418,14 @@ __global__ __launch_bounds__(FC_THREADS) void coarse_fused_kernel(
     }
 }
 
-#define FC_J 8  // keys per (wave, lane, row)
+// Keys per (wave, lane, row): 8 up to 32 probes, 10 above, where a list
+// holding more than 8 of the window's lists flags the query more often
+// (about 5 queries of a 10k batch at 16,384 lists and 64 probes).
+#define FC_J 8
+#define FC_J_WIDE 10
+static int fc_keys(int P) { return P > 32 ? FC_J_WIDE : FC_J; }
 
-int coarse_fused_cap(int P) {
-    (void)P;
-    return 32 * FC_J;
-}
+int coarse_fused_cap(int P) { return 32 * fc_keys(P); }
 
 bool coarse_fused_supported(int d, int P) { return d >= 1 && d <= 128 && P >= 1 && P <= 64; }
 
@@ -445,7 +447,10 @@ template <int DT>
 static void launch_fused_j(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int Pe,
                            int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
                            hipStream_t s) {
-    launch_fused<DT, FC_J>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s);
+    if (fc_keys(Pe) == FC_J_WIDE)
+        launch_fused<DT, FC_J_WIDE>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s);
+    else
+        launch_fused<DT, FC_J>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s);
 }
 
 void launch_coarse_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int P,
@@ -464,6 +469,8 @@ void launch_coarse_fused(const float* Q, int nq, int d, const uint4* Cb, int L, 
 // ---- exact ordering of the candidates, one wave per query ---------------
 #define TP_QD 512
 
+// E: keys per lane, candidate rows of up to 64 E.
+template <int E>
 __global__ __launch_bounds__(256) void coarse_topp_kernel(
     const uint32_t* __restrict__ cand, const uint32_t* __restrict__ cand_n, int CAP,
     const float* __restrict__ qn, const float* __restrict__ C, int nq, int L, int d, int P,
@@ -482,31 +489,37 @@ __global__ __launch_bounds__(256) void coarse_topp_kernel(
     for (int j = lane; j < d; j += 64) qs[j] = qn[(size_t)q * d + j];
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    uint64_t k4[4];
+    uint64_t kv[E];
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
+    for (int e = 0; e < E; e++) {
         const uint32_t t = e * 64 + lane;
-        k4[e] = ~0ull;
+        kv[e] = ~0ull;
         if (t < n) {
             const uint32_t cidx = cand[(size_t)q * CAP + t];
-            k4[e] = cand_key(1.0f - seq_dot_stream(qs, C + (size_t)cidx * d, d), cidx);
+            kv[e] = cand_key(1.0f - seq_dot_stream(qs, C + (size_t)cidx * d, d), cidx);
         }
     }
     if (n <= 64) {
-        uint64_t k1[1] = {k4[0]};
+        uint64_t k1[1] = {kv[0]};
         wave_sort_regs<1>(k1);
         if (lane < Pe) probe[(size_t)q * P + lane] = (uint32_t)k1[0];
     } else if (n <= 128) {
-        uint64_t k2[2] = {k4[0], k4[1]};
+        uint64_t k2[2] = {kv[0], kv[1]};
         wave_sort_regs<2>(k2);
 #pragma unroll
         for (int e = 0; e < 2; e++)
             if (e * 64 + lane < Pe) probe[(size_t)q * P + e * 64 + lane] = (uint32_t)k2[e];
-    } else {
+    } else if (E == 4 || n <= 256) {
+        uint64_t k4[4] = {kv[0], kv[1], kv[2], kv[3]};
         wave_sort_regs<4>(k4);
 #pragma unroll
         for (int e = 0; e < 4; e++)
             if (e * 64 + lane < Pe) probe[(size_t)q * P + e * 64 + lane] = (uint32_t)k4[e];
+    } else {
+        wave_sort_regs<E>(kv);
+#pragma unroll
+        for (int e = 0; e < E; e++)
+            if (e * 64 + lane < Pe) probe[(size_t)q * P + e * 64 + lane] = (uint32_t)kv[e];
     }
 }
 
@@ -515,8 +528,14 @@ void launch_coarse_topp(const uint32_t* cand, const uint32_t* cand_n, int P, con
                         uint32_t* flag_count, hipStream_t s) {
     if (nq <= 0) return;
     const int Pe = P < L ? P : L;
-    hipLaunchKernelGGL(coarse_topp_kernel, dim3((nq + 3) / 4), dim3(VGPU_BLOCK), 0, s, cand, cand_n,
-                       coarse_fused_cap(Pe), qn, C, nq, L, d, P, probe, flag_list, flag_count);
+    const int cap = coarse_fused_cap(Pe);
+    static_assert(32 * FC_J <= 256 && 32 * FC_J_WIDE <= 512, "keys per lane");
+    if (cap <= 256)
+        hipLaunchKernelGGL(coarse_topp_kernel<4>, dim3((nq + 3) / 4), dim3(VGPU_BLOCK), 0, s, cand, cand_n, cap,
+                           qn, C, nq, L, d, P, probe, flag_list, flag_count);
+    else
+        hipLaunchKernelGGL(coarse_topp_kernel<8>, dim3((nq + 3) / 4), dim3(VGPU_BLOCK), 0, s, cand, cand_n, cap,
+                           qn, C, nq, L, d, P, probe, flag_list, flag_count);
 }
 
 // ---- test entry: the bf16x3 dot products of the fused kernel ------------
