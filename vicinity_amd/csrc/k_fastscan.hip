@@ -31,31 +31,27 @@ __device__ __forceinline__ uint32_t round_to_u8(float v) {
     return (uint32_t)r;
 }
 
-// Four byte lookups: sel holds four indices 0..15 (one per byte) into the
-// 16-byte table t0..t3.  The byte mask of the indices >= 8 comes from
-// v_perm_b32's sign-replicating selectors (8..11 give 0xff when bit 15, 31,
-// 47 or 63 of the source pair is set): sel << 4 puts bit 3 of bytes 1 and 3
-// at bits 15 and 31, sel << 12 bit 3 of bytes 0 and 2 at bits 47 and 63.
-__device__ __forceinline__ uint32_t lookup16(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3,
-                                             uint32_t sel) {
-    uint32_t i7 = sel & 0x07070707u;
-    uint32_t lo = __builtin_amdgcn_perm(t1, t0, i7);  // entries 0..7
-    uint32_t hi = __builtin_amdgcn_perm(t3, t2, i7);  // entries 8..15
-    uint32_t m = __builtin_amdgcn_perm(sel << 12, sel << 4, 0x090b080au);
-    return (hi & m) | (lo & ~m);
-}
-
 // Accumulate one codebook of one packed dword (8 entries) into four packed
 // u16 pairs: a0 = entries (4w, 4w+2), a1 = (4w+1, 4w+3), a2/a3 the same + 16.
+// Each byte's index selects from the table's low (t0, t1) or high (t2, t3)
+// 8 bytes by its bit 3.  That byte mask comes from v_perm_b32's
+// sign-replicating selectors (8..11 give 0xff when bit 15, 31, 47 or 63 of
+// the source pair is set), straight from x: bit 3 of the low nibbles sits
+// at bits 3, 11, 19, 27 (brought to those bits by x << 4 and x << 12), bit 3
+// of the high nibbles at bits 7, 15, 23, 31 (x and x << 8).  Odd bytes move
+// to u16 slots by a byte select against zero (selector 0x0c gives 0x00).
 __device__ __forceinline__ void fs_accumulate(uint32_t x, uint32_t t0, uint32_t t1, uint32_t t2,
                                               uint32_t t3, uint32_t& a0, uint32_t& a1,
                                               uint32_t& a2, uint32_t& a3) {
-    uint32_t rl = lookup16(t0, t1, t2, t3, x & 0x0f0f0f0fu);
-    uint32_t rh = lookup16(t0, t1, t2, t3, (x >> 4) & 0x0f0f0f0fu);
+    const uint32_t il = x & 0x07070707u, ih = (x >> 4) & 0x07070707u;
+    const uint32_t ml = __builtin_amdgcn_perm(x << 12, x << 4, 0x090b080au);
+    const uint32_t mh = __builtin_amdgcn_perm(x << 8, x, 0x090b080au);
+    const uint32_t rl = (__builtin_amdgcn_perm(t3, t2, il) & ml) | (__builtin_amdgcn_perm(t1, t0, il) & ~ml);
+    const uint32_t rh = (__builtin_amdgcn_perm(t3, t2, ih) & mh) | (__builtin_amdgcn_perm(t1, t0, ih) & ~mh);
     a0 += rl & 0x00ff00ffu;
-    a1 += (rl >> 8) & 0x00ff00ffu;
+    a1 += __builtin_amdgcn_perm(0u, rl, 0x0c030c01u);
     a2 += rh & 0x00ff00ffu;
-    a3 += (rh >> 8) & 0x00ff00ffu;
+    a3 += __builtin_amdgcn_perm(0u, rh, 0x0c030c01u);
 }
 
 // u16 accumulator of entry c (0..7) of a lane: c -> vector 4w + c (c < 4) or
