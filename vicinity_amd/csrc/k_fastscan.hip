@@ -70,13 +70,15 @@ __device__ __forceinline__ uint32_t fs_acc(int c, uint32_t a0, uint32_t a1, uint
     }
 }
 
-// Wave-level quantisation of a float table lutf[M*16] into qlut (bytes).
-__device__ inline void fs_quantize(const float* lutf, uint8_t* qlut, int M, float& scale,
-                                   float& base_offset) {
+// Wave-level quantisation (quantize_lut_flat, pq_simd.rs:576-611) of the
+// float table whose entry e is value_of(e), e < M * 16, into qlut (bytes):
+// min and max over the entries, then each entry again for its byte.
+template <typename V>
+__device__ inline void fs_quantize_entries(V value_of, uint8_t* qlut, int M, float& scale, float& base_offset) {
     const int lane = threadIdx.x & 63;
     float mn = __int_as_float(0x7f800000), mx = __int_as_float(0xff800000);
     for (int e = lane; e < M * 16; e += 64) {
-        float v = lutf[e];
+        const float v = value_of(e);
         if (v < mn) mn = v;
         if (v > mx) mx = v;
     }
@@ -94,9 +96,14 @@ __device__ inline void fs_quantize(const float* lutf, uint8_t* qlut, int M, floa
         sc = range / 255.0f;
         inv = 255.0f / range;
     }
-    for (int e = lane; e < M * 16; e += 64) qlut[e] = (uint8_t)round_to_u8((lutf[e] - mn) * inv);
+    for (int e = lane; e < M * 16; e += 64) qlut[e] = (uint8_t)round_to_u8((value_of(e) - mn) * inv);
     scale = sc;
     base_offset = mn * (float)M;
+}
+
+// A float table held in LDS.
+__device__ inline void fs_quantize(const float* lutf, uint8_t* qlut, int M, float& scale, float& base_offset) {
+    fs_quantize_entries([&](int e) { return lutf[e]; }, qlut, M, scale, base_offset);
 }
 
 // Codebooks of at most this many bytes are staged in LDS once per query for
@@ -118,35 +125,12 @@ __device__ __forceinline__ float fs_lut_value(const float* rw, const float* cb, 
     return acc;
 }
 
-// The quantised table of one list by one wave, as fs_quantize makes it from
-// the float table, with the float entries recomputed in a second pass
-// instead of kept: min and max, then the bytes.
+// The quantised table of one list by one wave, its float entries computed
+// from the residual and the codebooks in each of the two passes instead of
+// kept.
 __device__ inline void fs_build_qlut(const float* rw, const float* cb, int M, int ds, uint8_t* qlut,
                                      float& scale, float& base_offset) {
-    const int lane = threadIdx.x & 63;
-    float mn = __int_as_float(0x7f800000), mx = __int_as_float(0xff800000);
-    for (int e = lane; e < M * 16; e += 64) {
-        const float v = fs_lut_value(rw, cb, ds, e);
-        if (v < mn) mn = v;
-        if (v > mx) mx = v;
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-        float omn = __shfl_xor(mn, off, 64), omx = __shfl_xor(mx, off, 64);
-        if (omn < mn) mn = omn;
-        if (omx > mx) mx = omx;
-    }
-    float range = mx - mn;
-    float sc, inv;
-    if (range < 1.1920929e-07f) {
-        sc = 1.0f;
-        inv = 0.0f;
-    } else {
-        sc = range / 255.0f;
-        inv = 255.0f / range;
-    }
-    for (int e = lane; e < M * 16; e += 64) qlut[e] = (uint8_t)round_to_u8((fs_lut_value(rw, cb, ds, e) - mn) * inv);
-    scale = sc;
-    base_offset = mn * (float)M;
+    fs_quantize_entries([&](int e) { return fs_lut_value(rw, cb, ds, e); }, qlut, M, scale, base_offset);
 }
 
 // Ascending bitonic sort of keys[0..n) by one wave (n a power of two).
