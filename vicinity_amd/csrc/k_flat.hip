@@ -688,16 +688,16 @@ static int flat_rank_keep(int k) {
     return 16 * FR_J;
 }
 
-// Slices for the ranking kernel: an even number of tiles each (stages are
-// tile pairs), enough workgroups for four waves of two per CU on 256 CUs,
-// slices of at least 64 tiles, and splits * kk merge entries within the
-// merge buffer; ib = the bits of a tile index within a slice.
+// Slices for the ranking kernel: a whole number of stages (FR_TPS tiles)
+// each, enough workgroups for four waves of two per CU on 256 CUs, slices of
+// at least 64 tiles, and splits * kk merge entries within the merge buffer;
+// ib = the bits of a tile index within a slice.
 static int flat_rank_splits(int nq, int n, int kk, int* tps, int* ib) {
     const int qb = (nq + FR_ROWS - 1) / FR_ROWS, ntiles = (n + 15) / 16;
     int sp = 1;
     while (qb * sp < 2048 && 2 * sp * kk <= FL_BUF && ntiles / (2 * sp) >= 64) sp <<= 1;
     int t = (ntiles + sp - 1) / sp;
-    t += t & 1;
+    t = (t + FR_TPS - 1) / FR_TPS * FR_TPS;  // whole stages: a stage never reaches past the padded copy
     int b = 1;
     while ((1 << b) < t) b++;
     *tps = t;
