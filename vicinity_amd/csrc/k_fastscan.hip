@@ -274,6 +274,10 @@ __global__ __launch_bounds__(256, 6) void fastscan_kernel(DevIndex ix, ScanArgs 
     // built when the blocks ahead of the round run short and the older list's
     // blocks are all scanned (its slot is then free).  Shorter lists take the
     // exact float path as their table is built.
+    // the packed blocks through a buffer resource: a lane's block offset in a
+    // vector register once per round, each codebook's row offset a scalar
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(ix.packed), (short)0, (int)(ix.pack_off[ix.L] * 16u * (uint32_t)M), 0x00020000);
     FsList prv, cur;
     prv.slot = 0;
     cur.slot = 1;
@@ -350,21 +354,21 @@ __global__ __launch_bounds__(256, 6) void fastscan_kernel(DevIndex ix, ScanArgs 
         const uint32_t* qw = (const uint32_t*)(qlut + (in_cur ? cur.slot : prv.slot) * M * 16);
         uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
         if (valid) {
-            const uint32_t* src =
-                (const uint32_t*)(ix.packed + ((size_t)(in_cur ? cur.pack : prv.pack) + bl) * 16 * M) + w;
+            const uint32_t voff = ((in_cur ? cur.pack : prv.pack) + bl) * 16u * (uint32_t)M + 4u * w;
             // FS_CW codebooks' code words in flight at a time
             int m = 0;
             for (; m + FS_CW <= M; m += FS_CW) {
                 uint32_t x[FS_CW];
 #pragma unroll
-                for (int u = 0; u < FS_CW; u++) x[u] = src[(m + u) * 4];
+                for (int u = 0; u < FS_CW; u++) x[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, voff, (m + u) * 16, 0);
 #pragma unroll
                 for (int u = 0; u < FS_CW; u++)
                     fs_accumulate(x[u], qw[(m + u) * 4], qw[(m + u) * 4 + 1], qw[(m + u) * 4 + 2],
                                   qw[(m + u) * 4 + 3], a0, a1, a2, a3);
             }
             for (; m < M; m++)
-                fs_accumulate(src[m * 4], qw[m * 4], qw[m * 4 + 1], qw[m * 4 + 2], qw[m * 4 + 3], a0, a1, a2, a3);
+                fs_accumulate(__builtin_amdgcn_raw_buffer_load_b32(prs, voff, m * 16, 0), qw[m * 4], qw[m * 4 + 1],
+                              qw[m * 4 + 2], qw[m * 4 + 3], a0, a1, a2, a3);
         }
 #pragma unroll
         for (int cc = 0; cc < 8; cc++) {
