@@ -2,7 +2,8 @@
 centroids, lists, codebooks and codes built on the GPU (assignment and
 centroid updates in kernels) equal the oracle's build bit for bit across
 shapes: the row width above the update kernel's 256 (host update), ds = 1,
-ksub 16, a training sample, and crowded k-means where clusters empty out."""
+ksub 16, a training sample, crowded k-means where clusters empty out, and a
+sample of many row blocks for the update's member-list sort."""
 
 import zlib
 
@@ -26,6 +27,8 @@ CASES = {
     "ksub16_d128": dict(n=3000, d=128, L=32, M=16, K=16, sample=None, iters=10),
     "sampled": dict(n=5000, d=64, L=40, M=8, K=128, sample=1500, iters=10),
     "crowded": dict(n=600, d=24, L=300, M=4, K=128, sample=None, iters=30),
+    # about 20 row blocks of the k-means update's member-list sort per pass
+    "many_blocks": dict(n=20000, d=32, L=64, M=8, K=256, sample=None, iters=6),
 }
 
 
