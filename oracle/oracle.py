@@ -1,8 +1,8 @@
 """ctypes wrapper around the C oracle (vicinity_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg as the checker.  The product (vicinity_amd/) never
-imports this module.
+bench.py's cpu_baseline leg, to check results against.  The product
+(vicinity_amd/) never imports this module.
 """
 
 from __future__ import annotations

@@ -1,8 +1,9 @@
 /*
  * vicinity_oracle.c -- CPU restatement of vicinity's IVF-PQ search path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker, never the product).  Loaded by
- * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
+ * TEST INFRASTRUCTURE ONLY (results are checked against it; it is never the
+ * product).  Loaded by tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg.
  *
  * Reference files (vicinity repository root):
  *   src/ivf_pq/search.rs   normalize_query 55-62, finish_top_k_by_distance 64-75,

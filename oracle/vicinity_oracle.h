@@ -1,9 +1,9 @@
 /*
  * vicinity_oracle.h -- CPU restatement of vicinity's IVF-PQ search path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: it is loaded by
- * tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg, and
- * never by the product (vicinity_amd/).  Every function cites the reference
+ * TEST INFRASTRUCTURE ONLY.  Results are checked against this library: it is
+ * loaded by tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline
+ * leg, and never by the product (vicinity_amd/).  Every function cites the reference
  * file:line it restates (paths relative to the vicinity repository root).
  *
  * Arithmetic rules (all in IEEE binary32, compiled with -ffp-contract=off and
