@@ -424,6 +424,7 @@ hipError_t launch_kmeans_update(const float* x, int n, int d, int w, int M, cons
                                 int K, const uint8_t* active, bool normalize, float* out, uint32_t* scratch,
                                 size_t scratch_words, hipStream_t s) {
     if (n <= 0 || M <= 0 || K <= 0) return hipSuccess;
+    if ((uint64_t)M * (uint64_t)n >= ((uint64_t)1 << 32)) return hipErrorInvalidValue;  // 32-bit member lists
     if (scratch_words < kmeans_update_scratch_words(n, M, K)) return hipErrorInvalidValue;
     const KmSort ks = km_layout(n, M, K, scratch);
     launch_zero_words(reinterpret_cast<unsigned long long*>(ks.cnt), (ks.keys * ks.nb + 1) / 2, s);

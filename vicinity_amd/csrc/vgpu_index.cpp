@@ -310,7 +310,8 @@ void IvfpqIndex::train_pq(const std::vector<float>& res, size_t nt, size_t Kc, u
     dcodes.reserve(nt * M);
     std::vector<uint8_t> cur(nt * M), prev(nt * M), active(M);
     std::vector<char> frozen(M, 0);
-    const bool gpu_update = ds <= 256;
+    // the update's member lists hold 32-bit row indices of every subspace
+    const bool gpu_update = ds <= 256 && (uint64_t)nt * M < ((uint64_t)1 << 32);
     DevBuf<uint32_t> dks;  // member lists of the update
     if (gpu_update) dks.reserve(kmeans_update_scratch_words((int)nt, (int)M, (int)Ke));
     dcb.upload(codebooks.data(), codebooks.size(), stream);
@@ -559,6 +560,10 @@ void IvfpqIndex::upload_index() {
             uint64_t len = offsets[l + 1] - offsets[l];
             poff[l + 1] = poff[l] + (len >= 16 ? (uint32_t)((len + 31) / 32) : 0u);
         }
+        // the FastScan kernel addresses the packed blocks with 32-bit byte offsets
+        if ((uint64_t)poff[L] * 16 * M >= ((uint64_t)1 << 32))
+            throw Error(VGPU_ERR_UNSUPPORTED, "4-bit packed codes of " + std::to_string((uint64_t)poff[L] * 16 * M) +
+                                                  " bytes: FastScan addresses at most 4 GiB");
         d_pack_off.upload(poff.data(), L + 1, stream);
         d_packed.reserve((size_t)poff[L] * 16 * M + 16);
         dix.pack_off = d_pack_off.p;

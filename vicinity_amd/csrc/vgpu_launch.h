@@ -202,8 +202,9 @@ void launch_procrustes(const uint8_t* codes, const float* cb, int M, int K, int 
 // row; subspaces with active[m] == 0 are skipped (active may be null).  u8:
 // labels[i * M + m] code bytes over row slices x[i * d + m * w .. + w);
 // otherwise u32 labels[i] over whole rows (w = d <= 256).  Labels must be
-// below K.  The member lists live in scratch (device words, at least
-// kmeans_update_scratch_words(n, M, K); hipErrorInvalidValue when fewer).
+// below K, and M n below 2^32 (32-bit member lists).  The member lists live
+// in scratch (device words, at least kmeans_update_scratch_words(n, M, K));
+// hipErrorInvalidValue when either does not hold.
 size_t kmeans_update_scratch_words(int n, int M, int K);
 hipError_t launch_kmeans_update(const float* x, int n, int d, int w, int M, const void* labels, bool u8,
                                 int K, const uint8_t* active, bool normalize, float* out, uint32_t* scratch,
