@@ -109,7 +109,7 @@ __device__ inline void fs_quantize(const float* lutf, uint8_t* qlut, int M, floa
 // Codebooks of at most this many bytes are staged in LDS once per query for
 // the table builds; larger ones are read from global memory.
 #define FS_CB_LDS 16384
-#define FS_CW 8  // codebooks whose code words a lane loads together
+#define FS_CW 16  // codebooks whose code words a lane loads together
 __host__ __device__ inline bool fs_cb_in_lds(int M, int ds) { return (size_t)M * 16 * ds * 4 <= FS_CB_LDS; }
 
 // Entry e = m * 16 + c of the float table of residual rw:
