@@ -115,6 +115,15 @@ __host__ __device__ inline bool fs_cb_in_lds(int M, int ds) { return (size_t)M *
 // Entry e = m * 16 + c of the float table of residual rw:
 // sum_j (r_mj - cw_mcj)^2 in j order (pq.rs:232-251).
 __device__ __forceinline__ float fs_lut_value(const float* rw, const float* cb, int ds, int e) {
+    if (ds == 2) {  // straight-line: one 8-byte read of each operand, the same sum
+        const float2 c2 = *reinterpret_cast<const float2*>(cb + (size_t)e * 2);
+        const float2 r2 = *reinterpret_cast<const float2*>(rw + (e >> 4) * 2);
+        const float d0 = r2.x - c2.x, d1 = r2.y - c2.y;
+        float acc = 0.0f;
+        acc += d0 * d0;
+        acc += d1 * d1;
+        return acc;
+    }
     const float* cw = cb + (size_t)e * ds;
     const float* r = rw + (e >> 4) * ds;
     float acc = 0.0f;
