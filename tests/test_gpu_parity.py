@@ -477,3 +477,37 @@ def test_many_flagged_probe_queries(vg, oracle):
         lists = ix.probe(q, P)
         for i in range(len(q)):
             assert lists[i].tolist() == oix.probe(q[i], P)[0].tolist(), (rep, i)
+
+@pytest.mark.parametrize("P", [48, 64])
+def test_wide_candidate_window_probe_ties(vg, oracle, P):
+    """Above 32 probes the coarse lists keep ten keys and a query may bring up
+    to 320 candidates to the exact order: 300 exact copies of one centroid,
+    spread over every column class (about five per kept list, so no list
+    overflows), all tie for a query near them.  Probe lists equal the
+    oracle's, ties in list order (find_nearest_centroids, search.rs:1602-1617)."""
+    from vicinity_amd import IVFPQIndex
+
+    _print_case(f"probe ties: 300 copies of a centroid, nprobe {P}, L 4096")
+    d, L, copies = 32, 4096, 300
+    rng = np.random.default_rng(5 + P)
+    cent = oracle.normalize_rows(rng.standard_normal((L, d)).astype(np.float32))
+    base = cent[7].copy()
+    cent[(7 + 13 * np.arange(copies)) % L] = base
+    n = 2 * L
+    M, K = 4, 16
+    cb = rng.standard_normal(M * K * (d // M)).astype(np.float32)
+    off, ids = oracle.build_lists((np.arange(n) % L).astype(np.uint32), L)
+    codes = rng.integers(0, K, (n, M), dtype=np.uint8)
+    ix = IVFPQIndex(d, num_clusters=L, num_codebooks=M, codebook_size=K, nprobe=P)
+    ix.load_artifacts(cent, cb, off, ids, codes)
+    near = (base[None, :] + 0.001 * rng.standard_normal((40, d))).astype(np.float32)
+    q = np.concatenate([near, rng.standard_normal((24, d)).astype(np.float32)])
+    oix = oracle.Index(cent, cb, off, ids, codes, np.arange(n, dtype=np.uint32), None, M, K)
+    lists = ix.probe(q, P)
+    for i in range(len(q)):
+        assert lists[i].tolist() == oix.probe(q[i], P)[0].tolist(), i
+    # nearly all of the 40 tied windows went through the candidate order, not
+    # the exact fallback (a window that also takes near-tied other lists may
+    # still overflow a kept list)
+    ix.batch_search(q, 10, nprobe=P)
+    assert ix.last_stats()["coarse_overflow"] <= 4
