@@ -53,6 +53,11 @@
  *                                          category over reconstruct, results
  *                                          carry the category
  *   or_pq_encode                           argmin property (pq.rs:485-551)
+ *   or_assign_cosine                       float64 argmin of 1 - x.c wherever the
+ *                                          float32 rounding bound separates it,
+ *                                          equals or_nearest_centroids(.., 1),
+ *                                          exact ties (duplicated centroids, zero
+ *                                          row, d = 1) go to the lowest index
  *   or_matvec / or_matvec_t                KATs opq.rs:362-385, float64 products,
  *                                          a permutation exactly
  *   or_polar                               numpy (LAPACK) SVD U V^T, R^T M

@@ -355,6 +355,76 @@ def test_sample_indices(oracle):
     assert np.array_equal(oracle.sample_indices(10, 0, 1), np.arange(10))
 
 
+def _assign_f64_candidates(x, cent):
+    """Rows of candidate sets for argmin_c (1 - x.c): every c whose float64
+    score is within twice the float32 rounding bound of the float64 minimum.
+    Bound per score: a sequential float32 dot of length d is within
+    gamma_d * sum|x_j c_j| of the true dot (gamma_d = d u / (1 - d u),
+    u = 2^-24), and 1 - dot adds one rounding of at most u * |1 - dot|."""
+    d = x.shape[1]
+    u = 2.0 ** -24
+    gamma = d * u / (1 - d * u)
+    x64, c64 = x.astype(np.float64), cent.astype(np.float64)
+    s = 1.0 - x64 @ c64.T
+    err = gamma * (np.abs(x64) @ np.abs(c64).T) + u * np.abs(s)
+    out = []
+    for i in range(x.shape[0]):
+        lo = s[i].min()
+        out.append(np.flatnonzero(s[i] - err[i] <= lo + err[i].max() * 1.0001))
+    return out
+
+
+@pytest.mark.parametrize("n,L,d", [(500, 37, 13), (300, 64, 32), (200, 9, 3), (150, 128, 97)])
+def test_assign_cosine_is_the_argmin(oracle, n, L, d):
+    """kmeans.rs:97-107 (called from search.rs:621, metric distance.rs:104-109):
+    each vector goes to argmin over centroids of 1 - dot, first minimum wins.
+    Checked against a float64 argmin wherever the float32 rounding bound
+    separates the minimum, against the brute-force-pinned probe selection
+    with nprobe 1, and on exact ties (duplicated centroids, a zero row)."""
+    rng = np.random.default_rng(n + L + d)
+    x = oracle.normalize_rows(rng.standard_normal((n, d)).astype(np.float32))
+    cent = oracle.normalize_rows(rng.standard_normal((L, d)).astype(np.float32))
+    a = oracle.assign_cosine(x, cent)
+    assert a.dtype == np.uint32 and a.shape == (n,)
+    cands = _assign_f64_candidates(x, cent)
+    unique = 0
+    for i in range(n):
+        assert a[i] in cands[i]
+        if cands[i].size == 1:
+            unique += 1
+    assert unique >= n * 0.9  # the float64 check decides most rows
+    for i in range(0, n, max(1, n // 40)):
+        lists, _ = oracle.nearest_centroids(x[i], cent, 1)
+        assert lists.tolist() == [a[i]]
+
+
+def test_assign_cosine_ties_go_to_the_lowest_index(oracle):
+    rng = np.random.default_rng(11)
+    d = 21
+    base = oracle.normalize_rows(rng.standard_normal((6, d)).astype(np.float32))
+    # centroid rows 0..11: base rows, then the same rows again in reverse
+    # order, so every score occurs twice at indices i and 11 - i.
+    cent = np.ascontiguousarray(np.concatenate([base, base[::-1]]))
+    x = oracle.normalize_rows(
+        (base[rng.integers(0, 6, 200)] + 0.3 * rng.standard_normal((200, d))).astype(np.float32))
+    a = oracle.assign_cosine(x, cent)
+    assert a.max() < 6  # a `<=` rule would take the later copy
+    for i in range(200):
+        assert a[i] == np.argmin(1.0 - x[i].astype(np.float64) @ base.astype(np.float64).T) \
+            or a[i] in _assign_f64_candidates(x[i:i + 1], base)[0]
+    # A zero vector scores 1 against every centroid: index 0.
+    z = np.zeros((1, d), np.float32)
+    assert oracle.assign_cosine(z, cent).tolist() == [0]
+    # All centroids equal: index 0 for every row.
+    same = np.ascontiguousarray(np.repeat(base[:1], 9, axis=0))
+    assert oracle.assign_cosine(x[:20], same).tolist() == [0] * 20
+    # d = 1: rows are +-1, every score is exactly 0 or 2, and the answer is
+    # the first centroid of the row's sign.
+    c1 = np.array([[-1.0], [-1.0], [1.0], [-1.0], [1.0]], np.float32)
+    x1 = np.array([[1.0], [-1.0], [1.0]], np.float32)
+    assert oracle.assign_cosine(x1, c1).tolist() == [2, 0, 2]
+
+
 @pytest.mark.parametrize("metric", [0, 1])
 def test_kmeans_fixed_point(oracle, metric):
     rng = np.random.default_rng(metric)
