@@ -134,7 +134,10 @@ int vgpu_ivfpq_search_batch(vgpu_ivfpq *h, const float *queries, size_t nq, size
                             size_t nprobe, size_t rerank_pool, int64_t *out_ids,
                             float *out_dists);
 /* Same with device pointers on `stream` (a hipStream_t; NULL = the stream
- * of the call's borrowed workspace); returns after the search completes. */
+ * of the call's borrowed workspace); returns after the search completes.
+ * A query holding a NaN or an infinity is VGPU_ERR_INVALID_PARAMETER, as in
+ * vgpu_ivfpq_search_batch; the other rows of the batch are still written, and
+ * the offending rows are padding (-1, +inf). */
 int vgpu_ivfpq_search_batch_device(vgpu_ivfpq *h, const float *d_queries, size_t nq,
                                    size_t dim, size_t k, size_t nprobe, size_t rerank_pool,
                                    int64_t *d_out_ids, float *d_out_dists, void *stream);
@@ -145,10 +148,18 @@ int vgpu_ivfpq_search_batch_device(vgpu_ivfpq *h, const float *d_queries, size_t
  * per GPU, held until the process ends), and a batch goes in query chunks
  * that fit it; a shape whose single query does not fit (about 2.5 KB per
  * query at d 128, nprobe 32, k 100) is VGPU_ERR_INVALID_PARAMETER.  Every
- * call on one GPU shares that array, whatever the handle: calls that overlap
- * on one GPU race.  The index's device must be current.  stream NULL = the
+ * call on one GPU shares that array, whatever the handle: the library holds a
+ * per-GPU lock across each call, so synchronous calls from several threads
+ * take turns.  The index's device must be current.  stream NULL = the
  * handle's own stream; returns after the search completes; does not update
- * vgpu_ivfpq_last_stats or the profiling timers. */
+ * vgpu_ivfpq_last_stats or the profiling timers.  Non-finite queries as for
+ * vgpu_ivfpq_search_batch_device.
+ * Under stream capture (hipStreamIsCapturing) the call records its kernels
+ * and returns without waiting: completion is the caller's, a non-finite query
+ * shows only as a padding row, and replays of captured graphs that overlap
+ * each other or another call on the same GPU race (the lock covers recording,
+ * not replay).  The first call on a GPU (which looks up the array's address)
+ * must not be under capture. */
 int vgpu_ivfpq_search_batch_device_noalloc(vgpu_ivfpq *h, const float *d_queries, size_t nq,
                                            size_t dim, size_t k, size_t nprobe,
                                            size_t rerank_pool, int64_t *d_out_ids,

@@ -106,3 +106,83 @@ def test_a_batch_that_takes_several_scratch_chunks(small):
         a = _alloc(ix, qq, 100, 8)
         b = _noalloc(ix, qq, 100, 8)
         assert np.array_equal(a[0], b[0]) and a[1].tobytes() == b[1].tobytes()
+
+
+def test_two_threads_on_two_handles(small):
+    """Every call on a GPU shares its one scratch array: the library's per-GPU
+    lock makes concurrent synchronous calls (here on two handles from two
+    threads) take turns, so both results equal the allocating entry point."""
+    import threading
+
+    import vicinity_amd as v
+
+    ix, q = small
+    _print_case("no-alloc: two threads, two handles, 40 calls each")
+    w = v.datagen.ivfpq_small(n=8000, nq=300)
+    other = v.IVFPQIndex(32, num_clusters=32, num_codebooks=8, codebook_size=256, nprobe=6, seed=9)
+    other.add_items(w.base)
+    other.build(kmeans_max_iter=5)
+    cases = [(ix, q[:900].contiguous(), 10, 8), (other, q[:700].contiguous(), 20, 6)]
+    want = [_alloc(h, qq, k, p) for h, qq, k, p in cases]
+    errors = []
+
+    def run(i):
+        import torch
+
+        torch.cuda.set_device(0)
+        h, qq, k, p = cases[i]
+        try:
+            for _ in range(40):
+                got = _noalloc(h, qq, k, p)
+                if not (np.array_equal(got[0], want[i][0]) and got[1].tobytes() == want[i][1].tobytes()):
+                    errors.append(f"thread {i}: result differs")
+                    return
+        except Exception as e:  # reported below
+            errors.append(f"thread {i}: {e!r}")
+
+    ts = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors, errors
+
+
+def test_graph_capture_and_replay(small):
+    """The call under stream capture records its kernels without waiting;
+    each replay of the graph (with eager work and synchronisations between
+    replays) equals the allocating entry point on the replay's queries."""
+    import torch
+
+    from vicinity_amd import _lib
+
+    ix, q = small
+    nq, k, nprobe = 800, 10, 8
+    _print_case(f"no-alloc: capture nq {nq} k {k} nprobe {nprobe}, four replays")
+    qbuf = q[:nq].clone()
+    ids = torch.full((nq, k), -7, dtype=torch.int64, device="cuda:0")
+    dists = torch.full((nq, k), -7.0, dtype=torch.float32, device="cuda:0")
+    lib = _lib.load()
+    # warm-up call outside capture: scratch address lookup, kernel attributes
+    _noalloc(ix, qbuf, k, nprobe)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        rc = lib.vgpu_ivfpq_search_batch_device_noalloc(
+            ix._h, qbuf.data_ptr(), nq, qbuf.shape[1], k, nprobe, 0, ids.data_ptr(),
+            dists.data_ptr(), ctypes.c_void_p(side.cuda_stream))
+    assert rc == 0, lib.vgpu_last_error()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        src = q[200:200 + nq] if rep % 2 else q[:nq]
+        qbuf.copy_(src)
+        ids.fill_(-7)
+        dists.fill_(-7.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want = _alloc(ix, src.contiguous(), k, nprobe)
+        assert np.array_equal(ids.cpu().numpy(), want[0]), f"replay {rep}"
+        assert dists.cpu().numpy().tobytes() == want[1].tobytes(), f"replay {rep}"
+    del g

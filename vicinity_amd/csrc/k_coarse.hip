@@ -18,11 +18,16 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // one lane per row, norm = sqrt(s), then every element x / norm when
 // norm > 1e-10 (search.rs:55-62; divide and sqrt are correctly rounded).
 // norms[i] receives an upper bound of ||out_i|| used by the error margins.
+// A row holding a NaN or an infinity is searched as the zero vector (every
+// later kernel sees finite values), marked in qbad[i] (when given) and
+// counted in *nbad, so the host reports it and its result row is padding.
 #define NR_ROWS 16
 
 __global__ __launch_bounds__(256) void normalize_kernel(const float* __restrict__ x,
                                                         float* __restrict__ out,
-                                                        float* __restrict__ norms, int n, int d) {
+                                                        float* __restrict__ norms, int n, int d,
+                                                        uint32_t* __restrict__ qbad,
+                                                        unsigned int* __restrict__ nbad) {
     extern __shared__ float srow[];  // [NR_ROWS][d + 1]
     __shared__ float snorm[NR_ROWS];
     const int tid = threadIdx.x;
@@ -33,7 +38,14 @@ __global__ __launch_bounds__(256) void normalize_kernel(const float* __restrict_
     for (int e = tid; e < rows * d; e += VGPU_BLOCK) srow[(e / d) * st + e % d] = src[e];
     __syncthreads();
     if (tid < rows) {
-        const float* xr = srow + tid * st;
+        float* xr = srow + tid * st;
+        if (row_nonfinite(xr, d)) {
+            for (int j = 0; j < d; j++) xr[j] = 0.0f;
+            if (nbad) atomicAdd(nbad, 1u);
+            if (qbad) qbad[r0 + tid] = 1u;
+        } else if (qbad) {
+            qbad[r0 + tid] = 0u;
+        }
         float s = 0.0f;
         for (int j = 0; j < d; j++) s = __fadd_rn(s, __fmul_rn(xr[j], xr[j]));
         const float nrm = sqrtf(s);
@@ -49,12 +61,13 @@ __global__ __launch_bounds__(256) void normalize_kernel(const float* __restrict_
     }
 }
 
-void launch_normalize(const float* x, float* out, float* norms, int n, int d, hipStream_t s) {
+void launch_normalize(const float* x, float* out, float* norms, int n, int d, hipStream_t s,
+                      uint32_t* qbad, unsigned int* nbad) {
     if (n <= 0) return;
     const size_t lds = (size_t)NR_ROWS * (d + 1) * sizeof(float);
     ensure_dyn_lds((const void*)normalize_kernel, lds);
     hipLaunchKernelGGL(normalize_kernel, dim3((n + NR_ROWS - 1) / NR_ROWS), dim3(VGPU_BLOCK), lds, s,
-                       x, out, norms, n, d);
+                       x, out, norms, n, d, qbad, nbad);
 }
 
 // ---- coarse GEMM --------------------------------------------------------

@@ -280,7 +280,8 @@ template <int DT, int J>
 __global__ __launch_bounds__(FC_THREADS) void coarse_fused_kernel(
     const float* __restrict__ Q, int nq, int d, const uint4* __restrict__ Cb, int L, float cmax,
     int Pe, int IB, int normalize, float* __restrict__ qn_out, float* __restrict__ qnorm_out,
-    uint32_t* __restrict__ cand, uint32_t* __restrict__ cand_n) {
+    uint32_t* __restrict__ cand, uint32_t* __restrict__ cand_n, uint32_t* __restrict__ qbad,
+    unsigned int* __restrict__ nbad) {
     extern __shared__ __align__(16) char smem[];
     constexpr int CAP = 32 * J;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
@@ -293,6 +294,8 @@ __global__ __launch_bounds__(FC_THREADS) void coarse_fused_kernel(
     const int st = d + 1;
 
     // ---- normalise (search.rs:55-62): sequential sum of squares per row.
+    // A row holding a NaN or an infinity is searched as the zero vector,
+    // marked in qbad and counted in *nbad (its result row becomes padding).
     const float* src = Q + (size_t)q0 * d;
     for (int e = tid; e < FC_QB * d; e += FC_THREADS) {
         const int r = e / d;
@@ -300,7 +303,14 @@ __global__ __launch_bounds__(FC_THREADS) void coarse_fused_kernel(
     }
     __syncthreads();
     if (tid < FC_QB) {
-        const float* xr = tile + tid * st;
+        float* xr = tile + tid * st;
+        if (row_nonfinite(xr, d)) {
+            for (int j = 0; j < d; j++) xr[j] = 0.0f;
+            if (nbad) atomicAdd(nbad, 1u);
+            if (qbad && tid < rows) qbad[q0 + tid] = 1u;
+        } else if (qbad && tid < rows) {
+            qbad[q0 + tid] = 0u;
+        }
         float s = 0.0f;
         for (int j = 0; j < d; j++) s = __fadd_rn(s, __fmul_rn(xr[j], xr[j]));
         const float nrm = sqrtf(s);
@@ -432,7 +442,7 @@ bool coarse_fused_supported(int d, int P) { return d >= 1 && d <= 128 && P >= 1 
 template <int DT, int J>
 static void launch_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int Pe,
                          int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
-                         hipStream_t s) {
+                         hipStream_t s, uint32_t* qbad, unsigned int* nbad) {
     const size_t lds = fc_lds_bytes(d, DT, J);
     // index bits: tiles ceil(L / 16) <= 2^IB
     int IB = 0;
@@ -440,29 +450,29 @@ static void launch_fused(const float* Q, int nq, int d, const uint4* Cb, int L, 
     auto k = coarse_fused_kernel<DT, J>;
     ensure_dyn_lds((const void*)k, lds);
     hipLaunchKernelGGL(k, dim3((nq + FC_QB - 1) / FC_QB), dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, cmax,
-                       Pe, IB, normalize, qn, qnorm, cand, cand_n);
+                       Pe, IB, normalize, qn, qnorm, cand, cand_n, qbad, nbad);
 }
 
 template <int DT>
 static void launch_fused_j(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int Pe,
                            int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
-                           hipStream_t s) {
+                           hipStream_t s, uint32_t* qbad, unsigned int* nbad) {
     if (fc_keys(Pe) == FC_J_WIDE)
-        launch_fused<DT, FC_J_WIDE>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s);
+        launch_fused<DT, FC_J_WIDE>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s, qbad, nbad);
     else
-        launch_fused<DT, FC_J>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s);
+        launch_fused<DT, FC_J>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s, qbad, nbad);
 }
 
 void launch_coarse_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int P,
                          int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
-                         hipStream_t s) {
+                         hipStream_t s, uint32_t* qbad, unsigned int* nbad) {
     if (nq <= 0) return;
     const int Pe = P < L ? P : L;
     switch ((d + 31) / 32) {
-        case 1: launch_fused_j<1>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s); break;
-        case 2: launch_fused_j<2>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s); break;
-        case 3: launch_fused_j<3>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s); break;
-        default: launch_fused_j<4>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s); break;
+        case 1: launch_fused_j<1>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s, qbad, nbad); break;
+        case 2: launch_fused_j<2>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s, qbad, nbad); break;
+        case 3: launch_fused_j<3>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s, qbad, nbad); break;
+        default: launch_fused_j<4>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s, qbad, nbad); break;
     }
 }
 

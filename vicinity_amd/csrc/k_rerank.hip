@@ -110,7 +110,8 @@ __global__ __launch_bounds__(256) void finish_kernel(
     const uint32_t* __restrict__ vidx, const float* __restrict__ dist,
     const uint32_t* __restrict__ doc_ids, int nq, int kin, int k, int64_t* __restrict__ out_ids,
     float* __restrict__ out_dists, const uint32_t* __restrict__ qstat,
-    unsigned long long* __restrict__ counters, uint32_t* flag_count, uint32_t* cflag_count) {
+    unsigned long long* __restrict__ counters, uint32_t* flag_count, uint32_t* cflag_count,
+    const uint32_t* __restrict__ qbad) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool map = vidx != nullptr;
     const int q0 = blockIdx.x * (map ? FINISH_Q : FINISH_Q * FINISH_STATS);
@@ -125,6 +126,7 @@ __global__ __launch_bounds__(256) void finish_kernel(
         for (int u = 0; u < U; u++) {
             const int r = wave + (VGPU_BLOCK / 64) * (u % RW), j = c0 + lane + 64 * (u / RW);
             v[u] = r < nqb && j < k && j < kin ? vidx[(size_t)(q0 + r) * kin + j] : 0xffffffffu;
+            if (qbad && r < nqb && qbad[q0 + r]) v[u] = 0xffffffffu;  // non-finite query
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -140,6 +142,20 @@ __global__ __launch_bounds__(256) void finish_kernel(
                 const size_t o = (size_t)(q0 + r) * k + j;
                 out_ids[o] = v[u] != 0xffffffffu ? (int64_t)id[u] : (int64_t)-1;
                 out_dists[o] = dv[u];
+            }
+        }
+    }
+    // rows written by the scan: a non-finite query's row becomes padding
+    if (!map && qbad && wave < 2) {
+        const int r = wave * 64 + lane;
+        uint64_t m = __ballot(q0 + r < nq && qbad[q0 + r] != 0u);
+        while (m) {
+            const int b = __ffsll((unsigned long long)m) - 1;
+            m &= m - 1;
+            const size_t row = (size_t)(q0 + wave * 64 + b) * k;
+            for (int j = lane; j < k; j += 64) {
+                out_ids[row + j] = -1;
+                out_dists[row + j] = __int_as_float(0x7f800000);
             }
         }
     }
@@ -178,12 +194,12 @@ __global__ __launch_bounds__(256) void finish_kernel(
 void launch_finish(const uint32_t* vidx, const float* dist, const uint32_t* doc_ids, int nq, int kin,
                    int k, int64_t* out_ids, float* out_dists, const uint32_t* qstat,
                    unsigned long long* counters, uint32_t* flag_count, uint32_t* cflag_count,
-                   hipStream_t s) {
+                   hipStream_t s, const uint32_t* qbad) {
     if (nq <= 0) return;
     const int per = vidx ? FINISH_Q : FINISH_Q * FINISH_STATS;
     hipLaunchKernelGGL(finish_kernel, dim3((nq + per - 1) / per), dim3(VGPU_BLOCK), 0, s, vidx,
                        dist, doc_ids, nq, kin, k, out_ids, out_dists, qstat, counters, flag_count,
-                       cflag_count);
+                       cflag_count, qbad);
 }
 
 // Clear n 64-bit words (the per-call scalars) with a kernel, not a

@@ -234,6 +234,7 @@ int vgpu_ivfpq_search_batch_device_noalloc(vgpu_ivfpq* h, const float* d_queries
         check_dim(*h->ix, dim);
         if (nq == 0 || k == 0) return;
         uint8_t* scratch = vgpu::noalloc_scratch(h->ix->device);
+        std::lock_guard<std::mutex> dev_lk(vgpu::noalloc_call_mutex(h->ix->device));
         h->ix->search_device_in(d_queries, nq, k, nprobe, rerank_pool, d_out_ids, d_out_dists,
                                 (hipStream_t)stream, scratch, NOALLOC_SCRATCH_BYTES);
     });

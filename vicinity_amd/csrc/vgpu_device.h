@@ -10,6 +10,13 @@
 #define VGPU_BLOCK 256
 #define VGPU_WAVE 64
 
+// True when one of the n values is a NaN or an infinity (exponent all ones).
+__device__ __forceinline__ bool row_nonfinite(const float* x, int n) {
+    uint32_t any = 0;
+    for (int j = 0; j < n; j++) any |= (__float_as_uint(x[j]) & 0x7f800000u) == 0x7f800000u;
+    return any != 0;
+}
+
 // f32::total_cmp as an unsigned key: u32 order == total_cmp order
 // (src/ivf_pq/search.rs:64-75 sorts with total_cmp; NaN sorts last).
 __device__ __forceinline__ uint32_t fkey(float f) {

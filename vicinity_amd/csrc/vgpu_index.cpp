@@ -723,6 +723,7 @@ size_t IvfpqIndex::ws_layout(const SearchPlan& pl, uint8_t* base, WsPtrs* out) c
     carve(w.scal, kScalWords);
     carve(w.qn, c * d);
     carve(w.qnorm, c);
+    carve(w.qbad, c);
     if (pl.fused) {
         carve(w.cand, c * (size_t)coarse_fused_cap((int)pl.P));
         carve(w.cand_n, c);
@@ -751,13 +752,14 @@ void IvfpqIndex::coarse_probe(const float* d_q, size_t nq, size_t P, const Searc
                               const WsPtrs& w, hipStream_t s, hipEvent_t mid) {
     unsigned int* overflow = reinterpret_cast<unsigned int*>(w.scal + kOverflowWord);
     uint32_t* cflag_count = reinterpret_cast<uint32_t*>(w.scal + kCFlagWord);
+    unsigned int* nbad = reinterpret_cast<unsigned int*>(w.scal + kBadWord);
     if (P == 0) {
-        launch_normalize(d_q, w.qn, w.qnorm, (int)nq, (int)d, s);
+        launch_normalize(d_q, w.qn, w.qnorm, (int)nq, (int)d, s, w.qbad, nbad);
         return;
     }
     if (pl.fused) {
         launch_coarse_fused(d_q, (int)nq, (int)d, dix.cb16, (int)L, dix.cmax, (int)P, 1, w.qn, w.qnorm,
-                            w.cand, w.cand_n, s);
+                            w.cand, w.cand_n, s, w.qbad, nbad);
         if (mid) VGPU_HIP(hipEventRecord(mid, s));
         launch_coarse_topp(w.cand, w.cand_n, (int)P, w.qn, d_centroids.p, (int)nq, (int)L, (int)d, w.probe,
                            w.cflag_list, cflag_count, s);
@@ -765,16 +767,40 @@ void IvfpqIndex::coarse_probe(const float* d_q, size_t nq, size_t P, const Searc
                                     w.probe, overflow, w.cflag_list, cflag_count, s, w.fdots,
                                     reinterpret_cast<uint32_t*>(w.scal + kFDoneWord));
     } else if (P > 1024) {  // every list's exact score, then the P smallest
-        launch_normalize(d_q, w.qn, w.qnorm, (int)nq, (int)d, s);
+        launch_normalize(d_q, w.qn, w.qnorm, (int)nq, (int)d, s, w.qbad, nbad);
         if (mid) VGPU_HIP(hipEventRecord(mid, s));
         launch_coarse_select_wide(w.dots, w.qn, d_centroids.p, (int)nq, (int)L, (int)d, (int)P, w.probe, s);
     } else {
-        launch_normalize(d_q, w.qn, w.qnorm, (int)nq, (int)d, s);
+        launch_normalize(d_q, w.qn, w.qnorm, (int)nq, (int)d, s, w.qbad, nbad);
         launch_coarse_dots(w.qn, d_centroids.p, w.dots, (int)nq, (int)L, (int)d, s);
         if (mid) VGPU_HIP(hipEventRecord(mid, s));
         launch_coarse_select(w.dots, w.qn, w.qnorm, d_centroids.p, (int)nq, (int)L, (int)d, (int)P, dix.cmax,
                              w.probe, overflow, w.cflag_list, cflag_count, s);
     }
+}
+
+// A query holding a NaN or an infinity is searched as the zero vector and its
+// row padded; the call then reports it, like the host entry points.
+static void check_nonfinite(unsigned long long word) {
+    const unsigned int n = (unsigned int)(word & 0xffffffffu);
+    if (n)
+        throw Error(VGPU_ERR_INVALID_PARAMETER, "query contains a non-finite value (" + std::to_string(n) +
+                                                    " queries; their rows are padding)");
+}
+
+// End of an allocation-free call.  Under stream capture nothing may wait on
+// the stream: the call returns with its work recorded, completion is the
+// caller's, and non-finite queries show only as padding rows.  Otherwise wait,
+// then read the non-finite count back with a synchronous 4-byte copy (no
+// allocation).
+static void complete_noalloc(const WsPtrs& w, hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    VGPU_HIP(hipStreamIsCapturing(s, &cs));
+    if (cs != hipStreamCaptureStatusNone) return;
+    VGPU_HIP(hipStreamSynchronize(s));
+    unsigned int nbad = 0;
+    VGPU_HIP(hipMemcpy(&nbad, w.scal + kBadWord, sizeof(nbad), hipMemcpyDeviceToHost));
+    check_nonfinite(nbad);
 }
 
 void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, const WsPtrs& w,
@@ -785,10 +811,20 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
     uint32_t* flag_count = reinterpret_cast<uint32_t*>(w.scal + kFlagWord);
     uint32_t* cflag_count = reinterpret_cast<uint32_t*>(w.scal + kCFlagWord);
     launch_zero_words(w.scal, kScalWords, s);
-    if (P == 0) {  // no probed list: every row is padding
+    if (P == 0) {  // no probed list: every row is padding (the queries are still checked)
+        for (size_t q0 = 0; q0 < nq; q0 += chunk)
+            launch_normalize(d_q + q0 * d, w.qn, w.qnorm, (int)std::min(chunk, nq - q0), (int)d, s,
+                             nullptr, reinterpret_cast<unsigned int*>(w.scal + kBadWord));
         launch_finalize(nullptr, nullptr, nullptr, (int)nq, 0, (int)k, d_ids, d_dists, s);
         VGPU_HIP(hipGetLastError());
+        if (!ws) {
+            complete_noalloc(w, s);
+            return;
+        }
+        VGPU_HIP(hipMemcpyAsync(ws->h_scal, w.scal, kScalWords * sizeof(unsigned long long),
+                                hipMemcpyDeviceToHost, s));
         VGPU_HIP(hipStreamSynchronize(s));
+        check_nonfinite(ws->h_scal[kBadWord]);
         return;
     }
     float t[7] = {0, 0, 0, 0, 0, 0, 0};
@@ -812,7 +848,8 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
         if (allp) VGPU_HIP(hipEventRecord(ev[1], s));
         const uint32_t* probe = w.probe;
         if (d_given) {
-            launch_normalize(d_q + q0 * d, w.qn, w.qnorm, (int)nc, (int)d, s);
+            launch_normalize(d_q + q0 * d, w.qn, w.qnorm, (int)nc, (int)d, s, w.qbad,
+                             reinterpret_cast<unsigned int*>(w.scal + kBadWord));
             if (allp) VGPU_HIP(hipEventRecord(ev[2], s));
             probe = d_given + q0 * P;
         } else {
@@ -877,7 +914,7 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
         }
         if (allp) VGPU_HIP(hipEventRecord(ev[6], s));
         launch_finish(vout, dout, d_doc_ids.p, (int)nc, (int)kin, (int)k, d_ids + q0 * k, d_dists + q0 * k,
-                      w.qstat, counters, flag_count, cflag_count, s);
+                      w.qstat, counters, flag_count, cflag_count, s, w.qbad);
         if (allp) VGPU_HIP(hipEventRecord(ev[7], s));
         VGPU_HIP(hipGetLastError());
         if (allp) {
@@ -890,12 +927,13 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
         }
     }
     if (!ws) {
-        VGPU_HIP(hipStreamSynchronize(s));
+        complete_noalloc(w, s);
         return;
     }
     unsigned long long* h_scal = ws->h_scal;
     VGPU_HIP(hipMemcpyAsync(h_scal, w.scal, kScalWords * sizeof(unsigned long long), hipMemcpyDeviceToHost, s));
     VGPU_HIP(hipStreamSynchronize(s));
+    check_nonfinite(h_scal[kBadWord]);
     if (scanp) {  // the scan kernels of every chunk, read after the final wait
         for (size_t c = 0; c < ci; c++) {
             float ms;

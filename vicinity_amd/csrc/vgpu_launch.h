@@ -86,7 +86,10 @@ __device__ __forceinline__ void scan_emit(const ScanArgs& a, int q, int j, uint6
     }
 }
 
-void launch_normalize(const float* x, float* out, float* norms, int n, int d, hipStream_t s);
+// qbad / nbad (optional): per-row non-finite marks and their count; such a
+// row is normalised as the zero vector.
+void launch_normalize(const float* x, float* out, float* norms, int n, int d, hipStream_t s,
+                      uint32_t* qbad = nullptr, unsigned int* nbad = nullptr);
 void launch_coarse_dots(const float* Q, const float* C, float* D, int nq, int L, int d,
                         hipStream_t s);
 // Probe selection with exact rescoring: probe[q*P..] = the P lists of smallest
@@ -112,10 +115,11 @@ size_t coarse_bf16_pack_chunks(int L, int d);
 void launch_coarse_bf16_pack(const float* C, int L, int d, uint4* Cb, hipStream_t s);
 // Normalise the raw queries Q (or use them as given, normalize = 0) into qn /
 // qnorm, and write each query's candidate lists: cand[q][coarse_fused_cap(P)],
-// cand_n[q] (a count above the cap means overflow).
+// cand_n[q] (a count above the cap means overflow).  qbad / nbad as for
+// launch_normalize.
 void launch_coarse_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int P,
                          int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
-                         hipStream_t s);
+                         hipStream_t s, uint32_t* qbad = nullptr, unsigned int* nbad = nullptr);
 // probe[q][0..P) from the candidates by exact score; overflowed queries are
 // appended to flag_list (*flag_count must be 0 on entry).
 void launch_coarse_topp(const uint32_t* cand, const uint32_t* cand_n, int P, const float* qn,
@@ -160,11 +164,12 @@ void launch_scan8_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hip
 #define COUNTER_STRIDE 8
 // Chunk epilogue: doc-id mapping and padding of (vidx, dist)[nq][kin] into
 // (out_ids, out_dists)[nq][k]; counters += the qstat rows (qstat may be null);
-// *flag_count = *cflag_count = 0 (either may be null).
+// *flag_count = *cflag_count = 0 (either may be null).  Rows q with
+// qbad[q] != 0 (a non-finite query; qbad may be null) become padding.
 void launch_finish(const uint32_t* vidx, const float* dist, const uint32_t* doc_ids, int nq, int kin,
                    int k, int64_t* out_ids, float* out_dists, const uint32_t* qstat,
                    unsigned long long* counters, uint32_t* flag_count, uint32_t* cflag_count,
-                   hipStream_t s);
+                   hipStream_t s, const uint32_t* qbad = nullptr);
 size_t fastscan_lds_bytes(const DevIndex& ix, const ScanArgs& a);
 void launch_fastscan(const DevIndex& ix, const ScanArgs& a, hipStream_t s);
 

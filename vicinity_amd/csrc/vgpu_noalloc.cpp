@@ -16,7 +16,15 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 uint8_t* g_scratch_ptr[kMaxDevices] = {};
+// Serialises the synchronous calls that share one device's array.
+std::mutex g_call_mu[kMaxDevices];
 }  // namespace
+
+std::mutex& noalloc_call_mutex(int device) {
+    if (device < 0 || device >= kMaxDevices)
+        throw Error(VGPU_ERR_DEVICE, "device ordinal " + std::to_string(device) + " out of range");
+    return g_call_mu[device];
+}
 
 uint8_t* noalloc_scratch(int device) {
     if (device < 0 || device >= kMaxDevices)

@@ -92,17 +92,20 @@ struct WsPtrs {
           *rres = nullptr;
     uint32_t *cand = nullptr, *cand_n = nullptr, *cflag_list = nullptr, *probe = nullptr,
              *vidx = nullptr, *vidx2 = nullptr, *qstat = nullptr, *flag_list = nullptr;
+    uint32_t* qbad = nullptr;  // per chunk query: 1 when the query holds a NaN or an infinity
     float* fdots = nullptr;  // coarse fallback: dot-product rows of the first flagged queries
     unsigned long long* scal = nullptr;  // per-call scalars (counters, flag-list lengths)
 };
 
 // Per-call device scalars: counter i at word i * COUNTER_STRIDE, then the
-// overflow count and the two flag-list lengths, each on a cache line of its own.
+// overflow count and the two flag-list lengths, each on a cache line of its own,
+// the coarse fallback's slice counters and the count of non-finite queries.
 constexpr size_t kOverflowWord = (NUM_SCAN_COUNTERS + 1) * COUNTER_STRIDE;
 constexpr size_t kFlagWord = kOverflowWord + 8;
 constexpr size_t kCFlagWord = kFlagWord + 8;
 constexpr size_t kFDoneWord = kCFlagWord + 8;  // COARSE_FLAG_PAR uint32 slice counters
-constexpr size_t kScalWords = kFDoneWord + COARSE_FLAG_PAR / 2;
+constexpr size_t kBadWord = kFDoneWord + (COARSE_FLAG_PAR / 2 + 7) / 8 * 8;  // non-finite queries
+constexpr size_t kScalWords = kBadWord + 8;
 
 // Workspace of one search call.  A handle keeps a pool of these: each call
 // borrows one for its whole duration, so concurrent searches on one handle
@@ -334,6 +337,9 @@ struct FileIvfpq {
 // The scratch array's device address on `device`, which must be current;
 // looked up once per device (hipGetSymbolAddress) and kept.
 uint8_t* noalloc_scratch(int device);
+// Held across a whole allocation-free call on `device`, so calls from several
+// threads (on any handles) take turns with the device's one array.
+std::mutex& noalloc_call_mutex(int device);
 
 // Host-side seeded sampling shared with the build (splitmix64 partial
 // Fisher-Yates, ascending sample).
