@@ -205,6 +205,7 @@ def run_ivfpq(args, w):
     ms_step = dt * 1e3 / args.steps
     qps = nq * args.steps / dt
     scan_ms = float(np.mean([s["ms_scan"] for s in stats]))
+    table_ms = float(np.mean([s["ms_table"] for s in stats]))
     scan_bytes = float(np.mean([s["scan_bytes"] for s in stats]))
     cands = float(np.mean([s["candidates"] for s in stats]))
     achieved = scan_bytes / (scan_ms * 1e-3) / 1e9
@@ -215,8 +216,8 @@ def run_ivfpq(args, w):
         pstats.append(ix.last_stats())
     ix.set_profiling(0)
     phases = {key: round(float(np.mean([s[key] for s in pstats])), 4)
-              for key in ("ms_normalize", "ms_coarse", "ms_select", "ms_scan", "ms_fallback",
-                          "ms_rerank", "ms_total")}
+              for key in ("ms_normalize", "ms_coarse", "ms_select", "ms_table", "ms_scan",
+                          "ms_fallback", "ms_rerank", "ms_total")}
     fallbacks = int(max(s["fallback_queries"] for s in stats))
     scan_diag = {"flushes_per_query": round(stats[-1]["fast_flushes"] / nq, 3),
                  "appends_per_query": round(stats[-1]["fast_appends"] / nq, 1),
@@ -253,7 +254,10 @@ def run_ivfpq(args, w):
     elif exact:
         kernel, kname = f"scan8_exact_kernel<{M},{K}>", "scan8_exact"
     else:
-        kernel, kname = f"scan8_fast_kernel<{M},{K},{d // M},1>", "scan8_fast"
+        # 16 codebooks on transposed blocks read their tables from the MFMA
+        # pre-pass (t2_table_kernel): the scan's fifth template argument is 1
+        pre = ",1" if M == 16 and K == 256 and d // M in (2, 4, 8) else ""
+        kernel, kname = f"scan8_fast_kernel<{M},{K},{d // M},1{pre}>", "scan8_fast"
     wl = w.name + ("_opq" if args.opq else "")
     config = {"workload": wl, "n": w.base.shape[0], "d": d, "nlist": p["num_clusters"],
               "M": M, "ksub": K, "nprobe": nprobe, "k": k, "rerank_pool": pool, "batch": nq,
@@ -267,6 +271,7 @@ def run_ivfpq(args, w):
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None if exact or args.n else traffic_from_profile(f"{kname}_{w.name}"),
                      "kernel": kernel, "kernel_ms": round(scan_ms, 4),
+                     "table_prepass_ms": round(table_ms, 4),
                      "algorithmic_bytes_per_launch": int(scan_bytes),
                      "candidates_per_launch": int(cands)},
         "recall_at_k": recall,

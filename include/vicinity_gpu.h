@@ -78,6 +78,7 @@ typedef struct vgpu_search_stats {
     uint64_t fast_appends;     /* FAST: entries that passed the running threshold */
     uint32_t fallback_ties;    /* FAST fallbacks caused by more equal distances than the buffer holds */
     uint32_t fast_retries;     /* FAST queries that needed a second pass over their lists */
+    float ms_table;            /* FAST: the per-query table pre-pass (not part of ms_scan) */
 } vgpu_search_stats;
 
 typedef struct vgpu_ivfpq vgpu_ivfpq;

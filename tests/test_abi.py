@@ -70,8 +70,10 @@ def test_struct_layouts_match_header():
 
     assert ctypes.sizeof(_lib.Params) == 5 * 8 + 8
     assert ctypes.sizeof(_lib.Info) == 7 * 8 + 3 * 4 + 4
-    # 7 floats, pad, 2 u64, 3 u32, pad, 2 u64 (flushes, appends), 2 u32
-    assert ctypes.sizeof(_lib.Stats) == 7 * 4 + 4 + 2 * 8 + 3 * 4 + 4 + 2 * 8 + 4 + 4
+    # 7 floats, pad, 2 u64, 3 u32, pad, 2 u64 (flushes, appends), 2 u32,
+    # ms_table, tail pad
+    assert ctypes.sizeof(_lib.Stats) == 7 * 4 + 4 + 2 * 8 + 3 * 4 + 4 + 2 * 8 + 4 + 4 + 4 + 4
+    assert _lib.Stats.ms_table.offset == 88
 
 
 def test_datagen_shapes_and_determinism():

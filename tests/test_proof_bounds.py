@@ -157,18 +157,44 @@ def _fast_case(rng, kind, d=32, M=8, K=32, n=400):
             rng.integers(0, K, size=(n, M)).astype(np.uint8), d, M, K, ds)
 
 
-def _fast_a(q, c, cb, codes, d, M, ds, order):
+def _round_toward_zero(s):
+    """float64 sums rounded to float32 toward zero (a truncating adder)."""
+    r = np.asarray(s).astype(F32)
+    too_big = np.abs(r.astype(np.float64)) > np.abs(s)
+    return np.where(too_big, np.nextafter(r, F32(0)), r).astype(F32)
+
+
+def _t2_table(q, cb, M, ds, table):
+    """T2[m][k] = -2 q_m . cw_mk as the kernels form it.  'fma': the scan's
+    own build, -2 times an fma chain over the dimensions.  The pre-pass
+    (t2_table_kernel): fp32 MFMA on (-2 q) and cw, exact products summed in
+    float32 with sums that may truncate, either after every product
+    ('mfma_seq') or once per step of four dimensions ('mfma_step')."""
+    qm = q.reshape(M, ds)
+    if table == "fma":
+        t2 = np.zeros(cb.shape[:2], F32)
+        for j in range(ds):
+            t2 = fma(qm[:, None, j], cb[:, :, j], t2)
+        return (F32(-2.0) * t2).astype(F32)
+    prods = (F32(-2.0) * qm).astype(np.float64)[:, None, :] * cb.astype(np.float64)  # exact in float64
+    acc = np.zeros(cb.shape[:2], F32)
+    if table == "mfma_seq":
+        for j in range(ds):
+            acc = _round_toward_zero(acc.astype(np.float64) + prods[..., j])
+    else:
+        for j0 in range(0, ds, 4):
+            acc = _round_toward_zero(acc.astype(np.float64) + prods[..., j0:j0 + 4].sum(-1))
+    return acc
+
+
+def _fast_a(q, c, cb, codes, d, M, ds, order, table="fma"):
     """The FAST kernel's ranking value for each entry (codes [n, M])."""
     diff = (q - c).astype(F32)
     acc = np.zeros(8, F32)  # term0: eight lanes, fma over j = lane mod 8, then a tree
     for j in range(d):
         acc[j % 8] = fma(diff[j], diff[j], acc[j % 8])
     term0 = tree_sum(acc, axis=0)
-    # T2[m][k] = -2 fma-dot(q_m, cw_mk)
-    t2 = np.zeros(cb.shape[:2], F32)
-    for j in range(ds):
-        t2 = fma(q.reshape(M, ds)[:, None, j], cb[:, :, j], t2)
-    t2 = (F32(-2.0) * t2).astype(F32)
+    t2 = _t2_table(q, cb, M, ds, table)
     # b(x) = sum_m (||cw||^2 + 2 c_m . cw), no FMA (bias_kernel)
     cw = cb[np.arange(M)[None, :], codes]  # [n, M, ds]
     e1 = np.zeros(codes.shape, F32)
@@ -185,18 +211,19 @@ def _fast_a(q, c, cb, codes, d, M, ds, order):
     return (term0 + (b + S).astype(F32)).astype(F32), term0
 
 
+@pytest.mark.parametrize("table", ["fma", "mfma_seq", "mfma_step"])
 @pytest.mark.parametrize("kind", ["gaussian", "large_centroid", "tiny_residual", "mantissa"])
-def test_fast_ranking_value_within_fast_tau(oracle, kind):
+def test_fast_ranking_value_within_fast_tau(oracle, kind, table):
     rng = np.random.default_rng({"gaussian": 1, "large_centroid": 2, "tiny_residual": 3,
                                  "mantissa": 4}[kind])
     worst = 0.0
-    for _ in range(3):
-        q, c, cb, codes, d, M, K, ds = _fast_case(rng, kind)
+    for ds_case in (4, 8):
+        q, c, cb, codes, d, M, K, ds = _fast_case(rng, kind, M=32 // ds_case)
         r = (q - c).astype(F32)
         e = oracle.adc_scan(codes, M, K, oracle.adc_table(cb.reshape(-1), M, K, ds, r))
         rmax = F32(np.sqrt(np.sum(np.max(np.sum(cb.astype(np.float64) ** 2, -1), -1))) * 1.0001 + 1e-30)
         for order in ("tree", "seq"):
-            a, term0 = _fast_a(q, c, cb, codes, d, M, ds, order)
+            a, term0 = _fast_a(q, c, cb, codes, d, M, ds, order, table)
             tau = fast_tau(d, M, ds, bound_norm(q), bound_norm(c), rmax, float(term0))
             err = np.abs(a.astype(np.float64) - e.astype(np.float64)).max()
             assert err <= tau, (kind, order, err, tau)

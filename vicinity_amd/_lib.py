@@ -12,7 +12,10 @@ import os
 
 import numpy as np
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvicinity_gpu.so")
+# VGPU_LIB: another build of the library (for example an instrumented one) in
+# place of the in-tree libvicinity_gpu.so.
+LIB_PATH = os.environ.get("VGPU_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                      "libvicinity_gpu.so")
 
 # status codes (src/error.rs:17-80)
 OK = 0
@@ -70,7 +73,8 @@ class Stats(ctypes.Structure):
                 ("scan_bytes", ctypes.c_uint64), ("fallback_queries", ctypes.c_uint32),
                 ("coarse_overflow", ctypes.c_uint32), ("nq", ctypes.c_uint32),
                 ("fast_flushes", ctypes.c_uint64), ("fast_appends", ctypes.c_uint64),
-                ("fallback_ties", ctypes.c_uint32), ("fast_retries", ctypes.c_uint32)]
+                ("fallback_ties", ctypes.c_uint32), ("fast_retries", ctypes.c_uint32),
+                ("ms_table", ctypes.c_float)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}

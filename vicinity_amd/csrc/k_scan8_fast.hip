@@ -198,6 +198,30 @@ __device__ inline FastLds fs8_carve(char* smem, float* static_lut, int d, int M,
     return s;
 }
 
+// Packed key labels (transposed blocks, P <= 64, fewer than 2^26 padded
+// entries per query): the low key word is t | slot << 26, so the probe slot
+// and the list position follow without a search over the prefix sums.
+#define FS_LBL_BITS 26
+#define FS_LBL_MASK ((1u << FS_LBL_BITS) - 1u)
+
+// A key (distance, label) as (probe slot << 32) | list position.  Packed
+// labels carry the slot; otherwise the largest slot p < P with pref[p] <= t
+// is the non-empty list holding t.
+__device__ __forceinline__ uint64_t fs8_relabel(const FastLds& s, uint64_t v, int P, bool packed) {
+    const uint32_t lo32 = (uint32_t)v;
+    if (packed) {
+        const uint32_t p = lo32 >> FS_LBL_BITS;
+        return ((uint64_t)p << 32) | (s.bt[p].x + (lo32 & FS_LBL_MASK));  // bt.x = lbeg - pref
+    }
+    uint32_t lo = 0, hi = (uint32_t)P;
+    while (hi - lo > 1u) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (s.pref[mid] <= lo32) lo = mid;
+        else hi = mid;
+    }
+    return ((uint64_t)lo << 32) | (s.lbeg[lo] + (lo32 - s.pref[lo]));
+}
+
 // Keep the keys key_at(0 .. n) whose high word is <= T, written densely to
 // keys[0 ..) chunk by chunk: a chunk is read into registers before any slot
 // is rewritten, and the compacted prefix never passes the slot of a key not
@@ -207,7 +231,7 @@ __device__ inline FastLds fs8_carve(char* smem, float* static_lut, int d, int M,
 // search over the list prefix sums.
 template <typename KeyAt>
 __device__ inline uint32_t fs8_compact(FastLds& s, KeyAt key_at, uint32_t n, uint32_t T, bool relabel,
-                                       int P) {
+                                       int P, bool packed) {
     const int tid = threadIdx.x;
     __syncthreads();
     if (tid == 0) s.misc[0] = 0;
@@ -217,17 +241,7 @@ __device__ inline uint32_t fs8_compact(FastLds& s, KeyAt key_at, uint32_t n, uin
         uint64_t v = i < n ? key_at(i) : ~0ull;
         bool take = i < n && (uint32_t)(v >> 32) <= T;
         __syncthreads();
-        if (take && relabel) {
-            // the largest slot p < P with pref[p] <= t is the non-empty list holding t
-            const uint32_t t = (uint32_t)v;
-            uint32_t lo = 0, hi = (uint32_t)P;
-            while (hi - lo > 1u) {
-                const uint32_t mid = (lo + hi) >> 1;
-                if (s.pref[mid] <= t) lo = mid;
-                else hi = mid;
-            }
-            v = ((uint64_t)lo << 32) | (s.lbeg[lo] + (t - s.pref[lo]));
-        }
+        if (take && relabel) v = fs8_relabel(s, v, P, packed);
         int slot = wave_append_slot(take, &s.misc[0]);
         if (take) s.keys[slot] = v;
         __syncthreads();
@@ -340,19 +354,25 @@ __device__ __forceinline__ uint4 readlane4(const uint4& v, int lane) {
 // (usually none or one) is read out and the lanes at or past it switch to its
 // record.  Otherwise the wave keeps a cursor cw over the LDS prefix sums
 // (windows only move forward) and counts the starts inside the window.
+// *slot (when given) receives the slot index.
 __device__ __forceinline__ uint4 slot_record(const FastLds& s, const SlotRegs& r, int P, uint32_t wb,
-                                             uint32_t x, int& cw) {
+                                             uint32_t x, int& cw, uint32_t* slot = nullptr) {
     if (P <= 64) {
         const int c = (int)__popcll(__ballot(r.pref <= wb)) - 1;
         uint4 e = readlane4(r.bt, c);
+        uint32_t sl = (uint32_t)c;
         uint64_t inwin = __ballot(r.pref > wb && r.pref < wb + 64u);
         while (inwin) {
             const int p = (int)__builtin_ctzll(inwin);
             inwin &= inwin - 1;
             const uint32_t b = __builtin_amdgcn_readlane(r.pref, p);
             const uint4 f = readlane4(r.bt, p);
-            if (x >= b) e = f;
+            if (x >= b) {
+                e = f;
+                sl = (uint32_t)p;
+            }
         }
+        if (slot) *slot = sl;
         return e;
     }
     while (cw + 1 < P && __builtin_amdgcn_readfirstlane(s.pref[cw + 1]) <= wb) cw++;
@@ -362,8 +382,10 @@ __device__ __forceinline__ uint4 slot_record(const FastLds& s, const SlotRegs& r
         if (b >= wb + 64u) break;
         lst += x >= b ? 1 : 0;
     }
+    if (slot) *slot = (uint32_t)lst;
     return s.bt[lst];
 }
+
 
 // Entry t = rbase + wave * 64 + lane: the waves take interleaved windows of
 // 64 consecutive entries.
@@ -401,7 +423,7 @@ __device__ __forceinline__ void fs8_fetch(const DevIndex& ix, const FastLds& s, 
 template <int MT>
 __device__ __forceinline__ void fs8t_fetch(__amdgpu_buffer_rsrc_t trs, const FastLds& s, const SlotRegs& sr,
                                            uint32_t rbase, uint32_t lc_code, uint32_t lc_bias, int P,
-                                           int& cw, RoundRegs<MT>& g) {
+                                           int& cw, RoundRegs<MT>& g, bool packed) {
     static_assert(FS_U == 1 && MT % 16 == 0, "one window per wave and round");
     const uint32_t lane = threadIdx.x & 63u, m = lane & 15u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -411,6 +433,7 @@ __device__ __forceinline__ void fs8t_fetch(__amdgpu_buffer_rsrc_t trs, const Fas
     const uint32_t wofs = (uint32_t)(MT + 4) * wb;
     uint32_t base;  // block byte offset of the lane's row, less (MT + 4) tb
     float t0;
+    uint32_t slot = 0;
     bool uniform = false;
     if (P <= 64) {
         // Usually one list covers the whole window (no list starts inside it
@@ -424,10 +447,11 @@ __device__ __forceinline__ void fs8t_fetch(__amdgpu_buffer_rsrc_t trs, const Fas
             uniform = true;
             base = ez + wofs;
             t0 = __uint_as_float(ey);
+            slot = (uint32_t)c;
         }
     }
     if (!uniform) {
-        const uint4 e = slot_record(s, sr, P, wb, tb, cw);
+        const uint4 e = slot_record(s, sr, P, wb, tb, cw, &slot);
         base = e.z + wofs;
         t0 = t < e.w ? __uint_as_float(e.y) : __builtin_nanf("");
     }
@@ -442,7 +466,7 @@ __device__ __forceinline__ void fs8t_fetch(__amdgpu_buffer_rsrc_t trs, const Fas
     }
     g.bias[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(trs, base + lc_bias, 0u, 0));
     g.t0[0] = t0;
-    g.t[0] = t;
+    g.t[0] = packed ? t | slot << FS_LBL_BITS : t;
 }
 
 // a + DPP-moved b (row-local patterns, every source lane active, so no lane
@@ -841,10 +865,13 @@ __device__ __forceinline__ float fs8_pair_distance(const DevIndex& ix, const flo
     return total_e;
 }
 
-template <int MT, int KT, int DS, int NC>
+// PRE: the per-query table T2 was written by t2_table_kernel (a.t2) and is
+// copied into LDS instead of being built here.
+template <int MT, int KT, int DS, int NC, int PRE>
 __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArgs a, int buf) {
     constexpr bool TR = NC > 0;
     static_assert(!TR || (MT % 16 == 0 && KT == 256 && DS > 0), "transposed blocks");
+    static_assert(!PRE || (TR && NC == 1), "precomputed tables: transposed layout, one copy");
     constexpr bool kStatic = MT > 0 && KT >= 64;
     constexpr int D = MT * DS;  // compile-time dimension when > 0
     constexpr int LUTF = kStatic ? MT * KT * (TR ? NC : 1) : 1;  // static table floats
@@ -880,7 +907,60 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
         if constexpr (TR) s.tbo[p] = rt;
     };
     if (tid < 32) s.misc[tid] = tid == 8 ? 0xffffffffu : 0u;  // counts 0, no bound yet
-    if constexpr (TR) {
+    // PRE: eight lanes per probed slot (the first PG slots) hold the residual
+    // r = q - c of their slot (dimensions 32 i + 4 sub .. + 3, the reference's
+    // single subtraction) from the prologue to the rescoring, which stages it
+    // in LDS without loading the centroids again.
+    constexpr int PG = VGPU_BLOCK / 8;
+    float4 rres[PRE ? D / 32 : 1];
+    if constexpr (PRE) {
+        // Two round trips.  First: the query's table (LUTF floats, coalesced
+        // 16-byte pieces), the query, the thread's probed slot and the slot of
+        // its eight-lane group.  Second: the slot's list record and the group
+        // slot's centroid slices, from which ||q - c||^2 and r follow.
+        constexpr int TPT = LUTF / 4 / VGPU_BLOCK;  // 16-byte pieces per thread
+        static_assert(LUTF % (4 * VGPU_BLOCK) == 0 && D % 32 == 0 && D / 4 <= VGPU_BLOCK, "table copy split");
+        const float4* src = reinterpret_cast<const float4*>(a.t2 + (size_t)q * LUTF);
+        float4 tv[TPT];
+#pragma unroll
+        for (int i = 0; i < TPT; i++) tv[i] = src[i * VGPU_BLOCK + tid];
+        const int g = tid >> 3, sub = tid & 7;
+        const uint32_t gid = g < P ? a.probe[(size_t)q * P + g] : 0u;
+        const float4* qrow = reinterpret_cast<const float4*>(a.qn + (size_t)q * D);
+        float4 qsl[D / 32];
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) qsl[i] = qrow[8 * i + sub];
+        // the table is stored before the second round trip is issued (that
+        // round trip waits on the probed ids anyway), which frees its registers
+        float4* dst = reinterpret_cast<float4*>(slut);
+#pragma unroll
+        for (int i = 0; i < TPT; i++) dst[i * VGPU_BLOCK + tid] = tv[i];
+        if (tid < P) rec_load(l0id);
+        const bool gok = g < P && gid < (uint32_t)ix.L;  // no such list: scanned as empty
+        const float4* crow = reinterpret_cast<const float4*>(ix.centroids + (size_t)(gok ? gid : 0u) * D);
+        float4 cv[D / 32];
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) cv[i] = crow[8 * i + sub];
+        if (g == 0) {  // the query itself: group 0's lanes hold every dimension once
+#pragma unroll
+            for (int i = 0; i < D / 32; i++) reinterpret_cast<float4*>(s.qs)[8 * i + sub] = qsl[i];
+        }
+        if (tid < P) rec_store(tid);
+        float acc = 0.0f;  // ||q - c||^2, ranking only: any order, FMA allowed
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) {
+            rres[i] = make_float4(__fsub_rn(qsl[i].x, cv[i].x), __fsub_rn(qsl[i].y, cv[i].y),
+                                  __fsub_rn(qsl[i].z, cv[i].z), __fsub_rn(qsl[i].w, cv[i].w));
+            acc = __builtin_fmaf(rres[i].x, rres[i].x, acc);
+            acc = __builtin_fmaf(rres[i].y, rres[i].y, acc);
+            acc = __builtin_fmaf(rres[i].z, rres[i].z, acc);
+            acc = __builtin_fmaf(rres[i].w, rres[i].w, acc);
+        }
+        acc += __uint_as_float(shfl_xor_u32(__float_as_uint(acc), 1));
+        acc += __uint_as_float(shfl_xor_u32(__float_as_uint(acc), 2));
+        acc += __uint_as_float(shfl_xor_u32(__float_as_uint(acc), 4));
+        if (g < P && sub == 0) s.term0[g] = gok ? acc : 0.0f;
+    } else if constexpr (TR) {
         // T2[m][k] = -2 q_m . cw_mk (ranking only: FMA allowed), built before
         // the first barrier from the query in global memory.  Every load
         // instruction reads one whole 64-byte line of each of 16 codebooks:
@@ -1022,7 +1102,7 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
     }
     {  // ||q - c||^2: eight lanes per probed list (ranking only: any order)
         const int g = tid >> 3, sub = tid & 7;
-        for (int p0 = 0; p0 < P; p0 += VGPU_BLOCK / 8) {
+        for (int p0 = PRE ? PG : 0; p0 < P; p0 += VGPU_BLOCK / 8) {
             const int p = p0 + g;
             float acc = 0.0f;
             if (p < P) {
@@ -1129,8 +1209,9 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
         lc_code = (uint32_t)(MT + 4) * ((uint32_t)lane & 48u) + ((uint32_t)lane & 15u) * 16u;
         lc_bias = (uint32_t)(MT + 4) * ((uint32_t)lane & 48u) + 16u * MT + ((uint32_t)lane & 15u) * 4u;
     }
+    const bool packed = TR && P <= 64 && total < (1u << FS_LBL_BITS);  // wave-uniform
     auto fetch = [&](uint32_t rb, RoundRegs<MT>& g) {
-        if constexpr (TR) fs8t_fetch<MT>(trs, s, sr, rb, lc_code, lc_bias, P, cur, g);
+        if constexpr (TR) fs8t_fetch<MT>(trs, s, sr, rb, lc_code, lc_bias, P, cur, g, packed);
         else fs8_fetch<MT>(ix, s, sr, rb, total, P, cur, g);
     };
     if (total > 0) {
@@ -1270,8 +1351,15 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
     // dimensions 4 (t % (D / 4)) .. + 3 of slots t / (D / 4), + SPT, ...: the
     // slot ids are read first and every centroid load is in flight at once
     // (a store to the table region could otherwise hold back the next id read).
+    if constexpr (PRE) {
+        if (P <= PG && (tid >> 3) < P) {  // the residuals held since the prologue
+            float* o = s.lut + (tid >> 3) * D + 4 * (tid & 7);
+#pragma unroll
+            for (int i = 0; i < D / 32; i++) *reinterpret_cast<float4*>(o + 32 * i) = rres[i];
+        }
+    }
     if constexpr ((MT == 8 || MT == 16 || MT == 32) && KT > 0 && DS > 0) {
-        if ((size_t)P * D <= (size_t)LUTF) {
+        if ((size_t)P * D <= (size_t)LUTF && (!PRE || P > PG)) {
             constexpr int SPT = VGPU_BLOCK / (D / 4);         // slots per pass
             constexpr int SMAX = (LUTF / D + SPT - 1) / SPT;  // passes for P D <= LUTF
             static_assert(VGPU_BLOCK % (D / 4) == 0, "staging split");
@@ -1297,7 +1385,92 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
             }
         }
     }
-    n = fs8_compact(s, key_at, n, bk, true, P);  // R, keys relabelled (probe slot, position)
+    // Regions in place and residuals staged: each wave keeps the keys of its
+    // own region that belong to R, relabelled, at the front of its region
+    // (no block barrier; an odd count is followed by a key above every other,
+    // for the pairwise reads of the ordering).  R is then rescored where it
+    // lies, two threads per entry with the exact distance below, and ordered
+    // across the regions without merging them.
+    if constexpr ((MT == 8 || MT == 16 || MT == 32) && KT > 0 && DS > 0) {
+        if ((size_t)P * D <= (size_t)LUTF && !merged) {
+            const uint32_t cntw = cnts[wave];
+            uint32_t kept = 0;
+            for (uint32_t i0 = 0; i0 < cntw; i0 += 64) {  // chunk read before any slot of it is rewritten
+                const uint32_t idx = i0 + (uint32_t)lane;
+                uint64_t v = idx < cntw ? reg[idx] : ~0ull;
+                const bool take = idx < cntw && (uint32_t)(v >> 32) <= bk;
+                const uint64_t mask = __ballot(take);
+                if (take) {
+                    v = fs8_relabel(s, v, P, packed);
+                    reg[kept + __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u))] = v;
+                }
+                kept += (uint32_t)__popcll(mask);
+            }
+            if (lane == 0) {
+                s.misc[16 + wave] = kept;
+                if (kept & 1u) reg[kept] = ~0ull;  // kept < capw < BW
+            }
+            __syncthreads();  // residuals staged, R final in every region
+            uint32_t ro[VGPU_BLOCK / 64 + 1];
+            ro[0] = 0;
+#pragma unroll
+            for (int w = 0; w < VGPU_BLOCK / 64; w++) ro[w + 1] = ro[w] + s.misc[16 + w];
+            n = ro[VGPU_BLOCK / 64];
+            for (uint32_t c0 = 0; c0 < n; c0 += VGPU_BLOCK / 2) {
+                const uint32_t i = c0 + ((uint32_t)tid >> 1), half = (uint32_t)tid & 1u;
+                const bool act = i < n;
+                const uint32_t at = act ? region_slot(i, ro, BW) : 0u;
+                const uint64_t v = act ? s.keys[at] : 0ull;
+                const uint32_t vid = act && half == 0 ? ix.list_ids[(uint32_t)v] : 0u;
+                CodeRow<MT> row;  // both lanes of the pair hold the whole row (entry 0 when inactive)
+                load_row<MT>(row, ix.codes + (size_t)(uint32_t)v * MT);
+                const float total_e =
+                    fs8_pair_distance<MT, KT, DS, MT <= 16 ? 4 : 2>(ix, s.lut, (uint32_t)(v >> 32), row, half);
+                if (act && half == 0) s.keys[at] = cand_key(total_e, vid);  // its own slot: no other reads it
+            }
+            __syncthreads();
+            if (n <= (uint32_t)VGPU_BLOCK) {
+                // Each thread takes one key and writes it at its rank, the number
+                // of smaller keys over the regions (distinct keys: one per
+                // vector); its doc id load flies during the count.
+                if ((uint32_t)tid < n) {
+                    const uint64_t ki = s.keys[region_slot((uint32_t)tid, ro, BW)];
+                    const uint32_t vi = (uint32_t)ki;
+                    const uint32_t doc = a.out_ids && a.doc_ids ? a.doc_ids[vi] : vi;
+                    uint32_t r = 0;
+#pragma unroll
+                    for (int w = 0; w < VGPU_BLOCK / 64; w++) {
+                        const uint64_t* rk = s.keys + (uint32_t)w * BW;
+                        const uint32_t cw2 = ro[w + 1] - ro[w];
+#pragma unroll 4
+                        for (uint32_t jj = 0; jj < cw2; jj += 2) {
+                            const ulonglong2 kj = *reinterpret_cast<const ulonglong2*>(rk + jj);
+                            r += (kj.x < ki ? 1u : 0u) + (kj.y < ki ? 1u : 0u);
+                        }
+                    }
+                    if (r < (uint32_t)kout) {
+                        const size_t o = (size_t)q * kout + r;
+                        if (a.out_ids) {
+                            a.out_ids[o] = (int64_t)doc;
+                            a.out_dists[o] = key_dist(ki);
+                        } else {
+                            a.out_vidx[o] = vi;
+                            a.out_dist[o] = key_dist(ki);
+                        }
+                    }
+                }
+                for (int j = (int)n + tid; j < kout; j += VGPU_BLOCK) scan_emit(a, q, j, ~0ull, false);  // padding
+                return;
+            }
+            uint32_t kc[VGPU_BLOCK / 64];
+#pragma unroll
+            for (int w = 0; w < VGPU_BLOCK / 64; w++) kc[w] = ro[w + 1] - ro[w];
+            n = fs8w_merge(s, kc, BW);
+            goto rescored;
+        }
+    }
+    n = fs8_compact(s, key_at, n, bk, true, P, packed);  // R, keys relabelled (probe slot, position)
 
     // Two threads per entry (codebooks 0 .. M/2 - 1 and M/2 .. M - 1) when the
     // probed lists' residuals r = q - c fit the idle table region (built
@@ -1407,6 +1580,111 @@ rescored:
     for (int j = tid; j < kout; j += VGPU_BLOCK) scan_emit(a, q, j, s.keys[j], (uint32_t)j < n);
 }
 
+// ---- per-query tables for a chunk of queries -----------------------------
+// T2[q][(16 gi + r) codebook, c codeword] = -2 q_m . cw_mc (m = 16 gi + r)
+// at float ((gi * 256 + c) * 16 + r) of query q's M * 256 floats: the layout
+// of the FAST scan's LDS table (transposed blocks, one copy).  Ranking only,
+// like the table the scan builds itself: the dot products are fp32 MFMA
+// (v_mfma_f32_16x16x4_f32, products of fp32 operands summed in fp32), within
+// 2 ds u sum_j |q_j cw_j| of the real ones even if the sums truncate, which
+// the error bound fast_tau covers.  One workgroup per (16 queries, 16
+// codewords of a 16-codebook group).  The queries' slices of the group and
+// the tile's codewords (16 ds floats per row, contiguous in both arrays) are
+// staged in LDS with coalesced 16-byte loads, one dimension step padded to 4
+// per codebook; wave w then computes codebooks 4 w .. 4 w + 3 (A = the query
+// values scaled by -2, exact; B = the codewords).  The 16 x 16 x 16 results
+// are staged in LDS and stored with each instruction covering 4 KB of
+// consecutive bytes (one kilobyte per query).  Loading the operands straight
+// from global memory, four bytes per lane, took 2.4x as long.
+template <int DS>
+__global__ __launch_bounds__(256) void t2_table_kernel(const float* __restrict__ qn, int nq, int M,
+                                                       const float* __restrict__ cb, float* __restrict__ t2) {
+    typedef float floatx4 __attribute__((ext_vector_type(4)));
+    constexpr int KS = (DS + 3) / 4;  // MFMA steps of 4 dimensions
+    constexpr int DP = KS * 4;        // padded dimensions per codebook
+    constexpr int RS = 16 * DP + 4;   // LDS row stride (+4: the 16 rows of an operand read in distinct banks)
+    constexpr int RF = 16 * DS / 4;   // 16-byte pieces per operand row
+    static_assert(DS % 2 == 0, "16-byte pieces within one codebook");
+    __shared__ __align__(16) float stage[16 * 256];  // [query][codeword][codebook r]
+    __shared__ __align__(16) float sa[16 * RS];      // [query][codebook * DP + k]
+    __shared__ __align__(16) float sb[16 * RS];      // [codeword][codebook * DP + k]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tiles = (M / 16) * 16;
+    const int qb = blockIdx.x / tiles, gt = blockIdx.x % tiles, gi = gt >> 4, ct = gt & 15;
+    const int q0 = qb * 16;
+    const int i = lane & 15, kq = lane >> 4;  // A row / B column i, dimension 4 step + kq
+    const int rows = min(16, nq - q0);
+    const int d = M * DS;
+    if (DP != DS)
+        for (int f = tid; f < 16 * RS; f += VGPU_BLOCK) sa[f] = sb[f] = 0.0f;  // the padded dimensions
+    __syncthreads();
+    for (int f = tid; f < 16 * RF; f += VGPU_BLOCK) {
+        const int r = f / RF, c4 = f % RF, m = 4 * c4 / DS, k = 4 * c4 % DS;
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < rows) x = reinterpret_cast<const float4*>(qn + (size_t)(q0 + r) * d + (size_t)gi * 16 * DS)[c4];
+        const float4 y = reinterpret_cast<const float4*>(cb + ((size_t)(16 * gi + r) * 256 + 16 * ct) * DS)[c4];
+        const int cw = 4 * c4 / DS;  // B: row r is codebook 16 gi + r, piece c4 is codeword cw, dims k..
+        if constexpr (DS == 2) {     // a piece spans two codebooks (A) or two codewords (B)
+            sa[r * RS + m * DP] = x.x;
+            sa[r * RS + m * DP + 1] = x.y;
+            sa[r * RS + (m + 1) * DP] = x.z;
+            sa[r * RS + (m + 1) * DP + 1] = x.w;
+            sb[cw * RS + r * DP] = y.x;
+            sb[cw * RS + r * DP + 1] = y.y;
+            sb[(cw + 1) * RS + r * DP] = y.z;
+            sb[(cw + 1) * RS + r * DP + 1] = y.w;
+        } else {
+            *reinterpret_cast<float4*>(sa + r * RS + m * DP + k) = x;
+            *reinterpret_cast<float4*>(sb + cw * RS + r * DP + (4 * c4 % DS)) = y;
+        }
+    }
+    __syncthreads();
+    floatx4 acc[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int m = 4 * wave + r;
+        acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < KS; st++)
+            acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(-2.0f * sa[i * RS + m * DP + 4 * st + kq],
+                                                          sb[i * RS + m * DP + 4 * st + kq], acc[r], 0, 0, 0);
+    }
+    // acc[r][e]: query 4 kq + e, codeword 16 ct + i, codebook 16 gi + 4 wave + r
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        *reinterpret_cast<float4*>(stage + ((4 * kq + e) * 16 + i) * 16 + 4 * wave) =
+            make_float4(acc[0][e], acc[1][e], acc[2][e], acc[3][e]);
+    __syncthreads();
+    const size_t per_q = (size_t)M * 256;
+    const float4* src = reinterpret_cast<const float4*>(stage);
+#pragma unroll
+    for (int v = 0; v < 4; v++) {  // piece f of the tile: query f / 64, its 16 bytes f % 64
+        const int f = v * VGPU_BLOCK + tid, qq = f >> 6;
+        if (qq < rows)
+            reinterpret_cast<float4*>(t2 + (size_t)(q0 + qq) * per_q + (size_t)(gi * 256 + 16 * ct) * 16)[f & 63] =
+                src[f];
+    }
+}
+
+bool scan8_fast_uses_tables(const DevIndex& ix) {
+    return ix.tblocks && ix.K == 256 && ix.M == 16 && (ix.ds == 2 || ix.ds == 4 || ix.ds == 8);
+}
+
+void launch_t2_tables(const DevIndex& ix, const float* qn, int nq, float* t2, hipStream_t s, hipEvent_t t0,
+                      hipEvent_t t1) {
+    if (nq <= 0) return;
+    const dim3 grid((unsigned)((size_t)((nq + 15) / 16) * (size_t)(ix.M / 16) * 16)), block(VGPU_BLOCK);
+    auto go = [&](auto k) {
+        if (t0) hipExtLaunchKernelGGL(k, grid, block, 0, s, t0, t1, 0u, qn, nq, ix.M, ix.codebooks, t2);
+        else hipLaunchKernelGGL(k, grid, block, 0, s, qn, nq, ix.M, ix.codebooks, t2);
+    };
+    switch (ix.ds) {
+        case 2: go(t2_table_kernel<2>); return;
+        case 4: go(t2_table_kernel<4>); return;
+        default: go(t2_table_kernel<8>); return;
+    }
+}
+
 bool scan8_fast_blocks_supported(int M, int K, int ds) {
     return K == 256 && (M == 16 || M == 32 || M == 48) && (ds == 2 || ds == 4 || ds == 8);
 }
@@ -1435,13 +1713,13 @@ size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
     return st + fs8_layout(ix.d, ix.M, ix.K, a.P, fs8_buf(a.kk), st != 0, off);
 }
 
-template <int MT, int KT, int DS, int NC>
+template <int MT, int KT, int DS, int NC, int PRE = 0>
 static void launch_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hipEvent_t t0,
                         hipEvent_t t1) {
     const int buf = fs8_buf(a.kk);
     size_t off[12];
     const size_t dyn = fs8_layout(ix.d, ix.M, ix.K, a.P, buf, MT > 0 && KT >= 64, off);
-    auto k = scan8_fast_kernel<MT, KT, DS, NC>;
+    auto k = scan8_fast_kernel<MT, KT, DS, NC, PRE>;
     ensure_dyn_lds((const void*)k, dyn);
     if (t0)
         hipExtLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), (uint32_t)dyn, s, t0, t1, 0u, ix, a, buf);
@@ -1454,6 +1732,8 @@ template <int MT, int DS>
 static void launch_fast_ds(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hipEvent_t t0,
                            hipEvent_t t1) {
     if constexpr (MT == 16 || MT == 32 || MT == 48) {
+        if constexpr (MT == 16)
+            if (table_copies(ix) == 1 && a.t2) return launch_fast<MT, 256, DS, 1, 1>(ix, a, s, t0, t1);
         if (table_copies(ix) == 1) return launch_fast<MT, 256, DS, 1>(ix, a, s, t0, t1);
         return launch_fast<MT, 256, 0, 0>(ix, a, s, t0, t1);  // blocks missing: row layout
     } else {

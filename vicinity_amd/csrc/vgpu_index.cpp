@@ -610,12 +610,14 @@ static int fast_keep(size_t kout) {
 SearchWs::SearchWs() {
     // non-blocking: no implicit wait on the null stream (default priority)
     VGPU_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+
     for (auto& e : ev) VGPU_HIP(hipEventCreate(&e));
     VGPU_HIP(hipHostMalloc((void**)&h_scal, kScalWords * sizeof(unsigned long long)));
 }
 
 SearchWs::~SearchWs() {
     if (stream) (void)hipStreamSynchronize(stream);
+
     if (h_scal) (void)hipHostFree(h_scal);
     for (auto& e : ev)
         if (e) (void)hipEventDestroy(e);
@@ -702,8 +704,11 @@ SearchPlan IvfpqIndex::plan_search(size_t nq, size_t k, size_t nprobe, size_t po
     }
     pl.opq = !rotation.empty();
     pl.fused = coarse_fused_supported((int)d, (int)pl.P);
+    pl.t2 = pl.P && K != 16 && mode == VGPU_MODE_FAST && !pl.opq && !pl.wide && scan8_fast_uses_tables(dix);
     size_t chunk = std::max<size_t>(1, std::min<size_t>(nq, ((size_t)1 << 28) / std::max<size_t>(L, 1)));
     chunk = std::min<size_t>(chunk, 65536);
+    if (pl.t2)  // tables of a chunk within 256 MiB
+        chunk = std::max<size_t>(1, std::min<size_t>(chunk, ((size_t)1 << 26) / ((size_t)M * K)));
     if (pl.opq && pl.P)
         chunk = std::max<size_t>(1, std::min<size_t>(chunk, ((size_t)1 << 28) / (pl.P * d)));
     pl.chunk = chunk;
@@ -742,6 +747,7 @@ size_t IvfpqIndex::ws_layout(const SearchPlan& pl, uint8_t* base, WsPtrs* out) c
     carve(w.qstat, c * QSTAT_WORDS);
     carve(w.flag_list, c);
     if (pl.opq) carve(w.rres, c * pl.P * d);
+    if (pl.t2) carve(w.t2, c * M * K);
     if (out) *out = w;
     return (off + 255) & ~(size_t)255;
 }
@@ -827,11 +833,11 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
         check_nonfinite(ws->h_scal[kBadWord]);
         return;
     }
-    float t[7] = {0, 0, 0, 0, 0, 0, 0};
+    float t[7] = {0, 0, 0, 0, 0, 0, 0}, t_table = 0;
     const int prof = ws ? profiling : 0;
     const bool allp = prof == 1, scanp = prof == 2;
     if (scanp) {
-        const size_t need_ev = 2 * ((nq + chunk - 1) / chunk);
+        const size_t need_ev = 4 * ((nq + chunk - 1) / chunk);
         while (ws->sev.size() < need_ev) {
             hipEvent_t e;
             VGPU_HIP(hipEventCreate(&e));
@@ -862,7 +868,7 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
         // scan-only timing: the FAST kernel's dispatch records the two events
         // itself; the other scan kernels are bracketed by marker events
         const bool scan_fast = K != 16 && mode == VGPU_MODE_FAST && !pl.opq && !pl.wide;
-        if (scanp && !scan_fast) VGPU_HIP(hipEventRecord(ws->sev[2 * ci], s));
+        if (scanp && !scan_fast) VGPU_HIP(hipEventRecord(ws->sev[4 * ci], s));
         ScanArgs a;
         a.qn = w.qn;
         a.qnorm = w.qnorm;
@@ -885,11 +891,17 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
             a.kk = (int)kout;
             launch_fastscan(dix, a, s);
             if (allp) VGPU_HIP(hipEventRecord(ev[4], s));
-            if (scanp) VGPU_HIP(hipEventRecord(ws->sev[2 * ci + 1], s));
+            if (scanp) VGPU_HIP(hipEventRecord(ws->sev[4 * ci + 1], s));
         } else if (scan_fast) {
             a.kk = fast_keep(kout);
             a.exact = 0;
-            launch_scan8_fast(dix, a, s, scanp ? ws->sev[2 * ci] : nullptr, scanp ? ws->sev[2 * ci + 1] : nullptr);
+            if (pl.t2) {  // the per-query tables (ms_table)
+                launch_t2_tables(dix, w.qn, (int)nc, w.t2, s, scanp ? ws->sev[4 * ci + 2] : nullptr,
+                                 scanp ? ws->sev[4 * ci + 3] : nullptr);
+                if (allp) VGPU_HIP(hipEventRecord(ev[8], s));
+                a.t2 = w.t2;
+            }
+            launch_scan8_fast(dix, a, s, scanp ? ws->sev[4 * ci] : nullptr, scanp ? ws->sev[4 * ci + 1] : nullptr);
             if (allp) VGPU_HIP(hipEventRecord(ev[4], s));
             a.kk = (int)kout;
             a.exact = 1;
@@ -900,7 +912,7 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
             a.exact = 1;
             launch_scan8_exact(dix, a, s);
             if (allp) VGPU_HIP(hipEventRecord(ev[4], s));
-            if (scanp) VGPU_HIP(hipEventRecord(ws->sev[2 * ci + 1], s));
+            if (scanp) VGPU_HIP(hipEventRecord(ws->sev[4 * ci + 1], s));
         }
         if (allp) VGPU_HIP(hipEventRecord(ev[5], s));
         const uint32_t* vout = nullptr;  // rows already final
@@ -924,6 +936,11 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
                 VGPU_HIP(hipEventElapsedTime(&ms, ev[i], ev[i + 1]));
                 t[i] += ms;
             }
+            if (pl.t2) {  // the scan phase less the table pre-pass
+                VGPU_HIP(hipEventElapsedTime(&ms, ev[3], ev[8]));
+                t[3] -= ms;
+                t_table += ms;
+            }
         }
     }
     if (!ws) {
@@ -937,8 +954,12 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
     if (scanp) {  // the scan kernels of every chunk, read after the final wait
         for (size_t c = 0; c < ci; c++) {
             float ms;
-            VGPU_HIP(hipEventElapsedTime(&ms, ws->sev[2 * c], ws->sev[2 * c + 1]));
+            VGPU_HIP(hipEventElapsedTime(&ms, ws->sev[4 * c], ws->sev[4 * c + 1]));
             t[3] += ms;
+            if (pl.t2) {
+                VGPU_HIP(hipEventElapsedTime(&ms, ws->sev[4 * c + 2], ws->sev[4 * c + 3]));
+                t_table += ms;
+            }
         }
     }
     unsigned long long cnt[NUM_SCAN_COUNTERS];
@@ -951,7 +972,8 @@ void IvfpqIndex::run_search(const float* d_q, size_t nq, const SearchPlan& pl, c
     st->ms_scan = t[3];
     st->ms_fallback = t[4];
     st->ms_rerank = t[5];
-    st->ms_total = t[0] + t[1] + t[2] + t[3] + t[4] + t[5] + t[6];
+    st->ms_table = t_table;
+    st->ms_total = t[0] + t[1] + t[2] + t[3] + t[4] + t[5] + t[6] + t_table;
     st->candidates = cnt[0];
     st->fallback_queries = (uint32_t)cnt[1];
     st->fast_flushes = cnt[2];

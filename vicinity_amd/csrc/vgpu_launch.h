@@ -68,6 +68,10 @@ struct ScanArgs {
     // null: the residual q - c (Quantizer::Product).  EXACT, filtered and
     // FastScan kernels only.
     const float* rres = nullptr;
+    // FAST scan with 16 codebooks on transposed blocks: the per-query tables
+    // written by launch_t2_tables ([nq][M * 256], the scan's LDS layout);
+    // null: the scan builds each query's table itself.
+    const float* t2 = nullptr;
 };
 
 // Writes result j of query q from a (distance, insertion index) key, or
@@ -221,6 +225,13 @@ void launch_bias(const DevIndex& ix, float* bias, hipStream_t s);
 #define TBLK_BYTES(M) (16 * (size_t)(M) + 64)
 // Whether the FAST scan reads transposed blocks for this shape.
 bool scan8_fast_blocks_supported(int M, int K, int ds);
+// The FAST scan shapes whose per-query tables come from launch_t2_tables
+// (16 codebooks of 256 codewords on transposed blocks, ds 2, 4 or 8).
+bool scan8_fast_uses_tables(const DevIndex& ix);
+// T2 = -2 q.cw of nq normalised queries into t2[nq][M * 256] (fp32 MFMA);
+// t0 / t1 (optional) are recorded around the kernel.
+void launch_t2_tables(const DevIndex& ix, const float* qn, int nq, float* t2, hipStream_t s,
+                      hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
 // Fill ix.tblocks from ix.codes, ix.bias and ix.tblk_off.
 void launch_tblocks(const DevIndex& ix, uint8_t* tblocks, hipStream_t s);
 void launch_pack4(const DevIndex& ix, uint8_t* packed, hipStream_t s);

@@ -79,6 +79,7 @@ struct SearchPlan {
     size_t pool = 0;   // rerank pool (0: no rerank)
     size_t chunk = 0;  // queries per launch sequence
     bool fused = false, opq = false;
+    bool t2 = false;   // FAST scan tables from the MFMA pre-pass (chunk * M * 256 floats)
     // nprobe above 1024 or kout above 2048: probes chosen from exact scores of
     // every list, scans in EXACT (or FastScan) mode with per-slot list reads
     bool wide = false;
@@ -89,7 +90,7 @@ struct SearchPlan {
 // allocation-free entry point.
 struct WsPtrs {
     float *qn = nullptr, *qnorm = nullptr, *dots = nullptr, *dist = nullptr, *dist2 = nullptr,
-          *rres = nullptr;
+          *rres = nullptr, *t2 = nullptr;
     uint32_t *cand = nullptr, *cand_n = nullptr, *cflag_list = nullptr, *probe = nullptr,
              *vidx = nullptr, *vidx2 = nullptr, *qstat = nullptr, *flag_list = nullptr;
     uint32_t* qbad = nullptr;  // per chunk query: 1 when the query holds a NaN or an infinity
@@ -113,8 +114,8 @@ constexpr size_t kScalWords = kBadWord + 8;
 // streams.  The arena grows to the largest plan seen and is reused.
 struct SearchWs {
     hipStream_t stream = nullptr;
-    hipEvent_t ev[8] = {};
-    std::vector<hipEvent_t> sev;  // scan-only timing: two per chunk
+    hipEvent_t ev[9] = {};
+    std::vector<hipEvent_t> sev;  // scan-only timing: four per chunk (scan kernel, table pre-pass)
     DevBuf<uint8_t> arena;
     DevBuf<float> q, odist;       // host-buffer entry points: staged queries and distances
     DevBuf<int64_t> ids;          // host-buffer entry points: staged ids
