@@ -108,34 +108,36 @@ void launch_bias(const DevIndex& ix, float* bias, hipStream_t s) {
     hipLaunchKernelGGL(bias_kernel, dim3((ix.n + 255) / 256), dim3(256), 0, s, ix, bias);
 }
 
-// One workgroup per list, one thread per 4-byte word of the list's blocks.
-__global__ void tblocks_kernel(DevIndex ix, uint8_t* __restrict__ out) {
+// One workgroup per list, one thread per 4-byte word of the list's lane
+// records: M bytes of codes per record (codebooks m, m + 16, ...: byte j is
+// the code of entry j ^ m), then one b(x) per record.
+__global__ void tblocks_kernel(DevIndex ix, uint8_t* __restrict__ tcodes, float* __restrict__ tbias) {
     const int l = blockIdx.x;
     const uint32_t beg = ix.offsets[l], len = ix.offsets[l + 1] - beg;
     const uint32_t b0 = ix.tblk_off[l], nb = ix.tblk_off[l + 1] - b0;
-    const uint32_t M = (uint32_t)ix.M, blk = (uint32_t)TBLK_BYTES(M), cb = 16u * M;
-    uint32_t* o = reinterpret_cast<uint32_t*>(out + (size_t)b0 * blk);
-    for (uint32_t w = threadIdx.x; w < nb * blk / 4u; w += blockDim.x) {
-        const uint32_t b = w / (blk / 4u), within = (w % (blk / 4u)) * 4u;
+    const uint32_t M = (uint32_t)ix.M;
+    uint32_t* o = reinterpret_cast<uint32_t*>(tcodes + (size_t)b0 * 16u * M);
+    for (uint32_t w = threadIdx.x; w < nb * 4u * M; w += blockDim.x) {
+        const uint32_t rec = w / (M / 4u), r = (w % (M / 4u)) * 4u;  // lane record, byte within
+        const uint32_t b = rec / 16u, mm = rec % 16u;
+        const uint32_t m = (r / 16u) * 16u + mm;  // codebook
         uint32_t word = 0u;
-        if (within < cb) {
-            const uint32_t m = within / 16u;
-            for (uint32_t i = 0; i < 4u; i++) {
-                const uint32_t j = within % 16u + i, e = b * 16u + (j ^ (m & 15u));
-                const uint32_t c = e < len ? ix.codes[(size_t)(beg + e) * M + m] : 0u;
-                word |= c << (8u * i);
-            }
-        } else {
-            const uint32_t e = b * 16u + (within - cb) / 4u;
-            word = e < len ? __float_as_uint(ix.bias[beg + e]) : 0u;
+        for (uint32_t i = 0; i < 4u; i++) {
+            const uint32_t j = r % 16u + i, e = b * 16u + (j ^ mm);
+            const uint32_t c = e < len ? ix.codes[(size_t)(beg + e) * M + m] : 0u;
+            word |= c << (8u * i);
         }
         o[w] = word;
     }
+    // padding entries get a NaN b(x): their approximate distance is NaN,
+    // which no filter takes
+    for (uint32_t e = threadIdx.x; e < nb * 16u; e += blockDim.x)
+        tbias[(size_t)b0 * 16u + e] = e < len ? ix.bias[beg + e] : __int_as_float(0x7fc00000);
 }
 
-void launch_tblocks(const DevIndex& ix, uint8_t* tblocks, hipStream_t s) {
+void launch_tblocks(const DevIndex& ix, uint8_t* tcodes, float* tbias, hipStream_t s) {
     if (ix.L <= 0) return;
-    hipLaunchKernelGGL(tblocks_kernel, dim3(ix.L), dim3(256), 0, s, ix, tblocks);
+    hipLaunchKernelGGL(tblocks_kernel, dim3(ix.L), dim3(256), 0, s, ix, tcodes, tbias);
 }
 
 // One workgroup per list; lists shorter than 16 entries have no blocks

@@ -34,7 +34,7 @@
 // query that still cannot be proved is flagged and rerun by the EXACT kernel.
 //
 // Layouts.  With codebook_size 256 and 16, 32 or 48 codebooks the lists are
-// read from transposed 16-entry blocks (see DevIndex::tblocks), the table is
+// read from transposed 16-entry blocks (see DevIndex::tcodes), the table is
 // stored code-major so that the 16 lanes of a row read 16 different banks,
 // and a row's 16 lanes exchange partial sums; otherwise one lane scores one
 // list-major code row.
@@ -126,8 +126,9 @@ struct FastLds {
     uint32_t* pref;  // [P + 1]
     float* term0;    // [P] ||q - c||^2
     // [P] per probed slot, one read per entry: x = lbeg - pref (u32), y = bits
-    // of term0; transposed blocks: z = 16 * first block - pref (u32),
-    // w = pref + llen (end of the slot's entries)
+    // of term0; transposed blocks: z = (M + 4) (16 * first block - pref) (u32),
+    // w = pref + llen (end of the slot's entries).  In LDS only when P > 64;
+    // otherwise lane p holds slot p's record (SlotRegs).
     uint4* bt;
     uint32_t* tbo;   // [P] first transposed block of each probed list
     RadixScratch* rs;
@@ -150,7 +151,7 @@ __host__ __device__ inline int fs8_buf(int keep) {
 // Dynamic LDS layout; the table region is omitted when the kernel holds the
 // table in a static array (static_lut: compile-time M and K = 256).
 __host__ __device__ inline size_t fs8_layout(int d, int M, int K, int P, int buf, bool static_lut,
-                                             size_t* off) {
+                                             size_t* off, bool static_rs = false) {
     size_t o = 0;
     const int KL = K > 64 ? K : 64;
     off[0] = o; o = static_lut ? 0 : fs8_align(o + (size_t)M * KL * 4);  // lut
@@ -158,9 +159,9 @@ __host__ __device__ inline size_t fs8_layout(int d, int M, int K, int P, int buf
     off[3] = o; o = fs8_align(o + (size_t)P * 4);          // lid
     off[4] = o; o = fs8_align(o + (size_t)P * 4);          // lbeg
     off[6] = o; o = fs8_align(o + (size_t)(P + 1) * 4);    // pref
-    off[8] = o; o = fs8_align(o + sizeof(RadixScratch));   // radix scratch
+    off[8] = o; o = static_rs ? o : fs8_align(o + sizeof(RadixScratch));   // radix scratch
     off[9] = o; o = fs8_align(o + 32 * 4);                 // misc
-    off[10] = o; o = fs8_align(o + (size_t)P * 16);        // bt
+    off[10] = o; o = fs8_align(o + (P > 64 ? (size_t)P * 16 : 0));  // bt (P <= 64: in registers)
     // qs, llen, term0 and tbo are read only before the scan: they share the
     // key buffer when they fit in it
     const size_t pa = fs8_align((size_t)P * 4), qa = fs8_align((size_t)d * 4);
@@ -179,9 +180,9 @@ __host__ __device__ inline size_t fs8_layout(int d, int M, int K, int P, int buf
 }
 
 __device__ inline FastLds fs8_carve(char* smem, float* static_lut, int d, int M, int K, int P,
-                                    int buf) {
+                                    int buf, RadixScratch* static_rs = nullptr) {
     size_t off[12];
-    fs8_layout(d, M, K, P, buf, static_lut != nullptr, off);
+    fs8_layout(d, M, K, P, buf, static_lut != nullptr, off, static_rs != nullptr);
     FastLds s;
     s.lut = static_lut ? static_lut : (float*)(smem + off[0]);
     s.keys = (uint64_t*)(smem + off[1]);
@@ -191,7 +192,7 @@ __device__ inline FastLds fs8_carve(char* smem, float* static_lut, int d, int M,
     s.llen = (uint32_t*)(smem + off[5]);
     s.pref = (uint32_t*)(smem + off[6]);
     s.term0 = (float*)(smem + off[7]);
-    s.rs = (RadixScratch*)(smem + off[8]);
+    s.rs = static_rs ? static_rs : (RadixScratch*)(smem + off[8]);
     s.misc = (uint32_t*)(smem + off[9]);
     s.bt = (uint4*)(smem + off[10]);
     s.tbo = (uint32_t*)(smem + off[11]);
@@ -204,6 +205,28 @@ __device__ inline FastLds fs8_carve(char* smem, float* static_lut, int d, int M,
 #define FS_LBL_BITS 26
 #define FS_LBL_MASK ((1u << FS_LBL_BITS) - 1u)
 
+// Block map of the main pass (16 codebooks, transposed blocks, P < 64):
+// slot4[b] = 4 x the probe slot of padded block b of the query's
+// concatenated lists, vb16[p] = 16 x (the first transposed block of slot p
+// less its first padded block), t0[p] = ||q - c||^2 of slot p.  Slot P is a
+// sentinel (vb16 0, t0 NaN) for the blocks past the last list, up to the
+// last round the main pass reads.  A lane then finds its entry's lane record
+// in the transposed blocks and its list term with three LDS reads and one
+// add.  The map shares its LDS with
+// the radix scratch of the proof, which runs after the main pass; a query
+// whose blocks do not fit takes the slot search instead.
+#define FS_MAP_BLOCKS 960
+struct FsMap {
+    uint32_t vb16[65];  // first (the union sits at LDS address 0): vb16 and t0 of a
+    float t0[65];       // slot are one paired read at 8-bit dword offsets
+    uint8_t slot4[FS_MAP_BLOCKS];
+};
+union FsAux {
+    RadixScratch rs;
+    FsMap map;
+};
+__host__ __device__ constexpr bool fs8_has_map(int MT, int NC) { return NC == 1 && MT == 16; }
+
 // A key (distance, label) as (probe slot << 32) | list position.  Packed
 // labels carry the slot; otherwise the largest slot p < P with pref[p] <= t
 // is the non-empty list holding t.
@@ -211,7 +234,7 @@ __device__ __forceinline__ uint64_t fs8_relabel(const FastLds& s, uint64_t v, in
     const uint32_t lo32 = (uint32_t)v;
     if (packed) {
         const uint32_t p = lo32 >> FS_LBL_BITS;
-        return ((uint64_t)p << 32) | (s.bt[p].x + (lo32 & FS_LBL_MASK));  // bt.x = lbeg - pref
+        return ((uint64_t)p << 32) | (s.lbeg[p] - s.pref[p] + (lo32 & FS_LBL_MASK));
     }
     uint32_t lo = 0, hi = (uint32_t)P;
     while (hi - lo > 1u) {
@@ -411,27 +434,51 @@ __device__ __forceinline__ void fs8_fetch(const DevIndex& ix, const FastLds& s, 
     }
 }
 
+// Structured buffer loads (index x stride + offset, range-checked by index,
+// zeros past the last record): the LLVM intrinsics, which have no clang
+// builtin.
+__device__ u32x4 fs8_sload4(__amdgpu_buffer_rsrc_t rsrc, uint32_t vindex, uint32_t voffset, uint32_t soffset,
+                            int aux) __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
+__device__ uint32_t fs8_sload1(__amdgpu_buffer_rsrc_t rsrc, uint32_t vindex, uint32_t voffset, uint32_t soffset,
+                               int aux) __asm("llvm.amdgcn.struct.ptr.buffer.load.i32");
+
+// The codes and b(x) of lane record `vi` of the transposed blocks: `rsc`
+// addresses tcodes in records of MT bytes, `rsb` tbias in records of one
+// float, so both loads take the one index register and no offset.
+template <int MT>
+__device__ __forceinline__ void fs8t_load(__amdgpu_buffer_rsrc_t rsc, __amdgpu_buffer_rsrc_t rsb, uint32_t vi,
+                                          RoundRegs<MT>& g) {
+#pragma unroll
+    for (int gi = 0; gi < MT / 16; gi++) {
+        const u32x4 x = fs8_sload4(rsc, vi, 16u * gi, 0u, 0);
+        g.row[0].w[4 * gi] = x.x;
+        g.row[0].w[4 * gi + 1] = x.y;
+        g.row[0].w[4 * gi + 2] = x.z;
+        g.row[0].w[4 * gi + 3] = x.w;
+    }
+    g.bias[0] = __uint_as_float(fs8_sload1(rsb, vi, 0u, 0u, 0));
+}
+
 // Transposed blocks: the probed lists are concatenated in whole 16-entry
 // blocks (t runs over the padded sequence, pref holds padded starts).  A
-// wave's window of 64 entries is four blocks, one per row of 16 lanes; lane m
-// of a row loads the 16 codes of codebooks m, m + 16, ... of its block (code j
-// of entry j ^ m) and the b(x) of the block's entry m, which is the entry it
-// ends up scoring.  Raw buffer loads: the block's byte offset is the slot's
-// e.z plus (MT + 4) tb, split into the window's part `wofs` and the lane's
-// constants lc_code / lc_bias; rows past the end of the lists read zeros or
-// an unrelated block, and their entries are invalid (NaN term).
+// wave's window of 64 entries is four blocks, one per row of 16 lanes; lane
+// (row, m) loads lane record m of its row's block: the 16 codes of codebooks
+// m, m + 16, ... (code j of entry j ^ m) and the b(x) of the block's entry
+// m, which is the entry it ends up scoring.  The record index is the slot's
+// e.z = 16 x its first block - pref, plus t; rows past the end of the lists
+// read zeros or an unrelated record, and their entries are invalid (NaN
+// term).
 template <int MT>
-__device__ __forceinline__ void fs8t_fetch(__amdgpu_buffer_rsrc_t trs, const FastLds& s, const SlotRegs& sr,
-                                           uint32_t rbase, uint32_t lc_code, uint32_t lc_bias, int P,
-                                           int& cw, RoundRegs<MT>& g, bool packed) {
+__device__ __forceinline__ void fs8t_fetch(__amdgpu_buffer_rsrc_t rsc, __amdgpu_buffer_rsrc_t rsb, const FastLds& s,
+                                           const SlotRegs& sr, uint32_t rbase, int P, int& cw, RoundRegs<MT>& g,
+                                           bool packed) {
     static_assert(FS_U == 1 && MT % 16 == 0, "one window per wave and round");
     const uint32_t lane = threadIdx.x & 63u, m = lane & 15u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t wb = rbase + wave * 64u;  // window start
     const uint32_t tb = wb + (lane & 48u);   // the row's block start
     const uint32_t t = tb + m;
-    const uint32_t wofs = (uint32_t)(MT + 4) * wb;
-    uint32_t base;  // block byte offset of the lane's row, less (MT + 4) tb
+    uint32_t base;  // record index of the window's first entry (the lane adds its own)
     float t0;
     uint32_t slot = 0;
     bool uniform = false;
@@ -445,28 +492,59 @@ __device__ __forceinline__ void fs8t_fetch(__amdgpu_buffer_rsrc_t trs, const Fas
         const uint32_t ew = __builtin_amdgcn_readlane(sr.bt.w, c);
         if (lt == le && ew >= wb + 64u) {
             uniform = true;
-            base = ez + wofs;
+            base = ez + wb;
             t0 = __uint_as_float(ey);
             slot = (uint32_t)c;
         }
     }
     if (!uniform) {
         const uint4 e = slot_record(s, sr, P, wb, tb, cw, &slot);
-        base = e.z + wofs;
+        base = e.z + wb;
         t0 = t < e.w ? __uint_as_float(e.y) : __builtin_nanf("");
     }
-#pragma unroll
-    for (int gi = 0; gi < MT / 16; gi++) {
-        // the whole offset in the range-checked VGPR part (soffset is not checked)
-        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(trs, base + lc_code + (uint32_t)gi * 256u, 0u, 0);
-        g.row[0].w[4 * gi] = x.x;
-        g.row[0].w[4 * gi + 1] = x.y;
-        g.row[0].w[4 * gi + 2] = x.z;
-        g.row[0].w[4 * gi + 3] = x.w;
-    }
-    g.bias[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(trs, base + lc_bias, 0u, 0));
+    fs8t_load<MT>(rsc, rsb, base + lane, g);
     g.t0[0] = t0;
     g.t[0] = packed ? t | slot << FS_LBL_BITS : t;
+}
+
+// Main-pass fetch through the block map, in three stages one round apart so
+// that no stage waits on the LDS read of another: the map byte of round
+// f + 2, the record of round f + 1 from its map byte, and the loads of round
+// f from its record.  Lane (row, m) of the window at wb scores entry m of
+// padded block wb / 16 + row, whose lane record is 16 vb[slot] + wb + lane,
+// so the record index is one add.  A sentinel row reads record wb + lane (or
+// zeros past the end) and its NaN t0 keeps its entries out.  Labels are
+// packed.
+struct MapPipe {
+    uint32_t s4n;  // map byte of the round after next
+    uint32_t vi;   // next round: lane record, packed label, t0
+    uint32_t lbl;
+    float t0;
+};
+
+__device__ __forceinline__ uint32_t fs8m_byte(const FsMap& mp, uint32_t rbase) {
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t b0 = __builtin_amdgcn_readfirstlane((rbase + wave * 64u) >> 4);  // the window's first block
+    return mp.slot4[b0 + ((threadIdx.x & 63u) >> 4)];
+}
+
+__device__ __forceinline__ void fs8m_record(const FsMap& mp, uint32_t rbase, uint32_t s4, MapPipe& mpp) {
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t t = rbase + wave * 64u + (threadIdx.x & 63u);  // wb + lane
+    mpp.vi = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(mp.vb16) + s4) + t;
+    mpp.t0 = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(mp.t0) + s4);
+    mpp.lbl = t | (s4 << (FS_LBL_BITS - 2));
+}
+
+template <int MT>
+__device__ __forceinline__ void fs8m_fetch(__amdgpu_buffer_rsrc_t rsc, __amdgpu_buffer_rsrc_t rsb, const FsMap& mp,
+                                           uint32_t rbase, MapPipe& mpp, RoundRegs<MT>& g) {
+    static_assert(FS_U == 1 && MT % 16 == 0, "one window per wave and round");
+    fs8t_load<MT>(rsc, rsb, mpp.vi, g);
+    g.t0[0] = mpp.t0;
+    g.t[0] = mpp.lbl;
+    fs8m_record(mp, rbase + FS_ROUND, mpp.s4n, mpp);
+    mpp.s4n = fs8m_byte(mp, rbase + 2 * FS_ROUND);
 }
 
 // a + DPP-moved b (row-local patterns, every source lane active, so no lane
@@ -875,14 +953,19 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
     constexpr bool kStatic = MT > 0 && KT >= 64;
     constexpr int D = MT * DS;  // compile-time dimension when > 0
     constexpr int LUTF = kStatic ? MT * KT * (TR ? NC : 1) : 1;  // static table floats
-    __shared__ __align__(16) float slut[LUTF];
+    constexpr bool kMap = fs8_has_map(MT, NC);
+    // Static LDS: the block map / radix scratch (kMap) at address 0, then the table.
+    constexpr int AUXB = kMap ? (int)((sizeof(FsAux) + 15) & ~(size_t)15) : 0;
+    __shared__ __align__(16) char sstat[AUXB + LUTF * 4];
+    float* const slut = reinterpret_cast<float*>(sstat + AUXB);
     extern __shared__ __align__(16) char smem[];
     const int q = blockIdx.x;
     if (q >= a.nq) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int d = D > 0 ? D : ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K;
     const int ds = DS > 0 ? DS : ix.ds, P = a.P;
-    FastLds s = fs8_carve(smem, kStatic ? slut : nullptr, d, M, K, P, buf);
+    FsAux* aux = reinterpret_cast<FsAux*>(sstat);
+    FastLds s = fs8_carve(smem, kStatic ? slut : nullptr, d, M, K, P, buf, kMap ? &aux->rs : nullptr);
 
     // ---- prologue: query, probed lists, ||q - c||^2, the per-query table.
     // Round trip 1: the thread's first probed slot and (blocks) the query
@@ -1164,10 +1247,39 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
         }
     }
     __syncthreads();  // pref (wave 0) and term0 complete
-    for (int p = tid; p < P; p += VGPU_BLOCK)
-        s.bt[p] = make_uint4(s.lbeg[p] - s.pref[p], __float_as_uint(s.term0[p]),
-                             TR ? (uint32_t)(MT + 4) * (16u * s.tbo[p] - s.pref[p]) : 0u,
-                             s.pref[p] + s.llen[p]);
+    auto slot_rec = [&](int p) {
+        return make_uint4(s.lbeg[p] - s.pref[p], __float_as_uint(s.term0[p]),
+                          TR ? 16u * s.tbo[p] - s.pref[p] : 0u, s.pref[p] + s.llen[p]);
+    };
+    SlotRegs sr;  // P <= 64: lane p holds slot p's prefix sum and record
+    sr.pref = lane < P ? s.pref[lane] : 0xffffffffu;
+    sr.bt = lane < P ? slot_rec(lane) : make_uint4(0u, 0u, 0u, 0u);
+    if (P > 64)
+        for (int p = tid; p < P; p += VGPU_BLOCK) s.bt[p] = slot_rec(p);
+    // The main pass's block map, when the blocks it fetches fit (block-uniform).
+    bool use_map = false;
+    if constexpr (kMap) {
+        const uint32_t nb = s.pref[P] >> 4;               // padded blocks of the probed lists
+        const uint32_t cover = ((nb + 15u) & ~15u) + 80u;  // map bytes read up to five rounds past the last
+        use_map = P < 64 && cover <= (uint32_t)FS_MAP_BLOCKS;
+        if (use_map) {
+            FsMap& mp = aux->map;
+            const int g = tid >> 3, sub = tid & 7;
+            for (int p = g; p < P; p += VGPU_BLOCK / 8) {  // eight lanes per probed slot
+                const uint32_t b0 = s.pref[p] >> 4, b1 = s.pref[p + 1] >> 4;  // empty lists write nothing
+                for (uint32_t b = b0 + (uint32_t)sub; b < b1; b += 8u) mp.slot4[b] = (uint8_t)(4 * p);
+                if (sub == 0) {
+                    mp.vb16[p] = 16u * (s.tbo[p] - b0);
+                    mp.t0[p] = s.term0[p];
+                }
+            }
+            for (uint32_t b = nb + (uint32_t)tid; b < cover; b += VGPU_BLOCK) mp.slot4[b] = (uint8_t)(4 * P);
+            if (tid == 0) {
+                mp.vb16[P] = 0u;
+                mp.t0[P] = __builtin_nanf("");
+            }
+        }
+    }
     if (tid < 64) {  // max ||q - c||^2 for tau
         float t0max = 0.0f;
         for (int p = lane; p < P; p += 64) t0max = fmaxf(t0max, s.term0[p]);
@@ -1194,35 +1306,42 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
     const uint32_t wave = __builtin_amdgcn_readfirstlane((uint32_t)tid >> 6);
     uint64_t* reg = s.keys + wave * BW;
     const float tau = fast_tau(d, M, ds, a.qnorm[q], ix.cmax, ix.rmax, __uint_as_float(s.misc[9]));
-    SlotRegs sr;
-    sr.pref = lane < P ? s.pref[lane] : 0xffffffffu;
-    sr.bt = lane < P ? s.bt[lane] : make_uint4(0u, 0u, 0u, 0u);
     uint32_t cnt = 0, thr = 0xffffffffu, F = 0xffffffffu, Fused = 0xffffffffu, evicted = 0, flushes = 0;
     bool lost = false;
     int cur = 0;
     RoundRegs<MT> ga, gb, gc, gd;
-    // transposed blocks (unused by the row layout)
-    const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(ix.tblocks), (short)0, (int)ix.tblk_bytes, 0x00020000);
-    uint32_t lc_code = 0, lc_bias = 0;
-    if constexpr (TR) {
-        lc_code = (uint32_t)(MT + 4) * ((uint32_t)lane & 48u) + ((uint32_t)lane & 15u) * 16u;
-        lc_bias = (uint32_t)(MT + 4) * ((uint32_t)lane & 48u) + 16u * MT + ((uint32_t)lane & 15u) * 4u;
-    }
+    // transposed blocks as lane records (unused by the row layout)
+    const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(ix.tcodes), (short)(TR ? MT : 0), (int)(TR ? 16u * ix.tblk_count : 0u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(ix.tbias), (short)4, (int)(TR ? 16u * ix.tblk_count : 0u), 0x00020000);
     const bool packed = TR && P <= 64 && total < (1u << FS_LBL_BITS);  // wave-uniform
     auto fetch = [&](uint32_t rb, RoundRegs<MT>& g) {
-        if constexpr (TR) fs8t_fetch<MT>(trs, s, sr, rb, lc_code, lc_bias, P, cur, g, packed);
+        if constexpr (TR) fs8t_fetch<MT>(rsc, rsb, s, sr, rb, P, cur, g, packed);
         else fs8_fetch<MT>(ix, s, sr, rb, total, P, cur, g);
     };
+    MapPipe mpp{0u, 0u, 0u, 0.0f};
+    if (kMap && use_map) {  // the record of round 0 and the map byte of round 1
+        fs8m_record(aux->map, 0u, fs8m_byte(aux->map, 0u), mpp);
+        mpp.s4n = fs8m_byte(aux->map, FS_ROUND);
+    }
+    auto mfetch = [&](uint32_t rb, RoundRegs<MT>& g) {
+        if constexpr (kMap) fs8m_fetch<MT>(rsc, rsb, aux->map, rb, mpp, g);
+    };
+    // Whole groups of four rounds in the loop, which has no other exit (an
+    // exit inside would make the loads of its first round look outstanding
+    // at the loop head and drain the ring there), then the last 0 .. 3.
+    const uint32_t nr = (total + FS_ROUND - 1) / FS_ROUND;  // rounds
+    auto main_pass = [&](auto&& fetchf) {
     if (total > 0) {
-        fetch(0, ga);
-        fetch(FS_ROUND, gb);
-        fetch(2 * FS_ROUND, gc);
+        fetchf(0, ga);
+        fetchf(FS_ROUND, gb);
+        fetchf(2 * FS_ROUND, gc);
     }
 #define FS8_STEP(CONSUME, NEXT, R)                                                           \
     {                                                                                        \
         const uint32_t rbase = (R) * FS_ROUND;                                               \
-        fetch(rbase + 3 * FS_ROUND, NEXT);                                                   \
+        fetchf(rbase + 3 * FS_ROUND, NEXT);                                                  \
         const uint32_t shared = __atomic_load_n(&s.misc[8], __ATOMIC_RELAXED);               \
         Fused = F;                                                                           \
         fs8w_consume<MT, KT, NC>(ix, s, slut, CONSUME, filter_float(F), reg, cnt);           \
@@ -1240,10 +1359,6 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
             F = thr < sh ? thr : sh;                                                         \
         }                                                                                    \
     }
-    // Whole groups of four rounds in the loop, which has no other exit (an
-    // exit inside would make the loads of its first round look outstanding
-    // at the loop head and drain the ring there), then the last 0 .. 3.
-    const uint32_t nr = (total + FS_ROUND - 1) / FS_ROUND;  // rounds
     uint32_t r = 0;
     for (; r + 4 <= nr; r += 4) {
         FS8_STEP(ga, gd, r)
@@ -1259,6 +1374,9 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
         }
     }
 #undef FS8_STEP
+    };
+    if (kMap && use_map) main_pass(mfetch);
+    else main_pass(fetch);
     {
         const uint32_t G = Fused < thr ? Fused : thr;  // the wave's region holds its entries <= G
         if (lane == 0) {
@@ -1667,7 +1785,7 @@ __global__ __launch_bounds__(256) void t2_table_kernel(const float* __restrict__
 }
 
 bool scan8_fast_uses_tables(const DevIndex& ix) {
-    return ix.tblocks && ix.K == 256 && ix.M == 16 && (ix.ds == 2 || ix.ds == 4 || ix.ds == 8);
+    return ix.tcodes && ix.K == 256 && ix.M == 16 && (ix.ds == 2 || ix.ds == 4 || ix.ds == 8);
 }
 
 void launch_t2_tables(const DevIndex& ix, const float* qn, int nq, float* t2, hipStream_t s, hipEvent_t t0,
@@ -1693,7 +1811,7 @@ bool scan8_fast_blocks_supported(int M, int K, int ds) {
 // 16 codebooks two copies would let a half wave read 32 distinct banks, but
 // the doubled table costs more in occupancy than the conflicts it removes.
 static int table_copies(const DevIndex& ix) {
-    return ix.tblocks && scan8_fast_blocks_supported(ix.M, ix.K, ix.ds) ? 1 : 0;
+    return ix.tcodes && scan8_fast_blocks_supported(ix.M, ix.K, ix.ds) ? 1 : 0;
 }
 
 // Static table bytes of the specialisations (compile-time M, K = 256).
@@ -1710,7 +1828,9 @@ static size_t static_lut_bytes(const DevIndex& ix) {
 size_t scan8_fast_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
     size_t off[12];
     const size_t st = static_lut_bytes(ix);
-    return st + fs8_layout(ix.d, ix.M, ix.K, a.P, fs8_buf(a.kk), st != 0, off);
+    // the block map's static LDS (in place of the dynamic radix scratch)
+    const bool map = st != 0 && fs8_has_map(ix.M, table_copies(ix));
+    return st + (map ? (sizeof(FsAux) + 15) & ~(size_t)15 : 0) + fs8_layout(ix.d, ix.M, ix.K, a.P, fs8_buf(a.kk), st != 0, off, map);
 }
 
 template <int MT, int KT, int DS, int NC, int PRE = 0>
@@ -1718,7 +1838,7 @@ static void launch_fast(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hi
                         hipEvent_t t1) {
     const int buf = fs8_buf(a.kk);
     size_t off[12];
-    const size_t dyn = fs8_layout(ix.d, ix.M, ix.K, a.P, buf, MT > 0 && KT >= 64, off);
+    const size_t dyn = fs8_layout(ix.d, ix.M, ix.K, a.P, buf, MT > 0 && KT >= 64, off, fs8_has_map(MT, NC));
     auto k = scan8_fast_kernel<MT, KT, DS, NC, PRE>;
     ensure_dyn_lds((const void*)k, dyn);
     if (t0)

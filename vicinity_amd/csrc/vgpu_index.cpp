@@ -575,7 +575,8 @@ void IvfpqIndex::upload_index() {
         d_tblocks.release();
         d_tblk_off.release();
         dix.bias = nullptr;
-        dix.tblocks = nullptr;
+        dix.tcodes = nullptr;
+        dix.tbias = nullptr;
         dix.tblk_off = nullptr;
     } else {
         d_bias.reserve(n);
@@ -584,14 +585,16 @@ void IvfpqIndex::upload_index() {
         std::vector<uint32_t> toff(L + 1, 0);
         for (size_t l = 0; l < L; l++)
             toff[l + 1] = toff[l] + (uint32_t)((offsets[l + 1] - offsets[l] + 15) / 16);
-        const size_t tbytes = ((size_t)toff[L] + 1) * TBLK_BYTES(M);  // + one block of slack
-        if (scan8_fast_blocks_supported((int)M, (int)K, (int)ds) && tbytes < ((size_t)1 << 31)) {
+        const size_t nblk = (size_t)toff[L] + 1;  // + one block of slack
+        // lane records are indexed by 32-bit structured-buffer indices
+        if (scan8_fast_blocks_supported((int)M, (int)K, (int)ds) && nblk * 16 < ((size_t)1 << 31)) {
             d_tblk_off.upload(toff.data(), L + 1, stream);
-            d_tblocks.reserve(tbytes);
+            d_tblocks.reserve(nblk * TBLK_BYTES(M));  // codes, then the b(x) floats
             dix.tblk_off = d_tblk_off.p;
-            dix.tblocks = d_tblocks.p;
-            dix.tblk_bytes = (uint32_t)tbytes;
-            launch_tblocks(dix, d_tblocks.p, stream);
+            dix.tcodes = d_tblocks.p;
+            dix.tbias = reinterpret_cast<float*>(d_tblocks.p + nblk * 16 * M);
+            dix.tblk_count = (uint32_t)nblk;
+            launch_tblocks(dix, d_tblocks.p, const_cast<float*>(dix.tbias), stream);
         } else {
             d_tblocks.release();
             d_tblk_off.release();

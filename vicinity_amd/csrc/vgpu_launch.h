@@ -29,13 +29,15 @@ struct DevIndex {
     const uint8_t* packed = nullptr;   // FastScan blocks of every list (K == 16)
     const uint32_t* pack_off = nullptr;// [L+1] block offset of each list (K == 16)
     // Transposed 16-entry blocks of every list for the FAST scan (K == 256,
-    // M a multiple of 16; null otherwise): block b of list l is block
-    // tblk_off[l] + b, TBLK_BYTES(M) bytes: codes [m][j] with byte (m, j) the
-    // code of entry j ^ (m & 15) in codebook m, then the 16 entries' b(x).
-    // Entries past the end of the list have code 0 and b(x) 0.
-    const uint8_t* tblocks = nullptr;
+    // M a multiple of 16; null otherwise).  Block b of list l is block
+    // tblk_off[l] + b; lane record m of block B (index 16 B + m) is M bytes of
+    // tcodes, the 16 codes of codebooks m, m + 16, ... (byte j the code of
+    // entry j ^ m), and one float of tbias, b(x) of entry m.  Entries past
+    // the end of the list have code 0 and b(x) NaN.
+    const uint8_t* tcodes = nullptr;
+    const float* tbias = nullptr;
     const uint32_t* tblk_off = nullptr;// [L+1]
-    uint32_t tblk_bytes = 0;           // bytes of tblocks (< 2^31: 32-bit buffer offsets)
+    uint32_t tblk_count = 0;           // blocks (one of slack past the last list's)
     float cmax = 0.f;                  // max ||c||
     float rmax = 0.f;                  // max ||decoded residual||
 };
@@ -232,8 +234,8 @@ bool scan8_fast_uses_tables(const DevIndex& ix);
 // t0 / t1 (optional) are recorded around the kernel.
 void launch_t2_tables(const DevIndex& ix, const float* qn, int nq, float* t2, hipStream_t s,
                       hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
-// Fill ix.tblocks from ix.codes, ix.bias and ix.tblk_off.
-void launch_tblocks(const DevIndex& ix, uint8_t* tblocks, hipStream_t s);
+// Fill ix.tcodes and ix.tbias from ix.codes, ix.bias and ix.tblk_off.
+void launch_tblocks(const DevIndex& ix, uint8_t* tcodes, float* tbias, hipStream_t s);
 void launch_pack4(const DevIndex& ix, uint8_t* packed, hipStream_t s);
 // LUT kernels for tests.
 void launch_adc_tables(const float* codebooks, int M, int K, int ds, const float* r, int nr,
