@@ -228,6 +228,23 @@ int vgpu_ivfpq_export(const vgpu_ivfpq *h, float *centroids, float *codebooks,
                       uint64_t *list_offsets, uint32_t *list_ids, uint8_t *codes,
                       uint32_t *doc_ids, float *vectors);
 
+/* IVFPQIndex::reconstruct (search.rs:857-884): the vector the codes of
+ * insertion index idx approximate, out f32[d]: the decoded residual
+ * (pq.rs:284-290; OPQ: R^T of it, opq.rs:134-139) plus the centroid of the
+ * list holding idx.  Works after compact().  VGPU_ERR_INVALID_PARAMETER when
+ * not built or idx >= num_vectors. */
+int vgpu_ivfpq_reconstruct(const vgpu_ivfpq *h, size_t idx, float *out, size_t len);
+
+/* IVFPQIndex::memory_usage (search.rs:1552-1577, MemoryReport in
+ * src/memory.rs): host bytes by the reference's categories (raw vectors;
+ * graph, always 0; codes and quantizer; doc ids, centroids and lists), plus
+ * the HBM the index and its search workspaces hold. */
+typedef struct {
+    size_t vectors_bytes, graph_bytes, quantized_bytes, metadata_bytes;
+    size_t device_bytes;
+} vgpu_memory_report;
+int vgpu_ivfpq_memory_usage(const vgpu_ivfpq *h, vgpu_memory_report *out);
+
 /* ---- file-backed search: IVFPQFileSearcher (src/ivf_pq/search.rs:247-282,
  * :1620-2041) --------------------------------------------------------------
  * The routing metadata in memory (what load_from_parts, search.rs:1679-1762,

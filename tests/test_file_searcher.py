@@ -84,6 +84,28 @@ def test_half_a_list_code_sidecar_is_rejected_before_device_work(oracle, tmp_pat
     assert e.value.code == _lib.ERR_INVALID_PARAMETER
 
 
+def test_repeated_list_member_is_rejected_at_open(oracle, tmp_path):
+    """A snapshot whose lists hold one vector twice (and another not at all)
+    is reported when the searcher opens it, before any device work."""
+    from vicinity_amd import IVFPQFileSearcher, _lib
+
+    rng = np.random.default_rng(3)
+    base = oracle.normalize_rows(rng.standard_normal((400, 16)).astype(np.float32))
+    oix, _ = oracle.ivfpq_build(base, 8, 4, 16, 3, 0, 5)
+    list_ids = oix.list_ids.copy()
+    list_ids[1] = list_ids[0]
+    path = tmp_path / "dup"
+    write_snapshot(path, dimension=16,
+                   params=dict(num_clusters=8, nprobe=2, num_codebooks=4, codebook_size=16,
+                               use_opq=False, seed=3),
+                   centroids=oix.centroids, codebooks=oix.codebooks, codebook_size=16,
+                   num_codebooks=4, list_offsets=oix.list_offsets, list_ids=list_ids, codes=oix.codes,
+                   doc_ids=np.arange(400, dtype=np.uint32), vectors=None, rotation=None)
+    with pytest.raises(ValueError, match="permutation") as e:
+        IVFPQFileSearcher.load(path)
+    assert e.value.code == _lib.ERR_INVALID_PARAMETER
+
+
 # ---- GPU ------------------------------------------------------------------------
 
 @pytest.fixture
@@ -175,3 +197,38 @@ def test_file_searcher_generation_compacted_and_mmap_warning(vg_device, oracle, 
     assert np.array_equal(ids, oids)
     with pytest.raises(ValueError, match="without raw vectors"):
         fs2.batch_search(q, 10, rerank_pool=20)
+
+
+@pytest.mark.gpu
+def test_explicit_nprobe_zero_probes_nothing(vg_device, oracle, tmp_path):
+    """python.rs:1085-1096 / 1127-1139: an explicit nprobe replaces the index
+    default for the call, 0 included (no list is probed, every row is padding);
+    None keeps the default, which is unchanged afterwards."""
+    from vicinity_amd import MISSING_DISTANCE, MISSING_LABEL, IVFPQFileSearcher, IVFPQIndex
+
+    _print_case("explicit nprobe 0: file searcher and in-memory index")
+    path, oix, rng = _oracle_snapshot(oracle, tmp_path, seed=9)
+    q = rng.standard_normal((20, 32)).astype(np.float32)
+    fs = IVFPQFileSearcher.load(path)
+    mem = IVFPQIndex.load(path)
+    for ix in (fs, mem):
+        for pool in (None, 30):
+            ids, dists = ix.batch_search(q, 10, nprobe=0, rerank_pool=pool)
+            assert (ids == MISSING_LABEL).all() and (dists == MISSING_DISTANCE).all()
+            ids, dists = ix.search(q[0], 10, nprobe=0, rerank_pool=pool)
+            assert ids.size == 0 and dists.size == 0
+        assert ix.nprobe == 4
+        ids, dists = ix.batch_search(q, 10)
+        oids, odists = oix.search_batch(q, 10, 4)
+        assert np.array_equal(ids, oids) and dists.tobytes() == odists.tobytes()
+    _, _, diag = fs.batch_search_with_diagnostics(q, 10, nprobe=0)
+    assert all(g["probed_lists"] == 0 and g["scanned_vectors"] == 0 for g in diag)
+    # the reference's checks still apply: a non-finite query, and a rerank
+    # after the raw vectors are dropped
+    bad = q.copy()
+    bad[3, 5] = np.nan
+    with pytest.raises(ValueError, match="non-finite"):
+        mem.batch_search(bad, 10, nprobe=0)
+    mem.compact()
+    with pytest.raises(ValueError, match="compact"):
+        mem.batch_search(q, 10, nprobe=0, rerank_pool=30)

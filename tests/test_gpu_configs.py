@@ -1,5 +1,6 @@
-"""Full-size runs of the other benchmark configurations, checked through
-size-independent properties and an oracle sample:
+"""Full-size runs of the other benchmark configurations, each whole 10k-query
+batch checked against the oracle (16 threads) and through size-independent
+properties:
 
 - 10M x 96 angular IVF-PQ (nlist 16384, M 48 x 2, ksub 256, nprobe 64, k 10);
 - 1M x 100 4-bit FastScan IVF-PQ with rerank (nlist 2048, M 50 x 2, ksub 16,
@@ -9,8 +10,8 @@ size-independent properties and an oracle sample:
 Base and query vectors are drawn on the GPU from a seeded torch generator with
 the distributions of vicinity_amd/datagen.py (mixtures on the unit sphere,
 std 0.1), because the numpy generator needs minutes at 10M rows.  The oracle
-checks a sample of queries on the arrays the GPU build exports, and the
-build itself: list assignment and PQ codes of sampled vectors recomputed by the
+runs every query on the arrays the GPU build exports, and checks the build
+itself: list assignment and PQ codes of sampled vectors recomputed by the
 oracle from the exported centroids and codebooks (argmin, ties to the lowest
 index)."""
 
@@ -83,13 +84,12 @@ def test_config_10m_d96_angular(oracle):
     _check_rows(ids, dists, 10)
     art = ix.export()
     rng = np.random.default_rng(7)
-    _print_case("10M x 96 angular: oracle sample")
-    qs = rng.choice(len(queries), 60, replace=False)
+    _print_case("10M x 96 angular: oracle on all 10k queries")
     oix = oracle.Index(art["centroids"], art["codebooks"], art["list_offsets"], art["list_ids"],
                        art["codes"], art["doc_ids"], None, art["M"], art["K"])
-    oids, odists = oix.search_batch(queries[qs], 10, 64)
-    assert np.array_equal(ids[qs], oids)
-    assert dists[qs].tobytes() == odists.tobytes()
+    oids, odists = oix.search_batch(queries, 10, 64, threads=16)
+    assert np.array_equal(ids, oids)
+    assert dists.tobytes() == odists.tobytes()
     _check_build(oracle, art, oracle.normalize_rows(base), rng.choice(len(base), 4000, replace=False))
     # EXACT mode agrees with FAST on the whole batch (same reference arithmetic)
     _print_case("10M x 96 angular: exact mode")
@@ -114,16 +114,16 @@ def test_config_1m_d100_fastscan_rerank(oracle):
     _check_rows(ids, dists, 10)
     art = ix.export()
     rng = np.random.default_rng(8)
-    qs = rng.choice(len(queries), 100, replace=False)
-    _print_case("1M x 100 FastScan + rerank: oracle sample")
+    _print_case("1M x 100 FastScan + rerank: oracle on all 10k queries")
     oix = oracle.Index(art["centroids"], art["codebooks"], art["list_offsets"], art["list_ids"],
                        art["codes"], art["doc_ids"], art["vectors"], art["M"], art["K"])
-    oids, odists = oix.search_batch(queries[qs], 10, 64, rerank_pool=100)
-    assert np.array_equal(ids[qs], oids)
-    assert dists[qs].tobytes() == odists.tobytes()
+    oids, odists = oix.search_batch(queries, 10, 64, rerank_pool=100, threads=16)
+    assert np.array_equal(ids, oids)
+    assert dists.tobytes() == odists.tobytes()
     # without rerank (FastScan distances)
-    pids, pdists = ix.batch_search(queries[qs], 10)
-    oids, odists = oix.search_batch(queries[qs], 10, 64)
+    _print_case("1M x 100 FastScan, no rerank: oracle on all 10k queries")
+    pids, pdists = ix.batch_search(queries, 10)
+    oids, odists = oix.search_batch(queries, 10, 64, threads=16)
     assert np.array_equal(pids, oids)
     assert pdists.tobytes() == odists.tobytes()
     _check_build(oracle, art, art["vectors"], rng.choice(len(base), 4000, replace=False))
@@ -138,10 +138,10 @@ def test_config_flat_100k_d96(oracle):
     fx.add(w.base)
     ids, dists = fx.search(w.queries, 10)
     _check_rows(ids, dists, 10)
-    qs = np.random.default_rng(9).choice(len(w.queries), 200, replace=False)
-    oids, odists = oracle.flat_search(w.base, w.queries[qs], 10, metric=0)
-    assert np.array_equal(ids[qs], oids)
-    assert dists[qs].tobytes() == odists.tobytes()
+    _print_case("flat 100k x 96 L2: oracle on all 10k queries")
+    oids, odists = oracle.flat_search(w.base, w.queries, 10, metric=0, threads=16)
+    assert np.array_equal(ids, oids)
+    assert dists.tobytes() == odists.tobytes()
 
 
 def test_config_1m_d128_headline(oracle):

@@ -219,3 +219,91 @@ def test_opq_quantizer_is_serdes_optimized_variant(tmp_path):
         read_snapshot(tmp_path)
     _write(tmp_path / "plain", a)
     assert read_snapshot(tmp_path / "plain")["rotation"] is None
+
+
+def _crc32_bitwise(data: bytes) -> int:
+    """checksum_file (src/persistence/generation.rs:451-470) restated bit by
+    bit: reflected polynomial 0xEDB88320, initial and final inversion."""
+    crc = 0xFFFFFFFF
+    for byte in data:
+        crc ^= byte
+        for _ in range(8):
+            crc = (crc >> 1) ^ (0xEDB88320 & (-(crc & 1) & 0xFFFFFFFF))
+    return crc ^ 0xFFFFFFFF
+
+
+def test_crc32_of_the_inventory_is_the_references():
+    import zlib
+
+    assert _crc32_bitwise(b"123456789") == 0xCBF43926  # the CRC-32 check value
+    rng = np.random.default_rng(4)
+    for n in (0, 1, 7, 300):
+        data = rng.integers(0, 256, n, dtype=np.uint8).tobytes()
+        assert zlib.crc32(data) == _crc32_bitwise(data)
+
+
+def test_generation_publication_layout(tmp_path):
+    """GenerationWriter (generation.rs:36-140): CURRENT names the published
+    generation, whose manifest lists its components (manifest.rs:64-77) and
+    whose GENERATION.json holds each other file's length and CRC-32, sorted
+    by path (serde's pretty JSON); a second publication replaces CURRENT and
+    keeps the first generation."""
+    from vicinity_amd.snapshot import open_current, publish_generation
+
+    a = _arrays(seed=3)
+    root = tmp_path / "root"
+    g1 = publish_generation(root, lambda d: _write(d, a, generation_components=True))
+    cur = (root / "CURRENT").read_text()
+    assert cur.endswith("\n") and os.path.join(root, "generations", cur.strip()) == g1
+    assert open_current(root) == g1
+    man = json.loads(open(os.path.join(g1, "manifest.json")).read())
+    assert man["generation_components"] == ["centroids.bin", "clusters.bin", "codes.bin", "doc_ids.bin",
+                                             "list_codes.bin", "list_offsets.bin", "raw_vectors.bin"]
+    inv_text = open(os.path.join(g1, "GENERATION.json")).read()
+    inv = json.loads(inv_text)
+    assert inv_text == json.dumps(inv, indent=2)
+    assert inv["version"] == 1
+    names = sorted(f for f in os.listdir(g1) if f != "GENERATION.json")
+    assert [e["path"] for e in inv["files"]] == names
+    for e in inv["files"]:
+        data = open(os.path.join(g1, e["path"]), "rb").read()
+        assert e["length"] == len(data) and e["crc32"] == _crc32_bitwise(data), e["path"]
+    assert not [f for f in os.listdir(root / "generations") if f.startswith(".staging")]
+    snap = read_snapshot(open_current(root))
+    assert np.array_equal(snap["codes"], a["codes"])
+    g2 = publish_generation(root, lambda d: _write(d, _arrays(seed=5), generation_components=True))
+    assert open_current(root) == g2 != g1 and os.path.isdir(g1)
+
+
+def test_generation_publication_refusals(tmp_path):
+    """A contended publication lock and a CURRENT replaced while the
+    generation was staged are errors that leave CURRENT as it was
+    (generation.rs:142-188); a manifest whose component list disagrees with
+    its files is refused on load (manifest.rs:79-98)."""
+    import fcntl
+
+    from vicinity_amd.snapshot import publish_generation
+
+    a = _arrays(seed=6)
+    root = tmp_path / "root"
+    g1 = publish_generation(root, lambda d: _write(d, a, generation_components=True))
+    cur = (root / "CURRENT").read_text()
+    with open(root / ".PUBLISH.lock", "a") as held:
+        fcntl.flock(held.fileno(), fcntl.LOCK_EX)
+        with pytest.raises(SnapshotFormatError, match="advisory lock"):
+            publish_generation(root, lambda d: _write(d, a, generation_components=True))
+        fcntl.flock(held.fileno(), fcntl.LOCK_UN)
+    assert (root / "CURRENT").read_text() == cur
+
+    def racing_writer(d):
+        _write(d, a, generation_components=True)
+        (root / "CURRENT").write_text("someone-else\n")
+
+    with pytest.raises(SnapshotFormatError, match="CURRENT changed"):
+        publish_generation(root, racing_writer)
+    man_path = os.path.join(g1, "manifest.json")
+    man = json.loads(open(man_path).read())
+    man["generation_components"] = man["generation_components"][:-1]
+    open(man_path, "w").write(json.dumps(man, indent=2))
+    with pytest.raises(SnapshotFormatError, match="component inventory mismatch"):
+        read_snapshot(g1)

@@ -65,6 +65,17 @@ class FileDiagnostics(ctypes.Structure):
         return {name: int(getattr(self, name)) for name, _ in self._fields_}
 
 
+class MemoryReport(ctypes.Structure):
+    """MemoryReport (src/memory.rs:4-14) plus the HBM the index holds."""
+    _fields_ = [(name, ctypes.c_size_t) for name in (
+        "vectors_bytes", "graph_bytes", "quantized_bytes", "metadata_bytes", "device_bytes")]
+
+    def as_dict(self) -> dict:
+        d = {name: int(getattr(self, name)) for name, _ in self._fields_}
+        d["total"] = d["vectors_bytes"] + d["graph_bytes"] + d["quantized_bytes"] + d["metadata_bytes"]
+        return d
+
+
 class Stats(ctypes.Structure):
     _fields_ = [("ms_normalize", ctypes.c_float), ("ms_coarse", ctypes.c_float),
                 ("ms_select", ctypes.c_float), ("ms_scan", ctypes.c_float),
@@ -119,6 +130,8 @@ SIGNATURES = {
     "vgpu_ivfpq_set_rotation": (_i, [_H, _vp, _sz]),
     "vgpu_ivfpq_probe_batch": (_i, [_H, _vp, _sz, _sz, _sz, _vp, ctypes.POINTER(_sz)]),
     "vgpu_ivfpq_export": (_i, [_H, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "vgpu_ivfpq_reconstruct": (_i, [_H, _sz, _vp, _sz]),
+    "vgpu_ivfpq_memory_usage": (_i, [_H, ctypes.POINTER(MemoryReport)]),
     "vgpu_ivfpq_file_open": (_i, [_sz, ctypes.POINTER(Params), _vp, _sz, _vp, _sz, _vp, _vp, _vp, _sz, _vp,
                                   ctypes.c_char_p, _i, ctypes.POINTER(_H)]),
     "vgpu_ivfpq_file_free": (None, [_H]),

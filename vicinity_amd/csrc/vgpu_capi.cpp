@@ -433,6 +433,23 @@ int vgpu_ivfpq_export(const vgpu_ivfpq* h, float* centroids, float* codebooks, u
     });
 }
 
+int vgpu_ivfpq_reconstruct(const vgpu_ivfpq* h, size_t idx, float* out, size_t len) {
+    return guard([&] {
+        need(h && out, VGPU_ERR_INVALID_PARAMETER, "null argument");
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
+        need(len >= h->ix->d, VGPU_ERR_INVALID_PARAMETER, "output shorter than the dimension");
+        h->ix->reconstruct(idx, out);
+    });
+}
+
+int vgpu_ivfpq_memory_usage(const vgpu_ivfpq* h, vgpu_memory_report* out) {
+    return guard([&] {
+        need(h && out, VGPU_ERR_INVALID_PARAMETER, "null argument");
+        std::shared_lock<std::shared_mutex> lk(h->ix->mu);
+        *out = h->ix->memory_usage();
+    });
+}
+
 /* ---- flat ---------------------------------------------------------------- */
 
 int vgpu_flat_new(size_t dimension, int metric, vgpu_flat** out) {

@@ -80,8 +80,14 @@ FileIvfpq::FileIvfpq(size_t dim, const vgpu_ivfpq_params& p, const float* cent, 
     for (size_t l = 0; l < L; l++)
         if (offsets[l + 1] < offsets[l])
             throw Error(VGPU_ERR_INVALID_PARAMETER, "list_offsets must be non-decreasing");
-    for (size_t i = 0; i < nv; i++)
-        if (list_ids[i] >= nv) throw Error(VGPU_ERR_INVALID_PARAMETER, "list id beyond num_vectors");
+    {
+        std::vector<uint8_t> seen(nv, 0);  // each vector in exactly one list position
+        for (size_t i = 0; i < nv; i++) {
+            if (list_ids[i] >= nv) throw Error(VGPU_ERR_INVALID_PARAMETER, "list id beyond num_vectors");
+            if (seen[list_ids[i]]++)
+                throw Error(VGPU_ERR_INVALID_PARAMETER, "list_ids must be a permutation of 0..num_vectors");
+        }
+    }
     // search.rs:1707-1735: list_codes.bin + list_offsets.bin when present
     // (both or neither), codes.bin otherwise; raw_vectors.bin for rerank.
     fd_codes.v = open_file(dir + "/codes.bin", true);

@@ -1039,6 +1039,63 @@ void IvfpqIndex::search_device_in(const float* d_q, size_t nq, size_t k, size_t 
     run_search(d_q, nq, pl, w, d_ids, d_dists, s ? s : stream, nullptr, nullptr);
 }
 
+// search.rs:857-884: codes of insertion index idx decoded (pq.rs:284-290;
+// OPQ: opq.rs:134-139, R^T v summed in order with one rounding per product
+// and per sum, opq.rs:194-204), plus the centroid of the list holding idx
+// (found by a scan of the lists, as cluster_of does).
+void IvfpqIndex::reconstruct(size_t idx, float* out) const {
+    if (!built) throw Error(VGPU_ERR_INVALID_PARAMETER, "index must be built before reconstruct");
+    if (idx >= n())
+        throw Error(VGPU_ERR_INVALID_PARAMETER, "vector index " + std::to_string(idx) +
+                                                    " out of range (num_vectors = " + std::to_string(n()) + ")");
+    size_t pos = 0;
+    while (pos < list_ids.size() && list_ids[pos] != (uint32_t)idx) pos++;
+    if (pos == list_ids.size())
+        throw Error(VGPU_ERR_DEVICE, "vector index " + std::to_string(idx) + " is not in any inverted list");
+    const size_t l = std::upper_bound(offsets.begin(), offsets.end(), (uint64_t)pos) - offsets.begin() - 1;
+    std::vector<float> dec(d);
+    for (size_t m = 0; m < M; m++) {
+        const uint8_t c = codes[idx * M + m];
+        std::memcpy(&dec[m * ds], &codebooks[(m * K + c) * ds], ds * sizeof(float));
+    }
+    if (!rotation.empty()) {
+        std::vector<float> r(d);
+        for (size_t i = 0; i < d; i++) {
+            float sum = 0.0f;
+            for (size_t j = 0; j < d; j++) sum += rotation[j * d + i] * dec[j];  // -ffp-contract=off: no FMA
+            r[i] = sum;
+        }
+        dec.swap(r);
+    }
+    for (size_t i = 0; i < d; i++) out[i] = dec[i] + centroids[l * d + i];
+}
+
+// search.rs:1552-1577 by the reference's categories over the host mirror,
+// plus the device buffers of the index and its pooled search workspaces.
+vgpu_memory_report IvfpqIndex::memory_usage() {
+    vgpu_memory_report r{};
+    r.vectors_bytes = vectors.size() * sizeof(float);
+    r.quantized_bytes = codes.size() + codebooks.size() * sizeof(float) + rotation.size() * sizeof(float);
+    r.metadata_bytes = doc_ids.size() * sizeof(uint32_t) + centroids.size() * sizeof(float) +
+                       offsets.size() * sizeof(uint64_t) + list_ids.size() * sizeof(uint32_t) +
+                       list_mask.size() * sizeof(uint64_t);
+    size_t dev = d_centroids.bytes() + d_codebooks.bytes() + d_bias.bytes() + d_vectors.bytes() +
+                 d_rotation.bytes() + d_cb16.bytes() + d_offsets.bytes() + d_list_ids.bytes() +
+                 d_doc_ids.bytes() + d_pack_off.bytes() + d_codes.bytes() + d_packed.bytes() +
+                 d_tblocks.bytes() + d_tblk_off.bytes() + d_ecat.bytes() + b_cb16.bytes() + b_dots.bytes() +
+                 b_cand.bytes() + b_cand_n.bytes() + b_cflag_list.bytes() + b_cflag_count.bytes() +
+                 b_overflow.bytes();
+    {
+        std::lock_guard<std::mutex> lk(pool_mu);
+        for (const auto& w : ws_pool)
+            dev += w->arena.bytes() + w->q.bytes() + w->odist.bytes() + w->ids.bytes() + w->slots.bytes() +
+                   w->want.bytes() + w->fqn.bytes() + w->fdist.bytes() + w->frres.bytes() + w->fvidx.bytes() +
+                   w->gprobe.bytes();
+    }
+    r.device_bytes = dev;
+    return r;
+}
+
 void IvfpqIndex::search_host(const float* q, size_t nq, size_t k, size_t nprobe, size_t pool,
                              int64_t* ids, float* dists) {
     for (size_t i = 0; i < nq * d; i++)

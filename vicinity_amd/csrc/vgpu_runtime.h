@@ -46,6 +46,7 @@ struct DevBuf {
         p = nullptr;
         n = 0;
     }
+    size_t bytes() const { return p ? n * sizeof(T) : 0; }
     // Grow-only allocation (contents are not preserved on growth).
     void reserve(size_t count) {
         if (count <= n && p) return;
@@ -232,6 +233,8 @@ struct IvfpqIndex {
     void search_filtered(const float* q, size_t nq, size_t k, const int* cats, int64_t* ids,
                          float* dists);
     vgpu_search_stats last_stats();
+    void reconstruct(size_t idx, float* out) const;
+    vgpu_memory_report memory_usage();
 
     // Borrow a workspace from the pool (a new one when all are in use).
     std::unique_ptr<SearchWs> take_ws();

@@ -15,27 +15,18 @@ from __future__ import annotations
 
 import ctypes
 import os
-import re
+import threading
 import warnings
 
 import numpy as np
 
 from . import _lib
 from .ivf_pq import MISSING_DISTANCE, MISSING_LABEL, _f32_2d
-from .snapshot import SnapshotFormatError, read_snapshot
+from .snapshot import open_current, read_snapshot
 
 
-def _current_generation(root) -> str:
-    """open_current (persistence/generation.rs:191-205): root/CURRENT names a
-    directory under root/generations."""
-    with open(os.path.join(root, "CURRENT"), encoding="utf-8") as f:
-        gen = f.read().strip()
-    if not re.fullmatch(r"[A-Za-z0-9_.-]+", gen) or gen in (".", ".."):
-        raise SnapshotFormatError(f"invalid generation id {gen!r}")
-    path = os.path.join(root, "generations", gen)
-    if os.path.islink(path) or not os.path.isdir(path):
-        raise SnapshotFormatError(f"current generation {path} is not a directory")
-    return path
+# open_current (generation.rs:191-205)
+_current_generation = open_current
 
 
 class IVFPQFileSearcher:
@@ -51,6 +42,7 @@ class IVFPQFileSearcher:
         self._num_codebooks = int(p["num_codebooks"])
         self._codebook_size = int(p["codebook_size"])
         self._nprobe = int(p["nprobe"])
+        self._search_lock = threading.Lock()  # python.rs:172, the per-call nprobe
         self._path = os.fspath(path)
         prm = _lib.Params(self._num_clusters, self._nprobe, self._num_codebooks,
                           self._codebook_size, int(p["seed"]),
@@ -90,8 +82,9 @@ class IVFPQFileSearcher:
         return IVFPQFileSearcher.load(_current_generation(root))
 
     def set_nprobe(self, nprobe: int) -> None:
-        _lib.check(self._L.vgpu_ivfpq_file_set_nprobe(self._h, int(nprobe)))
-        self._nprobe = int(nprobe)
+        with self._search_lock:
+            _lib.check(self._L.vgpu_ivfpq_file_set_nprobe(self._h, int(nprobe)))
+            self._nprobe = int(nprobe)
 
     # ---- search (python.rs:921-1046) ---------------------------------------
     def _run(self, queries, k: int, nprobe, rerank_pool):
@@ -107,9 +100,18 @@ class IVFPQFileSearcher:
         dists = np.full((nq, k), MISSING_DISTANCE, np.float32)
         diag = (_lib.FileDiagnostics * max(nq, 1))()
         pool = 0 if rerank_pool is None else max(int(rerank_pool), k, 1)
-        _lib.check(self._L.vgpu_ivfpq_file_search_batch(
-            self._h, _lib.ptr(q) if nq else None, nq, self._dim, k, nprobe or 0, pool,
-            _lib.ptr(ids) if ids.size else None, _lib.ptr(dists) if dists.size else None, diag))
+        # python.rs:1116-1142: under the search lock, an explicit nprobe (0
+        # included: no list is probed) replaces the default for the call
+        with self._search_lock:
+            if nprobe is not None:
+                _lib.check(self._L.vgpu_ivfpq_file_set_nprobe(self._h, int(nprobe)))
+            try:
+                _lib.check(self._L.vgpu_ivfpq_file_search_batch(
+                    self._h, _lib.ptr(q) if nq else None, nq, self._dim, k, 0, pool,
+                    _lib.ptr(ids) if ids.size else None, _lib.ptr(dists) if dists.size else None, diag))
+            finally:
+                if nprobe is not None:
+                    _lib.check(self._L.vgpu_ivfpq_file_set_nprobe(self._h, self._nprobe))
         return ids, dists, [diag[i].as_dict() for i in range(nq)]
 
     def batch_search(self, queries, k: int, nprobe: int | None = None,

@@ -13,12 +13,13 @@ search follows the Rust API (``with_filtering``, ``add_metadata``,
 from __future__ import annotations
 
 import ctypes
+import os
 
 import numpy as np
 
 from . import _lib
 from .filtering import MetadataFilter, filter_category, metadata_category
-from .snapshot import read_snapshot, write_snapshot
+from .snapshot import open_current, publish_generation, read_snapshot, write_snapshot
 
 # python.rs:1303-1304 (faiss convention)
 MISSING_LABEL = -1
@@ -171,6 +172,24 @@ class IVFPQIndex:
     def save(self, path) -> None:
         """Save the built index as a directory snapshot in the reference's
         format (IVFPQIndex::save_to_dir, search.rs:906-1002)."""
+        self._save(path, False)
+
+    def save_generation(self, path) -> None:
+        """Publish the built index as an immutable generation below `path`
+        (IVFPQIndex::save_to_generation, search.rs:918-936; python.rs:660-665)."""
+        if not self._info().built:
+            raise ValueError("IVF-PQ index: save before build")
+        publish_generation(path, lambda staging: self._save(staging, True))
+
+    @staticmethod
+    def load_generation(path) -> "IVFPQIndex":
+        """Load the generation named by ``path/CURRENT``
+        (IVFPQIndex::load_from_generation, search.rs:938-943; python.rs:683-697)."""
+        if not os.path.exists(os.path.join(path, "CURRENT")):
+            raise FileNotFoundError(os.path.join(path, "CURRENT"))
+        return IVFPQIndex.load(open_current(path))
+
+    def _save(self, path, generation: bool) -> None:
         inf = self._info()
         if not inf.built:
             raise ValueError("IVF-PQ index: save before build")
@@ -189,7 +208,7 @@ class IVFPQIndex:
             codes=art["codes"], doc_ids=art["doc_ids"], vectors=art["vectors"], list_masks=masks,
             filter_field=self._filter_field,
             filter_metadata=self._metadata if self._filter_field is not None else None,
-            rotation=art["rotation"])
+            rotation=art["rotation"], generation_components=generation)
 
     @staticmethod
     def load(path) -> "IVFPQIndex":
@@ -334,10 +353,28 @@ class IVFPQIndex:
         ids = np.full((nq, k), MISSING_LABEL, np.int64)
         dists = np.full((nq, k), MISSING_DISTANCE, np.float32)
         pool = 0 if rerank_pool is None else max(int(rerank_pool), k, 1)
+        if nprobe is not None and int(nprobe) == 0:
+            self._check_no_probe(q, rerank_pool)
+            return ids, dists
         _lib.check(self._L.vgpu_ivfpq_search_batch(
             self._h, _lib.ptr(q) if nq else None, nq, self._dim, k, nprobe or 0, pool,
             _lib.ptr(ids) if ids.size else None, _lib.ptr(dists) if dists.size else None))
         return ids, dists
+
+    def _check_no_probe(self, q, rerank_pool) -> None:
+        """An explicit nprobe of 0 is the index's nprobe for the call
+        (python.rs:1085-1096): find_nearest_centroids probes no list
+        (search.rs:1610), so every row is padding once the reference's checks
+        pass: built (search.rs:1181-1186), query values (checked by the engine,
+        which searches nothing with k = 0), raw vectors for a rerank
+        (search.rs:1137-1142)."""
+        nq = q.shape[0]
+        _lib.check(self._L.vgpu_ivfpq_search_batch(self._h, _lib.ptr(q) if nq else None, nq, self._dim,
+                                                   0, 0, 0, None, None))
+        if rerank_pool is not None and not self._info().has_vectors:
+            err = ValueError("search_reranked after compact(): raw vectors were dropped")
+            err.code = _lib.ERR_UNSUPPORTED  # type: ignore[attr-defined]
+            raise err
 
     def search_batch_device(self, queries, k: int, nprobe: int | None = None,
                             rerank_pool: int | None = None, out_ids=None, out_dists=None,
@@ -369,6 +406,24 @@ class IVFPQIndex:
         _lib.check(self._L.vgpu_ivfpq_probe_batch(self._h, _lib.ptr(q), q.shape[0], q.shape[1], P,
                                                    _lib.ptr(lists), ctypes.byref(out_p)))
         return lists[:, :out_p.value]
+
+    def reconstruct(self, idx: int) -> np.ndarray:
+        """IVFPQIndex::reconstruct (search.rs:857-884): the vector the codes
+        of insertion index `idx` approximate, the decoded residual plus its
+        list's centroid (float32 [d]); works after compact()."""
+        if idx < 0:
+            raise ValueError(f"vector index {idx} out of range (num_vectors = {len(self)})")
+        out = np.empty(self._dim, np.float32)
+        _lib.check(self._L.vgpu_ivfpq_reconstruct(self._h, int(idx), _lib.ptr(out), out.size))
+        return out
+
+    def memory_usage(self) -> dict:
+        """IVFPQIndex::memory_usage (search.rs:1552-1577): host bytes by the
+        reference's MemoryReport categories and their total, plus
+        device_bytes, the HBM the index and its search workspaces hold."""
+        r = _lib.MemoryReport()
+        _lib.check(self._L.vgpu_ivfpq_memory_usage(self._h, ctypes.byref(r)))
+        return r.as_dict()
 
     def last_stats(self) -> dict:
         st = _lib.Stats()

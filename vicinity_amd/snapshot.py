@@ -16,6 +16,10 @@ Files (src/ivf_pq/persistence.rs, manifest.rs, file_storage.rs):
   list by list), the file searcher's sidecars (file_storage.rs:39-71); written
   for it, not read by load (search.rs:1034-1084 does not read them).
 
+Generations (src/persistence/generation.rs): ``root/generations/<id>`` holds a
+snapshot whose manifest lists its component files, plus ``GENERATION.json``
+(each file's length and CRC-32); ``root/CURRENT`` names the published one.
+
 Floats in the manifest are decimal strings; codebook values are read back to
 the nearest float32 of the decimal (correctly rounded, no double rounding), so
 a loaded index holds the saved codebooks bit for bit.
@@ -23,9 +27,14 @@ a loaded index holds the saved codebooks bit for bit.
 
 from __future__ import annotations
 
+import fcntl
+import itertools
 import json
 import os
+import re
 import struct
+import time
+import zlib
 from decimal import Decimal
 
 import numpy as np
@@ -127,12 +136,14 @@ def _write_atomic(path: str, data: bytes) -> None:
 def write_snapshot(path, *, dimension: int, params: dict, centroids, codebooks, codebook_size: int,
                    num_codebooks: int, list_offsets, list_ids, codes, doc_ids, vectors=None,
                    list_masks=None, filter_field=None, filter_metadata=None,
-                   rotation=None) -> None:
+                   rotation=None, generation_components=False) -> None:
     """Write a built index's arrays as a snapshot directory.  `params` holds
     num_clusters, nprobe, num_codebooks, codebook_size, use_opq and seed as
     the index was configured; list_offsets / list_ids are the lists as entry
     offsets and member indices.  With use_opq the quantizer is written as
-    Quantizer::Optimized holding `rotation` (d x d, or None)."""
+    Quantizer::Optimized holding `rotation` (d x d, or None).  A generation's
+    manifest lists its component files (search.rs:991-995,
+    manifest.rs:64-77)."""
     centroids = np.ascontiguousarray(centroids, np.float32).reshape(-1, dimension)
     codebooks = np.ascontiguousarray(codebooks, np.float32).reshape(-1)
     list_offsets = np.asarray(list_offsets, np.uint64)
@@ -189,6 +200,8 @@ def write_snapshot(path, *, dimension: int, params: dict, centroids, codebooks, 
         }}
     else:
         manifest["quantizer"] = {"Product": product}
+    if generation_components:
+        manifest["generation_components"] = _COMPONENTS + (["raw_vectors.bin"] if present else [])
     text = json.dumps(manifest, indent=2)
     text = text.replace('"@CODEBOOKS@"', "[" + ", ".join(_f32_text(v) for v in codebooks) + "]")
     if rotation is not None:
@@ -364,3 +377,123 @@ def read_snapshot(path, arrays: bool = True) -> dict:
         "filter_field": filter_field, "filter_metadata": filter_metadata, "rotation": rotation,
         "raw_vectors_present": bool(present),
     }
+
+
+# ---- generations (src/persistence/generation.rs) ----------------------------
+
+_GEN_SEQUENCE = itertools.count()
+
+
+def open_current(root) -> str:
+    """open_current (generation.rs:191-205): root/CURRENT names a directory
+    under root/generations."""
+    with open(os.path.join(root, "CURRENT"), encoding="utf-8") as f:
+        gen = f.read().strip()
+    if not re.fullmatch(r"[A-Za-z0-9_.-]+", gen) or gen in (".", ".."):
+        raise SnapshotFormatError(f"invalid generation id {gen!r}")
+    path = os.path.join(root, "generations", gen)
+    if os.path.islink(path) or not os.path.isdir(path):
+        raise SnapshotFormatError(f"current generation {path} is not a directory")
+    return path
+
+
+def _fsync_dir(path) -> None:
+    fd = os.open(path, os.O_RDONLY)
+    try:
+        os.fsync(fd)
+    finally:
+        os.close(fd)
+
+
+def generation_inventory(directory) -> dict:
+    """write_inventory (generation.rs:389-449): every file below the
+    generation but GENERATION.json, sorted by its '/'-separated path, with its
+    length and CRC-32 (the reflected 0xEDB88320 polynomial, generation.rs:
+    451-470, which zlib.crc32 computes).  Symlinks and other entries are
+    format errors."""
+    files = []
+    for top, dirs, names in os.walk(directory, followlinks=False):
+        for name in list(dirs) + names:
+            full = os.path.join(top, name)
+            if os.path.islink(full):
+                raise SnapshotFormatError(f"generation contains symlink {full}")
+        for name in names:
+            full = os.path.join(top, name)
+            rel = os.path.relpath(full, directory).replace(os.sep, "/")
+            if rel == "GENERATION.json":
+                continue
+            if not os.path.isfile(full):
+                raise SnapshotFormatError(f"generation contains unsupported entry {full}")
+            crc, length = 0, 0
+            with open(full, "rb") as f:
+                for chunk in iter(lambda: f.read(1 << 20), b""):
+                    crc = zlib.crc32(chunk, crc)
+                    length += len(chunk)
+            files.append({"path": rel, "length": length, "crc32": crc})
+    files.sort(key=lambda e: e["path"].encode("utf-8"))
+    return {"version": 1, "files": files}
+
+
+def publish_generation(root, write) -> str:
+    """GenerationWriter (generation.rs:36-140): write(staging) fills a hidden
+    staging directory under root/generations, which is then checked by
+    reading it back, inventoried (GENERATION.json), synced and renamed to
+    generations/<id>; root/CURRENT is replaced last (temporary file, sync,
+    rename), under the advisory lock root/.PUBLISH.lock, and only if CURRENT
+    still names the generation it named when the writer started.  Returns the
+    published directory."""
+    root = os.fspath(root)
+    gens = os.path.join(root, "generations")
+    os.makedirs(gens, exist_ok=True)
+    cur_path = os.path.join(root, "CURRENT")
+    try:
+        with open(cur_path, encoding="utf-8") as f:
+            expected = f.read().strip()
+    except FileNotFoundError:
+        expected = None
+    gen_id = f"{time.time_ns()}-{os.getpid()}-{next(_GEN_SEQUENCE)}"
+    staging = os.path.join(gens, f".staging-{gen_id}")
+    os.mkdir(staging)
+    write(staging)
+    read_snapshot(staging)  # validate_staged_generation (search.rs:1016-1031)
+    with open(os.path.join(root, ".PUBLISH.lock"), "a") as lock:
+        try:
+            fcntl.flock(lock.fileno(), fcntl.LOCK_EX | fcntl.LOCK_NB)
+        except BlockingIOError:
+            raise SnapshotFormatError(
+                f"{root}/.PUBLISH.lock: another generation publisher holds the advisory lock") from None
+        try:
+            try:
+                with open(cur_path, encoding="utf-8") as f:
+                    now = f.read().strip()
+            except FileNotFoundError:
+                now = None
+            if now != expected:
+                raise SnapshotFormatError(f"{cur_path}: CURRENT changed while this generation was being built")
+            inv = os.path.join(staging, "GENERATION.json")
+            if os.path.exists(inv):
+                raise SnapshotFormatError("GENERATION.json is reserved for the generation inventory")
+            _write_atomic(inv, json.dumps(generation_inventory(staging), indent=2).encode("utf-8"))
+            for top, _, names in os.walk(staging):
+                for name in names:
+                    with open(os.path.join(top, name), "rb") as f:
+                        os.fsync(f.fileno())
+                _fsync_dir(top)
+            published = os.path.join(gens, gen_id)
+            os.rename(staging, published)
+            _fsync_dir(gens)
+            tmp = os.path.join(root, f".CURRENT.tmp.{os.getpid()}.{next(_GEN_SEQUENCE)}")
+            try:
+                with open(tmp, "w", encoding="utf-8") as f:
+                    f.write(gen_id + "\n")
+                    f.flush()
+                    os.fsync(f.fileno())
+                os.replace(tmp, cur_path)
+            except BaseException:
+                if os.path.exists(tmp):
+                    os.remove(tmp)
+                raise
+            _fsync_dir(root)
+        finally:
+            fcntl.flock(lock.fileno(), fcntl.LOCK_UN)
+    return published
