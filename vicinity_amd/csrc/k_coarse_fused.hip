@@ -8,12 +8,12 @@
 //       their list index into one float key; two waves share a query block and
 //       merge their lists.  The keys above a threshold derived from the P-th
 //       largest key and the error bounds are the query's candidates.
-//   coarse_topp_kernel   one wave per query: rescores the candidates with the
-//       reference's sequential dot (cosine_distance_normalized,
-//       src/distance.rs:104-109), sorts by (score, list) and writes the P
-//       smallest in order (find_nearest_centroids, search.rs:1602-1617).  A
-//       query whose candidate set may be incomplete goes to
-//       launch_coarse_exact_flagged.
+//       At its end each wave takes four of the workgroup's queries in turn:
+//       it rescores their candidates with the reference's sequential dot
+//       (cosine_distance_normalized, src/distance.rs:104-109), sorts them by
+//       (score, list) and writes the P smallest in order
+//       (find_nearest_centroids, search.rs:1602-1617).  A query whose
+//       candidate set may be incomplete goes to launch_coarse_exact_flagged.
 //
 // MFMA layout (v_mfma_f32_16x16x32_bf16, wave64): lane l holds row/column
 // l % 16 and eight consecutive k of group l / 16 for A and B; the result
@@ -91,19 +91,25 @@ void launch_coarse_bf16_pack(const float* C, int L, int d, uint4* Cb, hipStream_
                        L, Lp, d, DT, Cb);
 }
 
-// Dynamic LDS of the fused kernel, in turn: the normalisation tile
-// [FC_QB][d + 1] floats; two pipeline stages of (hi, lo) centroid chunks; the
-// waves' key lists [FC_QBW][FC_NH][4][J][64]; then [FC_QB] norms and bounds.
+// Dynamic LDS of the fused kernel: one region used in turn by two pipeline
+// stages of (hi, lo) centroid chunks, the waves' key lists
+// [FC_QBW][FC_NH][4][J][64] and the candidate rows [FC_QB][32 J] with their
+// keys, later exact scores; then the query tile [FC_QB][fc_tile_stride(d)]
+// floats (kept for the exact rescoring); then [FC_QB] norms, bounds,
+// candidate counts, score margins and counts of candidates to rescore.
 __host__ __device__ inline size_t fc_stage_chunks(int DT) { return (size_t)FC_ST * DT * 4 * 16; }
-__host__ __device__ inline size_t fc_main_bytes(int d, int DT, int J) {
-    const size_t tile = (size_t)FC_QB * (d + 1) * 4;
+__host__ __device__ inline size_t fc_main_bytes(int DT, int J) {
     const size_t stages = 2 * 2 * fc_stage_chunks(DT) * 16;
     const size_t merge = (size_t)FC_QBW * FC_NH * 4 * J * 64 * 4;
-    size_t m = tile > stages ? tile : stages;
-    return m > merge ? m : merge;
+    const size_t rows = 2 * (size_t)FC_QB * 32 * J * 4;  // candidate lists and their scores
+    size_t m = stages > merge ? stages : merge;
+    return m > rows ? m : rows;
 }
+// query tile row stride: a multiple of four floats (16-byte aligned rows)
+__host__ __device__ inline int fc_tile_stride(int d) { return (d & ~3) + 4; }
+__host__ __device__ inline size_t fc_tile_bytes(int d) { return (size_t)FC_QB * fc_tile_stride(d) * 4; }
 __host__ __device__ inline size_t fc_lds_bytes(int d, int DT, int J) {
-    return fc_main_bytes(d, DT, J) + FC_QB * 2 * 4;
+    return fc_main_bytes(DT, J) + fc_tile_bytes(d) + FC_QB * 5 * 4;
 }
 
 // One pass over all centroids.  The wave with role (qb, h) = (wave % FC_QBW,
@@ -276,12 +282,85 @@ __device__ __forceinline__ void top_insert(float (&t)[J], float v) {
 // query blocks of FC_NH waves (48 queries, 12 waves) per workgroup: a 10k
 // batch is 209 workgroups, one per CU with none left over (with 32 queries,
 // 313 workgroups left 57 CUs running two and the launch waited for them).
+// Sequential dots (src/simd.rs:88-91 order, one rounding per product and per
+// sum) of G (query, centroid) pairs at once: the centroids stream from global
+// memory 32 floats per pair and step, all G pairs' loads in flight together,
+// and the G sums interleave.  Rows 16-byte aligned; d % 4 == 0 (else one
+// float at a time).
+template <int G>
+__device__ __forceinline__ void fc_seq_dots(const float* const (&qa)[G], const float* const (&cb)[G], int d,
+                                            float (&out)[G]) {
+#pragma unroll
+    for (int g = 0; g < G; g++) out[g] = 0.0f;
+    if (d & 3) {
+        for (int j = 0; j < d; j++)
+#pragma unroll
+            for (int g = 0; g < G; g++) out[g] = __fadd_rn(out[g], __fmul_rn(qa[g][j], cb[g][j]));
+        return;
+    }
+    int j0 = 0;
+    for (; j0 + 32 <= d; j0 += 32) {
+        float4 v[G][8];
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[g][i] = reinterpret_cast<const float4*>(cb[g] + j0)[i];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float4 a[G];
+#pragma unroll
+            for (int g = 0; g < G; g++) a[g] = reinterpret_cast<const float4*>(qa[g] + j0)[i];
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                out[g] = __fadd_rn(out[g], __fmul_rn(a[g].x, v[g][i].x));
+                out[g] = __fadd_rn(out[g], __fmul_rn(a[g].y, v[g][i].y));
+                out[g] = __fadd_rn(out[g], __fmul_rn(a[g].z, v[g][i].z));
+                out[g] = __fadd_rn(out[g], __fmul_rn(a[g].w, v[g][i].w));
+            }
+        }
+    }
+    for (; j0 < d; j0 += 4) {
+        float4 v[G], a[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            v[g] = reinterpret_cast<const float4*>(cb[g] + j0)[0];
+            a[g] = reinterpret_cast<const float4*>(qa[g] + j0)[0];
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            out[g] = __fadd_rn(out[g], __fmul_rn(a[g].x, v[g].x));
+            out[g] = __fadd_rn(out[g], __fmul_rn(a[g].y, v[g].y));
+            out[g] = __fadd_rn(out[g], __fmul_rn(a[g].z, v[g].z));
+            out[g] = __fadd_rn(out[g], __fmul_rn(a[g].w, v[g].w));
+        }
+    }
+}
+
+// The exact selection of one query from its scored candidate row (n <= 64 E
+// (fkey(1 - dot), list) pairs in LDS), one wave: the wave sorts the keys and
+// lanes write the Pe smallest lists in order.
+template <int E>
+__device__ __forceinline__ void fc_select_row(const uint32_t* cand, const uint32_t* score, uint32_t n, int Pe,
+                                              uint32_t* __restrict__ probe_row) {
+    const int lane = threadIdx.x & 63;
+    uint64_t kv[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const uint32_t t = e * 64 + lane;
+        kv[e] = t < n ? ((uint64_t)score[t] << 32) | cand[t] : ~0ull;
+    }
+    wave_sort_regs<E>(kv);
+#pragma unroll
+    for (int e = 0; e < E; e++)
+        if (e * 64 + lane < Pe) probe_row[e * 64 + lane] = (uint32_t)kv[e];
+}
+
 template <int DT, int J>
 __global__ __launch_bounds__(FC_THREADS) void coarse_fused_kernel(
     const float* __restrict__ Q, int nq, int d, const uint4* __restrict__ Cb, int L, float cmax,
-    int Pe, int IB, int normalize, float* __restrict__ qn_out, float* __restrict__ qnorm_out,
-    uint32_t* __restrict__ cand, uint32_t* __restrict__ cand_n, uint32_t* __restrict__ qbad,
-    unsigned int* __restrict__ nbad) {
+    int Pe, int P, int IB, int normalize, int ordered, float* __restrict__ qn_out, float* __restrict__ qnorm_out,
+    const float* __restrict__ C, uint32_t* __restrict__ probe, uint32_t* __restrict__ flag_list,
+    uint32_t* __restrict__ flag_count, uint32_t* __restrict__ qbad, unsigned int* __restrict__ nbad) {
     extern __shared__ __align__(16) char smem[];
     constexpr int CAP = 32 * J;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
@@ -289,9 +368,13 @@ __global__ __launch_bounds__(FC_THREADS) void coarse_fused_kernel(
     const int h = __builtin_amdgcn_readfirstlane(wave / FC_QBW);
     const int q0 = blockIdx.x * FC_QB;
     const int rows = min(FC_QB, nq - q0);
-    float* tile = reinterpret_cast<float*>(smem);
-    float* snorm = reinterpret_cast<float*>(smem + fc_main_bytes(d, DT, J));  // [FC_QB] norm, [FC_QB] bound
-    const int st = d + 1;
+    float* tile = reinterpret_cast<float*>(smem + fc_main_bytes(DT, J));
+    // [FC_QB] norm, [FC_QB] bound, [FC_QB] candidate count
+    float* snorm = reinterpret_cast<float*>(smem + fc_main_bytes(DT, J) + fc_tile_bytes(d));
+    uint32_t* scnt = reinterpret_cast<uint32_t*>(snorm + 2 * FC_QB);
+    float* smar = snorm + 3 * FC_QB;     // [FC_QB] score margin of the keys
+    uint32_t* sunc = scnt + 2 * FC_QB;   // [FC_QB] candidates left to rescore
+    const int st = fc_tile_stride(d);
 
     // ---- normalise (search.rs:55-62): sequential sum of squares per row.
     // A row holding a NaN or an infinity is searched as the zero vector,
@@ -336,7 +419,6 @@ __global__ __launch_bounds__(FC_THREADS) void coarse_fused_kernel(
         const float* xr = tile + (qb * 16 + c) * st;
         fc_split_rows<DT>([&](int j) { return xr[j]; }, d, g, ah, al);
     }
-    __syncthreads();  // the tile region becomes the pipeline buffers
 
     // ---- the pass: J largest packed keys per (lane, row 4 g + r).
     const uint32_t kmask = ~((1u << IB) - 1u);
@@ -365,15 +447,16 @@ __global__ __launch_bounds__(FC_THREADS) void coarse_fused_kernel(
     __syncthreads();
 
     // ---- rows FC_RPW h .. + FC_RPW - 1: threshold, overflow test and output.
-#pragma unroll
-    for (int rr = 0; rr < FC_RPW; rr++) {
-        const int r = FC_RPW * h + rr;
+    static_assert(FC_RPW == 1, "one row per lane group and wave");
+    {
+        const int r = h;
         const int row = qb * 16 + 4 * g + r;
         float lst[FC_NH][J];  // the FC_NH waves' lists of this (lane, row)
 #pragma unroll
         for (int w = 0; w < FC_NH; w++)
 #pragma unroll
             for (int j = 0; j < J; j++) lst[w][j] = mg[((((qb * FC_NH + w) * 4 + r) * J + j) << 6) + lane];
+        __syncthreads();  // every list read: the region becomes the candidate rows
         // T = the Pe-th largest of the lists' first FC_TR keys (a subset, so
         // Pe distinct lists still have keys >= T; T is below the full rank
         // only when a list holds more than FC_TR of the top Pe).
@@ -411,19 +494,147 @@ __global__ __launch_bounds__(FC_THREADS) void coarse_fused_kernel(
         const uint32_t total = __shfl(incl, (lane & 48) | 15, 64);
         // a list that may have dropped a member, or more candidates than a row holds
         const bool any_over = (__ballot(over) >> (16 * g) & 0xffffull) || total > (uint32_t)CAP;
-        if (row < rows) {
-            uint32_t* out = cand + (size_t)(q0 + row) * CAP + (incl - n);
-            if (!any_over) {
-                uint32_t o = 0;
+        // candidate lists [row][CAP] and their keys [row][CAP] beside them
+        uint32_t* out = reinterpret_cast<uint32_t*>(smem) + (size_t)row * CAP + (incl - n);
+        float* okey = reinterpret_cast<float*>(smem) + (size_t)FC_QB * CAP + (size_t)row * CAP + (incl - n);
+        if (!any_over) {
+            uint32_t o = 0;
 #pragma unroll
-                for (int w = 0; w < FC_NH; w++) {
+            for (int w = 0; w < FC_NH; w++) {
 #pragma unroll
-                    for (int j = 0; j < J; j++)
-                        if ((uint32_t)j < nw[w]) out[o + j] = 16u * (__float_as_uint(lst[w][j]) & ~kmask) + (uint32_t)c;
-                    o += nw[w];
+                for (int j = 0; j < J; j++)
+                    if ((uint32_t)j < nw[w]) {
+                        out[o + j] = 16u * (__float_as_uint(lst[w][j]) & ~kmask) + (uint32_t)c;
+                        okey[o + j] = lst[w][j];
+                    }
+                o += nw[w];
+            }
+        }
+        if (c == 0) {
+            scnt[row] = any_over ? (uint32_t)CAP + 1u : total;
+            // a key is within E of a + 2 and a within eps of the reference's
+            // dot: the reference score 1 - dot is within this of 3 - key
+            smar[row] = E + 1.25f * coarse_eps_bf16(d, qb_norm, cmax) + 4.0f * ub * u;
+        }
+    }
+    __syncthreads();
+
+    // ---- the selection (find_nearest_centroids, search.rs:1602-1617: the Pe
+    // smallest reference scores 1 - dot, ties to the lower list).  Wave w
+    // takes rows w, w + 12, ...  A candidate's reference score lies within
+    // the row's margin m of 3 - key, so one that at least n - Pe others
+    // surely trail is among the Pe, one that Pe others surely lead is not,
+    // and only the rest are rescored with the reference's sequential dot
+    // against the query as searched (distance.rs:104-109) and ranked by
+    // (score, list) for the remaining places.  The sure members are a prefix
+    // of the order by 3 - key (any candidate ahead of one trails at least as
+    // many), so each is written at its place in that order, and the rescored
+    // ones follow in rank order: nearest lists first, which tightens the
+    // scan's bound soonest.  With `ordered` every candidate is rescored and
+    // the Pe lists are written in rank order.
+    {
+        constexpr int RPW = FC_QB / (FC_THREADS / 64);  // rows per wave
+        uint32_t* lc = reinterpret_cast<uint32_t*>(smem);                    // ids [FC_QB][CAP]
+        uint32_t* sc = reinterpret_cast<uint32_t*>(smem) + (size_t)FC_QB * CAP;  // keys, then scores
+        uint32_t rn[RPW], rbeg[RPW + 1], rin[RPW];
+        rbeg[0] = 0;
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
+            const int row = wave + i * (FC_THREADS / 64);
+            uint32_t n = row < rows ? scnt[row] : 0u;
+            if (n > (uint32_t)CAP) {  // may be incomplete: the exact fallback
+                if (lane == 0) flag_list[atomicAdd(flag_count, 1u)] = (uint32_t)(q0 + row);
+                n = 0;
+            }
+            uint32_t in = 0, un = n;
+            if (!ordered && n > 0) {
+                uint32_t* ids = lc + (size_t)row * CAP;
+                const float* keys = reinterpret_cast<const float*>(sc) + (size_t)row * CAP;
+                const float m2 = 2.0f * smar[row];
+                uint32_t* pr = probe + (size_t)(q0 + row) * P;
+                un = 0;
+                // every lane reads its candidates before any slot is rewritten
+                constexpr int EM = (32 * J + 63) / 64;
+                uint32_t id[EM], st_[EM], ahead[EM];
+                float cs[EM];
+#pragma unroll
+                for (int e = 0; e < EM; e++) {
+                    const uint32_t t = e * 64 + lane;
+                    id[e] = t < n ? ids[t] : 0u;
+                    cs[e] = t < n ? 3.0f - keys[t] : 0.0f;
+                    st_[e] = 0u;
+                    ahead[e] = 0u;
+                }
+#pragma unroll
+                for (int e = 0; e < EM; e++) {
+                    if ((uint32_t)(e * 64) >= n) break;  // wave-uniform
+                    const uint32_t t = e * 64 + lane;
+                    uint32_t better = 0, worse = 0, a = 0;
+                    for (uint32_t j = 0; j < n; j++) {
+                        const float cj = 3.0f - keys[j];
+                        better += cj + m2 < cs[e] ? 1u : 0u;
+                        worse += cj - m2 > cs[e] ? 1u : 0u;
+                        a += cj < cs[e] || (cj == cs[e] && j < t) ? 1u : 0u;
+                    }
+                    ahead[e] = a;
+                    st_[e] = t >= n ? 0u : worse >= n - (uint32_t)Pe ? 1u : better >= (uint32_t)Pe ? 0u : 2u;
+                }
+#pragma unroll
+                for (int e = 0; e < EM; e++) {
+                    if ((uint32_t)(e * 64) >= n) break;
+                    const uint64_t bi = __ballot(st_[e] == 1u), bu = __ballot(st_[e] == 2u);
+                    const uint32_t ou = __builtin_amdgcn_mbcnt_hi((uint32_t)(bu >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bu, 0u));
+                    if (st_[e] == 1u && ahead[e] < (uint32_t)Pe) pr[ahead[e]] = id[e];
+                    if (st_[e] == 2u) ids[un + ou] = id[e];
+                    in += (uint32_t)__popcll(bi);
+                    un += (uint32_t)__popcll(bu);
                 }
             }
-            if (c == 0) cand_n[q0 + row] = any_over ? (uint32_t)CAP + 1u : total;
+            rn[i] = in < (uint32_t)Pe ? un : 0u;  // no place left: nothing to rescore
+            rin[i] = in;
+            rbeg[i + 1] = rbeg[i] + rn[i];
+        }
+        // the candidates left to rescore, numbered in row order: lane l takes
+        // numbers l, l + 64, ..., three at a time
+        const uint32_t tot = rbeg[RPW];
+        constexpr int G = 3;  // pairs per lane in flight (registers: 32 G floats)
+        for (uint32_t b0 = 0; b0 < tot; b0 += 64 * G) {
+            const float* qa[G];
+            const float* cb[G];
+            uint32_t at[G];  // LDS slot of each number (row * CAP + t), or ~0
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const uint32_t x = b0 + 64 * g + lane;
+                int ri = 0;
+#pragma unroll
+                for (int i = 1; i < RPW; i++) ri += x >= rbeg[i] ? 1 : 0;
+                const int row = wave + ri * (FC_THREADS / 64);
+                const bool ok = x < tot;
+                at[g] = ok ? (uint32_t)row * CAP + (x - rbeg[ri]) : ~0u;
+                qa[g] = tile + (ok ? row : 0) * st;
+                cb[g] = C + (size_t)(ok ? lc[at[g]] : 0u) * d;
+            }
+            float dot[G];
+            fc_seq_dots<G>(qa, cb, d, dot);
+#pragma unroll
+            for (int g = 0; g < G; g++)
+                if (at[g] != ~0u) sc[at[g]] = fkey(1.0f - dot[g]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
+            const int row = wave + i * (FC_THREADS / 64);
+            const uint32_t n = rn[i];
+            if (n == 0) continue;  // nothing left to rank, overflowed or past the batch
+            const uint32_t* cr = lc + (size_t)row * CAP;
+            const uint32_t* sr = sc + (size_t)row * CAP;
+            uint32_t* pr = probe + (size_t)(q0 + row) * P + rin[i];
+            const int need = Pe - (int)rin[i];
+            if (n <= 64) fc_select_row<1>(cr, sr, n, need, pr);
+            else if (n <= 128) fc_select_row<2>(cr, sr, n, need, pr);
+            else if (n <= 256) fc_select_row<4>(cr, sr, n, need, pr);
+            else fc_select_row<8>(cr, sr, n, need, pr);
         }
     }
 }
@@ -440,9 +651,10 @@ int coarse_fused_cap(int P) { return 32 * fc_keys(P); }
 bool coarse_fused_supported(int d, int P) { return d >= 1 && d <= 128 && P >= 1 && P <= 64; }
 
 template <int DT, int J>
-static void launch_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int Pe,
-                         int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
-                         hipStream_t s, uint32_t* qbad, unsigned int* nbad) {
+static void launch_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int Pe, int P,
+                         int normalize, int ordered, float* qn, float* qnorm, const float* C, uint32_t* probe,
+                         uint32_t* flag_list, uint32_t* flag_count, hipStream_t s, uint32_t* qbad,
+                         unsigned int* nbad) {
     const size_t lds = fc_lds_bytes(d, DT, J);
     // index bits: tiles ceil(L / 16) <= 2^IB
     int IB = 0;
@@ -450,102 +662,37 @@ static void launch_fused(const float* Q, int nq, int d, const uint4* Cb, int L, 
     auto k = coarse_fused_kernel<DT, J>;
     ensure_dyn_lds((const void*)k, lds);
     hipLaunchKernelGGL(k, dim3((nq + FC_QB - 1) / FC_QB), dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, cmax,
-                       Pe, IB, normalize, qn, qnorm, cand, cand_n, qbad, nbad);
+                       Pe, P, IB, normalize, ordered, qn, qnorm, C, probe, flag_list, flag_count, qbad, nbad);
 }
 
 template <int DT>
-static void launch_fused_j(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int Pe,
-                           int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
-                           hipStream_t s, uint32_t* qbad, unsigned int* nbad) {
+static void launch_fused_j(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int Pe, int P,
+                           int normalize, int ordered, float* qn, float* qnorm, const float* C, uint32_t* probe,
+                           uint32_t* flag_list, uint32_t* flag_count, hipStream_t s, uint32_t* qbad,
+                           unsigned int* nbad) {
     if (fc_keys(Pe) == FC_J_WIDE)
-        launch_fused<DT, FC_J_WIDE>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s, qbad, nbad);
+        launch_fused<DT, FC_J_WIDE>(Q, nq, d, Cb, L, cmax, Pe, P, normalize, ordered, qn, qnorm, C, probe, flag_list,
+                                    flag_count, s, qbad, nbad);
     else
-        launch_fused<DT, FC_J>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s, qbad, nbad);
+        launch_fused<DT, FC_J>(Q, nq, d, Cb, L, cmax, Pe, P, normalize, ordered, qn, qnorm, C, probe, flag_list,
+                               flag_count, s, qbad, nbad);
 }
 
 void launch_coarse_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int P,
-                         int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
-                         hipStream_t s, uint32_t* qbad, unsigned int* nbad) {
+                         int normalize, int ordered, float* qn, float* qnorm, const float* C, uint32_t* probe,
+                         uint32_t* flag_list, uint32_t* flag_count, hipStream_t s, uint32_t* qbad,
+                         unsigned int* nbad) {
     if (nq <= 0) return;
     const int Pe = P < L ? P : L;
+#define FC_L(DTV) launch_fused_j<DTV>(Q, nq, d, Cb, L, cmax, Pe, P, normalize, ordered, qn, qnorm, C, probe, flag_list, \
+                                      flag_count, s, qbad, nbad)
     switch ((d + 31) / 32) {
-        case 1: launch_fused_j<1>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s, qbad, nbad); break;
-        case 2: launch_fused_j<2>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s, qbad, nbad); break;
-        case 3: launch_fused_j<3>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s, qbad, nbad); break;
-        default: launch_fused_j<4>(Q, nq, d, Cb, L, cmax, Pe, normalize, qn, qnorm, cand, cand_n, s, qbad, nbad); break;
+        case 1: FC_L(1); break;
+        case 2: FC_L(2); break;
+        case 3: FC_L(3); break;
+        default: FC_L(4); break;
     }
-}
-
-// ---- exact ordering of the candidates, one wave per query ---------------
-#define TP_QD 512
-
-// E: keys per lane, candidate rows of up to 64 E.
-template <int E>
-__global__ __launch_bounds__(256) void coarse_topp_kernel(
-    const uint32_t* __restrict__ cand, const uint32_t* __restrict__ cand_n, int CAP,
-    const float* __restrict__ qn, const float* __restrict__ C, int nq, int L, int d, int P,
-    uint32_t* __restrict__ probe, uint32_t* __restrict__ flag_list, uint32_t* flag_count) {
-    __shared__ float wq[4][TP_QD];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int q = blockIdx.x * 4 + wave;
-    if (q >= nq) return;  // per wave: no block barriers below
-    const int Pe = P < L ? P : L;
-    const uint32_t n = cand_n[q];
-    if (n > (uint32_t)CAP) {
-        if (lane == 0) flag_list[atomicAdd(flag_count, 1u)] = (uint32_t)q;
-        return;
-    }
-    float* qs = wq[wave];
-    for (int j = lane; j < d; j += 64) qs[j] = qn[(size_t)q * d + j];
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    uint64_t kv[E];
-#pragma unroll
-    for (int e = 0; e < E; e++) {
-        const uint32_t t = e * 64 + lane;
-        kv[e] = ~0ull;
-        if (t < n) {
-            const uint32_t cidx = cand[(size_t)q * CAP + t];
-            kv[e] = cand_key(1.0f - seq_dot_stream(qs, C + (size_t)cidx * d, d), cidx);
-        }
-    }
-    if (n <= 64) {
-        uint64_t k1[1] = {kv[0]};
-        wave_sort_regs<1>(k1);
-        if (lane < Pe) probe[(size_t)q * P + lane] = (uint32_t)k1[0];
-    } else if (n <= 128) {
-        uint64_t k2[2] = {kv[0], kv[1]};
-        wave_sort_regs<2>(k2);
-#pragma unroll
-        for (int e = 0; e < 2; e++)
-            if (e * 64 + lane < Pe) probe[(size_t)q * P + e * 64 + lane] = (uint32_t)k2[e];
-    } else if (E == 4 || n <= 256) {
-        uint64_t k4[4] = {kv[0], kv[1], kv[2], kv[3]};
-        wave_sort_regs<4>(k4);
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            if (e * 64 + lane < Pe) probe[(size_t)q * P + e * 64 + lane] = (uint32_t)k4[e];
-    } else {
-        wave_sort_regs<E>(kv);
-#pragma unroll
-        for (int e = 0; e < E; e++)
-            if (e * 64 + lane < Pe) probe[(size_t)q * P + e * 64 + lane] = (uint32_t)kv[e];
-    }
-}
-
-void launch_coarse_topp(const uint32_t* cand, const uint32_t* cand_n, int P, const float* qn,
-                        const float* C, int nq, int L, int d, uint32_t* probe, uint32_t* flag_list,
-                        uint32_t* flag_count, hipStream_t s) {
-    if (nq <= 0) return;
-    const int Pe = P < L ? P : L;
-    const int cap = coarse_fused_cap(Pe);
-    static_assert(32 * FC_J <= 256 && 32 * FC_J_WIDE <= 512, "keys per lane");
-    if (cap <= 256)
-        hipLaunchKernelGGL(coarse_topp_kernel<4>, dim3((nq + 3) / 4), dim3(VGPU_BLOCK), 0, s, cand, cand_n, cap,
-                           qn, C, nq, L, d, P, probe, flag_list, flag_count);
-    else
-        hipLaunchKernelGGL(coarse_topp_kernel<8>, dim3((nq + 3) / 4), dim3(VGPU_BLOCK), 0, s, cand, cand_n, cap,
-                           qn, C, nq, L, d, P, probe, flag_list, flag_count);
+#undef FC_L
 }
 
 // ---- test entry: the bf16x3 dot products of the fused kernel ------------

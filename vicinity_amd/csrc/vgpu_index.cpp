@@ -201,10 +201,7 @@ void IvfpqIndex::assign_cosine(const float* d_x, const float* d_norms, size_t nx
                                hipStream_t s) {
     if (coarse_fused_supported((int)d, 1)) {
         const size_t chunk = std::min<size_t>(nx, (size_t)1 << 18);
-        const int cap = coarse_fused_cap(1);
         b_cb16.reserve(coarse_bf16_pack_chunks((int)k, (int)d));
-        b_cand.reserve(chunk * cap);
-        b_cand_n.reserve(chunk);
         b_cflag_list.reserve(chunk);
         b_cflag_count.reserve(1);
         b_overflow.reserve(1);
@@ -213,10 +210,8 @@ void IvfpqIndex::assign_cosine(const float* d_x, const float* d_norms, size_t nx
         for (size_t q0 = 0; q0 < nx; q0 += chunk) {
             const size_t nc = std::min(chunk, nx - q0);
             VGPU_HIP(hipMemsetAsync(b_cflag_count.p, 0, sizeof(uint32_t), s));
-            launch_coarse_fused(d_x + q0 * d, (int)nc, (int)d, b_cb16.p, (int)k, cmax, 1, 0, nullptr,
-                                nullptr, b_cand.p, b_cand_n.p, s);
-            launch_coarse_topp(b_cand.p, b_cand_n.p, 1, d_x + q0 * d, d_cent, (int)nc, (int)k, (int)d,
-                               d_assign + q0, b_cflag_list.p, b_cflag_count.p, s);
+            launch_coarse_fused(d_x + q0 * d, (int)nc, (int)d, b_cb16.p, (int)k, cmax, 1, 0, 0, nullptr,
+                                nullptr, d_cent, d_assign + q0, b_cflag_list.p, b_cflag_count.p, s);
             launch_coarse_exact_flagged(d_x + q0 * d, d_norms + q0, d_cent, (int)nc, (int)k, (int)d, 1,
                                         cmax, d_assign + q0, b_overflow.p, b_cflag_list.p,
                                         b_cflag_count.p, s);
@@ -733,8 +728,6 @@ size_t IvfpqIndex::ws_layout(const SearchPlan& pl, uint8_t* base, WsPtrs* out) c
     carve(w.qnorm, c);
     carve(w.qbad, c);
     if (pl.fused) {
-        carve(w.cand, c * (size_t)coarse_fused_cap((int)pl.P));
-        carve(w.cand_n, c);
         carve(w.fdots, (size_t)COARSE_FLAG_PAR * L);
     } else if (pl.P) {
         carve(w.dots, c * L);
@@ -758,7 +751,7 @@ size_t IvfpqIndex::ws_layout(const SearchPlan& pl, uint8_t* base, WsPtrs* out) c
 // Normalise (search.rs:55-62) and probe (search.rs:1602-1617) nq <= chunk
 // queries.  The fused path normalises in its prologue; P == 0 only normalises.
 void IvfpqIndex::coarse_probe(const float* d_q, size_t nq, size_t P, const SearchPlan& pl,
-                              const WsPtrs& w, hipStream_t s, hipEvent_t mid) {
+                              const WsPtrs& w, hipStream_t s, hipEvent_t mid, bool ordered) {
     unsigned int* overflow = reinterpret_cast<unsigned int*>(w.scal + kOverflowWord);
     uint32_t* cflag_count = reinterpret_cast<uint32_t*>(w.scal + kCFlagWord);
     unsigned int* nbad = reinterpret_cast<unsigned int*>(w.scal + kBadWord);
@@ -767,11 +760,9 @@ void IvfpqIndex::coarse_probe(const float* d_q, size_t nq, size_t P, const Searc
         return;
     }
     if (pl.fused) {
-        launch_coarse_fused(d_q, (int)nq, (int)d, dix.cb16, (int)L, dix.cmax, (int)P, 1, w.qn, w.qnorm,
-                            w.cand, w.cand_n, s, w.qbad, nbad);
+        launch_coarse_fused(d_q, (int)nq, (int)d, dix.cb16, (int)L, dix.cmax, (int)P, 1, ordered ? 1 : 0, w.qn, w.qnorm,
+                            d_centroids.p, w.probe, w.cflag_list, cflag_count, s, w.qbad, nbad);
         if (mid) VGPU_HIP(hipEventRecord(mid, s));
-        launch_coarse_topp(w.cand, w.cand_n, (int)P, w.qn, d_centroids.p, (int)nq, (int)L, (int)d, w.probe,
-                           w.cflag_list, cflag_count, s);
         launch_coarse_exact_flagged(w.qn, w.qnorm, d_centroids.p, (int)nq, (int)L, (int)d, (int)P, dix.cmax,
                                     w.probe, overflow, w.cflag_list, cflag_count, s, w.fdots,
                                     reinterpret_cast<uint32_t*>(w.scal + kFDoneWord));
@@ -1083,7 +1074,7 @@ vgpu_memory_report IvfpqIndex::memory_usage() {
                  d_rotation.bytes() + d_cb16.bytes() + d_offsets.bytes() + d_list_ids.bytes() +
                  d_doc_ids.bytes() + d_pack_off.bytes() + d_codes.bytes() + d_packed.bytes() +
                  d_tblocks.bytes() + d_tblk_off.bytes() + d_ecat.bytes() + b_cb16.bytes() + b_dots.bytes() +
-                 b_cand.bytes() + b_cand_n.bytes() + b_cflag_list.bytes() + b_cflag_count.bytes() +
+                 b_cflag_list.bytes() + b_cflag_count.bytes() +
                  b_overflow.bytes();
     {
         std::lock_guard<std::mutex> lk(pool_mu);
@@ -1165,7 +1156,7 @@ void IvfpqIndex::probe_host(const float* q, size_t nq, size_t nprobe, uint32_t* 
     for (size_t q0 = 0; q0 < nq; q0 += pl.chunk) {
         const size_t nc = std::min(pl.chunk, nq - q0);
         launch_zero_words(reinterpret_cast<unsigned long long*>(cflag_count), 1, s);
-        coarse_probe(ws->q.p + q0 * d, nc, P, pl, w, s, nullptr);
+        coarse_probe(ws->q.p + q0 * d, nc, P, pl, w, s, nullptr, true);
         VGPU_HIP(hipMemcpyAsync(lists + q0 * P, w.probe, nc * P * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
     }
     VGPU_HIP(hipGetLastError());
@@ -1274,7 +1265,7 @@ void IvfpqIndex::search_filtered(const float* q, size_t nq, size_t k, const int*
     for (size_t q0 = 0; q0 < nq; q0 += pl.chunk) {
         const size_t nc = std::min(pl.chunk, nq - q0);
         launch_zero_words(reinterpret_cast<unsigned long long*>(cflag_count), 1, s);
-        coarse_probe(ws->q.p + q0 * d, nc, P, pl, w, s, nullptr);
+        coarse_probe(ws->q.p + q0 * d, nc, P, pl, w, s, nullptr, true);
         VGPU_HIP(hipMemcpyAsync(ws->fqn.p + q0 * d, w.qn, nc * d * sizeof(float), hipMemcpyDeviceToDevice, s));
         if (P)
             VGPU_HIP(hipMemcpyAsync(probes.data() + q0 * P, w.probe, nc * P * sizeof(uint32_t),

@@ -114,23 +114,22 @@ void launch_coarse_select(float* D, const float* qn, const float* qnorm, const f
 
 // ---- fused coarse quantiser (k_coarse_fused.hip): d <= 128, 1 <= P <= 64.
 bool coarse_fused_supported(int d, int P);
-int coarse_fused_cap(int P);  // candidate row length for P probes
 // bf16 hi/lo copy of the centroids: L * ceil(d/32) * 8 uint4.
 // uint4 chunks of the packed centroids (L padded to whole pipeline stages).
 size_t coarse_bf16_pack_chunks(int L, int d);
 void launch_coarse_bf16_pack(const float* C, int L, int d, uint4* Cb, hipStream_t s);
 // Normalise the raw queries Q (or use them as given, normalize = 0) into qn /
-// qnorm, and write each query's candidate lists: cand[q][coarse_fused_cap(P)],
-// cand_n[q] (a count above the cap means overflow).  qbad / nbad as for
+// qnorm (either may be null), take each query's candidate lists by bf16x3
+// MFMA scores and write probe[q][0..P) from them by exact score (C: the
+// float32 centroids): the P lists of smallest reference score, in ascending
+// order when `ordered`, else in no set order (what a scan needs); a query
+// whose candidates may be incomplete is appended to flag_list (*flag_count
+// must be 0 on entry) for launch_coarse_exact_flagged.  qbad / nbad as for
 // launch_normalize.
 void launch_coarse_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int P,
-                         int normalize, float* qn, float* qnorm, uint32_t* cand, uint32_t* cand_n,
-                         hipStream_t s, uint32_t* qbad = nullptr, unsigned int* nbad = nullptr);
-// probe[q][0..P) from the candidates by exact score; overflowed queries are
-// appended to flag_list (*flag_count must be 0 on entry).
-void launch_coarse_topp(const uint32_t* cand, const uint32_t* cand_n, int P, const float* qn,
-                        const float* C, int nq, int L, int d, uint32_t* probe, uint32_t* flag_list,
-                        uint32_t* flag_count, hipStream_t s);
+                         int normalize, int ordered, float* qn, float* qnorm, const float* C, uint32_t* probe,
+                         uint32_t* flag_list, uint32_t* flag_count, hipStream_t s, uint32_t* qbad = nullptr,
+                         unsigned int* nbad = nullptr);
 // Exact probe selection for the flagged queries (dot products in LDS).
 // fdots (COARSE_FLAG_PAR rows of L floats) and fdone (COARSE_FLAG_PAR zeroed
 // counters) spread the first flagged queries' dot products over the grid;

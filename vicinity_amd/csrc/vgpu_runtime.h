@@ -92,7 +92,7 @@ struct SearchPlan {
 struct WsPtrs {
     float *qn = nullptr, *qnorm = nullptr, *dots = nullptr, *dist = nullptr, *dist2 = nullptr,
           *rres = nullptr, *t2 = nullptr;
-    uint32_t *cand = nullptr, *cand_n = nullptr, *cflag_list = nullptr, *probe = nullptr,
+    uint32_t *cflag_list = nullptr, *probe = nullptr,
              *vidx = nullptr, *vidx2 = nullptr, *qstat = nullptr, *flag_list = nullptr;
     uint32_t* qbad = nullptr;  // per chunk query: 1 when the query holds a NaN or an infinity
     float* fdots = nullptr;  // coarse fallback: dot-product rows of the first flagged queries
@@ -171,7 +171,7 @@ struct IvfpqIndex {
     // build workspace (k-means assignment), used under the exclusive lock
     DevBuf<uint4> b_cb16;
     DevBuf<float> b_dots;
-    DevBuf<uint32_t> b_cand, b_cand_n, b_cflag_list, b_cflag_count;
+    DevBuf<uint32_t> b_cflag_list, b_cflag_count;
     DevBuf<unsigned int> b_overflow;
 
     std::shared_mutex mu;
@@ -253,8 +253,11 @@ struct IvfpqIndex {
                     vgpu_search_stats* st, const uint32_t* d_given = nullptr);
     // Normalise and probe nq queries into w.qn / w.qnorm / w.probe (P may be 0).
     // mid (may be null) is recorded between the scoring and the selection.
+    // ordered: each row in ascending score order (the probe order of
+    // search.rs:1602-1617); otherwise the same lists in no set order, which
+    // is all a scan depends on.
     void coarse_probe(const float* d_q, size_t nq, size_t P, const SearchPlan& pl, const WsPtrs& w,
-                      hipStream_t s, hipEvent_t mid);
+                      hipStream_t s, hipEvent_t mid, bool ordered = false);
     void kmeans_cosine(const std::vector<float>& x, size_t nt, size_t k, uint64_t seed,
                        size_t max_iter, std::vector<float>& cent);
     void assign_cosine(const float* d_x, const float* d_norms, size_t nx, const float* d_cent,
