@@ -1,19 +1,22 @@
-// Coarse quantiser in two kernels, without a query x centroid score matrix:
+// Coarse quantiser without a query x centroid score matrix:
 //
-//   coarse_fused_kernel  48 queries per workgroup.  Normalises its queries
-//       (search.rs:55-62, writes qn), then makes one pass of bf16x3 MFMA dot
-//       products against every centroid: q.c ~ qh.ch + qh.cl + ql.ch with
-//       x = xh + xl + O(2^-16 |x|) split into bfloat16 halves.  Each (lane, query)
-//       keeps the J largest products of the lane's column class, packed with
-//       their list index into one float key; two waves share a query block and
-//       merge their lists.  The keys above a threshold derived from the P-th
-//       largest key and the error bounds are the query's candidates.
-//       At its end each wave takes four of the workgroup's queries in turn:
-//       it rescores their candidates with the reference's sequential dot
-//       (cosine_distance_normalized, src/distance.rs:104-109), sorts them by
-//       (score, list) and writes the P smallest in order
-//       (find_nearest_centroids, search.rs:1602-1617).  A query whose
-//       candidate set may be incomplete goes to launch_coarse_exact_flagged.
+//   coarse_fused_kernel  48 queries per workgroup of eight waves.  Normalises
+//       its queries (search.rs:55-62, writes qn), then every wave holds all 48
+//       queries as bf16 hi/lo MFMA operands and makes one pass of bf16x3 dot
+//       products, q.c ~ qh.ch + qh.cl + ql.ch with x = xh + xl + O(2^-16 |x|),
+//       over its eighth of the centroid tiles (16 centroids each), loading
+//       them straight from L2.  Each (wave, lane column, query) keeps the J
+//       largest products of its 1/128 of the lists, packed with their tile
+//       number into one float key.  The Pe-th largest of a query's 128 list
+//       maxima bounds its Pe-th largest key from below (those are Pe distinct
+//       lists), and the keys above that bound less the error margins are the
+//       query's candidates.  A candidate whose approximate score is surely
+//       among the Pe smallest is written at once, one surely outside is
+//       dropped, and the rest are rescored with the reference's sequential
+//       dot (cosine_distance_normalized, src/distance.rs:104-109) and ranked
+//       by (score, list) for the remaining places (find_nearest_centroids,
+//       search.rs:1602-1617).  A query whose candidate set may be incomplete
+//       goes to launch_coarse_exact_flagged.
 //
 // MFMA layout (v_mfma_f32_16x16x32_bf16, wave64): lane l holds row/column
 // l % 16 and eight consecutive k of group l / 16 for A and B; the result
@@ -31,15 +34,12 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // Native 128-bit vector (HIP's uint4 is a struct whose copies stay in memory).
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-#define FC_QBW 3               // query blocks (16 queries each) per workgroup
-#define FC_QB (16 * FC_QBW)    // queries per workgroup
-#define FC_NH 4                // waves per query block; each takes its own tiles of a stage
-#define FC_SUB 1               // 16-centroid tiles per wave and stage
-#define FC_ST (FC_NH * FC_SUB) // tiles per stage
-#define FC_TR 4                // keys per list that enter the rank (<= FC_J)
-#define FC_THREADS (FC_QBW * FC_NH * 64)  // threads per workgroup
-#define FC_RPW (4 / FC_NH)     // rows of a lane's four that each wave finishes
-static_assert(4 % FC_NH == 0, "wave roles");
+#define FC_QBW 3                  // query blocks (16 queries each) per workgroup
+#define FC_QB (16 * FC_QBW)       // queries per workgroup
+#define FC_NW 8                   // waves per workgroup; wave h takes tiles h, h + FC_NW, ...
+#define FC_THREADS (FC_NW * 64)
+#define FC_LISTS (FC_NW * 16)     // key lists per query: (wave, lane column)
+#define FC_RPW (FC_QB / FC_NW)    // queries each wave selects for
 
 // Round to nearest even bfloat16 (finite inputs).
 __device__ __forceinline__ uint32_t bf16_bits(float x) {
@@ -55,12 +55,12 @@ __device__ __forceinline__ void bf16_split(float x, uint32_t& hi, uint32_t& lo) 
     lo = bf16_bits(rem);
 }
 
-// Pack centroids into bf16 hi/lo chunks in the order the MFMA tiles read them
-// from LDS, so a pipeline stage is one contiguous copy: chunk
+// Pack centroids into bf16 hi/lo chunks in the order the MFMA lanes read
+// them, so each (tile, half, slice) is one contiguous 1 KB load: chunk
 // Cb[(((tile * 2 + h) * DT + t) * 4 + g) * 16 + c % 16], tile = c / 16, holds
 // the eight dimensions 32 t + 8 g .. + 7 of centroid c (h = 0: hi, 1: lo),
 // zero beyond d and for the padding centroids L .. Lp - 1 (Lp = L rounded up
-// to a whole pipeline stage, so stage loads need no bounds).
+// to an even number of rounds of FC_NW tiles, so tile loads need no bounds).
 __global__ void coarse_bf16_pack_kernel(const float* __restrict__ C, int L, int Lp, int d, int DT,
                                         uint4* __restrict__ Cb) {
     const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // (c, t, g)
@@ -79,7 +79,9 @@ __global__ void coarse_bf16_pack_kernel(const float* __restrict__ C, int L, int 
         make_uint4(l[0] | l[1] << 16, l[2] | l[3] << 16, l[4] | l[5] << 16, l[6] | l[7] << 16);
 }
 
-static int fc_padded_lists(int L) { return (L + FC_ST * 16 - 1) / (FC_ST * 16) * (FC_ST * 16); }
+// L padded to an even number of rounds of FC_NW tiles (every wave has the
+// same tiles, in pairs)
+static int fc_padded_lists(int L) { return (L + 2 * FC_LISTS - 1) / (2 * FC_LISTS) * (2 * FC_LISTS); }
 
 size_t coarse_bf16_pack_chunks(int L, int d) { return (size_t)fc_padded_lists(L) * ((d + 31) / 32) * 8; }
 
@@ -91,110 +93,110 @@ void launch_coarse_bf16_pack(const float* C, int L, int d, uint4* Cb, hipStream_
                        L, Lp, d, DT, Cb);
 }
 
-// Dynamic LDS of the fused kernel: one region used in turn by two pipeline
-// stages of (hi, lo) centroid chunks, the waves' key lists
-// [FC_QBW][FC_NH][4][J][64] and the candidate rows [FC_QB][32 J] with their
-// keys, later exact scores; then the query tile [FC_QB][fc_tile_stride(d)]
-// floats (kept for the exact rescoring); then [FC_QB] norms, bounds,
-// candidate counts, score margins and counts of candidates to rescore.
-__host__ __device__ inline size_t fc_stage_chunks(int DT) { return (size_t)FC_ST * DT * 4 * 16; }
-__host__ __device__ inline size_t fc_main_bytes(int DT, int J) {
-    const size_t stages = 2 * 2 * fc_stage_chunks(DT) * 16;
-    const size_t merge = (size_t)FC_QBW * FC_NH * 4 * J * 64 * 4;
-    const size_t rows = 2 * (size_t)FC_QB * 32 * J * 4;  // candidate lists and their scores
-    size_t m = stages > merge ? stages : merge;
-    return m > rows ? m : rows;
-}
-// query tile row stride: a multiple of four floats (16-byte aligned rows)
-__host__ __device__ inline int fc_tile_stride(int d) { return (d & ~3) + 4; }
+// Keys per list and candidates per query: a list holds 1/128 of the
+// centroids, so J of them cover the Pe nearest unless more than J of those
+// (and of the lists within the error margin) share one list: rare at these J
+// (about 1e-4 of queries at Pe = 32, J = 6).  Up to 320 candidates above 32
+// probes (a few hundred exactly tied lists still take the candidate path).
+__host__ __device__ constexpr int fc_cap(int J) { return J <= 6 ? 128 : 320; }
+
+// Dynamic LDS of the fused kernel: the query tile [FC_QB][fc_tile_stride(d)]
+// floats (kept for the exact rescoring); one region used first for the list
+// maxima [FC_QB][FC_LISTS] and the MFMA operands, then for the candidate
+// lists [FC_QB][CAP] and their keys [FC_QB][CAP] (later the lists to rescore
+// and their scores); then ten [FC_QB] arrays of per-query values.
+__host__ __device__ inline int fc_tile_stride(int d) { return (d & ~3) + 4; }  // 16-byte rows
 __host__ __device__ inline size_t fc_tile_bytes(int d) { return (size_t)FC_QB * fc_tile_stride(d) * 4; }
-__host__ __device__ inline size_t fc_lds_bytes(int d, int DT, int J) {
-    return fc_main_bytes(DT, J) + fc_tile_bytes(d) + FC_QB * 5 * 4;
+__host__ __device__ inline size_t fc_work_bytes(int J, int DT) {
+    // the maxima and, until the pass, the MFMA operands [FC_QBW][DT][2][64] after them
+    const size_t mx = (size_t)FC_QB * FC_LISTS * 4 + (size_t)FC_QBW * DT * 2 * 64 * 16;
+    const size_t cand = 2 * (size_t)FC_QB * fc_cap(J) * 4;
+    return mx > cand ? mx : cand;
+}
+__host__ __device__ inline size_t fc_lds_bytes(int d, int J, int DT) {
+    return fc_tile_bytes(d) + fc_work_bytes(J, DT) + 10 * FC_QB * 4;
 }
 
-// One pass over all centroids.  The wave with role (qb, h) = (wave % FC_QBW,
-// wave / FC_QBW) computes, for tiles h * FC_SUB .. + FC_SUB - 1 of every stage
-// of FC_ST 16-centroid tiles, acc = Q_qb . C_tile^T (16 x 16, bf16x3) and hands
-// it to `epi(acc, col_base, masked)`, col_base the tile's first centroid and
-// masked = the tile may reach past L (only in the last stage).  Stages are
-// double-buffered in LDS with one barrier each and loaded two stages ahead
-// into registers; a stage's epilogue runs after the next stage's MFMAs are
-// issued, so the two overlap.  All threads call this.
-template <int DT, typename Epi>
-__device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb_in, int L, const u32x4 (&ah)[DT],
-                                        const u32x4 (&al)[DT], u32x4* lds, Epi epi) {
-    const u32x4* Cb = reinterpret_cast<const u32x4*>(Cb_in);
-    constexpr int SC = FC_ST * DT * 4 * 16;  // chunks per stage and half
-    // chunks each thread copies per stage; with 768 threads the last slot is
-    // only partly used, so a thread copies slot i only when it exists
-    constexpr int PER = (2 * SC + FC_THREADS - 1) / FC_THREADS;
-    constexpr bool EXACT_SPLIT = (2 * SC) % FC_THREADS == 0;
-    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
-    const int h = __builtin_amdgcn_readfirstlane((tid >> 6) / FC_QBW);
-    const int nst = (L + FC_ST * 16 - 1) / (FC_ST * 16);
-    // A stage is 2 SC contiguous chunks of Cb (padded to whole stages), copied
-    // to LDS unchanged: slot i of thread tid is chunk i * FC_THREADS + tid.
-    // Buffer loads: per-lane offset in a VGPR, stage and slot offsets in
-    // SGPRs.  Only stages below nst are fetched.
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<u32x4*>(Cb), (short)0, nst * 2 * SC * 16, 0x00020000);
-    const uint32_t lofs = (uint32_t)tid * 16u;
-    // One register set: stage st + 1 is stored from it at the start of stage
-    // st and stage st + 2 loads into it, so a stage's loads have one stage
-    // to arrive (the other waves of the CU cover the rest).
-    u32x4 pa[PER];
-#define FC_FETCH(SET, ST)                                                              \
-    _Pragma("unroll") for (int i = 0; i < PER; i++) if (EXACT_SPLIT || i * FC_THREADS + tid < 2 * SC) SET[i] = __builtin_amdgcn_raw_buffer_load_b128( \
-        rsrc, lofs, (uint32_t)((ST) * 2 * SC * 16 + i * FC_THREADS * 16), 0);
-#define FC_STORE(SET, BUF)                                                             \
-    _Pragma("unroll") for (int i = 0; i < PER; i++) if (EXACT_SPLIT || i * FC_THREADS + tid < 2 * SC) lds[(size_t)(BUF) * 2 * SC + i * FC_THREADS + tid] = SET[i];
-    floatx4 prev[FC_SUB];
-    // Stage ST: everyone has finished stage ST - 1 (buffer (ST + 1) & 1) and
-    // stage ST's chunks are visible; SET holds stage ST + 1, then ST + 2.
-#define FC_STEP(ST, SET)                                                               \
-    {                                                                                  \
-        const int st_ = (ST);                                                          \
-        __syncthreads();                                                               \
-        if (st_ + 1 < nst) {                                                           \
-            FC_STORE(SET, (st_ + 1) & 1)                                               \
-            if (st_ + 2 < nst) { FC_FETCH(SET, st_ + 2) }                              \
-        }                                                                              \
-        const u32x4* b = lds + (size_t)(st_ & 1) * 2 * SC;                             \
-        floatx4 acc[FC_SUB];                                                           \
-        _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++) acc[sub] = floatx4{0.f, 0.f, 0.f, 0.f}; \
-        _Pragma("unroll") for (int t = 0; t < DT; t++) {                               \
-            bf16x8 bh[FC_SUB], bl[FC_SUB];                                             \
-            _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++) {                 \
-                const int o = (((h * FC_SUB + sub) * 2 * DT + t) * 4 + g) * 16 + c;    \
-                bh[sub] = __builtin_bit_cast(bf16x8, b[o]);                            \
-                bl[sub] = __builtin_bit_cast(bf16x8, b[o + DT * 64]);                  \
-            }                                                                          \
-            const bf16x8 a_h = __builtin_bit_cast(bf16x8, ah[t]);                      \
-            const bf16x8 a_l = __builtin_bit_cast(bf16x8, al[t]);                      \
-            _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++)                   \
-                acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bl[sub], acc[sub], 0, 0, 0); \
-            _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++)                   \
-                acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_l, bh[sub], acc[sub], 0, 0, 0); \
-            _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++)                   \
-                acc[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h, bh[sub], acc[sub], 0, 0, 0); \
-        }                                                                              \
-        if (st_ > 0) { /* stage st_ - 1 < nst - 1 is whole */                          \
-            _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++)                   \
-                epi(prev[sub], ((st_ - 1) * FC_ST + h * FC_SUB + sub) * 16, false);    \
-        }                                                                              \
-        _Pragma("unroll") for (int sub = 0; sub < FC_SUB; sub++) prev[sub] = acc[sub]; \
-    }
-    FC_FETCH(pa, 0)
-    FC_STORE(pa, 0)
-    if (nst > 1) { FC_FETCH(pa, 1) }
-    for (int st = 0; st < nst; st++) FC_STEP(st, pa)
-#undef FC_STEP
-    const bool masked = nst * FC_ST * 16 > L;
-#pragma unroll
-    for (int sub = 0; sub < FC_SUB; sub++) epi(prev[sub], ((nst - 1) * FC_ST + h * FC_SUB + sub) * 16, masked);
-#undef FC_FETCH
-#undef FC_STORE
+// One pass of bf16x3 products over every centroid.  Wave h takes the
+// 16-centroid tiles h, h + FC_NW, ... (nt of them; Cb is padded to whole rounds
+// of FC_NW tiles, so no load needs a bound) and, for its i-th tile, hands
+// acc[b] = Q_b . C_tile^T (16 x 16, query block b) to epi(acc, i).  The B
+// operands come straight from L2: each (tile, half, 32-dimension slice) is
+// 1 KB, one 16-byte chunk per lane, and slice t of the next tile is loaded as
+// soon as the current tile's products with slice t are issued (with DB,
+// slice t of the tile after next, into a second register set).
+template <int DT>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t fc_rsrc(const uint4* Cb, int nt) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4*>(Cb), (short)0, nt * FC_NW * 2 * DT * 1024,
+                                             0x00020000);
 }
+
+// slice T of tile TILE into register set S
+#define FC_LOAD(S, TILE, T)                                                                              \
+    bh[S][T] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, lofs, (uint32_t)((((TILE) * 2 + 0) * DT + (T)) * 1024), 0); \
+    bl[S][T] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, lofs, (uint32_t)((((TILE) * 2 + 1) * DT + (T)) * 1024), 0);
+
+// The loads of the wave's first tiles (two register sets with DB: tiles 0
+// and 1; else tile 0), issued before fc_pass so they travel while the
+// workgroup prepares its queries.
+template <int DT, bool DB>
+__device__ __forceinline__ void fc_prefetch(const uint4* __restrict__ Cb, int nt, int h, u32x4 (&bh)[DB ? 2 : 1][DT],
+                                            u32x4 (&bl)[DB ? 2 : 1][DT]) {
+    const __amdgpu_buffer_rsrc_t rsrc = fc_rsrc<DT>(Cb, nt);
+    const uint32_t lofs = (uint32_t)(threadIdx.x & 63) * 16u;
+#pragma unroll
+    for (int t = 0; t < DT; t++) { FC_LOAD(0, h, t) }
+    if (DB) {
+#pragma unroll
+        for (int t = 0; t < DT; t++) { FC_LOAD(DB ? 1 : 0, FC_NW * (nt > 1 ? 1 : 0) + h, t) }
+    }
+}
+
+template <int DT, bool DB, typename Epi>
+__device__ __forceinline__ void fc_pass(const uint4* __restrict__ Cb, int nt, int h, u32x4 (&bh)[DB ? 2 : 1][DT],
+                                        u32x4 (&bl)[DB ? 2 : 1][DT], const u32x4 (&ah)[FC_QBW][DT],
+                                        const u32x4 (&al)[FC_QBW][DT], Epi epi) {
+    const __amdgpu_buffer_rsrc_t rsrc = fc_rsrc<DT>(Cb, nt);
+    const uint32_t lofs = (uint32_t)(threadIdx.x & 63) * 16u;
+    // two register sets (DB): tile i + 2 loads into the set tile i used;
+    // else one, and tile i + 1 loads into it
+    constexpr int NS = DB ? 2 : 1, AHEAD = DB ? 2 : 1;
+    // tile i from set S; set S then loads tile i + AHEAD (the last ones
+    // reload themselves: in bounds, never used)
+#define FC_TILE(S, I, M)                                                                                 \
+    {                                                                                                    \
+        const int i_ = (I);                                                                              \
+        const int nxt = FC_NW * (i_ + AHEAD < nt ? i_ + AHEAD : i_) + h;                                 \
+        floatx4 acc[FC_QBW];                                                                             \
+        _Pragma("unroll") for (int b = 0; b < FC_QBW; b++) acc[b] = floatx4{0.f, 0.f, 0.f, 0.f};         \
+        _Pragma("unroll") for (int t = 0; t < DT; t++) {                                                 \
+            const bf16x8 b_h = __builtin_bit_cast(bf16x8, bh[S][t]);                                     \
+            const bf16x8 b_l = __builtin_bit_cast(bf16x8, bl[S][t]);                                     \
+            _Pragma("unroll") for (int b = 0; b < FC_QBW; b++)                                           \
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah[b][t]), b_l, acc[b], 0, 0, 0); \
+            _Pragma("unroll") for (int b = 0; b < FC_QBW; b++)                                           \
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al[b][t]), b_h, acc[b], 0, 0, 0); \
+            _Pragma("unroll") for (int b = 0; b < FC_QBW; b++)                                           \
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah[b][t]), b_h, acc[b], 0, 0, 0); \
+            FC_LOAD(S, nxt, t)                                                                           \
+        }                                                                                                \
+        epi(acc, i_, M);                                                                                 \
+    }
+    // only the last round may reach past L (M: the epilogue masks)
+    if (DB) {  // nt is even
+        for (int i = 0; i + 2 < nt; i += 2) {
+            FC_TILE(0, i, false)
+            FC_TILE(NS - 1, i + 1, false)
+        }
+        FC_TILE(0, nt - 2, true)
+        FC_TILE(NS - 1, nt - 1, true)
+    } else {
+        for (int i = 0; i + 1 < nt; i++) FC_TILE(0, i, false)
+        FC_TILE(0, nt - 1, true)
+    }
+#undef FC_TILE
+}
+#undef FC_LOAD
 
 // bf16 hi/lo A operands of one row, element j = x(j), dimensions
 // 32 t + 8 g .. + 7 for lane group g.
@@ -213,46 +215,6 @@ __device__ __forceinline__ void fc_split_rows(X x, int d, int g, u32x4 (&ah)[DT]
     }
 }
 
-// Rank k (0-based, ascending) among the 16 J keys held by the 16 lanes of
-// this lane's 16-lane group, J per lane (bitonic sort over element
-// e * 16 + lane % 16; strides below 16 stay inside the group).
-template <int J>
-__device__ __forceinline__ uint32_t group16_rank(uint32_t (&v)[J], int k) {
-    const int l16 = threadIdx.x & 15;
-#pragma unroll
-    for (int size = 2; size <= 16 * J; size <<= 1) {
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            if (stride >= 16) {
-                const int es = stride >> 4;
-#pragma unroll
-                for (int e = 0; e < J; e++) {
-                    const int f = e ^ es;
-                    if (f > e) {
-                        const bool asc = (((e << 4) | l16) & size) == 0;
-                        const uint32_t a = v[e], b = v[f];
-                        const bool sw = (a > b) == asc;
-                        v[e] = sw ? b : a;
-                        v[f] = sw ? a : b;
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < J; e++) {
-                    const uint32_t o = shfl_xor_u32(v[e], stride);
-                    const bool asc = (((e << 4) | l16) & size) == 0;
-                    const bool lower = (l16 & stride) == 0;
-                    v[e] = (lower == asc) ? (o < v[e] ? o : v[e]) : (o > v[e] ? o : v[e]);
-                }
-            }
-        }
-    }
-    uint32_t x = v[0];
-#pragma unroll
-    for (int e = 1; e < J; e++) x = (k >> 4) == e ? v[e] : x;
-    return __shfl(x, (threadIdx.x & 48) | (k & 15), 64);
-}
-
 // Insert v into the descending list t[0] >= .. >= t[J-1] (the J largest of
 // the list and v): t_i' = med3(t_{i-1}, t_i, v), updated from the bottom so
 // each step reads the old t_{i-1}; t_0' = max(t_0, v) as med3 against a
@@ -264,76 +226,113 @@ __device__ __forceinline__ void top_insert(float (&t)[J], float v) {
     t[0] = __builtin_amdgcn_fmed3f(t[0], v, 3.0e38f);
 }
 
-// One pass of bf16x3 products.  Every (wave, lane, row) keeps the J largest
-// keys k = (a + 2) with its low IB mantissa bits replaced by the tile index
-// (a = approximate q.c; the lane's column c = lane % 16 completes the list
-// index 16 tile + c); the FC_NH waves of a query block see disjoint tiles, so
-// a row has FC_NH x 16 sorted lists of J.  T = the Pe-th largest of the row's
-// keys bounds the Pe-th largest approximate dot from below (Pe distinct lists
-// have keys >= T, so approximate dots >= T - 2 - E, E the packing error).  Pe
-// lists then have exact scores within eps of those, so every list among the
-// Pe exact nearest has an approximate dot within 2 eps of T - 2 - E and a key
-// >= T - 2E - 2 eps (taken with a factor 1.25 and a few ulps to spare); those
-// keys form a prefix of each list.  (T is taken over the lists' first FC_TR
-// keys, Pe <= 16 FC_NH FC_TR.)  A list whose J-th key is itself above that
-// threshold may have dropped such a list, and a row holds at most CAP
-// candidates: the row is then marked overflowed (cand_n = CAP + 1).  After the
-// pass wave h finishes rows FC_RPW h .. + FC_RPW - 1 of each lane.  Three
-// query blocks of FC_NH waves (48 queries, 12 waves) per workgroup: a 10k
-// batch is 209 workgroups, one per CU with none left over (with 32 queries,
-// 313 workgroups left 57 CUs running two and the launch waited for them).
-// Sequential dots (src/simd.rs:88-91 order, one rounding per product and per
-// sum) of G (query, centroid) pairs at once: the centroids stream from global
-// memory 32 floats per pair and step, all G pairs' loads in flight together,
-// and the G sums interleave.  Rows 16-byte aligned; d % 4 == 0 (else one
-// float at a time).
-template <int G>
-__device__ __forceinline__ void fc_seq_dots(const float* const (&qa)[G], const float* const (&cb)[G], int d,
-                                            float (&out)[G]) {
+// Inclusive prefix sum over the 16 lanes of each DPP row (row_shr 1, 2, 4, 8;
+// lanes shifted in from outside the row add 0).
+__device__ __forceinline__ uint32_t prefix16(uint32_t x) {
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, false);
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, false);
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, false);
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, false);
+    return x;
+}
+
+// Element pos (wave-uniform) of a wave-held array, element e * 64 + lane in v[e].
+template <int E>
+__device__ __forceinline__ float wave_at(const float (&v)[E], int pos) {
+    float x = v[0];
 #pragma unroll
-    for (int g = 0; g < G; g++) out[g] = 0.0f;
+    for (int e = 1; e < E; e++) x = (pos >> 6) == e ? v[e] : x;
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), pos & 63));
+}
+
+// Classification of one query's n <= 64 E candidates (lists ids[t], keys
+// keys[t]), one wave.  Keys are sorted descending with the slot t in their
+// low SB bits (so each is truncated by under 2^SB ulps, ulp <= `ulp`); score
+// s = 3 - key is then within m = mar + 2^SB ulp of the reference score
+// 1 - dot, so with m2 = 2 m a candidate is surely among the Pe smallest when s + m2 is below
+// the score at position Pe (the n - Pe candidates from there on all trail it
+// for sure), and surely not when s - m2 is above the score at position Pe - 1.
+// The sure members are the first `in` positions and are written to pr at
+// their position (nearest first); the `un` uncertain ones follow them and are
+// copied to unc in that order.  `ordered`: every candidate is uncertain.
+// Reads all keys before it writes unc, which may overlay them.
+template <int E>
+__device__ __forceinline__ void fc_classify_sorted(const uint32_t (&sk)[E], const uint32_t* ids, uint32_t* unc,
+                                                   uint32_t* pr, uint32_t n, int Pe, float mar, float ulp,
+                                                   int ordered, uint32_t& in, uint32_t& un) {
+    const int lane = threadIdx.x & 63;
+    constexpr int SB = E == 1 ? 6 : E == 2 ? 7 : E == 4 ? 8 : 9;
+    constexpr uint32_t SM = (1u << SB) - 1u;
+    const float m2 = 2.0f * (mar + (float)(1u << SB) * ulp);
+    float cs[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) cs[e] = 3.0f - fkey_to_float(~(sk[e] | SM));
+    float lo_m = 3.0e38f, hi_m = 3.0e38f;  // every candidate a sure member (n <= Pe)
+    if (ordered) {
+        lo_m = -3.0e38f;  // none sure either way
+    } else if (n > (uint32_t)Pe) {
+        lo_m = wave_at<E>(cs, Pe) - m2;
+        hi_m = wave_at<E>(cs, Pe - 1) + m2;
+    }
+    in = 0;
+    un = 0;
+    uint32_t cls[E];  // 1 sure member, 2 to rescore, 0 out
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const uint32_t t = e * 64 + lane;
+        cls[e] = t >= n ? 0u : lo_m > cs[e] ? 1u : hi_m < cs[e] ? 0u : 2u;
+        in += (uint32_t)__popcll(__ballot(cls[e] == 1u));
+        un += (uint32_t)__popcll(__ballot(cls[e] == 2u));
+    }
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const uint32_t t = e * 64 + lane;
+        if (cls[e] == 1u) pr[t] = ids[sk[e] & SM];
+        if (cls[e] == 2u) unc[t - in] = ids[sk[e] & SM];
+    }
+}
+
+template <int E>
+__device__ __forceinline__ void fc_classify(const uint32_t* ids, const float* keys, uint32_t* unc, uint32_t* pr,
+                                            uint32_t n, int Pe, float mar, float ulp, int ordered, uint32_t& in,
+                                            uint32_t& un) {
+    const int lane = threadIdx.x & 63;
+    constexpr int SB = E == 1 ? 6 : E == 2 ? 7 : E == 4 ? 8 : 9;
+    constexpr uint32_t SM = (1u << SB) - 1u;
+    uint32_t sk[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const uint32_t t = e * 64 + lane;
+        sk[e] = t < n ? (~fkey(keys[t]) & ~SM) | t : ~0u;
+    }
+    wave_sort_u32<E>(sk);
+    fc_classify_sorted<E>(sk, ids, unc, pr, n, Pe, mar, ulp, ordered, in, un);
+}
+
+// One sequential dot (src/simd.rs:88-91 order) with the whole centroid row
+// (d <= 32 DT floats) loaded before the sum starts; q in LDS.  Rows 16-byte
+// aligned when d % 4 == 0 (else one float at a time).
+template <int DT>
+__device__ __forceinline__ float fc_seq_dot(const float* q, const float* __restrict__ cr, int d) {
+    float out = 0.0f;
     if (d & 3) {
-        for (int j = 0; j < d; j++)
-#pragma unroll
-            for (int g = 0; g < G; g++) out[g] = __fadd_rn(out[g], __fmul_rn(qa[g][j], cb[g][j]));
-        return;
+        for (int j = 0; j < d; j++) out = __fadd_rn(out, __fmul_rn(q[j], cr[j]));
+        return out;
     }
-    int j0 = 0;
-    for (; j0 + 32 <= d; j0 += 32) {
-        float4 v[G][8];
+    float4 v[8 * DT];
 #pragma unroll
-        for (int g = 0; g < G; g++)
+    for (int i = 0; i < 8 * DT; i++)
+        v[i] = 4 * i < d ? reinterpret_cast<const float4*>(cr)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int i = 0; i < 8; i++) v[g][i] = reinterpret_cast<const float4*>(cb[g] + j0)[i];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float4 a[G];
-#pragma unroll
-            for (int g = 0; g < G; g++) a[g] = reinterpret_cast<const float4*>(qa[g] + j0)[i];
-#pragma unroll
-            for (int g = 0; g < G; g++) {
-                out[g] = __fadd_rn(out[g], __fmul_rn(a[g].x, v[g][i].x));
-                out[g] = __fadd_rn(out[g], __fmul_rn(a[g].y, v[g][i].y));
-                out[g] = __fadd_rn(out[g], __fmul_rn(a[g].z, v[g][i].z));
-                out[g] = __fadd_rn(out[g], __fmul_rn(a[g].w, v[g][i].w));
-            }
-        }
+    for (int i = 0; i < 8 * DT; i++) {
+        // past d: 0 * 0 adds nothing
+        const float4 a = 4 * i < d ? reinterpret_cast<const float4*>(q)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        out = __fadd_rn(out, __fmul_rn(a.x, v[i].x));
+        out = __fadd_rn(out, __fmul_rn(a.y, v[i].y));
+        out = __fadd_rn(out, __fmul_rn(a.z, v[i].z));
+        out = __fadd_rn(out, __fmul_rn(a.w, v[i].w));
     }
-    for (; j0 < d; j0 += 4) {
-        float4 v[G], a[G];
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            v[g] = reinterpret_cast<const float4*>(cb[g] + j0)[0];
-            a[g] = reinterpret_cast<const float4*>(qa[g] + j0)[0];
-        }
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            out[g] = __fadd_rn(out[g], __fmul_rn(a[g].x, v[g].x));
-            out[g] = __fadd_rn(out[g], __fmul_rn(a[g].y, v[g].y));
-            out[g] = __fadd_rn(out[g], __fmul_rn(a[g].z, v[g].z));
-            out[g] = __fadd_rn(out[g], __fmul_rn(a[g].w, v[g].w));
-        }
-    }
+    return out;
 }
 
 // The exact selection of one query from its scored candidate row (n <= 64 E
@@ -357,311 +356,485 @@ __device__ __forceinline__ void fc_select_row(const uint32_t* cand, const uint32
 
 template <int DT, int J>
 __global__ __launch_bounds__(FC_THREADS) void coarse_fused_kernel(
-    const float* __restrict__ Q, int nq, int d, const uint4* __restrict__ Cb, int L, float cmax,
+    const float* __restrict__ Q, int nq, int d, const uint4* __restrict__ Cb, int L, int nt, float cmax,
     int Pe, int P, int IB, int normalize, int ordered, float* __restrict__ qn_out, float* __restrict__ qnorm_out,
     const float* __restrict__ C, uint32_t* __restrict__ probe, uint32_t* __restrict__ flag_list,
     uint32_t* __restrict__ flag_count, uint32_t* __restrict__ qbad, unsigned int* __restrict__ nbad) {
     extern __shared__ __align__(16) char smem[];
-    constexpr int CAP = 32 * J;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
-    const int qb = wave % FC_QBW;
-    const int h = __builtin_amdgcn_readfirstlane(wave / FC_QBW);
+    constexpr int CAP = fc_cap(J);
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    const int h = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q0 = blockIdx.x * FC_QB;
     const int rows = min(FC_QB, nq - q0);
-    float* tile = reinterpret_cast<float*>(smem + fc_main_bytes(DT, J));
-    // [FC_QB] norm, [FC_QB] bound, [FC_QB] candidate count
-    float* snorm = reinterpret_cast<float*>(smem + fc_main_bytes(DT, J) + fc_tile_bytes(d));
-    uint32_t* scnt = reinterpret_cast<uint32_t*>(snorm + 2 * FC_QB);
-    float* smar = snorm + 3 * FC_QB;     // [FC_QB] score margin of the keys
-    uint32_t* sunc = scnt + 2 * FC_QB;   // [FC_QB] candidates left to rescore
     const int st = fc_tile_stride(d);
+    float* tile = reinterpret_cast<float*>(smem);
+    char* work = smem + fc_tile_bytes(d);
+    float* mx = reinterpret_cast<float*>(work);                   // [FC_QB][FC_LISTS] list maxima
+    uint32_t* cid = reinterpret_cast<uint32_t*>(work);           // [FC_QB][CAP] candidate lists
+    float* ckey = reinterpret_cast<float*>(work) + FC_QB * CAP;  // [FC_QB][CAP] their keys
+    float* rv = reinterpret_cast<float*>(work + fc_work_bytes(J, DT));
+    float* snorm = rv;               // the norm divided by (0: rows used as given)
+    float* sbnd = rv + FC_QB;        // bound on ||q||
+    float* skthr = rv + 2 * FC_QB;   // candidate threshold on the keys
+    float* smar = rv + 3 * FC_QB;    // margin of the candidates' scores
+    float* sulp = rv + 7 * FC_QB;    // bound on the ulp of the keys
+    uint32_t* sin = reinterpret_cast<uint32_t*>(rv + 8 * FC_QB);  // probes written: the sure members
+    uint32_t* sun = reinterpret_cast<uint32_t*>(rv + 9 * FC_QB);  // lists left to rescore
+    uint32_t* scnt = reinterpret_cast<uint32_t*>(rv + 4 * FC_QB);   // candidates
+    uint32_t* sbad = reinterpret_cast<uint32_t*>(rv + 5 * FC_QB);   // holds a NaN or an infinity
+    uint32_t* sover = reinterpret_cast<uint32_t*>(rv + 6 * FC_QB);  // candidate set may be incomplete
 
-    // ---- normalise (search.rs:55-62): sequential sum of squares per row.
-    // A row holding a NaN or an infinity is searched as the zero vector,
-    // marked in qbad and counted in *nbad (its result row becomes padding).
+    constexpr bool DB = !(DT == 4 && J == 8);  // a second register set fits
+    u32x4 bh[DB ? 2 : 1][DT], bl[DB ? 2 : 1][DT];
+    fc_prefetch<DT, DB>(Cb, nt, h, bh, bl);
+
+    // ---- normalise (search.rs:55-62): sequential sum of squares per row.  A
+    // row holding a NaN or an infinity is searched as the zero vector, marked
+    // in qbad and counted in *nbad (its result row becomes padding).
+    if (tid < FC_QB) {
+        scnt[tid] = 0u;
+        sbad[tid] = 0u;
+        sover[tid] = 0u;
+    }
+    __syncthreads();
     const float* src = Q + (size_t)q0 * d;
-    for (int e = tid; e < FC_QB * d; e += FC_THREADS) {
-        const int r = e / d;
-        tile[r * st + e % d] = r < rows ? src[e] : 0.0f;
+    // thread -> (rows r0, r0 + rstep, ..., one column): one division per thread
+    const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 &&
+                     (!normalize || (reinterpret_cast<uintptr_t>(qn_out) & 15) == 0);
+    const int wrow = vec ? d >> 2 : d;  // items per row
+    const int rstep = FC_THREADS / wrow;
+    const int r0 = tid / wrow, jc = tid - r0 * wrow;
+    const uint32_t ex = 0x7f800000u;
+    if (r0 < rstep) {
+        if (vec && rstep * 3 >= FC_QB) {  // d > 64: every load in flight at once
+            float4 v[3];
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                const int r = r0 + k * rstep;
+                v[k] = r < rows ? reinterpret_cast<const float4*>(src + (size_t)r * d)[jc]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                const int r = r0 + k * rstep;
+                if (r < FC_QB) {
+                    if ((__float_as_uint(v[k].x) & ex) == ex || (__float_as_uint(v[k].y) & ex) == ex ||
+                        (__float_as_uint(v[k].z) & ex) == ex || (__float_as_uint(v[k].w) & ex) == ex)
+                        sbad[r] = 1u;
+                    *reinterpret_cast<float4*>(tile + r * st + 4 * jc) = v[k];
+                }
+            }
+        } else if (vec) {
+            for (int r = r0; r < FC_QB; r += rstep) {
+                const float4 v = r < rows ? reinterpret_cast<const float4*>(src + (size_t)r * d)[jc]
+                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+                if ((__float_as_uint(v.x) & ex) == ex || (__float_as_uint(v.y) & ex) == ex ||
+                    (__float_as_uint(v.z) & ex) == ex || (__float_as_uint(v.w) & ex) == ex)
+                    sbad[r] = 1u;
+                *reinterpret_cast<float4*>(tile + r * st + 4 * jc) = v;
+            }
+        } else {
+            for (int r = r0; r < FC_QB; r += rstep) {
+                const float v = r < rows ? src[(size_t)r * d + jc] : 0.0f;
+                if ((__float_as_uint(v) & ex) == ex) sbad[r] = 1u;
+                tile[r * st + jc] = v;
+            }
+        }
     }
     __syncthreads();
     if (tid < FC_QB) {
-        float* xr = tile + tid * st;
-        if (row_nonfinite(xr, d)) {
-            for (int j = 0; j < d; j++) xr[j] = 0.0f;
-            if (nbad) atomicAdd(nbad, 1u);
-            if (qbad && tid < rows) qbad[q0 + tid] = 1u;
-        } else if (qbad && tid < rows) {
-            qbad[q0 + tid] = 0u;
-        }
+        const float* xr = tile + tid * st;
+        const bool bad = sbad[tid] != 0u;
         float s = 0.0f;
-        for (int j = 0; j < d; j++) s = __fadd_rn(s, __fmul_rn(xr[j], xr[j]));
+        if (!bad) {
+            if ((d & 3) == 0) {
+                // all of the row's loads first, then the sequential sum
+                // (the zeros past d add nothing)
+#pragma unroll
+                for (int t = 0; t < DT; t++) {
+                    float4 v[8];
+#pragma unroll
+                    for (int i = 0; i < 8; i++)
+                        v[i] = 32 * t + 4 * i < d ? *reinterpret_cast<const float4*>(xr + 32 * t + 4 * i)
+                                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        s = __fadd_rn(s, __fmul_rn(v[i].x, v[i].x));
+                        s = __fadd_rn(s, __fmul_rn(v[i].y, v[i].y));
+                        s = __fadd_rn(s, __fmul_rn(v[i].z, v[i].z));
+                        s = __fadd_rn(s, __fmul_rn(v[i].w, v[i].w));
+                    }
+                }
+            } else {
+                for (int j = 0; j < d; j++) s = __fadd_rn(s, __fmul_rn(xr[j], xr[j]));
+            }
+        }
+        if (bad && nbad) atomicAdd(nbad, 1u);
+        if (qbad && tid < rows) qbad[q0 + tid] = bad ? 1u : 0u;
         const float nrm = sqrtf(s);
         // without normalisation the rows are used as given; the bound is ||x||
         snorm[tid] = normalize ? nrm : 0.0f;
-        snorm[FC_QB + tid] = normalize && nrm > 1e-10f ? 1.0001f : nrm * 1.0001f + 1e-30f;
-        if (tid < rows && qnorm_out) qnorm_out[q0 + tid] = snorm[FC_QB + tid];
+        sbnd[tid] = normalize && nrm > 1e-10f ? 1.0001f : nrm * 1.0001f + 1e-30f;
+        if (tid < rows && qnorm_out) qnorm_out[q0 + tid] = sbnd[tid];
     }
     __syncthreads();
-    if (normalize) {
-        for (int e = tid; e < FC_QB * d; e += FC_THREADS) {
-            const int r = e / d, j = e % d;
-            const float nrm = snorm[r];
-            const float v = tile[r * st + j];
-            const float x = nrm > 1e-10f ? v / nrm : v;
-            tile[r * st + j] = x;
-            if (r < rows) qn_out[(size_t)(q0 + r) * d + j] = x;
-        }
-        __syncthreads();
-    }
-    u32x4 ah[DT], al[DT];
+    // divide by the norm (zeroing the marked rows), write qn, and split each
+    // 8-dimension group into its bf16 hi/lo MFMA operands, kept in LDS past
+    // the maxima: As[((b * DT + t) * 2 + half) * 64 + 16 g + c] holds
+    // dimensions 32 t + 8 g .. + 7 of query 16 b + c
+    u32x4* As = reinterpret_cast<u32x4*>(work + (size_t)FC_QB * FC_LISTS * 4);
     {
-        const float* xr = tile + (qb * 16 + c) * st;
-        fc_split_rows<DT>([&](int j) { return xr[j]; }, d, g, ah, al);
-    }
-
-    // ---- the pass: J largest packed keys per (lane, row 4 g + r).
-    const uint32_t kmask = ~((1u << IB) - 1u);
-    float top[4][J];
+        constexpr int G8 = 4 * DT;  // 8-dimension groups per row
+        const bool v8 = (d & 7) == 0 && (!normalize || (reinterpret_cast<uintptr_t>(qn_out) & 15) == 0);
+        for (int k = tid; k < FC_QB * G8; k += FC_THREADS) {
+            const int r = k / G8, g8 = k - r * G8, j0 = 8 * g8;
+            const float nrm = snorm[r];
+            const bool zero = sbad[r] != 0u, div = nrm > 1e-10f;
+            float* tr = tile + r * st + j0;
+            float x[8];
+            if (v8) {
+                const float4 lo = j0 < d ? reinterpret_cast<const float4*>(tr)[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float4 hi = j0 < d ? reinterpret_cast<const float4*>(tr)[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+                x[0] = lo.x; x[1] = lo.y; x[2] = lo.z; x[3] = lo.w;
+                x[4] = hi.x; x[5] = hi.y; x[6] = hi.z; x[7] = hi.w;
+            } else {
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+                for (int i = 0; i < 8; i++) x[i] = j0 + i < d ? tr[i] : 0.0f;
+            }
 #pragma unroll
-        for (int j = 0; j < J; j++) top[r][j] = -3.0e38f;  // below every key
-    fc_pass<DT>(Cb, L, ah, al, reinterpret_cast<u32x4*>(smem), [&](const floatx4& acc, int cb, bool masked) {
-        const uint32_t ti = (uint32_t)cb >> 4;
-        const bool valid = !masked || cb + c < L;
+            for (int i = 0; i < 8; i++) x[i] = zero ? 0.0f : div ? x[i] / nrm : x[i];
+            if (v8) {
+                if (j0 < d) {
+                    const float4 lo = make_float4(x[0], x[1], x[2], x[3]), hi = make_float4(x[4], x[5], x[6], x[7]);
+                    reinterpret_cast<float4*>(tr)[0] = lo;
+                    reinterpret_cast<float4*>(tr)[1] = hi;
+                    if (normalize && r < rows) {
+                        float4* qo = reinterpret_cast<float4*>(qn_out + (size_t)(q0 + r) * d + j0);
+                        qo[0] = lo;
+                        qo[1] = hi;
+                    }
+                }
+            } else {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float k = __uint_as_float((__float_as_uint(acc[r] + 2.0f) & kmask) | ti);
-            top_insert<J>(top[r], valid ? k : -3.0e38f);
+                for (int i = 0; i < 8; i++)
+                    if (j0 + i < d) {
+                        tr[i] = x[i];
+                        if (normalize && r < rows) qn_out[(size_t)(q0 + r) * d + j0 + i] = x[i];
+                    }
+            }
+            uint32_t hb[8], lb[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) bf16_split(x[i], hb[i], lb[i]);
+            const int slot = ((r >> 4) * DT + (g8 >> 2)) * 2 * 64 + 16 * (g8 & 3) + (r & 15);
+            As[slot] = u32x4{hb[0] | hb[1] << 16, hb[2] | hb[3] << 16, hb[4] | hb[5] << 16, hb[6] | hb[7] << 16};
+            As[slot + 64] = u32x4{lb[0] | lb[1] << 16, lb[2] | lb[3] << 16, lb[4] | lb[5] << 16, lb[6] | lb[7] << 16};
         }
+    }
+    __syncthreads();
+    u32x4 ah[FC_QBW][DT], al[FC_QBW][DT];
+#pragma unroll
+    for (int b = 0; b < FC_QBW; b++)
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+            ah[b][t] = As[(b * DT + t) * 2 * 64 + lane];
+            al[b][t] = As[(b * DT + t) * 2 * 64 + 64 + lane];
+        }
+
+    // ---- the pass: every (lane, query 16 b + 4 g + r) keeps the J largest
+    // keys k = (a + 2) with the low IB mantissa bits replaced by the wave's
+    // tile number i (a = approximate q.c; list = 16 (FC_NW i + h) + c).
+    const uint32_t kmask = ~((1u << IB) - 1u);
+    float top[FC_QBW][4][J];
+#pragma unroll
+    for (int b = 0; b < FC_QBW; b++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int j = 0; j < J; j++) top[b][r][j] = -3.0e38f;  // below every key
+    fc_pass<DT, DB>(Cb, nt, h, bh, bl, ah, al, [&](const floatx4 (&acc)[FC_QBW], int i, bool masked) {
+        const bool valid = !masked || (FC_NW * i + h) * 16 + c < L;
+        // the tile number in a vector register, so mask and insert are one
+        // v_and_or_b32 (a single scalar operand per instruction)
+        const uint32_t ti = (uint32_t)__builtin_amdgcn_update_dpp(0, i, 0xE4, 0xF, 0xF, false);
+#pragma unroll
+        for (int b = 0; b < FC_QBW; b++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float k = __uint_as_float((__float_as_uint(acc[b][r] + 2.0f) & kmask) | ti);
+                top_insert<J>(top[b][r], valid ? k : -3.0e38f);
+            }
     });
 
-    // ---- exchange: every wave's lists to LDS [qb][h][r][j][lane].
-    __syncthreads();  // the pipeline buffers become the exchange area
-    float* mg = reinterpret_cast<float*>(smem);
+    // ---- threshold: the Pe-th largest of a query's 128 list maxima, T,
+    // bounds its Pe-th largest key from below.  Keys are within E of a + 2 and
+    // a within eps of the reference's dot, so every list among the Pe exact
+    // nearest has a key >= T - 2E - 2 eps (taken with a factor 1.25 and a few
+    // ulps to spare); in each list those keys are a prefix.
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+    for (int b = 0; b < FC_QBW; b++)
 #pragma unroll
-        for (int j = 0; j < J; j++) mg[((((qb * FC_NH + h) * 4 + r) * J + j) << 6) + lane] = top[r][j];
+        for (int r = 0; r < 4; r++) mx[(b * 16 + 4 * g + r) * FC_LISTS + h * 16 + c] = top[b][r][0];
     __syncthreads();
-
-    // ---- rows FC_RPW h .. + FC_RPW - 1: threshold, overflow test and output.
-    static_assert(FC_RPW == 1, "one row per lane group and wave");
+    const float u = 5.9604645e-08f;
     {
-        const int r = h;
-        const int row = qb * 16 + 4 * g + r;
-        float lst[FC_NH][J];  // the FC_NH waves' lists of this (lane, row)
+        // radix selection, all of the wave's queries at once: the largest t
+        // with at least Pe maxima >= t is the Pe-th largest; stopped at bit
+        // 8, t is below it by under 256 units of the key order (ulps), still
+        // a bound with Pe maxima at or above it
+        uint32_t v0[FC_RPW], v1[FC_RPW], res[FC_RPW];
 #pragma unroll
-        for (int w = 0; w < FC_NH; w++)
-#pragma unroll
-            for (int j = 0; j < J; j++) lst[w][j] = mg[((((qb * FC_NH + w) * 4 + r) * J + j) << 6) + lane];
-        __syncthreads();  // every list read: the region becomes the candidate rows
-        // T = the Pe-th largest of the lists' first FC_TR keys (a subset, so
-        // Pe distinct lists still have keys >= T; T is below the full rank
-        // only when a list holds more than FC_TR of the top Pe).
-        uint32_t kv[FC_NH * FC_TR];
-#pragma unroll
-        for (int w = 0; w < FC_NH; w++)
-#pragma unroll
-            for (int j = 0; j < FC_TR; j++) kv[w * FC_TR + j] = fkey(lst[w][j]);
-        const float T = fkey_to_float(group16_rank<FC_NH * FC_TR>(kv, 16 * FC_NH * FC_TR - Pe));
-        const float qb_norm = snorm[FC_QB + row];
-        const float qc = qb_norm * cmax;
-        const float u = 5.9604645e-08f;
-        // packing: < 2^IB ulps of a + 2 plus half an ulp of its rounding; every
-        // |a + 2| <= qc + 2 < ub (a power of two) has ulp <= ub u
-        const float ub = __uint_as_float((__float_as_uint(qc + 2.0f) & 0x7f800000u) + 0x00800000u);
-        const float E = ((float)(1u << IB) + 0.5f) * ub * u;
-        const float kthr = T - (2.0f * E + 2.5f * coarse_eps_bf16(d, qb_norm, cmax) + 8.0f * ub * u);
-        uint32_t nw[FC_NH], n = 0;
-        bool over = false;
-#pragma unroll
-        for (int w = 0; w < FC_NH; w++) {
-            nw[w] = 0;
-#pragma unroll
-            for (int j = 0; j < J; j++) nw[w] += lst[w][j] >= kthr ? 1u : 0u;
-            n += nw[w];
-            over = over || lst[w][J - 1] >= kthr;
+        for (int i = 0; i < FC_RPW; i++) {
+            const int row = h + FC_NW * i;
+            const bool act = row < rows;
+            v0[i] = act ? fkey(mx[row * FC_LISTS + lane]) : 0u;
+            v1[i] = act ? fkey(mx[row * FC_LISTS + 64 + lane]) : 0u;
+            res[i] = 0u;
         }
-        // exclusive prefix of n over the 16 lanes of the group
-        uint32_t incl = n;
+        if (Pe <= 32) {
+            // the maxima of list pairs (l, l + 64): still Pe distinct lists
+            // at or above t, one comparison per bit
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            const uint32_t x = __shfl_up(incl, o, 16);
-            if (c >= o) incl += x;
-        }
-        const uint32_t total = __shfl(incl, (lane & 48) | 15, 64);
-        // a list that may have dropped a member, or more candidates than a row holds
-        const bool any_over = (__ballot(over) >> (16 * g) & 0xffffull) || total > (uint32_t)CAP;
-        // candidate lists [row][CAP] and their keys [row][CAP] beside them
-        uint32_t* out = reinterpret_cast<uint32_t*>(smem) + (size_t)row * CAP + (incl - n);
-        float* okey = reinterpret_cast<float*>(smem) + (size_t)FC_QB * CAP + (size_t)row * CAP + (incl - n);
-        if (!any_over) {
-            uint32_t o = 0;
+            for (int i = 0; i < FC_RPW; i++) v0[i] = max(v0[i], v1[i]);
+            for (int bit = 31; bit >= 8; bit--) {
 #pragma unroll
-            for (int w = 0; w < FC_NH; w++) {
+                for (int i = 0; i < FC_RPW; i++) {
+                    const uint32_t cand = res[i] | (1u << bit);
+                    res[i] = (uint32_t)__popcll(__ballot(v0[i] >= cand)) >= (uint32_t)Pe ? cand : res[i];
+                }
+            }
+        } else {
+            for (int bit = 31; bit >= 8; bit--) {
 #pragma unroll
-                for (int j = 0; j < J; j++)
-                    if ((uint32_t)j < nw[w]) {
-                        out[o + j] = 16u * (__float_as_uint(lst[w][j]) & ~kmask) + (uint32_t)c;
-                        okey[o + j] = lst[w][j];
-                    }
-                o += nw[w];
+                for (int i = 0; i < FC_RPW; i++) {
+                    const uint32_t cand = res[i] | (1u << bit);
+                    const uint32_t cnt =
+                        (uint32_t)__popcll(__ballot(v0[i] >= cand)) + (uint32_t)__popcll(__ballot(v1[i] >= cand));
+                    res[i] = cnt >= (uint32_t)Pe ? cand : res[i];
+                }
             }
         }
-        if (c == 0) {
-            scnt[row] = any_over ? (uint32_t)CAP + 1u : total;
-            // a key is within E of a + 2 and a within eps of the reference's
-            // dot: the reference score 1 - dot is within this of 3 - key
-            smar[row] = E + 1.25f * coarse_eps_bf16(d, qb_norm, cmax) + 4.0f * ub * u;
+        if (lane < FC_RPW) {
+            uint32_t tk = res[0];
+#pragma unroll
+            for (int i = 1; i < FC_RPW; i++) tk = lane == i ? res[i] : tk;
+            const int row = h + FC_NW * lane;
+            if (row < rows) {
+                const float T = fkey_to_float(tk);
+                const float qb_norm = sbnd[row];
+                const float qc = qb_norm * cmax;
+                // packing: < 2^IB ulps of a + 2 plus half an ulp of its
+                // rounding; every |a + 2| <= qc + 2 < ub (a power of two) has
+                // ulp <= ub u
+                const float ub = __uint_as_float((__float_as_uint(qc + 2.0f) & 0x7f800000u) + 0x00800000u);
+                const float E = ((float)(1u << IB) + 0.5f) * ub * u;
+                const float eps = coarse_eps_bf16(d, qb_norm, cmax);
+                skthr[row] = T - (2.0f * E + 2.5f * eps + 8.0f * ub * u);
+                // the reference score 1 - dot is within this of 3 - key
+                smar[row] = E + 1.25f * eps + 4.0f * ub * u;
+                sulp[row] = ub * u;
+            }
         }
     }
     __syncthreads();
 
-    // ---- the selection (find_nearest_centroids, search.rs:1602-1617: the Pe
-    // smallest reference scores 1 - dot, ties to the lower list).  Wave w
-    // takes rows w, w + 12, ...  A candidate's reference score lies within
-    // the row's margin m of 3 - key, so one that at least n - Pe others
-    // surely trail is among the Pe, one that Pe others surely lead is not,
-    // and only the rest are rescored with the reference's sequential dot
-    // against the query as searched (distance.rs:104-109) and ranked by
-    // (score, list) for the remaining places.  The sure members are a prefix
-    // of the order by 3 - key (any candidate ahead of one trails at least as
-    // many), so each is written at its place in that order, and the rescored
-    // ones follow in rank order: nearest lists first, which tightens the
-    // scan's bound soonest.  With `ordered` every candidate is rescored and
-    // the Pe lists are written in rank order.
+    // ---- candidates: the keys >= the threshold, to LDS [row][CAP].  A list
+    // whose J-th key passes may have dropped one, and a query holds at most
+    // CAP: the query is then marked.
     {
-        constexpr int RPW = FC_QB / (FC_THREADS / 64);  // rows per wave
-        uint32_t* lc = reinterpret_cast<uint32_t*>(smem);                    // ids [FC_QB][CAP]
-        uint32_t* sc = reinterpret_cast<uint32_t*>(smem) + (size_t)FC_QB * CAP;  // keys, then scores
-        uint32_t rn[RPW], rbeg[RPW + 1], rin[RPW];
-        rbeg[0] = 0;
+        uint32_t nn[FC_QBW * 4], base[FC_QBW * 4];
 #pragma unroll
-        for (int i = 0; i < RPW; i++) {
-            const int row = wave + i * (FC_THREADS / 64);
-            uint32_t n = row < rows ? scnt[row] : 0u;
-            if (n > (uint32_t)CAP) {  // may be incomplete: the exact fallback
-                if (lane == 0) flag_list[atomicAdd(flag_count, 1u)] = (uint32_t)(q0 + row);
-                n = 0;
+        for (int b = 0; b < FC_QBW; b++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int row = b * 16 + 4 * g + r;
+                const bool act = row < rows;
+                const float kthr = act ? skthr[row] : 3.0e38f;
+                uint32_t n = 0;
+#pragma unroll
+                for (int j = 0; j < J; j++) n += top[b][r][j] >= kthr ? 1u : 0u;
+                nn[b * 4 + r] = n;
+                base[b * 4 + r] = prefix16(n);
+                if (act && top[b][r][J - 1] >= kthr) sover[row] = 1u;
             }
-            uint32_t in = 0, un = n;
-            if (!ordered && n > 0) {
-                uint32_t* ids = lc + (size_t)row * CAP;
-                const float* keys = reinterpret_cast<const float*>(sc) + (size_t)row * CAP;
-                const float m2 = 2.0f * smar[row];
-                uint32_t* pr = probe + (size_t)(q0 + row) * P;
-                un = 0;
-                // every lane reads its candidates before any slot is rewritten
-                constexpr int EM = (32 * J + 63) / 64;
-                uint32_t id[EM], st_[EM], ahead[EM];
-                float cs[EM];
+        // the last lane of each group reserves the group's slots: every
+        // reservation issued before the first result is read
+        uint32_t o[FC_QBW * 4];
 #pragma unroll
-                for (int e = 0; e < EM; e++) {
-                    const uint32_t t = e * 64 + lane;
-                    id[e] = t < n ? ids[t] : 0u;
-                    cs[e] = t < n ? 3.0f - keys[t] : 0.0f;
-                    st_[e] = 0u;
-                    ahead[e] = 0u;
-                }
+        for (int k = 0; k < FC_QBW * 4; k++) {
+            const int row = (k >> 2) * 16 + 4 * g + (k & 3);
+            o[k] = 0;
+            if (row < rows && c == 15 && base[k] > 0) o[k] = atomicAdd(&scnt[row], base[k]);
+        }
 #pragma unroll
-                for (int e = 0; e < EM; e++) {
-                    if ((uint32_t)(e * 64) >= n) break;  // wave-uniform
-                    const uint32_t t = e * 64 + lane;
-                    uint32_t better = 0, worse = 0, a = 0;
-                    for (uint32_t j = 0; j < n; j++) {
-                        const float cj = 3.0f - keys[j];
-                        better += cj + m2 < cs[e] ? 1u : 0u;
-                        worse += cj - m2 > cs[e] ? 1u : 0u;
-                        a += cj < cs[e] || (cj == cs[e] && j < t) ? 1u : 0u;
+        for (int k = 0; k < FC_QBW * 4; k++)
+            base[k] = (uint32_t)__shfl((int)o[k], (lane & 48) | 15, 64) + base[k] - nn[k];
+#pragma unroll
+        for (int b = 0; b < FC_QBW; b++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int row = b * 16 + 4 * g + r;
+                const uint32_t n = nn[b * 4 + r], o = base[b * 4 + r];
+#pragma unroll
+                for (int j = 0; j < J; j++) {
+                    if (__ballot((uint32_t)j < n) == 0) break;  // no lane has a j-th candidate
+                    if ((uint32_t)j < n && o + j < (uint32_t)CAP) {
+                        const uint32_t ti = __float_as_uint(top[b][r][j]) & ~kmask;
+                        cid[row * CAP + o + j] = 16u * (FC_NW * ti + (uint32_t)h) + (uint32_t)c;
+                        ckey[row * CAP + o + j] = top[b][r][j];
                     }
-                    ahead[e] = a;
-                    st_[e] = t >= n ? 0u : worse >= n - (uint32_t)Pe ? 1u : better >= (uint32_t)Pe ? 0u : 2u;
-                }
-#pragma unroll
-                for (int e = 0; e < EM; e++) {
-                    if ((uint32_t)(e * 64) >= n) break;
-                    const uint64_t bi = __ballot(st_[e] == 1u), bu = __ballot(st_[e] == 2u);
-                    const uint32_t ou = __builtin_amdgcn_mbcnt_hi((uint32_t)(bu >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bu, 0u));
-                    if (st_[e] == 1u && ahead[e] < (uint32_t)Pe) pr[ahead[e]] = id[e];
-                    if (st_[e] == 2u) ids[un + ou] = id[e];
-                    in += (uint32_t)__popcll(bi);
-                    un += (uint32_t)__popcll(bu);
                 }
             }
-            rn[i] = in < (uint32_t)Pe ? un : 0u;  // no place left: nothing to rescore
-            rin[i] = in;
-            rbeg[i + 1] = rbeg[i] + rn[i];
-        }
-        // the candidates left to rescore, numbered in row order: lane l takes
-        // numbers l, l + 64, ..., three at a time
-        const uint32_t tot = rbeg[RPW];
-        constexpr int G = 3;  // pairs per lane in flight (registers: 32 G floats)
-        for (uint32_t b0 = 0; b0 < tot; b0 += 64 * G) {
-            const float* qa[G];
-            const float* cb[G];
-            uint32_t at[G];  // LDS slot of each number (row * CAP + t), or ~0
+    }
+    __syncthreads();
+
+    // ---- the selection, wave h for queries h, h + FC_NW, ...: the sure
+    // members go out at once, the uncertain ones are rescored with the
+    // reference's sequential dot against the query as searched
+    // (distance.rs:104-109) and ranked by (score, list) for the places left.
+    uint32_t* uid = reinterpret_cast<uint32_t*>(ckey);  // lists to rescore, over the keys
+    {
+        uint32_t nr[FC_RPW];  // candidates of each query (0: nothing to select)
+        uint32_t sk[FC_RPW];  // keys of the queries with at most 64, sorted together
+        uint32_t big = 0;     // queries with more than 64
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                const uint32_t x = b0 + 64 * g + lane;
-                int ri = 0;
-#pragma unroll
-                for (int i = 1; i < RPW; i++) ri += x >= rbeg[i] ? 1 : 0;
-                const int row = wave + ri * (FC_THREADS / 64);
-                const bool ok = x < tot;
-                at[g] = ok ? (uint32_t)row * CAP + (x - rbeg[ri]) : ~0u;
-                qa[g] = tile + (ok ? row : 0) * st;
-                cb[g] = C + (size_t)(ok ? lc[at[g]] : 0u) * d;
+        for (int i = 0; i < FC_RPW; i++) {
+            const int row = h + FC_NW * i;
+            uint32_t n = 0;
+            if (row < rows) {
+                n = scnt[row];
+                if (sover[row] || n > (uint32_t)CAP) {  // may be incomplete: the exact fallback
+                    if (lane == 0) flag_list[atomicAdd(flag_count, 1u)] = (uint32_t)(q0 + row);
+                    n = 0;
+                }
+                if (lane == 0) {
+                    sin[row] = (uint32_t)Pe;
+                    sun[row] = 0u;
+                }
             }
-            float dot[G];
-            fc_seq_dots<G>(qa, cb, d, dot);
-#pragma unroll
-            for (int g = 0; g < G; g++)
-                if (at[g] != ~0u) sc[at[g]] = fkey(1.0f - dot[g]);
+            nr[i] = n;
+            big |= n > 64u ? 1u << i : 0u;
+            sk[i] = (uint32_t)lane < n && n <= 64u ? (~fkey(ckey[row * CAP + lane]) & ~63u) | (uint32_t)lane : ~0u;
         }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
+        wave_sort_u32_sep<FC_RPW>(sk);
 #pragma unroll
-        for (int i = 0; i < RPW; i++) {
-            const int row = wave + i * (FC_THREADS / 64);
-            const uint32_t n = rn[i];
-            if (n == 0) continue;  // nothing left to rank, overflowed or past the batch
-            const uint32_t* cr = lc + (size_t)row * CAP;
-            const uint32_t* sr = sc + (size_t)row * CAP;
-            uint32_t* pr = probe + (size_t)(q0 + row) * P + rin[i];
-            const int need = Pe - (int)rin[i];
-            if (n <= 64) fc_select_row<1>(cr, sr, n, need, pr);
-            else if (n <= 128) fc_select_row<2>(cr, sr, n, need, pr);
-            else if (n <= 256) fc_select_row<4>(cr, sr, n, need, pr);
-            else fc_select_row<8>(cr, sr, n, need, pr);
+        for (int i = 0; i < FC_RPW; i++) {
+            const int row = h + FC_NW * i;
+            const uint32_t n = nr[i];
+            if (n > 0 && n <= 64) {
+                uint32_t in, un;
+                const uint32_t s1[1] = {sk[i]};
+                fc_classify_sorted<1>(s1, cid + row * CAP, uid + row * CAP, probe + (size_t)(q0 + row) * P, n,
+                                      Pe, smar[row], sulp[row], ordered, in, un);
+                if (lane == 0) {
+                    sin[row] = in;
+                    sun[row] = in < (uint32_t)Pe ? un : 0u;
+                }
+            }
+        }
+#pragma unroll 1
+        for (int i = 0; i < FC_RPW; i++) {
+            if (!(big >> i & 1u)) continue;
+            const int row = h + FC_NW * i;
+            const uint32_t n = scnt[row];
+            uint32_t* pr = probe + (size_t)(q0 + row) * P;
+            const uint32_t* ids = cid + row * CAP;
+            const float* keys = ckey + row * CAP;
+            uint32_t* unc = uid + row * CAP;
+            const float mar = smar[row], ulp = sulp[row];
+            uint32_t in, un;
+            if (CAP <= 128 || n <= 128) fc_classify<2>(ids, keys, unc, pr, n, Pe, mar, ulp, ordered, in, un);
+            else if (n <= 256) fc_classify<4>(ids, keys, unc, pr, n, Pe, mar, ulp, ordered, in, un);
+            else fc_classify<8>(ids, keys, unc, pr, n, Pe, mar, ulp, ordered, in, un);
+            if (lane == 0) {
+                sin[row] = in;
+                sun[row] = in < (uint32_t)Pe ? un : 0u;
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    // the lists to rescore, numbered in query order, one per lane; the
+    // scores go over the candidate lists
+    uint32_t rbeg[FC_RPW + 1];
+    rbeg[0] = 0;
+#pragma unroll
+    for (int i = 0; i < FC_RPW; i++) {
+        const int row = h + FC_NW * i;
+        rbeg[i + 1] = rbeg[i] + (row < rows ? sun[row] : 0u);
+    }
+    const uint32_t tot = rbeg[FC_RPW];
+    for (uint32_t b0 = 0; b0 < tot; b0 += 64) {
+        const uint32_t x = b0 + lane;
+        int row = h;
+        uint32_t beg = 0;
+#pragma unroll
+        for (int i = 1; i < FC_RPW; i++)
+            if (x >= rbeg[i]) {
+                row = h + FC_NW * i;
+                beg = rbeg[i];
+            }
+        if (x < tot) {
+            const uint32_t at = (uint32_t)row * CAP + (x - beg);
+            const float dot = fc_seq_dot<DT>(tile + row * st, C + (size_t)uid[at] * d, d);
+            cid[at] = fkey(1.0f - dot);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll 1
+    for (int i = 0; i < FC_RPW; i++) {
+        const int row = h + FC_NW * i;
+        if (row >= rows) break;
+        const uint32_t n = sun[row];
+        if (n == 0) continue;  // nothing left to rank or marked
+        const uint32_t* cr = uid + row * CAP;
+        const uint32_t* sr = cid + row * CAP;
+        const uint32_t rin = sin[row];
+        uint32_t* pr = probe + (size_t)(q0 + row) * P + rin;
+        const int need = Pe - (int)rin;
+        if (n <= 16) {
+            // a few: each one's rank by counting
+            const bool mine = (uint32_t)lane < n;
+            const uint64_t kv = mine ? ((uint64_t)sr[lane] << 32) | cr[lane] : ~0ull;
+            uint32_t rank = 0;
+            for (uint32_t j = 0; j < n; j++) {
+                const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(kv >> 32), (int)j) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)kv, (int)j);
+                rank += o < kv ? 1u : 0u;
+            }
+            if (mine && rank < (uint32_t)need) pr[rank] = (uint32_t)kv;
+        } else if (n <= 64) {
+            fc_select_row<1>(cr, sr, n, need, pr);
+        } else if (CAP <= 128 || n <= 128) {
+            fc_select_row<2>(cr, sr, n, need, pr);
+        } else if (n <= 256) {
+            fc_select_row<4>(cr, sr, n, need, pr);
+        } else {
+            fc_select_row<8>(cr, sr, n, need, pr);
         }
     }
 }
 
-// Keys per (wave, lane, row): 8 up to 32 probes, 10 above, where a list
-// holding more than 8 of the window's lists flags the query more often
-// (about 5 queries of a 10k batch at 16,384 lists and 64 probes).
-#define FC_J 8
-#define FC_J_WIDE 10
-static int fc_keys(int P) { return P > 32 ? FC_J_WIDE : FC_J; }
-
-int coarse_fused_cap(int P) { return 32 * fc_keys(P); }
+// Keys per list: 4 up to 8 probes, 6 up to 32, 8 above.
+static int fc_keys(int Pe) { return Pe <= 8 ? 4 : Pe <= 32 ? 6 : 8; }
 
 bool coarse_fused_supported(int d, int P) { return d >= 1 && d <= 128 && P >= 1 && P <= 64; }
+
+static int fc_tiles_per_wave(int L) { return fc_padded_lists(L) / FC_LISTS; }
 
 template <int DT, int J>
 static void launch_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int Pe, int P,
                          int normalize, int ordered, float* qn, float* qnorm, const float* C, uint32_t* probe,
                          uint32_t* flag_list, uint32_t* flag_count, hipStream_t s, uint32_t* qbad,
                          unsigned int* nbad) {
-    const size_t lds = fc_lds_bytes(d, DT, J);
-    // index bits: tiles ceil(L / 16) <= 2^IB
+    const size_t lds = fc_lds_bytes(d, J, DT);
+    const int nt = fc_tiles_per_wave(L);
+    // index bits: a wave's tile numbers 0 .. nt - 1 < 2^IB
     int IB = 0;
-    while ((1 << IB) < (L + 15) / 16) IB++;
+    while ((1 << IB) < nt) IB++;
     auto k = coarse_fused_kernel<DT, J>;
     ensure_dyn_lds((const void*)k, lds);
-    hipLaunchKernelGGL(k, dim3((nq + FC_QB - 1) / FC_QB), dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, cmax,
+    hipLaunchKernelGGL(k, dim3((nq + FC_QB - 1) / FC_QB), dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, nt, cmax,
                        Pe, P, IB, normalize, ordered, qn, qnorm, C, probe, flag_list, flag_count, qbad, nbad);
 }
 
@@ -670,12 +843,14 @@ static void launch_fused_j(const float* Q, int nq, int d, const uint4* Cb, int L
                            int normalize, int ordered, float* qn, float* qnorm, const float* C, uint32_t* probe,
                            uint32_t* flag_list, uint32_t* flag_count, hipStream_t s, uint32_t* qbad,
                            unsigned int* nbad) {
-    if (fc_keys(Pe) == FC_J_WIDE)
-        launch_fused<DT, FC_J_WIDE>(Q, nq, d, Cb, L, cmax, Pe, P, normalize, ordered, qn, qnorm, C, probe, flag_list,
-                                    flag_count, s, qbad, nbad);
-    else
-        launch_fused<DT, FC_J>(Q, nq, d, Cb, L, cmax, Pe, P, normalize, ordered, qn, qnorm, C, probe, flag_list,
-                               flag_count, s, qbad, nbad);
+#define FC_J(JV) launch_fused<DT, JV>(Q, nq, d, Cb, L, cmax, Pe, P, normalize, ordered, qn, qnorm, C, probe, \
+                                      flag_list, flag_count, s, qbad, nbad)
+    switch (fc_keys(Pe)) {
+        case 4: FC_J(4); break;
+        case 6: FC_J(6); break;
+        default: FC_J(8); break;
+    }
+#undef FC_J
 }
 
 void launch_coarse_fused(const float* Q, int nq, int d, const uint4* Cb, int L, float cmax, int P,
@@ -699,47 +874,41 @@ void launch_coarse_fused(const float* Q, int nq, int d, const uint4* Cb, int L, 
 // D[q][c] = Q[q] . C[c] through fc_pass (Q already normalised or not).
 template <int DT>
 __global__ __launch_bounds__(FC_THREADS) void coarse_bf16x3_dots_kernel(const float* __restrict__ Q, int nq,
-                                                                 int d, const uint4* __restrict__ Cb,
-                                                                 int L, float* __restrict__ D) {
-    extern __shared__ __align__(16) char smem[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
-    const int qb = wave % FC_QBW;
+                                                                        int d, const uint4* __restrict__ Cb,
+                                                                        int L, int nt, float* __restrict__ D) {
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    const int h = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q0 = blockIdx.x * FC_QB;
-    const int row_a = q0 + qb * 16 + c;
-    u32x4 ah[DT], al[DT];
-    fc_split_rows<DT>([&](int j) { return row_a < nq ? Q[(size_t)row_a * d + j] : 0.0f; }, d, g, ah, al);
-    fc_pass<DT>(Cb, L, ah, al, reinterpret_cast<u32x4*>(smem), [&](const floatx4& acc, int cb, bool) {
+    u32x4 ah[FC_QBW][DT], al[FC_QBW][DT];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int row = q0 + qb * 16 + 4 * g + r, col = cb + c;
-            if (row < nq && col < L) D[(size_t)row * L + col] = acc[r];
-        }
+    for (int b = 0; b < FC_QBW; b++) {
+        const int row_a = q0 + b * 16 + c;
+        fc_split_rows<DT>([&](int j) { return row_a < nq ? Q[(size_t)row_a * d + j] : 0.0f; }, d, g, ah[b], al[b]);
+    }
+    u32x4 bh[2][DT], bl[2][DT];
+    fc_prefetch<DT, true>(Cb, nt, h, bh, bl);
+    fc_pass<DT, true>(Cb, nt, h, bh, bl, ah, al, [&](const floatx4 (&acc)[FC_QBW], int i, bool) {
+        const int col = (FC_NW * i + h) * 16 + c;
+#pragma unroll
+        for (int b = 0; b < FC_QBW; b++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int row = q0 + b * 16 + 4 * g + r;
+                if (row < nq && col < L) D[(size_t)row * L + col] = acc[b][r];
+            }
     });
 }
 
 void launch_coarse_bf16x3_dots(const float* Q, int nq, int d, const uint4* Cb, int L, float* D,
                                hipStream_t s) {
     if (nq <= 0 || L <= 0) return;
-    const int DT = (d + 31) / 32;
-    const size_t lds = 2 * 2 * fc_stage_chunks(DT) * 16;
+    const int DT = (d + 31) / 32, nt = fc_tiles_per_wave(L);
     const dim3 grid((nq + FC_QB - 1) / FC_QB);
     switch (DT) {
-        case 1:
-            ensure_dyn_lds((const void*)coarse_bf16x3_dots_kernel<1>, lds);
-            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<1>, grid, dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, D);
-            break;
-        case 2:
-            ensure_dyn_lds((const void*)coarse_bf16x3_dots_kernel<2>, lds);
-            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<2>, grid, dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, D);
-            break;
-        case 3:
-            ensure_dyn_lds((const void*)coarse_bf16x3_dots_kernel<3>, lds);
-            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<3>, grid, dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, D);
-            break;
-        default:
-            ensure_dyn_lds((const void*)coarse_bf16x3_dots_kernel<4>, lds);
-            hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<4>, grid, dim3(FC_THREADS), lds, s, Q, nq, d, Cb, L, D);
-            break;
+        case 1: hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<1>, grid, dim3(FC_THREADS), 0, s, Q, nq, d, Cb, L, nt, D); break;
+        case 2: hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<2>, grid, dim3(FC_THREADS), 0, s, Q, nq, d, Cb, L, nt, D); break;
+        case 3: hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<3>, grid, dim3(FC_THREADS), 0, s, Q, nq, d, Cb, L, nt, D); break;
+        default: hipLaunchKernelGGL(coarse_bf16x3_dots_kernel<4>, grid, dim3(FC_THREADS), 0, s, Q, nq, d, Cb, L, nt, D); break;
     }
 }
 

@@ -368,6 +368,59 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int stride) {
     return ((uint64_t)hi << 32) | lo;
 }
 
+// R separate ascending sorts of 64 32-bit keys, one per lane in k[r], their
+// networks interleaved.
+template <int R>
+__device__ __forceinline__ void wave_sort_u32_sep(uint32_t (&k)[R]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const bool asc = (lane & size) == 0;
+            const bool lower = (lane & stride) == 0;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t o = shfl_xor_u32(k[r], stride);
+                k[r] = lower == asc ? min(o, k[r]) : max(o, k[r]);
+            }
+        }
+    }
+}
+
+// wave_sort_regs for 32-bit keys.
+template <int E>
+__device__ __forceinline__ void wave_sort_u32(uint32_t (&k)[E]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int size = 2; size <= 64 * E; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride >= 64) {
+                const int es = stride >> 6;
+#pragma unroll
+                for (int e = 0; e < E; e++) {
+                    const int f = e ^ es;
+                    if (f > e) {
+                        const bool asc = (((e << 6) | lane) & size) == 0;
+                        const uint32_t a = k[e], b = k[f];
+                        k[e] = asc ? min(a, b) : max(a, b);
+                        k[f] = asc ? max(a, b) : min(a, b);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; e++) {
+                    const uint32_t o = shfl_xor_u32(k[e], stride);
+                    const bool asc = (((e << 6) | lane) & size) == 0;
+                    const bool lower = (lane & stride) == 0;
+                    k[e] = lower == asc ? min(o, k[e]) : max(o, k[e]);
+                }
+            }
+        }
+    }
+}
+
 // Ascending bitonic sort of 64*E keys held by one wave, E per lane; element
 // e*64 + lane lives in k[e] of that lane.  No LDS, no barriers.
 template <int E>
