@@ -394,7 +394,7 @@ __device__ inline float flat_exact(const float* q, const float* __restrict__ x, 
 // Exact top-k of query qv over the vectors item(0 .. W - 1) names (an index,
 // or 0xffffffff to skip the item) with a threshold-filtered LDS buffer: keys
 // (fkey(dist), index) sorted ascending in keys[0 ..) on return; returns how
-// many (all threads).  keys / pay hold FL_BUF entries.
+// many (all threads).  keys / pay hold FL_BUF entries; misc 12 words.
 template <class Item>
 __device__ int flat_exact_items(const float* qv, const float* __restrict__ X, int W, Item item, int d, int k,
                                 int metric, uint64_t* keys, uint32_t* pay, uint32_t* misc) {
@@ -404,9 +404,14 @@ __device__ int flat_exact_items(const float* qv, const float* __restrict__ X, in
         misc[3] = 0xffffffffu;
     }
     __syncthreads();
+    // the buffer count as every thread knows it: each round's appends are
+    // counted per wave into misc[4 + 4 par + wave] before the round's barrier
+    // and summed after it, so the flush decision is the same in every wave
+    // (the shared counter itself may already hold a faster wave's appends)
+    uint32_t cnt = 0, par = 0;
     for (int base = 0; base < W; base += FL_ROUND) {
-        if ((int)misc[2] > FL_BUF - FL_ROUND) {
-            int m = (int)misc[2];
+        if ((int)cnt > FL_BUF - FL_ROUND) {
+            int m = (int)cnt;
             int m2 = next_pow2(m);
             for (int i = m + tid; i < m2; i += blockDim.x) keys[i] = ~0ull;
             block_bitonic_sort(keys, pay, m2);
@@ -415,8 +420,10 @@ __device__ int flat_exact_items(const float* qv, const float* __restrict__ X, in
                 misc[2] = (uint32_t)k;
             }
             __syncthreads();
+            cnt = m >= k ? (uint32_t)k : (uint32_t)m;
         }
         const uint32_t th = misc[3];
+        uint32_t wn = 0;
         for (int u = 0; u < FL_ROUND / 256; u++) {
             const int i = base + u * 256 + tid;
             const uint32_t j = i < W ? item(i) : 0xffffffffu;
@@ -426,10 +433,14 @@ __device__ int flat_exact_items(const float* qv, const float* __restrict__ X, in
                 key = cand_key(flat_exact(qv, X + (size_t)j * d, d, metric), j);
                 take = (uint32_t)(key >> 32) <= th;
             }
+            wn += (uint32_t)__popcll(__ballot(take));
             int slot = wave_append_slot(take, &misc[2]);
             if (take) keys[slot] = key;
         }
+        if ((tid & 63) == 0) misc[4 + 4 * par + (tid >> 6)] = wn;
         __syncthreads();
+        cnt += misc[4 + 4 * par] + misc[5 + 4 * par] + misc[6 + 4 * par] + misc[7 + 4 * par];
+        par ^= 1u;
     }
     int m = (int)misc[2];
     int m2 = next_pow2(m > 0 ? m : 1);
@@ -452,7 +463,7 @@ __global__ __launch_bounds__(256) void flat_merge_kernel(
     float* __restrict__ out_dist, unsigned int* overflow, uint32_t* __restrict__ flag_list) {
     __shared__ uint64_t keys[FL_BUF];
     __shared__ uint32_t pay[FL_BUF];
-    __shared__ uint32_t misc[4];
+    __shared__ uint32_t misc[12];
     const int q = blockIdx.x, tid = threadIdx.x;
     if (q >= nq) return;
     const float* qv = Q + (size_t)q * d;
@@ -714,7 +725,7 @@ __global__ __launch_bounds__(256) void flat_exact_slice_kernel(
     int d, int k, int metric, int len, uint64_t* __restrict__ out_keys) {
     __shared__ uint64_t keys[FL_BUF];
     __shared__ uint32_t pay[FL_BUF];
-    __shared__ uint32_t misc[4];
+    __shared__ uint32_t misc[12];
     const int s = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
     const uint32_t q = flag_list[i];
     const int j0 = s * len, j1 = min(n, j0 + len);
@@ -765,7 +776,7 @@ __global__ __launch_bounds__(256) void flat_rank_fallback_kernel(
     if (nflag_dev && blockIdx.y >= *nflag_dev) return;  // uniform: no flagged query for this row
     __shared__ uint64_t keys[FL_BUF];
     __shared__ uint32_t pay[FL_BUF];
-    __shared__ uint32_t misc[4];
+    __shared__ uint32_t misc[12];
     __shared__ float qs[128];  // d <= 128
     __shared__ uint32_t rescan[16];
     const int s = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;

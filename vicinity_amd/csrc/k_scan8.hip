@@ -1,5 +1,5 @@
 // ADC scan over the probed inverted lists for byte codes (codebook_size != 16),
-// one workgroup (256 threads) per query.
+// one workgroup (512 threads) per query.
 //
 // Reference: search_approx_internal_observed src/ivf_pq/search.rs:1175-1391;
 // compute_adc_table_into src/ivf_pq/pq.rs:196-266; adc_batch_256_into
@@ -17,8 +17,20 @@
 
 namespace vgpu {
 
-#define SCAN_U 2                      // candidates per thread per round
-#define SCAN_ROUND (VGPU_BLOCK * SCAN_U)
+// 512 threads per query: thread (t, h) = (tid % 256, tid / 256) builds
+// codeword t's table entries of the codebooks m = h, h + 2, ..., so each holds
+// half the codewords in registers and two workgroups fit a CU.
+#define SCAN_THREADS 512
+#define SCAN_WAVES (SCAN_THREADS / 64)
+#define SCAN_U 1                        // candidates per thread per round
+#define SCAN_ROUND (SCAN_THREADS * SCAN_U)
+
+// Codewords a thread holds: ds (CWD < 0: exactly -CWD, CWD > 0: up to CWD)
+// floats of each of its ceil(MT / 2) codebooks.
+template <int MT, int CWD>
+constexpr int cw_count() {
+    return CWD != 0 ? (MT + 1) / 2 * (CWD > 0 ? CWD : -CWD) : 1;
+}
 
 // Probe slots kept in LDS per query; a wider probe (nprobe up to nlist) reads
 // each slot's list from global memory when it is scanned.
@@ -113,7 +125,17 @@ struct ScanLds {
     uint32_t* pref; // [P+1]
     float* term0;   // [P]
     TopkLds tk;
-    uint32_t* misc; // [4]
+    uint32_t* misc; // [4 + 2 SCAN_WAVES]
+};
+
+// The buffer count as every thread of the block knows it, without reading
+// the shared counter (which a faster wave may already have advanced): each
+// round's appends are counted per wave into misc[4 + 8 par + wave] before the
+// round's closing barrier and summed by every thread after it (par alternates,
+// so a wave one round ahead never overwrites counts still being read).
+struct TopkCnt {
+    uint32_t n = 0;
+    uint32_t par = 0;
 };
 
 __host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -139,7 +161,7 @@ __host__ __device__ inline size_t scan_lds_layout(int d, int M, int K, int P, in
     off[8] = o; o = align16(o + (size_t)buf * 8);        // keys
     off[9] = o; o = align16(o + (size_t)buf * 4);        // pos
     off[10] = o; o = align16(o + (size_t)buf * 2);       // probe
-    off[11] = o; o = align16(o + 16);                    // misc
+    off[11] = o; o = align16(o + 4 * (4 + 2 * SCAN_WAVES)); // misc: count, thr, 2 x 8 round counts
     return o;
 }
 
@@ -204,46 +226,50 @@ __device__ inline void write_out(const ScanArgs& a, ScanLds& s, int q, int n) {
 }
 
 // Probed list l (slot p, entries beg .. beg + len - 1) with the reference
-// arithmetic: the residual r = q - c (search.rs:1242-1245; with OPQ the
-// rotated residual R r, precomputed per slot in a.rres), the table
-// LUT[m][k] = sum_j (r_j - cw_j)^2 (pq.rs:232-251; ds == 1 gives
-// 0 + diff*diff == diff*diff), then each entry's M entries summed in
-// codebook order (pq.rs:272-279).  With FILT only the entries whose category
-// byte equals cq are candidates (filtering/mod.rs:151-153, 214-218).  Every
-// thread of the block calls it.
-template <int MT, int KT, bool FILT, int CWD>
-__device__ inline void scan_list(const DevIndex& ix, const ScanArgs& a, ScanLds& s, int buf,
-                                 uint32_t l, uint32_t beg, uint32_t len, int q, int p,
-                                 const uint8_t* __restrict__ ecat, uint8_t cq,
-                                 const float (&cw)[CWD != 0 ? MT * (CWD > 0 ? CWD : -CWD) : 1]) {
-    const int tid = threadIdx.x;
-    const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds;
+// arithmetic, in three steps: the residual r = q - c (search.rs:1242-1245;
+// with OPQ the rotated residual R r, precomputed per slot in a.rres) into
+// rsd; the table LUT[m][k] = sum_j (r_j - cw_j)^2 (pq.rs:232-251; ds == 1
+// gives 0 + diff*diff == diff*diff) from rsd into lut; then each entry's M
+// entries summed in codebook order (pq.rs:272-279).  With FILT only the
+// entries whose category byte equals cq are candidates (filtering/mod.rs:151-
+// 153, 214-218).  Every thread of the block calls each step.
+__device__ inline void stage_residual(const DevIndex& ix, const ScanArgs& a, const ScanLds& s, float* rsd,
+                                      uint32_t l, int q, int p) {
+    const int tid = threadIdx.x, d = ix.d;
     if (a.rres) {  // OPQ: R (q - c), formed by the rotation kernel (opq.rs:120-123)
         const float* rr = a.rres + ((size_t)q * a.P + p) * d;
-        for (int j = tid; j < d; j += blockDim.x) s.rsd[j] = rr[j];
+        for (int j = tid; j < d; j += blockDim.x) rsd[j] = rr[j];
     } else {
         const float* c = ix.centroids + (size_t)l * d;
-        for (int j = tid; j < d; j += blockDim.x) s.rsd[j] = s.qs[j] - c[j];
+        for (int j = tid; j < d; j += blockDim.x) rsd[j] = s.qs[j] - c[j];
     }
-    __syncthreads();
+}
+
+template <int MT, int KT, int CWD>
+__device__ inline void build_table(const DevIndex& ix, const float* rsd, float* lut,
+                                   const float (&cw)[cw_count<MT, CWD>()]) {
+    const int tid = threadIdx.x;
+    const int M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds;
+    const int t = tid & 255, h = tid >> 8;  // codeword, codebook parity (wave-uniform)
     if constexpr (CWD < 0) {  // ds == W: codewords in registers, the next slice read ahead
         constexpr int W = -CWD;
         float rc[W], rn[W];
 #pragma unroll
-        for (int j = 0; j < W; j++) rc[j] = s.rsd[j];
+        for (int j = 0; j < W; j++) rc[j] = h < MT ? rsd[h * W + j] : 0.0f;
 #pragma unroll
-        for (int m = 0; m < MT; m++) {
-            if (m + 1 < MT) {
+        for (int i = 0; i < (MT + 1) / 2; i++) {
+            const int m = 2 * i + h;
+            if (i + 1 < (MT + 1) / 2) {
 #pragma unroll
-                for (int j = 0; j < W; j++) rn[j] = s.rsd[(m + 1) * W + j];
+                for (int j = 0; j < W; j++) rn[j] = m + 2 < MT ? rsd[(m + 2) * W + j] : 0.0f;
             }
             float acc = 0.0f;
 #pragma unroll
             for (int j = 0; j < W; j++) {
-                float diff = rc[j] - cw[m * W + j];
+                float diff = rc[j] - cw[i * W + j];
                 acc += diff * diff;
             }
-            s.lut[m * 256 + tid] = acc;
+            if (m < MT) lut[m * 256 + t] = acc;
 #pragma unroll
             for (int j = 0; j < W; j++) rc[j] = rn[j];
             // two slices live at a time: the compiler may not hoist further reads
@@ -253,16 +279,17 @@ __device__ inline void scan_list(const DevIndex& ix, const ScanArgs& a, ScanLds&
         constexpr int W = CWD;
         const int dsx = ds;
 #pragma unroll
-        for (int m = 0; m < MT; m++) {
+        for (int i = 0; i < (MT + 1) / 2; i++) {
+            const int m = 2 * i + h;
             float acc = 0.0f;
 #pragma unroll
             for (int j = 0; j < W; j++) {
-                if (j < dsx) {
-                    float diff = s.rsd[m * dsx + j] - cw[m * W + j];
+                if (j < dsx && m < MT) {
+                    float diff = rsd[m * dsx + j] - cw[i * W + j];
                     acc += diff * diff;
                 }
             }
-            s.lut[m * 256 + tid] = acc;
+            if (m < MT) lut[m * 256 + t] = acc;
             // one codebook's residual slice live at a time (hoisting every
             // LDS read ahead of the arithmetic would double the registers)
             __builtin_amdgcn_sched_barrier(0);
@@ -273,49 +300,80 @@ __device__ inline void scan_list(const DevIndex& ix, const ScanArgs& a, ScanLds&
             const float* cwp = ix.codebooks + (size_t)e * ds;
             float acc = 0.0f;
             for (int j = 0; j < ds; j++) {
-                float diff = s.rsd[m * ds + j] - cwp[j];
+                float diff = rsd[m * ds + j] - cwp[j];
                 acc += diff * diff;
             }
-            s.lut[e] = acc;
+            lut[e] = acc;
         }
     }
-    __syncthreads();
+}
+
+// The entries of one list against its table; a block barrier ends every
+// round.  The flush decision uses the count every thread holds in tc, so it
+// is the same in every wave.
+template <int MT, int KT, bool FILT>
+__device__ inline void scan_entries(const DevIndex& ix, const ScanArgs& a, ScanLds& s, int buf, const float* lut,
+                                    uint32_t beg, uint32_t len, int p, const uint8_t* __restrict__ ecat,
+                                    uint8_t cq, TopkCnt& tc) {
+    const int tid = threadIdx.x;
+    const int M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K;
     for (uint32_t base = 0; base < len; base += SCAN_ROUND) {
-        if (*s.tk.count > (uint32_t)(buf - SCAN_ROUND)) topk_flush(s.tk, a.kk);
+        if (tc.n > (uint32_t)(buf - SCAN_ROUND)) {
+            topk_flush(s.tk, a.kk);
+            tc.n = tc.n >= (uint32_t)a.kk ? (uint32_t)a.kk : tc.n;  // the flush keeps kk when it has them
+        }
         const uint32_t thr = *s.tk.thr;
+        uint32_t wn = 0;  // this wave's appends in the round
 #pragma unroll
         for (int u = 0; u < SCAN_U; u++) {
-            uint32_t i = base + u * VGPU_BLOCK + tid;
+            uint32_t i = base + u * SCAN_THREADS + tid;
             bool take = false;
             uint32_t fk = 0, pos = 0;
             if (i < len) {
                 pos = beg + i;
                 if (!FILT || ecat[pos] == cq) {
-                    float dist = adc_sum<MT, KT>(ix.codes + (size_t)pos * M, s.lut, M, K, 0.0f);
+                    float dist = adc_sum<MT, KT>(ix.codes + (size_t)pos * M, lut, M, K, 0.0f);
                     fk = fkey(dist);
                     take = fk <= thr;
                 }
             }
+            wn += (uint32_t)__popcll(__ballot(take));
             topk_push(s.tk, take, fk, pos, p, ix.list_ids);
         }
+        if ((tid & 63) == 0) s.misc[4 + SCAN_WAVES * tc.par + (tid >> 6)] = wn;
         __syncthreads();
+#pragma unroll
+        for (int w = 0; w < SCAN_WAVES; w++) tc.n += s.misc[4 + SCAN_WAVES * tc.par + w];
+        tc.par ^= 1u;
     }
 }
 
-// Codeword t of every codebook into registers (ksub 256, 256 threads):
-// CWD > 0 holds ds <= CWD floats per codeword, CWD < 0 exactly ds = -CWD.  The
-// per-list tables then read no codebook memory.
+template <int MT, int KT, bool FILT, int CWD>
+__device__ inline void scan_list(const DevIndex& ix, const ScanArgs& a, ScanLds& s, int buf,
+                                 uint32_t l, uint32_t beg, uint32_t len, int q, int p,
+                                 const uint8_t* __restrict__ ecat, uint8_t cq,
+                                 const float (&cw)[cw_count<MT, CWD>()], TopkCnt& tc) {
+    stage_residual(ix, a, s, s.rsd, l, q, p);
+    __syncthreads();
+    build_table<MT, KT, CWD>(ix, s.rsd, s.lut, cw);
+    __syncthreads();
+    scan_entries<MT, KT, FILT>(ix, a, s, buf, s.lut, beg, len, p, ecat, cq, tc);
+}
+
+// Codeword t = tid % 256 of the codebooks h, h + 2, ... (h = tid / 256) into
+// registers (ksub 256): CWD > 0 holds ds <= CWD floats per codeword, CWD < 0
+// exactly ds = -CWD.  The per-list tables then read no codebook memory.
 template <int MT, int CWD>
-__device__ inline void load_codewords(const DevIndex& ix,
-                                      float (&cw)[CWD != 0 ? MT * (CWD > 0 ? CWD : -CWD) : 1]) {
+__device__ inline void load_codewords(const DevIndex& ix, float (&cw)[cw_count<MT, CWD>()]) {
     if constexpr (CWD != 0) {
         constexpr int W = CWD > 0 ? CWD : -CWD;
-        const int t = threadIdx.x, ds = CWD > 0 ? ix.ds : W;
+        const int t = threadIdx.x & 255, h = threadIdx.x >> 8, ds = CWD > 0 ? ix.ds : W;
 #pragma unroll
-        for (int m = 0; m < MT; m++) {
-            const float* src = ix.codebooks + ((size_t)m * 256 + t) * ds;
+        for (int i = 0; i < (MT + 1) / 2; i++) {
+            const int m = 2 * i + h;
+            const float* src = ix.codebooks + ((size_t)(m < MT ? m : 0) * 256 + t) * ds;
 #pragma unroll
-            for (int j = 0; j < W; j++) cw[m * W + j] = j < ds ? src[j] : 0.0f;
+            for (int j = 0; j < W; j++) cw[i * W + j] = j < ds && m < MT ? src[j] : 0.0f;
         }
     }
 }
@@ -327,14 +385,12 @@ __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char
     const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, P = a.P;
     const bool wide = P > SCAN_LDS_P;
     ScanLds s = carve(smem, d, M, K, wide ? 0 : P, buf);
-    float cw[CWD != 0 ? MT * (CWD > 0 ? CWD : -CWD) : 1];
+    float cw[cw_count<MT, CWD>()];
     load_codewords<MT, CWD>(ix, cw);
     load_query_and_lists(ix, a, s, q);
-    uint32_t total = 0;
-    for (int p = 0; p < P; p++) {
-        __syncthreads();
-        uint32_t l, beg, len;
-        if (wide) {  // the same for every thread
+    // list, begin and length of probe slot p (the same for every thread)
+    auto slot = [&](int p, uint32_t& l, uint32_t& beg, uint32_t& len) {
+        if (wide) {
             l = a.probe[(size_t)q * P + p];
             const bool ok = l < (uint32_t)ix.L;
             beg = ok ? ix.offsets[l] : 0u;
@@ -344,9 +400,16 @@ __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char
             beg = s.lbeg[p];
             len = s.llen[p];
         }
+    };
+    uint32_t total = 0;
+    TopkCnt tc;
+    for (int p = 0; p < P; p++) {
+        __syncthreads();
+        uint32_t l, beg, len;
+        slot(p, l, beg, len);
         total += len;
         if (len == 0) continue;
-        scan_list<MT, KT, false, CWD>(ix, a, s, buf, l, beg, len, q, p, nullptr, 0, cw);
+        scan_list<MT, KT, false, CWD>(ix, a, s, buf, l, beg, len, q, p, nullptr, 0, cw, tc);
     }
     topk_flush(s.tk, a.kk);
     const int n = (int)*s.tk.count;
@@ -365,7 +428,7 @@ __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char
 // is want[q].  The list bounds are read from global memory per slot, so the
 // list count is not bounded by LDS (a widened query takes every list).
 template <int MT, int KT, int CWD>
-__global__ __launch_bounds__(256) void scan8_filtered_kernel(DevIndex ix, ScanArgs a, int buf,
+__global__ __launch_bounds__(SCAN_THREADS, 4) void scan8_filtered_kernel(DevIndex ix, ScanArgs a, int buf,
                                                              const uint8_t* __restrict__ ecat,
                                                              const uint8_t* __restrict__ want) {
     extern __shared__ __align__(16) char smem[];
@@ -374,7 +437,7 @@ __global__ __launch_bounds__(256) void scan8_filtered_kernel(DevIndex ix, ScanAr
     const int tid = threadIdx.x;
     const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, P = a.P;
     ScanLds s = carve(smem, d, M, K, 0, buf);
-    float cw[CWD != 0 ? MT * (CWD > 0 ? CWD : -CWD) : 1];
+    float cw[cw_count<MT, CWD>()];
     load_codewords<MT, CWD>(ix, cw);
     for (int j = tid; j < d; j += blockDim.x) s.qs[j] = a.qn[(size_t)q * d + j];
     if (tid == 0) {
@@ -382,13 +445,14 @@ __global__ __launch_bounds__(256) void scan8_filtered_kernel(DevIndex ix, ScanAr
         *s.tk.thr = 0xffffffffu;
     }
     const uint8_t cq = want[q];
+    TopkCnt tc;
     for (int p = 0; p < P; p++) {
         __syncthreads();
         const uint32_t l = a.probe[(size_t)q * P + p];  // the same for every thread
         if (l >= (uint32_t)ix.L) continue;
         const uint32_t beg = ix.offsets[l], len = ix.offsets[l + 1] - beg;
         if (len == 0) continue;
-        scan_list<MT, KT, true, CWD>(ix, a, s, buf, l, beg, len, q, p, ecat, cq, cw);
+        scan_list<MT, KT, true, CWD>(ix, a, s, buf, l, beg, len, q, p, ecat, cq, cw, tc);
     }
     topk_flush(s.tk, a.kk);
     const int n = (int)*s.tk.count;
@@ -396,7 +460,7 @@ __global__ __launch_bounds__(256) void scan8_filtered_kernel(DevIndex ix, ScanAr
 }
 
 template <int MT, int KT, int CWD>
-__global__ __launch_bounds__(256) void scan8_exact_kernel(DevIndex ix, ScanArgs a, int buf) {
+__global__ __launch_bounds__(SCAN_THREADS, 4) void scan8_exact_kernel(DevIndex ix, ScanArgs a, int buf) {
     extern __shared__ __align__(16) char smem[];
     // Every query of the batch (block q takes query q), or the flagged queries
     // the FAST kernel listed before this launch (blocks stride over the list).
@@ -435,7 +499,7 @@ static void launch_mk(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     // Flagged queries: a small grid walks the list the FAST kernel wrote.
     // flagged queries are rare: a small grid keeps the usual empty launch cheap
     const int grid = a.only_flagged ? (a.nq < 64 ? a.nq : 64) : a.nq;
-    hipLaunchKernelGGL(k, dim3(grid), dim3(VGPU_BLOCK), lds, s, ix, a, buf);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(SCAN_THREADS), lds, s, ix, a, buf);
 }
 
 template <int KT>
@@ -468,7 +532,7 @@ static void launch_filtered_mk(const DevIndex& ix, const ScanArgs& a, const uint
              : (CWD > 0 && ix.ds < CWD) ? scan8_filtered_kernel<MT, KT, CWD>
                                         : scan8_filtered_kernel<MT, KT, 0>;
     ensure_dyn_lds((const void*)k, lds);
-    hipLaunchKernelGGL(k, dim3(a.nq), dim3(VGPU_BLOCK), lds, s, ix, a, buf, ecat, want);
+    hipLaunchKernelGGL(k, dim3(a.nq), dim3(SCAN_THREADS), lds, s, ix, a, buf, ecat, want);
 }
 
 template <int KT>

@@ -198,7 +198,7 @@ __device__ void block_bitonic_sort2(uint64_t* keys, P* pay, Q* pay2, int n) {
     for (int size = 2; size <= n; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             __syncthreads();
-            for (int t = threadIdx.x; t < (n >> 1); t += VGPU_BLOCK) {
+            for (int t = threadIdx.x; t < (n >> 1); t += blockDim.x) {
                 int i = 2 * t - (t & (stride - 1));
                 int j = i + stride;
                 bool asc = (i & size) == 0;
