@@ -468,29 +468,16 @@ __device__ __forceinline__ void fs8t_load(__amdgpu_buffer_rsrc_t rsc, __amdgpu_b
 // e.z = 16 x its first block - pref, plus t; rows past the end of the lists
 // read zeros or an unrelated record, and their entries are invalid (NaN
 // term).
-// The lane's record in its row's block: m, or with XR (one table copy) m ^ 8
-// in rows 1 and 3.  Lane m of a row reads table column (codebook) record(m),
-// at bank 16 (code & 1) + record(m); with rows 0 and 1 (and 2 and 3), which
-// share an LDS cycle, on columns m and m ^ 8, no two of the 32 lanes meet on
-// a bank.  The lane exchanges of trow_sum pair lanes m and m ^ k, whose
-// records also differ by k, so lane m still ends with the sum of the entry of
-// its record.
-template <bool XR>
-__device__ __forceinline__ uint32_t fs8_lane_rec() {
-    const uint32_t lane = threadIdx.x & 63u;
-    return XR ? lane ^ ((lane & 16u) >> 1) : lane;
-}
-
-template <int MT, bool XR>
+template <int MT>
 __device__ __forceinline__ void fs8t_fetch(__amdgpu_buffer_rsrc_t rsc, __amdgpu_buffer_rsrc_t rsb, const FastLds& s,
                                            const SlotRegs& sr, uint32_t rbase, int P, int& cw, RoundRegs<MT>& g,
                                            bool packed) {
     static_assert(FS_U == 1 && MT % 16 == 0, "one window per wave and round");
-    const uint32_t lane = threadIdx.x & 63u, lx = fs8_lane_rec<XR>();
+    const uint32_t lane = threadIdx.x & 63u, m = lane & 15u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t wb = rbase + wave * 64u;  // window start
     const uint32_t tb = wb + (lane & 48u);   // the row's block start
-    const uint32_t t = wb + lx;              // the entry the lane scores
+    const uint32_t t = tb + m;
     uint32_t base;  // record index of the window's first entry (the lane adds its own)
     float t0;
     uint32_t slot = 0;
@@ -515,7 +502,7 @@ __device__ __forceinline__ void fs8t_fetch(__amdgpu_buffer_rsrc_t rsc, __amdgpu_
         base = e.z + wb;
         t0 = t < e.w ? __uint_as_float(e.y) : __builtin_nanf("");
     }
-    fs8t_load<MT>(rsc, rsb, base + lx, g);
+    fs8t_load<MT>(rsc, rsb, base + lane, g);
     g.t0[0] = t0;
     g.t[0] = packed ? t | slot << FS_LBL_BITS : t;
 }
@@ -523,11 +510,11 @@ __device__ __forceinline__ void fs8t_fetch(__amdgpu_buffer_rsrc_t rsc, __amdgpu_
 // Main-pass fetch through the block map, in three stages one round apart so
 // that no stage waits on the LDS read of another: the map byte of round
 // f + 2, the record of round f + 1 from its map byte, and the loads of round
-// f from its record.  Lane (row, m) of the window at wb scores entry
-// record(m) of padded block wb / 16 + row (fs8_lane_rec), whose lane record is
-// 16 vb[slot] + wb + 16 row + record(m), so the record index is one add.  A
-// sentinel row reads record wb + lane (or zeros past the end) and its NaN t0
-// keeps its entries out.  Labels are packed.
+// f from its record.  Lane (row, m) of the window at wb scores entry m of
+// padded block wb / 16 + row, whose lane record is 16 vb[slot] + wb + lane,
+// so the record index is one add.  A sentinel row reads record wb + lane (or
+// zeros past the end) and its NaN t0 keeps its entries out.  Labels are
+// packed.
 struct MapPipe {
     uint32_t s4n;  // map byte of the round after next
     uint32_t vi;   // next round: lane record, packed label, t0
@@ -541,23 +528,22 @@ __device__ __forceinline__ uint32_t fs8m_byte(const FsMap& mp, uint32_t rbase) {
     return mp.slot4[b0 + ((threadIdx.x & 63u) >> 4)];
 }
 
-template <bool XR>
 __device__ __forceinline__ void fs8m_record(const FsMap& mp, uint32_t rbase, uint32_t s4, MapPipe& mpp) {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t t = rbase + wave * 64u + fs8_lane_rec<XR>();  // wb + the lane's record
+    const uint32_t t = rbase + wave * 64u + (threadIdx.x & 63u);  // wb + lane
     mpp.vi = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(mp.vb16) + s4) + t;
     mpp.t0 = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(mp.t0) + s4);
     mpp.lbl = t | (s4 << (FS_LBL_BITS - 2));
 }
 
-template <int MT, bool XR>
+template <int MT>
 __device__ __forceinline__ void fs8m_fetch(__amdgpu_buffer_rsrc_t rsc, __amdgpu_buffer_rsrc_t rsb, const FsMap& mp,
                                            uint32_t rbase, MapPipe& mpp, RoundRegs<MT>& g) {
     static_assert(FS_U == 1 && MT % 16 == 0, "one window per wave and round");
     fs8t_load<MT>(rsc, rsb, mpp.vi, g);
     g.t0[0] = mpp.t0;
     g.t[0] = mpp.lbl;
-    fs8m_record<XR>(mp, rbase + FS_ROUND, mpp.s4n, mpp);
+    fs8m_record(mp, rbase + FS_ROUND, mpp.s4n, mpp);
     mpp.s4n = fs8m_byte(mp, rbase + 2 * FS_ROUND);
 }
 
@@ -570,13 +556,11 @@ __device__ __forceinline__ float add_dpp(float a, float b) {
 
 // Transposed table: T2[m][c] of codebook m = 16 gi + r lives at float
 // ((gi * 256 + c) * NC + copy) * 16 + r, in NC copies; the lanes of row w read
-// copy w % NC, so a half wave (two rows) reads 32 distinct banks when NC = 2;
-// with one copy, lane m reads column record(m) (fs8_lane_rec), to the same
-// effect.  `lutl` is the table plus the lane's (copy * 16 + m).  Lane m's
-// terms v[j] belong to entry j ^ record(m) of its row; four exchange stages
-// with the lanes m ^ 1, m ^ 2, m ^ 7 and m ^ 8 (each halving the registers
-// still needed) leave the sum of entry record(m) in v[0].  Every lane of the
-// wave must be active.
+// copy w % NC, so a half wave (two rows) reads 32 distinct banks when NC = 2.
+// `lutl` is the table plus the lane's (copy * 16 + m).  Lane m's terms v[j]
+// belong to entry j ^ m of its row; four exchange stages with the lanes m ^ 1,
+// m ^ 2, m ^ 7 and m ^ 8 (each halving the registers still needed) leave the
+// sum of entry m in v[0].  Every lane of the wave must be active.
 // c * 64 + off for the code c held in the low (HI = 0) or high (HI = 1)
 // 16-bit half of h (the other half is ignored): one v_mad_u32_u16 with op_sel.
 template <int HI>
@@ -595,7 +579,7 @@ __device__ __forceinline__ float trow_sum(const CodeRow<MT>& r, const float* __r
         // 16-bit halves by a mask, codes 1 and 3 by a byte permute, and each
         // offset is one multiply-add on a half (1.5 instructions per code).
         const float* lut0 = lutl - (threadIdx.x & 15);
-        const uint32_t m4 = (fs8_lane_rec<true>() & 15u) * 4u;  // the lane's codebook column
+        const uint32_t m4 = (threadIdx.x & 15u) * 4u;
 #pragma unroll
         for (int gi = 0; gi < MT / 16; gi++) {
 #pragma unroll
@@ -1333,16 +1317,16 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
         const_cast<float*>(ix.tbias), (short)4, (int)(TR ? 16u * ix.tblk_count : 0u), 0x00020000);
     const bool packed = TR && P <= 64 && total < (1u << FS_LBL_BITS);  // wave-uniform
     auto fetch = [&](uint32_t rb, RoundRegs<MT>& g) {
-        if constexpr (TR) fs8t_fetch<MT, NC == 1>(rsc, rsb, s, sr, rb, P, cur, g, packed);
+        if constexpr (TR) fs8t_fetch<MT>(rsc, rsb, s, sr, rb, P, cur, g, packed);
         else fs8_fetch<MT>(ix, s, sr, rb, total, P, cur, g);
     };
     MapPipe mpp{0u, 0u, 0u, 0.0f};
     if (kMap && use_map) {  // the record of round 0 and the map byte of round 1
-        fs8m_record<NC == 1>(aux->map, 0u, fs8m_byte(aux->map, 0u), mpp);
+        fs8m_record(aux->map, 0u, fs8m_byte(aux->map, 0u), mpp);
         mpp.s4n = fs8m_byte(aux->map, FS_ROUND);
     }
     auto mfetch = [&](uint32_t rb, RoundRegs<MT>& g) {
-        if constexpr (kMap) fs8m_fetch<MT, NC == 1>(rsc, rsb, aux->map, rb, mpp, g);
+        if constexpr (kMap) fs8m_fetch<MT>(rsc, rsb, aux->map, rb, mpp, g);
     };
     // Whole groups of four rounds in the loop, which has no other exit (an
     // exit inside would make the loads of its first round look outstanding
