@@ -50,7 +50,7 @@ __device__ void topk_flush(TopkLds& t, int keep) {
     __syncthreads();
     int n = (int)*t.count;
     int n2 = next_pow2(n > 0 ? n : 1);
-    for (int i = n + threadIdx.x; i < n2; i += blockDim.x) {
+    for (int i = n + threadIdx.x; i < n2; i += SCAN_THREADS) {
         t.keys[i] = ~0ull;
         t.pos[i] = 0;
         t.probe[i] = 0;
@@ -63,17 +63,6 @@ __device__ void topk_flush(TopkLds& t, int keep) {
         }
     }
     __syncthreads();
-}
-
-__device__ __forceinline__ void topk_push(TopkLds& t, bool take, uint32_t fk, uint32_t pos,
-                                          int probe, const uint32_t* __restrict__ list_ids) {
-    int slot = wave_append_slot(take, t.count);
-    if (take) {
-        uint32_t vidx = list_ids[pos];
-        t.keys[slot] = ((uint64_t)fk << 32) | vidx;
-        t.pos[slot] = pos;
-        t.probe[slot] = (uint16_t)probe;
-    }
 }
 
 // Four table lookups from one code word, in codebook order.
@@ -119,6 +108,9 @@ struct ScanLds {
     float* qs;      // [d]
     float* rsd;     // [d] EXACT residual
     float* lut;     // [M*K]
+    float* rsd2;    // second residual and table (two lists per step), else rsd / lut
+    float* lut2;
+    int G;          // lists per step, 1 or 2
     uint32_t* lbeg; // [P]
     uint32_t* llen; // [P]
     uint32_t* lid;  // [P]
@@ -126,6 +118,8 @@ struct ScanLds {
     float* term0;   // [P]
     TopkLds tk;
     uint32_t* misc; // [4 + 2 SCAN_WAVES]
+    uint4* cst;     // [SCAN_THREADS] code row of the thread's first-round entry (M <= 16)
+    uint32_t* vst;  // [SCAN_THREADS] its vector index
 };
 
 // The buffer count as every thread of the block knows it, without reading
@@ -147,12 +141,15 @@ __host__ __device__ inline int scan_buf(int kk) {
     return b;
 }
 
-__host__ __device__ inline size_t scan_lds_layout(int d, int M, int K, int P, int buf,
-                                                  size_t* off /* 12 */) {
+// G residuals and tables (G lists scanned per step).
+__host__ __device__ inline size_t scan_lds_layout(int d, int M, int K, int P, int buf, int G,
+                                                  size_t* off /* 16 */) {
     size_t o = 0;
     off[0] = o; o = align16(o + (size_t)d * 4);          // qs
     off[1] = o; o = align16(o + (size_t)d * 4);          // rsd
+    off[14] = G == 2 ? o : off[1]; o = G == 2 ? align16(o + (size_t)d * 4) : o;          // rsd2
     off[2] = o; o = align16(o + (size_t)M * K * 4);      // lut
+    off[15] = G == 2 ? o : off[2]; o = G == 2 ? align16(o + (size_t)M * K * 4) : o;      // lut2
     off[3] = o; o = align16(o + (size_t)P * 4);          // lbeg
     off[4] = o; o = align16(o + (size_t)P * 4);          // llen
     off[5] = o; o = align16(o + (size_t)P * 4);          // lid
@@ -162,16 +159,29 @@ __host__ __device__ inline size_t scan_lds_layout(int d, int M, int K, int P, in
     off[9] = o; o = align16(o + (size_t)buf * 4);        // pos
     off[10] = o; o = align16(o + (size_t)buf * 2);       // probe
     off[11] = o; o = align16(o + 4 * (4 + 2 * SCAN_WAVES)); // misc: count, thr, 2 x 8 round counts
+    off[12] = o; o = align16(o + (size_t)SCAN_THREADS * 16);  // cst
+    off[13] = o; o = align16(o + (size_t)SCAN_THREADS * 4);   // vst
     return o;
 }
 
+// Two lists per step when their tables fit in half a CU's 160 KiB of LDS (so
+// two workgroups still share a CU), else one.
+#define SCAN_PAIR_LDS (80 * 1024)
+__host__ __device__ inline int scan_groups(int d, int M, int K, int P, int buf) {
+    size_t off[16];
+    return scan_lds_layout(d, M, K, P, buf, 2, off) <= SCAN_PAIR_LDS ? 2 : 1;
+}
+
 __device__ inline ScanLds carve(char* smem, int d, int M, int K, int P, int buf) {
-    size_t off[12];
-    scan_lds_layout(d, M, K, P, buf, off);
+    size_t off[16];
     ScanLds s;
+    s.G = scan_groups(d, M, K, P, buf);
+    scan_lds_layout(d, M, K, P, buf, s.G, off);
     s.qs = (float*)(smem + off[0]);
     s.rsd = (float*)(smem + off[1]);
     s.lut = (float*)(smem + off[2]);
+    s.rsd2 = (float*)(smem + off[14]);
+    s.lut2 = (float*)(smem + off[15]);
     s.lbeg = (uint32_t*)(smem + off[3]);
     s.llen = (uint32_t*)(smem + off[4]);
     s.lid = (uint32_t*)(smem + off[5]);
@@ -181,6 +191,8 @@ __device__ inline ScanLds carve(char* smem, int d, int M, int K, int P, int buf)
     s.tk.pos = (uint32_t*)(smem + off[9]);
     s.tk.probe = (uint16_t*)(smem + off[10]);
     s.misc = (uint32_t*)(smem + off[11]);
+    s.cst = (uint4*)(smem + off[12]);
+    s.vst = (uint32_t*)(smem + off[13]);
     s.tk.count = s.misc;
     s.tk.thr = s.misc + 1;
     return s;
@@ -191,8 +203,8 @@ __device__ inline ScanLds carve(char* smem, int d, int M, int K, int P, int buf)
 __device__ inline void load_query_and_lists(const DevIndex& ix, const ScanArgs& a, ScanLds& s,
                                             int q) {
     const int tid = threadIdx.x, d = ix.d, P = a.P > SCAN_LDS_P ? 0 : a.P;
-    for (int j = tid; j < d; j += blockDim.x) s.qs[j] = a.qn[(size_t)q * d + j];
-    for (int p = tid; p < P; p += blockDim.x) {
+    for (int j = tid; j < d; j += SCAN_THREADS) s.qs[j] = a.qn[(size_t)q * d + j];
+    for (int p = tid; p < P; p += SCAN_THREADS) {
         uint32_t l = a.probe[(size_t)q * P + p];
         if (l >= (uint32_t)ix.L) {  // no such list: scanned as empty
             s.lid[p] = 0;
@@ -222,7 +234,7 @@ __device__ inline void load_query_and_lists(const DevIndex& ix, const ScanArgs& 
 
 // Write the first kout sorted entries, padded (scan_emit).
 __device__ inline void write_out(const ScanArgs& a, ScanLds& s, int q, int n) {
-    for (int j = threadIdx.x; j < a.kout; j += blockDim.x) scan_emit(a, q, j, s.tk.keys[j], j < n);
+    for (int j = threadIdx.x; j < a.kout; j += SCAN_THREADS) scan_emit(a, q, j, s.tk.keys[j], j < n);
 }
 
 // Probed list l (slot p, entries beg .. beg + len - 1) with the reference
@@ -238,10 +250,10 @@ __device__ inline void stage_residual(const DevIndex& ix, const ScanArgs& a, con
     const int tid = threadIdx.x, d = ix.d;
     if (a.rres) {  // OPQ: R (q - c), formed by the rotation kernel (opq.rs:120-123)
         const float* rr = a.rres + ((size_t)q * a.P + p) * d;
-        for (int j = tid; j < d; j += blockDim.x) rsd[j] = rr[j];
+        for (int j = tid; j < d; j += SCAN_THREADS) rsd[j] = rr[j];
     } else {
         const float* c = ix.centroids + (size_t)l * d;
-        for (int j = tid; j < d; j += blockDim.x) rsd[j] = s.qs[j] - c[j];
+        for (int j = tid; j < d; j += SCAN_THREADS) rsd[j] = s.qs[j] - c[j];
     }
 }
 
@@ -250,18 +262,22 @@ __device__ inline void build_table(const DevIndex& ix, const float* rsd, float* 
                                    const float (&cw)[cw_count<MT, CWD>()]) {
     const int tid = threadIdx.x;
     const int M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, ds = ix.ds;
-    const int t = tid & 255, h = tid >> 8;  // codeword, codebook parity (wave-uniform)
+    const int t = tid & 255, h = (tid >> 8) & 1;  // codeword, codebook parity (wave-uniform)
     if constexpr (CWD < 0) {  // ds == W: codewords in registers, the next slice read ahead
         constexpr int W = -CWD;
+        static_assert(MT % 2 == 0 && KT == 256, "codebook pairs of ksub 256");
+        // one LDS base each, the codebook in the immediate offset: the slice
+        // of codebook m = 2 i + h at rr[2 i W], entry (m, t) at lw[512 i]
+        const float* rr = rsd + h * W;
+        float* lw = lut + (tid & 511);
         float rc[W], rn[W];
 #pragma unroll
-        for (int j = 0; j < W; j++) rc[j] = h < MT ? rsd[h * W + j] : 0.0f;
+        for (int j = 0; j < W; j++) rc[j] = rr[j];
 #pragma unroll
-        for (int i = 0; i < (MT + 1) / 2; i++) {
-            const int m = 2 * i + h;
-            if (i + 1 < (MT + 1) / 2) {
+        for (int i = 0; i < MT / 2; i++) {
+            if (i + 1 < MT / 2) {
 #pragma unroll
-                for (int j = 0; j < W; j++) rn[j] = m + 2 < MT ? rsd[(m + 2) * W + j] : 0.0f;
+                for (int j = 0; j < W; j++) rn[j] = rr[(2 * i + 2) * W + j];
             }
             float acc = 0.0f;
 #pragma unroll
@@ -269,7 +285,7 @@ __device__ inline void build_table(const DevIndex& ix, const float* rsd, float* 
                 float diff = rc[j] - cw[i * W + j];
                 acc += diff * diff;
             }
-            if (m < MT) lut[m * 256 + t] = acc;
+            lw[512 * i] = acc;
 #pragma unroll
             for (int j = 0; j < W; j++) rc[j] = rn[j];
             // two slices live at a time: the compiler may not hoist further reads
@@ -295,7 +311,7 @@ __device__ inline void build_table(const DevIndex& ix, const float* rsd, float* 
             __builtin_amdgcn_sched_barrier(0);
         }
     } else {
-        for (int e = tid; e < M * K; e += blockDim.x) {
+        for (int e = tid; e < M * K; e += SCAN_THREADS) {
             const int m = e / K;
             const float* cwp = ix.codebooks + (size_t)e * ds;
             float acc = 0.0f;
@@ -308,15 +324,146 @@ __device__ inline void build_table(const DevIndex& ix, const float* rsd, float* 
     }
 }
 
-// The entries of one list against its table; a block barrier ends every
-// round.  The flush decision uses the count every thread holds in tc, so it
-// is the same in every wave.
-template <int MT, int KT, bool FILT>
-__device__ inline void scan_entries(const DevIndex& ix, const ScanArgs& a, ScanLds& s, int buf, const float* lut,
-                                    uint32_t beg, uint32_t len, int p, const uint8_t* __restrict__ ecat,
-                                    uint8_t cq, TopkCnt& tc) {
+// The tables of a step: slot A's from s.rsd into s.lut and, when two, slot
+// B's from s.rsd2 into s.lut2.  With ds == -CWD (codewords in registers) the
+// two tables are built in one pass over the codebooks, each codeword register
+// serving both, and the second residual and table sit at fixed offsets from
+// the first (the layout places them back to back), so one LDS address serves
+// both.
+template <int MT, int KT, int CWD>
+__device__ inline void build_tables(const DevIndex& ix, const ScanLds& s, bool two,
+                                    const float (&cw)[cw_count<MT, CWD>()]) {
+    if constexpr (CWD < 0 && KT == 256) {
+        constexpr int W = -CWD;
+        constexpr int RS = (MT * W + 3) & ~3;  // floats from rsd to rsd2
+        constexpr int LS = MT * KT;            // floats from lut to lut2
+        const int tid = threadIdx.x, h = (tid >> 8) & 1;
+        if (!two) {
+            build_table<MT, KT, CWD>(ix, s.rsd, s.lut, cw);
+            return;
+        }
+        const float* rr = s.rsd + h * W;  // as in build_table, both tables off one base
+        float* lw = s.lut + (tid & 511);
+#pragma unroll
+        for (int i = 0; i < MT / 2; i++) {
+            float ra[W], rb[W];
+#pragma unroll
+            for (int j = 0; j < W; j++) {
+                ra[j] = rr[2 * i * W + j];
+                rb[j] = rr[RS + 2 * i * W + j];
+            }
+            float acc_a = 0.0f, acc_b = 0.0f;
+#pragma unroll
+            for (int j = 0; j < W; j++) {
+                const float da = ra[j] - cw[i * W + j], db = rb[j] - cw[i * W + j];
+                acc_a += da * da;
+                acc_b += db * db;
+            }
+            lw[512 * i] = acc_a;
+            lw[LS + 512 * i] = acc_b;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+        build_table<MT, KT, CWD>(ix, s.rsd, s.lut, cw);
+        if (two) build_table<MT, KT, CWD>(ix, s.rsd2, s.lut2, cw);
+    }
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Code rows of at most 16 bytes are read one slot ahead (pre_words words).
+template <int MT>
+constexpr int pre_words() {
+    return (MT == 4 || MT == 8 || MT == 16) ? MT / 4 : 0;
+}
+
+// s + the table entries of the code row held in words w, in codebook order
+// (the sum adc_sum forms from the row in memory).
+template <int MT, int KT>
+__device__ __forceinline__ float adc_words(const uint4& w, const float* __restrict__ lut, int K, float s) {
+    const int k = KT > 0 ? KT : K;
+    s = add4<KT>(s, w.x, lut, K);
+    if constexpr (MT >= 8) s = add4<KT>(s, w.y, lut + 4 * k, K);
+    if constexpr (MT >= 16) {
+        s = add4<KT>(s, w.z, lut + 8 * k, K);
+        s = add4<KT>(s, w.w, lut + 12 * k, K);
+    }
+    return s;
+}
+
+// A probe slot: its index, list, first entry and length (uniform).
+struct SlotRef {
+    int p;
+    uint32_t l, beg, len;
+};
+
+// The loads of the next step's slots A and B (B.len == 0 when there is no
+// B), issued while the current step is scanned: element tid of each residual
+// source (the centroid row, or with OPQ the rotated residual), and the vector
+// index and (M <= 16) code row of entry tid of A's list followed by B's,
+// which the step's first round scores.
+template <int MT>
+struct PairPre {
+    float ca, cb;
+    uint32_t vid;
+    uint4 w;
+};
+
+template <int MT>
+__device__ inline void pair_prefetch(const DevIndex& ix, const ScanArgs& a, int q, int P, const SlotRef& A,
+                                     const SlotRef& B, PairPre<MT>& pr) {
+    // Raw buffer loads over the slots' own ranges: uniform bases, 32-bit lane
+    // offsets, and lanes past a range read zeros without touching memory.
+    const uint32_t tid = threadIdx.x, d = (uint32_t)ix.d;
+    auto resid = [&](const SlotRef& X) {
+        const float* src = a.rres ? a.rres + ((size_t)q * a.P + X.p) * d : ix.centroids + (size_t)X.l * d;
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src), (short)0, (int)(d * 4u), 0x00020000);
+        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, tid * 4u, 0u, 0));
+    };
+    pr.ca = resid(A);
+    pr.cb = B.p < P ? resid(B) : 0.0f;
+    pr.vid = 0u;
+    pr.w = make_uint4(0u, 0u, 0u, 0u);
+    auto entry = [&](const SlotRef& X, uint32_t e) {
+        const __amdgpu_buffer_rsrc_t ri = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint32_t*>(ix.list_ids + X.beg), (short)0, (int)(X.len * 4u), 0x00020000);
+        pr.vid = __builtin_amdgcn_raw_buffer_load_b32(ri, e * 4u, 0u, 0);
+        if constexpr (pre_words<MT>() > 0) {
+            const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint8_t*>(ix.codes + (size_t)X.beg * MT), (short)0, (int)(X.len * (uint32_t)MT),
+                0x00020000);
+            if constexpr (pre_words<MT>() == 4) {
+                const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rw, e * 16u, 0u, 0);
+                pr.w = make_uint4(x[0], x[1], x[2], x[3]);
+            } else if constexpr (pre_words<MT>() == 2) {
+                const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rw, e * 8u, 0u, 0);
+                pr.w.x = x[0];
+                pr.w.y = x[1];
+            } else {
+                pr.w.x = __builtin_amdgcn_raw_buffer_load_b32(rw, e * 4u, 0u, 0);
+            }
+        }
+    };
+    if (tid < A.len) entry(A, tid);
+    else if (tid - A.len < B.len) entry(B, tid - A.len);
+}
+
+// The entries of list A, then of list B (B.len == 0: none), each against its
+// own table (lut_a, lut_b); a block barrier ends every round.  The flush
+// decision uses the count every thread holds in tc, so it is the same in every
+// wave.  PRE: the first round takes each thread's code row (M <= 16) and
+// vector index from s.cst / s.vst, staged by the thread itself from its
+// pair_prefetch loads.
+template <int MT, int KT, bool FILT, bool PRE = false>
+__device__ inline void scan_entries(const DevIndex& ix, const ScanArgs& a, ScanLds& s, int buf, const SlotRef& A,
+                                    const float* lut_a, const SlotRef& B, const float* lut_b,
+                                    const uint8_t* __restrict__ ecat, uint8_t cq, TopkCnt& tc) {
     const int tid = threadIdx.x;
     const int M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K;
+    static_assert(!PRE || SCAN_U == 1, "one staged entry per thread");
+    const uint32_t len = A.len + B.len;
     for (uint32_t base = 0; base < len; base += SCAN_ROUND) {
         if (tc.n > (uint32_t)(buf - SCAN_ROUND)) {
             topk_flush(s.tk, a.kk);
@@ -329,16 +476,27 @@ __device__ inline void scan_entries(const DevIndex& ix, const ScanArgs& a, ScanL
             uint32_t i = base + u * SCAN_THREADS + tid;
             bool take = false;
             uint32_t fk = 0, pos = 0;
+            const bool staged = PRE && base == 0;  // uniform
+            const bool in_a = i < A.len;
+            const int p = in_a ? A.p : B.p;
             if (i < len) {
-                pos = beg + i;
+                pos = in_a ? A.beg + i : B.beg + (i - A.len);
                 if (!FILT || ecat[pos] == cq) {
-                    float dist = adc_sum<MT, KT>(ix.codes + (size_t)pos * M, lut, M, K, 0.0f);
+                    const float* lut = in_a ? lut_a : lut_b;
+                    float dist;
+                    if (staged && pre_words<MT>() > 0) dist = adc_words<MT, KT>(s.cst[tid], lut, K, 0.0f);
+                    else dist = adc_sum<MT, KT>(ix.codes + (size_t)pos * M, lut, M, K, 0.0f);
                     fk = fkey(dist);
                     take = fk <= thr;
                 }
             }
             wn += (uint32_t)__popcll(__ballot(take));
-            topk_push(s.tk, take, fk, pos, p, ix.list_ids);
+            const int slot = wave_append_slot(take, s.tk.count);
+            if (take) {
+                s.tk.keys[slot] = ((uint64_t)fk << 32) | (staged ? s.vst[tid] : ix.list_ids[pos]);
+                s.tk.pos[slot] = pos;
+                s.tk.probe[slot] = (uint16_t)p;
+            }
         }
         if ((tid & 63) == 0) s.misc[4 + SCAN_WAVES * tc.par + (tid >> 6)] = wn;
         __syncthreads();
@@ -357,7 +515,8 @@ __device__ inline void scan_list(const DevIndex& ix, const ScanArgs& a, ScanLds&
     __syncthreads();
     build_table<MT, KT, CWD>(ix, s.rsd, s.lut, cw);
     __syncthreads();
-    scan_entries<MT, KT, FILT>(ix, a, s, buf, s.lut, beg, len, p, ecat, cq, tc);
+    const SlotRef A{p, l, beg, len}, none{0, 0u, 0u, 0u};
+    scan_entries<MT, KT, FILT>(ix, a, s, buf, A, s.lut, none, s.lut, ecat, cq, tc);
 }
 
 // Codeword t = tid % 256 of the codebooks h, h + 2, ... (h = tid / 256) into
@@ -367,7 +526,7 @@ template <int MT, int CWD>
 __device__ inline void load_codewords(const DevIndex& ix, float (&cw)[cw_count<MT, CWD>()]) {
     if constexpr (CWD != 0) {
         constexpr int W = CWD > 0 ? CWD : -CWD;
-        const int t = threadIdx.x & 255, h = threadIdx.x >> 8, ds = CWD > 0 ? ix.ds : W;
+        const int t = threadIdx.x & 255, h = (threadIdx.x >> 8) & 1, ds = CWD > 0 ? ix.ds : W;
 #pragma unroll
         for (int i = 0; i < (MT + 1) / 2; i++) {
             const int m = 2 * i + h;
@@ -380,13 +539,14 @@ __device__ inline void load_codewords(const DevIndex& ix, float (&cw)[cw_count<M
 
 // One query with the reference arithmetic; every thread of the block calls it.
 template <int MT, int KT, int CWD>
-__device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char* smem, int q) {
+__device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char* smem, int q,
+                            const float (&cw)[cw_count<MT, CWD>()]) {
     const int tid = threadIdx.x;
-    const int d = ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, P = a.P;
+    // with ds == -CWD the dimension is MT * ds: compile-time, and so are the
+    // LDS offsets of the query, residuals and tables
+    const int d = CWD < 0 ? MT * -CWD : ix.d, M = MT > 0 ? MT : ix.M, K = KT > 0 ? KT : ix.K, P = a.P;
     const bool wide = P > SCAN_LDS_P;
     ScanLds s = carve(smem, d, M, K, wide ? 0 : P, buf);
-    float cw[cw_count<MT, CWD>()];
-    load_codewords<MT, CWD>(ix, cw);
     load_query_and_lists(ix, a, s, q);
     // list, begin and length of probe slot p (the same for every thread)
     auto slot = [&](int p, uint32_t& l, uint32_t& beg, uint32_t& len) {
@@ -395,21 +555,63 @@ __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char
             const bool ok = l < (uint32_t)ix.L;
             beg = ok ? ix.offsets[l] : 0u;
             len = ok ? ix.offsets[l + 1] - beg : 0u;
-        } else {
-            l = s.lid[p];
-            beg = s.lbeg[p];
-            len = s.llen[p];
+        } else {  // uniform: held in scalar registers
+            l = __builtin_amdgcn_readfirstlane(s.lid[p]);
+            beg = __builtin_amdgcn_readfirstlane(s.lbeg[p]);
+            len = __builtin_amdgcn_readfirstlane(s.llen[p]);
         }
     };
     uint32_t total = 0;
+    // the first non-empty slot at or after `from` ({P, 0, 0, 0} when there is none)
+    auto next = [&](int from, SlotRef& x) {
+        x = SlotRef{P, 0u, 0u, 0u};
+        for (int pn = from; pn < P; pn++) {
+            uint32_t l, beg, len;
+            slot(pn, l, beg, len);
+            total += len;
+            if (len != 0u) {
+                x = SlotRef{pn, l, beg, len};
+                break;
+            }
+        }
+    };
+    // the next step's slots: A, and B after it when two lists fit per step
+    auto step = [&](int from, SlotRef& x, SlotRef& y) {
+        next(from, x);
+        y = SlotRef{P, 0u, 0u, 0u};
+        if (s.G == 2 && x.p < P) next(x.p + 1, y);
+    };
+    // the residual of slot x into r, from the element tid loaded a step ahead
+    auto stage = [&](const SlotRef& x, float c, float* r) {
+        if (tid < d) r[tid] = a.rres ? c : s.qs[tid] - c;
+        for (int j = tid + SCAN_THREADS; j < d; j += SCAN_THREADS)
+            r[j] = a.rres ? a.rres[((size_t)q * P + x.p) * d + j] : s.qs[j] - ix.centroids[(size_t)x.l * d + j];
+    };
     TopkCnt tc;
-    for (int p = 0; p < P; p++) {
+    PairPre<MT> pre;
+    SlotRef A, B;
+    step(0, A, B);
+    if (A.p < P) pair_prefetch<MT>(ix, a, q, P, A, B, pre);
+    // Each step: the residuals from the elements loaded a step earlier, the
+    // loads of the next step issued, the tables, then the entries of both
+    // lists (the first round from the staged code rows).
+    while (A.p < P) {
+        SlotRef nA, nB;
+        step((B.p < P ? B.p : A.p) + 1, nA, nB);
+        __syncthreads();  // the previous step's residuals, tables and staging are no longer read
+        stage(A, pre.ca, s.rsd);
+        if (B.p < P) stage(B, pre.cb, s.rsd2);
+        if ((uint32_t)tid < A.len + B.len) {  // read back by this thread only
+            if constexpr (pre_words<MT>() > 0) s.cst[tid] = pre.w;
+            s.vst[tid] = pre.vid;
+        }
+        if (nA.p < P) pair_prefetch<MT>(ix, a, q, P, nA, nB, pre);
         __syncthreads();
-        uint32_t l, beg, len;
-        slot(p, l, beg, len);
-        total += len;
-        if (len == 0) continue;
-        scan_list<MT, KT, false, CWD>(ix, a, s, buf, l, beg, len, q, p, nullptr, 0, cw, tc);
+        build_tables<MT, KT, CWD>(ix, s, B.p < P, cw);
+        __syncthreads();
+        scan_entries<MT, KT, false, true>(ix, a, s, buf, A, s.lut, B, s.lut2, nullptr, 0, tc);
+        A = nA;
+        B = nB;
     }
     topk_flush(s.tk, a.kk);
     const int n = (int)*s.tk.count;
@@ -439,7 +641,7 @@ __global__ __launch_bounds__(SCAN_THREADS, 4) void scan8_filtered_kernel(DevInde
     ScanLds s = carve(smem, d, M, K, 0, buf);
     float cw[cw_count<MT, CWD>()];
     load_codewords<MT, CWD>(ix, cw);
-    for (int j = tid; j < d; j += blockDim.x) s.qs[j] = a.qn[(size_t)q * d + j];
+    for (int j = tid; j < d; j += SCAN_THREADS) s.qs[j] = a.qn[(size_t)q * d + j];
     if (tid == 0) {
         *s.tk.count = 0;
         *s.tk.thr = 0xffffffffu;
@@ -467,10 +669,13 @@ __global__ __launch_bounds__(SCAN_THREADS, 4) void scan8_exact_kernel(DevIndex i
     // One call site, so the query body is inlined once.
     const uint32_t nf = a.only_flagged ? *a.flag_count : (uint32_t)a.nq;
     const uint32_t step = a.only_flagged ? gridDim.x : nf;
+    if (blockIdx.x >= nf) return;
+    float cw[cw_count<MT, CWD>()];  // the same for every query
+    load_codewords<MT, CWD>(ix, cw);
     for (uint32_t fi = blockIdx.x; fi < nf; fi += step) {
         __syncthreads();
         const int q = a.only_flagged ? (int)a.flag_list[fi] : (int)fi;
-        exact_query<MT, KT, CWD>(ix, a, buf, smem, q);
+        exact_query<MT, KT, CWD>(ix, a, buf, smem, q, cw);
     }
 }
 
@@ -483,8 +688,9 @@ constexpr int cw_regs() {
 }
 
 size_t scan8_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
-    size_t off[12];
-    return scan_lds_layout(ix.d, ix.M, ix.K, a.P > SCAN_LDS_P ? 0 : a.P, scan_buf(a.kk), off);
+    size_t off[16];
+    const int P = a.P > SCAN_LDS_P ? 0 : a.P, buf = scan_buf(a.kk);
+    return scan_lds_layout(ix.d, ix.M, ix.K, P, buf, scan_groups(ix.d, ix.M, ix.K, P, buf), off);
 }
 
 template <int MT, int KT>
@@ -525,8 +731,8 @@ template <int MT, int KT>
 static void launch_filtered_mk(const DevIndex& ix, const ScanArgs& a, const uint8_t* ecat,
                                const uint8_t* want, hipStream_t s) {
     const int buf = scan_buf(a.kk);
-    size_t off[12];
-    const size_t lds = scan_lds_layout(ix.d, ix.M, ix.K, 0, buf, off);
+    size_t off[16];
+    const size_t lds = scan_lds_layout(ix.d, ix.M, ix.K, 0, buf, scan_groups(ix.d, ix.M, ix.K, 0, buf), off);
     constexpr int CWD = cw_regs<MT, KT>();
     auto k = (CWD > 0 && ix.ds == CWD)  ? scan8_filtered_kernel<MT, KT, -CWD>
              : (CWD > 0 && ix.ds < CWD) ? scan8_filtered_kernel<MT, KT, CWD>
