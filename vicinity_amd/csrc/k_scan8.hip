@@ -37,25 +37,102 @@ constexpr int cw_count() {
 #define SCAN_LDS_P 1024
 
 struct TopkLds {
-    uint64_t* keys;  // (distance key << 32) | insertion index
-    uint32_t* pos;   // list-major position of the entry
-    uint16_t* probe; // probe slot (which probed list)
+    uint64_t* keys;  // (distance key << 32) | vector index
     uint32_t* count;
     uint32_t* thr;   // distance key threshold: accept fkey(dist) <= thr
 };
 
+// Ascending sort of the N = SCAN_THREADS * E keys in LDS, in place.  Lane l
+// of wave w holds element w * 64 E + 64 j + l in k[j]: the bitonic stages of
+// strides below 64 exchange registers between lanes, those of strides 64 to
+// 64 E - 1 between a thread's own registers, and only the strides of 64 E and
+// up (across waves) go through LDS, two barriers each.
+template <int E>
+__device__ void scan_sort_keys(uint64_t* keys) {
+    constexpr int N = SCAN_THREADS * E, WE = 64 * E;
+    const int lane = threadIdx.x & 63, wbase = (threadIdx.x >> 6) * WE + lane;
+    uint64_t k[E];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < E; j++) k[j] = keys[wbase + 64 * j];
+#pragma unroll
+    for (int size = 2; size <= N; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride >= WE) {
+                __syncthreads();  // the previous exchange's reads are done
+#pragma unroll
+                for (int j = 0; j < E; j++) keys[wbase + 64 * j] = k[j];
+                __syncthreads();
+#pragma unroll
+                for (int j = 0; j < E; j++) {
+                    const int e = wbase + 64 * j;
+                    const uint64_t o = keys[e ^ stride];
+                    k[j] = ((e & stride) == 0) == ((e & size) == 0) ? min(o, k[j]) : max(o, k[j]);
+                }
+            } else if (stride >= 64) {
+                const int js = stride >> 6;
+#pragma unroll
+                for (int j = 0; j < E; j++) {
+                    const int f = j ^ js;
+                    if (f > j) {
+                        const bool asc = ((wbase + 64 * j) & size) == 0;
+                        const uint64_t a = k[j], b = k[f];
+                        k[j] = asc ? min(a, b) : max(a, b);
+                        k[f] = asc ? max(a, b) : min(a, b);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < E; j++) {
+                    const int e = wbase + 64 * j;
+                    const uint64_t o = shfl_xor_u64(k[j], stride);
+                    k[j] = ((e & stride) == 0) == ((e & size) == 0) ? min(o, k[j]) : max(o, k[j]);
+                }
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < E; j++) keys[wbase + 64 * j] = k[j];
+    __syncthreads();
+}
+
+// Ascending bitonic sort of keys[0..n) in LDS (n a power of two), every
+// thread of the block taking pairs.
+__device__ void scan_sort_keys_lds(uint64_t* keys, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (int t = threadIdx.x; t < (n >> 1); t += SCAN_THREADS) {
+                const int i = 2 * t - (t & (stride - 1)), j = i + stride;
+                const bool asc = (i & size) == 0;
+                const uint64_t a = keys[i], b = keys[j];
+                if ((a > b) == asc) {
+                    keys[i] = b;
+                    keys[j] = a;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // Sort the buffer and keep the best `keep` entries; later candidates must beat
-// the keep-th distance.  All threads call it.
+// the keep-th distance.  All threads call it.  The keys are unique (vector
+// index in the low word), so the kept set is the same whatever order the
+// candidates arrived in.  REG: the register sort (a final flush, when the
+// caller holds no other large register state), else the LDS sort.
+template <bool REG>
 __device__ void topk_flush(TopkLds& t, int keep) {
     __syncthreads();
-    int n = (int)*t.count;
-    int n2 = next_pow2(n > 0 ? n : 1);
-    for (int i = n + threadIdx.x; i < n2; i += SCAN_THREADS) {
-        t.keys[i] = ~0ull;
-        t.pos[i] = 0;
-        t.probe[i] = 0;
-    }
-    block_bitonic_sort2(t.keys, t.pos, t.probe, n2);
+    const int n = (int)*t.count;
+    const int n2 = next_pow2(n > 0 ? n : 1);
+    const int N = n2 < SCAN_THREADS ? SCAN_THREADS : n2;  // the buffer holds at least 2 x SCAN_THREADS
+    for (int i = n + threadIdx.x; i < N; i += SCAN_THREADS) t.keys[i] = ~0ull;
+    if (REG && N == SCAN_THREADS) scan_sort_keys<1>(t.keys);
+    else if (REG && N == 2 * SCAN_THREADS) scan_sort_keys<2>(t.keys);
+    else scan_sort_keys_lds(t.keys, N);
     if (threadIdx.x == 0) {
         if (n >= keep) {
             *t.thr = (uint32_t)(t.keys[keep - 1] >> 32);
@@ -156,8 +233,6 @@ __host__ __device__ inline size_t scan_lds_layout(int d, int M, int K, int P, in
     off[6] = o; o = align16(o + (size_t)(P + 1) * 4);    // pref
     off[7] = o; o = align16(o + (size_t)P * 4);          // term0
     off[8] = o; o = align16(o + (size_t)buf * 8);        // keys
-    off[9] = o; o = align16(o + (size_t)buf * 4);        // pos
-    off[10] = o; o = align16(o + (size_t)buf * 2);       // probe
     off[11] = o; o = align16(o + 4 * (4 + 2 * SCAN_WAVES)); // misc: count, thr, 2 x 8 round counts
     off[12] = o; o = align16(o + (size_t)SCAN_THREADS * 16);  // cst
     off[13] = o; o = align16(o + (size_t)SCAN_THREADS * 4);   // vst
@@ -188,8 +263,6 @@ __device__ inline ScanLds carve(char* smem, int d, int M, int K, int P, int buf)
     s.pref = (uint32_t*)(smem + off[6]);
     s.term0 = (float*)(smem + off[7]);
     s.tk.keys = (uint64_t*)(smem + off[8]);
-    s.tk.pos = (uint32_t*)(smem + off[9]);
-    s.tk.probe = (uint16_t*)(smem + off[10]);
     s.misc = (uint32_t*)(smem + off[11]);
     s.cst = (uint4*)(smem + off[12]);
     s.vst = (uint32_t*)(smem + off[13]);
@@ -466,7 +539,7 @@ __device__ inline void scan_entries(const DevIndex& ix, const ScanArgs& a, ScanL
     const uint32_t len = A.len + B.len;
     for (uint32_t base = 0; base < len; base += SCAN_ROUND) {
         if (tc.n > (uint32_t)(buf - SCAN_ROUND)) {
-            topk_flush(s.tk, a.kk);
+            topk_flush<false>(s.tk, a.kk);
             tc.n = tc.n >= (uint32_t)a.kk ? (uint32_t)a.kk : tc.n;  // the flush keeps kk when it has them
         }
         const uint32_t thr = *s.tk.thr;
@@ -478,7 +551,6 @@ __device__ inline void scan_entries(const DevIndex& ix, const ScanArgs& a, ScanL
             uint32_t fk = 0, pos = 0;
             const bool staged = PRE && base == 0;  // uniform
             const bool in_a = i < A.len;
-            const int p = in_a ? A.p : B.p;
             if (i < len) {
                 pos = in_a ? A.beg + i : B.beg + (i - A.len);
                 if (!FILT || ecat[pos] == cq) {
@@ -492,11 +564,7 @@ __device__ inline void scan_entries(const DevIndex& ix, const ScanArgs& a, ScanL
             }
             wn += (uint32_t)__popcll(__ballot(take));
             const int slot = wave_append_slot(take, s.tk.count);
-            if (take) {
-                s.tk.keys[slot] = ((uint64_t)fk << 32) | (staged ? s.vst[tid] : ix.list_ids[pos]);
-                s.tk.pos[slot] = pos;
-                s.tk.probe[slot] = (uint16_t)p;
-            }
+            if (take) s.tk.keys[slot] = ((uint64_t)fk << 32) | (staged ? s.vst[tid] : ix.list_ids[pos]);
         }
         if ((tid & 63) == 0) s.misc[4 + SCAN_WAVES * tc.par + (tid >> 6)] = wn;
         __syncthreads();
@@ -613,7 +681,7 @@ __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char
         A = nA;
         B = nB;
     }
-    topk_flush(s.tk, a.kk);
+    topk_flush<true>(s.tk, a.kk);
     const int n = (int)*s.tk.count;
     if (tid == 0 && !a.only_flagged) {
         uint32_t* st = a.qstat + (size_t)q * QSTAT_WORDS;
@@ -656,7 +724,7 @@ __global__ __launch_bounds__(SCAN_THREADS, 4) void scan8_filtered_kernel(DevInde
         if (len == 0) continue;
         scan_list<MT, KT, true, CWD>(ix, a, s, buf, l, beg, len, q, p, ecat, cq, cw, tc);
     }
-    topk_flush(s.tk, a.kk);
+    topk_flush<true>(s.tk, a.kk);
     const int n = (int)*s.tk.count;
     write_out(a, s, q, n < a.kout ? n : a.kout);
 }
