@@ -98,12 +98,24 @@ __device__ void scan_sort_keys(uint64_t* keys) {
     __syncthreads();
 }
 
-// Ascending bitonic sort of keys[0..n) in LDS (n a power of two), every
-// thread of the block taking pairs.
+// Ascending bitonic sort of keys[0..n) in LDS (n a power of two), thread t
+// taking pairs t, t + SCAN_THREADS, ...  Pair t lies in the 128-key chunk t /
+// 64 for strides up to 64, and every pair of a chunk belongs to one wave, so
+// such a stage waits only for its own wave when the stage before it was also
+// chunk-local; the stages of strides 128 and up, and the stage after each,
+// wait for the block.
 __device__ void scan_sort_keys_lds(uint64_t* keys, int n) {
+    bool prev_wide = true;  // the caller's writes: the first stage waits for the block
     for (int size = 2; size <= n; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            __syncthreads();
+            const bool wide = stride >= 128;
+            if (wide || prev_wide) {
+                __syncthreads();
+            } else {
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+            }
+            prev_wide = wide;
             for (int t = threadIdx.x; t < (n >> 1); t += SCAN_THREADS) {
                 const int i = 2 * t - (t & (stride - 1)), j = i + stride;
                 const bool asc = (i & size) == 0;
@@ -666,7 +678,8 @@ __device__ void exact_query(const DevIndex& ix, const ScanArgs& a, int buf, char
     while (A.p < P) {
         SlotRef nA, nB;
         step((B.p < P ? B.p : A.p) + 1, nA, nB);
-        __syncthreads();  // the previous step's residuals, tables and staging are no longer read
+        // no barrier: the last round of the previous step ended with one, after
+        // every read of its residuals, tables and staged rows
         stage(A, pre.ca, s.rsd);
         if (B.p < P) stage(B, pre.cb, s.rsd2);
         if ((uint32_t)tid < A.len + B.len) {  // read back by this thread only
