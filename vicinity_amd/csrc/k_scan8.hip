@@ -9,6 +9,9 @@
 // EXACT mode restates the reference arithmetic: per probed list the residual
 // r = q - c and the table LUT[m][k] = sum_j (r_j - cw_j)^2 (sub, mul, add in
 // order) live in LDS; each candidate sums its M entries in codebook order.
+// A step takes two probed lists when both tables fit (built in one pass over
+// the codebooks, scanned in one set of rounds), with the next step's residual
+// elements, list ids and code rows already loading.
 //
 // This kernel serves EXACT mode and the queries FAST mode (k_scan8_fast.hip)
 // could not prove; it writes the same rows FAST mode would have written.
