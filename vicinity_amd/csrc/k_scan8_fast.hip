@@ -990,17 +990,17 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
         if constexpr (TR) s.tbo[p] = rt;
     };
     if (tid < 32) s.misc[tid] = tid == 8 ? 0xffffffffu : 0u;  // counts 0, no bound yet
-    // PRE: eight lanes per probed slot (the first PG slots) hold the residual
-    // r = q - c of their slot (dimensions 32 i + 4 sub .. + 3, the reference's
-    // single subtraction) from the prologue to the rescoring, which stages it
-    // in LDS without loading the centroids again.
+    // PRE: eight lanes per probed slot (the first PG slots) form ||q - c||^2
+    // of their slot here.  The residual itself is not held until the
+    // rescoring: sixteen more registers across the main pass spilled 32 bytes
+    // per lane to scratch (70 MB of writes per 10k batch); the rescoring
+    // stages it again from the centroids.
     constexpr int PG = VGPU_BLOCK / 8;
-    float4 rres[PRE ? D / 32 : 1];
     if constexpr (PRE) {
         // Two round trips.  First: the query's table (LUTF floats, coalesced
         // 16-byte pieces), the query, the thread's probed slot and the slot of
         // its eight-lane group.  Second: the slot's list record and the group
-        // slot's centroid slices, from which ||q - c||^2 and r follow.
+        // slot's centroid slices, from which ||q - c||^2 follows.
         constexpr int TPT = LUTF / 4 / VGPU_BLOCK;  // 16-byte pieces per thread
         static_assert(LUTF % (4 * VGPU_BLOCK) == 0 && D % 32 == 0 && D / 4 <= VGPU_BLOCK, "table copy split");
         const float4* src = reinterpret_cast<const float4*>(a.t2 + (size_t)q * LUTF);
@@ -1032,12 +1032,12 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
         float acc = 0.0f;  // ||q - c||^2, ranking only: any order, FMA allowed
 #pragma unroll
         for (int i = 0; i < D / 32; i++) {
-            rres[i] = make_float4(__fsub_rn(qsl[i].x, cv[i].x), __fsub_rn(qsl[i].y, cv[i].y),
-                                  __fsub_rn(qsl[i].z, cv[i].z), __fsub_rn(qsl[i].w, cv[i].w));
-            acc = __builtin_fmaf(rres[i].x, rres[i].x, acc);
-            acc = __builtin_fmaf(rres[i].y, rres[i].y, acc);
-            acc = __builtin_fmaf(rres[i].z, rres[i].z, acc);
-            acc = __builtin_fmaf(rres[i].w, rres[i].w, acc);
+            const float4 r = make_float4(__fsub_rn(qsl[i].x, cv[i].x), __fsub_rn(qsl[i].y, cv[i].y),
+                                         __fsub_rn(qsl[i].z, cv[i].z), __fsub_rn(qsl[i].w, cv[i].w));
+            acc = __builtin_fmaf(r.x, r.x, acc);
+            acc = __builtin_fmaf(r.y, r.y, acc);
+            acc = __builtin_fmaf(r.z, r.z, acc);
+            acc = __builtin_fmaf(r.w, r.w, acc);
         }
         acc += __uint_as_float(shfl_xor_u32(__float_as_uint(acc), 1));
         acc += __uint_as_float(shfl_xor_u32(__float_as_uint(acc), 2));
@@ -1469,15 +1469,8 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
     // dimensions 4 (t % (D / 4)) .. + 3 of slots t / (D / 4), + SPT, ...: the
     // slot ids are read first and every centroid load is in flight at once
     // (a store to the table region could otherwise hold back the next id read).
-    if constexpr (PRE) {
-        if (P <= PG && (tid >> 3) < P) {  // the residuals held since the prologue
-            float* o = s.lut + (tid >> 3) * D + 4 * (tid & 7);
-#pragma unroll
-            for (int i = 0; i < D / 32; i++) *reinterpret_cast<float4*>(o + 32 * i) = rres[i];
-        }
-    }
     if constexpr ((MT == 8 || MT == 16 || MT == 32) && KT > 0 && DS > 0) {
-        if ((size_t)P * D <= (size_t)LUTF && (!PRE || P > PG)) {
+        if ((size_t)P * D <= (size_t)LUTF) {
             constexpr int SPT = VGPU_BLOCK / (D / 4);         // slots per pass
             constexpr int SMAX = (LUTF / D + SPT - 1) / SPT;  // passes for P D <= LUTF
             static_assert(VGPU_BLOCK % (D / 4) == 0, "staging split");
