@@ -745,21 +745,28 @@ __global__ __launch_bounds__(SCAN_THREADS, 4) void scan8_filtered_kernel(DevInde
     write_out(a, s, q, n < a.kout ? n : a.kout);
 }
 
-template <int MT, int KT, int CWD>
+// FL = false: every query of the batch, block q taking query q.  FL = true:
+// the flagged queries the FAST kernel listed before this launch, the blocks
+// striding over the list.  Two kernels, each with one call site of the query
+// body: a loop over queries in the whole-batch kernel would keep the body's
+// per-lane addresses live across it (they are loop-invariant) and spill them
+// to scratch in every workgroup.
+template <int MT, int KT, int CWD, bool FL>
 __global__ __launch_bounds__(SCAN_THREADS, 4) void scan8_exact_kernel(DevIndex ix, ScanArgs a, int buf) {
     extern __shared__ __align__(16) char smem[];
-    // Every query of the batch (block q takes query q), or the flagged queries
-    // the FAST kernel listed before this launch (blocks stride over the list).
-    // One call site, so the query body is inlined once.
-    const uint32_t nf = a.only_flagged ? *a.flag_count : (uint32_t)a.nq;
-    const uint32_t step = a.only_flagged ? gridDim.x : nf;
-    if (blockIdx.x >= nf) return;
     float cw[cw_count<MT, CWD>()];  // the same for every query
-    load_codewords<MT, CWD>(ix, cw);
-    for (uint32_t fi = blockIdx.x; fi < nf; fi += step) {
-        __syncthreads();
-        const int q = a.only_flagged ? (int)a.flag_list[fi] : (int)fi;
-        exact_query<MT, KT, CWD>(ix, a, buf, smem, q, cw);
+    if constexpr (!FL) {
+        if (blockIdx.x >= (uint32_t)a.nq) return;
+        load_codewords<MT, CWD>(ix, cw);
+        exact_query<MT, KT, CWD>(ix, a, buf, smem, (int)blockIdx.x, cw);
+    } else {
+        const uint32_t nf = *a.flag_count;
+        if (blockIdx.x >= nf) return;
+        load_codewords<MT, CWD>(ix, cw);
+        for (uint32_t fi = blockIdx.x; fi < nf; fi += gridDim.x) {
+            __syncthreads();
+            exact_query<MT, KT, CWD>(ix, a, buf, smem, (int)a.flag_list[fi], cw);
+        }
     }
 }
 
@@ -782,9 +789,13 @@ static void launch_mk(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     int buf = scan_buf(a.kk);
     size_t lds = scan8_lds_bytes(ix, a);
     constexpr int CWD = cw_regs<MT, KT>();
-    auto k = (CWD > 0 && ix.ds == CWD)  ? scan8_exact_kernel<MT, KT, -CWD>
-             : (CWD > 0 && ix.ds < CWD) ? scan8_exact_kernel<MT, KT, CWD>
-                                        : scan8_exact_kernel<MT, KT, 0>;
+    auto pick = [&](auto fl) {
+        constexpr bool FL = decltype(fl)::value;
+        return (CWD > 0 && ix.ds == CWD)  ? scan8_exact_kernel<MT, KT, -CWD, FL>
+               : (CWD > 0 && ix.ds < CWD) ? scan8_exact_kernel<MT, KT, CWD, FL>
+                                          : scan8_exact_kernel<MT, KT, 0, FL>;
+    };
+    auto k = a.only_flagged ? pick(std::true_type{}) : pick(std::false_type{});
     ensure_dyn_lds((const void*)k, lds);
     // Flagged queries: a small grid walks the list the FAST kernel wrote.
     // flagged queries are rare: a small grid keeps the usual empty launch cheap
