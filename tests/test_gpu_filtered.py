@@ -80,6 +80,24 @@ def test_filtered_search_is_bitexact(k256, k):
         assert all(cat[np.flatnonzero(art["doc_ids"] == i)[0]] == g for i in ids.tolist())
 
 
+@pytest.mark.parametrize("d,M", [(64, 16), (64, 8), (32, 16)])
+def test_filtered_widths_against_oracle(vg, oracle, d, M):
+    """Subvector widths a half or a quarter of the widest the kernels hold in
+    registers (4, 8 and 2 floats)."""
+    from vicinity_amd import MetadataFilter
+
+    _print_case(f"build filtered index 4000 x {d}, nlist 16, M {M}, ksub 256")
+    ix, rng = _build(vg, 4000, d, 16, M, 256, 3, 3 + d + M)
+    art = ix.export()
+    oix, cat = _oracle_index(oracle, art), _categories(art, _group_of)
+    for k in (10, 100):
+        for t in range(6):
+            q = rng.standard_normal(d).astype(np.float32)
+            ids, dists = ix.search_with_filter(q, k, MetadataFilter.equals("group", t % 7))
+            oids, odists = oix.search_filtered(q, k, 3, t % 7, cat)
+            assert ids.tolist() == oids.tolist() and dists.tobytes() == odists.tobytes(), (k, t)
+
+
 def test_ksub16_uses_the_table_arithmetic(vg, oracle):
     _print_case("build filtered index 3000 x 16, nlist 16, M 4, ksub 16")
     ix, rng = _build(vg, 3000, 16, 16, 4, 16, 2, 2)

@@ -772,10 +772,30 @@ __global__ __launch_bounds__(SCAN_THREADS, 4) void scan8_exact_kernel(DevIndex i
 
 // Codewords held per thread: ksub 256 with a fixed codebook count and
 // d <= 128 (M * ds floats per thread); 0 = read the codebooks per list.  The
-// kernels take -cw_regs when ds is exactly that width.
+// kernels take -W when ds is exactly W = cw_regs, cw_regs / 2 or cw_regs / 4
+// (W >= 2: compile-time d, no guards), cw_regs for other ds below it.  At
+// d 64 the guarded variant took 2.25x (16 codebooks) and 1.57x (32) the time
+// of the exact-width one: its codeword guards, and 56 to 136 bytes per lane of
+// spills.
 template <int MT, int KT>
 constexpr int cw_regs() {
     return (KT == 256 && MT > 0 && MT <= 64) ? 128 / MT : 0;
+}
+
+// The codeword width parameter for a run-time ds: -W, CWD, or 0 (see cw_regs),
+// as the kernel template `K` instantiated at it.
+template <int CWD, typename Fn, typename K>
+static Fn cw_pick(int ds, K kern) {
+    Fn f = kern(std::integral_constant<int, 0>{});
+    if constexpr (CWD > 0) {
+        if (ds == CWD) f = kern(std::integral_constant<int, -CWD>{});
+        else if (ds < CWD) f = kern(std::integral_constant<int, CWD>{});
+        if constexpr (CWD >= 4)
+            if (ds == CWD / 2) f = kern(std::integral_constant<int, -(CWD / 2)>{});
+        if constexpr (CWD >= 8)
+            if (ds == CWD / 4) f = kern(std::integral_constant<int, -(CWD / 4)>{});
+    }
+    return f;
 }
 
 size_t scan8_lds_bytes(const DevIndex& ix, const ScanArgs& a) {
@@ -791,9 +811,10 @@ static void launch_mk(const DevIndex& ix, const ScanArgs& a, hipStream_t s) {
     constexpr int CWD = cw_regs<MT, KT>();
     auto pick = [&](auto fl) {
         constexpr bool FL = decltype(fl)::value;
-        return (CWD > 0 && ix.ds == CWD)  ? scan8_exact_kernel<MT, KT, -CWD, FL>
-               : (CWD > 0 && ix.ds < CWD) ? scan8_exact_kernel<MT, KT, CWD, FL>
-                                          : scan8_exact_kernel<MT, KT, 0, FL>;
+        using Fn = void (*)(DevIndex, ScanArgs, int);
+        return cw_pick<CWD, Fn>(ix.ds, [](auto w) -> Fn {
+            return scan8_exact_kernel<MT, KT, decltype(w)::value, FL>;
+        });
     };
     auto k = a.only_flagged ? pick(std::true_type{}) : pick(std::false_type{});
     ensure_dyn_lds((const void*)k, lds);
@@ -829,9 +850,8 @@ static void launch_filtered_mk(const DevIndex& ix, const ScanArgs& a, const uint
     size_t off[16];
     const size_t lds = scan_lds_layout(ix.d, ix.M, ix.K, 0, buf, scan_groups(ix.d, ix.M, ix.K, 0, buf), off);
     constexpr int CWD = cw_regs<MT, KT>();
-    auto k = (CWD > 0 && ix.ds == CWD)  ? scan8_filtered_kernel<MT, KT, -CWD>
-             : (CWD > 0 && ix.ds < CWD) ? scan8_filtered_kernel<MT, KT, CWD>
-                                        : scan8_filtered_kernel<MT, KT, 0>;
+    using Fn = decltype(&scan8_filtered_kernel<MT, KT, 0>);
+    auto k = cw_pick<CWD, Fn>(ix.ds, [](auto w) -> Fn { return scan8_filtered_kernel<MT, KT, decltype(w)::value>; });
     ensure_dyn_lds((const void*)k, lds);
     hipLaunchKernelGGL(k, dim3(a.nq), dim3(SCAN_THREADS), lds, s, ix, a, buf, ecat, want);
 }
