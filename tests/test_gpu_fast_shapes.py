@@ -3,9 +3,9 @@ the oracle in FAST and EXACT mode: 32 codebooks (transposed blocks at
 subvector widths 4 and 2), 64 codebooks (row layout, width 2), 16 codebooks
 of width 3 (row layout, subvector width read at run time) and 48 codebooks
 of width 4 at d 192 (transposed blocks; the coarse step takes the path for
-d > 128), and d 64 with 16 or 8 codebooks and d 32 with 16 or 4 (widths 4, 8,
-2 and 8: in EXACT mode the kernels whose codeword registers are a half or a
-quarter of the widest width).  The reference accepts any number of codebooks
+d > 128), d 64 with 16 or 8 codebooks, d 32 with 16 or 4 and d 96 with 16 or
+32 (widths 4, 8, 2, 8, 6 and 3: in EXACT mode the kernels whose codeword
+registers are a half, a quarter or three quarters of the widest width).  The reference accepts any number of codebooks
 (src/pq_simd.rs:314-327).  Indexes are built by the oracle and uploaded, so
 the comparison covers the scan alone; distances are compared bit for bit."""
 
@@ -19,7 +19,7 @@ def _print_case(msg):
     print(f"[case] {msg}", flush=True)
 
 
-@pytest.mark.parametrize("d,M", [(128, 32), (64, 32), (128, 64), (48, 16), (192, 48), (64, 16), (64, 8), (32, 16), (32, 4)])
+@pytest.mark.parametrize("d,M", [(128, 32), (64, 32), (128, 64), (48, 16), (192, 48), (64, 16), (64, 8), (32, 16), (32, 4), (96, 16), (96, 32)])
 def test_fast_scan_shapes_against_oracle(oracle, d, M):
     import vicinity_amd as v
 

@@ -80,10 +80,10 @@ def test_filtered_search_is_bitexact(k256, k):
         assert all(cat[np.flatnonzero(art["doc_ids"] == i)[0]] == g for i in ids.tolist())
 
 
-@pytest.mark.parametrize("d,M", [(64, 16), (64, 8), (32, 16)])
+@pytest.mark.parametrize("d,M", [(64, 16), (64, 8), (32, 16), (96, 16)])
 def test_filtered_widths_against_oracle(vg, oracle, d, M):
-    """Subvector widths a half or a quarter of the widest the kernels hold in
-    registers (4, 8 and 2 floats)."""
+    """Subvector widths a half, a quarter or three quarters of the widest the
+    kernels hold in registers (4, 8, 2 and 6 floats)."""
     from vicinity_amd import MetadataFilter
 
     _print_case(f"build filtered index 4000 x {d}, nlist 16, M {M}, ksub 256")

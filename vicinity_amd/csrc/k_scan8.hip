@@ -772,8 +772,9 @@ __global__ __launch_bounds__(SCAN_THREADS, 4) void scan8_exact_kernel(DevIndex i
 
 // Codewords held per thread: ksub 256 with a fixed codebook count and
 // d <= 128 (M * ds floats per thread); 0 = read the codebooks per list.  The
-// kernels take -W when ds is exactly W = cw_regs, cw_regs / 2 or cw_regs / 4
-// (W >= 2: compile-time d, no guards), cw_regs for other ds below it.  At
+// kernels take -W when ds is exactly W = cw_regs, 3 cw_regs / 4, cw_regs / 2 or
+// cw_regs / 4 (W >= 2; d 128, 96, 64, 32: compile-time d, no guards), cw_regs
+// for other ds below it.  At
 // d 64 the guarded variant took 2.25x (16 codebooks) and 1.57x (32) the time
 // of the exact-width one: its codeword guards, and 56 to 136 bytes per lane of
 // spills.
@@ -794,6 +795,8 @@ static Fn cw_pick(int ds, K kern) {
             if (ds == CWD / 2) f = kern(std::integral_constant<int, -(CWD / 2)>{});
         if constexpr (CWD >= 8)
             if (ds == CWD / 4) f = kern(std::integral_constant<int, -(CWD / 4)>{});
+        if constexpr (CWD >= 4)
+            if (ds == 3 * CWD / 4) f = kern(std::integral_constant<int, -(3 * CWD / 4)>{});
     }
     return f;
 }
