@@ -846,8 +846,8 @@ __device__ __forceinline__ float fs8_pair_distance(const DevIndex& ix, const flo
                                                    uint32_t p, const CodeRow<MT>& row, uint32_t half) {
     constexpr int D = MT * DS;
     constexpr int H = MT / 2;                 // codebooks per thread
-    constexpr int CB0 = 64 / DS;
-    constexpr int CB = CB0 < H ? CB0 : H;     // codewords in flight
+    constexpr int CB1 = 64 / DS < H ? 64 / DS : H;
+    constexpr int CB = CB1 >= 16 ? 16 : CB1 >= 8 ? 8 : CB1 >= 4 ? 4 : CB1 >= 2 ? 2 : 1;  // codewords in flight
     static_assert(H % CB == 0 && H % 4 == 0, "codebook batches");
     constexpr int HW = H / 4;                 // code words per half row
     uint32_t cwd[HW];
@@ -1473,8 +1473,9 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
         if ((size_t)P * D <= (size_t)LUTF) {
             constexpr int SPT = VGPU_BLOCK / (D / 4);         // slots per pass
             constexpr int SMAX = (LUTF / D + SPT - 1) / SPT;  // passes for P D <= LUTF
-            static_assert(VGPU_BLOCK % (D / 4) == 0, "staging split");
-            const int j = 4 * (tid % (D / 4)), pp0 = tid / (D / 4);
+            static_assert(D % 4 == 0, "staging split");
+            // threads past the pass's SPT whole slots stage nothing
+            const int j = 4 * (tid % (D / 4)), pp0 = tid < SPT * (D / 4) ? tid / (D / 4) : P;
             uint32_t lr[SMAX];
 #pragma unroll
             for (int it = 0; it < SMAX; it++) lr[it] = pp0 + it * SPT < P ? s.lid[pp0 + it * SPT] : 0u;
@@ -1854,6 +1855,18 @@ static void launch_fast_ds(const DevIndex& ix, const ScanArgs& a, hipStream_t s,
     }
 }
 
+// Subvector widths 3, 6 and 12 (d 96 or 48 with 8, 16 or 32 codebooks, ...):
+// the row layout with the width fixed at compile time, which scanned d 96
+// about twice as fast as the run-time width.  Up to 32 codebooks and d 192;
+// 16 codebooks of 12 (d 192) spilled and take the run-time width, as do the
+// rest.
+template <int MT, int DS>
+static void launch_fast_row(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hipEvent_t t0,
+                            hipEvent_t t1) {
+    if constexpr (MT <= 32 && MT * DS <= 192 && !(MT == 16 && DS == 12)) launch_fast<MT, 256, DS, 0>(ix, a, s, t0, t1);
+    else launch_fast<MT, 256, 0, 0>(ix, a, s, t0, t1);
+}
+
 template <int MT>
 static void launch_fast_m(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hipEvent_t t0,
                           hipEvent_t t1) {
@@ -1861,6 +1874,9 @@ static void launch_fast_m(const DevIndex& ix, const ScanArgs& a, hipStream_t s, 
         case 2: launch_fast_ds<MT, 2>(ix, a, s, t0, t1); return;
         case 4: launch_fast_ds<MT, 4>(ix, a, s, t0, t1); return;
         case 8: launch_fast_ds<MT, 8>(ix, a, s, t0, t1); return;
+        case 3: launch_fast_row<MT, 3>(ix, a, s, t0, t1); return;
+        case 6: launch_fast_row<MT, 6>(ix, a, s, t0, t1); return;
+        case 12: launch_fast_row<MT, 12>(ix, a, s, t0, t1); return;
         default: launch_fast<MT, 256, 0, 0>(ix, a, s, t0, t1); return;
     }
 }
