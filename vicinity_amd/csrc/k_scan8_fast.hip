@@ -1716,7 +1716,7 @@ __global__ __launch_bounds__(256) void t2_table_kernel(const float* __restrict__
     constexpr int DP = KS * 4;        // padded dimensions per codebook
     constexpr int RS = 16 * DP + 4;   // LDS row stride (+4: the 16 rows of an operand read in distinct banks)
     constexpr int RF = 16 * DS / 4;   // 16-byte pieces per operand row
-    static_assert(DS % 2 == 0, "16-byte pieces within one codebook");
+    static_assert(DS % 2 == 0, "even subvector widths");
     __shared__ __align__(16) float stage[16 * 256];  // [query][codeword][codebook r]
     __shared__ __align__(16) float sa[16 * RS];      // [query][codebook * DP + k]
     __shared__ __align__(16) float sb[16 * RS];      // [codeword][codebook * DP + k]
@@ -1745,9 +1745,17 @@ __global__ __launch_bounds__(256) void t2_table_kernel(const float* __restrict__
             sb[cw * RS + r * DP + 1] = y.y;
             sb[(cw + 1) * RS + r * DP] = y.z;
             sb[(cw + 1) * RS + r * DP + 1] = y.w;
-        } else {
+        } else if constexpr (DS % 4 == 0) {
             *reinterpret_cast<float4*>(sa + r * RS + m * DP + k) = x;
             *reinterpret_cast<float4*>(sb + cw * RS + r * DP + (4 * c4 % DS)) = y;
+        } else {  // DS = 6: a piece may span two codebooks (A) or two codewords (B)
+            const float xv[4] = {x.x, x.y, x.z, x.w}, yv[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int jj = 4 * c4 + e;  // float of the row: codebook / codeword jj / DS, dimension jj % DS
+                sa[r * RS + (jj / DS) * DP + jj % DS] = xv[e];
+                sb[(jj / DS) * RS + r * DP + jj % DS] = yv[e];
+            }
         }
     }
     __syncthreads();
@@ -1779,7 +1787,7 @@ __global__ __launch_bounds__(256) void t2_table_kernel(const float* __restrict__
 }
 
 bool scan8_fast_uses_tables(const DevIndex& ix) {
-    return ix.tcodes && ix.K == 256 && ix.M == 16 && (ix.ds == 2 || ix.ds == 4 || ix.ds == 8);
+    return ix.tcodes && ix.K == 256 && ix.M == 16 && (ix.ds == 2 || ix.ds == 4 || ix.ds == 6 || ix.ds == 8);
 }
 
 void launch_t2_tables(const DevIndex& ix, const float* qn, int nq, float* t2, hipStream_t s, hipEvent_t t0,
@@ -1793,12 +1801,15 @@ void launch_t2_tables(const DevIndex& ix, const float* qn, int nq, float* t2, hi
     switch (ix.ds) {
         case 2: go(t2_table_kernel<2>); return;
         case 4: go(t2_table_kernel<4>); return;
+        case 6: go(t2_table_kernel<6>); return;
         default: go(t2_table_kernel<8>); return;
     }
 }
 
+// Width 6 only with 16 codebooks, whose scan takes its table from the pre-pass
+// (the scan's own transposed table build reads 64-byte lines of 2, 4 or 8).
 bool scan8_fast_blocks_supported(int M, int K, int ds) {
-    return K == 256 && (M == 16 || M == 32 || M == 48) && (ds == 2 || ds == 4 || ds == 8);
+    return K == 256 && (((M == 16 || M == 32 || M == 48) && (ds == 2 || ds == 4 || ds == 8)) || (M == 16 && ds == 6));
 }
 
 // Table copies of the transposed kernels (0: row layout).  One copy: with
@@ -1859,10 +1870,13 @@ static void launch_fast_ds(const DevIndex& ix, const ScanArgs& a, hipStream_t s,
 // the row layout with the width fixed at compile time, which scanned d 96
 // about twice as fast as the run-time width.  Up to 32 codebooks and d 192;
 // 16 codebooks of 12 (d 192) spilled and take the run-time width, as do the
-// rest.
+// rest.  With 16 codebooks of 6 (d 96) the transposed blocks and the
+// pre-pass tables serve the scan instead.
 template <int MT, int DS>
 static void launch_fast_row(const DevIndex& ix, const ScanArgs& a, hipStream_t s, hipEvent_t t0,
                             hipEvent_t t1) {
+    if constexpr (MT == 16 && DS == 6)  // d 96: transposed blocks with the pre-pass tables
+        if (table_copies(ix) == 1 && a.t2) return launch_fast<MT, 256, DS, 1, 1>(ix, a, s, t0, t1);
     if constexpr (MT <= 32 && MT * DS <= 192 && !(MT == 16 && DS == 12)) launch_fast<MT, 256, DS, 0>(ix, a, s, t0, t1);
     else launch_fast<MT, 256, 0, 0>(ix, a, s, t0, t1);
 }
