@@ -6,8 +6,9 @@ of width 4 at d 192 (transposed blocks; the coarse step takes the path for
 d > 128), d 64 with 16 or 8 codebooks, d 32 with 16 or 4 and d 96 with 16 or
 32 (widths 4, 8, 2, 8, 6 and 3: in EXACT mode the kernels whose codeword
 registers are a half, a quarter or three quarters of the widest width), and
-the FAST row layout at compile-time widths 3, 6 and 12 (d 96 with 8, 16 or 32
-codebooks, d 48 with 16, 8 or 4, d 24 with 8 or 4, d 12 with 4, d 192 with 32).  The reference accepts any number of codebooks
+the FAST row layout at compile-time widths 3, 6, 12 and 16 (d 96 with 8, 16 or
+32 codebooks, d 48 with 16, 8 or 4, d 24 with 8 or 4, d 12 with 4, d 192 with
+32, d 128 with 8, d 64 with 4).  The reference accepts any number of codebooks
 (src/pq_simd.rs:314-327).  Indexes are built by the oracle and uploaded, so
 the comparison covers the scan alone; distances are compared bit for bit."""
 
@@ -22,7 +23,8 @@ def _print_case(msg):
 
 
 @pytest.mark.parametrize("d,M", [(128, 32), (64, 32), (128, 64), (48, 16), (192, 48), (64, 16), (64, 8), (32, 16), (32, 4), (96, 16), (96, 32),
-                                 (96, 8), (48, 8), (48, 4), (24, 8), (24, 4), (12, 4), (192, 32)])
+                                 (96, 8), (48, 8), (48, 4), (24, 8), (24, 4), (12, 4), (192, 32),
+                                 (128, 8), (64, 4)])
 def test_fast_scan_shapes_against_oracle(oracle, d, M):
     import vicinity_amd as v
 

@@ -1219,7 +1219,7 @@ __global__ __launch_bounds__(256, 6) void scan8_fast_kernel(DevIndex ix, ScanArg
     if constexpr (TR) {
     } else if constexpr (MT > 0 && KT > 0 && DS > 0 && (MT * KT) % VGPU_BLOCK == 0) {
         constexpr int NE = MT * KT / VGPU_BLOCK;           // entries per thread
-        constexpr int G = DS >= 8 ? 4 : (NE < 8 ? NE : 8);  // entries whose loads fly together
+        constexpr int G = DS >= 16 ? 2 : DS >= 8 ? 4 : (NE < 8 ? NE : 8);  // entries whose loads fly together
         static_assert(NE % G == 0, "table split");
 #pragma unroll
         for (int g0 = 0; g0 < NE; g0 += G) {
@@ -1866,9 +1866,9 @@ static void launch_fast_ds(const DevIndex& ix, const ScanArgs& a, hipStream_t s,
     }
 }
 
-// Subvector widths 3, 6 and 12 (d 96 or 48 with 8, 16 or 32 codebooks, ...):
-// the row layout with the width fixed at compile time, which scanned d 96
-// about twice as fast as the run-time width.  Up to 32 codebooks and d 192;
+// Subvector widths 3, 6, 12 and 16 (d 96 or 48 with 8, 16 or 32 codebooks,
+// d 128 or 64 with 8 or 4, ...): the row layout with the width fixed at
+// compile time, which scanned d 96 about twice as fast as the run-time width.  Up to 32 codebooks and d 192;
 // 16 codebooks of 12 (d 192) spilled and take the run-time width, as do the
 // rest.  With 16 codebooks of 6 (d 96) the transposed blocks and the
 // pre-pass tables serve the scan instead.
@@ -1891,6 +1891,7 @@ static void launch_fast_m(const DevIndex& ix, const ScanArgs& a, hipStream_t s, 
         case 3: launch_fast_row<MT, 3>(ix, a, s, t0, t1); return;
         case 6: launch_fast_row<MT, 6>(ix, a, s, t0, t1); return;
         case 12: launch_fast_row<MT, 12>(ix, a, s, t0, t1); return;
+        case 16: launch_fast_row<MT, 16>(ix, a, s, t0, t1); return;
         default: launch_fast<MT, 256, 0, 0>(ix, a, s, t0, t1); return;
     }
 }
